@@ -1,0 +1,340 @@
+"""Benchmark: GradDotProd on GPT-2-small, T=1024 on one MI355X.
+
+A step is one GradDotProd training step of the reference's loop
+(Examples/GradDotProd_LM/training_loop.py:99-166): forward on the concatenated 16 train + 4
+val rows, backward with the dot-product hooks, .grad <- train grads, AdamW step, aggregate
+and log the per-train-row dot vector (with its device->host copy), clear.  Inputs are
+synthetic token ids already resident in HBM; weights are random N(0, 0.02), bf16.
+
+Prints one JSON line: samples/s (train rows scored per second), step overhead versus
+plain backprop of the same batch, the roofline of the dominant hot-path kernel (timed with
+HIP events inside the timed region, on the stream it runs on), the fused ghost kernel at the
+Linear microbench shape against the bf16 MFMA peak, and a CPU
+baseline (the oracle's reference op sequence on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16 = 2.5e15   # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12    # MI355X HBM3E, B/s
+METRIC = "samples/sec w/ ghost dot-products, GPT-2-small T=1024; MFMA util %; step overhead"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ op timing
+class TimedOps:
+    """Wraps the kernel layer: brackets every call with HIP events on the current stream
+    and records (op, algorithm, algorithmic work, events)."""
+
+    def __init__(self, inner):
+        self.inner = inner
+        self.records = []
+        self.enabled = False
+
+    def _run(self, name, work, fn, *a, **k):
+        if not self.enabled:
+            return fn(*a, **k)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn(*a, **k)
+        e.record()
+        self.records.append((name, work, s, e))
+        return out
+
+    def linear_algo(self, *a, **k):
+        return self.inner.linear_algo(*a, **k)
+
+    def linear_dot(self, A, G, n_val, **k):
+        from ghostsuite_amd import _native
+        N, d_in, d_out = A.shape[0], A.shape[-1], G.shape[-1]
+        T = A.numel() // (N * d_in)
+        sem = k.get("semantics", 0)
+        algo = self.inner.linear_algo(A.dtype, N, n_val, T, d_in, d_out, sem,
+                                      k.get("algo", 0), k.get("want_pair", False))
+        n_t = N - n_val
+        nv = n_val if sem == _native.SEM_PAIRWISE_SUM else 1
+        if algo == _native.ALGO_GHOST:
+            flops = 2.0 * n_t * nv * T * T * (d_in + d_out)
+        else:
+            flops = 2.0 * (nv * T + n_t * T) * d_in * d_out
+        name = f"linear_{_native.ALGO_NAMES[algo]}[{d_in}x{d_out}]"
+        return self._run(name, ("mfma", flops), self.inner.linear_dot, A, G, n_val, **k)
+
+    def bias_dot(self, G, n_val, **k):
+        return self._run("bias_dot", ("hbm", G.numel() * G.element_size()),
+                         self.inner.bias_dot, G, n_val, **k)
+
+    def embedding_dot(self, ids, G, n_val, vocab, **k):
+        nbytes = G.numel() * G.element_size() + ids.numel() * 8
+        return self._run("embedding_dot", ("hbm", nbytes), self.inner.embedding_dot, ids, G,
+                         n_val, vocab, **k)
+
+    def layernorm_dot(self, X, G, n_val, eps, **k):
+        nbytes = X.numel() * X.element_size() + G.numel() * G.element_size()
+        return self._run("layernorm_dot", ("hbm", nbytes), self.inner.layernorm_dot, X, G,
+                         n_val, eps, **k)
+
+    def kron_proj(self, A, G, P_i, P_o, scale, **k):
+        nbytes = A.numel() * A.element_size() + G.numel() * G.element_size()
+        return self._run("kron_proj", ("hbm", nbytes), self.inner.kron_proj, A, G, P_i, P_o,
+                         scale, **k)
+
+    def summary(self):
+        torch.cuda.synchronize()
+        agg = {}
+        for name, (bound, work), s, e in self.records:
+            ms = s.elapsed_time(e)
+            a = agg.setdefault(name, {"bound": bound, "work": work, "ms": 0.0, "n": 0})
+            a["ms"] += ms
+            a["n"] += 1
+        return agg
+
+
+# ------------------------------------------------------------------ GPT-2-small step
+def gpt2_bench(steps: int, warmup: int, dev):
+    from ghostsuite_amd import GradDotProdEngine, _native
+    from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+    from ghostsuite_amd.workloads import CausalLM, GPT2_SMALL, synthetic_tokens
+
+    n_train, n_val, T = 16, 4, 1024
+    cfg = GPT2_SMALL
+    torch.manual_seed(0)
+    model = CausalLM(cfg).to(dev, torch.bfloat16)
+    plain = CausalLM(cfg).to(dev, torch.bfloat16)
+    plain.load_state_dict(model.state_dict())
+    X, Y = synthetic_tokens(n_train + n_val, T, cfg.vocab, seed=1234, device=dev)
+    X_tr, Y_tr = X[:n_train], Y[:n_train]
+
+    timed = TimedOps(_native.ops())
+    _native._install_backend(timed)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    engine = GradDotProdEngine(model, val_batch_size=n_val, loss_reduction="mean",
+                               use_dummy_bias=True, record_algorithms=True)
+    engine.attach(opt)
+
+    def ghost_step(i):
+        engine.attach_train_batch(X_tr, Y_tr, i, 0)
+        loss = model(X, Y)
+        loss.backward()
+        engine.prepare_gradients()
+        opt.step()
+        engine.aggregate_and_log()
+        engine.clear_gradients()
+        opt.zero_grad(set_to_none=True)
+        engine.dot_product_log.clear()
+
+    popt = torch.optim.AdamW(plain.parameters(), lr=1e-4)
+
+    def plain_step(i):
+        loss = plain(X, Y)
+        loss.backward()
+        popt.step()
+        popt.zero_grad(set_to_none=True)
+
+    def run(fn, n_steps, n_warm, label):
+        for i in range(n_warm):
+            fn(i)
+        torch.cuda.synchronize()
+        log(f"[bench] {label}: warmup done, timing {n_steps} steps")
+        t0 = time.perf_counter()
+        for i in range(n_steps):
+            fn(i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_steps
+
+    t_ghost_warm = None
+    timed.enabled = False
+    for i in range(warmup):
+        ghost_step(i)
+    torch.cuda.synchronize()
+    log("[bench] ghost: warmup done")
+    timed.enabled = True
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ghost_step(i)
+    torch.cuda.synchronize()
+    t_ghost = (time.perf_counter() - t0) / steps
+    timed.enabled = False
+    ops_summary = timed.summary()
+    log(f"[bench] ghost step {t_ghost * 1e3:.2f} ms")
+    t_plain = run(plain_step, steps, warmup, "plain")
+    log(f"[bench] plain step {t_plain * 1e3:.2f} ms")
+    _native._install_backend(None)
+    engine.detach()
+    algos = dict(S.ALGO_LOG)
+    del model, plain, opt, popt, engine
+    torch.cuda.empty_cache()
+    return {
+        "n_train": n_train, "n_val": n_val, "T": T,
+        "t_ghost": t_ghost, "t_plain": t_plain, "ops": ops_summary, "algos": algos,
+        "plain_tflop": __import__("ghostsuite_amd.workloads", fromlist=["x"]).lm_flops_per_step(
+            cfg, n_train + n_val, T) / 1e12,
+    }
+
+
+# ------------------------------------------------------------------ ghost kernel microbench
+def ghost_kernel_bench(dev, reps: int = 20, T: int = 1024):
+    """A[32,T,768], G[32,T,3072] bf16, first 8 rows val, fused ghost."""
+    from ghostsuite_amd import _native
+    g = torch.Generator().manual_seed(1234)
+    N, n_val, d_in, d_out = 32, 8, 768, 3072
+    A = torch.randn(N, T, d_in, generator=g).to(dev, torch.bfloat16)
+    G = (torch.randn(N, T, d_out, generator=g) * 1e-3).to(dev, torch.bfloat16)
+    ops = _native.ops()
+    for _ in range(3):
+        ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_GHOST)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_GHOST)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    flops = 2.0 * (N - n_val) * n_val * T * T * (d_in + d_out)
+    # same semantics through the val-gradient algorithm, for reference
+    s.record()
+    for _ in range(reps):
+        ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_VALGRAD)
+    e.record()
+    torch.cuda.synchronize()
+    ms_vg = s.elapsed_time(e) / reps
+    return {"T": T, "ms": ms, "tflops": flops / ms / 1e9, "frac": flops / (ms * 1e-3) / PEAK_BF16,
+            "valgrad_ms": ms_vg}
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(budget_s: float = 20.0):
+    """The oracle's restatement of the reference op sequence (ghost dots + train grads) for
+    the hooked layers of one GPT-2-small block at the bench batch (N=20, T=1024, bf16), on
+    the host cores, scaled to 12 blocks; reported as train rows per second."""
+    from oracle import ghost_ref as R
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    N, n_val, T, d, m = 20, 4, 1024, 768, 3072
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+
+    def rnd(*shape, s=1.0):
+        return (torch.randn(*shape, generator=g) * s).to(bf)
+
+    layers = [("qkv", d, 3 * d), ("proj", d, d), ("fc", d, m), ("fc_out", m, d)]
+    acts = {n: (rnd(N, T, a), rnd(N, T, b, s=1e-3)) for n, a, b in layers}
+    ln_in = rnd(N, T, d)
+    ln_g = rnd(N, T, d, s=1e-3)
+
+    def one_block():
+        for name, a, b in layers:
+            A, B = acts[name]
+            use_ghost = R.should_use_ghost(T, a * b)
+            R.linear_dot_ref(A, B, n_val, use_ghost)
+            R.linear_train_grad(A, B * N, n_val)
+        for _ in range(2):
+            R.layernorm_dot_ref(ln_in, ln_g, n_val, 1e-5)
+            R.layernorm_train_grad(ln_in, ln_g * N, n_val, 1e-5)
+
+    t0 = time.perf_counter()
+    one_block()
+    t_block = time.perf_counter() - t0
+    reps = 1
+    while time.perf_counter() - t0 + t_block < budget_s and reps < 3:
+        one_block()
+        reps += 1
+    t_block = (time.perf_counter() - t0) / reps
+    t_step = 12 * t_block
+    return {"value": 16.0 / t_step, "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle reference-op sequence (Linear ghost/materialised dots + train "
+                       f"grads, 2 LayerNorm dots + grads) of one GPT-2-small block at N=20, "
+                       f"T=1024, bf16, x{reps} reps, {t_block:.2f} s/block, scaled to 12 "
+                       f"blocks; model fwd/bwd not included")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus "
+              f"{args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    from ghostsuite_amd import _native
+    _native.load_library()
+
+    res = gpt2_bench(args.steps, args.warmup, dev)
+    log("[bench] GPT-2 step done; ghost kernel microbench")
+    gk = ghost_kernel_bench(dev)
+    log(f"[bench] ghost kernel T=1024: {gk['ms']:.3f} ms, {gk['tflops']:.1f} TF/s")
+
+    ops = res["ops"]
+    steps = args.steps
+    dom_name, dom = max(ops.items(), key=lambda kv: kv[1]["ms"])
+    avg_ms = dom["ms"] / dom["n"]
+    achieved = dom["work"] / (avg_ms * 1e-3)
+    if dom["bound"] == "mfma":
+        roof = {"bound": "mfma", "kernel": dom_name, "achieved": achieved / 1e12,
+                "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16,
+                "traffic": None, "avg_ms": avg_ms, "launches_per_step": dom["n"] / steps}
+    else:
+        roof = {"bound": "hbm", "kernel": dom_name, "achieved": achieved / 1e9,
+                "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved / PEAK_HBM,
+                "traffic": None, "avg_ms": avg_ms, "launches_per_step": dom["n"] / steps}
+    hot_ms = sum(v["ms"] for v in ops.values()) / steps
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
+    value = res["n_train"] / res["t_ghost"]
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["t_ghost"] * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform token ids, random-init N(0,0.02) weights)",
+        "config": {"workload": "GPT-2-small GradDotProd step, 16 train + 4 val rows, T=1024",
+                   "global_batch": res["n_train"] + res["n_val"], "seq_len": res["T"],
+                   "parallelism": "single GPU"},
+        "plain_ms_per_step": res["t_plain"] * 1e3,
+        "step_overhead": res["t_ghost"] / res["t_plain"],
+        "rows_per_s_total": (res["n_train"] + res["n_val"]) / res["t_ghost"],
+        "hot_path_ms_per_step": hot_ms,
+        "roofline": roof,
+        "ghost_kernel": {"shape": "A[32,1024,768] G[32,1024,3072] bf16, 8 val rows first",
+                         "ms": gk["ms"], "achieved": gk["tflops"], "unit": "TFLOP/s",
+                         "peak": PEAK_BF16 / 1e12, "frac": gk["frac"],
+                         "valgrad_same_semantics_ms": gk["valgrad_ms"]},
+        "ops": {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["n"] / steps}
+                for k, v in sorted(ops.items(), key=lambda kv: -kv[1]["ms"])},
+        "algorithms": {k: list(v) for k, v in list(res["algos"].items())[:8]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

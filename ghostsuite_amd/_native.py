@@ -1,0 +1,311 @@
+"""ctypes binding of libghost_hip.so (include/ghost_hip.h) and torch-tensor wrappers.
+
+Every wrapper takes device tensors, checks shapes on the host, sizes and allocates the
+workspace from torch's caching allocator, and launches on torch's current stream; no call
+synchronises.  There is no CPU path: a tensor that is not on a ROCm device, or a missing
+library, raises.
+
+Host-logic tests swap the kernel layer for a checker through ``_install_backend`` (the
+samplers call ``ops()``); product code never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from typing import Optional, Tuple
+
+import torch
+
+from . import build as _build
+
+# gs_dtype / gs_semantics / gs_algo / gs_rounding / gs_proj_layout (include/ghost_hip.h)
+DTYPE_BF16, DTYPE_F32, DTYPE_F16 = 0, 1, 2
+SEM_PAIRWISE_SUM, SEM_PRESUM = 0, 1
+ALGO_AUTO, ALGO_GHOST, ALGO_VALGRAD = 0, 1, 2
+ROUND_FP32, ROUND_REF_BF16 = 0, 1
+PROJ_KO_KI, PROJ_KI_KO = 0, 1
+ABI_VERSION = 1
+
+_TORCH_TO_GS = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32, torch.float16: DTYPE_F16}
+ALGO_NAMES = {ALGO_AUTO: "auto", ALGO_GHOST: "ghost", ALGO_VALGRAD: "valgrad"}
+
+
+class GhostHipError(RuntimeError):
+    """A libghost_hip.so entry point returned an error status."""
+
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+_I64 = ctypes.c_int64
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+_SIGNATURES = {
+    "gs_abi_version": (_I, []),
+    "gs_last_error": (ctypes.c_char_p, []),
+    "gs_linear_dot_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I, _I]),
+    "gs_linear_dot_algo": (_I, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I, _I]),
+    "gs_linear_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
+                           _P, _P, _P, _SZ, _P]),
+    "gs_bias_dot_workspace": (_SZ, [_I64, _I64, _I64]),
+    "gs_bias_dot": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _P, _I, _F, _P, _SZ, _P]),
+    "gs_embedding_dot_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "gs_embedding_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
+                              _P]),
+    "gs_layernorm_dot_workspace": (_SZ, [_I64, _I64, _I64]),
+    "gs_layernorm_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P,
+                              _I, _F, _P, _SZ, _P]),
+    "gs_kron_proj_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+    "gs_kron_proj": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I, _F,
+                          _P, _I, _P, _SZ, _P]),
+}
+
+
+def load_library() -> ctypes.CDLL:
+    """Loads libghost_hip.so (built in-tree by ghostsuite_amd.build) once per process."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = _build.library_path()
+        if not path.exists():
+            raise GhostHipError(
+                f"{path} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python ghostsuite_amd/build.py` first")
+        lib = ctypes.CDLL(str(path))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.gs_abi_version()
+        if ver != ABI_VERSION:
+            raise GhostHipError(f"libghost_hip ABI {ver}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def exported_symbols() -> list:
+    return list(_SIGNATURES)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().gs_last_error().decode(errors="replace")
+        raise GhostHipError(f"{what} failed ({rc}): {msg}")
+
+
+def _gs_dtype(t: torch.Tensor) -> int:
+    try:
+        return _TORCH_TO_GS[t.dtype]
+    except KeyError:
+        raise GhostHipError(f"unsupported dtype {t.dtype}") from None
+
+
+def _require_device(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise GhostHipError(
+                "ghostsuite_amd kernels need tensors on a ROCm GPU device; got a tensor on "
+                f"{t.device} (there is no CPU path)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise GhostHipError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def _tokens(x: torch.Tensor, n: int, feat: int) -> int:
+    if x.dim() < 2 or x.shape[0] != n:
+        raise GhostHipError(f"expected a [N, ..., F] tensor with N={n}, got {tuple(x.shape)}")
+    return x.numel() // (n * feat) if n * feat > 0 else 0
+
+
+class HipOps:
+    """The kernel layer the samplers call: one C-ABI call per op, async on the current stream."""
+
+    name = "hip"
+
+    def linear_algo(self, dtype: torch.dtype, N: int, n_val: int, T: int, d_in: int, d_out: int,
+                    semantics: int, algo: int, want_pair: bool) -> int:
+        lib = load_library()
+        rc = lib.gs_linear_dot_algo(_TORCH_TO_GS[dtype], N, n_val, T, d_in, d_out, semantics,
+                                    algo, int(want_pair))
+        _check(rc if rc < 0 else 0, "gs_linear_dot_algo")
+        return rc
+
+    def linear_dot(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *, val_start=None,
+                   semantics: int = SEM_PAIRWISE_SUM, algo: int = ALGO_AUTO,
+                   rounding: int = ROUND_FP32, want_pair: bool = False
+                   ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        dev = _require_device(A, G)
+        if A.dtype != G.dtype:
+            raise GhostHipError(f"A and G dtypes differ: {A.dtype} vs {G.dtype}")
+        A = A.contiguous()
+        G = G.contiguous()
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T:
+            raise GhostHipError(f"A {tuple(A.shape)} and G {tuple(G.shape)} token counts differ")
+        vs = N - n_val if val_start is None else int(val_start)
+        n_t = N - n_val
+        dt = _gs_dtype(A)
+        lib = load_library()
+        ws_bytes = lib.gs_linear_dot_workspace(dt, N, n_val, T, d_in, d_out, semantics, algo,
+                                               int(want_pair))
+        if ws_bytes == 0:
+            raise GhostHipError(
+                f"gs_linear_dot: invalid arguments N={N} n_val={n_val} T={T} d_in={d_in} "
+                f"d_out={d_out} semantics={semantics} algo={algo} pair={want_pair}")
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty(n_t, dtype=torch.float32, device=dev)
+        pair = torch.empty((n_val, n_t), dtype=torch.float32, device=dev) if want_pair else None
+        rc = lib.gs_linear_dot(A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in, d_out,
+                               semantics, algo, rounding, out.data_ptr(), _ptr(pair),
+                               ws.data_ptr(), ws_bytes, _stream(dev))
+        _check(rc, "gs_linear_dot")
+        return out, pair
+
+    def bias_dot(self, G: torch.Tensor, n_val: int, *, val_start=None,
+                 grad_scale: Optional[float] = None, grad_dtype: Optional[torch.dtype] = None
+                 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        dev = _require_device(G)
+        G = G.contiguous()
+        N, d = G.shape[0], G.shape[-1]
+        T = _tokens(G, N, d)
+        vs = N - n_val if val_start is None else int(val_start)
+        lib = load_library()
+        ws_bytes = lib.gs_bias_dot_workspace(N, T, d)
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty(N - n_val, dtype=torch.float32, device=dev)
+        grad = None
+        if grad_scale is not None:
+            grad = torch.empty(d, dtype=grad_dtype or G.dtype, device=dev)
+        gdt = _gs_dtype(grad) if grad is not None else DTYPE_F32
+        rc = lib.gs_bias_dot(G.data_ptr(), _gs_dtype(G), N, n_val, vs, T, d, out.data_ptr(),
+                             _ptr(grad), gdt, float(grad_scale or 0.0), ws.data_ptr(), ws_bytes,
+                             _stream(dev))
+        _check(rc, "gs_bias_dot")
+        return out, grad
+
+    def embedding_dot(self, ids: torch.Tensor, G: torch.Tensor, n_val: int, vocab: int, *,
+                      val_start=None) -> torch.Tensor:
+        dev = _require_device(ids, G)
+        ids = ids.to(torch.int64).contiguous()
+        G = G.contiguous()
+        N, d = G.shape[0], G.shape[-1]
+        T = ids.numel() // N
+        if _tokens(G, N, d) != T:
+            raise GhostHipError(f"ids {tuple(ids.shape)} and G {tuple(G.shape)} disagree")
+        vs = N - n_val if val_start is None else int(val_start)
+        lib = load_library()
+        ws_bytes = lib.gs_embedding_dot_workspace(N, n_val, T, d, vocab)
+        if ws_bytes == 0:
+            raise GhostHipError(f"gs_embedding_dot: invalid arguments N={N} n_val={n_val}")
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty(N - n_val, dtype=torch.float32, device=dev)
+        rc = lib.gs_embedding_dot(ids.data_ptr(), G.data_ptr(), _gs_dtype(G), N, n_val, vs, T, d,
+                                  vocab, out.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
+        _check(rc, "gs_embedding_dot")
+        return out
+
+    def layernorm_dot(self, X: torch.Tensor, G: torch.Tensor, n_val: int, eps: float, *,
+                      val_start=None, want_dot: bool = True, want_bias: bool = True,
+                      grad_scale: Optional[float] = None,
+                      grad_dtype: Optional[torch.dtype] = None):
+        """Returns (dot_w, dot_b, grad_w, grad_b); entries not asked for are None."""
+        dev = _require_device(X, G)
+        if X.dtype != G.dtype:
+            raise GhostHipError(f"X and G dtypes differ: {X.dtype} vs {G.dtype}")
+        X = X.contiguous()
+        G = G.contiguous()
+        N, F = X.shape[0], X.shape[-1]
+        T = _tokens(X, N, F)
+        vs = N - n_val if val_start is None else int(val_start)
+        lib = load_library()
+        ws_bytes = lib.gs_layernorm_dot_workspace(N, T, F)
+        ws = _workspace(ws_bytes, dev)
+        n_t = N - n_val
+        dw = torch.empty(n_t, dtype=torch.float32, device=dev) if want_dot else None
+        db = torch.empty(n_t, dtype=torch.float32, device=dev) if (want_dot and want_bias) else None
+        gw = gb = None
+        gdt = grad_dtype or X.dtype
+        if grad_scale is not None:
+            gw = torch.empty(F, dtype=gdt, device=dev)
+            gb = torch.empty(F, dtype=gdt, device=dev) if want_bias else None
+        rc = lib.gs_layernorm_dot(X.data_ptr(), G.data_ptr(), _gs_dtype(X), N, n_val, vs, T, F,
+                                  float(eps), _ptr(dw), _ptr(db), _ptr(gw), _ptr(gb),
+                                  _TORCH_TO_GS[gdt], float(grad_scale or 0.0), ws.data_ptr(),
+                                  ws_bytes, _stream(dev))
+        _check(rc, "gs_layernorm_dot")
+        return dw, db, gw, gb
+
+    def kron_proj(self, A: torch.Tensor, G: torch.Tensor, P_i: torch.Tensor, P_o: torch.Tensor,
+                  scale: float, *, layout: int = PROJ_KO_KI,
+                  out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        dev = _require_device(A, G, P_i, P_o)
+        if A.dtype != G.dtype:
+            raise GhostHipError(f"A and G dtypes differ: {A.dtype} vs {G.dtype}")
+        A = A.contiguous()
+        G = G.contiguous()
+        P_i = P_i.to(A.dtype).contiguous()
+        P_o = P_o.to(A.dtype).contiguous()
+        B = A.shape[0]
+        n_a, n_g = A.shape[-1], G.shape[-1]
+        T = A.numel() // (B * n_a)
+        if G.numel() // (B * n_g) != T:
+            raise GhostHipError(f"A {tuple(A.shape)} and G {tuple(G.shape)} token counts differ")
+        k_i, k_o = P_i.shape[0], P_o.shape[0]
+        if layout == PROJ_KO_KI:
+            if P_i.shape[1] != n_a or P_o.shape[1] != n_g:
+                raise GhostHipError("projection widths do not match the layer")
+            shape = (B, k_o, k_i)
+        else:
+            if P_i.shape[1] != n_g or P_o.shape[1] != n_a:
+                raise GhostHipError("projection widths do not match the layer (Conv1D roles)")
+            shape = (B, k_i, k_o)
+        lib = load_library()
+        ws_bytes = lib.gs_kron_proj_workspace(B, T, k_i, k_o)
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty(shape, dtype=out_dtype, device=dev)
+        rc = lib.gs_kron_proj(A.data_ptr(), G.data_ptr(), _gs_dtype(A), B, T, n_a, n_g,
+                              P_i.data_ptr(), P_o.data_ptr(), _gs_dtype(P_i), k_i, k_o, layout,
+                              float(scale), out.data_ptr(), _TORCH_TO_GS[out_dtype],
+                              ws.data_ptr(), ws_bytes, _stream(dev))
+        _check(rc, "gs_kron_proj")
+        return out
+
+
+_backend = None
+
+
+def ops():
+    """The active kernel layer (the HIP library unless a test installed a checker)."""
+    global _backend
+    if _backend is None:
+        _backend = HipOps()
+    return _backend
+
+
+def _install_backend(backend) -> None:
+    """Test seam: replace the kernel layer (host-logic tests on machines without a GPU)."""
+    global _backend
+    _backend = backend

@@ -1,0 +1,511 @@
+// HBM-bound per-sample kernels: bias dots, LayerNorm dots/grads and Embedding dots.
+//
+// All three reduce to "per-sample feature sums, then dots against the val aggregate":
+//   stage 1 (one pass over HBM): S_n[f] partials per (sample n, token chunk c)
+//   stage 2: S_n[f] = sum_c partial, val aggregate Sval[f], optional train grad
+//   stage 3: dot_i = <S_i, Sval>
+// Every reduction runs in a fixed order (no float atomics), so results are
+// bit-reproducible.  Loads are coalesced along the feature axis.
+
+#include <algorithm>
+
+#include "gs_common.h"
+
+namespace gs {
+
+constexpr int BW_THREADS = 256;
+constexpr int TOK_CHUNK = 32;  // tokens per stage-1 block
+
+template <class E>
+__device__ __forceinline__ float ld(const E* p) {
+  return to_f32<E>(*p);
+}
+
+// ---------------------------------------------------------------- stage 1: bias sums
+// part[(n * chunks + c) * F + f] = sum_{t in chunk c} g[n, t, f]
+template <class E>
+__global__ void colsum_kernel(const E* __restrict__ G, int64_t T, int64_t F, int64_t chunks,
+                              float* __restrict__ part) {
+  const int64_t n = blockIdx.y, c = blockIdx.x;
+  const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
+  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+    float s = 0.f;
+    for (int64_t t = t0; t < t1; ++t) s += ld(G + (n * T + t) * F + f);
+    part[(n * chunks + c) * F + f] = s;
+  }
+}
+
+// ---------------------------------------------------------------- stage 1: LayerNorm sums
+// One wave per token row: mean/rstd by wave reduction, then g*xhat and g accumulated per
+// lane over the block's tokens; the 4 waves combine through LDS.
+template <class E, int PL>
+__global__ void __launch_bounds__(BW_THREADS) ln_sums_kernel(const E* __restrict__ X,
+                                                             const E* __restrict__ G, int64_t T,
+                                                             int64_t F, float eps, int64_t chunks,
+                                                             float* __restrict__ part_w,
+                                                             float* __restrict__ part_b) {
+  extern __shared__ float sm[];  // [4][F] for w then [4][F] for b
+  const int64_t n = blockIdx.y, c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
+  float aw[PL], ab[PL];
+#pragma unroll
+  for (int k = 0; k < PL; ++k) aw[k] = ab[k] = 0.f;
+  const float invF = 1.0f / static_cast<float>(F);
+  for (int64_t t = t0 + wid; t < t1; t += 4) {
+    const E* xr = X + (n * T + t) * F;
+    const E* gr = G + (n * T + t) * F;
+    float xv[PL];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PL; ++k) {
+      const int64_t f = lane + 64 * k;
+      xv[k] = f < F ? ld(xr + f) : 0.f;
+      s += xv[k];
+    }
+    const float mean = wave_sum(s) * invF;
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < PL; ++k) {
+      const int64_t f = lane + 64 * k;
+      const float dlt = f < F ? xv[k] - mean : 0.f;
+      v += dlt * dlt;
+    }
+    const float rstd = rsqrtf(wave_sum(v) * invF + eps);
+#pragma unroll
+    for (int k = 0; k < PL; ++k) {
+      const int64_t f = lane + 64 * k;
+      if (f < F) {
+        const float g = ld(gr + f);
+        aw[k] += g * ((xv[k] - mean) * rstd);
+        ab[k] += g;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PL; ++k) {
+    const int64_t f = lane + 64 * k;
+    if (f < F) {
+      sm[wid * F + f] = aw[k];
+      sm[(4 + wid) * F + f] = ab[k];
+    }
+  }
+  __syncthreads();
+  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+    const float w = sm[f] + sm[F + f] + sm[2 * F + f] + sm[3 * F + f];
+    const float b = sm[4 * F + f] + sm[5 * F + f] + sm[6 * F + f] + sm[7 * F + f];
+    part_w[(n * chunks + c) * F + f] = w;
+    if (part_b != nullptr) part_b[(n * chunks + c) * F + f] = b;
+  }
+}
+
+// ---------------------------------------------------------------- stage 2/3 (shared)
+// S[n][f] = sum_c part[n][c][f]   (grid: feature blocks x samples)
+__global__ void feature_sample_totals_kernel(const float* __restrict__ part, int64_t chunks,
+                                             int64_t F, float* __restrict__ S) {
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t n = blockIdx.y;
+  if (f >= F) return;
+  float s = 0.f;
+  for (int64_t c = 0; c < chunks; ++c) s += part[(n * chunks + c) * F + f];
+  S[n * F + f] = s;
+}
+
+// sval[f] = sum over val rows of S; grad[f] = scale * sum over train rows of S.
+template <class GE>
+__global__ void feature_val_totals_kernel(const float* __restrict__ S, int64_t N, int64_t F,
+                                          int64_t n_val, int64_t val_start,
+                                          float* __restrict__ sval, GE* __restrict__ grad,
+                                          float grad_scale) {
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (f >= F) return;
+  float vs = 0.f, ts = 0.f;
+  for (int64_t n = 0; n < N; ++n) {
+    const float s = S[n * F + f];
+    if (n >= val_start && n < val_start + n_val)
+      vs += s;
+    else
+      ts += s;
+  }
+  sval[f] = vs;
+  if (grad != nullptr) grad[f] = from_f32<GE>(grad_scale * ts);
+}
+
+__global__ void feature_dots_kernel(const float* __restrict__ S, const float* __restrict__ sval,
+                                    int64_t F, RowMap train, float* __restrict__ out) {
+  __shared__ float red[BW_THREADS / 64];
+  const int64_t i = blockIdx.x;
+  const float* row = S + train.phys_sample(i) * F;
+  float s = 0.f;
+  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) s += row[f] * sval[f];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) out[i] = s;
+}
+
+// ---------------------------------------------------------------- embedding
+// Val tokens with the same id form one segment represented by its first val token index
+// (table[id] = min index, an order-independent integer atomicMin).  Segment sums are
+// accumulated in 64-bit fixed point with integer atomics (order-independent, hence
+// deterministic), then converted to fp32 rows; each train token finds its segment through
+// table[id] and takes a dot with that row.
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = v;
+}
+
+// table[id] = min val token index; maxbits = max |g| bits over val rows.
+template <class E>
+__global__ void emb_index_kernel(const int64_t* __restrict__ ids, const E* __restrict__ G,
+                                 RowMap val, int64_t d, int64_t vocab, int32_t* __restrict__ table,
+                                 unsigned* __restrict__ maxbits) {
+  const int64_t q = blockIdx.x;  // val token index
+  const int64_t seg = q / val.seglen;
+  const int64_t row = val.phys_row(seg, q - seg * val.seglen);
+  const int64_t id = ids[row];
+  if (threadIdx.x == 0 && id >= 0 && id < vocab) atomicMin(table + id, static_cast<int32_t>(q));
+  float m = 0.f;
+  for (int64_t f = threadIdx.x; f < d; f += blockDim.x) m = fmaxf(m, fabsf(ld(G + row * d + f)));
+  __shared__ float red[BW_THREADS / 64];
+  // block max
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = 0.f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) b = fmaxf(b, red[w]);
+    atomicMax(maxbits, __float_as_uint(b));  // non-negative floats order like their bits
+  }
+}
+
+// Power-of-two scale so that n_vt * max|g| * scale < 2^62.
+__device__ __forceinline__ double emb_scale(unsigned maxbits, int64_t n_vt) {
+  const float mx = __uint_as_float(maxbits);
+  if (!(mx > 0.f) || !isfinite(mx)) return 1.0;
+  const int e = 62 - static_cast<int>(ceil(log2(static_cast<double>(mx) * static_cast<double>(n_vt)))) - 1;
+  return ldexp(1.0, e);
+}
+
+template <class E>
+__global__ void emb_accum_kernel(const int64_t* __restrict__ ids, const E* __restrict__ G,
+                                 RowMap val, int64_t d, int64_t vocab,
+                                 const int32_t* __restrict__ table,
+                                 const unsigned* __restrict__ maxbits,
+                                 unsigned long long* __restrict__ fix) {
+  const int64_t q = blockIdx.x;
+  const int64_t seg = q / val.seglen;
+  const int64_t row = val.phys_row(seg, q - seg * val.seglen);
+  const int64_t id = ids[row];
+  if (id < 0 || id >= vocab) return;
+  const int64_t rep = table[id];
+  const double scale = emb_scale(*maxbits, val.total());
+  for (int64_t f = threadIdx.x; f < d; f += blockDim.x) {
+    const long long v = llrint(static_cast<double>(ld(G + row * d + f)) * scale);
+    atomicAdd(fix + rep * d + f, static_cast<unsigned long long>(v));
+  }
+}
+
+__global__ void emb_zero_kernel(const int64_t* __restrict__ ids, RowMap val, int64_t d,
+                                int64_t vocab, const int32_t* __restrict__ table,
+                                unsigned long long* __restrict__ fix) {
+  const int64_t q = blockIdx.x;
+  const int64_t seg = q / val.seglen;
+  const int64_t id = ids[val.phys_row(seg, q - seg * val.seglen)];
+  if (id < 0 || id >= vocab || table[id] != q) return;
+  for (int64_t f = threadIdx.x; f < d; f += blockDim.x) fix[q * d + f] = 0ull;
+}
+
+__global__ void emb_finish_kernel(const int64_t* __restrict__ ids, RowMap val, int64_t d,
+                                  int64_t vocab, const int32_t* __restrict__ table,
+                                  const unsigned* __restrict__ maxbits,
+                                  const unsigned long long* __restrict__ fix,
+                                  float* __restrict__ vrow) {
+  const int64_t q = blockIdx.x;
+  const int64_t seg = q / val.seglen;
+  const int64_t id = ids[val.phys_row(seg, q - seg * val.seglen)];
+  if (id < 0 || id >= vocab || table[id] != q) return;
+  const double inv = 1.0 / emb_scale(*maxbits, val.total());
+  for (int64_t f = threadIdx.x; f < d; f += blockDim.x)
+    vrow[q * d + f] = static_cast<float>(static_cast<double>(static_cast<long long>(fix[q * d + f])) * inv);
+}
+
+// part[i * chunks + c] = sum over train row i's tokens in chunk c of <g_it, V[x_it]>.
+template <class E>
+__global__ void emb_dot_kernel(const int64_t* __restrict__ ids, const E* __restrict__ G,
+                               RowMap train, int64_t d, int64_t vocab,
+                               const int32_t* __restrict__ table, const float* __restrict__ vrow,
+                               int64_t chunks, float* __restrict__ part) {
+  __shared__ float red[BW_THREADS / 64];
+  const int64_t i = blockIdx.y, c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t T = train.seglen;
+  const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
+  float s = 0.f;
+  for (int64_t t = t0 + wid; t < t1; t += 4) {
+    const int64_t row = train.phys_row(i, t);
+    const int64_t id = ids[row];
+    if (id < 0 || id >= vocab) continue;
+    const int32_t rep = table[id];
+    if (rep == INT32_MAX) continue;
+    const float* vr = vrow + static_cast<int64_t>(rep) * d;
+    const E* gr = G + row * d;
+    for (int64_t f = lane; f < d; f += 64) s += ld(gr + f) * vr[f];
+  }
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) part[i * chunks + c] = s;
+}
+
+__global__ void sum_chunks_kernel(const float* __restrict__ part, int64_t chunks,
+                                  float* __restrict__ out) {
+  __shared__ float red[BW_THREADS / 64];
+  const int64_t i = blockIdx.x;
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < chunks; c += blockDim.x) s += part[i * chunks + c];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) out[i] = s;
+}
+
+namespace {
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <class S>
+void carve_feature(S& c, int64_t N, int64_t T, int64_t F, int two) {
+  const int64_t chunks = cdiv(T, TOK_CHUNK);
+  c.template take<float>(N * chunks * F);  // part w (or bias)
+  if (two) c.template take<float>(N * chunks * F);
+  c.template take<float>(N * F);  // S
+  if (two) c.template take<float>(N * F);
+  c.template take<float>(F);  // sval
+  if (two) c.template take<float>(F);
+}
+
+template <class GE>
+int finish_feature(const float* part, int64_t N, int64_t chunks, int64_t F, int64_t n_val,
+                   int64_t val_start, int64_t T, float* S, float* sval, void* grad,
+                   float grad_scale, float* out_dot, hipStream_t s) {
+  hipLaunchKernelGGL(feature_sample_totals_kernel,
+                     dim3(static_cast<unsigned>(cdiv(F, 64)), static_cast<unsigned>(N)), dim3(64),
+                     0, s, part, chunks, F, S);
+  hipLaunchKernelGGL(feature_val_totals_kernel<GE>, dim3(static_cast<unsigned>(cdiv(F, 64))),
+                     dim3(64), 0, s, S, N, F, n_val, val_start, sval, static_cast<GE*>(grad),
+                     grad_scale);
+  if (out_dot != nullptr)
+    hipLaunchKernelGGL(feature_dots_kernel, dim3(static_cast<unsigned>(N - n_val)),
+                       dim3(BW_THREADS), 0, s, S, sval, F, train_rows(N, n_val, val_start, T),
+                       out_dot);
+  return check_launch("feature_totals/dots");
+}
+
+int finish_feature_any(int grad_dtype, const float* part, int64_t N, int64_t chunks, int64_t F,
+                       int64_t n_val, int64_t val_start, int64_t T, float* S, float* sval,
+                       void* grad, float grad_scale, float* out_dot, hipStream_t s) {
+  if (grad_dtype == GS_DTYPE_F32)
+    return finish_feature<float>(part, N, chunks, F, n_val, val_start, T, S, sval, grad,
+                                 grad_scale, out_dot, s);
+  return finish_feature<uint16_t>(part, N, chunks, F, n_val, val_start, T, S, sval, grad,
+                                  grad_scale, out_dot, s);
+}
+
+bool batch_ok(int64_t N, int64_t n_val, int64_t val_start, int64_t T, int64_t F) {
+  return N > 0 && n_val > 0 && n_val < N && val_start >= 0 && val_start + n_val <= N && T > 0 &&
+         F > 0;
+}
+
+template <class E, int PL>
+void launch_ln(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
+               int64_t chunks, float* pw, float* pb, hipStream_t s) {
+  const size_t lds = 8 * F * sizeof(float);
+  hipLaunchKernelGGL((ln_sums_kernel<E, PL>),
+                     dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(N)),
+                     dim3(BW_THREADS), lds, s, static_cast<const E*>(X),
+                     static_cast<const E*>(G), T, F, eps, chunks, pw, pb);
+}
+
+template <class E>
+int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
+                  int64_t chunks, float* pw, float* pb, hipStream_t s) {
+  const int64_t pl = cdiv(F, 64);
+  if (pl <= 4)
+    launch_ln<E, 4>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  else if (pl <= 8)
+    launch_ln<E, 8>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  else if (pl <= 16)
+    launch_ln<E, 16>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  else if (pl <= 32)
+    launch_ln<E, 32>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  else
+    return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: F > 2048 not supported");
+  return check_launch("ln_sums_kernel");
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+// ------------------------------------------------------------------------------ bias
+extern "C" size_t gs_bias_dot_workspace(int64_t N, int64_t T, int64_t d_out) {
+  if (N <= 0 || T <= 0 || d_out <= 0) return 0;
+  Sizer sz;
+  carve_feature(sz, N, T, d_out, 0);
+  return sz.used + 256;
+}
+
+extern "C" int gs_bias_dot(const void* G, int dtype, int64_t N, int64_t n_val, int64_t val_start,
+                           int64_t T, int64_t d_out, float* out_dot, void* out_grad,
+                           int grad_dtype, float grad_scale, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_bias_dot: dtype must be bf16 or fp32");
+  if (grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_bias_dot: grad_dtype must be bf16 or fp32");
+  if (!batch_ok(N, n_val, val_start, T, d_out) || G == nullptr)
+    return fail(GS_ERR_INVALID, "gs_bias_dot: invalid arguments");
+  Sizer sz;
+  carve_feature(sz, N, T, d_out, 0);
+  if (workspace == nullptr || workspace_bytes < sz.used)
+    return fail(GS_ERR_WORKSPACE, "gs_bias_dot: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  const int64_t chunks = cdiv(T, TOK_CHUNK);
+  float* part = cv.take<float>(N * chunks * d_out);
+  float* S = cv.take<float>(N * d_out);
+  float* sval = cv.take<float>(d_out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(N));
+  if (dtype == GS_DTYPE_BF16)
+    hipLaunchKernelGGL(colsum_kernel<uint16_t>, grid, dim3(BW_THREADS), 0, s,
+                       static_cast<const uint16_t*>(G), T, d_out, chunks, part);
+  else
+    hipLaunchKernelGGL(colsum_kernel<float>, grid, dim3(BW_THREADS), 0, s,
+                       static_cast<const float*>(G), T, d_out, chunks, part);
+  int rc = check_launch("colsum_kernel");
+  if (rc) return rc;
+  return finish_feature_any(grad_dtype, part, N, chunks, d_out, n_val, val_start, T, S, sval,
+                            out_grad, grad_scale, out_dot, s);
+}
+
+// ------------------------------------------------------------------------------ layernorm
+extern "C" size_t gs_layernorm_dot_workspace(int64_t N, int64_t T, int64_t F) {
+  if (N <= 0 || T <= 0 || F <= 0) return 0;
+  Sizer sz;
+  carve_feature(sz, N, T, F, 1);
+  return sz.used + 256;
+}
+
+extern "C" int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t N, int64_t n_val,
+                                int64_t val_start, int64_t T, int64_t F, float eps,
+                                float* out_dot_w, float* out_dot_b, void* out_grad_w,
+                                void* out_grad_b, int grad_dtype, float grad_scale,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_layernorm_dot: dtype must be bf16 or fp32");
+  if (grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_layernorm_dot: grad_dtype must be bf16 or fp32");
+  if (!batch_ok(N, n_val, val_start, T, F) || X == nullptr || G == nullptr)
+    return fail(GS_ERR_INVALID, "gs_layernorm_dot: invalid arguments");
+  if (F > 2048) return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: F > 2048 not supported");
+  Sizer sz;
+  carve_feature(sz, N, T, F, 1);
+  if (workspace == nullptr || workspace_bytes < sz.used)
+    return fail(GS_ERR_WORKSPACE, "gs_layernorm_dot: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  const int64_t chunks = cdiv(T, TOK_CHUNK);
+  float* pw = cv.take<float>(N * chunks * F);
+  float* pb = cv.take<float>(N * chunks * F);
+  float* Sw = cv.take<float>(N * F);
+  float* Sb = cv.take<float>(N * F);
+  float* vw = cv.take<float>(F);
+  float* vb = cv.take<float>(F);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = dtype == GS_DTYPE_BF16
+               ? launch_ln_any<uint16_t>(X, G, N, T, F, eps, chunks, pw, pb, s)
+               : launch_ln_any<float>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  if (rc) return rc;
+  rc = finish_feature_any(grad_dtype, pw, N, chunks, F, n_val, val_start, T, Sw, vw, out_grad_w,
+                          grad_scale, out_dot_w, s);
+  if (rc) return rc;
+  if (out_dot_b != nullptr || out_grad_b != nullptr)
+    rc = finish_feature_any(grad_dtype, pb, N, chunks, F, n_val, val_start, T, Sb, vb,
+                            out_grad_b, grad_scale, out_dot_b, s);
+  return rc;
+}
+
+// ------------------------------------------------------------------------------ embedding
+namespace {
+template <class S>
+void carve_embedding(S& c, int64_t N, int64_t n_val, int64_t T, int64_t d, int64_t vocab) {
+  const int64_t n_vt = n_val * T, n_t = N - n_val, chunks = cdiv(T, TOK_CHUNK);
+  c.template take<int32_t>(vocab);
+  c.template take<unsigned>(4);
+  c.template take<unsigned long long>(n_vt * d);
+  c.template take<float>(n_vt * d);
+  c.template take<float>(n_t * chunks);
+}
+}  // namespace
+
+extern "C" size_t gs_embedding_dot_workspace(int64_t N, int64_t n_val, int64_t T, int64_t d,
+                                             int64_t vocab) {
+  if (N <= 0 || n_val <= 0 || n_val >= N || T <= 0 || d <= 0 || vocab <= 0) return 0;
+  Sizer sz;
+  carve_embedding(sz, N, n_val, T, d, vocab);
+  return sz.used + 256;
+}
+
+extern "C" int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, int64_t N,
+                                int64_t n_val, int64_t val_start, int64_t T, int64_t d,
+                                int64_t vocab, float* out_dot, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_embedding_dot: dtype must be bf16 or fp32");
+  if (!batch_ok(N, n_val, val_start, T, d) || ids == nullptr || G == nullptr || vocab <= 0 ||
+      out_dot == nullptr)
+    return fail(GS_ERR_INVALID, "gs_embedding_dot: invalid arguments");
+  if (n_val * T >= INT32_MAX || vocab >= INT32_MAX)
+    return fail(GS_ERR_UNSUPPORTED, "gs_embedding_dot: more than 2^31 val tokens or ids");
+  Sizer sz;
+  carve_embedding(sz, N, n_val, T, d, vocab);
+  if (workspace == nullptr || workspace_bytes < sz.used)
+    return fail(GS_ERR_WORKSPACE, "gs_embedding_dot: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  const int64_t n_vt = n_val * T, n_t = N - n_val, chunks = cdiv(T, TOK_CHUNK);
+  int32_t* table = cv.take<int32_t>(vocab);
+  unsigned* maxbits = cv.take<unsigned>(4);
+  unsigned long long* fix = cv.take<unsigned long long>(n_vt * d);
+  float* vrow = cv.take<float>(n_vt * d);
+  float* part = cv.take<float>(n_t * chunks);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const RowMap va = val_rows(n_val, val_start, T);
+  const RowMap tr = train_rows(N, n_val, val_start, T);
+
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(vocab, 256), 4096))),
+                     dim3(256), 0, s, table, vocab, INT32_MAX);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<int32_t*>(maxbits),
+                     int64_t{1}, 0);
+  const dim3 gv(static_cast<unsigned>(n_vt));
+  if (dtype == GS_DTYPE_BF16)
+    hipLaunchKernelGGL(emb_index_kernel<uint16_t>, gv, dim3(BW_THREADS), 0, s, ids,
+                       static_cast<const uint16_t*>(G), va, d, vocab, table, maxbits);
+  else
+    hipLaunchKernelGGL(emb_index_kernel<float>, gv, dim3(BW_THREADS), 0, s, ids,
+                       static_cast<const float*>(G), va, d, vocab, table, maxbits);
+  hipLaunchKernelGGL(emb_zero_kernel, gv, dim3(BW_THREADS), 0, s, ids, va, d, vocab, table, fix);
+  if (dtype == GS_DTYPE_BF16)
+    hipLaunchKernelGGL(emb_accum_kernel<uint16_t>, gv, dim3(BW_THREADS), 0, s, ids,
+                       static_cast<const uint16_t*>(G), va, d, vocab, table, maxbits, fix);
+  else
+    hipLaunchKernelGGL(emb_accum_kernel<float>, gv, dim3(BW_THREADS), 0, s, ids,
+                       static_cast<const float*>(G), va, d, vocab, table, maxbits, fix);
+  hipLaunchKernelGGL(emb_finish_kernel, gv, dim3(BW_THREADS), 0, s, ids, va, d, vocab, table,
+                     maxbits, fix, vrow);
+  const dim3 gt(static_cast<unsigned>(chunks), static_cast<unsigned>(n_t));
+  if (dtype == GS_DTYPE_BF16)
+    hipLaunchKernelGGL(emb_dot_kernel<uint16_t>, gt, dim3(BW_THREADS), 0, s, ids,
+                       static_cast<const uint16_t*>(G), tr, d, vocab, table, vrow, chunks, part);
+  else
+    hipLaunchKernelGGL(emb_dot_kernel<float>, gt, dim3(BW_THREADS), 0, s, ids,
+                       static_cast<const float*>(G), tr, d, vocab, table, vrow, chunks, part);
+  hipLaunchKernelGGL(sum_chunks_kernel, dim3(static_cast<unsigned>(n_t)), dim3(BW_THREADS), 0, s,
+                     part, chunks, out_dot);
+  return check_launch("embedding kernels");
+}

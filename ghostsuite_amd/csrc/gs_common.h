@@ -1,0 +1,126 @@
+// Shared helpers for the gfx950 kernels of libghost_hip.so: status/error plumbing,
+// bf16 conversions, row maps for the train/val batch split, and wave reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+
+#include "../../include/ghost_hip.h"
+
+namespace gs {
+
+// ---------------------------------------------------------------- error plumbing
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+// Checks the launch status of the kernels enqueued so far by this thread.
+int check_launch(const char* what);
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Carves aligned sub-buffers out of the caller's workspace.
+struct Carver {
+  char* base;
+  size_t used = 0;
+  size_t cap;
+  Carver(void* b, size_t c) : base(static_cast<char*>(b)), cap(c) {}
+  template <class T>
+  T* take(size_t n) {
+    used = align_up(used, 256);
+    T* p = reinterpret_cast<T*>(base + used);
+    used += n * sizeof(T);
+    return p;
+  }
+  bool ok() const { return used <= cap; }
+};
+
+// Sizes-only twin of Carver, used by the *_workspace() queries.
+struct Sizer {
+  size_t used = 0;
+  template <class T>
+  void take(size_t n) {
+    used = align_up(used, 256);
+    used += n * sizeof(T);
+  }
+};
+
+inline size_t elem_size(int dtype) {
+  return dtype == GS_DTYPE_F32 ? 4 : 2;
+}
+
+// ---------------------------------------------------------------- bf16 helpers
+// bf16 values travel as raw uint16_t bits; conversions use round-to-nearest-even.
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+template <class E>
+__device__ __forceinline__ float to_f32(E v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+
+template <class E>
+__device__ __forceinline__ E from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ uint16_t from_f32<uint16_t>(float v) { return f32_to_bf16(v); }
+
+// ---------------------------------------------------------------- batch row maps
+// A set of rows drawn from a [N, T, ld] tensor: `nseg` segments (samples) of `seglen`
+// rows (tokens) each.  Segment s lives at physical sample seg_offset + s, plus skip_n when
+// s >= skip_at; this expresses "the train rows" (seg_offset 0, skip the val block) and
+// "the val rows" (seg_offset val_start, no skip) of one batch.
+struct RowMap {
+  int64_t nseg;
+  int64_t seglen;
+  int64_t seg_offset;
+  int64_t skip_at;
+  int64_t skip_n;
+  __host__ __device__ int64_t phys_sample(int64_t s) const {
+    return seg_offset + s + (s >= skip_at ? skip_n : 0);
+  }
+  __host__ __device__ int64_t phys_row(int64_t s, int64_t pos) const {
+    return phys_sample(s) * seglen + pos;
+  }
+  __host__ __device__ int64_t total() const { return nseg * seglen; }
+};
+
+inline RowMap train_rows(int64_t N, int64_t n_val, int64_t val_start, int64_t T) {
+  return RowMap{N - n_val, T, 0, val_start, n_val};
+}
+inline RowMap val_rows(int64_t n_val, int64_t val_start, int64_t T) {
+  return RowMap{n_val, T, val_start, INT64_MAX, 0};
+}
+inline RowMap plain_rows(int64_t rows) { return RowMap{1, rows, 0, INT64_MAX, 0}; }
+
+// ---------------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Block-wide sum; `red` must hold blockDim.x/64 floats.  Result is valid in every thread.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int w = 0; w < nw; ++w) s += red[w];
+  return s;
+}
+
+}  // namespace gs

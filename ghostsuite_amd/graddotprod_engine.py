@@ -1,0 +1,174 @@
+"""GradDotProdEngine: in-run gradient dot products between a val batch and each train row.
+
+Public behaviour mirrors ghostEngines/graddotprod_engine.py (constructor, attach/detach,
+prepare_gradients, clear_gradients, aggregate_and_log, save_dot_product_log,
+attach_and_store_valset, attach_train_batch, the dot_product_log record format).  Extra
+keyword arguments set the sampler options of
+``supported_layers_grad_samplers_dotprod.options`` (precision, linear_algo, rounding,
+store_pairs, skip_overwritten_tied_dots, record_algorithms).
+"""
+from __future__ import annotations
+
+import os
+import warnings
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import autograd_grad_sample_dotprod
+from . import transformers_support
+from . import supported_layers_grad_samplers_dotprod as _samplers
+
+
+class GradDotProdEngine:
+    """Computes per-train-row dot products with the val gradient during backward and
+    supplies the train-row gradient to the optimizer."""
+
+    def __init__(self, module: nn.Module, val_batch_size: int, loss_reduction: str = 'mean',
+                 use_dummy_bias: bool = False, dot_prod_save_path: Optional[str] = None,
+                 **sampler_options):
+        super().__init__()
+        unknown = set(sampler_options) - set(_samplers.options)
+        if unknown:
+            raise TypeError(f"unknown GradDotProdEngine options: {sorted(unknown)}")
+        _samplers.options.update(sampler_options)
+
+        self.module = module
+        self.val_batch_size = val_batch_size
+        self.loss_reduction = loss_reduction
+        self.dot_prod_save_path = dot_prod_save_path
+        self.named_params = list((n, p) for (n, p) in module.named_parameters() if p.requires_grad)
+        self._grad_creation_locked = False
+        self.dot_product_log = []
+        self.batch_idx_lst = []
+
+        # Dummy-bias trick (reference :64-73): remember trainability, then let autograd skip
+        # every weight-grad GEMM when enabled; the hooks supply the train gradients.
+        for _, param in module.named_parameters():
+            param.initially_requires_grad = bool(param.requires_grad)
+            param.requires_grad = not use_dummy_bias
+
+        transformers_support.forward_swapper(module=module)
+
+    def _lock_grad_creation(self):
+        self._grad_creation_locked = True
+
+    def _unlock_grad_creation(self):
+        self._grad_creation_locked = False
+
+    def attach(self, optimizer: torch.optim.Optimizer):
+        """Registers the hooks and keeps a back-reference on the optimizer."""
+        self.optimizer = optimizer
+        autograd_grad_sample_dotprod.add_hooks(model=self.module,
+                                               val_batch_size=self.val_batch_size,
+                                               loss_reduction=self.loss_reduction)
+        optimizer.grad_dot_prod_engine = self
+
+    def detach(self):
+        """Removes the hooks and the engine's per-parameter attributes."""
+        optimizer = self.optimizer
+        if hasattr(optimizer, "grad_dot_prod_engine"):
+            del optimizer.grad_dot_prod_engine
+        autograd_grad_sample_dotprod.remove_hooks(self.module)
+        self.module.zero_grad()
+        for param in self.module.parameters():
+            for attr in ('train_grad', 'grad_dot_prod', 'grad_dot_prod_pair', 'activations',
+                         'backprops'):
+                if hasattr(param, attr):
+                    delattr(param, attr)
+
+    def _prepare_and_apply_train_grad(self):
+        """Moves ``param.train_grad`` into ``param.grad`` (reference :131-163)."""
+        if self._grad_creation_locked:
+            return
+        for name, param in self.module.named_parameters():
+            if not param.initially_requires_grad:
+                continue
+            if "dummy_bias" in name:
+                continue
+            if hasattr(param, 'train_grad'):
+                if param.train_grad is None:
+                    raise ValueError(
+                        f"Parameter {name} requires grad has no accumulated training gradient. ")
+                param.grad = param.train_grad
+            else:
+                raise ValueError(
+                    f"Parameter {name} requires grad but does not have 'train_grad' attribute. ")
+        self._lock_grad_creation()
+
+    def _clear_train_grad(self):
+        for param in self.module.parameters():
+            if hasattr(param, 'train_grad'):
+                del param.train_grad
+        self._unlock_grad_creation()
+
+    def prepare_gradients(self):
+        """Move accumulated training gradients to ``.grad`` for the optimizer."""
+        self._prepare_and_apply_train_grad()
+
+    def clear_gradients(self):
+        """Remove stored training gradients after the optimizer step."""
+        self._clear_train_grad()
+
+    def aggregate_and_log(self):
+        """Aggregate per-layer dot products and append them to the log."""
+        self._aggregate_and_log_dot_products()
+
+    def _aggregate_and_log_dot_products(self):
+        """Sums ``grad_dot_prod`` over parameters in ``named_parameters`` order -- the first
+        tensor accumulates the rest in place -- and logs a CPU copy (reference :192-230)."""
+        total = None
+        for _, param in self.module.named_parameters():
+            if hasattr(param, 'grad_dot_prod') and param.initially_requires_grad:
+                if param.grad_dot_prod.numel() > 0:
+                    if total is None:
+                        total = param.grad_dot_prod
+                    else:
+                        total += param.grad_dot_prod
+                delattr(param, 'grad_dot_prod')
+            if hasattr(param, 'grad_dot_prod_pair'):
+                delattr(param, 'grad_dot_prod_pair')
+        if total is not None:
+            self.dot_product_log.append({
+                'dot_product': to_device(total, 'cpu'),
+                'X_train': to_device(self.X_train, 'cpu'),
+                'Y_train': to_device(self.Y_train, 'cpu'),
+                'iter_num': self.iter_num,
+                'batch_idx': self.batch_idx,
+            })
+        else:
+            warnings.warn("No gradient dot products computed for this iteration.")
+
+    def save_dot_product_log(self, iter_num: int):
+        """Writes ``dot_prod_log_iter_{iter_num}.pt`` (a list of the per-step records)."""
+        if not self.dot_product_log:
+            raise ValueError("No gradient dot products found to save for this iteration.")
+        print(f"[INFO] Saving dot product log at iteration {iter_num} ...")
+        file_path = os.path.join(self.dot_prod_save_path, f"dot_prod_log_iter_{iter_num}.pt")
+        torch.save(self.dot_product_log, file_path)
+        self.dot_product_log.clear()
+
+    def attach_and_store_valset(self, X_val, Y_val):
+        """Writes ``valset.pt`` = {'X_val', 'Y_val'} on the CPU."""
+        valset_path = os.path.join(self.dot_prod_save_path, "valset.pt")
+        torch.save({'X_val': to_device(X_val, 'cpu'), 'Y_val': to_device(Y_val, 'cpu')},
+                   valset_path)
+        print(f"[INFO] Saved validation set to {valset_path}")
+
+    def attach_train_batch(self, X_train, Y_train, iter_num, batch_idx=None):
+        """Records the current train batch for the log."""
+        self.X_train = X_train
+        self.Y_train = Y_train
+        self.iter_num = iter_num
+        self.batch_idx = batch_idx
+
+
+def to_device(data, device):
+    """Move a tensor, or each tensor of a dict, to ``device``."""
+    if isinstance(data, dict):
+        return {k: v.to(device) if hasattr(v, 'to') else v for k, v in data.items()}
+    elif hasattr(data, 'to'):
+        return data.to(device)
+    raise TypeError(f"Unsupported data type for moving to GPU: {type(data)}. "
+                    "Expected tensor or dict of tensors.")

@@ -1,0 +1,316 @@
+"""Per-layer samplers of the GradDotProd engine, backed by the gfx950 kernels.
+
+Same registry, function names, signatures, side effects and exceptions as the reference
+(ghostEngines/supported_layers_grad_samplers_dotprod.py); the arithmetic runs in
+libghost_hip.so (one C-ABI call per sampler, asynchronous on the current stream).
+
+Semantics kept from the reference:
+  - the ghost/materialise switch 2*T^2 <= weight.numel(), cached on the layer (:7-41);
+  - nn.Linear: ghost branch = pairwise-sum over val rows, materialised branch = presum
+    (:108-135); HF Conv1D: presum in both branches (:369-447);
+  - bias dots <sum_t b_it, sum_{j,t} b_jt> (:137-146);
+  - embedding dot through token-id equality (:181-211), LayerNorm weight/bias dots (:242-300);
+  - train gradients averaged over the train rows of the N-scaled backprops, accumulated
+    into ``param.train_grad`` (:44-69).
+Algorithm choice inside a semantics is this build's (``options['linear_algo']``): the fused
+ghost kernel or the val-gradient form, by MFMA flop count when 'auto'.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import _native
+from ._native import ops
+
+try:  # HF Conv1D is a registry key only when transformers is importable
+    import transformers.pytorch_utils as _hf_utils
+    _HFConv1D = _hf_utils.Conv1D
+except Exception:  # pragma: no cover - transformers absent
+    _HFConv1D = None
+
+# Engine-wide knobs (set through GradDotProdEngine(**options) or directly).
+#   precision:     'reference' -- bf16 operands for the ghost/pairwise path (the reference
+#                  casts A, B to bf16, :92-93), original dtype for presum (:104-105);
+#                  'fp32' -- no down-casts (fp32 operands everywhere).
+#   linear_algo:   'auto' | 'ghost' | 'valgrad'
+#   rounding:      'fp32' | 'ref_bf16' (ghost Gram entries rounded to bf16 like the
+#                  reference's bf16 matmul outputs)
+#   store_pairs:   also keep the [n_val, n_train] per-pair matrix on pairwise-sum Linear
+#                  layers as ``weight.grad_dot_prod_pair``
+#   skip_overwritten_tied_dots: skip a tied Linear weight's dot when the Embedding that
+#                  shares the weight runs later in backward and overwrites it (:130 vs :211)
+#   record_algorithms: keep {layer name: algorithm} in ``ALGO_LOG``
+options = {
+    "precision": "reference",
+    "linear_algo": "auto",
+    "rounding": "fp32",
+    "store_pairs": False,
+    "skip_overwritten_tied_dots": True,
+    "record_algorithms": False,
+}
+ALGO_LOG: dict = {}
+
+_ALGOS = {"auto": _native.ALGO_AUTO, "ghost": _native.ALGO_GHOST, "valgrad": _native.ALGO_VALGRAD}
+_ROUNDINGS = {"fp32": _native.ROUND_FP32, "ref_bf16": _native.ROUND_REF_BF16}
+
+
+def _should_use_ghost_computation(layer: nn.Module, A: torch.Tensor, B: torch.Tensor,
+                                  conv: bool = False):
+    """Caches ``layer.use_ghost_computation = 2*T^2 <= weight.numel()`` on the first call
+    (reference :7-41; never reset)."""
+    if hasattr(layer, "use_ghost_computation"):
+        return
+    if not conv:
+        T = math.prod(A.shape[1:-1]) if A.dim() > 2 else 1
+    else:
+        T = A.shape[-1]
+    layer.use_ghost_computation = bool(2 * T ** 2 <= layer.weight.numel())
+
+
+def _create_or_accumulate_train_grad(param: torch.Tensor, grad: torch.Tensor) -> None:
+    """Stores or adds ``grad`` into ``param.train_grad`` (reference :44-69)."""
+    assert grad.shape == param.shape, \
+        f"Gradient shape ({grad.shape}) does not match parameter shape ({param.shape})"
+    new_grad = grad.detach()
+    if hasattr(param, 'train_grad'):
+        param.train_grad.add_(new_grad)
+    else:
+        param.train_grad = new_grad
+
+
+def _train_split(A: torch.Tensor, val_batch_size: int):
+    n_t = A.size(0) - val_batch_size
+    return n_t, A[:n_t]
+
+
+def _dot_dtype(x: torch.Tensor, pairwise: bool) -> torch.dtype:
+    if options["precision"] == "fp32":
+        return torch.float32
+    if pairwise:
+        return torch.bfloat16
+    return x.dtype if x.dtype in (torch.bfloat16, torch.float32) else torch.float32
+
+
+def _overwritten_later(layer: nn.Module) -> bool:
+    """True when this Linear's weight is tied to a hooked Embedding whose forward ran
+    earlier in the current step, so the Embedding's backward hook runs later and its
+    assignment of ``grad_dot_prod`` replaces this layer's."""
+    if not options["skip_overwritten_tied_dots"]:
+        return False
+    emb = getattr(layer, "_gs_tied_embedding", None)
+    if emb is None:
+        return False
+    mine, theirs = getattr(layer, "_gs_fwd_seq", None), getattr(emb, "_gs_fwd_seq", None)
+    return mine is not None and theirs is not None and theirs[0] == mine[0] and theirs[1] < mine[1]
+
+
+def _bias_dot_and_grad(layer: nn.Module, B: torch.Tensor, val_batch_size: int,
+                       dtype: torch.dtype) -> None:
+    """Bias dot (reference :137-146); when the hook announced the train-grad scale, the
+    same pass also produces the bias train gradient and parks it for _apply_train_grad."""
+    scale = getattr(layer, "_gs_bias_grad_scale", None)
+    dot, grad = ops().bias_dot(B.to(dtype) if B.dtype != dtype else B, val_batch_size,
+                               grad_scale=scale, grad_dtype=layer.bias.dtype)
+    layer.bias.grad_dot_prod = dot
+    if grad is not None:
+        layer._gs_bias_train_grad = grad
+
+
+# Linear Layer ##############################################################################
+
+def _linear_like_dot(layer: nn.Module, A: torch.Tensor, B: torch.Tensor, val_batch_size: int,
+                     pairwise: bool, dtype: torch.dtype) -> None:
+    if options["store_pairs"] and pairwise:
+        want_pair = True
+    else:
+        want_pair = False
+    Ac = A.to(dtype) if A.dtype != dtype else A
+    Bc = B.to(dtype) if B.dtype != dtype else B
+    sem = _native.SEM_PAIRWISE_SUM if pairwise else _native.SEM_PRESUM
+    algo = _ALGOS[options["linear_algo"]]
+    if options["record_algorithms"]:
+        N, d_in, d_out = Ac.shape[0], Ac.shape[-1], Bc.shape[-1]
+        T = Ac.numel() // (N * d_in)
+        chosen = ops().linear_algo(dtype, N, val_batch_size, T, d_in, d_out, sem, algo,
+                                   want_pair)
+        ALGO_LOG[getattr(layer, "name", id(layer))] = (
+            "pairwise" if pairwise else "presum", _native.ALGO_NAMES.get(chosen, str(chosen)))
+    dot, pair = ops().linear_dot(Ac, Bc, val_batch_size, semantics=sem, algo=algo,
+                                 rounding=_ROUNDINGS[options["rounding"]], want_pair=want_pair)
+    layer.weight.grad_dot_prod = dot
+    if pair is not None:
+        layer.weight.grad_dot_prod_pair = pair
+
+
+def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tensor,
+                                val_batch_size: int):
+    """Gradient dot-product of an nn.Linear layer (reference :75-146).
+
+    Sets ``layer.weight.grad_dot_prod`` ([n_train] fp32) and, with a bias,
+    ``layer.bias.grad_dot_prod``.
+    """
+    if A is None:
+        raise ValueError("Input activations A cannot be None.")
+    if B is None:
+        raise ValueError("Output gradients B cannot be None.")
+    A = A.detach()
+    B = B.detach()
+    train_bs = A.size(0) - val_batch_size
+    if train_bs <= 0:
+        raise ValueError("No training samples to compute dot product, check batch sizes.")
+    _should_use_ghost_computation(layer, A, B)
+    pairwise = layer.use_ghost_computation
+    if not _overwritten_later(layer):
+        _linear_like_dot(layer, A, B, val_batch_size, pairwise, _dot_dtype(A, pairwise))
+    if layer.bias is not None:
+        _bias_dot_and_grad(layer, B, val_batch_size, _dot_dtype(B, False))
+
+
+def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tensor,
+                               val_batch_size: int, scale: float = 1.0):
+    """scale * sum_train B^T A / n_train (reference :155-173, with B pre-scaled there;
+    here the N-scaling of the backprops may be passed as ``scale``)."""
+    n_t = A.size(0) - val_batch_size
+    if n_t <= 0:
+        return None
+    A_tr = A[:n_t].reshape(-1, A.shape[-1])
+    B_tr = B[:n_t].reshape(-1, B.shape[-1])
+    if B_tr.dtype != A_tr.dtype:
+        B_tr = B_tr.to(A_tr.dtype)
+    grad = torch.mm(B_tr.t(), A_tr)
+    grad.mul_(scale / n_t)
+    return grad
+
+
+# Embedding Layer ###########################################################################
+
+def _compute_embedding_dot_product(layer: nn.Embedding, A: torch.Tensor, B: torch.Tensor,
+                                   val_batch_size: int):
+    """Gradient dot-product of an nn.Embedding (reference :181-211)."""
+    A = A.detach()
+    B = B.detach()
+    train_bs = A.size(0) - val_batch_size
+    if train_bs <= 0:
+        raise ValueError("No training samples to compute dot product, check batch sizes.")
+    if options["precision"] == "fp32" and B.dtype != torch.float32:
+        B = B.float()
+    elif B.dtype not in (torch.bfloat16, torch.float32):
+        B = B.float()
+    layer.weight.grad_dot_prod = ops().embedding_dot(A, B, val_batch_size,
+                                                     vocab=layer.weight.shape[0])
+
+
+def _compute_embedding_train_grad(layer: nn.Embedding, A: torch.Tensor, B: torch.Tensor,
+                                  val_batch_size: int, scale: float = 1.0):
+    """scale * index_add of the train rows / n_train (reference :214-235)."""
+    n_t = A.size(0) - val_batch_size
+    if n_t <= 0:
+        return None
+    grad = torch.zeros_like(layer.weight)
+    grad.index_add_(0, A[:n_t].long().reshape(-1),
+                    B[:n_t].reshape(-1, B.shape[-1]).to(grad.dtype))
+    grad.mul_(scale / n_t)
+    return grad
+
+
+# LayerNorm Layer ###########################################################################
+
+def _ln_features(layer: nn.LayerNorm) -> int:
+    if len(layer.normalized_shape) != 1:
+        raise NotImplementedError("LayerNorm over more than the last dimension is not supported")
+    return layer.normalized_shape[0]
+
+
+def _compute_layernorm_dot_product(layer: nn.LayerNorm, A: torch.Tensor, B: torch.Tensor,
+                                   val_batch_size: int):
+    """Weight/bias dot-products of an nn.LayerNorm (reference :242-300).  The same pass
+    produces the train gradients when the hook announced their scale."""
+    A = A.detach()
+    B = B.detach()
+    train_bs = A.size(0) - val_batch_size
+    if train_bs <= 0:
+        return
+    _ln_features(layer)
+    dt = torch.float32 if options["precision"] == "fp32" else (
+        A.dtype if A.dtype in (torch.bfloat16, torch.float32) else torch.float32)
+    Ac = A.to(dt) if A.dtype != dt else A
+    Bc = B.to(dt) if B.dtype != dt else B
+    scale = getattr(layer, "_gs_ln_grad_scale", None)
+    dw, db, gw, gb = ops().layernorm_dot(
+        Ac, Bc, val_batch_size, layer.eps, want_dot=True, want_bias=layer.bias is not None,
+        grad_scale=scale, grad_dtype=layer.weight.dtype)
+    layer.weight.grad_dot_prod = dw
+    if layer.bias is not None:
+        layer.bias.grad_dot_prod = db
+    if gw is not None:
+        layer._gs_ln_train_grads = (gw, gb)
+
+
+def _compute_layernorm_train_grad(layer: nn.LayerNorm, A: torch.Tensor, B: torch.Tensor,
+                                  val_batch_size: int, scale: float = 1.0) -> None:
+    """Applies the LayerNorm train gradients itself and returns None (reference :303-366)."""
+    train_bs = A.size(0) - val_batch_size
+    if train_bs <= 0:
+        raise ValueError("No training samples to compute gradients, check batch sizes.")
+    stash = layer.__dict__.pop("_gs_ln_train_grads", None)
+    if stash is None:
+        _ln_features(layer)
+        dt = A.dtype if A.dtype in (torch.bfloat16, torch.float32) else torch.float32
+        _, _, gw, gb = ops().layernorm_dot(
+            A.detach().to(dt), B.detach().to(dt), val_batch_size, layer.eps, want_dot=False,
+            want_bias=layer.bias is not None, grad_scale=scale / train_bs,
+            grad_dtype=layer.weight.dtype)
+    else:
+        gw, gb = stash
+    _create_or_accumulate_train_grad(layer.weight, gw)
+    if layer.bias is not None:
+        _create_or_accumulate_train_grad(layer.bias, gb)
+    return None
+
+
+# HF Conv1D (weight [d_in, d_out]) ##########################################################
+
+def _compute_Conv1D_dot_product(layer, A: torch.Tensor, B: torch.Tensor, val_batch_size: int):
+    """Conv1D dot-products (reference :369-471): presum in both branches, bf16."""
+    if A is None:
+        raise ValueError("Input activations A cannot be None.")
+    if B is None:
+        raise ValueError("Output gradients B cannot be None.")
+    A = A.detach()
+    B = B.detach()
+    train_bs = A.size(0) - val_batch_size
+    if train_bs <= 0:
+        raise ValueError("No training samples to compute dot product, check batch sizes.")
+    _should_use_ghost_computation(layer, A, B)
+    if A.dim() > 3:
+        raise ValueError("Currently we only expect 3D input tensors (batch, seq_len, features). "
+                         "Extending this to 4D or higher requires additional handling.")
+    dt = torch.float32 if options["precision"] == "fp32" else torch.bfloat16
+    _linear_like_dot(layer, A, B, val_batch_size, False, dt)
+    if layer.bias is not None:
+        _bias_dot_and_grad(layer, B, val_batch_size, dt)
+
+
+def _compute_Conv1D_train_grad(layer, A: torch.Tensor, B: torch.Tensor, val_batch_size: int,
+                               scale: float = 1.0) -> torch.Tensor:
+    """scale * sum_train A^T B / n_train, [d_in, d_out] (reference :474-506)."""
+    n_t = A.size(0) - val_batch_size
+    A_tr = A[:n_t].reshape(-1, A.shape[-1])
+    B_tr = B[:n_t].reshape(-1, B.shape[-1]).to(A_tr.dtype)
+    grad = torch.mm(A_tr.t(), B_tr)
+    grad.mul_(scale / n_t)
+    return grad
+
+
+_supported_layers_dotprod = {
+    nn.Linear: (_compute_linear_dot_product, _compute_linear_train_grad),
+    nn.Embedding: (_compute_embedding_dot_product, _compute_embedding_train_grad),
+    nn.LayerNorm: (_compute_layernorm_dot_product, _compute_layernorm_train_grad),
+}
+if _HFConv1D is not None:
+    _supported_layers_dotprod[_HFConv1D] = (_compute_Conv1D_dot_product,
+                                            _compute_Conv1D_train_grad)

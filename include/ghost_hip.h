@@ -1,0 +1,150 @@
+/*
+ * ghost_hip.h -- C ABI of libghost_hip.so, the MI355X (gfx950) kernels behind the
+ * per-sample-gradient samplers of GhostSuite.
+ *
+ * Conventions shared by every entry point
+ *   - All tensors are caller-owned device buffers, contiguous, row-major, batch outermost.
+ *   - A batch holds N = n_train + n_val rows (samples).  The n_val validation rows are the
+ *     contiguous block [val_start, val_start + n_val); the train rows are all other rows in
+ *     their original order, and output index i is the i-th train row.  The reference layout
+ *     (train first, val last; engine_manager.py:201-202, and every torch.split(A,
+ *     [train_bs, val_bs]) in supported_layers_grad_samplers_dotprod.py) is
+ *     val_start = N - n_val.
+ *   - T is the number of tokens per row (product of the middle dims; 1 for 2-D inputs).
+ *   - Outputs are fp32 unless stated.  Nothing is allocated: scratch memory comes from the
+ *     caller as (workspace, workspace_bytes), sized by the matching *_workspace() query.
+ *   - Every call is asynchronous on `stream` (a hipStream_t; NULL = default stream) and
+ *     makes no host synchronisation.  The caller keeps inputs alive until the stream
+ *     passes.  Functions are stateless and re-entrant.
+ *   - Return value: GS_OK or a negative gs_status; gs_last_error() returns a thread-local
+ *     message for the last failure on the calling thread.  The library never aborts.
+ */
+#ifndef GHOST_HIP_H
+#define GHOST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_ABI_VERSION 1
+
+typedef enum {
+  GS_OK = 0,
+  GS_ERR_INVALID = -1,     /* bad shape, size, pointer or enum value */
+  GS_ERR_DTYPE = -2,       /* dtype not supported by this entry point */
+  GS_ERR_WORKSPACE = -3,   /* workspace missing or smaller than the *_workspace() query */
+  GS_ERR_LAUNCH = -4,      /* a kernel launch or HIP runtime call failed */
+  GS_ERR_UNSUPPORTED = -5  /* valid request outside this build's limits */
+} gs_status;
+
+typedef enum { GS_DTYPE_BF16 = 0, GS_DTYPE_F32 = 1, GS_DTYPE_F16 = 2 } gs_dtype;
+
+/* Val-aggregation semantics of a Linear weight dot product.
+ *   PAIRWISE_SUM: dot_i = sum_{j in val} sum_{t,s} <a_it,a_js><b_it,b_js>
+ *                 (ghost branch, supported_layers_grad_samplers_dotprod.py:108-130)
+ *   PRESUM:       dot_i = sum_{t,s} <a_it,abar_s><b_it,bbar_s>, abar_s = sum_j a_js
+ *                 (materialised branch, supported_layers_grad_samplers_dotprod.py:131-135) */
+typedef enum { GS_SEM_PAIRWISE_SUM = 0, GS_SEM_PRESUM = 1 } gs_semantics;
+
+/* Algorithm used to evaluate a given semantics (the result is the same quantity).
+ *   GHOST:   fused dual-Gram MFMA kernel; the T x T Gram blocks live only in registers.
+ *   VALGRAD: V = sum_val B^T A (one GEMM), then dot_i = sum_t <b_it, V a_it> fused into
+ *            the epilogue of a second GEMM; per-sample gradients are never stored.
+ *   AUTO:    the one with fewer MFMA flops for the shape. */
+typedef enum { GS_ALGO_AUTO = 0, GS_ALGO_GHOST = 1, GS_ALGO_VALGRAD = 2 } gs_algo;
+
+/* Rounding of the ghost Gram blocks.
+ *   FP32:    Gram entries and their Hadamard product stay fp32.
+ *   REF_BF16: Gram entries and their product are rounded to bf16 before the fp32 sum, as
+ *            the reference's bf16 matmul outputs are (supported_layers_grad_samplers_dotprod.py:125-129). */
+typedef enum { GS_ROUND_FP32 = 0, GS_ROUND_REF_BF16 = 1 } gs_rounding;
+
+/* Layout of a Kronecker projection output block per sample.
+ *   KO_KI: [k_o, k_i] (nn.Linear, autograd_gradproj.py:155-158)
+ *   KI_KO: [k_i, k_o] with P_i applied to the output grads and P_o to the inputs
+ *          (transformers Conv1D, autograd_gradproj.py:141-147) */
+typedef enum { GS_PROJ_KO_KI = 0, GS_PROJ_KI_KO = 1 } gs_proj_layout;
+
+int gs_abi_version(void);
+const char* gs_last_error(void);
+
+/* ---- Linear weight dot product ------------------------------------------------------
+ * Replaces the weight part of _compute_linear_dot_product
+ * (ghostEngines/supported_layers_grad_samplers_dotprod.py:75-135), and the weight part of
+ * _compute_Conv1D_dot_product (:369-447, which is PRESUM in both of its branches).
+ * A: [N, T, d_in] layer inputs.  G: [N, T, d_out] output grads (raw grad_output of the loss).
+ * dtype: GS_DTYPE_BF16 or GS_DTYPE_F32 for both A and G.
+ * out_dot:  [n_train] fp32, dot of each train row's weight grad with the val aggregate.
+ * out_pair: NULL, or [n_val, n_train] fp32 with out_pair[j][i] = <grad_i, grad_j> (pairwise
+ *           semantics) -- the per-pair matrix; sum over j equals out_dot.  Must be NULL
+ *           for PRESUM. */
+size_t gs_linear_dot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
+                               int64_t d_out, int semantics, int algo, int want_pair);
+/* The algorithm (GS_ALGO_GHOST or GS_ALGO_VALGRAD) a call with these arguments runs. */
+int gs_linear_dot_algo(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
+                       int64_t d_out, int semantics, int algo, int want_pair);
+int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                  int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, int semantics,
+                  int algo, int rounding, float* out_dot, float* out_pair, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* ---- Bias dot product and bias train gradient ---------------------------------------
+ * Replaces the bias part of _compute_linear_dot_product (:137-146), the bias part of
+ * _compute_Conv1D_dot_product (:450-471) and _compute_train_grad_bias
+ * (ghostEngines/autograd_grad_sample_dotprod.py:199-222).
+ * G: [N, T, d_out].  out_dot: [n_train] = <sum_t g_it, sum_{j,t} g_jt>.
+ * out_grad: NULL, or [d_out] (dtype grad_dtype) = grad_scale * sum_{train i,t} g_it. */
+size_t gs_bias_dot_workspace(int64_t N, int64_t T, int64_t d_out);
+int gs_bias_dot(const void* G, int dtype, int64_t N, int64_t n_val, int64_t val_start,
+                int64_t T, int64_t d_out, float* out_dot, void* out_grad, int grad_dtype,
+                float grad_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Embedding dot product -----------------------------------------------------------
+ * Replaces _compute_embedding_dot_product (:181-211):
+ *   dot_i = sum_t <g_it, V[x_it]>,  V[v] = sum_{j in val, s : x_js = v} g_js
+ * without a [vocab, d] table: val tokens with equal ids form one segment (keyed by the
+ * first such val token through a [vocab] int32 index), segment sums are accumulated in
+ * 64-bit fixed point (deterministic), and each train token looks its segment up by id.
+ * ids: [N, T] int64 token ids in [0, vocab).  G: [N, T, d]. */
+size_t gs_embedding_dot_workspace(int64_t N, int64_t n_val, int64_t T, int64_t d,
+                                  int64_t vocab);
+int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, int64_t N, int64_t n_val,
+                     int64_t val_start, int64_t T, int64_t d, int64_t vocab, float* out_dot,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- LayerNorm dot products and train gradients -------------------------------------
+ * Replaces _compute_layernorm_dot_product (:242-300) and _compute_layernorm_train_grad
+ * (:303-366) in one pass over X and G.
+ * X: [N, T, F] LayerNorm inputs, G: [N, T, F] output grads, eps as in the layer.
+ *   xhat = (x - mean) * rsqrt(var + eps)   (biased variance, no affine)
+ *   out_dot_w[i] = <sum_t g_it*xhat_it, sum_{j,t} g_jt*xhat_jt>, out_dot_b likewise with g.
+ * out_dot_b may be NULL (no bias).  out_grad_w / out_grad_b: NULL or [F] of grad_dtype,
+ *   = grad_scale * sum_{train i,t} (g_it*xhat_it) and grad_scale * sum_{train i,t} g_it. */
+size_t gs_layernorm_dot_workspace(int64_t N, int64_t T, int64_t F);
+int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t N, int64_t n_val,
+                     int64_t val_start, int64_t T, int64_t F, float eps, float* out_dot_w,
+                     float* out_dot_b, void* out_grad_w, void* out_grad_b, int grad_dtype,
+                     float grad_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Kronecker gradient projection -----------------------------------------------------
+ * Replaces GradProjHooks._compute_dense_proj
+ * (ghostEngines/gradProjection/autograd_gradproj.py:120-165):
+ *   KO_KI: out[b] = scale * sum_t (P_o g_bt)(P_i a_bt)^T   [k_o, k_i]
+ *   KI_KO: out[b] = scale * sum_t (P_i g_bt)(P_o a_bt)^T   [k_i, k_o]  (Conv1D roles)
+ * A: [B, T, n_a], G: [B, T, n_g] (dtype), P_i / P_o: row-major projection matrices of
+ * p_dtype whose column counts match the operand each multiplies.
+ * out: [B, k_rows, k_cols] of out_dtype. */
+size_t gs_kron_proj_workspace(int64_t B, int64_t T, int64_t k_i, int64_t k_o);
+int gs_kron_proj(const void* A, const void* G, int dtype, int64_t B, int64_t T, int64_t n_a,
+                 int64_t n_g, const void* P_i, const void* P_o, int p_dtype, int64_t k_i,
+                 int64_t k_o, int layout, float scale, void* out, int out_dtype,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GHOST_HIP_H */

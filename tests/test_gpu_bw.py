@@ -1,0 +1,91 @@
+"""GPU parity of the Embedding, LayerNorm and Kronecker-projection kernels (C ABI)."""
+import pytest
+import torch
+
+from ghostsuite_amd import _native
+from oracle import ghost_ref as R
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, gen, randn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(6, 2, 5, 24, 11), (20, 4, 64, 96, 50), (10, 3, 33, 40, 3000)])
+def test_embedding_dot(gpu, dtype, shape):
+    N, n_val, T, d, vocab = shape
+    ids = torch.randint(0, vocab, (N, T), generator=gen(3 + T))
+    G = randn((N, T, d), 4 + T, 1e-3, dtype)
+    for val_start in (N - n_val, 0):
+        print(f"embedding shape={shape} dtype={dtype} val_start={val_start}", flush=True)
+        dot = _native.ops().embedding_dot(ids.to(gpu), G.to(gpu), n_val, vocab,
+                                          val_start=val_start)
+        torch.cuda.synchronize()
+        want = R.embedding_dot_exact(ids, G, n_val, val_start=val_start)
+        tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+        assert_close(dot.cpu(), want, tol, "embedding dot")
+
+
+def test_embedding_positions_and_all_equal_ids(gpu):
+    N, n_val, T, d = 8, 2, 40, 32
+    G = randn((N, T, d), 9, 1e-3)
+    pos = torch.arange(T).repeat(N, 1)   # per-sample position ids (wpe)
+    dot = _native.ops().embedding_dot(pos.to(gpu), G.to(gpu), n_val, T)
+    same = torch.full((N, T), 7)
+    dot2 = _native.ops().embedding_dot(same.to(gpu), G.to(gpu), n_val, 50)
+    torch.cuda.synchronize()
+    # positions: dot_i = sum_t <g_it, sum_j g_jt>
+    tr, va = G[:N - n_val].double(), G[N - n_val:].double()
+    assert_close(dot.cpu(), (tr * va.sum(0)).sum((1, 2)), FP32_TOL, "positions")
+    # one shared id: dot_i = <sum_t g_it, sum_{j,s} g_js>
+    assert_close(dot2.cpu(), tr.sum(1) @ va.sum((0, 1)), FP32_TOL, "all-equal ids")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100)])
+def test_layernorm_dots_and_grads(gpu, dtype, shape):
+    N, n_val, T, Fd = shape
+    X = randn((N, T, Fd), 11 + T, 2.0, dtype) + 0.5
+    G = randn((N, T, Fd), 12 + T, 1e-3, dtype)
+    n_t = N - n_val
+    print(f"layernorm shape={shape} dtype={dtype}", flush=True)
+    dw, db, gw, gb = _native.ops().layernorm_dot(X.to(gpu), G.to(gpu), n_val, 1e-5,
+                                                 grad_scale=N / n_t, grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ww, wb = R.layernorm_dot_exact(X, G, n_val, 1e-5)
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert_close(dw.cpu(), ww, tol, "ln weight dot")
+    assert_close(db.cpu(), wb, tol, "ln bias dot")
+    gw_ref, gb_ref = R.layernorm_train_grad(X.double(), G.double() * N, n_val, 1e-5)
+    assert_close(gw.cpu(), gw_ref, tol, "ln weight grad")
+    assert_close(gb.cpu(), gb_ref, tol, "ln bias grad")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("conf", [
+    # B, T, n_i, n_o, k_i, k_o
+    (3, 5, 24, 40, 4, 6),
+    (4, 130, 256, 512, 16, 16),
+    (2, 64, 96, 384, 28, 9),
+    (2, 3, 1, 10, 1, 8),
+])
+@pytest.mark.parametrize("conv1d", [False, True])
+def test_kron_projection(gpu, dtype, conf, conv1d):
+    B, T, n_i, n_o, k_i, k_o = conf
+    A = randn((B, T, n_i), 21 + T, 1.0, dtype)
+    G = randn((B, T, n_o), 22 + T, 1e-3, dtype)
+    if conv1d:   # Conv1D: P_i acts on the output grads (width n_o), P_o on the inputs
+        P_i = randn((k_i, n_o), 23, 1.0 / k_i ** 0.5)
+        P_o = randn((k_o, n_i), 24, 1.0 / k_o ** 0.5)
+        layout = _native.PROJ_KI_KO
+    else:
+        P_i = randn((k_i, n_i), 23, 1.0 / k_i ** 0.5)
+        P_o = randn((k_o, n_o), 24, 1.0 / k_o ** 0.5)
+        layout = _native.PROJ_KO_KI
+    print(f"kron conf={conf} dtype={dtype} conv1d={conv1d}", flush=True)
+    out = _native.ops().kron_proj(A.to(gpu), G.to(gpu), P_i.to(gpu), P_o.to(gpu), float(B),
+                                  layout=layout)
+    torch.cuda.synchronize()
+    want = R.kron_proj_exact(A.float(), G.float(), P_i.to(dtype).float(), P_o.to(dtype).float(),
+                             float(B), conv1d=conv1d)
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert_close(out.cpu(), want, tol, "kron")

@@ -1,0 +1,111 @@
+"""GPU parity of the Linear weight/bias dot kernels against the oracle (through the C ABI).
+
+Tolerances: bf16 operands 2e-2 normwise, fp32 operands 1e-4 normwise, both against the
+float64 closed forms; the ghost kernel with reference rounding against the reference's
+own bf16 op sequence at 2e-3.
+"""
+import pytest
+import torch
+
+from ghostsuite_amd import _native
+from oracle import ghost_ref as R
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, randn
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # N, n_val, T, d_in, d_out
+    (6, 2, 5, 24, 40),        # ragged everything, K tails below one tile
+    (10, 3, 64, 128, 96),
+    (80, 16, 1, 512, 1024),   # the MLP layer shape (T = 1)
+    (8, 2, 300, 200, 136),    # T and K not multiples of the tile sizes
+    (12, 4, 130, 64, 10),     # d_out = 10: unaligned rows, scalar loads
+]
+
+
+def _inputs(N, T, d_in, d_out, seed, dtype):
+    A = randn((N, T, d_in), seed, 1.0, dtype)
+    G = randn((N, T, d_out), seed + 1, 1e-3, dtype)
+    return A, G
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("algo", [_native.ALGO_GHOST, _native.ALGO_VALGRAD])
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_linear_dot_matches_closed_form(gpu, shape, dtype, algo, semantics):
+    N, n_val, T, d_in, d_out = shape
+    print(f"linear_dot shape={shape} dtype={dtype} algo={algo} sem={semantics}", flush=True)
+    A, G = _inputs(N, T, d_in, d_out, 100 + N + T, dtype)
+    sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
+    dot, _ = _native.ops().linear_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem, algo=algo)
+    torch.cuda.synchronize()
+    want = R.linear_dot_exact(A, G, n_val, semantics)
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert_close(dot.cpu(), want, tol, f"{semantics}/{algo}")
+
+
+@pytest.mark.parametrize("shape", SHAPES[:4])
+@pytest.mark.parametrize("algo", [_native.ALGO_GHOST, _native.ALGO_VALGRAD])
+def test_linear_pairs_and_val_first_layout(gpu, shape, algo):
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 7 + T, torch.float32)
+    for val_start in (0, N - n_val, 1):
+        if val_start + n_val > N:
+            continue
+        print(f"pairs shape={shape} algo={algo} val_start={val_start}", flush=True)
+        dot, pair = _native.ops().linear_dot(A.to(gpu), G.to(gpu), n_val, val_start=val_start,
+                                             algo=algo, want_pair=True)
+        torch.cuda.synchronize()
+        want_pair = R.linear_dot_exact(A, G, n_val, "pairwise", val_start=val_start, pair=True)
+        want_dot = R.linear_dot_exact(A, G, n_val, "pairwise", val_start=val_start)
+        assert_close(pair.cpu(), want_pair, FP32_TOL, "pair")
+        assert_close(dot.cpu(), want_dot, FP32_TOL, "dot")
+        # invariant: summing the pair matrix over val rows gives the dot vector
+        assert_close(pair.cpu().double().sum(0), dot.cpu().double(), 1e-5, "pair-sum")
+
+
+@pytest.mark.parametrize("shape", [(10, 3, 64, 128, 96), (6, 2, 40, 64, 72)])
+def test_ghost_reference_rounding_matches_reference_sequence(gpu, shape):
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 31, torch.float32)
+    dot, _ = _native.ops().linear_dot(A.to(gpu).bfloat16(), G.to(gpu).bfloat16(), n_val,
+                                      algo=_native.ALGO_GHOST,
+                                      rounding=_native.ROUND_REF_BF16)
+    torch.cuda.synchronize()
+    want, _ = R.linear_dot_ref(A, G, n_val, use_ghost=True, has_bias=False)
+    assert_close(dot.cpu(), want, 2e-3, "ref-rounding")
+
+
+def test_linear_auto_picks_cheaper_algorithm(gpu):
+    ops = _native.ops()
+    # microbench T=1024: ghost 1.5 TF vs val-gradient 0.15 TF
+    assert ops.linear_algo(torch.bfloat16, 32, 8, 1024, 768, 3072, 0, 0, False) == _native.ALGO_VALGRAD
+    # tiny T with big layers: ghost
+    assert ops.linear_algo(torch.bfloat16, 20, 4, 4, 1024, 4096, 0, 0, False) == _native.ALGO_GHOST
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(6, 2, 5, 40), (10, 3, 130, 96), (80, 16, 1, 10)])
+def test_bias_dot_and_grad(gpu, dtype, shape):
+    N, n_val, T, d = shape
+    G = randn((N, T, d), 5 + T, 1e-3, dtype)
+    scale = N / (N - n_val)
+    dot, grad = _native.ops().bias_dot(G.to(gpu), n_val, grad_scale=scale,
+                                       grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert_close(dot.cpu(), R.bias_dot_exact(G, n_val), tol, "bias dot")
+    want_grad = R.bias_train_grad(G.double() * N, n_val)
+    assert_close(grad.cpu(), want_grad, tol, "bias grad")
+
+
+def test_linear_rejects_bad_arguments(gpu):
+    A = torch.zeros(4, 3, 8, device=gpu)
+    G = torch.zeros(4, 3, 8, device=gpu)
+    with pytest.raises(_native.GhostHipError):
+        _native.ops().linear_dot(A, G, 4)            # no train rows
+    with pytest.raises(_native.GhostHipError):
+        _native.ops().linear_dot(A, G.bfloat16(), 1)  # dtype mismatch
+    with pytest.raises(_native.GhostHipError):
+        _native.ops().linear_dot(A, G, 1, semantics=_native.SEM_PRESUM, want_pair=True)

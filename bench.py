@@ -265,8 +265,49 @@ def cpu_baseline(budget_s: float = 20.0):
                        f"blocks; model fwd/bwd not included")}
 
 
+def kernels_leg(dev, reps: int = 10):
+    """Kernel-level leg for counter runs: the fused ghost kernel at the microbench shape, the
+    val-gradient path at the GPT-2-small fc_out shape, and a 1 GiB device copy (the HBM
+    calibration for FETCH_SIZE / WRITE_SIZE)."""
+    from ghostsuite_amd import _native
+    out = {}
+    gk = ghost_kernel_bench(dev, reps=reps)
+    out["ghost_T1024"] = gk
+    g = torch.Generator().manual_seed(7)
+    N, n_val, T, d_in, d_out = 20, 4, 1024, 3072, 768
+    A = torch.randn(N, T, d_in, generator=g).to(dev, torch.bfloat16)
+    G = (torch.randn(N, T, d_out, generator=g) * 1e-3).to(dev, torch.bfloat16)
+    ops = _native.ops()
+    for _ in range(2):
+        ops.linear_dot(A, G, n_val, algo=_native.ALGO_VALGRAD)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        ops.linear_dot(A, G, n_val, algo=_native.ALGO_VALGRAD)
+    e.record()
+    torch.cuda.synchronize()
+    out["valgrad_fc_out_ms"] = s.elapsed_time(e) / reps
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    out["copy_1GiB_ms"] = ms
+    out["copy_GBps"] = 2 * (1 << 30) / (ms * 1e-3) / 1e9
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--mode", choices=["full", "kernels"], default="full")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
@@ -281,6 +322,9 @@ def main():
     dev = torch.device("cuda:0")
     from ghostsuite_amd import _native
     _native.load_library()
+    if args.mode == "kernels":
+        kernels_leg(dev)
+        return
 
     res = gpt2_bench(args.steps, args.warmup, dev)
     log("[bench] GPT-2 step done; ghost kernel microbench")

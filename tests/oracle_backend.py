@@ -1,0 +1,80 @@
+"""CPU stand-in for the kernel layer, used only by host-logic tests (routing, hooks, engine
+state machine) on machines without a GPU.  Every op is the oracle's float64 closed form,
+so these tests check what the engines do with the results, not the kernels."""
+import torch
+
+from ghostsuite_amd import _native
+from oracle import ghost_ref as R
+
+
+class OracleOps:
+    name = "oracle"
+
+    def __init__(self):
+        self.calls = []
+
+    def linear_algo(self, dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair):
+        return _native.ALGO_GHOST if algo in (_native.ALGO_AUTO, _native.ALGO_GHOST) else algo
+
+    def linear_dot(self, A, G, n_val, *, val_start=None, semantics=0, algo=0, rounding=0,
+                   want_pair=False):
+        self.calls.append(("linear_dot", tuple(A.shape), tuple(G.shape), semantics))
+        sem = "pairwise" if semantics == _native.SEM_PAIRWISE_SUM else "presum"
+        dot = R.linear_dot_exact(A.float(), G.float(), n_val, sem, val_start=val_start).float()
+        pair = None
+        if want_pair:
+            pair = R.linear_dot_exact(A.float(), G.float(), n_val, sem, val_start=val_start,
+                                      pair=True).float()
+        return dot.to(A.device), pair
+
+    def bias_dot(self, G, n_val, *, val_start=None, grad_scale=None, grad_dtype=None):
+        self.calls.append(("bias_dot", tuple(G.shape)))
+        dot = R.bias_dot_exact(G.float(), n_val, val_start).float()
+        grad = None
+        if grad_scale is not None:
+            N, d = G.shape[0], G.shape[-1]
+            tr, _ = R.split_rows(G.double().reshape(N, -1, d), n_val, val_start)
+            grad = (tr.sum((0, 1)) * grad_scale).to(grad_dtype or G.dtype)
+        return dot, grad
+
+    def embedding_dot(self, ids, G, n_val, vocab, *, val_start=None):
+        self.calls.append(("embedding_dot", tuple(G.shape)))
+        return R.embedding_dot_exact(ids, G.float(), n_val, val_start).float()
+
+    def layernorm_dot(self, X, G, n_val, eps, *, val_start=None, want_dot=True, want_bias=True,
+                      grad_scale=None, grad_dtype=None):
+        self.calls.append(("layernorm_dot", tuple(X.shape)))
+        dw = db = gw = gb = None
+        if want_dot:
+            w, b = R.layernorm_dot_exact(X.float(), G.float(), n_val, eps, val_start)
+            dw = w.float()
+            db = b.float() if want_bias else None
+        if grad_scale is not None:
+            N, Fd = X.shape[0], X.shape[-1]
+            x = X.double().reshape(N, -1, Fd)
+            g = G.double().reshape(N, -1, Fd)
+            xh = torch.nn.functional.layer_norm(x, (Fd,), eps=eps)
+            tw, _ = R.split_rows((g * xh).sum(1), n_val, val_start)
+            tb, _ = R.split_rows(g.sum(1), n_val, val_start)
+            gw = (tw.sum(0) * grad_scale).to(grad_dtype or X.dtype)
+            gb = (tb.sum(0) * grad_scale).to(grad_dtype or X.dtype) if want_bias else None
+        return dw, db, gw, gb
+
+    def kron_proj(self, A, G, P_i, P_o, scale, *, layout=0, out_dtype=torch.float32):
+        self.calls.append(("kron_proj", tuple(A.shape)))
+        out = R.kron_proj_exact(A.float(), G.float(), P_i.float(), P_o.float(), scale,
+                                conv1d=layout == _native.PROJ_KI_KO)
+        return out.to(out_dtype)
+
+
+class use_oracle_backend:
+    """Context manager installing OracleOps as the kernel layer."""
+
+    def __enter__(self):
+        self.ops = OracleOps()
+        _native._install_backend(self.ops)
+        return self.ops
+
+    def __exit__(self, *exc):
+        _native._install_backend(None)
+        return False

@@ -1,0 +1,340 @@
+"""Host logic of the engines on the CPU, with the kernel layer replaced by the oracle's
+closed forms (tests/oracle_backend.py): hook registration, the ghost/materialise switch,
+semantics per layer, tied-weight overwrite, train-gradient routing into .grad, the
+named_parameters summation order, error paths, save formats, and GradProj set-up."""
+import copy
+import json
+import types
+
+import pytest
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ghostsuite_amd import GhostEngineManager, GradDotProdEngine, GradProjLoraEngine, _native
+from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+from ghostsuite_amd.workloads import MLP, CausalLM, LMConfig, synthetic_tokens
+from oracle import brute
+from oracle import ghost_ref as R
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, gen
+from tests.oracle_backend import use_oracle_backend
+
+
+@pytest.fixture(autouse=True)
+def _reset_options():
+    saved = dict(S.options)
+    yield
+    S.options.clear()
+    S.options.update(saved)
+
+
+def _ce_sum(m, x, y):
+    return F.cross_entropy(m(x), y, reduction="sum")
+
+
+# ------------------------------------------------------------------ MLP
+@pytest.mark.parametrize("precision,tol", [("fp32", FP32_TOL), ("reference", BF16_TOL)])
+def test_mlp_engine_dots_and_grads_match_per_sample_gradients(precision, tol):
+    torch.manual_seed(0)
+    dims = (64, 48, 32, 10)
+    model = MLP(dims)
+    ref = copy.deepcopy(model).double()
+    n_t, n_v = 24, 8
+    X = torch.randn(n_t + n_v, dims[0], generator=gen(1))
+    Y = torch.randint(0, 10, (n_t + n_v,), generator=gen(2))
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    ref_opt = torch.optim.SGD(ref.parameters(), lr=0.1)
+    with use_oracle_backend():
+        eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False,
+                                precision=precision)
+        eng.attach(opt)
+        for step in range(3):
+            eng.attach_train_batch(X[:n_t], Y[:n_t], step, 0)
+            loss = F.cross_entropy(model(X), Y)
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            per_param = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()}
+            eng.aggregate_and_log()
+            eng.prepare_gradients()
+            grads_now = {n: p.grad.clone() for n, p in model.named_parameters()}
+            opt.step()
+            eng.clear_gradients()
+
+            g = brute.per_sample_grads(ref, X.double(), Y, _ce_sum, 1.0 / X.shape[0])
+            total = 0
+            for name, gr in g.items():
+                want = brute.pairwise_dots(gr, n_v)
+                assert_close(per_param[name], want, tol, f"step {step} {name}")
+                assert_close(grads_now[name], brute.train_mean(gr, n_v, X.shape[0]), FP32_TOL,
+                             f"step {step} grad {name}")
+                total = total + want
+            assert_close(eng.dot_product_log[-1]["dot_product"], total, tol, "aggregate")
+            # drive the reference copy with the same train gradients
+            for (name, p) in ref.named_parameters():
+                p.grad = brute.train_mean(g[name], n_v, X.shape[0])
+            ref_opt.step()
+        eng.detach()
+    assert len(eng.dot_product_log) == 3
+    assert set(eng.dot_product_log[0]) == {"dot_product", "X_train", "Y_train", "iter_num",
+                                           "batch_idx"}
+
+
+# ------------------------------------------------------------------ small GPT-2
+def _tiny_lm(d=16, T=8, vocab=50):
+    return LMConfig(n_layer=2, n_head=2, d_model=d, d_mlp=2 * d, vocab=vocab, n_ctx=T)
+
+
+def _lm_sample_loss(T):
+    def f(m, x, y):
+        return m(x, y) * T   # token-mean loss of one row, times its T tokens
+    return f
+
+
+def test_gpt2_engine_routing_and_tied_overwrite():
+    torch.manual_seed(3)
+    T, vocab = 8, 50
+    cfg = _tiny_lm(T=T, vocab=vocab)
+    model = CausalLM(cfg)
+    untied = CausalLM(cfg)
+    untied.load_state_dict(model.state_dict())
+    untied.lm_head.weight = nn.Parameter(model.wte.weight.detach().clone())  # same values, own param
+    tied_ref = copy.deepcopy(model).double()
+    untied = untied.double()
+    n_t, n_v = 5, 1
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=4)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    with use_oracle_backend() as ops:
+        eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True,
+                                precision="fp32")
+        eng.attach(opt)
+        names = {n for n, m in model.named_modules() if hasattr(m, "name")}
+        assert {"wte", "wpe", "lm_head", "ln_f", "h.0.qkv", "h.1.fc_out", "h.0.ln_1"} <= names
+        eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+        loss = model(X, Y)
+        loss.backward()
+        # the lm_head dot is overwritten by wte's in the reference; it is not computed here
+        linear_shapes = [c[1] for c in ops.calls if c[0] == "linear_dot"]
+        assert (n_t + n_v, T, cfg.d_model) in linear_shapes
+        assert not any(c[2][-1] == vocab for c in ops.calls if c[0] == "linear_dot")
+        dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()
+                if hasattr(p, "grad_dot_prod")}
+        eng.prepare_gradients()
+        grads = {n: p.grad.clone() for n, p in model.named_parameters() if p.grad is not None}
+        eng.aggregate_and_log()
+        eng.detach()
+
+    N = n_t + n_v
+    g_untied = brute.per_sample_grads(untied, X, Y, _lm_sample_loss(T), 1.0 / (N * T))
+    g_tied = brute.per_sample_grads(tied_ref, X, Y, _lm_sample_loss(T), 1.0 / (N * T))
+    assert "lm_head.weight" not in dots
+    for name, d in dots.items():
+        want = brute.pairwise_dots(g_untied[name], n_v)   # wte: embedding part only
+        assert_close(d, want, FP32_TOL, f"dot {name}")
+    # dummy biases get autograd's (zero) grad; the engine leaves them alone
+    grads = {n: g for n, g in grads.items() if "dummy_bias" not in n}
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g_tied[name], n_v, N), FP32_TOL, f"grad {name}")
+    total = sum(brute.pairwise_dots(g_untied[n], n_v) for n in dots)
+    assert_close(eng.dot_product_log[-1]["dot_product"], total, FP32_TOL, "aggregate")
+
+
+def test_switch_selects_semantics_per_layer():
+    torch.manual_seed(5)
+    T = 16
+    cfg = LMConfig(n_layer=1, n_head=2, d_model=8, d_mlp=64, vocab=30, n_ctx=T)
+    model = CausalLM(cfg)
+    X, Y = synthetic_tokens(5, T, 30, seed=6)
+    with use_oracle_backend() as ops:
+        eng = GradDotProdEngine(model, val_batch_size=2, use_dummy_bias=True)
+        eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+        model(X, Y).backward()
+        eng.detach()
+    sems = {c[2][-1] if c[1][-1] == 8 else c[1][-1]: c[3] for c in ops.calls
+            if c[0] == "linear_dot"}
+    # qkv 8x24=192 < 2*16^2 -> presum; fc 8x64=512 -> ghost (pairwise); fc_out 64x8 likewise
+    assert model.h[0].qkv.use_ghost_computation is False
+    assert model.h[0].fc.use_ghost_computation is True
+    assert sems[24] == _native.SEM_PRESUM
+    assert sems[64] == _native.SEM_PAIRWISE_SUM
+
+
+def test_error_paths():
+    model = MLP((8, 4, 3))
+    with use_oracle_backend():
+        eng = GradDotProdEngine(model, val_batch_size=4, use_dummy_bias=False)
+        opt = torch.optim.SGD(model.parameters(), lr=0.1)
+        eng.attach(opt)
+        with pytest.raises(ValueError, match="twice"):
+            from ghostsuite_amd import autograd_grad_sample_dotprod as H
+            H.add_hooks(model, 4)
+        X = torch.randn(4, 8)
+        with pytest.raises(ValueError, match="No training samples"):
+            F.cross_entropy(model(X), torch.zeros(4, dtype=torch.long)).backward()
+        eng.detach()
+    # a trainable parameter outside the supported layers has no train_grad
+    m2 = nn.Sequential(nn.Linear(4, 4), nn.Conv1d(1, 1, 1))
+    with use_oracle_backend():
+        e2 = GradDotProdEngine(m2, val_batch_size=1, use_dummy_bias=False)
+        e2.attach(torch.optim.SGD(m2.parameters(), lr=0.1))
+        out = m2[0](torch.randn(3, 4)).sum()
+        out.backward()
+        with pytest.raises(ValueError, match="train_grad"):
+            e2.prepare_gradients()
+    with pytest.raises(TypeError):
+        GradDotProdEngine(MLP((4, 2)), val_batch_size=1, not_an_option=True)
+
+
+def test_manager_flow_and_save_formats(tmp_path):
+    torch.manual_seed(7)
+    model = MLP((16, 8, 4))
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    Xv, Yv = torch.randn(3, 16), torch.randint(0, 4, (3,))
+    cfg = types.SimpleNamespace(method="GradDotProd", result_dir=str(tmp_path), val_batch_size=3,
+                                dot_prod_save_interval=2)
+    with use_oracle_backend():
+        mgr = GhostEngineManager(cfg, model, opt, {"master_process": True}, (Xv, Yv))
+        for model_p in model.parameters():   # the manager always uses the dummy-bias trick
+            model_p.requires_grad_(True)
+        for it in range(1, 5):
+            Xt, Yt = torch.randn(5, 16), torch.randint(0, 4, (5,))
+            mgr.attach_train_batch(Xt, Yt, it, batch_idx=it)
+            Xc, Yc = mgr.prepare_forward_input(Xt, Yt)
+            assert torch.equal(Xc[:5], Xt) and torch.equal(Xc[5:], Xv)
+            F.cross_entropy(model(Xc), Yc).backward()
+            mgr.prepare_gradients()
+            opt.step()
+            mgr.aggregate_and_log()
+            mgr.clear_gradients()
+            opt.zero_grad(set_to_none=True)
+            if mgr.should_save_metrics(it):
+                mgr.save_metrics(it)
+        mgr.cleanup()
+    d = tmp_path / "grad_dotprods"
+    assert (d / "valset.pt").exists()
+    vs = torch.load(d / "valset.pt", weights_only=True)
+    assert torch.equal(vs["X_val"], Xv)
+    log2 = torch.load(d / "dot_prod_log_iter_2.pt", weights_only=True)
+    assert [r["iter_num"] for r in log2] == [1, 2] and log2[0]["dot_product"].shape == (5,)
+    assert (d / "dot_prod_log_iter_4.pt").exists()
+    assert not hasattr(model, "autograd_grad_sample_hooks")
+
+
+def test_detach_reattach_gives_same_dots():
+    torch.manual_seed(8)
+    model = MLP((12, 6, 3))
+    X = torch.randn(7, 12)
+    Y = torch.randint(0, 3, (7,))
+    with use_oracle_backend():
+        eng = GradDotProdEngine(model, val_batch_size=2, use_dummy_bias=False, precision="fp32")
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        out = []
+        for _ in range(2):
+            eng.attach(opt)
+            eng.attach_train_batch(X[:5], Y[:5], 0)
+            F.cross_entropy(model(X), Y).backward()
+            eng.aggregate_and_log()
+            eng.prepare_gradients()
+            eng.clear_gradients()
+            out.append(eng.dot_product_log[-1]["dot_product"])
+            eng.detach()
+            assert not any(hasattr(p, "train_grad") for p in model.parameters())
+    assert torch.allclose(out[0], out[1])
+
+
+# ------------------------------------------------------------------ GradProj
+class SimpleMLP(nn.Module):
+    def __init__(self, i=10, h=20, o=5):
+        super().__init__()
+        self.fc1 = nn.Linear(i, h)
+        self.relu = nn.ReLU()
+        self.fc2 = nn.Linear(h, o)
+
+    def forward(self, x):
+        return self.fc2(self.relu(self.fc1(x)))
+
+
+def test_gradproj_naive_equality_and_files(tmp_path):
+    torch.manual_seed(9)
+    model = SimpleMLP()
+    X, Y = torch.randn(4, 10), torch.randint(0, 5, (4,))
+    conf = dict(proj_layers="fc", proj_rank_total=16, proj_rank_min=2, proj_seed=42,
+                proj_dtype="float32", proj_dir=str(tmp_path))
+    with use_oracle_backend():
+        eng = GradProjLoraEngine(model, **conf)
+        eng.attach()
+        F.cross_entropy(model(X), Y).backward()
+        proj = eng.collect_batch(batch_indices=[0, 1, 2, 3])
+        eng.detach()
+    # naive: per-sample gradient (batch of 1) then P_o W P_i^T, layers in sorted order
+    naive = []
+    for b in range(4):
+        model.zero_grad()
+        F.cross_entropy(model(X[b:b + 1]), Y[b:b + 1]).backward()
+        parts = []
+        for name in sorted(eng.matched_layers):
+            P_i, P_o = eng.projection_matrices[name]
+            parts.append((P_o @ eng.matched_layers[name].weight.grad @ P_i.t()).reshape(-1))
+        naive.append(torch.cat(parts))
+    assert torch.allclose(proj, torch.stack(naive), rtol=1e-4, atol=1e-5)
+    saved = torch.load(tmp_path / "proj_iter_000000.pt", weights_only=True)
+    assert saved["batch_size"] == 4 and saved["batch_idx"] == [0, 1, 2, 3]
+    meta = json.loads((tmp_path / "metadata.json").read_text())
+    assert meta["total_proj_dim"] == proj.shape[1]
+    assert [l["name"] for l in meta["layers"]] == ["fc1", "fc2"]
+    assert meta["layers"][1]["slice_start"] == meta["layers"][0]["slice_end"]
+
+
+def test_gradproj_non_interference(tmp_path):
+    torch.manual_seed(10)
+    m1 = SimpleMLP()
+    m2 = copy.deepcopy(m1)
+    X, Y = torch.randn(8, 10), torch.randint(0, 5, (8,))
+    o1 = torch.optim.SGD(m1.parameters(), lr=0.01)
+    o2 = torch.optim.SGD(m2.parameters(), lr=0.01)
+    with use_oracle_backend():
+        eng = GradProjLoraEngine(m2, proj_layers="fc", proj_rank_total=16, proj_rank_min=2,
+                                 proj_seed=1, proj_dtype="float16", proj_dir=str(tmp_path))
+        eng.attach()
+        for _ in range(5):
+            for m, o in ((m1, o1), (m2, o2)):
+                o.zero_grad()
+                F.cross_entropy(m(X), Y).backward()
+                o.step()
+            assert eng.collect_batch().dtype == torch.float16
+        eng.detach()
+    for p1, p2 in zip(m1.parameters(), m2.parameters()):
+        assert torch.allclose(p1, p2, rtol=1e-5, atol=1e-6)
+
+
+def test_gradproj_choose_ki_ko_matches_known_answers():
+    from ghostsuite_amd.gradProjection.projection_utils import choose_ki_ko
+    for (n_i, n_o), want in {(1024, 3072): (28, 9), (3072, 1024): (9, 28),
+                             (1024, 4096): (32, 8), (4096, 1024): (8, 32),
+                             (1024, 1024): (16, 16)}.items():
+        assert choose_ki_ko(n_i, n_o, 256, 8) == want
+    for n_i, n_o, k, kmin in [(10, 20, 16, 2), (20, 5, 16, 2), (7, 300, 64, 4), (512, 3, 12, 1)]:
+        assert choose_ki_ko(n_i, n_o, k, kmin) == R.choose_ki_ko(n_i, n_o, k, kmin)
+
+
+def test_gradproj_embedding_projection_matches_naive(tmp_path):
+    torch.manual_seed(11)
+    emb = nn.Embedding(30, 6)
+    model = nn.Sequential(emb, nn.Flatten(), nn.Linear(6 * 4, 3))
+    X = torch.randint(0, 30, (3, 4))
+    Y = torch.randint(0, 3, (3,))
+    with use_oracle_backend():
+        eng = GradProjLoraEngine(model, proj_layers="0", proj_rank_total=12, proj_rank_min=2,
+                                 proj_seed=5, proj_dtype="float32", proj_dir=str(tmp_path),
+                                 include_embeddings=True)
+        eng.attach()
+        F.cross_entropy(model(X), Y).backward()
+        got = eng.matched_layers["0"]._ghost_grad_proj.clone()
+        eng.detach()
+    P_i, P_o = eng.projection_matrices["0"]
+    for b in range(3):
+        model.zero_grad()
+        F.cross_entropy(model(X[b:b + 1]), Y[b:b + 1], reduction="sum").backward()
+        W = emb.weight.grad   # [V, d]: per-sample grad of the embedding table
+        naive = P_o @ W.t() @ P_i.t()
+        # the reference does not multiply embedding projections by the batch size
+        assert torch.allclose(got[b] * 3, naive, rtol=1e-4, atol=1e-6)

@@ -21,79 +21,150 @@ __device__ __forceinline__ float ld(const E* p) {
   return to_f32<E>(*p);
 }
 
-// ---------------------------------------------------------------- stage 1: bias sums
-// part[(n * chunks + c) * F + f] = sum_{t in chunk c} g[n, t, f]
+// 16-byte vector of VE elements of type E, widened to fp32.
 template <class E>
-__global__ void colsum_kernel(const E* __restrict__ G, int64_t T, int64_t F, int64_t chunks,
-                              float* __restrict__ part) {
+struct Vec {
+  static constexpr int VE = 16 / sizeof(E);
+  float v[VE];
+  __device__ __forceinline__ void load(const E* p, bool full, int64_t n_left) {
+    if (full) {
+      union { uint4 u; E e[VE]; } w;
+      w.u = *reinterpret_cast<const uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < VE; ++i) v[i] = to_f32<E>(w.e[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VE; ++i) v[i] = i < n_left ? to_f32<E>(p[i]) : 0.f;
+    }
+  }
+};
+
+// ---------------------------------------------------------------- stage 1: bias sums
+// part[(n * chunks + c) * F + f] = sum_{t in chunk c} g[n, t, f]; each thread owns a
+// 16-byte feature chunk and walks the chunk's tokens.
+template <class E>
+__global__ void __launch_bounds__(BW_THREADS) colsum_kernel(const E* __restrict__ G, int64_t T,
+                                                            int64_t F, int64_t chunks, int vec,
+                                                            float* __restrict__ part) {
+  constexpr int VE = Vec<E>::VE;
   const int64_t n = blockIdx.y, c = blockIdx.x;
   const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
-  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
-    float s = 0.f;
-    for (int64_t t = t0; t < t1; ++t) s += ld(G + (n * T + t) * F + f);
-    part[(n * chunks + c) * F + f] = s;
+  for (int64_t f = static_cast<int64_t>(threadIdx.x) * VE; f < F;
+       f += static_cast<int64_t>(blockDim.x) * VE) {
+    const bool full = vec && f + VE <= F;
+    float s[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) s[i] = 0.f;
+#pragma unroll 4
+    for (int64_t t = t0; t < t1; ++t) {
+      Vec<E> x;
+      x.load(G + (n * T + t) * F + f, full, F - f);
+#pragma unroll
+      for (int i = 0; i < VE; ++i) s[i] += x.v[i];
+    }
+    float* dst = part + (n * chunks + c) * F + f;
+#pragma unroll
+    for (int i = 0; i < VE; ++i)
+      if (f + i < F) dst[i] = s[i];
   }
 }
 
 // ---------------------------------------------------------------- stage 1: LayerNorm sums
-// One wave per token row: mean/rstd by wave reduction, then g*xhat and g accumulated per
-// lane over the block's tokens; the 4 waves combine through LDS.
-template <class E, int PL>
-__global__ void __launch_bounds__(BW_THREADS) ln_sums_kernel(const E* __restrict__ X,
-                                                             const E* __restrict__ G, int64_t T,
-                                                             int64_t F, float eps, int64_t chunks,
-                                                             float* __restrict__ part_w,
-                                                             float* __restrict__ part_b) {
-  extern __shared__ float sm[];  // [4][F] for w then [4][F] for b
+// One wave per token row (LN_WAVES waves per block): lanes own 16-byte feature chunks,
+// mean/rstd by wave reductions (two passes over registers), g*xhat and g accumulated per
+// lane over the block's tokens; the waves combine through LDS.
+constexpr int LN_WAVES = 8;
+template <class E, int PC>
+__global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
+    const E* __restrict__ X, const E* __restrict__ G, int64_t T, int64_t F, float eps,
+    int64_t chunks, int vec, float* __restrict__ part_w, float* __restrict__ part_b) {
+  constexpr int VE = Vec<E>::VE;
+  extern __shared__ float sm[];  // [LN_WAVES/2][F] for w, then the same for b
   const int64_t n = blockIdx.y, c = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
-  float aw[PL], ab[PL];
+  float aw[PC][VE], ab[PC][VE];
 #pragma unroll
-  for (int k = 0; k < PL; ++k) aw[k] = ab[k] = 0.f;
+  for (int k = 0; k < PC; ++k)
+#pragma unroll
+    for (int i = 0; i < VE; ++i) aw[k][i] = ab[k][i] = 0.f;
   const float invF = 1.0f / static_cast<float>(F);
-  for (int64_t t = t0 + wid; t < t1; t += 4) {
+  for (int64_t t = t0 + wid; t < t1; t += LN_WAVES) {
     const E* xr = X + (n * T + t) * F;
     const E* gr = G + (n * T + t) * F;
-    float xv[PL];
+    Vec<E> xv[PC], gv[PC];
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < PL; ++k) {
-      const int64_t f = lane + 64 * k;
-      xv[k] = f < F ? ld(xr + f) : 0.f;
-      s += xv[k];
+    for (int k = 0; k < PC; ++k) {
+      const int64_t f = (lane + 64 * k) * VE;
+      const bool in = f < F;
+      const bool full = vec && f + VE <= F;
+      if (in) {
+        xv[k].load(xr + f, full, F - f);
+        gv[k].load(gr + f, full, F - f);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VE; ++i) xv[k].v[i] = gv[k].v[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < VE; ++i) s += xv[k].v[i];
     }
     const float mean = wave_sum(s) * invF;
-    float v = 0.f;
+    float var = 0.f;
 #pragma unroll
-    for (int k = 0; k < PL; ++k) {
-      const int64_t f = lane + 64 * k;
-      const float dlt = f < F ? xv[k] - mean : 0.f;
-      v += dlt * dlt;
-    }
-    const float rstd = rsqrtf(wave_sum(v) * invF + eps);
+    for (int k = 0; k < PC; ++k) {
+      const int64_t f = (lane + 64 * k) * VE;
 #pragma unroll
-    for (int k = 0; k < PL; ++k) {
-      const int64_t f = lane + 64 * k;
-      if (f < F) {
-        const float g = ld(gr + f);
-        aw[k] += g * ((xv[k] - mean) * rstd);
-        ab[k] += g;
+      for (int i = 0; i < VE; ++i) {
+        const float dlt = (f + i < F) ? xv[k].v[i] - mean : 0.f;
+        var += dlt * dlt;
       }
     }
-  }
+    const float rstd = rsqrtf(wave_sum(var) * invF + eps);
 #pragma unroll
-  for (int k = 0; k < PL; ++k) {
-    const int64_t f = lane + 64 * k;
-    if (f < F) {
-      sm[wid * F + f] = aw[k];
-      sm[(4 + wid) * F + f] = ab[k];
+    for (int k = 0; k < PC; ++k)
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        aw[k][i] += gv[k].v[i] * ((xv[k].v[i] - mean) * rstd);
+        ab[k][i] += gv[k].v[i];
+      }
+  }
+  // Two-step combine through [LN_WAVES/2][F] (x2) floats of LDS: the upper half of the
+  // waves parks its sums, the lower half adds its own, then the rows are summed.
+  constexpr int HALF = LN_WAVES / 2;
+  if (wid >= HALF) {
+#pragma unroll
+    for (int k = 0; k < PC; ++k) {
+      const int64_t f = (lane + 64 * k) * VE;
+#pragma unroll
+      for (int i = 0; i < VE; ++i)
+        if (f + i < F) {
+          sm[(wid - HALF) * F + f + i] = aw[k][i];
+          sm[(HALF + wid - HALF) * F + f + i] = ab[k][i];
+        }
+    }
+  }
+  __syncthreads();
+  if (wid < HALF) {
+#pragma unroll
+    for (int k = 0; k < PC; ++k) {
+      const int64_t f = (lane + 64 * k) * VE;
+#pragma unroll
+      for (int i = 0; i < VE; ++i)
+        if (f + i < F) {
+          sm[wid * F + f + i] += aw[k][i];
+          sm[(HALF + wid) * F + f + i] += ab[k][i];
+        }
     }
   }
   __syncthreads();
   for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
-    const float w = sm[f] + sm[F + f] + sm[2 * F + f] + sm[3 * F + f];
-    const float b = sm[4 * F + f] + sm[5 * F + f] + sm[6 * F + f] + sm[7 * F + f];
+    float w = 0.f, b = 0.f;
+#pragma unroll
+    for (int q = 0; q < HALF; ++q) {
+      w += sm[q * F + f];
+      b += sm[(HALF + q) * F + f];
+    }
     part_w[(n * chunks + c) * F + f] = w;
     if (part_b != nullptr) part_b[(n * chunks + c) * F + f] = b;
   }
@@ -312,30 +383,33 @@ bool batch_ok(int64_t N, int64_t n_val, int64_t val_start, int64_t T, int64_t F)
          F > 0;
 }
 
-template <class E, int PL>
+template <class E, int PC>
 void launch_ln(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
-               int64_t chunks, float* pw, float* pb, hipStream_t s) {
-  const size_t lds = 8 * F * sizeof(float);
-  hipLaunchKernelGGL((ln_sums_kernel<E, PL>),
+               int64_t chunks, int vec, float* pw, float* pb, hipStream_t s) {
+  const size_t lds = LN_WAVES * F * sizeof(float);
+  hipLaunchKernelGGL((ln_sums_kernel<E, PC>),
                      dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(N)),
-                     dim3(BW_THREADS), lds, s, static_cast<const E*>(X),
-                     static_cast<const E*>(G), T, F, eps, chunks, pw, pb);
+                     dim3(64 * LN_WAVES), lds, s, static_cast<const E*>(X),
+                     static_cast<const E*>(G), T, F, eps, chunks, vec, pw, pb);
 }
 
 template <class E>
 int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
                   int64_t chunks, float* pw, float* pb, hipStream_t s) {
-  const int64_t pl = cdiv(F, 64);
-  if (pl <= 4)
-    launch_ln<E, 4>(X, G, N, T, F, eps, chunks, pw, pb, s);
-  else if (pl <= 8)
-    launch_ln<E, 8>(X, G, N, T, F, eps, chunks, pw, pb, s);
-  else if (pl <= 16)
-    launch_ln<E, 16>(X, G, N, T, F, eps, chunks, pw, pb, s);
-  else if (pl <= 32)
-    launch_ln<E, 32>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  constexpr int VE = 16 / sizeof(E);
+  const int64_t pc = cdiv(F, 64 * VE);
+  const int vec = (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
+                  (reinterpret_cast<uintptr_t>(G) % 16 == 0) && (F * sizeof(E)) % 16 == 0;
+  if (pc <= 1)
+    launch_ln<E, 1>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
+  else if (pc <= 2)
+    launch_ln<E, 2>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
+  else if (pc <= 4)
+    launch_ln<E, 4>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
+  else if (pc <= 8 && VE == 4)
+    launch_ln<E, 8>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
   else
-    return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: F > 2048 not supported");
+    return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: feature count too large");
   return check_launch("ln_sums_kernel");
 }
 
@@ -373,12 +447,14 @@ extern "C" int gs_bias_dot(const void* G, int dtype, int64_t N, int64_t n_val, i
   float* sval = cv.take<float>(d_out);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(N));
+  const int vec = (reinterpret_cast<uintptr_t>(G) % 16 == 0) &&
+                  (d_out * static_cast<int64_t>(elem_size(dtype))) % 16 == 0;
   if (dtype == GS_DTYPE_BF16)
     hipLaunchKernelGGL(colsum_kernel<uint16_t>, grid, dim3(BW_THREADS), 0, s,
-                       static_cast<const uint16_t*>(G), T, d_out, chunks, part);
+                       static_cast<const uint16_t*>(G), T, d_out, chunks, vec, part);
   else
     hipLaunchKernelGGL(colsum_kernel<float>, grid, dim3(BW_THREADS), 0, s,
-                       static_cast<const float*>(G), T, d_out, chunks, part);
+                       static_cast<const float*>(G), T, d_out, chunks, vec, part);
   int rc = check_launch("colsum_kernel");
   if (rc) return rc;
   return finish_feature_any(grad_dtype, part, N, chunks, d_out, n_val, val_start, T, S, sval,

@@ -83,6 +83,7 @@ struct GemmParams {
   float* P;
   int64_t p_ld;            // = R map total (flat train rows)
   int64_t p_row0;          // first P row of this launch
+  int tile_reduce;         // 1: one partial per (m tile, n tile) (tiles never straddle samples)
   int rounding;
   // ROWDOT
   const void* Z;
@@ -117,34 +118,42 @@ __device__ __forceinline__ int64_t tile_row(const Operand& o, int64_t tile, int 
   return o.map.phys_row(seg, f - seg * o.map.seglen);
 }
 
-// Per-thread state for streaming one operand tile (ROWS x BK) into LDS.
-template <class Tr, int ROWS, int NT>
+// Per-thread state for streaming one operand tile (ROWS x BK) into LDS.  Thread t owns
+// the 16-byte chunk (t % CPR) of rows t / CPR + pass * (NT / CPR).  AL (aligned): rows are
+// 16-byte aligned and K % VEC == 0, so a chunk is either wholly inside the row or wholly
+// past its end, and one masked 16-byte load fetches it; otherwise elements are loaded one
+// by one.
+template <class Tr, int ROWS, int NT, bool AL>
 struct Streamer {
   using E = typename Tr::E;
   static constexpr int CPR = Tr::BK / Tr::VEC;  // 16-byte chunks per row
   static constexpr int NQ = ROWS * CPR / NT;    // chunks per thread
-  static_assert(NT % CPR == 0, "thread count must cover whole rows");
+  static_assert(NT % CPR == 0 && NQ >= 1, "thread count must cover whole rows");
   const E* row[NQ];
-  int lrow[NQ];
-  int kc;
   uint4 buf[NQ];
+  int kc;
 
-  __device__ void init(const Operand& o, int64_t tile, int tid) {
+  __device__ __forceinline__ void init(const Operand& o, int64_t tile, int tid) {
     kc = tid % CPR;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      lrow[q] = tid / CPR + q * (NT / CPR);
-      const int64_t pr = tile_row<ROWS>(o, tile, lrow[q]);
+      const int64_t pr = tile_row<ROWS>(o, tile, tid / CPR + q * (NT / CPR));
       row[q] = pr < 0 ? nullptr : static_cast<const E*>(o.base) + pr * o.ld;
     }
   }
-  __device__ void fetch(int64_t k0, int64_t K, int vec_ok) {
+  __device__ __forceinline__ void fetch(int64_t k0, int64_t K) {
     const int64_t kb = k0 + kc * Tr::VEC;
+    if constexpr (AL) {
+      const bool kin = kb < K;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      if (row[q] != nullptr && vec_ok && kb + Tr::VEC <= K) {
-        buf[q] = *reinterpret_cast<const uint4*>(row[q] + kb);
-      } else {
+      for (int q = 0; q < NQ; ++q) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (kin && row[q] != nullptr) v = *reinterpret_cast<const uint4*>(row[q] + kb);
+        buf[q] = v;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
         union { uint4 v; E e[Tr::VEC]; } u;
 #pragma unroll
         for (int v = 0; v < Tr::VEC; ++v)
@@ -153,67 +162,87 @@ struct Streamer {
       }
     }
   }
-  __device__ void stash(E* lds) const {
+  __device__ __forceinline__ void stash(E* lds, int tid) const {
+    const int r0 = tid / CPR;
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
-      *reinterpret_cast<uint4*>(lds + lrow[q] * (Tr::BK + Tr::PAD) + kc * Tr::VEC) = buf[q];
+      *reinterpret_cast<uint4*>(lds + (r0 + q * (NT / CPR)) * (Tr::BK + Tr::PAD) +
+                                kc * Tr::VEC) = buf[q];
   }
 };
 
-template <class Tr, int WM, int WN>
+// Tile configuration: WM x WN waves, each owning MI x NI MFMA 32x32 blocks.
+template <class Tr, int WM_, int WN_, int MI_, int NI_>
 struct Cfg {
-  static constexpr int BM = 64 * WM, BN = 64 * WN, NT = 64 * WM * WN;
+  static constexpr int WM = WM_, WN = WN_, MI = MI_, NI = NI_;
+  static constexpr int BM = 32 * MI * WM, BN = 32 * NI * WN, NT = 64 * WM * WN;
   static constexpr int LDR = Tr::BK + Tr::PAD;
   static constexpr int STAGE = (BM + BN) * LDR;  // elements per stage
   static constexpr size_t LDS_BYTES = 2 * STAGE * sizeof(typename Tr::E);
+  static constexpr int MIN_WAVES = (MI * NI <= 4) ? 2 : 1;  // waves per SIMD to fit registers
 };
 
-// acc[mi][ni] += L_tile * R_tile^T over the whole K range.
-template <class Tr, int WM, int WN>
-__device__ __forceinline__ void mainloop(const Operand& L, const Operand& R, int64_t mt, int64_t nt,
-                                         int64_t K, typename Tr::E* lds, f32x16_t (&acc)[2][2]) {
-  using C = Cfg<Tr, WM, WN>;
+template <class Tr, class C>
+struct Frags {
+  typename Tr::Frag a[C::MI], b[C::NI];
+};
+
+template <class Tr, class C>
+__device__ __forceinline__ void load_frags(Frags<Tr, C>& f, const typename Tr::E* lt,
+                                           const typename Tr::E* rt, int ks) {
+#pragma unroll
+  for (int i = 0; i < C::MI; ++i) f.a[i] = Tr::frag(lt + i * 32 * C::LDR + ks * Tr::KSTEP);
+#pragma unroll
+  for (int j = 0; j < C::NI; ++j) f.b[j] = Tr::frag(rt + j * 32 * C::LDR + ks * Tr::KSTEP);
+}
+
+// acc[mi][ni] += L_tile * R_tile^T over the whole K range.  One barrier per k-stage: the
+// next stage's global loads are issued before the current stage's MFMAs and land in the
+// other LDS buffer after them; MFMA fragments are double-buffered across k-steps.
+template <class Tr, class C, bool AL>
+__device__ __forceinline__ void mainloop(const Operand& L, const Operand& R, int64_t mt,
+                                         int64_t nt, int64_t K, typename Tr::E* lds,
+                                         f32x16_t (&acc)[C::MI][C::NI]) {
   using E = typename Tr::E;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid / WN, wn = wid % WN;
-  Streamer<Tr, C::BM, C::NT> sl;
-  Streamer<Tr, C::BN, C::NT> sr;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  Streamer<Tr, C::BM, C::NT, AL> sl;
+  Streamer<Tr, C::BN, C::NT, AL> sr;
   sl.init(L, mt, tid);
   sr.init(R, nt, tid);
-  const int vec = L.vec_ok && R.vec_ok;
   const int64_t nk = (K + Tr::BK - 1) / Tr::BK;
 
-  sl.fetch(0, K, vec);
-  sr.fetch(0, K, vec);
-  sl.stash(lds);
-  sr.stash(lds + C::BM * C::LDR);
+  sl.fetch(0, K);
+  sr.fetch(0, K);
+  sl.stash(lds, tid);
+  sr.stash(lds + C::BM * C::LDR, tid);
   __syncthreads();
 
   const int frow = lane & 31, fk = (lane >> 5) * Tr::KPL;
+  constexpr int KS = Tr::BK / Tr::KSTEP;
   for (int64_t kt = 0; kt < nk; ++kt) {
     E* cur = lds + (kt & 1) * C::STAGE;
     E* nxt = lds + ((kt + 1) & 1) * C::STAGE;
     const bool more = kt + 1 < nk;
     if (more) {
-      sl.fetch((kt + 1) * Tr::BK, K, vec);
-      sr.fetch((kt + 1) * Tr::BK, K, vec);
+      sl.fetch((kt + 1) * Tr::BK, K);
+      sr.fetch((kt + 1) * Tr::BK, K);
     }
-    const E* lt = cur + (wm * 64 + frow) * C::LDR + fk;
-    const E* rt = cur + C::BM * C::LDR + (wn * 64 + frow) * C::LDR + fk;
+    const E* lt = cur + (wm * 32 * C::MI + frow) * C::LDR + fk;
+    const E* rt = cur + C::BM * C::LDR + (wn * 32 * C::NI + frow) * C::LDR + fk;
+    Frags<Tr, C> f[2];
+    load_frags<Tr, C>(f[0], lt, rt, 0);
 #pragma unroll
-    for (int ks = 0; ks < Tr::BK / Tr::KSTEP; ++ks) {
-      typename Tr::Frag a0 = Tr::frag(lt + ks * Tr::KSTEP);
-      typename Tr::Frag a1 = Tr::frag(lt + 32 * C::LDR + ks * Tr::KSTEP);
-      typename Tr::Frag b0 = Tr::frag(rt + ks * Tr::KSTEP);
-      typename Tr::Frag b1 = Tr::frag(rt + 32 * C::LDR + ks * Tr::KSTEP);
-      Tr::mma(acc[0][0], a0, b0);
-      Tr::mma(acc[0][1], a0, b1);
-      Tr::mma(acc[1][0], a1, b0);
-      Tr::mma(acc[1][1], a1, b1);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) load_frags<Tr, C>(f[(ks + 1) & 1], lt, rt, ks + 1);
+#pragma unroll
+      for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::NI; ++j) Tr::mma(acc[i][j], f[ks & 1].a[i], f[ks & 1].b[j]);
     }
     if (more) {
-      sl.stash(nxt);
-      sr.stash(nxt + C::BM * C::LDR);
+      sl.stash(nxt, tid);
+      sr.stash(nxt + C::BM * C::LDR, tid);
     }
     __syncthreads();
   }
@@ -238,9 +267,8 @@ __device__ __forceinline__ void tile_of_block(int64_t m_tiles, int64_t n_tiles, 
   mt = r / gsize;
 }
 
-template <class Tr, int WM, int WN, int EPI>
-__global__ void __launch_bounds__(64 * WM * WN, 2) gemm_nt_kernel(GemmParams p) {
-  using C = Cfg<Tr, WM, WN>;
+template <class Tr, class C, bool AL, int EPI>
+__global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_nt_kernel(GemmParams p) {
   using E = typename Tr::E;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   E* lds = reinterpret_cast<E*>(smem_raw);
@@ -249,49 +277,49 @@ __global__ void __launch_bounds__(64 * WM * WN, 2) gemm_nt_kernel(GemmParams p) 
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid / WN, wn = wid % WN;
+  const int wm = wid / C::WN, wn = wid % C::WN;
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[C::MI][C::NI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < C::NI; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  mainloop<Tr, WM, WN>(p.L1, p.R1, mt, nt, p.K1, lds, acc);
+  mainloop<Tr, C, AL>(p.L1, p.R1, mt, nt, p.K1, lds, acc);
 
   if constexpr (EPI == EPI_STORE) {
     E* out = static_cast<E*>(p.C);
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const int64_t n = nt * C::BN + wn * 64 + ni * 32 + (lane & 31);
+      for (int ni = 0; ni < C::NI; ++ni) {
+        const int64_t n = nt * C::BN + wn * 32 * C::NI + ni * 32 + (lane & 31);
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int64_t m =
-              mt * C::BM + wm * 64 + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int64_t m = mt * C::BM + wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) +
+                            4 * (lane >> 5) + (e & 3);
           if (m < p.m_rows && n < p.n_cols) out[m * p.c_ld + n] = from_f32<E>(acc[mi][ni][e]);
         }
       }
     return;
   } else {
-    float colsum[2];
+    float colsum[C::NI];
     if constexpr (EPI == EPI_GHOST) {
-      f32x16_t acc2[2][2];
+      f32x16_t acc2[C::MI][C::NI];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < C::NI; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc2[i][j][e] = 0.f;
-      mainloop<Tr, WM, WN>(p.L2, p.R2, mt, nt, p.K2, lds, acc2);
+      mainloop<Tr, C, AL>(p.L2, p.R2, mt, nt, p.K2, lds, acc2);
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
+      for (int ni = 0; ni < C::NI; ++ni) {
         float s = 0.f;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             if (p.rounding == GS_ROUND_REF_BF16)
@@ -305,6 +333,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 2) gemm_nt_kernel(GemmParams p) 
       constexpr int ZLD = C::BM + Tr::ZPAD;
       constexpr int CPR = C::BM / Tr::VEC;
       constexpr int NQ = C::BN * CPR / C::NT;
+      static_assert(C::BN * ZLD * sizeof(E) + C::WM * C::BN * 4 <= C::LDS_BYTES, "Z tile");
       const E* Zb = static_cast<const E*>(p.Z);
       const int kc = tid % CPR;
       const int64_t m0 = mt * C::BM + kc * Tr::VEC;
@@ -313,6 +342,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 2) gemm_nt_kernel(GemmParams p) 
         const int r = tid / CPR + q * (C::NT / CPR);
         const int64_t f = nt * C::BN + r;
         union { uint4 v; E e[Tr::VEC]; } u;
+        u.v = make_uint4(0u, 0u, 0u, 0u);
         if (f < p.z_map.total()) {
           const int64_t seg = f / p.z_map.seglen;
           const E* zr = Zb + p.z_map.phys_row(seg, f - seg * p.z_map.seglen) * p.z_ld;
@@ -322,22 +352,19 @@ __global__ void __launch_bounds__(64 * WM * WN, 2) gemm_nt_kernel(GemmParams p) 
 #pragma unroll
             for (int v = 0; v < Tr::VEC; ++v) u.e[v] = (m0 + v < p.m_rows) ? zr[m0 + v] : E(0);
           }
-        } else {
-#pragma unroll
-          for (int v = 0; v < Tr::VEC; ++v) u.e[v] = E(0);
         }
         *reinterpret_cast<uint4*>(lds + r * ZLD + kc * Tr::VEC) = u.v;
       }
       __syncthreads();
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const int nl = wn * 64 + ni * 32 + (lane & 31);
+      for (int ni = 0; ni < C::NI; ++ni) {
+        const int nl = wn * 32 * C::NI + ni * 32 + (lane & 31);
         float s = 0.f;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const int ml = wm * 64 + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const int ml = wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
             s += acc[mi][ni][e] * to_f32<E>(lds[nl * ZLD + ml]);
           }
         colsum[ni] = s;
@@ -347,33 +374,47 @@ __global__ void __launch_bounds__(64 * WM * WN, 2) gemm_nt_kernel(GemmParams p) 
     // Combine the two half-waves (rows 4*(l/32)+..), then the WM waves sharing columns.
     float* red = reinterpret_cast<float*>(smem_raw);
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
+    for (int ni = 0; ni < C::NI; ++ni) {
       const float s = colsum[ni] + __shfl_xor(colsum[ni], 32, 64);
-      if (lane < 32) red[wm * C::BN + wn * 64 + ni * 32 + lane] = s;
+      if (lane < 32) red[wm * C::BN + wn * 32 * C::NI + ni * 32 + lane] = s;
     }
     __syncthreads();
-    if (tid < C::BN) {
+    if (p.tile_reduce) {
+      // Every column of this tile belongs to one train sample: one partial per tile.
+      __shared__ float tred[C::NT / 64];
+      float v = 0.f;
+      for (int c = tid; c < C::BN; c += C::NT) {
+#pragma unroll
+        for (int w = 0; w < C::WM; ++w) v += red[w * C::BN + c];
+      }
+      v = block_sum(v, tred);
+      if (tid == 0) p.P[(p.p_row0 + mt) * p.p_ld + nt] = v;
+      return;
+    }
+    for (int c = tid; c < C::BN; c += C::NT) {
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < WM; ++w) s += red[w * C::BN + tid];
-      const int64_t n = nt * C::BN + tid;
+      for (int w = 0; w < C::WM; ++w) s += red[w * C::BN + c];
+      const int64_t n = nt * C::BN + c;
       if (n < p.p_ld) p.P[(p.p_row0 + mt) * p.p_ld + n] = s;
     }
   }
 }
 
-// P[g*rows_per_group + r][i*T + t] summed over r and t -> out_pair[g][i], out_dot[i].
+// P[(g*rows_per_group + r) * p_ld + i*cols + c] summed over r < rows_per_group and c < cols
+// -> out_pair[g][i] (optional) and out_dot[i] = sum_g; one block per train sample, fixed order.
 __global__ void reduce_partials_kernel(const float* __restrict__ P, int64_t groups,
-                                       int64_t rows_per_group, int64_t p_ld, int64_t T,
+                                       int64_t rows_per_group, int64_t p_ld, int64_t cols,
                                        int64_t n_train, float* out_pair, float* out_dot) {
   __shared__ float red[16];
   const int64_t i = blockIdx.x;
+  const int64_t per = rows_per_group * cols;
   float dot = 0.f;
   for (int64_t g = 0; g < groups; ++g) {
     float s = 0.f;
-    for (int64_t r = 0; r < rows_per_group; ++r) {
-      const float* row = P + (g * rows_per_group + r) * p_ld + i * T;
-      for (int64_t t = threadIdx.x; t < T; t += blockDim.x) s += row[t];
+    for (int64_t x = threadIdx.x; x < per; x += blockDim.x) {
+      const int64_t r = x / cols, c = x - r * cols;
+      s += P[(g * rows_per_group + r) * p_ld + i * cols + c];
     }
     s = block_sum(s, red);
     if (out_pair != nullptr && threadIdx.x == 0) out_pair[g * n_train + i] = s;
@@ -382,34 +423,72 @@ __global__ void reduce_partials_kernel(const float* __restrict__ P, int64_t grou
   if (threadIdx.x == 0 && out_dot != nullptr) out_dot[i] = dot;
 }
 
-// out[f][c] = in-row c, feature f  (c over the row set; with `presum`, c = position and the
-// value is summed over all segments).  64 x 64 tiles through LDS, fp32 accumulation.
+// out[f][c] = row c of the row set, feature f (with `presum`: c = position, summed over all
+// segments in fp32).  64 x 64 tiles: 16-byte loads along features, a padded LDS tile, and
+// 16-byte stores along c.  Requires d % 8 == 0 and 16-byte aligned rows when `vec`.
 template <class E>
-__global__ void transpose_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap map,
-                                      int64_t d, int presum, E* __restrict__ out,
-                                      int64_t out_ld) {
-  __shared__ float tile[64][65];
-  const int64_t f0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * 64;
+__global__ void __launch_bounds__(256) transpose_rows_kernel(const E* __restrict__ in, int64_t ld,
+                                                             RowMap map, int64_t d, int presum,
+                                                             int vec, E* __restrict__ out,
+                                                             int64_t out_ld) {
+  constexpr int TILE = 64, VE = 16 / sizeof(E), CH = TILE / VE;  // chunks per tile row
+  __shared__ E tile[TILE][TILE];
+  const int64_t f0 = static_cast<int64_t>(blockIdx.x) * TILE;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * TILE;
   const int64_t ncols = presum ? map.seglen : map.total();
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 256 threads: 4 rows per pass
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t c = c0 + r, f = f0 + tx;
-    float v = 0.f;
-    if (c < ncols && f < d) {
-      if (presum) {
-        for (int64_t s = 0; s < map.nseg; ++s) v += to_f32<E>(in[map.phys_row(s, c) * ld + f]);
-      } else {
-        const int64_t seg = c / map.seglen;
-        v = to_f32<E>(in[map.phys_row(seg, c - seg * map.seglen) * ld + f]);
+  for (int x = threadIdx.x; x < TILE * CH; x += blockDim.x) {
+    const int r = x / CH, ch = x % CH;   // r: row of the set (token), ch: feature chunk
+    const int64_t c = c0 + r, f = f0 + ch * VE;
+    float acc[VE];
+#pragma unroll
+    for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+    if (c < ncols) {
+      const int64_t nseg = presum ? map.nseg : 1;
+      for (int64_t sgi = 0; sgi < nseg; ++sgi) {
+        int64_t row;
+        if (presum) {
+          row = map.phys_row(sgi, c);
+        } else {
+          const int64_t seg = c / map.seglen;
+          row = map.phys_row(seg, c - seg * map.seglen);
+        }
+        const E* src = in + row * ld + f;
+        if (vec && f + VE <= d) {
+          union { uint4 u; E e[VE]; } w;
+          w.u = *reinterpret_cast<const uint4*>(src);
+#pragma unroll
+          for (int v = 0; v < VE; ++v) acc[v] += to_f32<E>(w.e[v]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VE; ++v)
+            if (f + v < d) acc[v] += to_f32<E>(src[v]);
+        }
       }
     }
-    tile[r][tx] = v;
+    // XOR-swizzled chunk position keeps the column reads below free of bank conflicts.
+    const int sw = (ch ^ (r >> 3)) & (CH - 1);
+#pragma unroll
+    for (int v = 0; v < VE; ++v) tile[r][sw * VE + v] = from_f32<E>(acc[v]);
   }
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t f = f0 + r, c = c0 + tx;
-    if (f < d && c < ncols) out[f * out_ld + c] = from_f32<E>(tile[tx][r]);
+  for (int x = threadIdx.x; x < TILE * CH; x += blockDim.x) {
+    const int fr = x / CH, ch = x % CH;  // fr: feature in tile, ch: chunk of columns
+    const int64_t f = f0 + fr, c = c0 + ch * VE;
+    if (f >= d) continue;
+    union { uint4 u; E e[VE]; } w;
+#pragma unroll
+    for (int v = 0; v < VE; ++v) {
+      const int row = ch * VE + v;
+      w.e[v] = tile[row][(((fr / VE) ^ (row >> 3)) & (CH - 1)) * VE + fr % VE];
+    }
+    E* dst = out + f * out_ld + c;
+    if (vec && c + VE <= ncols) {
+      *reinterpret_cast<uint4*>(dst) = w.u;
+    } else {
+#pragma unroll
+      for (int v = 0; v < VE; ++v)
+        if (c + v < ncols) dst[v] = w.e[v];
+    }
   }
 }
 
@@ -428,39 +507,52 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 }
 
 // ------------------------------------------------------------------------------ host side
+// Tile shapes per epilogue (overridable at build time for tuning sweeps).
+#ifndef GS_GHOST_TILE
+#define GS_GHOST_TILE 4, 2, 2, 2
+#endif
+#ifndef GS_ROWDOT_TILE
+#define GS_ROWDOT_TILE 2, 2, 2, 2
+#endif
+#ifndef GS_STORE_TILE
+#define GS_STORE_TILE 2, 2, 2, 2
+#endif
+// fp32 operands (precision checks, fp32 models) keep the small 128 x 128 tile.
+template <class Tr, int... Tile>
+using PickCfg = std::conditional_t<std::is_same<Tr, TrF32>::value, Cfg<Tr, 2, 2, 2, 2>,
+                                   Cfg<Tr, Tile...>>;
+template <class Tr> using GhostCfg = PickCfg<Tr, GS_GHOST_TILE>;
+template <class Tr> using RowdotCfg = PickCfg<Tr, GS_ROWDOT_TILE>;
+template <class Tr> using StoreCfg = PickCfg<Tr, GS_STORE_TILE>;
+
 namespace {
 
-constexpr int WM = 2, WN = 2;
-
-template <class Tr>
+template <class Tr, class C>
 struct Launch {
-  using C = Cfg<Tr, WM, WN>;
-  static int run(int epi, GemmParams& p, hipStream_t s) {
+  template <int EPI>
+  static int run(GemmParams& p, bool aligned, hipStream_t s) {
     const int64_t blocks = p.m_tiles * p.n_tiles;
     if (blocks <= 0) return GS_OK;
     if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
-    const size_t lds = C::LDS_BYTES;
-    if (epi == EPI_GHOST) return go(gemm_nt_kernel<Tr, WM, WN, EPI_GHOST>, grid, block, lds, p, s);
-    if (epi == EPI_ROWDOT) return go(gemm_nt_kernel<Tr, WM, WN, EPI_ROWDOT>, grid, block, lds, p, s);
-    return go(gemm_nt_kernel<Tr, WM, WN, EPI_STORE>, grid, block, lds, p, s);
+    if (aligned) return go(gemm_nt_kernel<Tr, C, true, EPI>, grid, block, p, s);
+    return go(gemm_nt_kernel<Tr, C, false, EPI>, grid, block, p, s);
   }
-  // Raises the dynamic-LDS limit of the kernel once (the stage buffers exceed 64 KiB).
-  static int go(void (*k)(GemmParams), dim3 grid, dim3 block, size_t lds, GemmParams& p,
-                hipStream_t s) {
-    static thread_local const void* raised[4] = {nullptr, nullptr, nullptr, nullptr};
+  // Raises the dynamic-LDS limit of each kernel once (the stage buffers exceed 64 KiB).
+  static int go(void (*k)(GemmParams), dim3 grid, dim3 block, GemmParams& p, hipStream_t s) {
+    static thread_local const void* raised[16] = {};
     const void* key = reinterpret_cast<const void*>(k);
     bool done = false;
     for (const void* r : raised) done = done || r == key;
     if (!done) {
       const hipError_t e = hipFuncSetAttribute(key, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(lds));
+                                               static_cast<int>(C::LDS_BYTES));
       if (e != hipSuccess)
         return fail(GS_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
       for (auto& r : raised)
         if (r == nullptr) { r = key; break; }
     }
-    hipLaunchKernelGGL(k, grid, block, lds, s, p);
+    hipLaunchKernelGGL(k, grid, block, C::LDS_BYTES, s, p);
     return check_launch("gemm_nt_kernel");
   }
 };
@@ -488,42 +580,57 @@ int64_t host_tiles(const Operand& o) {
 struct LinearPlan {
   int algo;        // GS_ALGO_GHOST or GS_ALGO_VALGRAD
   int ghost_flat;  // GHOST left side tiled flat (dot only, pairwise)
-  int64_t n_st;    // GHOST: position tiles per val segment
   int64_t p_rows;  // rows of the partial buffer
   int64_t groups;  // groups in the final reduction
   int64_t vcols;   // VALGRAD: columns of the transposed val operands
+  int tile_reduce; // partials per tile instead of per train row
+  int64_t p_ld;    // P row length: n-tiles (tile_reduce) or train rows
+  int64_t cols;    // P entries per train sample in a P row
 };
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+template <class Tr>
 LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
                        int semantics, int algo, int want_pair) {
-  constexpr int64_t BM = 64 * WM;
+  constexpr int64_t GBM = GhostCfg<Tr>::BM, RBM = RowdotCfg<Tr>::BM;
   const int64_t n_t = N - n_val;
   const int64_t nv_eff = semantics == GS_SEM_PRESUM ? 1 : n_val;  // val rows after presum
   LinearPlan pl{};
   // MFMA flops including tile padding.
-  const double ghost_flat_m = static_cast<double>(ceil_div(nv_eff * T, BM) * BM);
-  const double ghost_seg_m = static_cast<double>(nv_eff * ceil_div(T, BM) * BM);
   const bool flat = !want_pair;
-  const double ghost = 2.0 * n_t * T * (flat ? ghost_flat_m : ghost_seg_m) * (d_in + d_out);
-  const double rowdot = 2.0 * n_t * T * ceil_div(d_out, BM) * BM * d_in;
+  const double ghost_m = flat ? static_cast<double>(ceil_div(nv_eff * T, GBM) * GBM)
+                              : static_cast<double>(nv_eff * ceil_div(T, GBM) * GBM);
+  const double ghost = 2.0 * n_t * T * ghost_m * (d_in + d_out);
+  const double rowdot = 2.0 * n_t * T * ceil_div(d_out, RBM) * RBM * d_in;
   const double vgemm = 2.0 * nv_eff * T * d_out * d_in;
   const double valgrad = vgemm + rowdot * (want_pair ? n_val : 1);
   pl.algo = algo;
   if (algo == GS_ALGO_AUTO) pl.algo = ghost <= valgrad ? GS_ALGO_GHOST : GS_ALGO_VALGRAD;
+  int64_t bn;
   if (pl.algo == GS_ALGO_GHOST) {
     pl.ghost_flat = flat ? 1 : 0;
-    pl.n_st = ceil_div(T, BM);
-    pl.p_rows = flat ? ceil_div(nv_eff * T, BM) : nv_eff * pl.n_st;
+    pl.p_rows = flat ? ceil_div(nv_eff * T, GBM) : nv_eff * ceil_div(T, GBM);
     pl.groups = flat ? 1 : nv_eff;
+    bn = GhostCfg<Tr>::BN;
   } else {
-    const int64_t n_mt = ceil_div(d_out, BM);
+    const int64_t n_mt = ceil_div(d_out, RBM);
     pl.groups = want_pair ? n_val : 1;
     pl.p_rows = pl.groups * n_mt;
     pl.vcols = nv_eff * T;
+    bn = RowdotCfg<Tr>::BN;
   }
+  pl.tile_reduce = (T % bn == 0) ? 1 : 0;
+  pl.p_ld = pl.tile_reduce ? n_t * T / bn : n_t * T;
+  pl.cols = pl.tile_reduce ? T / bn : T;
   return pl;
+}
+
+LinearPlan plan_any(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
+                    int semantics, int algo, int want_pair) {
+  if (dtype == GS_DTYPE_F32)
+    return plan_linear<TrF32>(N, n_val, T, d_in, d_out, semantics, algo, want_pair);
+  return plan_linear<TrBF16>(N, n_val, T, d_in, d_out, semantics, algo, want_pair);
 }
 
 template <class S>
@@ -541,7 +648,7 @@ void carve_linear(S& c, const LinearPlan& pl, int dtype, int64_t N, int64_t n_va
     c.template take<char>(d_out * pl.vcols * esz);
     c.template take<char>(d_out * d_in * esz);
   }
-  c.template take<float>(pl.p_rows * n_t * T);
+  c.template take<float>(pl.p_rows * pl.p_ld);
 }
 
 bool linear_args_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
@@ -559,23 +666,18 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
                int64_t T, int64_t d_in, int64_t d_out, int semantics, int rounding,
                float* out_dot, float* out_pair, const LinearPlan& pl, Carver& cv, hipStream_t s) {
   using E = typename Tr::E;
-  using C = Cfg<Tr, WM, WN>;
+  using GC = GhostCfg<Tr>;
+  using RC = RowdotCfg<Tr>;
+  using SC = StoreCfg<Tr>;
   const size_t esz = sizeof(E);
   const int64_t n_t = N - n_val;
   const RowMap tr = train_rows(N, n_val, val_start, T);
   const RowMap va = val_rows(n_val, val_start, T);
-  const int dt = std::is_same<E, float>::value ? GS_DTYPE_F32 : GS_DTYPE_BF16;
-  (void)dt;
-
-  GemmParams p{};
-  p.p_ld = n_t * T;
-  p.rounding = rounding;
 
   if (pl.algo == GS_ALGO_GHOST) {
     const void* La = A;
     const void* Lg = G;
     RowMap lmap = va;
-    int64_t lda = d_in, ldg = d_out;
     if (semantics == GS_SEM_PRESUM) {
       E* abar = reinterpret_cast<E*>(cv.take<char>(T * d_in * esz));
       E* gbar = reinterpret_cast<E*>(cv.take<char>(T * d_out * esz));
@@ -589,25 +691,29 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
       La = abar;
       Lg = gbar;
       lmap = plain_rows(T);
-      lda = d_in;
-      ldg = d_out;
     }
-    float* P = cv.take<float>(pl.p_rows * n_t * T);
-    p.L1 = make_operand(La, lda, lmap, pl.ghost_flat ? 0 : 1, d_in, esz);
+    float* P = cv.take<float>(pl.p_rows * pl.p_ld);
+    GemmParams p{};
+    p.p_ld = pl.p_ld;
+    p.tile_reduce = pl.tile_reduce;
+    p.rounding = rounding;
+    p.L1 = make_operand(La, d_in, lmap, pl.ghost_flat ? 0 : 1, d_in, esz);
     p.R1 = make_operand(A, d_in, tr, 0, d_in, esz);
-    p.L2 = make_operand(Lg, ldg, lmap, pl.ghost_flat ? 0 : 1, d_out, esz);
+    p.L2 = make_operand(Lg, d_out, lmap, pl.ghost_flat ? 0 : 1, d_out, esz);
     p.R2 = make_operand(G, d_out, tr, 0, d_out, esz);
     p.K1 = d_in;
     p.K2 = d_out;
-    p.m_tiles = host_tiles<C::BM>(p.L1);
-    p.n_tiles = host_tiles<C::BN>(p.R1);
+    p.m_tiles = host_tiles<GC::BM>(p.L1);
+    p.n_tiles = host_tiles<GC::BN>(p.R1);
     p.P = P;
     p.p_row0 = 0;
     if (p.m_tiles != pl.p_rows) return fail(GS_ERR_INVALID, "internal: ghost partial rows");
-    int rc = Launch<Tr>::run(EPI_GHOST, p, s);
+    const bool al = p.L1.vec_ok && p.R1.vec_ok && p.L2.vec_ok && p.R2.vec_ok;
+    int rc = Launch<Tr, GC>::template run<EPI_GHOST>(p, al, s);
     if (rc) return rc;
     hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s,
-                       P, pl.groups, pl.p_rows / pl.groups, p.p_ld, T, n_t, out_pair, out_dot);
+                       P, pl.groups, pl.p_rows / pl.groups, pl.p_ld, pl.cols, n_t, out_pair,
+                       out_dot);
     return check_launch("reduce_partials_kernel");
   }
 
@@ -616,21 +722,25 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   E* At = reinterpret_cast<E*>(cv.take<char>(d_in * pl.vcols * esz));
   E* Gt = reinterpret_cast<E*>(cv.take<char>(d_out * pl.vcols * esz));
   E* V = reinterpret_cast<E*>(cv.take<char>(d_out * d_in * esz));
-  float* P = cv.take<float>(pl.p_rows * n_t * T);
+  float* P = cv.take<float>(pl.p_rows * pl.p_ld);
   const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
   {
     const dim3 ga(static_cast<unsigned>(ceil_div(d_in, 64)),
                   static_cast<unsigned>(ceil_div(pl.vcols, 64)));
     const dim3 gg(static_cast<unsigned>(ceil_div(d_out, 64)),
                   static_cast<unsigned>(ceil_div(pl.vcols, 64)));
+    const int vec_a = aligned16(A) && aligned16(At) && (d_in * esz) % 16 == 0 &&
+                      (pl.vcols * esz) % 16 == 0;
+    const int vec_g = aligned16(G) && aligned16(Gt) && (d_out * esz) % 16 == 0 &&
+                      (pl.vcols * esz) % 16 == 0;
     hipLaunchKernelGGL(transpose_rows_kernel<E>, ga, dim3(256), 0, s, static_cast<const E*>(A),
-                       d_in, va, d_in, presum, At, pl.vcols);
+                       d_in, va, d_in, presum, vec_a, At, pl.vcols);
     hipLaunchKernelGGL(transpose_rows_kernel<E>, gg, dim3(256), 0, s, static_cast<const E*>(G),
-                       d_out, va, d_out, presum, Gt, pl.vcols);
+                       d_out, va, d_out, presum, vec_g, Gt, pl.vcols);
     int rc = check_launch("transpose_rows_kernel");
     if (rc) return rc;
   }
-  const int64_t n_mt = ceil_div(d_out, C::BM);
+  const int64_t n_mt = ceil_div(d_out, RC::BM);
   const int64_t vsteps = pl.groups;  // one V per val row for pairs, else one V
   const int64_t kper = pl.vcols / vsteps;
   for (int64_t j = 0; j < vsteps; ++j) {
@@ -638,13 +748,13 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     q.L1 = make_operand(Gt + j * kper, pl.vcols, plain_rows(d_out), 0, kper, esz);
     q.R1 = make_operand(At + j * kper, pl.vcols, plain_rows(d_in), 0, kper, esz);
     q.K1 = kper;
-    q.m_tiles = host_tiles<C::BM>(q.L1);
-    q.n_tiles = host_tiles<C::BN>(q.R1);
+    q.m_tiles = host_tiles<SC::BM>(q.L1);
+    q.n_tiles = host_tiles<SC::BN>(q.R1);
     q.m_rows = d_out;
     q.n_cols = d_in;
     q.C = V;
     q.c_ld = d_in;
-    int rc = Launch<Tr>::run(EPI_STORE, q, s);
+    int rc = Launch<Tr, SC>::template run<EPI_STORE>(q, q.L1.vec_ok && q.R1.vec_ok, s);
     if (rc) return rc;
 
     GemmParams r{};
@@ -652,20 +762,21 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     r.R1 = make_operand(A, d_in, tr, 0, d_in, esz);
     r.K1 = d_in;
     r.m_tiles = n_mt;
-    r.n_tiles = host_tiles<C::BN>(r.R1);
+    r.n_tiles = host_tiles<RC::BN>(r.R1);
     r.m_rows = d_out;
     r.P = P;
-    r.p_ld = n_t * T;
+    r.p_ld = pl.p_ld;
+    r.tile_reduce = pl.tile_reduce;
     r.p_row0 = j * n_mt;
     r.Z = G;
     r.z_ld = d_out;
     r.z_map = tr;
     r.z_vec_ok = aligned16(G) && (d_out * static_cast<int64_t>(esz)) % 16 == 0;
-    rc = Launch<Tr>::run(EPI_ROWDOT, r, s);
+    rc = Launch<Tr, RC>::template run<EPI_ROWDOT>(r, r.L1.vec_ok && r.R1.vec_ok, s);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s, P,
-                     pl.groups, n_mt, n_t * T, T, n_t, out_pair, out_dot);
+                     pl.groups, n_mt, pl.p_ld, pl.cols, n_t, out_pair, out_dot);
   return check_launch("reduce_partials_kernel");
 }
 
@@ -678,7 +789,7 @@ extern "C" size_t gs_linear_dot_workspace(int dtype, int64_t N, int64_t n_val, i
                                           int64_t d_in, int64_t d_out, int semantics, int algo,
                                           int want_pair) {
   if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair)) return 0;
-  const LinearPlan pl = plan_linear(N, n_val, T, d_in, d_out, semantics, algo, want_pair);
+  const LinearPlan pl = plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair);
   Sizer sz;
   carve_linear(sz, pl, dtype, N, n_val, T, d_in, d_out, semantics);
   return sz.used + 256;
@@ -688,7 +799,7 @@ extern "C" int gs_linear_dot_algo(int dtype, int64_t N, int64_t n_val, int64_t T
                                   int64_t d_out, int semantics, int algo, int want_pair) {
   if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair))
     return fail(GS_ERR_INVALID, "gs_linear_dot_algo: invalid arguments");
-  return plan_linear(N, n_val, T, d_in, d_out, semantics, algo, want_pair).algo;
+  return plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair).algo;
 }
 
 extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
@@ -707,7 +818,7 @@ extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N,
     return fail(GS_ERR_INVALID, "gs_linear_dot: null pointer");
   if (rounding != GS_ROUND_FP32 && rounding != GS_ROUND_REF_BF16)
     return fail(GS_ERR_INVALID, "gs_linear_dot: invalid rounding");
-  const LinearPlan pl = plan_linear(N, n_val, T, d_in, d_out, semantics, algo, want_pair);
+  const LinearPlan pl = plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair);
   Sizer sz;
   carve_linear(sz, pl, dtype, N, n_val, T, d_in, d_out, semantics);
   if (workspace == nullptr || workspace_bytes < sz.used)

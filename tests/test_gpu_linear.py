@@ -20,6 +20,7 @@ SHAPES = [
     (80, 16, 1, 512, 1024),   # the MLP layer shape (T = 1)
     (8, 2, 300, 200, 136),    # T and K not multiples of the tile sizes
     (12, 4, 130, 64, 10),     # d_out = 10: unaligned rows, scalar loads
+    (6, 2, 256, 128, 192),    # T a multiple of the tile width: per-tile partial sums
 ]
 
 

@@ -72,6 +72,7 @@ struct Operand {
   RowMap map;
   int per_seg;
   int vec_ok;       // 16-byte loads allowed (aligned base, ld and K tail)
+  int64_t nbytes;   // extent of the tensor behind `base` (buffer-resource range)
 };
 
 struct GemmParams {
@@ -248,6 +249,185 @@ __device__ __forceinline__ void mainloop(const Operand& L, const Operand& R, int
   }
 }
 
+// ---------------------------------------------------------------- LDS-DMA mainloop (bf16)
+// Operand tiles go global -> LDS directly (buffer_load_dwordx4 ... lds): each wave-level
+// load moves 8 rows x 128 bytes (64 lanes x 16 B), lane i landing at M0 + 16 i.  Rows are
+// stored unpadded with the 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7): a 16-lane
+// group of ds_read_b128 is served from one 256-byte bank window (two rows), and this
+// swizzle gives the 16 rows of a fragment read 16 distinct 16-byte bank groups.  Lanes whose row or
+// k-chunk is out of range get an out-of-range buffer offset and write zeros.  Three stage
+// buffers (separate __shared__ arrays, so the compiler's LDS-DMA tracking does not force a
+// full vmcnt drain before each read) let the loads of stage k+2 overlap the MFMAs of stage k.
+// One wave-level DMA: lane i's 16 bytes at buffer offset voff land at LDS address
+// lds_addr + 16 i.  Issued as inline asm so that the compiler's own LDS-DMA tracking, which
+// has only a few slots and otherwise drains vmcnt before every LDS read, stays out of the
+// way; the mainloop orders these loads with explicit s_waitcnt vmcnt.  Nothing else in the
+// kernels uses M0.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                      const unsigned char* lds_dst) {
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds_dst));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(addr)), "v"(voff), "s"(r)
+               : "memory");
+}
+constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
+constexpr int DMA_ROW_BYTES = 128;  // BK = 64 bf16
+
+template <class C>
+struct DmaCfg {
+  static constexpr int NW = C::WM * C::WN;
+  static constexpr int GROUPS_L = C::BM / 8, GROUPS_R = C::BN / 8;
+  static constexpr int QL = GROUPS_L / NW, QR = GROUPS_R / NW;  // loads per wave per stage
+  static_assert(GROUPS_L % NW == 0 && GROUPS_R % NW == 0, "row groups must split over waves");
+  static constexpr int STAGE_BYTES = (C::BM + C::BN) * DMA_ROW_BYTES;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           static_cast<int>(nbytes), 0x00020000);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  // s_waitcnt: vmcnt = N (bits 3:0 and 15:14), expcnt and lgkmcnt left at their maxima.
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+  asm volatile("" ::: "memory");
+}
+
+// Barrier without the release/acquire fences of __syncthreads (those drain every LDS DMA in
+// flight); the caller orders LDS traffic with explicit s_waitcnt.
+__device__ __forceinline__ void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <class C>
+struct DmaStreamer {
+  using D = DmaCfg<C>;
+  __amdgpu_buffer_rsrc_t rl, rr;
+  unsigned offl[D::QL], offr[D::QR];  // row byte offset + chunk byte offset, or DMA_OOB
+  int kl[D::QL], kr[D::QR];            // this lane's k element offset within a stage
+
+  __device__ __forceinline__ void init(const Operand& L, const Operand& R, int64_t mt, int64_t nt,
+                                       int64_t K) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int sub = lane >> 3, slot = lane & 7;
+    rl = make_rsrc(L.base, L.nbytes);
+    rr = make_rsrc(R.base, R.nbytes);
+#pragma unroll
+    for (int q = 0; q < D::QL; ++q) {
+      const int r = 8 * (wid + D::NW * q) + sub;
+      const int c = slot ^ ((r >> 1) & 7);
+      const int64_t pr = tile_row<C::BM>(L, mt, r);
+      offl[q] = pr < 0 ? DMA_OOB : static_cast<unsigned>(pr * L.ld * 2 + c * 16);
+      kl[q] = c * 8;
+    }
+#pragma unroll
+    for (int q = 0; q < D::QR; ++q) {
+      const int r = 8 * (wid + D::NW * q) + sub;  // row within the R block of the stage
+      const int c = slot ^ (((C::BM + r) >> 1) & 7);
+      const int64_t pr = tile_row<C::BN>(R, nt, r);
+      offr[q] = pr < 0 ? DMA_OOB : static_cast<unsigned>(pr * R.ld * 2 + c * 16);
+      kr[q] = c * 8;
+    }
+    (void)K;
+  }
+  template <int S>
+  __device__ __forceinline__ void issue(unsigned char* stage, int64_t k0, int64_t K) {
+    const int wid = threadIdx.x >> 6;
+    const unsigned kb = static_cast<unsigned>(k0 * 2);
+#pragma unroll
+    for (int q = 0; q < D::QL; ++q) {
+      const bool kin = k0 + kl[q] < K;
+      const unsigned off = (kin && offl[q] != DMA_OOB) ? offl[q] + kb : DMA_OOB;
+      dma16(rl, off, stage + (wid + D::NW * q) * 8 * DMA_ROW_BYTES);
+    }
+#pragma unroll
+    for (int q = 0; q < D::QR; ++q) {
+      const bool kin = k0 + kr[q] < K;
+      const unsigned off = (kin && offr[q] != DMA_OOB) ? offr[q] + kb : DMA_OOB;
+      dma16(rr, off, stage + (C::BM + 8 * (wid + D::NW * q)) * DMA_ROW_BYTES);
+    }
+  }
+};
+
+template <class C>
+__device__ __forceinline__ void dma_compute(const unsigned char* stage, f32x16_t (&acc)[C::MI][C::NI]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  const int lo = (lane >> 1) & 7, hi = lane >> 5;  // rows start at multiples of 32
+  const unsigned char* lt = stage + (wm * 32 * C::MI + (lane & 31)) * DMA_ROW_BYTES;
+  const unsigned char* rt = stage + (C::BM + wn * 32 * C::NI + (lane & 31)) * DMA_ROW_BYTES;
+  bf16x8_t a[2][C::MI], b[2][C::NI];
+  auto load = [&](int buf, int ks) {
+    const int off = (((2 * ks + hi) ^ lo)) * 16;
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i)
+      a[buf][i] = *reinterpret_cast<const bf16x8_t*>(lt + i * 32 * DMA_ROW_BYTES + off);
+#pragma unroll
+    for (int j = 0; j < C::NI; ++j)
+      b[buf][j] = *reinterpret_cast<const bf16x8_t*>(rt + j * 32 * DMA_ROW_BYTES + off);
+  };
+  load(0, 0);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks + 1 < 4) load((ks + 1) & 1, ks + 1);
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j],
+                                                            acc[i][j], 0, 0, 0);
+  }
+}
+
+template <class C>
+struct DmaLds {
+  unsigned char* s0;
+  unsigned char* s1;
+  unsigned char* s2;
+};
+
+template <class C, int S>
+__device__ __forceinline__ unsigned char* dma_slot(const DmaLds<C>& l) {
+  return S == 0 ? l.s0 : (S == 1 ? l.s1 : l.s2);
+}
+
+template <class C, int S>
+__device__ __forceinline__ void dma_step(DmaStreamer<C>& st, const DmaLds<C>& l, int64_t kt,
+                                         int64_t nk, int64_t K, f32x16_t (&acc)[C::MI][C::NI]) {
+  constexpr int NQ = DmaCfg<C>::QL + DmaCfg<C>::QR;
+  if (kt + 1 < nk)
+    wait_vmcnt<NQ>();
+  else
+    wait_vmcnt<0>();
+  raw_barrier();
+  if (kt + 2 < nk) st.template issue<(S + 2) % 3>(dma_slot<C, (S + 2) % 3>(l), (kt + 2) * 64, K);
+  dma_compute<C>(dma_slot<C, S>(l), acc);
+}
+
+// acc += L_tile R_tile^T over K, bf16 operands through the LDS-DMA ring.
+template <class C>
+__device__ __forceinline__ void mainloop_dma(const Operand& L, const Operand& R, int64_t mt,
+                                             int64_t nt, int64_t K, const DmaLds<C>& l,
+                                             f32x16_t (&acc)[C::MI][C::NI]) {
+  DmaStreamer<C> st;
+  st.init(L, R, mt, nt, K);
+  const int64_t nk = (K + 63) / 64;
+  st.template issue<0>(l.s0, 0, K);
+  if (nk > 1) st.template issue<1>(l.s1, 64, K);
+  for (int64_t kt = 0; kt < nk; kt += 3) {
+    dma_step<C, 0>(st, l, kt, nk, K, acc);
+    if (kt + 1 < nk) dma_step<C, 1>(st, l, kt + 1, nk, K, acc);
+    if (kt + 2 < nk) dma_step<C, 2>(st, l, kt + 2, nk, K, acc);
+  }
+  wait_vmcnt<0>();
+  raw_barrier();
+}
+
 // Maps the launch index to (m tile, n tile): consecutive workgroups of one XCD get
 // consecutive logical ids, and logical ids sweep GROUP n-tiles per m-tile so that the
 // workgroups resident on an XCD share operand tiles in its L2.
@@ -267,137 +447,192 @@ __device__ __forceinline__ void tile_of_block(int64_t m_tiles, int64_t n_tiles, 
   mt = r / gsize;
 }
 
-template <class Tr, class C, bool AL, int EPI>
-__global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_nt_kernel(GemmParams p) {
-  using E = typename Tr::E;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  E* lds = reinterpret_cast<E*>(smem_raw);
-
-  int64_t mt, nt;
-  tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
-
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid / C::WN, wn = wid % C::WN;
-
-  f32x16_t acc[C::MI][C::NI];
+template <class Tr, class C>
+__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[C::MI][C::NI]) {
 #pragma unroll
   for (int i = 0; i < C::MI; ++i)
 #pragma unroll
     for (int j = 0; j < C::NI; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+}
 
-  mainloop<Tr, C, AL>(p.L1, p.R1, mt, nt, p.K1, lds, acc);
+// C = acc written to p.C (row-major, ld p.c_ld), bounded by p.m_rows x p.n_cols.
+template <class Tr, class C>
+__device__ __forceinline__ void store_epilogue(const GemmParams& p, f32x16_t (&acc)[C::MI][C::NI],
+                                               int64_t mt, int64_t nt) {
+  using E = typename Tr::E;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  E* out = static_cast<E*>(p.C);
+#pragma unroll
+  for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < C::NI; ++ni) {
+      const int64_t n = nt * C::BN + wn * 32 * C::NI + ni * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t m =
+            mt * C::BM + wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < p.m_rows && n < p.n_cols) out[m * p.c_ld + n] = from_f32<E>(acc[mi][ni][e]);
+      }
+    }
+}
 
-  if constexpr (EPI == EPI_STORE) {
-    E* out = static_cast<E*>(p.C);
+// Per-lane column sums of acc (.) acc2 over this wave's rows.
+template <class C>
+__device__ __forceinline__ void ghost_colsum(const GemmParams& p, f32x16_t (&acc)[C::MI][C::NI],
+                                             f32x16_t (&acc2)[C::MI][C::NI],
+                                             float (&colsum)[C::NI]) {
+#pragma unroll
+  for (int ni = 0; ni < C::NI; ++ni) {
+    float s = 0.f;
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < C::NI; ++ni) {
-        const int64_t n = nt * C::BN + wn * 32 * C::NI + ni * 32 + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int64_t m = mt * C::BM + wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) +
-                            4 * (lane >> 5) + (e & 3);
-          if (m < p.m_rows && n < p.n_cols) out[m * p.c_ld + n] = from_f32<E>(acc[mi][ni][e]);
-        }
+      for (int e = 0; e < 16; ++e) {
+        if (p.rounding == GS_ROUND_REF_BF16)
+          s += round_bf16(round_bf16(acc[mi][ni][e]) * round_bf16(acc2[mi][ni][e]));
+        else
+          s += acc[mi][ni][e] * acc2[mi][ni][e];
       }
+    colsum[ni] = s;
+  }
+}
+
+// Per-lane column sums of acc[m][n] * Z[n][m] over this wave's rows; the Z tile
+// [BN rows][BM cols] is staged through `lds` (at least BN * (BM + ZPAD) elements).
+template <class Tr, class C>
+__device__ __forceinline__ void rowdot_colsum(const GemmParams& p, f32x16_t (&acc)[C::MI][C::NI],
+                                              int64_t mt, int64_t nt, typename Tr::E* lds,
+                                              float (&colsum)[C::NI]) {
+  using E = typename Tr::E;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  constexpr int ZLD = C::BM + Tr::ZPAD;
+  constexpr int CPR = C::BM / Tr::VEC;
+  constexpr int NQ = C::BN * CPR / C::NT;
+  const E* Zb = static_cast<const E*>(p.Z);
+  const int kc = tid % CPR;
+  const int64_t m0 = mt * C::BM + kc * Tr::VEC;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int r = tid / CPR + q * (C::NT / CPR);
+    const int64_t f = nt * C::BN + r;
+    union { uint4 v; E e[Tr::VEC]; } u;
+    u.v = make_uint4(0u, 0u, 0u, 0u);
+    if (f < p.z_map.total()) {
+      const int64_t seg = f / p.z_map.seglen;
+      const E* zr = Zb + p.z_map.phys_row(seg, f - seg * p.z_map.seglen) * p.z_ld;
+      if (p.z_vec_ok && m0 + Tr::VEC <= p.m_rows) {
+        u.v = *reinterpret_cast<const uint4*>(zr + m0);
+      } else {
+#pragma unroll
+        for (int v = 0; v < Tr::VEC; ++v) u.e[v] = (m0 + v < p.m_rows) ? zr[m0 + v] : E(0);
+      }
+    }
+    *reinterpret_cast<uint4*>(lds + r * ZLD + kc * Tr::VEC) = u.v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int ni = 0; ni < C::NI; ++ni) {
+    const int nl = wn * 32 * C::NI + ni * 32 + (lane & 31);
+    float s = 0.f;
+#pragma unroll
+    for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int ml = wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        s += acc[mi][ni][e] * to_f32<E>(lds[nl * ZLD + ml]);
+      }
+    colsum[ni] = s;
+  }
+  __syncthreads();  // Z reads done before the reduction scratch reuses LDS
+}
+
+// Combines column sums across the half-waves and the WM waves sharing columns, then writes
+// per-row partials P[p_row0 + mt][n] or, with tile_reduce, one partial P[p_row0 + mt][nt].
+template <class C>
+__device__ __forceinline__ void write_partials(const GemmParams& p, float (&colsum)[C::NI],
+                                               int64_t mt, int64_t nt, float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+#pragma unroll
+  for (int ni = 0; ni < C::NI; ++ni) {
+    const float s = colsum[ni] + __shfl_xor(colsum[ni], 32, 64);
+    if (lane < 32) red[wm * C::BN + wn * 32 * C::NI + ni * 32 + lane] = s;
+  }
+  __syncthreads();
+  if (p.tile_reduce) {
+    __shared__ float tred[C::NT / 64];
+    float v = 0.f;
+    for (int c = tid; c < C::BN; c += C::NT) {
+#pragma unroll
+      for (int w = 0; w < C::WM; ++w) v += red[w * C::BN + c];
+    }
+    v = block_sum(v, tred);
+    if (tid == 0) p.P[(p.p_row0 + mt) * p.p_ld + nt] = v;
     return;
+  }
+  for (int c = tid; c < C::BN; c += C::NT) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < C::WM; ++w) s += red[w * C::BN + c];
+    const int64_t n = nt * C::BN + c;
+    if (n < p.p_ld) p.P[(p.p_row0 + mt) * p.p_ld + n] = s;
+  }
+}
+
+template <class Tr, class C, bool AL, int EPI>
+__global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_nt_kernel(GemmParams p) {
+  using E = typename Tr::E;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  E* lds = reinterpret_cast<E*>(smem_raw);
+  int64_t mt, nt;
+  tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
+  f32x16_t acc[C::MI][C::NI];
+  zero_acc<Tr, C>(acc);
+  mainloop<Tr, C, AL>(p.L1, p.R1, mt, nt, p.K1, lds, acc);
+  if constexpr (EPI == EPI_STORE) {
+    store_epilogue<Tr, C>(p, acc, mt, nt);
   } else {
     float colsum[C::NI];
     if constexpr (EPI == EPI_GHOST) {
       f32x16_t acc2[C::MI][C::NI];
-#pragma unroll
-      for (int i = 0; i < C::MI; ++i)
-#pragma unroll
-        for (int j = 0; j < C::NI; ++j)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) acc2[i][j][e] = 0.f;
+      zero_acc<Tr, C>(acc2);
       mainloop<Tr, C, AL>(p.L2, p.R2, mt, nt, p.K2, lds, acc2);
-#pragma unroll
-      for (int ni = 0; ni < C::NI; ++ni) {
-        float s = 0.f;
-#pragma unroll
-        for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            if (p.rounding == GS_ROUND_REF_BF16)
-              s += round_bf16(round_bf16(acc[mi][ni][e]) * round_bf16(acc2[mi][ni][e]));
-            else
-              s += acc[mi][ni][e] * acc2[mi][ni][e];
-          }
-        colsum[ni] = s;
-      }
-    } else {  // EPI_ROWDOT: Z tile [BN rows][BM cols] through LDS (operand buffers are free)
-      constexpr int ZLD = C::BM + Tr::ZPAD;
-      constexpr int CPR = C::BM / Tr::VEC;
-      constexpr int NQ = C::BN * CPR / C::NT;
-      static_assert(C::BN * ZLD * sizeof(E) + C::WM * C::BN * 4 <= C::LDS_BYTES, "Z tile");
-      const E* Zb = static_cast<const E*>(p.Z);
-      const int kc = tid % CPR;
-      const int64_t m0 = mt * C::BM + kc * Tr::VEC;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int r = tid / CPR + q * (C::NT / CPR);
-        const int64_t f = nt * C::BN + r;
-        union { uint4 v; E e[Tr::VEC]; } u;
-        u.v = make_uint4(0u, 0u, 0u, 0u);
-        if (f < p.z_map.total()) {
-          const int64_t seg = f / p.z_map.seglen;
-          const E* zr = Zb + p.z_map.phys_row(seg, f - seg * p.z_map.seglen) * p.z_ld;
-          if (p.z_vec_ok && m0 + Tr::VEC <= p.m_rows) {
-            u.v = *reinterpret_cast<const uint4*>(zr + m0);
-          } else {
-#pragma unroll
-            for (int v = 0; v < Tr::VEC; ++v) u.e[v] = (m0 + v < p.m_rows) ? zr[m0 + v] : E(0);
-          }
-        }
-        *reinterpret_cast<uint4*>(lds + r * ZLD + kc * Tr::VEC) = u.v;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int ni = 0; ni < C::NI; ++ni) {
-        const int nl = wn * 32 * C::NI + ni * 32 + (lane & 31);
-        float s = 0.f;
-#pragma unroll
-        for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int ml = wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            s += acc[mi][ni][e] * to_f32<E>(lds[nl * ZLD + ml]);
-          }
-        colsum[ni] = s;
-      }
-      __syncthreads();  // Z reads done before the reduction scratch reuses LDS
+      ghost_colsum<C>(p, acc, acc2, colsum);
+    } else {
+      rowdot_colsum<Tr, C>(p, acc, mt, nt, lds, colsum);
     }
-    // Combine the two half-waves (rows 4*(l/32)+..), then the WM waves sharing columns.
-    float* red = reinterpret_cast<float*>(smem_raw);
-#pragma unroll
-    for (int ni = 0; ni < C::NI; ++ni) {
-      const float s = colsum[ni] + __shfl_xor(colsum[ni], 32, 64);
-      if (lane < 32) red[wm * C::BN + wn * 32 * C::NI + ni * 32 + lane] = s;
-    }
-    __syncthreads();
-    if (p.tile_reduce) {
-      // Every column of this tile belongs to one train sample: one partial per tile.
-      __shared__ float tred[C::NT / 64];
-      float v = 0.f;
-      for (int c = tid; c < C::BN; c += C::NT) {
-#pragma unroll
-        for (int w = 0; w < C::WM; ++w) v += red[w * C::BN + c];
-      }
-      v = block_sum(v, tred);
-      if (tid == 0) p.P[(p.p_row0 + mt) * p.p_ld + nt] = v;
-      return;
-    }
-    for (int c = tid; c < C::BN; c += C::NT) {
-      float s = 0.f;
-#pragma unroll
-      for (int w = 0; w < C::WM; ++w) s += red[w * C::BN + c];
-      const int64_t n = nt * C::BN + c;
-      if (n < p.p_ld) p.P[(p.p_row0 + mt) * p.p_ld + n] = s;
-    }
+    write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(smem_raw));
+  }
+}
+
+// bf16, 16-byte aligned operands below 4 GiB: the LDS-DMA mainloop (GHOST and STORE).
+template <class C, int EPI>
+__global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParams p) {
+  constexpr int SB = DmaCfg<C>::STAGE_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char s0[SB];
+  __shared__ __attribute__((aligned(16))) unsigned char s1[SB];
+  __shared__ __attribute__((aligned(16))) unsigned char s2[SB];
+  const DmaLds<C> l{s0, s1, s2};
+  int64_t mt, nt;
+  tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
+  f32x16_t acc[C::MI][C::NI];
+  zero_acc<TrBF16, C>(acc);
+  mainloop_dma<C>(p.L1, p.R1, mt, nt, p.K1, l, acc);
+  if constexpr (EPI == EPI_STORE) {
+    store_epilogue<TrBF16, C>(p, acc, mt, nt);
+  } else {
+    static_assert(EPI == EPI_GHOST, "DMA kernel: GHOST or STORE");
+    f32x16_t acc2[C::MI][C::NI];
+    zero_acc<TrBF16, C>(acc2);
+    mainloop_dma<C>(p.L2, p.R2, mt, nt, p.K2, l, acc2);
+    float colsum[C::NI];
+    ghost_colsum<C>(p, acc, acc2, colsum);
+    static_assert(C::WM * C::BN * 4 <= SB, "partial scratch");
+    write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
   }
 }
 
@@ -527,6 +762,12 @@ template <class Tr> using StoreCfg = PickCfg<Tr, GS_STORE_TILE>;
 
 namespace {
 
+#ifndef GS_USE_DMA
+#define GS_USE_DMA 1
+#endif
+
+bool dma_ok(const Operand& o) { return o.vec_ok && o.nbytes > 0 && o.nbytes < INT32_MAX; }
+
 template <class Tr, class C>
 struct Launch {
   template <int EPI>
@@ -535,6 +776,15 @@ struct Launch {
     if (blocks <= 0) return GS_OK;
     if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
+    if constexpr (std::is_same<Tr, TrBF16>::value && EPI == EPI_GHOST &&
+                  3 * DmaCfg<C>::STAGE_BYTES <= 160 * 1024) {
+      const bool dma = GS_USE_DMA && aligned && dma_ok(p.L1) && dma_ok(p.R1) &&
+                       (EPI != EPI_GHOST || (dma_ok(p.L2) && dma_ok(p.R2)));
+      if (dma) {
+        hipLaunchKernelGGL((gemm_dma_kernel<C, EPI>), grid, block, 0, s, p);
+        return check_launch("gemm_dma_kernel");
+      }
+    }
     if (aligned) return go(gemm_nt_kernel<Tr, C, true, EPI>, grid, block, p, s);
     return go(gemm_nt_kernel<Tr, C, false, EPI>, grid, block, p, s);
   }
@@ -560,9 +810,10 @@ struct Launch {
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 Operand make_operand(const void* base, int64_t ld, RowMap map, int per_seg, int64_t K,
-                     size_t esz) {
+                     size_t esz, int64_t nbytes) {
   Operand o;
   o.base = base;
+  o.nbytes = nbytes;
   o.ld = ld;
   o.map = map;
   o.per_seg = per_seg;
@@ -673,10 +924,13 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   const int64_t n_t = N - n_val;
   const RowMap tr = train_rows(N, n_val, val_start, T);
   const RowMap va = val_rows(n_val, val_start, T);
+  const int64_t a_bytes = N * T * d_in * static_cast<int64_t>(esz);
+  const int64_t g_bytes = N * T * d_out * static_cast<int64_t>(esz);
 
   if (pl.algo == GS_ALGO_GHOST) {
     const void* La = A;
     const void* Lg = G;
+    int64_t la_bytes = a_bytes, lg_bytes = g_bytes;
     RowMap lmap = va;
     if (semantics == GS_SEM_PRESUM) {
       E* abar = reinterpret_cast<E*>(cv.take<char>(T * d_in * esz));
@@ -690,6 +944,8 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
                          static_cast<const E*>(G), d_out, va, d_out, gbar);
       La = abar;
       Lg = gbar;
+      la_bytes = T * d_in * static_cast<int64_t>(esz);
+      lg_bytes = T * d_out * static_cast<int64_t>(esz);
       lmap = plain_rows(T);
     }
     float* P = cv.take<float>(pl.p_rows * pl.p_ld);
@@ -697,10 +953,10 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     p.p_ld = pl.p_ld;
     p.tile_reduce = pl.tile_reduce;
     p.rounding = rounding;
-    p.L1 = make_operand(La, d_in, lmap, pl.ghost_flat ? 0 : 1, d_in, esz);
-    p.R1 = make_operand(A, d_in, tr, 0, d_in, esz);
-    p.L2 = make_operand(Lg, d_out, lmap, pl.ghost_flat ? 0 : 1, d_out, esz);
-    p.R2 = make_operand(G, d_out, tr, 0, d_out, esz);
+    p.L1 = make_operand(La, d_in, lmap, pl.ghost_flat ? 0 : 1, d_in, esz, la_bytes);
+    p.R1 = make_operand(A, d_in, tr, 0, d_in, esz, a_bytes);
+    p.L2 = make_operand(Lg, d_out, lmap, pl.ghost_flat ? 0 : 1, d_out, esz, lg_bytes);
+    p.R2 = make_operand(G, d_out, tr, 0, d_out, esz, g_bytes);
     p.K1 = d_in;
     p.K2 = d_out;
     p.m_tiles = host_tiles<GC::BM>(p.L1);
@@ -745,8 +1001,10 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   const int64_t kper = pl.vcols / vsteps;
   for (int64_t j = 0; j < vsteps; ++j) {
     GemmParams q{};
-    q.L1 = make_operand(Gt + j * kper, pl.vcols, plain_rows(d_out), 0, kper, esz);
-    q.R1 = make_operand(At + j * kper, pl.vcols, plain_rows(d_in), 0, kper, esz);
+    q.L1 = make_operand(Gt + j * kper, pl.vcols, plain_rows(d_out), 0, kper, esz,
+                        (d_out * pl.vcols - j * kper) * static_cast<int64_t>(esz));
+    q.R1 = make_operand(At + j * kper, pl.vcols, plain_rows(d_in), 0, kper, esz,
+                        (d_in * pl.vcols - j * kper) * static_cast<int64_t>(esz));
     q.K1 = kper;
     q.m_tiles = host_tiles<SC::BM>(q.L1);
     q.n_tiles = host_tiles<SC::BN>(q.R1);
@@ -758,8 +1016,8 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     if (rc) return rc;
 
     GemmParams r{};
-    r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, esz);
-    r.R1 = make_operand(A, d_in, tr, 0, d_in, esz);
+    r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, esz, d_out * d_in * esz);
+    r.R1 = make_operand(A, d_in, tr, 0, d_in, esz, a_bytes);
     r.K1 = d_in;
     r.m_tiles = n_mt;
     r.n_tiles = host_tiles<RC::BN>(r.R1);

@@ -187,6 +187,115 @@ def gpt2_bench(steps: int, warmup: int, dev):
     }
 
 
+# ------------------------------------------------------------------ GradProj
+def gradproj_bench(steps: int, warmup: int, dev):
+    """GPT-2-medium shape, B=32, T=1024, bf16; Kronecker projection k_i = k_o = 16 on every
+    block Linear (96 layers); per step: forward, backward, collect_batch (fp16), async copy of
+    the projections to pinned host memory.  Ends with the pairwise similarity proj @ proj^T."""
+    from ghostsuite_amd import _native
+    from ghostsuite_amd.gradProjection.gradproj_engine import GradProjLoraEngine
+    from ghostsuite_amd.workloads import CausalLM, GPT2_MEDIUM, synthetic_tokens
+    import tempfile
+    B, T = 32, 1024
+    torch.manual_seed(0)
+    model = CausalLM(GPT2_MEDIUM).to(dev, torch.bfloat16)
+    X, Y = synthetic_tokens(B, T, GPT2_MEDIUM.vocab, seed=77, device=dev)
+    timed = TimedOps(_native.ops())
+    _native._install_backend(timed)
+    tmp = tempfile.mkdtemp()
+    eng = GradProjLoraEngine(model, proj_layers="h.", proj_rank_total=256, proj_rank_min=8,
+                             proj_seed=42, proj_dtype="float16", proj_dir=tmp,
+                             proj_save_interval=10 ** 9, proj_dims_override=(16, 16))
+    eng.attach()
+    host = torch.empty((B, eng.total_proj_dim), dtype=torch.float16, pin_memory=True)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        loss = model(X, Y)
+        loss.backward()
+        proj = eng.collect_batch()
+        host.copy_(proj, non_blocking=True)
+        eng.clear_gradients()
+        return proj
+
+    if True:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        timed.enabled = True
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            proj = step()
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / steps
+        timed.enabled = False
+    sim = (proj.float() @ proj.float().t()).cpu()
+    ops = timed.summary()
+    _native._install_backend(None)
+    eng.detach()
+    kp = ops.get("kron_proj", {"ms": 0.0, "n": 1, "work": 0})
+    avg = kp["ms"] / max(kp["n"], 1)
+    bytes_per_step = kp["work"] * kp["n"] / steps if kp["n"] else 0
+    del model, eng
+    torch.cuda.empty_cache()
+    return {"workload": "GPT-2-medium shape GradProj, B=32, T=1024, k=16x16 on 96 Linear layers",
+            "ms_per_step": t * 1e3, "samples_per_s": B / t,
+            "proj_dim": int(host.shape[1]), "similarity_finite": bool(torch.isfinite(sim).all()),
+            "kron_ms_per_step": kp["ms"] / steps, "kron_calls_per_step": kp["n"] / steps,
+            "kron_avg_us": avg * 1e3,
+            "kron_hbm_GBps": (bytes_per_step / (kp["ms"] / steps * 1e-3) / 1e9) if kp["ms"] else None,
+            "kron_hbm_frac": (bytes_per_step / (kp["ms"] / steps * 1e-3) / PEAK_HBM) if kp["ms"] else None}
+
+
+# ------------------------------------------------------------------ Pythia-1B shape (configs[4])
+def pythia_bench(steps: int, warmup: int, dev):
+    """16 layers, d=2048, MLP 8192, T=2048, rotary, untied embed_out, bf16; 8 train + 2 val."""
+    from ghostsuite_amd import GradDotProdEngine
+    from ghostsuite_amd.workloads import CausalLM, PYTHIA_1B, synthetic_tokens
+    n_train, n_val, T = 8, 2, 2048
+    torch.manual_seed(0)
+    model = CausalLM(PYTHIA_1B).to(dev, torch.bfloat16)
+    plain = CausalLM(PYTHIA_1B).to(dev, torch.bfloat16)
+    plain.load_state_dict(model.state_dict())
+    X, Y = synthetic_tokens(n_train + n_val, T, PYTHIA_1B.vocab, seed=99, device=dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    eng = GradDotProdEngine(model, val_batch_size=n_val, use_dummy_bias=True)
+    eng.attach(opt)
+    popt = torch.optim.AdamW(plain.parameters(), lr=1e-4)
+
+    def ghost_step(i):
+        eng.attach_train_batch(X[:n_train], Y[:n_train], i, 0)
+        model(X, Y).backward()
+        eng.prepare_gradients()
+        opt.step()
+        eng.aggregate_and_log()
+        eng.clear_gradients()
+        opt.zero_grad(set_to_none=True)
+        eng.dot_product_log.clear()
+
+    def plain_step(i):
+        plain(X, Y).backward()
+        popt.step()
+        popt.zero_grad(set_to_none=True)
+
+    out = {}
+    for name, fn in (("ghost", ghost_step), ("plain", plain_step)):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            fn(i)
+        torch.cuda.synchronize()
+        out[name] = (time.perf_counter() - t0) / steps
+    eng.detach()
+    del model, plain, opt, popt, eng
+    torch.cuda.empty_cache()
+    return {"workload": "Pythia-1B shape GradDotProd, 8 train + 2 val, T=2048",
+            "ms_per_step": out["ghost"] * 1e3, "plain_ms_per_step": out["plain"] * 1e3,
+            "samples_per_s": n_train / out["ghost"], "step_overhead": out["ghost"] / out["plain"]}
+
+
 # ------------------------------------------------------------------ ghost kernel microbench
 def ghost_kernel_bench(dev, reps: int = 20, T: int = 1024):
     """A[32,T,768], G[32,T,3072] bf16, first 8 rows val, fused ghost."""
@@ -308,6 +417,8 @@ def kernels_leg(dev, reps: int = 10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--mode", choices=["full", "kernels"], default="full")
+    ap.add_argument("--legs", default="gradproj,pythia",
+                    help="extra legs after the GPT-2 step: gradproj, pythia (comma list or none)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
@@ -326,10 +437,23 @@ def main():
         kernels_leg(dev)
         return
 
-    res = gpt2_bench(args.steps, args.warmup, dev)
+    import contextlib
+    with contextlib.redirect_stdout(sys.stderr):
+        res = gpt2_bench(args.steps, args.warmup, dev)
     log("[bench] GPT-2 step done; ghost kernel microbench")
     gk = ghost_kernel_bench(dev)
     log(f"[bench] ghost kernel T=1024: {gk['ms']:.3f} ms, {gk['tflops']:.1f} TF/s")
+    legs = [l for l in args.legs.split(",") if l and l != "none"]
+    extra = {}
+    import contextlib
+    # The engines print progress like the reference does; keep stdout for the JSON line.
+    with contextlib.redirect_stdout(sys.stderr):
+        if "gradproj" in legs:
+            extra["gradproj"] = gradproj_bench(3, 1, dev)
+            log(f"[bench] gradproj: {extra['gradproj']['ms_per_step']:.1f} ms/step")
+        if "pythia" in legs:
+            extra["pythia"] = pythia_bench(3, 1, dev)
+            log(f"[bench] pythia: {extra['pythia']['ms_per_step']:.1f} ms/step")
 
     ops = res["ops"]
     steps = args.steps
@@ -372,10 +496,14 @@ def main():
                          "ms": gk["ms"], "achieved": gk["tflops"], "unit": "TFLOP/s",
                          "peak": PEAK_BF16 / 1e12, "frac": gk["frac"],
                          "valgrad_same_semantics_ms": gk["valgrad_ms"]},
-        "ops": {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["n"] / steps}
+        "ops": {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["n"] / steps,
+                    "avg_us": v["ms"] / v["n"] * 1e3,
+                    ("TFLOP/s" if v["bound"] == "mfma" else "GB/s"):
+                        v["work"] / (v["ms"] / v["n"] * 1e-3) / (1e12 if v["bound"] == "mfma" else 1e9)}
                 for k, v in sorted(ops.items(), key=lambda kv: -kv[1]["ms"])},
         "algorithms": {k: list(v) for k, v in list(res["algos"].items())[:8]},
         "cpu_baseline": cpu,
+        **extra,
     }
     print(json.dumps(out), flush=True)
 

@@ -172,45 +172,53 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
 
 // ---------------------------------------------------------------- stage 2/3 (shared)
 // S[n][f] = sum_c part[n][c][f]   (grid: feature blocks x samples)
-__global__ void feature_sample_totals_kernel(const float* __restrict__ part, int64_t chunks,
-                                             int64_t F, float* __restrict__ S) {
+__global__ void __launch_bounds__(256) feature_sample_totals_kernel(
+    const float* __restrict__ part, int64_t chunks, int64_t F, float* __restrict__ S) {
   const int64_t f = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t n = blockIdx.y;
   if (f >= F) return;
-  float s = 0.f;
-  for (int64_t c = 0; c < chunks; ++c) s += part[(n * chunks + c) * F + f];
-  S[n * F + f] = s;
-}
-
-// sval[f] = sum over val rows of S; grad[f] = scale * sum over train rows of S.
-template <class GE>
-__global__ void feature_val_totals_kernel(const float* __restrict__ S, int64_t N, int64_t F,
-                                          int64_t n_val, int64_t val_start,
-                                          float* __restrict__ sval, GE* __restrict__ grad,
-                                          float grad_scale) {
-  const int64_t f = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (f >= F) return;
-  float vs = 0.f, ts = 0.f;
-  for (int64_t n = 0; n < N; ++n) {
-    const float s = S[n * F + f];
-    if (n >= val_start && n < val_start + n_val)
-      vs += s;
-    else
-      ts += s;
+  const float* src = part + n * chunks * F + f;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int64_t c = 0;
+  for (; c + 4 <= chunks; c += 4) {
+    s0 += src[c * F];
+    s1 += src[(c + 1) * F];
+    s2 += src[(c + 2) * F];
+    s3 += src[(c + 3) * F];
   }
-  sval[f] = vs;
-  if (grad != nullptr) grad[f] = from_f32<GE>(grad_scale * ts);
+  for (; c < chunks; ++c) s0 += src[c * F];
+  S[n * F + f] = (s0 + s1) + (s2 + s3);
 }
 
-__global__ void feature_dots_kernel(const float* __restrict__ S, const float* __restrict__ sval,
-                                    int64_t F, RowMap train, float* __restrict__ out) {
+// Blocks [0, n_train): dot_i = <S_i, sum over val rows of S>, the val aggregate formed on the
+// fly.  Blocks [n_train, ...): grad[f] = scale * sum over train rows of S[.][f].
+template <class GE>
+__global__ void __launch_bounds__(BW_THREADS) feature_finish_kernel(
+    const float* __restrict__ S, int64_t N, int64_t F, int64_t n_val, int64_t val_start,
+    RowMap train, float* __restrict__ out_dot, GE* __restrict__ grad, float grad_scale) {
   __shared__ float red[BW_THREADS / 64];
-  const int64_t i = blockIdx.x;
-  const float* row = S + train.phys_sample(i) * F;
-  float s = 0.f;
-  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) s += row[f] * sval[f];
-  s = block_sum(s, red);
-  if (threadIdx.x == 0) out[i] = s;
+  const int64_t n_train = N - n_val;
+  const int64_t b = blockIdx.x;
+  if (b < n_train) {
+    if (out_dot == nullptr) return;
+    const float* row = S + train.phys_sample(b) * F;
+    float s = 0.f;
+    for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+      float v = 0.f;
+      for (int64_t j = 0; j < n_val; ++j) v += S[(val_start + j) * F + f];
+      s += row[f] * v;
+    }
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) out_dot[b] = s;
+    return;
+  }
+  if (grad == nullptr) return;
+  const int64_t f = (b - n_train) * blockDim.x + threadIdx.x;
+  if (f >= F) return;
+  float t = 0.f;
+  for (int64_t n = 0; n < N; ++n)
+    if (n < val_start || n >= val_start + n_val) t += S[n * F + f];
+  grad[f] = from_f32<GE>(grad_scale * t);
 }
 
 // ---------------------------------------------------------------- embedding
@@ -355,17 +363,17 @@ template <class GE>
 int finish_feature(const float* part, int64_t N, int64_t chunks, int64_t F, int64_t n_val,
                    int64_t val_start, int64_t T, float* S, float* sval, void* grad,
                    float grad_scale, float* out_dot, hipStream_t s) {
+  (void)sval;
   hipLaunchKernelGGL(feature_sample_totals_kernel,
-                     dim3(static_cast<unsigned>(cdiv(F, 64)), static_cast<unsigned>(N)), dim3(64),
-                     0, s, part, chunks, F, S);
-  hipLaunchKernelGGL(feature_val_totals_kernel<GE>, dim3(static_cast<unsigned>(cdiv(F, 64))),
-                     dim3(64), 0, s, S, N, F, n_val, val_start, sval, static_cast<GE*>(grad),
+                     dim3(static_cast<unsigned>(cdiv(F, 256)), static_cast<unsigned>(N)),
+                     dim3(256), 0, s, part, chunks, F, S);
+  const int64_t n_t = N - n_val;
+  const int64_t blocks = n_t + (grad != nullptr ? cdiv(F, BW_THREADS) : 0);
+  hipLaunchKernelGGL(feature_finish_kernel<GE>, dim3(static_cast<unsigned>(blocks)),
+                     dim3(BW_THREADS), 0, s, S, N, F, n_val, val_start,
+                     train_rows(N, n_val, val_start, T), out_dot, static_cast<GE*>(grad),
                      grad_scale);
-  if (out_dot != nullptr)
-    hipLaunchKernelGGL(feature_dots_kernel, dim3(static_cast<unsigned>(N - n_val)),
-                       dim3(BW_THREADS), 0, s, S, sval, F, train_rows(N, n_val, val_start, T),
-                       out_dot);
-  return check_launch("feature_totals/dots");
+  return check_launch("feature_totals/finish");
 }
 
 int finish_feature_any(int grad_dtype, const float* part, int64_t N, int64_t chunks, int64_t F,

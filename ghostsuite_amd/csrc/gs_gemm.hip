@@ -750,7 +750,7 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 #define GS_ROWDOT_TILE 2, 2, 2, 2
 #endif
 #ifndef GS_STORE_TILE
-#define GS_STORE_TILE 2, 2, 2, 2
+#define GS_STORE_TILE 2, 2, 1, 1
 #endif
 // fp32 operands (precision checks, fp32 models) keep the small 128 x 128 tile.
 template <class Tr, int... Tile>

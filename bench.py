@@ -374,44 +374,85 @@ def cpu_baseline(budget_s: float = 20.0):
                        f"blocks; model fwd/bwd not included")}
 
 
+KERNEL_SHAPES = {
+    # name: shape at which the kernel leg runs it (the GPT-2-small / GPT-2-medium bench shapes)
+    "ghost_microbench": "linear_dot GHOST, A[32,1024,768] G[32,1024,3072] bf16, 8 val first",
+    "valgrad_fc": "linear_dot VALGRAD pairwise, A[20,1024,768] G[20,1024,3072] bf16, 4 val",
+    "bias_fc": "bias_dot, G[20,1024,3072] bf16, 4 val",
+    "layernorm": "layernorm_dot + grads, X,G[20,1024,768] bf16, 4 val",
+    "embedding_wte": "embedding_dot, ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
+    "kron_fc": "kron_proj, A[32,1024,1024] G[32,1024,4096] bf16, k=16x16",
+    "copy_1GiB": "device copy of 1 GiB (HBM calibration)",
+}
+
+
 def kernels_leg(dev, reps: int = 10):
-    """Kernel-level leg for counter runs: the fused ghost kernel at the microbench shape, the
-    val-gradient path at the GPT-2-small fc_out shape, and a 1 GiB device copy (the HBM
-    calibration for FETCH_SIZE / WRITE_SIZE)."""
+    """Kernel-level leg for counter runs: every hot-path entry point once per rep at its bench
+    shape (KERNEL_SHAPES), plus a 1 GiB device copy (the calibration for FETCH_SIZE and
+    WRITE_SIZE).  Prints one JSON line of average milliseconds per call."""
     from ghostsuite_amd import _native
-    out = {}
-    gk = ghost_kernel_bench(dev, reps=reps)
-    out["ghost_T1024"] = gk
-    g = torch.Generator().manual_seed(7)
-    N, n_val, T, d_in, d_out = 20, 4, 1024, 3072, 768
-    A = torch.randn(N, T, d_in, generator=g).to(dev, torch.bfloat16)
-    G = (torch.randn(N, T, d_out, generator=g) * 1e-3).to(dev, torch.bfloat16)
     ops = _native.ops()
-    for _ in range(2):
-        ops.linear_dot(A, G, n_val, algo=_native.ALGO_VALGRAD)
-    torch.cuda.synchronize()
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
-        ops.linear_dot(A, G, n_val, algo=_native.ALGO_VALGRAD)
-    e.record()
-    torch.cuda.synchronize()
-    out["valgrad_fc_out_ms"] = s.elapsed_time(e) / reps
+    g = torch.Generator().manual_seed(7)
+
+    def rnd(*shape, s=1.0):
+        return (torch.randn(*shape, generator=g) * s).to(dev, torch.bfloat16)
+
+    def timeit(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    out = {}
+    A = rnd(32, 1024, 768)
+    G = rnd(32, 1024, 3072, s=1e-3)
+    out["ghost_microbench"] = timeit(lambda: ops.linear_dot(A, G, 8, val_start=0,
+                                                           algo=_native.ALGO_GHOST))
+    A2, G2 = A[:20].contiguous(), G[:20].contiguous()
+    out["valgrad_fc"] = timeit(lambda: ops.linear_dot(A2, G2, 4, algo=_native.ALGO_VALGRAD))
+    out["bias_fc"] = timeit(lambda: ops.bias_dot(G2, 4, grad_scale=1.25))
+    X = rnd(20, 1024, 768)
+    GL = rnd(20, 1024, 768, s=1e-3)
+    out["layernorm"] = timeit(lambda: ops.layernorm_dot(X, GL, 4, 1e-5, grad_scale=1.25))
+    ids = torch.randint(0, 50257, (20, 1024), generator=g).to(dev)
+    out["embedding_wte"] = timeit(lambda: ops.embedding_dot(ids, GL, 4, 50257))
+    del A, G, A2, G2, X, GL
+    Ak = rnd(32, 1024, 1024)
+    Gk = rnd(32, 1024, 4096, s=1e-3)
+    Pi = rnd(16, 1024, s=0.25)
+    Po = rnd(16, 4096, s=0.25)
+    out["kron_fc"] = timeit(lambda: ops.kron_proj(Ak, Gk, Pi, Po, 32.0))
+    del Ak, Gk
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    s.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / reps
-    out["copy_1GiB_ms"] = ms
-    out["copy_GBps"] = 2 * (1 << 30) / (ms * 1e-3) / 1e9
+    out["copy_1GiB"] = timeit(lambda: dst.copy_(src))
+    out["copy_GBps"] = 2 * (1 << 30) / (out["copy_1GiB"] * 1e-3) / 1e9
     print(json.dumps(out), flush=True)
+
+
+# bench op name -> kernel-leg entry at the same shape (profiles/traffic.json, from the
+# FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --mode kernels`)
+TRAFFIC_KEYS = {"linear_valgrad[768x3072]": "valgrad_fc", "bias_dot": "bias_fc",
+                "layernorm_dot": "layernorm", "embedding_dot": "embedding_wte",
+                "kron_proj": "kron_fc", "ghost": "ghost_microbench"}
+
+
+def measured_traffic(op_name):
+    """HBM bytes per launch measured by the counter runs for this op's shape, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    key = TRAFFIC_KEYS.get(op_name)
+    if key is None or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get(key)
+    return None if entry is None else entry.get("traffic_bytes")
 
 
 def main():
@@ -463,11 +504,13 @@ def main():
     if dom["bound"] == "mfma":
         roof = {"bound": "mfma", "kernel": dom_name, "achieved": achieved / 1e12,
                 "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16,
-                "traffic": None, "avg_ms": avg_ms, "launches_per_step": dom["n"] / steps}
+                "traffic": measured_traffic(dom_name), "avg_ms": avg_ms,
+                "launches_per_step": dom["n"] / steps}
     else:
         roof = {"bound": "hbm", "kernel": dom_name, "achieved": achieved / 1e9,
                 "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved / PEAK_HBM,
-                "traffic": None, "avg_ms": avg_ms, "launches_per_step": dom["n"] / steps}
+                "traffic": measured_traffic(dom_name), "avg_ms": avg_ms,
+                "launches_per_step": dom["n"] / steps}
     hot_ms = sum(v["ms"] for v in ops.values()) / steps
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
     value = res["n_train"] / res["t_ghost"]
@@ -495,6 +538,7 @@ def main():
         "ghost_kernel": {"shape": "A[32,1024,768] G[32,1024,3072] bf16, 8 val rows first",
                          "ms": gk["ms"], "achieved": gk["tflops"], "unit": "TFLOP/s",
                          "peak": PEAK_BF16 / 1e12, "frac": gk["frac"],
+                         "traffic": measured_traffic("ghost"),
                          "valgrad_same_semantics_ms": gk["valgrad_ms"]},
         "ops": {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["n"] / steps,
                     "avg_us": v["ms"] / v["n"] * 1e3,

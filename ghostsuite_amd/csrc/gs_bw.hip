@@ -225,19 +225,26 @@ __global__ void __launch_bounds__(BW_THREADS) feature_finish_kernel(
 // Val tokens with the same id form one segment represented by its first val token index
 // (table[id] = min index, an order-independent integer atomicMin).  Segment sums are
 // accumulated in 64-bit fixed point with integer atomics (order-independent, hence
-// deterministic), then converted to fp32 rows; each train token finds its segment through
-// table[id] and takes a dot with that row.
-__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    p[i] = v;
+// deterministic) under one power-of-two scale taken from max |g| over the val rows; each
+// train token finds its segment through table[id] and takes a dot with that row.
+constexpr int EMB_SLOTS = 256;  // max |g| is gathered in 256 slots to avoid one hot atomic
+
+// table[0, vocab) = INT32_MAX, slots = 0, fixed-point rows = 0.
+__global__ void emb_prep_kernel(int32_t* __restrict__ table, int64_t vocab,
+                                unsigned* __restrict__ slots, unsigned long long* __restrict__ fix,
+                                int64_t nfix) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = i0; i < vocab; i += stride) table[i] = INT32_MAX;
+  for (int64_t i = i0; i < EMB_SLOTS; i += stride) slots[i] = 0u;
+  for (int64_t i = i0; i < nfix; i += stride) fix[i] = 0ull;
 }
 
-// table[id] = min val token index; maxbits = max |g| bits over val rows.
+// table[id] = min val token index; slots[q % EMB_SLOTS] = max |g| bits of val token q's row.
 template <class E>
 __global__ void emb_index_kernel(const int64_t* __restrict__ ids, const E* __restrict__ G,
                                  RowMap val, int64_t d, int64_t vocab, int32_t* __restrict__ table,
-                                 unsigned* __restrict__ maxbits) {
+                                 unsigned* __restrict__ slots) {
   const int64_t q = blockIdx.x;  // val token index
   const int64_t seg = q / val.seglen;
   const int64_t row = val.phys_row(seg, q - seg * val.seglen);
@@ -246,22 +253,30 @@ __global__ void emb_index_kernel(const int64_t* __restrict__ ids, const E* __res
   float m = 0.f;
   for (int64_t f = threadIdx.x; f < d; f += blockDim.x) m = fmaxf(m, fabsf(ld(G + row * d + f)));
   __shared__ float red[BW_THREADS / 64];
-  // block max
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   if (threadIdx.x == 0) {
     float b = 0.f;
     for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) b = fmaxf(b, red[w]);
-    atomicMax(maxbits, __float_as_uint(b));  // non-negative floats order like their bits
+    atomicMax(slots + (q % EMB_SLOTS), __float_as_uint(b));  // non-negative: bits order
   }
 }
 
-// Power-of-two scale so that n_vt * max|g| * scale < 2^62.
-__device__ __forceinline__ double emb_scale(unsigned maxbits, int64_t n_vt) {
-  const float mx = __uint_as_float(maxbits);
+// Power-of-two scale so that n_vt * max|g| * scale < 2^61 (block-wide; all threads get it).
+__device__ __forceinline__ double emb_scale(const unsigned* __restrict__ slots, int64_t n_vt) {
+  __shared__ float red[BW_THREADS / 64];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < EMB_SLOTS; i += blockDim.x) m = fmaxf(m, __uint_as_float(slots[i]));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float mx = 0.f;
+  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) mx = fmaxf(mx, red[w]);
+  __syncthreads();
   if (!(mx > 0.f) || !isfinite(mx)) return 1.0;
-  const int e = 62 - static_cast<int>(ceil(log2(static_cast<double>(mx) * static_cast<double>(n_vt)))) - 1;
+  const int e =
+      62 - static_cast<int>(ceil(log2(static_cast<double>(mx) * static_cast<double>(n_vt)))) - 1;
   return ldexp(1.0, e);
 }
 
@@ -269,69 +284,51 @@ template <class E>
 __global__ void emb_accum_kernel(const int64_t* __restrict__ ids, const E* __restrict__ G,
                                  RowMap val, int64_t d, int64_t vocab,
                                  const int32_t* __restrict__ table,
-                                 const unsigned* __restrict__ maxbits,
+                                 const unsigned* __restrict__ slots,
                                  unsigned long long* __restrict__ fix) {
   const int64_t q = blockIdx.x;
+  const double scale = emb_scale(slots, val.total());
   const int64_t seg = q / val.seglen;
   const int64_t row = val.phys_row(seg, q - seg * val.seglen);
   const int64_t id = ids[row];
   if (id < 0 || id >= vocab) return;
   const int64_t rep = table[id];
-  const double scale = emb_scale(*maxbits, val.total());
   for (int64_t f = threadIdx.x; f < d; f += blockDim.x) {
     const long long v = llrint(static_cast<double>(ld(G + row * d + f)) * scale);
     atomicAdd(fix + rep * d + f, static_cast<unsigned long long>(v));
   }
 }
 
-__global__ void emb_zero_kernel(const int64_t* __restrict__ ids, RowMap val, int64_t d,
-                                int64_t vocab, const int32_t* __restrict__ table,
-                                unsigned long long* __restrict__ fix) {
-  const int64_t q = blockIdx.x;
-  const int64_t seg = q / val.seglen;
-  const int64_t id = ids[val.phys_row(seg, q - seg * val.seglen)];
-  if (id < 0 || id >= vocab || table[id] != q) return;
-  for (int64_t f = threadIdx.x; f < d; f += blockDim.x) fix[q * d + f] = 0ull;
-}
-
-__global__ void emb_finish_kernel(const int64_t* __restrict__ ids, RowMap val, int64_t d,
-                                  int64_t vocab, const int32_t* __restrict__ table,
-                                  const unsigned* __restrict__ maxbits,
-                                  const unsigned long long* __restrict__ fix,
-                                  float* __restrict__ vrow) {
-  const int64_t q = blockIdx.x;
-  const int64_t seg = q / val.seglen;
-  const int64_t id = ids[val.phys_row(seg, q - seg * val.seglen)];
-  if (id < 0 || id >= vocab || table[id] != q) return;
-  const double inv = 1.0 / emb_scale(*maxbits, val.total());
-  for (int64_t f = threadIdx.x; f < d; f += blockDim.x)
-    vrow[q * d + f] = static_cast<float>(static_cast<double>(static_cast<long long>(fix[q * d + f])) * inv);
-}
-
-// part[i * chunks + c] = sum over train row i's tokens in chunk c of <g_it, V[x_it]>.
+// part[i * chunks + c] = sum over train row i's tokens in chunk c of <g_it, V[x_it]>, with V
+// read from the fixed-point rows.
 template <class E>
 __global__ void emb_dot_kernel(const int64_t* __restrict__ ids, const E* __restrict__ G,
-                               RowMap train, int64_t d, int64_t vocab,
-                               const int32_t* __restrict__ table, const float* __restrict__ vrow,
-                               int64_t chunks, float* __restrict__ part) {
+                               RowMap train, int64_t d, int64_t vocab, int64_t n_vt,
+                               const int32_t* __restrict__ table,
+                               const unsigned* __restrict__ slots,
+                               const unsigned long long* __restrict__ fix, int64_t chunks,
+                               float* __restrict__ part) {
   __shared__ float red[BW_THREADS / 64];
+  const double inv = 1.0 / emb_scale(slots, n_vt);
   const int64_t i = blockIdx.y, c = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t T = train.seglen;
   const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
-  float s = 0.f;
+  double s = 0.0;
   for (int64_t t = t0 + wid; t < t1; t += 4) {
     const int64_t row = train.phys_row(i, t);
     const int64_t id = ids[row];
     if (id < 0 || id >= vocab) continue;
     const int32_t rep = table[id];
     if (rep == INT32_MAX) continue;
-    const float* vr = vrow + static_cast<int64_t>(rep) * d;
+    const unsigned long long* vr = fix + static_cast<int64_t>(rep) * d;
     const E* gr = G + row * d;
-    for (int64_t f = lane; f < d; f += 64) s += ld(gr + f) * vr[f];
+    for (int64_t f = lane; f < d; f += 64)
+      s += static_cast<double>(ld(gr + f)) * static_cast<double>(static_cast<long long>(vr[f]));
   }
-  s = block_sum(s, red);
-  if (threadIdx.x == 0) part[i * chunks + c] = s;
+  const float sf = static_cast<float>(s * inv);
+  const float tot = block_sum(sf, red);
+  if (threadIdx.x == 0) part[i * chunks + c] = tot;
 }
 
 __global__ void sum_chunks_kernel(const float* __restrict__ part, int64_t chunks,
@@ -521,9 +518,8 @@ template <class S>
 void carve_embedding(S& c, int64_t N, int64_t n_val, int64_t T, int64_t d, int64_t vocab) {
   const int64_t n_vt = n_val * T, n_t = N - n_val, chunks = cdiv(T, TOK_CHUNK);
   c.template take<int32_t>(vocab);
-  c.template take<unsigned>(4);
+  c.template take<unsigned>(EMB_SLOTS);
   c.template take<unsigned long long>(n_vt * d);
-  c.template take<float>(n_vt * d);
   c.template take<float>(n_t * chunks);
 }
 }  // namespace
@@ -554,41 +550,35 @@ extern "C" int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, in
   Carver cv(workspace, workspace_bytes);
   const int64_t n_vt = n_val * T, n_t = N - n_val, chunks = cdiv(T, TOK_CHUNK);
   int32_t* table = cv.take<int32_t>(vocab);
-  unsigned* maxbits = cv.take<unsigned>(4);
+  unsigned* slots = cv.take<unsigned>(EMB_SLOTS);
   unsigned long long* fix = cv.take<unsigned long long>(n_vt * d);
-  float* vrow = cv.take<float>(n_vt * d);
   float* part = cv.take<float>(n_t * chunks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const RowMap va = val_rows(n_val, val_start, T);
   const RowMap tr = train_rows(N, n_val, val_start, T);
-
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(vocab, 256), 4096))),
-                     dim3(256), 0, s, table, vocab, INT32_MAX);
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<int32_t*>(maxbits),
-                     int64_t{1}, 0);
+  const int64_t prep_n = std::max<int64_t>(vocab, n_vt * d);
+  hipLaunchKernelGGL(emb_prep_kernel,
+                     dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(prep_n, 256), 8192))),
+                     dim3(256), 0, s, table, vocab, slots, fix, n_vt * d);
   const dim3 gv(static_cast<unsigned>(n_vt));
-  if (dtype == GS_DTYPE_BF16)
-    hipLaunchKernelGGL(emb_index_kernel<uint16_t>, gv, dim3(BW_THREADS), 0, s, ids,
-                       static_cast<const uint16_t*>(G), va, d, vocab, table, maxbits);
-  else
-    hipLaunchKernelGGL(emb_index_kernel<float>, gv, dim3(BW_THREADS), 0, s, ids,
-                       static_cast<const float*>(G), va, d, vocab, table, maxbits);
-  hipLaunchKernelGGL(emb_zero_kernel, gv, dim3(BW_THREADS), 0, s, ids, va, d, vocab, table, fix);
-  if (dtype == GS_DTYPE_BF16)
-    hipLaunchKernelGGL(emb_accum_kernel<uint16_t>, gv, dim3(BW_THREADS), 0, s, ids,
-                       static_cast<const uint16_t*>(G), va, d, vocab, table, maxbits, fix);
-  else
-    hipLaunchKernelGGL(emb_accum_kernel<float>, gv, dim3(BW_THREADS), 0, s, ids,
-                       static_cast<const float*>(G), va, d, vocab, table, maxbits, fix);
-  hipLaunchKernelGGL(emb_finish_kernel, gv, dim3(BW_THREADS), 0, s, ids, va, d, vocab, table,
-                     maxbits, fix, vrow);
   const dim3 gt(static_cast<unsigned>(chunks), static_cast<unsigned>(n_t));
-  if (dtype == GS_DTYPE_BF16)
-    hipLaunchKernelGGL(emb_dot_kernel<uint16_t>, gt, dim3(BW_THREADS), 0, s, ids,
-                       static_cast<const uint16_t*>(G), tr, d, vocab, table, vrow, chunks, part);
-  else
-    hipLaunchKernelGGL(emb_dot_kernel<float>, gt, dim3(BW_THREADS), 0, s, ids,
-                       static_cast<const float*>(G), tr, d, vocab, table, vrow, chunks, part);
+  if (dtype == GS_DTYPE_BF16) {
+    const uint16_t* g = static_cast<const uint16_t*>(G);
+    hipLaunchKernelGGL(emb_index_kernel<uint16_t>, gv, dim3(BW_THREADS), 0, s, ids, g, va, d,
+                       vocab, table, slots);
+    hipLaunchKernelGGL(emb_accum_kernel<uint16_t>, gv, dim3(BW_THREADS), 0, s, ids, g, va, d,
+                       vocab, table, slots, fix);
+    hipLaunchKernelGGL(emb_dot_kernel<uint16_t>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, d,
+                       vocab, n_vt, table, slots, fix, chunks, part);
+  } else {
+    const float* g = static_cast<const float*>(G);
+    hipLaunchKernelGGL(emb_index_kernel<float>, gv, dim3(BW_THREADS), 0, s, ids, g, va, d, vocab,
+                       table, slots);
+    hipLaunchKernelGGL(emb_accum_kernel<float>, gv, dim3(BW_THREADS), 0, s, ids, g, va, d, vocab,
+                       table, slots, fix);
+    hipLaunchKernelGGL(emb_dot_kernel<float>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, d, vocab,
+                       n_vt, table, slots, fix, chunks, part);
+  }
   hipLaunchKernelGGL(sum_chunks_kernel, dim3(static_cast<unsigned>(n_t)), dim3(BW_THREADS), 0, s,
                      part, chunks, out_dot);
   return check_launch("embedding kernels");

@@ -61,6 +61,8 @@ _SIGNATURES = {
     "gs_kron_proj_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
     "gs_kron_proj": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I, _F,
                           _P, _I, _P, _SZ, _P]),
+    "gs_kron_embed_proj": (_I, [_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _F,
+                                _P, _I, _P, _SZ, _P]),
 }
 
 
@@ -291,6 +293,35 @@ class HipOps:
                               float(scale), out.data_ptr(), _TORCH_TO_GS[out_dtype],
                               ws.data_ptr(), ws_bytes, _stream(dev))
         _check(rc, "gs_kron_proj")
+        return out
+
+    def kron_embed_proj(self, ids: torch.Tensor, G: torch.Tensor, P_iT: torch.Tensor,
+                        P_o: torch.Tensor, scale: float = 1.0, *,
+                        out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """out[b] = scale * sum_t (P_o g_bt)(P_iT[ids_bt])^T, [B, k_o, k_i]."""
+        dev = _require_device(ids, G, P_iT, P_o)
+        B = ids.shape[0]
+        ids = ids.reshape(B, -1).long().contiguous()
+        T = ids.shape[1]
+        n_g = G.shape[-1]
+        if G.numel() != B * T * n_g:
+            raise GhostHipError(f"ids {tuple(ids.shape)} and G {tuple(G.shape)} disagree")
+        G = G.contiguous()
+        P_iT = P_iT.to(G.dtype).contiguous()
+        P_o = P_o.to(G.dtype).contiguous()
+        vocab, k_i = P_iT.shape
+        k_o = P_o.shape[0]
+        if P_o.shape[1] != n_g:
+            raise GhostHipError("P_o width does not match the embedding dimension")
+        lib = load_library()
+        ws_bytes = lib.gs_kron_proj_workspace(B, T, k_i, k_o)
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty((B, k_o, k_i), dtype=out_dtype, device=dev)
+        rc = lib.gs_kron_embed_proj(ids.data_ptr(), G.data_ptr(), _gs_dtype(G), B, T, n_g,
+                                    P_iT.data_ptr(), P_o.data_ptr(), _gs_dtype(P_iT), vocab, k_i,
+                                    k_o, float(scale), out.data_ptr(), _TORCH_TO_GS[out_dtype],
+                                    ws.data_ptr(), ws_bytes, _stream(dev))
+        _check(rc, "gs_kron_embed_proj")
         return out
 
 

@@ -99,12 +99,15 @@ __device__ __forceinline__ void project_rows(const typename Tr::E* row, const ty
   }
 }
 
-template <class Tr>
+// GATHER: the input side is an embedding, whose "projected input" for token id x is column
+// x of P_i, i.e. row x of R = P_i^T ([vocab, kR]); `ids` replaces A.
+template <class Tr, bool GATHER>
 __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
-    const typename Tr::E* __restrict__ A, const typename Tr::E* __restrict__ G, int64_t T,
-    int64_t n_a, int64_t n_g, const typename Tr::E* __restrict__ R,
-    const typename Tr::E* __restrict__ L, int64_t kR, int64_t kL, int vec_a, int vec_g,
-    int vec_r, int vec_l, int64_t chunks, float* __restrict__ part) {
+    const typename Tr::E* __restrict__ A, const int64_t* __restrict__ ids, int64_t vocab,
+    const typename Tr::E* __restrict__ G, int64_t T, int64_t n_a, int64_t n_g,
+    const typename Tr::E* __restrict__ R, const typename Tr::E* __restrict__ L, int64_t kR,
+    int64_t kL, int vec_a, int vec_g, int vec_r, int vec_l, int64_t chunks,
+    float* __restrict__ part) {
   using E = typename Tr::E;
   __shared__ float sg[PJ_TOK][PJ_KMAX + 1];
   __shared__ float sa[PJ_TOK][PJ_KMAX + 1];
@@ -113,8 +116,7 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
   const int64_t t = c * PJ_TOK + wid * 16 + (lane & 15);  // this lane's operand row
   const bool valid = t < T;
   const E* grow = valid ? G + (b * T + t) * n_g : nullptr;
-  const E* arow = valid ? A + (b * T + t) * n_a : nullptr;
-  const int nbl = kL > 16 ? 2 : 1, nbr = kR > 16 ? 2 : 1;
+  const int nbl = kL > 16 ? 2 : 1;
 
   f32x4_t accg[2], acca[2];
 #pragma unroll
@@ -122,7 +124,10 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
 #pragma unroll
     for (int e = 0; e < 4; ++e) accg[i][e] = acca[i][e] = 0.f;
   project_rows<Tr>(grow, L, n_g, kL, vec_g, vec_l, accg, nbl);
-  project_rows<Tr>(arow, R, n_a, kR, vec_a, vec_r, acca, nbr);
+  if constexpr (!GATHER) {
+    const E* arow = valid ? A + (b * T + t) * n_a : nullptr;
+    project_rows<Tr>(arow, R, n_a, kR, vec_a, vec_r, acca, kR > 16 ? 2 : 1);
+  }
 
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
@@ -131,8 +136,20 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
       const int tok = wid * 16 + 4 * (lane >> 4) + e;
       const int k = nb * 16 + (lane & 15);
       sg[tok][k] = accg[nb][e];
-      sa[tok][k] = acca[nb][e];
+      if constexpr (!GATHER) sa[tok][k] = acca[nb][e];
     }
+  if constexpr (GATHER) {
+    for (int x = threadIdx.x; x < PJ_TOK * PJ_KMAX; x += PJ_THREADS) {
+      const int tok = x / PJ_KMAX, q = x % PJ_KMAX;
+      const int64_t tt = c * PJ_TOK + tok;
+      float v = 0.f;
+      if (tt < T && q < kR) {
+        const int64_t id = ids[b * T + tt];
+        if (id >= 0 && id < vocab) v = to_f32<E>(R[id * kR + q]);
+      }
+      sa[tok][q] = v;
+    }
+  }
   __syncthreads();
   const int64_t nvalid = std::min<int64_t>(PJ_TOK, T - c * PJ_TOK);
   const int64_t nout = kL * kR;
@@ -165,6 +182,22 @@ __global__ void kron_reduce_kernel(const float* __restrict__ part, int64_t chunk
 namespace {
 int64_t pj_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Fixed-order per-sample sum of the chunk partials, scaled and converted to the output type.
+int kron_finish(const float* part, int64_t B, int64_t chunks, int64_t nout, float scale,
+                void* out, int out_dtype, hipStream_t s) {
+  const dim3 rg(static_cast<unsigned>(pj_cdiv(nout, 256)), static_cast<unsigned>(B));
+  if (out_dtype == GS_DTYPE_F32)
+    hipLaunchKernelGGL(kron_reduce_kernel<float>, rg, dim3(256), 0, s, part, chunks, nout, scale,
+                       static_cast<float*>(out));
+  else if (out_dtype == GS_DTYPE_F16)
+    hipLaunchKernelGGL(kron_reduce_kernel<__half>, rg, dim3(256), 0, s, part, chunks, nout, scale,
+                       static_cast<__half*>(out));
+  else
+    hipLaunchKernelGGL(kron_reduce_kernel<uint16_t>, rg, dim3(256), 0, s, part, chunks, nout,
+                       scale, static_cast<uint16_t*>(out));
+  return check_launch("kron_reduce_kernel");
+}
 }  // namespace
 
 }  // namespace gs
@@ -215,27 +248,60 @@ extern "C" int gs_kron_proj(const void* A, const void* G, int dtype, int64_t B, 
   const int vl = al16(L) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
   if (dtype == GS_DTYPE_BF16)
-    hipLaunchKernelGGL(kron_proj_kernel<PjBF16>, grid, dim3(PJ_THREADS), 0, s,
-                       static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(G), T, n_a,
-                       n_g, static_cast<const uint16_t*>(R), static_cast<const uint16_t*>(L), kR,
-                       kL, va, vg, vr, vl, chunks, part);
+    hipLaunchKernelGGL((kron_proj_kernel<PjBF16, false>), grid, dim3(PJ_THREADS), 0, s,
+                       static_cast<const uint16_t*>(A), nullptr, int64_t{0},
+                       static_cast<const uint16_t*>(G), T, n_a, n_g,
+                       static_cast<const uint16_t*>(R), static_cast<const uint16_t*>(L), kR, kL,
+                       va, vg, vr, vl, chunks, part);
   else
-    hipLaunchKernelGGL(kron_proj_kernel<PjF32>, grid, dim3(PJ_THREADS), 0, s,
-                       static_cast<const float*>(A), static_cast<const float*>(G), T, n_a, n_g,
-                       static_cast<const float*>(R), static_cast<const float*>(L), kR, kL, va, vg,
-                       vr, vl, chunks, part);
+    hipLaunchKernelGGL((kron_proj_kernel<PjF32, false>), grid, dim3(PJ_THREADS), 0, s,
+                       static_cast<const float*>(A), nullptr, int64_t{0},
+                       static_cast<const float*>(G), T, n_a, n_g, static_cast<const float*>(R),
+                       static_cast<const float*>(L), kR, kL, va, vg, vr, vl, chunks, part);
   int rc = check_launch("kron_proj_kernel");
   if (rc) return rc;
-  const int64_t nout = kL * kR;
-  const dim3 rg(static_cast<unsigned>(pj_cdiv(nout, 256)), static_cast<unsigned>(B));
-  if (out_dtype == GS_DTYPE_F32)
-    hipLaunchKernelGGL(kron_reduce_kernel<float>, rg, dim3(256), 0, s, part, chunks, nout, scale,
-                       static_cast<float*>(out));
-  else if (out_dtype == GS_DTYPE_F16)
-    hipLaunchKernelGGL(kron_reduce_kernel<__half>, rg, dim3(256), 0, s, part, chunks, nout, scale,
-                       static_cast<__half*>(out));
+  return kron_finish(part, B, chunks, kL * kR, scale, out, out_dtype, s);
+}
+
+extern "C" int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, int64_t B,
+                                  int64_t T, int64_t n_g, const void* P_iT, const void* P_o,
+                                  int p_dtype, int64_t vocab, int64_t k_i, int64_t k_o,
+                                  float scale, void* out, int out_dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_kron_embed_proj: dtype must be bf16 or fp32");
+  if (p_dtype != dtype)
+    return fail(GS_ERR_DTYPE, "gs_kron_embed_proj: projection dtype must equal the grad dtype");
+  if (out_dtype != GS_DTYPE_F32 && out_dtype != GS_DTYPE_BF16 && out_dtype != GS_DTYPE_F16)
+    return fail(GS_ERR_DTYPE, "gs_kron_embed_proj: out_dtype must be fp32, bf16 or fp16");
+  if (B <= 0 || T <= 0 || n_g <= 0 || vocab <= 0 || k_i <= 0 || k_o <= 0 || ids == nullptr ||
+      G == nullptr || P_iT == nullptr || P_o == nullptr || out == nullptr)
+    return fail(GS_ERR_INVALID, "gs_kron_embed_proj: invalid arguments");
+  if (k_i > PJ_KMAX || k_o > PJ_KMAX)
+    return fail(GS_ERR_UNSUPPORTED, "gs_kron_embed_proj: k_i and k_o must be <= 32");
+  const int64_t chunks = pj_cdiv(T, PJ_TOK);
+  if (workspace == nullptr || workspace_bytes < gs_kron_proj_workspace(B, T, k_i, k_o) - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_kron_embed_proj: workspace too small");
+  if (chunks > 65535 || B > 65535)
+    return fail(GS_ERR_UNSUPPORTED, "gs_kron_embed_proj: grid too large");
+  Carver cv(workspace, workspace_bytes);
+  float* part = cv.take<float>(B * chunks * k_o * k_i);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t esz = elem_size(dtype);
+  const int vg = al16(G) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
+  const int vl = al16(P_o) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
+  if (dtype == GS_DTYPE_BF16)
+    hipLaunchKernelGGL((kron_proj_kernel<PjBF16, true>), grid, dim3(PJ_THREADS), 0, s, nullptr,
+                       ids, vocab, static_cast<const uint16_t*>(G), T, int64_t{0}, n_g,
+                       static_cast<const uint16_t*>(P_iT), static_cast<const uint16_t*>(P_o), k_i,
+                       k_o, 0, vg, 0, vl, chunks, part);
   else
-    hipLaunchKernelGGL(kron_reduce_kernel<uint16_t>, rg, dim3(256), 0, s, part, chunks, nout,
-                       scale, static_cast<uint16_t*>(out));
-  return check_launch("kron_reduce_kernel");
+    hipLaunchKernelGGL((kron_proj_kernel<PjF32, true>), grid, dim3(PJ_THREADS), 0, s, nullptr,
+                       ids, vocab, static_cast<const float*>(G), T, int64_t{0}, n_g,
+                       static_cast<const float*>(P_iT), static_cast<const float*>(P_o), k_i, k_o,
+                       0, vg, 0, vl, chunks, part);
+  int rc = check_launch("kron_proj_kernel(gather)");
+  if (rc) return rc;
+  return kron_finish(part, B, chunks, k_o * k_i, scale, out, out_dtype, s);
 }

@@ -89,15 +89,20 @@ class GradProjHooks:
     def _compute_embedding_proj(self, module: nn.Module, indices: torch.Tensor,
                                 grad_output: torch.Tensor) -> None:
         """Projected per-sample gradients of an embedding (reference :167-222):
-        sum_t (P_o g_t)(P_i[:, x_t])^T, vectorised over tokens on the device (no per-token
-        host synchronisation)."""
+        sum_t (P_o g_t)(P_i[:, x_t])^T with no batch-size factor, as in the reference.  The
+        gfx950 kernel gathers P_i's columns by token id on the device (the reference reads
+        every id back to the host)."""
         bs = indices.shape[0]
-        ids = indices.reshape(bs, -1).long()
-        g = grad_output.reshape(bs, ids.shape[1], grad_output.shape[-1]).float()
-        P_i, P_o = self._proj(torch.float32)
-        g_proj = torch.matmul(g, P_o.t())                    # [B, T, k_o]
-        i_proj = P_i.t()[ids]                                # [B, T, k_i]
-        module._ghost_grad_proj = torch.einsum('bto,bti->boi', g_proj, i_proj).float()
+        g = grad_output.reshape(bs, -1, grad_output.shape[-1])
+        dt = g.dtype if g.dtype in (torch.bfloat16, torch.float32) else torch.float32
+        if g.dtype != dt:
+            g = g.to(dt)
+        if ('embT', dt) not in self._cast:
+            self._cast[('embT', dt)] = (self.P_i.t().to(dt).contiguous(),
+                                        self.P_o.to(dt).contiguous())
+        P_iT, P_o = self._cast[('embT', dt)]
+        module._ghost_grad_proj = ops().kron_embed_proj(indices, g, P_iT, P_o, 1.0,
+                                                        out_dtype=torch.float32)
 
     def attach(self, module: nn.Module) -> None:
         self._handle_forward = module.register_forward_hook(self.forward_hook_store_inputs)

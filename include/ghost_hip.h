@@ -143,6 +143,18 @@ int gs_kron_proj(const void* A, const void* G, int dtype, int64_t B, int64_t T, 
                  int64_t k_o, int layout, float scale, void* out, int out_dtype,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Replaces GradProjHooks._compute_embedding_proj
+ * (ghostEngines/gradProjection/autograd_gradproj.py:167-222), whose per-token loop reads
+ * every token id back to the host:
+ *   out[b] = scale * sum_t (P_o g_bt)(P_i[:, ids_bt])^T        [k_o, k_i]
+ * ids: [B, T] int64; G: [B, T, n_g] (dtype); P_iT: P_i transposed, [vocab, k_i] row-major;
+ * P_o: [k_o, n_g]; both of p_dtype (= dtype).  Ids outside [0, vocab) contribute nothing
+ * (the embedding's own forward rejects them first).  Workspace: gs_kron_proj_workspace. */
+int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, int64_t B, int64_t T,
+                       int64_t n_g, const void* P_iT, const void* P_o, int p_dtype,
+                       int64_t vocab, int64_t k_i, int64_t k_o, float scale, void* out,
+                       int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -330,6 +330,37 @@ def kron_proj_exact(A: torch.Tensor, B: torch.Tensor, P_i: torch.Tensor, P_o: to
     return scale * torch.einsum('op,bpd,id->boi', P_o.double(), Gs, P_i.double())
 
 
+def kron_embed_proj_ref(ids: torch.Tensor, g: torch.Tensor, P_i: torch.Tensor,
+                        P_o: torch.Tensor) -> torch.Tensor:
+    """_compute_embedding_proj (autograd_gradproj.py:167-222): per sample, per token,
+    accumulate (P_o g_t) (P_i[:, x_t])^T into a [k_o, k_i] fp32 matrix.  No batch-size
+    factor (unlike the dense path).  A direct loop: small inputs only."""
+    bs = ids.shape[0]
+    ids2 = ids.reshape(bs, -1)
+    g3 = g.reshape(bs, ids2.shape[1], g.shape[-1])
+    out = []
+    for b in range(bs):
+        acc = torch.zeros(P_o.shape[0], P_i.shape[0], dtype=torch.float32)
+        for t in range(ids2.shape[1]):
+            j = int(ids2[b, t])
+            acc += (P_o @ g3[b, t]).unsqueeze(1) @ P_i[:, j].unsqueeze(0)
+        out.append(acc)
+    return torch.stack(out).to(torch.float32)
+
+
+def kron_embed_proj_exact(ids: torch.Tensor, g: torch.Tensor, P_i: torch.Tensor,
+                          P_o: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """scale * P_o W_b P_i^T in float64, where W_b = sum_t g_t e_{x_t}^T is sample b's
+    embedding-weight gradient (transposed to [d, vocab])."""
+    bs = ids.shape[0]
+    ids2 = ids.reshape(bs, -1).long()
+    g3 = g.reshape(bs, ids2.shape[1], g.shape[-1]).double()
+    W = torch.zeros(bs, g3.shape[-1], P_i.shape[1], dtype=torch.float64)
+    W.scatter_add_(2, ids2.unsqueeze(1).expand(bs, g3.shape[-1], ids2.shape[1]),
+                   g3.transpose(1, 2))
+    return scale * torch.einsum('od,bdv,iv->boi', P_o.double(), W, P_i.double())
+
+
 def choose_ki_ko(n_i: int, n_o: int, k_total: int, k_min: int = 1):
     """choose_ki_ko (projection_utils.py:12-66): ratio rule, then a +-2 search with
     strict-improvement tie-break."""

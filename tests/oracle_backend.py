@@ -66,6 +66,11 @@ class OracleOps:
                                 conv1d=layout == _native.PROJ_KI_KO)
         return out.to(out_dtype)
 
+    def kron_embed_proj(self, ids, G, P_iT, P_o, scale=1.0, *, out_dtype=torch.float32):
+        self.calls.append(("kron_embed_proj", tuple(G.shape)))
+        out = R.kron_embed_proj_exact(ids, G.float(), P_iT.t().float(), P_o.float(), scale)
+        return out.to(out_dtype)
+
 
 class use_oracle_backend:
     """Context manager installing OracleOps as the kernel layer."""

@@ -89,3 +89,27 @@ def test_kron_projection(gpu, dtype, conf, conv1d):
                              float(B), conv1d=conv1d)
     tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
     assert_close(out.cpu(), want, tol, "kron")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("conf", [
+    # B, T, vocab, d, k_i, k_o
+    (3, 5, 30, 24, 4, 6),
+    (4, 130, 50257, 768, 16, 16),    # GPT-2 vocabulary, two token chunks + a tail
+    (2, 64, 1000, 100, 32, 32),      # d not a multiple of 8: scalar G loads
+    (5, 1, 7, 8, 1, 3),
+])
+def test_kron_embedding_projection(gpu, dtype, conf):
+    B, T, V, d, k_i, k_o = conf
+    ids = torch.randint(0, V, (B, T), generator=gen(31 + T))
+    ids[0, : min(T, 3)] = ids[0, 0]               # repeated ids in one sample
+    G = randn((B, T, d), 32 + T, 1e-3, dtype)
+    P_i = randn((k_i, V), 33, 1.0 / k_i ** 0.5)
+    P_o = randn((k_o, d), 34, 1.0 / k_o ** 0.5)
+    print(f"kron_embed conf={conf} dtype={dtype}", flush=True)
+    out = _native.ops().kron_embed_proj(ids.to(gpu), G.to(gpu), P_i.t().contiguous().to(gpu),
+                                        P_o.to(gpu), 1.0)
+    torch.cuda.synchronize()
+    want = R.kron_embed_proj_exact(ids, G.float(), P_i.to(dtype).float(), P_o.to(dtype).float())
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert_close(out.cpu(), want, tol, "kron embed")

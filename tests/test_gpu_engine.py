@@ -1,0 +1,192 @@
+"""End-to-end GPU parity through the reference API: engines and hooks on small models, with
+the HIP kernels underneath, checked against brute-force per-sample gradients (float64, CPU)."""
+import copy
+
+import pytest
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ghostsuite_amd import GradDotProdEngine, GradProjLoraEngine
+from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+from ghostsuite_amd.workloads import CausalLM, LMConfig, MLP, synthetic_tokens
+from oracle import brute
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, gen
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _reset_options():
+    saved = dict(S.options)
+    yield
+    S.options.clear()
+    S.options.update(saved)
+
+
+def _lm_loss(T):
+    return lambda m, x, y: m(x, y) * T
+
+
+@pytest.mark.parametrize("precision,tol", [("fp32", FP32_TOL), ("reference", BF16_TOL)])
+@pytest.mark.parametrize("algo", ["ghost", "valgrad"])
+def test_gpt2_engine_on_gpu_matches_per_sample_gradients(gpu, precision, tol, algo):
+    torch.manual_seed(12)
+    T, vocab = 16, 64
+    cfg = LMConfig(n_layer=2, n_head=2, d_model=32, d_mlp=64, vocab=vocab, n_ctx=T)
+    model = CausalLM(cfg)
+    untied = copy.deepcopy(model)
+    untied.lm_head.weight = nn.Parameter(model.wte.weight.detach().clone())
+    tied_ref = copy.deepcopy(model).double()
+    untied = untied.double()
+    n_t, n_v = 5, 2
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=13)
+    model = model.to(gpu)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    print(f"gpt2 engine precision={precision} algo={algo}", flush=True)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True, precision=precision,
+                            linear_algo=algo)
+    eng.attach(opt)
+    eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+    model(X.to(gpu), Y.to(gpu)).backward()
+    torch.cuda.synchronize()
+    dots = {n: p.grad_dot_prod.cpu() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    semantics = {n: m.use_ghost_computation for n, m in model.named_modules()
+                 if hasattr(m, "use_ghost_computation")}
+    eng.prepare_gradients()
+    grads = {n: p.grad.cpu() for n, p in model.named_parameters()
+             if p.grad is not None and "dummy_bias" not in n}
+    eng.aggregate_and_log()
+    eng.detach()
+
+    N = n_t + n_v
+    g_untied = brute.per_sample_grads(untied, X, Y, _lm_loss(T), 1.0 / (N * T))
+    g_tied = brute.per_sample_grads(tied_ref, X, Y, _lm_loss(T), 1.0 / (N * T))
+    total = 0
+    for name, d in dots.items():
+        layer = name.rsplit(".", 1)[0]
+        gr = g_untied[name]
+        if semantics.get(layer, True):
+            want = brute.pairwise_dots(gr, n_v)
+        else:   # materialised branch: presum over val rows, <g_i, sum_j g_j> is the same here
+            want = brute.pairwise_dots(gr, n_v) if n_v == 1 else None
+        if want is None:
+            continue
+        assert_close(d, want, tol, f"dot {name}")
+        total = total + want
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g_tied[name], n_v, N), tol, f"grad {name}")
+
+
+def test_mlp_engine_on_gpu_ten_steps(gpu):
+    """configs[0] in small: 10 SGD steps, per-step aggregated dots vs brute force."""
+    torch.manual_seed(14)
+    dims = (64, 48, 32, 10)
+    model = MLP(dims).to(gpu)
+    ref = copy.deepcopy(model).cpu().double()
+    n_t, n_v = 24, 8
+    X = torch.randn(n_t + n_v, dims[0], generator=gen(15))
+    Y = torch.randint(0, 10, (n_t + n_v,), generator=gen(16))
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False, precision="fp32")
+    eng.attach(opt)
+    for step in range(10):
+        print(f"mlp step {step}", flush=True)
+        eng.attach_train_batch(X[:n_t], Y[:n_t], step, 0)
+        loss = F.cross_entropy(model(X.to(gpu)), Y.to(gpu))
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        eng.aggregate_and_log()
+        eng.prepare_gradients()
+        opt.step()
+        eng.clear_gradients()
+        g = brute.per_sample_grads(
+            ref, X.double(), Y, lambda m, x, y: F.cross_entropy(m(x), y, reduction="sum"),
+            1.0 / X.shape[0])
+        want = sum(brute.pairwise_dots(gr, n_v) for gr in g.values())
+        assert_close(eng.dot_product_log[-1]["dot_product"], want, FP32_TOL, f"step {step}")
+        with torch.no_grad():
+            for name, p in ref.named_parameters():
+                p -= 0.1 * brute.train_mean(g[name], n_v, X.shape[0])
+    eng.detach()
+    for (n1, p1), (n2, p2) in zip(model.named_parameters(), ref.named_parameters()):
+        assert_close(p1.detach().cpu(), p2.detach(), 1e-4, f"weights {n1}")
+
+
+def test_hf_conv1d_layers_use_presum(gpu):
+    transformers = pytest.importorskip("transformers")
+    Conv1D = transformers.pytorch_utils.Conv1D
+    torch.manual_seed(17)
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.c1 = Conv1D(24, 16)   # nf=24 out, nx=16 in
+            self.c2 = Conv1D(8, 24)
+
+        def forward(self, x):
+            return self.c2(torch.tanh(self.c1(x)))
+
+    net = Net()
+    ref = copy.deepcopy(net).double()
+    N, n_v, T = 6, 1, 5
+    X = torch.randn(N, T, 16, generator=gen(18))
+    head = torch.randn(8, generator=gen(19))
+    net = net.to(gpu)
+    eng = GradDotProdEngine(net, val_batch_size=n_v, use_dummy_bias=False, precision="fp32")
+    eng.attach(torch.optim.SGD(net.parameters(), lr=0.0))
+    ((net(X.to(gpu)) * head.to(gpu)).reshape(N, -1).sum(1).mean()).backward()
+    torch.cuda.synchronize()
+    dots = {n: p.grad_dot_prod.cpu() for n, p in net.named_parameters()}
+    eng.detach()
+    g = brute.per_sample_grads(ref, X.double(), X, lambda m, x, y: (m(x) * head.double()).sum(),
+                               1.0 / N)
+    for name, d in dots.items():   # n_val = 1: presum equals <g_i, g_val>
+        assert_close(d, brute.pairwise_dots(g[name], n_v), FP32_TOL, f"conv1d {name}")
+
+
+def test_gradproj_engine_on_gpu_naive_check(gpu, tmp_path):
+    torch.manual_seed(20)
+    model = nn.Sequential(nn.Linear(10, 20), nn.ReLU(), nn.Linear(20, 5)).to(gpu)
+    X = torch.randn(4, 10, generator=gen(21)).to(gpu)
+    Y = torch.randint(0, 5, (4,), generator=gen(22)).to(gpu)
+    eng = GradProjLoraEngine(model, proj_layers="0,2", proj_rank_total=16, proj_rank_min=2,
+                             proj_seed=42, proj_dtype="float32", proj_dir=str(tmp_path))
+    eng.attach()
+    F.cross_entropy(model(X), Y).backward()
+    proj = eng.collect_batch().cpu()
+    eng.detach()
+    naive = []
+    for b in range(4):
+        model.zero_grad()
+        F.cross_entropy(model(X[b:b + 1]), Y[b:b + 1]).backward()
+        parts = []
+        for name in sorted(eng.matched_layers):
+            P_i, P_o = eng.projection_matrices[name]
+            W = eng.matched_layers[name].weight.grad.double()
+            parts.append((P_o.double() @ W @ P_i.double().t()).reshape(-1))
+        naive.append(torch.cat(parts).cpu())
+    assert_close(proj, torch.stack(naive), FP32_TOL, "gradproj naive")
+
+
+def test_gradproj_embedding_on_gpu_matches_naive(gpu, tmp_path):
+    torch.manual_seed(23)
+    emb = nn.Embedding(40, 12)
+    model = nn.Sequential(emb, nn.Flatten(), nn.Linear(12 * 5, 3)).to(gpu)
+    X = torch.randint(0, 40, (4, 5), generator=gen(24)).to(gpu)
+    Y = torch.randint(0, 3, (4,), generator=gen(25)).to(gpu)
+    eng = GradProjLoraEngine(model, proj_layers="0", proj_rank_total=12, proj_rank_min=2,
+                             proj_seed=6, proj_dtype="float32", proj_dir=str(tmp_path),
+                             include_embeddings=True)
+    eng.attach()
+    F.cross_entropy(model(X), Y).backward()
+    got = eng.matched_layers["0"]._ghost_grad_proj.cpu()
+    eng.detach()
+    P_i, P_o = (p.double().cpu() for p in eng.projection_matrices["0"])
+    for b in range(4):
+        model.zero_grad()
+        F.cross_entropy(model(X[b:b + 1]), Y[b:b + 1], reduction="sum").backward()
+        W = emb.weight.grad.double().cpu()
+        # the reference applies no batch-size factor to embedding projections
+        assert_close(got[b].double() * 4, P_o @ W.t() @ P_i.t(), FP32_TOL, f"emb proj {b}")

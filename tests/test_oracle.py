@@ -192,6 +192,28 @@ def test_kron_projection_matches_naive_projection(conv1d):
     assert_close(R.kron_proj_ref(A, B, P_i, P_o, conv1d=conv1d).double(), naive, 1e-6, "ref")
 
 
+def test_embedding_projection_forms_match_per_sample_gradients():
+    N, T, V, d, k_i, k_o = 3, 7, 11, 5, 4, 3
+    emb = nn.Embedding(V, d).double()
+    ids = torch.randint(0, V, (N, T), generator=gen(23))
+    ids[0, :4] = 2                         # repeated ids within a sample
+    head = _head(24, d).double()
+    P_i = randn((k_i, V), 25).double()
+    P_o = randn((k_o, d), 26).double()
+    out = emb(ids)
+    out.retain_grad()
+    (out * head).sum().backward()
+    g = out.grad                           # [N, T, d]
+    W = brute.per_sample_grads(emb, ids, ids, lambda m, x, y: (m(x) * head).sum(), 1.0)["weight"]
+    naive = torch.einsum('od,bvd,iv->boi', P_o, W, P_i)     # P_o W_b^T P_i^T
+    assert_close(R.kron_embed_proj_exact(ids, g, P_i, P_o), naive, 1e-10, "exact")
+    assert_close(R.kron_embed_proj_ref(ids, g.float(), P_i.float(), P_o.float()).double(),
+                 naive, 1e-6, "reference loop")
+    # an embedding is a Linear layer on one-hot inputs: the dense identity gives the same
+    onehot = torch.nn.functional.one_hot(ids, V).double()
+    assert_close(R.kron_proj_exact(onehot, g, P_i, P_o, 1.0), naive, 1e-10, "one-hot dense")
+
+
 def test_choose_ki_ko_known_answers():
     # GPT-2-medium shapes, k_total=256, k_min=8 (engine_manager defaults): values obtained
     # by hand from projection_utils.py:12-66.

@@ -36,7 +36,6 @@ struct TrBF16 {
   static constexpr int KPL = 8;     // k elements per lane per MFMA
   static constexpr int PAD = 8;     // LDS row padding (elements) -> conflict-free b128 reads
   static constexpr int VEC = 8;     // elements per 16-byte chunk
-  static constexpr int ZPAD = 8;
   using Frag = bf16x8_t;
   __device__ static __forceinline__ Frag frag(const E* p) {
     return *reinterpret_cast<const Frag*>(p);
@@ -53,7 +52,6 @@ struct TrF32 {
   static constexpr int KPL = 1;
   static constexpr int PAD = 4;
   static constexpr int VEC = 4;
-  static constexpr int ZPAD = 4;
   using Frag = float;
   __device__ static __forceinline__ Frag frag(const E* p) { return *p; }
   __device__ static __forceinline__ void mma(f32x16_t& c, Frag a, Frag b) {
@@ -272,15 +270,34 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned voff,
                : "memory");
 }
 constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
-constexpr int DMA_ROW_BYTES = 128;  // BK = 64 bf16
+#ifndef GS_SCHED
+#define GS_SCHED 1
+#endif
+#ifndef GS_PF
+#define GS_PF 1
+#endif
 
-template <class C>
+// Geometry of one LDS-DMA pipeline over the tile of config C: each stage holds ROWB bytes
+// (ROWB / 2 bf16 of K) of every L and R row, NS stage buffers.  A wave-level load moves
+// 1 KiB = RPL rows.
+template <class C, int ROWB, int NS>
 struct DmaCfg {
   static constexpr int NW = C::WM * C::WN;
-  static constexpr int GROUPS_L = C::BM / 8, GROUPS_R = C::BN / 8;
-  static constexpr int QL = GROUPS_L / NW, QR = GROUPS_R / NW;  // loads per wave per stage
-  static_assert(GROUPS_L % NW == 0 && GROUPS_R % NW == 0, "row groups must split over waves");
-  static constexpr int STAGE_BYTES = (C::BM + C::BN) * DMA_ROW_BYTES;
+  static constexpr int ROW_BYTES = ROWB, STAGES = NS;
+  static constexpr int CH = ROWB / 16;   // 16-byte chunks per row
+  static constexpr int RPL = 64 / CH;    // rows per wave-level load
+  static constexpr int KB = ROWB / 2;    // k elements per stage
+  static constexpr int KSTEPS = KB / 16; // MFMA k-steps per stage
+  static_assert(ROWB == 64 || ROWB == 128, "64- or 128-byte stage rows");
+  static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
+  static_assert((C::BM / RPL) % NW == 0 && (C::BN / RPL) % NW == 0,
+                "row groups must split over waves");
+  static constexpr int QL = C::BM / RPL / NW, QR = C::BN / RPL / NW;  // loads per wave
+  static constexpr int STAGE_BYTES = (C::BM + C::BN) * ROWB;
+  // Physical slot of logical chunk c of row r is c ^ swz(r): the 16 consecutive rows a
+  // 16-lane ds_read_b128 group reads (one logical chunk each) then occupy 16 distinct
+  // 16-byte bank groups of the 256-byte bank window.  swz depends on r mod 32 only.
+  __device__ static constexpr int swz(int r) { return CH == 8 ? (r >> 1) & 7 : (r >> 2) & 3; }
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t nbytes) {
@@ -304,38 +321,35 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <class C>
+template <class C, class D>
 struct DmaStreamer {
-  using D = DmaCfg<C>;
   __amdgpu_buffer_rsrc_t rl, rr;
   unsigned offl[D::QL], offr[D::QR];  // row byte offset + chunk byte offset, or DMA_OOB
   int kl[D::QL], kr[D::QR];            // this lane's k element offset within a stage
 
-  __device__ __forceinline__ void init(const Operand& L, const Operand& R, int64_t mt, int64_t nt,
-                                       int64_t K) {
+  __device__ __forceinline__ void init(const Operand& L, const Operand& R, int64_t mt,
+                                       int64_t nt) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int sub = lane >> 3, slot = lane & 7;
+    const int sub = lane / D::CH, slot = lane % D::CH;
     rl = make_rsrc(L.base, L.nbytes);
     rr = make_rsrc(R.base, R.nbytes);
 #pragma unroll
     for (int q = 0; q < D::QL; ++q) {
-      const int r = 8 * (wid + D::NW * q) + sub;
-      const int c = slot ^ ((r >> 1) & 7);
+      const int r = D::RPL * (wid + D::NW * q) + sub;
+      const int c = slot ^ D::swz(r);
       const int64_t pr = tile_row<C::BM>(L, mt, r);
       offl[q] = pr < 0 ? DMA_OOB : static_cast<unsigned>(pr * L.ld * 2 + c * 16);
       kl[q] = c * 8;
     }
 #pragma unroll
     for (int q = 0; q < D::QR; ++q) {
-      const int r = 8 * (wid + D::NW * q) + sub;  // row within the R block of the stage
-      const int c = slot ^ (((C::BM + r) >> 1) & 7);
+      const int r = D::RPL * (wid + D::NW * q) + sub;  // row within the R block of the stage
+      const int c = slot ^ D::swz(C::BM + r);
       const int64_t pr = tile_row<C::BN>(R, nt, r);
       offr[q] = pr < 0 ? DMA_OOB : static_cast<unsigned>(pr * R.ld * 2 + c * 16);
       kr[q] = c * 8;
     }
-    (void)K;
   }
-  template <int S>
   __device__ __forceinline__ void issue(unsigned char* stage, int64_t k0, int64_t K) {
     const int wid = threadIdx.x >> 6;
     const unsigned kb = static_cast<unsigned>(k0 * 2);
@@ -343,86 +357,120 @@ struct DmaStreamer {
     for (int q = 0; q < D::QL; ++q) {
       const bool kin = k0 + kl[q] < K;
       const unsigned off = (kin && offl[q] != DMA_OOB) ? offl[q] + kb : DMA_OOB;
-      dma16(rl, off, stage + (wid + D::NW * q) * 8 * DMA_ROW_BYTES);
+      dma16(rl, off, stage + (wid + D::NW * q) * D::RPL * D::ROW_BYTES);
     }
 #pragma unroll
     for (int q = 0; q < D::QR; ++q) {
       const bool kin = k0 + kr[q] < K;
       const unsigned off = (kin && offr[q] != DMA_OOB) ? offr[q] + kb : DMA_OOB;
-      dma16(rr, off, stage + (C::BM + 8 * (wid + D::NW * q)) * DMA_ROW_BYTES);
+      dma16(rr, off, stage + (C::BM + D::RPL * (wid + D::NW * q)) * D::ROW_BYTES);
     }
   }
 };
 
-template <class C>
-__device__ __forceinline__ void dma_compute(const unsigned char* stage, f32x16_t (&acc)[C::MI][C::NI]) {
+template <class C, class D>
+__device__ __forceinline__ void dma_compute(const unsigned char* stage,
+                                            f32x16_t (&acc)[C::MI][C::NI]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
-  const int lo = (lane >> 1) & 7, hi = lane >> 5;  // rows start at multiples of 32
-  const unsigned char* lt = stage + (wm * 32 * C::MI + (lane & 31)) * DMA_ROW_BYTES;
-  const unsigned char* rt = stage + (C::BM + wn * 32 * C::NI + (lane & 31)) * DMA_ROW_BYTES;
-  bf16x8_t a[2][C::MI], b[2][C::NI];
+  const int lo = D::swz(lane & 31), hi = lane >> 5;  // fragment rows start at multiples of 32
+  const unsigned char* lt = stage + (wm * 32 * C::MI + (lane & 31)) * D::ROW_BYTES;
+  const unsigned char* rt = stage + (C::BM + wn * 32 * C::NI + (lane & 31)) * D::ROW_BYTES;
+  constexpr int NB = GS_PF + 1;  // fragment buffers: reads run GS_PF k-steps ahead
+  bf16x8_t a[NB][C::MI], b[NB][C::NI];
   auto load = [&](int buf, int ks) {
-    const int off = (((2 * ks + hi) ^ lo)) * 16;
+    const int off = ((2 * ks + hi) ^ lo) * 16;
 #pragma unroll
     for (int i = 0; i < C::MI; ++i)
-      a[buf][i] = *reinterpret_cast<const bf16x8_t*>(lt + i * 32 * DMA_ROW_BYTES + off);
+      a[buf][i] = *reinterpret_cast<const bf16x8_t*>(lt + i * 32 * D::ROW_BYTES + off);
 #pragma unroll
     for (int j = 0; j < C::NI; ++j)
-      b[buf][j] = *reinterpret_cast<const bf16x8_t*>(rt + j * 32 * DMA_ROW_BYTES + off);
+      b[buf][j] = *reinterpret_cast<const bf16x8_t*>(rt + j * 32 * D::ROW_BYTES + off);
   };
-  load(0, 0);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (ks + 1 < 4) load((ks + 1) & 1, ks + 1);
+  for (int ks = 0; ks < GS_PF && ks < D::KSTEPS; ++ks) load(ks, ks);
+#pragma unroll
+  for (int ks = 0; ks < D::KSTEPS; ++ks) {
+    if (ks + GS_PF < D::KSTEPS) load((ks + GS_PF) % NB, ks + GS_PF);
 #pragma unroll
     for (int i = 0; i < C::MI; ++i)
 #pragma unroll
       for (int j = 0; j < C::NI; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j],
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks % NB][i], b[ks % NB][j],
                                                             acc[i][j], 0, 0, 0);
+  }
+#if GS_SCHED
+  // Instruction order for the scheduler: the first GS_PF k-steps' fragment reads, then
+  // each k-step's MFMAs with the reads GS_PF k-steps ahead interleaved one by one, so that
+  // LDS latency hides behind MFMAs instead of being waited out before each k-step.
+  constexpr int R = C::MI + C::NI, M = C::MI * C::NI;
+  constexpr int PF = GS_PF < D::KSTEPS ? GS_PF : D::KSTEPS;
+  __builtin_amdgcn_sched_group_barrier(0x100, R * PF, 0);
+#pragma unroll
+  for (int ks = 0; ks + PF < D::KSTEPS; ++ks) {
+#pragma unroll
+    for (int g = 0; g < (R < M ? R : M); ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (M > R) __builtin_amdgcn_sched_group_barrier(0x008, M - R, 0);
+    if constexpr (R > M) __builtin_amdgcn_sched_group_barrier(0x100, R - M, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, M * PF, 0);
+#endif
+}
+
+// The stage buffers: one __shared__ array of STAGES * STAGE_BYTES (the DMA is inline asm,
+// so the compiler does not track it and one array costs no extra waits).
+struct DmaLds {
+  unsigned char* base;
+};
+
+// Waits until at most `pending` (<= MAXP) stages of loads are still in flight.
+template <int NQ, int MAXP>
+__device__ __forceinline__ void wait_stages(int64_t pending) {
+  if constexpr (MAXP > 0) {
+    if (pending >= MAXP) {
+      wait_vmcnt<MAXP * NQ>();
+      return;
+    }
+    wait_stages<NQ, MAXP - 1>(pending);
+  } else {
+    wait_vmcnt<0>();
   }
 }
 
-template <class C>
-struct DmaLds {
-  unsigned char* s0;
-  unsigned char* s1;
-  unsigned char* s2;
-};
-
-template <class C, int S>
-__device__ __forceinline__ unsigned char* dma_slot(const DmaLds<C>& l) {
-  return S == 0 ? l.s0 : (S == 1 ? l.s1 : l.s2);
-}
-
-template <class C, int S>
-__device__ __forceinline__ void dma_step(DmaStreamer<C>& st, const DmaLds<C>& l, int64_t kt,
-                                         int64_t nk, int64_t K, f32x16_t (&acc)[C::MI][C::NI]) {
-  constexpr int NQ = DmaCfg<C>::QL + DmaCfg<C>::QR;
-  if (kt + 1 < nk)
-    wait_vmcnt<NQ>();
-  else
-    wait_vmcnt<0>();
-  raw_barrier();
-  if (kt + 2 < nk) st.template issue<(S + 2) % 3>(dma_slot<C, (S + 2) % 3>(l), (kt + 2) * 64, K);
-  dma_compute<C>(dma_slot<C, S>(l), acc);
-}
-
-// acc += L_tile R_tile^T over K, bf16 operands through the LDS-DMA ring.
-template <class C>
+// acc += L_tile R_tile^T over K, bf16 operands through the LDS-DMA ring.  Stage kt lives
+// in slot kt % STAGES; the loads of stage kt + STAGES - 1 are issued right after the
+// barrier that opens stage kt (every wave has finished reading that slot, stage kt - 1, by
+// then).  The steady-state loop body is one basic block: a constant vmcnt wait, barrier,
+// loads, MFMAs.
+template <class C, class D>
 __device__ __forceinline__ void mainloop_dma(const Operand& L, const Operand& R, int64_t mt,
-                                             int64_t nt, int64_t K, const DmaLds<C>& l,
+                                             int64_t nt, int64_t K, const DmaLds& l,
                                              f32x16_t (&acc)[C::MI][C::NI]) {
-  DmaStreamer<C> st;
-  st.init(L, R, mt, nt, K);
-  const int64_t nk = (K + 63) / 64;
-  st.template issue<0>(l.s0, 0, K);
-  if (nk > 1) st.template issue<1>(l.s1, 64, K);
-  for (int64_t kt = 0; kt < nk; kt += 3) {
-    dma_step<C, 0>(st, l, kt, nk, K, acc);
-    if (kt + 1 < nk) dma_step<C, 1>(st, l, kt + 1, nk, K, acc);
-    if (kt + 2 < nk) dma_step<C, 2>(st, l, kt + 2, nk, K, acc);
+  constexpr int NQ = D::QL + D::QR;
+  constexpr int AHEAD = D::STAGES - 1;  // stages in flight ahead of the one computed
+  static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
+  DmaStreamer<C, D> st;
+  st.init(L, R, mt, nt);
+  const int nk = static_cast<int>((K + D::KB - 1) / D::KB);
+  auto slot = [&](int k) { return l.base + (k % D::STAGES) * D::STAGE_BYTES; };
+#pragma unroll
+  for (int s = 0; s < AHEAD; ++s)
+    if (s < nk) st.issue(slot(s), static_cast<int64_t>(s) * D::KB, K);
+  int kt = 0;
+  for (; kt + AHEAD < nk; ++kt) {
+    wait_vmcnt<(AHEAD - 1) * NQ>();  // stage kt has landed
+    raw_barrier();
+    st.issue(slot(kt + AHEAD), static_cast<int64_t>(kt + AHEAD) * D::KB, K);
+    dma_compute<C, D>(slot(kt), acc);
+  }
+  // Tail: no more loads; the stages still in flight drain one by one.
+  for (; kt < nk; ++kt) {
+    wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
+    raw_barrier();
+    dma_compute<C, D>(slot(kt), acc);
   }
   wait_vmcnt<0>();
   raw_barrier();
@@ -500,54 +548,53 @@ __device__ __forceinline__ void ghost_colsum(const GemmParams& p, f32x16_t (&acc
   }
 }
 
-// Per-lane column sums of acc[m][n] * Z[n][m] over this wave's rows; the Z tile
-// [BN rows][BM cols] is staged through `lds` (at least BN * (BM + ZPAD) elements).
+// Per-lane column sums of acc[m][n] * Z[n][m] over this wave's rows.  Z is read straight
+// from memory: the 4 consecutive accumulator rows a lane holds per MFMA row group are 4
+// consecutive elements of Z row n, one 8-byte (bf16) or 16-byte (fp32) load.
 template <class Tr, class C>
 __device__ __forceinline__ void rowdot_colsum(const GemmParams& p, f32x16_t (&acc)[C::MI][C::NI],
-                                              int64_t mt, int64_t nt, typename Tr::E* lds,
-                                              float (&colsum)[C::NI]) {
+                                              int64_t mt, int64_t nt, float (&colsum)[C::NI]) {
   using E = typename Tr::E;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  using Z4 = std::conditional_t<sizeof(E) == 2, uint2, uint4>;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
-  constexpr int ZLD = C::BM + Tr::ZPAD;
-  constexpr int CPR = C::BM / Tr::VEC;
-  constexpr int NQ = C::BN * CPR / C::NT;
   const E* Zb = static_cast<const E*>(p.Z);
-  const int kc = tid % CPR;
-  const int64_t m0 = mt * C::BM + kc * Tr::VEC;
+  const int64_t mb = mt * C::BM + wm * 32 * C::MI + 4 * (lane >> 5);
+  const bool full = p.z_vec_ok && (mt + 1) * C::BM <= p.m_rows;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int r = tid / CPR + q * (C::NT / CPR);
-    const int64_t f = nt * C::BN + r;
-    union { uint4 v; E e[Tr::VEC]; } u;
-    u.v = make_uint4(0u, 0u, 0u, 0u);
+  for (int ni = 0; ni < C::NI; ++ni) {
+    const int64_t f = nt * C::BN + wn * 32 * C::NI + ni * 32 + (lane & 31);
+    float s = 0.f;
     if (f < p.z_map.total()) {
       const int64_t seg = f / p.z_map.seglen;
       const E* zr = Zb + p.z_map.phys_row(seg, f - seg * p.z_map.seglen) * p.z_ld;
-      if (p.z_vec_ok && m0 + Tr::VEC <= p.m_rows) {
-        u.v = *reinterpret_cast<const uint4*>(zr + m0);
+      union { Z4 v; E e[4]; } z[C::MI][4];
+      if (full) {
+#pragma unroll
+        for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            z[mi][g].v = *reinterpret_cast<const Z4*>(zr + mb + mi * 32 + 8 * g);
       } else {
 #pragma unroll
-        for (int v = 0; v < Tr::VEC; ++v) u.e[v] = (m0 + v < p.m_rows) ? zr[m0 + v] : E(0);
+        for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int64_t m = mb + mi * 32 + 8 * g + v;
+              z[mi][g].e[v] = m < p.m_rows ? zr[m] : E(0);
+            }
       }
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) s += acc[mi][ni][4 * g + v] * to_f32<E>(z[mi][g].e[v]);
     }
-    *reinterpret_cast<uint4*>(lds + r * ZLD + kc * Tr::VEC) = u.v;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int ni = 0; ni < C::NI; ++ni) {
-    const int nl = wn * 32 * C::NI + ni * 32 + (lane & 31);
-    float s = 0.f;
-#pragma unroll
-    for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int ml = wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        s += acc[mi][ni][e] * to_f32<E>(lds[nl * ZLD + ml]);
-      }
     colsum[ni] = s;
   }
-  __syncthreads();  // Z reads done before the reduction scratch reuses LDS
 }
 
 // Combines column sums across the half-waves and the WM waves sharing columns, then writes
@@ -603,37 +650,101 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_nt_kernel(GemmParams
       mainloop<Tr, C, AL>(p.L2, p.R2, mt, nt, p.K2, lds, acc2);
       ghost_colsum<C>(p, acc, acc2, colsum);
     } else {
-      rowdot_colsum<Tr, C>(p, acc, mt, nt, lds, colsum);
+      rowdot_colsum<Tr, C>(p, acc, mt, nt, colsum);
     }
     write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(smem_raw));
   }
 }
 
-// bf16, 16-byte aligned operands below 4 GiB: the LDS-DMA mainloop (GHOST and STORE).
-template <class C, int EPI>
+// bf16, 16-byte aligned operands below 4 GiB: the LDS-DMA mainloop.
+template <class C, class D, int EPI>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParams p) {
-  constexpr int SB = DmaCfg<C>::STAGE_BYTES;
-  __shared__ __attribute__((aligned(16))) unsigned char s0[SB];
-  __shared__ __attribute__((aligned(16))) unsigned char s1[SB];
-  __shared__ __attribute__((aligned(16))) unsigned char s2[SB];
-  const DmaLds<C> l{s0, s1, s2};
+  constexpr int SB = D::STAGE_BYTES;
+  static_assert(D::STAGES * SB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) unsigned char s0[D::STAGES * SB];
+  const DmaLds l{s0};
   int64_t mt, nt;
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
-  mainloop_dma<C>(p.L1, p.R1, mt, nt, p.K1, l, acc);
+  mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
   if constexpr (EPI == EPI_STORE) {
     store_epilogue<TrBF16, C>(p, acc, mt, nt);
   } else {
-    static_assert(EPI == EPI_GHOST, "DMA kernel: GHOST or STORE");
-    f32x16_t acc2[C::MI][C::NI];
-    zero_acc<TrBF16, C>(acc2);
-    mainloop_dma<C>(p.L2, p.R2, mt, nt, p.K2, l, acc2);
     float colsum[C::NI];
-    ghost_colsum<C>(p, acc, acc2, colsum);
+    if constexpr (EPI == EPI_GHOST) {
+      f32x16_t acc2[C::MI][C::NI];
+      zero_acc<TrBF16, C>(acc2);
+      mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc2);
+      ghost_colsum<C>(p, acc, acc2, colsum);
+    } else {
+      rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
+    }
     static_assert(C::WM * C::BN * 4 <= SB, "partial scratch");
     write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
   }
+}
+
+// GHOST with large wave tiles (one wave per SIMD): the first Gram tile (A_val A_tr^T over
+// K1) is rounded to bf16 and held packed in registers while the second (G_val G_tr^T over
+// K2) accumulates in fp32, which halves the registers the first tile needs.  The reference
+// rounds both Gram matrices to bf16 (its a_dot / b_dot are bf16 matmul outputs).
+template <class C, class D>
+__global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
+  constexpr int SB = D::STAGE_BYTES;
+  static_assert(D::STAGES * SB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) unsigned char s0[D::STAGES * SB];
+  const DmaLds l{s0};
+  int64_t mt, nt;
+  tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
+  f32x16_t acc[C::MI][C::NI];
+  zero_acc<TrBF16, C>(acc);
+  mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
+  uint32_t ga[C::MI][C::NI][8];  // bf16 pairs (even element in the low half)
+#pragma unroll
+  for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+    for (int j = 0; j < C::NI; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        ga[i][j][e] = pack_bf16x2(acc[i][j][2 * e], acc[i][j][2 * e + 1]);
+  // Materialise the packed tile here, so the first accumulators die before the second
+  // GEMM's accumulators come alive (otherwise both sets compete for the AGPRs).
+#pragma unroll
+  for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+    for (int j = 0; j < C::NI; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(ga[i][j][e]));
+  asm volatile("" ::: "memory");
+  zero_acc<TrBF16, C>(acc);
+  mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc);
+  float colsum[C::NI];
+  auto hadamard = [&](auto ref) {
+#pragma unroll
+    for (int j = 0; j < C::NI; ++j) {
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t w = ga[i][j][e >> 1];
+          const float a = __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
+          const float g = acc[i][j][e];
+          if constexpr (decltype(ref)::value)
+            sum += round_bf16(a * round_bf16(g));
+          else
+            sum += a * g;
+        }
+      colsum[j] = sum;
+    }
+  };
+  if (p.rounding == GS_ROUND_REF_BF16)
+    hadamard(std::true_type{});
+  else
+    hadamard(std::false_type{});
+  static_assert(C::WM * C::BN * 4 <= SB, "partial scratch");
+  write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
 }
 
 // P[(g*rows_per_group + r) * p_ld + i*cols + c] summed over r < rows_per_group and c < cols
@@ -747,10 +858,21 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 #define GS_GHOST_TILE 4, 2, 2, 2
 #endif
 #ifndef GS_ROWDOT_TILE
-#define GS_ROWDOT_TILE 2, 2, 2, 2
+#define GS_ROWDOT_TILE 2, 4, 4, 2
 #endif
 #ifndef GS_STORE_TILE
 #define GS_STORE_TILE 2, 2, 1, 1
+#endif
+// bf16 GHOST through ghost_stash_kernel: 256x256 tiles, 8 waves of 128x64 (2x4 waves),
+// 64-byte stage rows, 4 stages (128 KiB of LDS).
+#ifndef GS_GHOST_STASH
+#define GS_GHOST_STASH 1
+#endif
+#ifndef GS_STASH_TILE
+#define GS_STASH_TILE 2, 4, 4, 2
+#endif
+#ifndef GS_STASH_DMA
+#define GS_STASH_DMA 64, 4
 #endif
 // fp32 operands (precision checks, fp32 models) keep the small 128 x 128 tile.
 template <class Tr, int... Tile>
@@ -759,11 +881,24 @@ using PickCfg = std::conditional_t<std::is_same<Tr, TrF32>::value, Cfg<Tr, 2, 2,
 template <class Tr> using GhostCfg = PickCfg<Tr, GS_GHOST_TILE>;
 template <class Tr> using RowdotCfg = PickCfg<Tr, GS_ROWDOT_TILE>;
 template <class Tr> using StoreCfg = PickCfg<Tr, GS_STORE_TILE>;
+using StashCfg = Cfg<TrBF16, GS_STASH_TILE>;
+using StashDma = DmaCfg<StashCfg, GS_STASH_DMA>;
+// Both bf16 GHOST kernels share the M tile, so the partial-sum layout (one row per M tile,
+// one column per train token) does not depend on which one runs.
+static_assert(StashCfg::BM == GhostCfg<TrBF16>::BM, "GHOST kernels must share BM");
 
 namespace {
 
 #ifndef GS_USE_DMA
 #define GS_USE_DMA 1
+#endif
+// Stage geometry of gemm_dma_kernel: three 128-byte-row stages when they fit in LDS,
+// else four 64-byte-row stages.
+template <class C>
+using DmaFor = std::conditional_t<3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
+                                  DmaCfg<C, 64, 4>>;
+#ifndef GS_ROWDOT_DMA
+#define GS_ROWDOT_DMA 1
 #endif
 
 bool dma_ok(const Operand& o) { return o.vec_ok && o.nbytes > 0 && o.nbytes < INT32_MAX; }
@@ -776,12 +911,14 @@ struct Launch {
     if (blocks <= 0) return GS_OK;
     if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
-    if constexpr (std::is_same<Tr, TrBF16>::value && EPI == EPI_GHOST &&
-                  3 * DmaCfg<C>::STAGE_BYTES <= 160 * 1024) {
-      const bool dma = GS_USE_DMA && aligned && dma_ok(p.L1) && dma_ok(p.R1) &&
+    using D = DmaFor<C>;
+    if constexpr (std::is_same<Tr, TrBF16>::value && EPI != EPI_STORE &&
+                  D::STAGES * D::STAGE_BYTES <= 160 * 1024) {
+      const bool dma = GS_USE_DMA && (EPI == EPI_GHOST || GS_ROWDOT_DMA) && aligned &&
+                       dma_ok(p.L1) && dma_ok(p.R1) &&
                        (EPI != EPI_GHOST || (dma_ok(p.L2) && dma_ok(p.R2)));
       if (dma) {
-        hipLaunchKernelGGL((gemm_dma_kernel<C, EPI>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemm_dma_kernel<C, D, EPI>), grid, block, 0, s, p);
         return check_launch("gemm_dma_kernel");
       }
     }
@@ -871,7 +1008,8 @@ LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_
     pl.vcols = nv_eff * T;
     bn = RowdotCfg<Tr>::BN;
   }
-  pl.tile_reduce = (T % bn == 0) ? 1 : 0;
+  // GHOST keeps per-token partials: its two bf16 kernels differ in BN.
+  pl.tile_reduce = (pl.algo != GS_ALGO_GHOST && T % bn == 0) ? 1 : 0;
   pl.p_ld = pl.tile_reduce ? n_t * T / bn : n_t * T;
   pl.cols = pl.tile_reduce ? T / bn : T;
   return pl;
@@ -965,7 +1103,21 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     p.p_row0 = 0;
     if (p.m_tiles != pl.p_rows) return fail(GS_ERR_INVALID, "internal: ghost partial rows");
     const bool al = p.L1.vec_ok && p.R1.vec_ok && p.L2.vec_ok && p.R2.vec_ok;
-    int rc = Launch<Tr, GC>::template run<EPI_GHOST>(p, al, s);
+    int rc = GS_OK;
+    bool done = false;
+    if constexpr (std::is_same<Tr, TrBF16>::value) {
+      if (GS_GHOST_STASH && al && dma_ok(p.L1) && dma_ok(p.R1) && dma_ok(p.L2) &&
+          dma_ok(p.R2)) {
+        p.n_tiles = host_tiles<StashCfg::BN>(p.R1);
+        const int64_t blocks = p.m_tiles * p.n_tiles;
+        if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
+        hipLaunchKernelGGL((ghost_stash_kernel<StashCfg, StashDma>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(StashCfg::NT), 0, s, p);
+        rc = check_launch("ghost_stash_kernel");
+        done = true;
+      }
+    }
+    if (!done) rc = Launch<Tr, GC>::template run<EPI_GHOST>(p, al, s);
     if (rc) return rc;
     hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s,
                        P, pl.groups, pl.p_rows / pl.groups, pl.p_ld, pl.cols, n_t, out_pair,

@@ -11,15 +11,18 @@ train gradients, then frees the caches.  Differences are internal only:
 """
 from __future__ import annotations
 
+import contextlib
 import itertools
 from typing import Tuple
 
 import torch
 import torch.nn as nn
 
+from . import _overlap
 from .supported_layers_grad_samplers_dotprod import (
     _supported_layers_dotprod,
     _create_or_accumulate_train_grad,
+    options,
 )
 
 _step_counter = itertools.count()
@@ -108,12 +111,16 @@ def _prepare_sample_grad_or_dotprod(layer: nn.Module, grad_output: Tuple[torch.T
         layer._gs_ln_grad_scale = scale / n_train
 
     acts = layer.activations
-    if acts is not None and acts.dtype != backprops.dtype and acts.is_floating_point():
-        common = torch.promote_types(acts.dtype, backprops.dtype)
-        compute_layer_dotprod(layer, acts.to(common), backprops.to(common),
-                              val_batch_size=val_batch_size)
-    else:
-        compute_layer_dotprod(layer, acts, backprops, val_batch_size=val_batch_size)
+    # The dot kernels run on a side stream, overlapped with the rest of backward.
+    side = _overlap.on_side_stream(acts, backprops) if options["overlap"] else \
+        contextlib.nullcontext()
+    with side:
+        if acts is not None and acts.dtype != backprops.dtype and acts.is_floating_point():
+            common = torch.promote_types(acts.dtype, backprops.dtype)
+            compute_layer_dotprod(layer, acts.to(common), backprops.to(common),
+                                  val_batch_size=val_batch_size)
+        else:
+            compute_layer_dotprod(layer, acts, backprops, val_batch_size=val_batch_size)
 
     layer.backprops = backprops
     layer.backprops_scale = scale

@@ -754,13 +754,12 @@ __global__ void reduce_partials_kernel(const float* __restrict__ P, int64_t grou
                                        int64_t n_train, float* out_pair, float* out_dot) {
   __shared__ float red[16];
   const int64_t i = blockIdx.x;
-  const int64_t per = rows_per_group * cols;
   float dot = 0.f;
   for (int64_t g = 0; g < groups; ++g) {
     float s = 0.f;
-    for (int64_t x = threadIdx.x; x < per; x += blockDim.x) {
-      const int64_t r = x / cols, c = x - r * cols;
-      s += P[(g * rows_per_group + r) * p_ld + i * cols + c];
+    for (int64_t r = 0; r < rows_per_group; ++r) {
+      const float* row = P + (g * rows_per_group + r) * p_ld + i * cols;
+      for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s += row[c];
     }
     s = block_sum(s, red);
     if (out_pair != nullptr && threadIdx.x == 0) out_pair[g * n_train + i] = s;

@@ -14,7 +14,7 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from .. import _native
+from .. import _native, _overlap
 from .._native import ops
 
 
@@ -63,10 +63,12 @@ class GradProjHooks:
             delattr(module, '_ghost_A_raw')
             return
         B_out = B_out.detach()
-        if self.layer_type == 'Embedding':
-            self._compute_embedding_proj(module, A_raw, B_out)
-        else:
-            self._compute_dense_proj(module, A_raw, B_out)
+        # The projection kernels run on a side stream, overlapped with the rest of backward.
+        with _overlap.on_side_stream(A_raw, B_out):
+            if self.layer_type == 'Embedding':
+                self._compute_embedding_proj(module, A_raw, B_out)
+            else:
+                self._compute_dense_proj(module, A_raw, B_out)
         delattr(module, '_ghost_A_raw')
 
     def _compute_dense_proj(self, module: nn.Module, A_raw: torch.Tensor,

@@ -14,6 +14,7 @@ import torch.nn as nn
 
 from .projection_utils import (choose_ki_ko, compute_projection_metadata,
                                get_projection_initializer)
+from .. import _overlap
 from .autograd_gradproj import create_projection_hooks
 from .supported_layers_gradproj import (compute_total_projection_size, find_matching_layers,
                                         get_layer_dimensions, get_layer_slice_ranges,
@@ -140,6 +141,7 @@ class GradProjLoraEngine:
         proj_save_interval calls."""
         if not self.is_attached:
             raise RuntimeError("Engine is not attached. Call attach() first.")
+        _overlap.join()   # the projection kernels run on the side stream
         parts, batch_size = [], None
         for name in sorted(self.matched_layers.keys()):
             grad_proj = getattr(self.matched_layers[name], '_ghost_grad_proj', None)

@@ -5,7 +5,7 @@ prepare_gradients, clear_gradients, aggregate_and_log, save_dot_product_log,
 attach_and_store_valset, attach_train_batch, the dot_product_log record format).  Extra
 keyword arguments set the sampler options of
 ``supported_layers_grad_samplers_dotprod.options`` (precision, linear_algo, rounding,
-store_pairs, skip_overwritten_tied_dots, record_algorithms).
+store_pairs, skip_overwritten_tied_dots, record_algorithms, overlap).
 """
 from __future__ import annotations
 
@@ -16,6 +16,7 @@ from typing import Optional
 import torch
 from torch import nn
 
+from . import _overlap
 from . import autograd_grad_sample_dotprod
 from . import transformers_support
 from . import supported_layers_grad_samplers_dotprod as _samplers
@@ -82,6 +83,7 @@ class GradDotProdEngine:
         """Moves ``param.train_grad`` into ``param.grad`` (reference :131-163)."""
         if self._grad_creation_locked:
             return
+        _overlap.join()   # fused bias / LayerNorm train grads come from the side stream
         for name, param in self.module.named_parameters():
             if not param.initially_requires_grad:
                 continue
@@ -118,6 +120,7 @@ class GradDotProdEngine:
     def _aggregate_and_log_dot_products(self):
         """Sums ``grad_dot_prod`` over parameters in ``named_parameters`` order -- the first
         tensor accumulates the rest in place -- and logs a CPU copy (reference :192-230)."""
+        _overlap.join()
         total = None
         for _, param in self.module.named_parameters():
             if hasattr(param, 'grad_dot_prod') and param.initially_requires_grad:

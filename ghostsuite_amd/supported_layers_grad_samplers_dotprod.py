@@ -23,7 +23,7 @@ from typing import Optional
 import torch
 from torch import nn
 
-from . import _native
+from . import _native, _overlap
 from ._native import ops
 
 try:  # HF Conv1D is a registry key only when transformers is importable
@@ -51,6 +51,8 @@ options = {
     "store_pairs": False,
     "skip_overwritten_tied_dots": True,
     "record_algorithms": False,
+    # Run the dot kernels on a side stream, overlapped with the rest of backward.
+    "overlap": True,
 }
 ALGO_LOG: dict = {}
 
@@ -77,6 +79,7 @@ def _create_or_accumulate_train_grad(param: torch.Tensor, grad: torch.Tensor) ->
         f"Gradient shape ({grad.shape}) does not match parameter shape ({param.shape})"
     new_grad = grad.detach()
     if hasattr(param, 'train_grad'):
+        _overlap.join(new_grad.device)   # either addend may come from the side stream
         param.train_grad.add_(new_grad)
     else:
         param.train_grad = new_grad

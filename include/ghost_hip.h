@@ -57,7 +57,10 @@ typedef enum { GS_SEM_PAIRWISE_SUM = 0, GS_SEM_PRESUM = 1 } gs_semantics;
 typedef enum { GS_ALGO_AUTO = 0, GS_ALGO_GHOST = 1, GS_ALGO_VALGRAD = 2 } gs_algo;
 
 /* Rounding of the ghost Gram blocks.
- *   FP32:    Gram entries and their Hadamard product stay fp32.
+ *   FP32:    Gram entries and their Hadamard product stay fp32, except that with bf16
+ *            operands (16-byte aligned rows) the activation Gram block is held as bf16
+ *            while the grad Gram block accumulates, the rounding point the reference's
+ *            bf16 a_dot also has.
  *   REF_BF16: Gram entries and their product are rounded to bf16 before the fp32 sum, as
  *            the reference's bf16 matmul outputs are (supported_layers_grad_samplers_dotprod.py:125-129). */
 typedef enum { GS_ROUND_FP32 = 0, GS_ROUND_REF_BF16 = 1 } gs_rounding;

@@ -190,3 +190,56 @@ def test_gradproj_embedding_on_gpu_matches_naive(gpu, tmp_path):
         W = emb.weight.grad.double().cpu()
         # the reference applies no batch-size factor to embedding projections
         assert_close(got[b].double() * 4, P_o @ W.t() @ P_i.t(), FP32_TOL, f"emb proj {b}")
+
+
+def test_side_stream_overlap_gives_identical_results(gpu):
+    """The dot kernels on the side stream (default) and on the autograd stream give the same
+    bits over several optimizer steps of a model large enough to recycle memory (no
+    attention, whose backward need not be bit-reproducible)."""
+    vocab, d, T = 512, 128, 128
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.emb = nn.Embedding(vocab, d)
+            self.blocks = nn.ModuleList(
+                nn.Sequential(nn.LayerNorm(d), nn.Linear(d, 4 * d), nn.GELU(), nn.Linear(4 * d, d))
+                for _ in range(3))
+            self.ln_f = nn.LayerNorm(d)
+            self.head = nn.Linear(d, vocab)
+
+        def forward(self, x, y):
+            h = self.emb(x)
+            for b in self.blocks:
+                h = h + b(h)
+            logits = self.head(self.ln_f(h)).float()
+            return F.cross_entropy(logits.reshape(-1, vocab), y.reshape(-1))
+
+    X = torch.randint(0, vocab, (10, T), generator=gen(31))
+    Y = torch.randint(0, vocab, (10, T), generator=gen(32))
+
+    def run(overlap):
+        torch.manual_seed(30)
+        model = Net().to(gpu).bfloat16()
+        opt = torch.optim.SGD(model.parameters(), lr=1e-2)
+        eng = GradDotProdEngine(model, val_batch_size=2, use_dummy_bias=False,
+                                precision="reference", overlap=overlap)
+        eng.attach(opt)
+        for step in range(3):
+            eng.attach_train_batch(X[:8], Y[:8], step, 0)
+            model(X.to(gpu), Y.to(gpu)).backward()
+            eng.prepare_gradients()
+            opt.step()
+            eng.aggregate_and_log()
+            eng.clear_gradients()
+        eng.detach()
+        dots = torch.stack([r["dot_product"] for r in eng.dot_product_log])
+        return dots, [p.detach().float().cpu() for p in model.parameters()]
+
+    d_on, w_on = run(True)
+    d_off, w_off = run(False)
+    print(f"overlap dots {d_on[-1, :3].tolist()}", flush=True)
+    assert torch.isfinite(d_on).all()
+    assert torch.equal(d_on, d_off)
+    for a, b in zip(w_on, w_off):
+        assert torch.equal(a, b)

@@ -273,6 +273,13 @@ constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
 #ifndef GS_SCHED
 #define GS_SCHED 1
 #endif
+#ifndef GS_GROUP
+#define GS_GROUP 8
+#endif
+// Stage geometry of the DMA GEMMs whose tiles are too large for three 128-byte stages.
+#ifndef GS_WIDE_DMA
+#define GS_WIDE_DMA 128, 2
+#endif
 #ifndef GS_PF
 #define GS_PF 1
 #endif
@@ -481,7 +488,7 @@ __device__ __forceinline__ void mainloop_dma(const Operand& L, const Operand& R,
 // workgroups resident on an XCD share operand tiles in its L2.
 __device__ __forceinline__ void tile_of_block(int64_t m_tiles, int64_t n_tiles, int64_t& mt,
                                               int64_t& nt) {
-  constexpr int64_t GROUP = 8, XCDS = 8;
+  constexpr int64_t GROUP = GS_GROUP, XCDS = 8;
   const int64_t nb = static_cast<int64_t>(gridDim.x);
   const int64_t bid = blockIdx.x;
   int64_t lid = bid;
@@ -699,25 +706,27 @@ __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
-  mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
   uint32_t ga[C::MI][C::NI][8];  // bf16 pairs (even element in the low half)
+  auto pack = [&](f32x16_t (&a)[C::MI][C::NI]) {
 #pragma unroll
-  for (int i = 0; i < C::MI; ++i)
+    for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-    for (int j = 0; j < C::NI; ++j)
+      for (int j = 0; j < C::NI; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        ga[i][j][e] = pack_bf16x2(acc[i][j][2 * e], acc[i][j][2 * e + 1]);
-  // Materialise the packed tile here, so the first accumulators die before the second
-  // GEMM's accumulators come alive (otherwise both sets compete for the AGPRs).
+        for (int e = 0; e < 8; ++e) ga[i][j][e] = pack_bf16x2(a[i][j][2 * e], a[i][j][2 * e + 1]);
+    // Materialise the packed tile here, so the first accumulators die before the second
+    // GEMM's accumulators come alive (otherwise both sets compete for the AGPRs).
 #pragma unroll
-  for (int i = 0; i < C::MI; ++i)
+    for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-    for (int j = 0; j < C::NI; ++j)
+      for (int j = 0; j < C::NI; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(ga[i][j][e]));
-  asm volatile("" ::: "memory");
-  zero_acc<TrBF16, C>(acc);
+        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(ga[i][j][e]));
+    asm volatile("" ::: "memory");
+    zero_acc<TrBF16, C>(a);
+  };
+  mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
+  pack(acc);
   mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc);
   float colsum[C::NI];
   auto hadamard = [&](auto ref) {
@@ -863,7 +872,7 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 #define GS_STORE_TILE 2, 2, 1, 1
 #endif
 // bf16 GHOST through ghost_stash_kernel: 256x256 tiles, 8 waves of 128x64 (2x4 waves),
-// 64-byte stage rows, 4 stages (128 KiB of LDS).
+// 128-byte stage rows, 2 stages (128 KiB of LDS).
 #ifndef GS_GHOST_STASH
 #define GS_GHOST_STASH 1
 #endif
@@ -871,7 +880,7 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 #define GS_STASH_TILE 2, 4, 4, 2
 #endif
 #ifndef GS_STASH_DMA
-#define GS_STASH_DMA 64, 4
+#define GS_STASH_DMA 128, 2
 #endif
 // fp32 operands (precision checks, fp32 models) keep the small 128 x 128 tile.
 template <class Tr, int... Tile>
@@ -892,12 +901,15 @@ namespace {
 #define GS_USE_DMA 1
 #endif
 // Stage geometry of gemm_dma_kernel: three 128-byte-row stages when they fit in LDS,
-// else four 64-byte-row stages.
+// else GS_WIDE_DMA.
 template <class C>
 using DmaFor = std::conditional_t<3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
-                                  DmaCfg<C, 64, 4>>;
+                                  DmaCfg<C, GS_WIDE_DMA>>;
 #ifndef GS_ROWDOT_DMA
 #define GS_ROWDOT_DMA 1
+#endif
+#ifndef GS_STORE_DMA
+#define GS_STORE_DMA 1
 #endif
 
 bool dma_ok(const Operand& o) { return o.vec_ok && o.nbytes > 0 && o.nbytes < INT32_MAX; }
@@ -911,9 +923,11 @@ struct Launch {
     if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
     using D = DmaFor<C>;
-    if constexpr (std::is_same<Tr, TrBF16>::value && EPI != EPI_STORE &&
+    if constexpr (std::is_same<Tr, TrBF16>::value &&
                   D::STAGES * D::STAGE_BYTES <= 160 * 1024) {
-      const bool dma = GS_USE_DMA && (EPI == EPI_GHOST || GS_ROWDOT_DMA) && aligned &&
+      const bool on = EPI == EPI_GHOST || (EPI == EPI_ROWDOT && GS_ROWDOT_DMA) ||
+                      (EPI == EPI_STORE && GS_STORE_DMA);
+      const bool dma = GS_USE_DMA && on && aligned &&
                        dma_ok(p.L1) && dma_ok(p.R1) &&
                        (EPI != EPI_GHOST || (dma_ok(p.L2) && dma_ok(p.R2)));
       if (dma) {
@@ -1025,7 +1039,8 @@ template <class S>
 void carve_linear(S& c, const LinearPlan& pl, int dtype, int64_t N, int64_t n_val, int64_t T,
                   int64_t d_in, int64_t d_out, int semantics) {
   const size_t esz = elem_size(dtype);
-  const int64_t n_t = N - n_val;
+  (void)N;
+  (void)n_val;
   if (pl.algo == GS_ALGO_GHOST) {
     if (semantics == GS_SEM_PRESUM) {
       c.template take<char>(T * d_in * esz);

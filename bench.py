@@ -411,6 +411,7 @@ KERNEL_SHAPES = {
     "layernorm": "layernorm_dot + grads, X,G[20,1024,768] bf16, 4 val",
     "embedding_wte": "embedding_dot, ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
     "kron_fc": "kron_proj, A[32,1024,1024] G[32,1024,4096] bf16, k=16x16",
+    "kron_embed_wte": "kron_embed_proj, ids[32,1024] vocab 50257, G[32,1024,1024] bf16, k=16x16",
     "copy_1GiB": "device copy of 1 GiB (HBM calibration)",
 }
 
@@ -458,7 +459,12 @@ def kernels_leg(dev, reps: int = 10):
     Pi = rnd(16, 1024, s=0.25)
     Po = rnd(16, 4096, s=0.25)
     out["kron_fc"] = timeit(lambda: ops.kron_proj(Ak, Gk, Pi, Po, 32.0))
-    del Ak, Gk
+    del Gk
+    idk = torch.randint(0, 50257, (32, 1024), generator=g).to(dev)
+    PiT = rnd(50257, 16, s=0.25)
+    Poe = rnd(16, 1024, s=0.25)
+    out["kron_embed_wte"] = timeit(lambda: ops.kron_embed_proj(idk, Ak, PiT, Poe, 1.0))
+    del Ak, idk, PiT
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
     dst = torch.empty_like(src)
     out["copy_1GiB"] = timeit(lambda: dst.copy_(src))
@@ -470,7 +476,8 @@ def kernels_leg(dev, reps: int = 10):
 # FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --mode kernels`)
 TRAFFIC_KEYS = {"linear_valgrad[768x3072]": "valgrad_fc", "bias_dot": "bias_fc",
                 "layernorm_dot": "layernorm", "embedding_dot": "embedding_wte",
-                "kron_proj": "kron_fc", "ghost": "ghost_microbench"}
+                "kron_proj": "kron_fc", "kron_embed_proj": "kron_embed_wte",
+                "ghost": "ghost_microbench"}
 
 
 def measured_traffic(op_name):

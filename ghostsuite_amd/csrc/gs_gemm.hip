@@ -765,11 +765,21 @@ __global__ void reduce_partials_kernel(const float* __restrict__ P, int64_t grou
   const int64_t i = blockIdx.x;
   float dot = 0.f;
   for (int64_t g = 0; g < groups; ++g) {
-    float s = 0.f;
-    for (int64_t r = 0; r < rows_per_group; ++r) {
-      const float* row = P + (g * rows_per_group + r) * p_ld + i * cols;
-      for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s += row[c];
+    // Four independent partial sums keep several loads in flight per thread.
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    int64_t r = 0;
+    for (; r + 4 <= rows_per_group; r += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float* row = P + (g * rows_per_group + r + u) * p_ld + i * cols;
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s4[u] += row[c];
+      }
     }
+    for (; r < rows_per_group; ++r) {
+      const float* row = P + (g * rows_per_group + r) * p_ld + i * cols;
+      for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s4[0] += row[c];
+    }
+    float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
     s = block_sum(s, red);
     if (out_pair != nullptr && threadIdx.x == 0) out_pair[g * n_train + i] = s;
     dot += s;
@@ -1021,7 +1031,8 @@ LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_
     pl.vcols = nv_eff * T;
     bn = RowdotCfg<Tr>::BN;
   }
-  // GHOST keeps per-token partials: its two bf16 kernels differ in BN.
+  // GHOST sizes the per-token layout (its two bf16 kernels differ in BN; run_linear picks
+  // the per-tile layout when the kernel that runs allows it).
   pl.tile_reduce = (pl.algo != GS_ALGO_GHOST && T % bn == 0) ? 1 : 0;
   pl.p_ld = pl.tile_reduce ? n_t * T / bn : n_t * T;
   pl.cols = pl.tile_reduce ? T / bn : T;
@@ -1102,8 +1113,6 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     }
     float* P = cv.take<float>(pl.p_rows * pl.p_ld);
     GemmParams p{};
-    p.p_ld = pl.p_ld;
-    p.tile_reduce = pl.tile_reduce;
     p.rounding = rounding;
     p.L1 = make_operand(La, d_in, lmap, pl.ghost_flat ? 0 : 1, d_in, esz, la_bytes);
     p.R1 = make_operand(A, d_in, tr, 0, d_in, esz, a_bytes);
@@ -1117,24 +1126,30 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     p.p_row0 = 0;
     if (p.m_tiles != pl.p_rows) return fail(GS_ERR_INVALID, "internal: ghost partial rows");
     const bool al = p.L1.vec_ok && p.R1.vec_ok && p.L2.vec_ok && p.R2.vec_ok;
+    bool stash = false;
+    if constexpr (std::is_same<Tr, TrBF16>::value)
+      stash = GS_GHOST_STASH && al && dma_ok(p.L1) && dma_ok(p.R1) && dma_ok(p.L2) &&
+              dma_ok(p.R2);
+    // Partials: one per (M tile, N tile) when N tiles never straddle samples, else one per
+    // (M tile, train token); the workspace holds the larger layout.
+    const int64_t bn = stash ? static_cast<int64_t>(StashCfg::BN) : static_cast<int64_t>(GC::BN);
+    p.tile_reduce = T % bn == 0 ? 1 : 0;
+    p.p_ld = p.tile_reduce ? n_t * T / bn : n_t * T;
+    const int64_t cols = p.tile_reduce ? T / bn : T;
     int rc = GS_OK;
-    bool done = false;
-    if constexpr (std::is_same<Tr, TrBF16>::value) {
-      if (GS_GHOST_STASH && al && dma_ok(p.L1) && dma_ok(p.R1) && dma_ok(p.L2) &&
-          dma_ok(p.R2)) {
-        p.n_tiles = host_tiles<StashCfg::BN>(p.R1);
-        const int64_t blocks = p.m_tiles * p.n_tiles;
-        if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-        hipLaunchKernelGGL((ghost_stash_kernel<StashCfg, StashDma>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(StashCfg::NT), 0, s, p);
-        rc = check_launch("ghost_stash_kernel");
-        done = true;
-      }
+    if (stash) {
+      p.n_tiles = host_tiles<StashCfg::BN>(p.R1);
+      const int64_t blocks = p.m_tiles * p.n_tiles;
+      if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
+      hipLaunchKernelGGL((ghost_stash_kernel<StashCfg, StashDma>),
+                         dim3(static_cast<unsigned>(blocks)), dim3(StashCfg::NT), 0, s, p);
+      rc = check_launch("ghost_stash_kernel");
+    } else {
+      rc = Launch<Tr, GC>::template run<EPI_GHOST>(p, al, s);
     }
-    if (!done) rc = Launch<Tr, GC>::template run<EPI_GHOST>(p, al, s);
     if (rc) return rc;
     hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s,
-                       P, pl.groups, pl.p_rows / pl.groups, pl.p_ld, pl.cols, n_t, out_pair,
+                       P, pl.groups, pl.p_rows / pl.groups, p.p_ld, cols, n_t, out_pair,
                        out_dot);
     return check_launch("reduce_partials_kernel");
   }

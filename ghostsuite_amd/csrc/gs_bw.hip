@@ -14,7 +14,8 @@
 namespace gs {
 
 constexpr int BW_THREADS = 256;
-constexpr int TOK_CHUNK = 32;  // tokens per stage-1 block
+constexpr int TOK_CHUNK = 32;     // tokens per stage-1 block (bias, embedding)
+constexpr int LN_TOK_CHUNK = 64;  // tokens per LayerNorm stage-1 block (8 per wave)
 
 template <class E>
 __device__ __forceinline__ float ld(const E* p) {
@@ -82,33 +83,39 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
   extern __shared__ float sm[];  // [LN_WAVES/2][F] for w, then the same for b
   const int64_t n = blockIdx.y, c = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
+  const int64_t t0 = c * LN_TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + LN_TOK_CHUNK);
   float aw[PC][VE], ab[PC][VE];
 #pragma unroll
   for (int k = 0; k < PC; ++k)
 #pragma unroll
     for (int i = 0; i < VE; ++i) aw[k][i] = ab[k][i] = 0.f;
   const float invF = 1.0f / static_cast<float>(F);
-  for (int64_t t = t0 + wid; t < t1; t += LN_WAVES) {
+  // The next token's rows are loaded while the current one is reduced.
+  Vec<E> xv[PC], gv[PC], xn[PC], gn[PC];
+  auto load_row = [&](int64_t t, Vec<E> (&xd)[PC], Vec<E> (&gd)[PC]) {
     const E* xr = X + (n * T + t) * F;
     const E* gr = G + (n * T + t) * F;
-    Vec<E> xv[PC], gv[PC];
-    float s = 0.f;
 #pragma unroll
     for (int k = 0; k < PC; ++k) {
       const int64_t f = (lane + 64 * k) * VE;
-      const bool in = f < F;
       const bool full = vec && f + VE <= F;
-      if (in) {
-        xv[k].load(xr + f, full, F - f);
-        gv[k].load(gr + f, full, F - f);
+      if (f < F) {
+        xd[k].load(xr + f, full, F - f);
+        gd[k].load(gr + f, full, F - f);
       } else {
 #pragma unroll
-        for (int i = 0; i < VE; ++i) xv[k].v[i] = gv[k].v[i] = 0.f;
+        for (int i = 0; i < VE; ++i) xd[k].v[i] = gd[k].v[i] = 0.f;
       }
+    }
+  };
+  if (t0 + wid < t1) load_row(t0 + wid, xv, gv);
+  for (int64_t t = t0 + wid; t < t1; t += LN_WAVES) {
+    if (t + LN_WAVES < t1) load_row(t + LN_WAVES, xn, gn);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PC; ++k)
 #pragma unroll
       for (int i = 0; i < VE; ++i) s += xv[k].v[i];
-    }
     const float mean = wave_sum(s) * invF;
     float var = 0.f;
 #pragma unroll
@@ -128,6 +135,11 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
         aw[k][i] += gv[k].v[i] * ((xv[k].v[i] - mean) * rstd);
         ab[k][i] += gv[k].v[i];
       }
+#pragma unroll
+    for (int k = 0; k < PC; ++k) {
+      xv[k] = xn[k];
+      gv[k] = gn[k];
+    }
   }
   // Two-step combine through [LN_WAVES/2][F] (x2) floats of LDS: the upper half of the
   // waves parks its sums, the lower half adds its own, then the rows are summed.
@@ -171,54 +183,80 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
 }
 
 // ---------------------------------------------------------------- stage 2/3 (shared)
-// S[n][f] = sum_c part[n][c][f]   (grid: feature blocks x samples)
-__global__ void __launch_bounds__(256) feature_sample_totals_kernel(
-    const float* __restrict__ part, int64_t chunks, int64_t F, float* __restrict__ S) {
-  const int64_t f = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t n = blockIdx.y;
-  if (f >= F) return;
-  const float* src = part + n * chunks * F + f;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  int64_t c = 0;
-  for (; c + 4 <= chunks; c += 4) {
-    s0 += src[c * F];
-    s1 += src[(c + 1) * F];
-    s2 += src[(c + 2) * F];
-    s3 += src[(c + 3) * F];
+// One or two feature sets (bias: g; LayerNorm: g*xhat and g) share each launch; blockIdx.z
+// (totals) / blockIdx.y (finish) selects the set.
+struct FeatureSet {
+  const float* part;  // [N][chunks][F] stage-1 partials
+  float* S;           // [N][F] per-sample totals
+  float* sval;        // [F] val aggregate
+  void* grad;         // [F] train gradient (bf16 or fp32) or null
+  float* out_dot;     // [n_train] or null
+};
+struct FeatureSets {
+  FeatureSet set[2];
+};
+
+// Rows y < N: S[y][f] = sum_c part[y][c][f].  Row y == N: sval[f] = the same sum over the val
+// rows (straight from the partials, so the finish kernel reads two vectors per dot).  A
+// block covers 64 features; its 4 waves take every 4th chunk and combine through LDS in a
+// fixed order.
+constexpr int TOT_F = 64, TOT_G = 4;
+__global__ void __launch_bounds__(TOT_F * TOT_G) feature_sample_totals_kernel(
+    FeatureSets sets, int64_t chunks, int64_t F, int64_t N, int64_t n_val, int64_t val_start) {
+  __shared__ float red[TOT_G][TOT_F];
+  const FeatureSet& fs = sets.set[blockIdx.z];
+  const int fi = threadIdx.x % TOT_F, cg = threadIdx.x / TOT_F;
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * TOT_F + fi;
+  const int64_t y = blockIdx.y;
+  const int64_t r0 = y < N ? y : val_start, nr = y < N ? 1 : n_val;
+  float s0 = 0.f, s1 = 0.f;
+  if (f < F) {
+    for (int64_t r = r0; r < r0 + nr; ++r) {
+      const float* src = fs.part + r * chunks * F + f;
+      int64_t c = cg;
+      for (; c + TOT_G < chunks; c += 2 * TOT_G) {
+        s0 += src[c * F];
+        s1 += src[(c + TOT_G) * F];
+      }
+      if (c < chunks) s0 += src[c * F];
+    }
   }
-  for (; c < chunks; ++c) s0 += src[c * F];
-  S[n * F + f] = (s0 + s1) + (s2 + s3);
+  red[cg][fi] = s0 + s1;
+  __syncthreads();
+  if (cg != 0 || f >= F) return;
+  const float t = (red[0][fi] + red[1][fi]) + (red[2][fi] + red[3][fi]);
+  if (y < N)
+    fs.S[y * F + f] = t;
+  else
+    fs.sval[f] = t;
 }
 
-// Blocks [0, n_train): dot_i = <S_i, sum over val rows of S>, the val aggregate formed on the
-// fly.  Blocks [n_train, ...): grad[f] = scale * sum over train rows of S[.][f].
+// Blocks x < n_train: dot_x = <S_x, sval>.  Blocks x >= n_train: grad[f] = scale * sum over
+// train rows of S[.][f].
 template <class GE>
 __global__ void __launch_bounds__(BW_THREADS) feature_finish_kernel(
-    const float* __restrict__ S, int64_t N, int64_t F, int64_t n_val, int64_t val_start,
-    RowMap train, float* __restrict__ out_dot, GE* __restrict__ grad, float grad_scale) {
+    FeatureSets sets, int64_t N, int64_t F, int64_t n_val, int64_t val_start, RowMap train,
+    float grad_scale) {
   __shared__ float red[BW_THREADS / 64];
+  const FeatureSet& fs = sets.set[blockIdx.y];
   const int64_t n_train = N - n_val;
   const int64_t b = blockIdx.x;
   if (b < n_train) {
-    if (out_dot == nullptr) return;
-    const float* row = S + train.phys_sample(b) * F;
+    if (fs.out_dot == nullptr) return;
+    const float* row = fs.S + train.phys_sample(b) * F;
     float s = 0.f;
-    for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
-      float v = 0.f;
-      for (int64_t j = 0; j < n_val; ++j) v += S[(val_start + j) * F + f];
-      s += row[f] * v;
-    }
+    for (int64_t f = threadIdx.x; f < F; f += blockDim.x) s += row[f] * fs.sval[f];
     s = block_sum(s, red);
-    if (threadIdx.x == 0) out_dot[b] = s;
+    if (threadIdx.x == 0) fs.out_dot[b] = s;
     return;
   }
-  if (grad == nullptr) return;
+  if (fs.grad == nullptr) return;
   const int64_t f = (b - n_train) * blockDim.x + threadIdx.x;
   if (f >= F) return;
   float t = 0.f;
   for (int64_t n = 0; n < N; ++n)
-    if (n < val_start || n >= val_start + n_val) t += S[n * F + f];
-  grad[f] = from_f32<GE>(grad_scale * t);
+    if (n < val_start || n >= val_start + n_val) t += fs.S[n * F + f];
+  static_cast<GE*>(fs.grad)[f] = from_f32<GE>(grad_scale * t);
 }
 
 // ---------------------------------------------------------------- embedding
@@ -347,7 +385,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 template <class S>
 void carve_feature(S& c, int64_t N, int64_t T, int64_t F, int two) {
-  const int64_t chunks = cdiv(T, TOK_CHUNK);
+  const int64_t chunks = cdiv(T, two ? LN_TOK_CHUNK : TOK_CHUNK);
   c.template take<float>(N * chunks * F);  // part w (or bias)
   if (two) c.template take<float>(N * chunks * F);
   c.template take<float>(N * F);  // S
@@ -357,30 +395,31 @@ void carve_feature(S& c, int64_t N, int64_t T, int64_t F, int two) {
 }
 
 template <class GE>
-int finish_feature(const float* part, int64_t N, int64_t chunks, int64_t F, int64_t n_val,
-                   int64_t val_start, int64_t T, float* S, float* sval, void* grad,
-                   float grad_scale, float* out_dot, hipStream_t s) {
-  (void)sval;
+int finish_feature(const FeatureSets& sets, int nsets, int64_t N, int64_t chunks, int64_t F,
+                   int64_t n_val, int64_t val_start, int64_t T, float grad_scale,
+                   hipStream_t s) {
   hipLaunchKernelGGL(feature_sample_totals_kernel,
-                     dim3(static_cast<unsigned>(cdiv(F, 256)), static_cast<unsigned>(N)),
-                     dim3(256), 0, s, part, chunks, F, S);
+                     dim3(static_cast<unsigned>(cdiv(F, TOT_F)), static_cast<unsigned>(N + 1),
+                          static_cast<unsigned>(nsets)),
+                     dim3(TOT_F * TOT_G), 0, s, sets, chunks, F, N, n_val, val_start);
   const int64_t n_t = N - n_val;
-  const int64_t blocks = n_t + (grad != nullptr ? cdiv(F, BW_THREADS) : 0);
-  hipLaunchKernelGGL(feature_finish_kernel<GE>, dim3(static_cast<unsigned>(blocks)),
-                     dim3(BW_THREADS), 0, s, S, N, F, n_val, val_start,
-                     train_rows(N, n_val, val_start, T), out_dot, static_cast<GE*>(grad),
-                     grad_scale);
+  bool any_grad = false;
+  for (int k = 0; k < nsets; ++k) any_grad = any_grad || sets.set[k].grad != nullptr;
+  const int64_t blocks = n_t + (any_grad ? cdiv(F, BW_THREADS) : 0);
+  hipLaunchKernelGGL(feature_finish_kernel<GE>,
+                     dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(nsets)),
+                     dim3(BW_THREADS), 0, s, sets, N, F, n_val, val_start,
+                     train_rows(N, n_val, val_start, T), grad_scale);
   return check_launch("feature_totals/finish");
 }
 
-int finish_feature_any(int grad_dtype, const float* part, int64_t N, int64_t chunks, int64_t F,
-                       int64_t n_val, int64_t val_start, int64_t T, float* S, float* sval,
-                       void* grad, float grad_scale, float* out_dot, hipStream_t s) {
+int finish_feature_any(int grad_dtype, const FeatureSets& sets, int nsets, int64_t N,
+                       int64_t chunks, int64_t F, int64_t n_val, int64_t val_start, int64_t T,
+                       float grad_scale, hipStream_t s) {
   if (grad_dtype == GS_DTYPE_F32)
-    return finish_feature<float>(part, N, chunks, F, n_val, val_start, T, S, sval, grad,
-                                 grad_scale, out_dot, s);
-  return finish_feature<uint16_t>(part, N, chunks, F, n_val, val_start, T, S, sval, grad,
-                                  grad_scale, out_dot, s);
+    return finish_feature<float>(sets, nsets, N, chunks, F, n_val, val_start, T, grad_scale, s);
+  return finish_feature<uint16_t>(sets, nsets, N, chunks, F, n_val, val_start, T, grad_scale,
+                                  s);
 }
 
 bool batch_ok(int64_t N, int64_t n_val, int64_t val_start, int64_t T, int64_t F) {
@@ -411,10 +450,14 @@ int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F,
     launch_ln<E, 2>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
   else if (pc <= 4)
     launch_ln<E, 4>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
-  else if (pc <= 8 && VE == 4)
-    launch_ln<E, 8>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
-  else
+  else if constexpr (VE == 4) {
+    if (pc <= 8)
+      launch_ln<E, 8>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
+    else
+      return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: feature count too large");
+  } else {
     return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: feature count too large");
+  }
   return check_launch("ln_sums_kernel");
 }
 
@@ -462,8 +505,10 @@ extern "C" int gs_bias_dot(const void* G, int dtype, int64_t N, int64_t n_val, i
                        static_cast<const float*>(G), T, d_out, chunks, vec, part);
   int rc = check_launch("colsum_kernel");
   if (rc) return rc;
-  return finish_feature_any(grad_dtype, part, N, chunks, d_out, n_val, val_start, T, S, sval,
-                            out_grad, grad_scale, out_dot, s);
+  FeatureSets sets{};
+  sets.set[0] = FeatureSet{part, S, sval, out_grad, out_dot};
+  return finish_feature_any(grad_dtype, sets, 1, N, chunks, d_out, n_val, val_start, T,
+                            grad_scale, s);
 }
 
 // ------------------------------------------------------------------------------ layernorm
@@ -491,7 +536,7 @@ extern "C" int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t
   if (workspace == nullptr || workspace_bytes < sz.used)
     return fail(GS_ERR_WORKSPACE, "gs_layernorm_dot: workspace too small");
   Carver cv(workspace, workspace_bytes);
-  const int64_t chunks = cdiv(T, TOK_CHUNK);
+  const int64_t chunks = cdiv(T, LN_TOK_CHUNK);
   float* pw = cv.take<float>(N * chunks * F);
   float* pb = cv.take<float>(N * chunks * F);
   float* Sw = cv.take<float>(N * F);
@@ -503,13 +548,12 @@ extern "C" int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t
                ? launch_ln_any<uint16_t>(X, G, N, T, F, eps, chunks, pw, pb, s)
                : launch_ln_any<float>(X, G, N, T, F, eps, chunks, pw, pb, s);
   if (rc) return rc;
-  rc = finish_feature_any(grad_dtype, pw, N, chunks, F, n_val, val_start, T, Sw, vw, out_grad_w,
-                          grad_scale, out_dot_w, s);
-  if (rc) return rc;
-  if (out_dot_b != nullptr || out_grad_b != nullptr)
-    rc = finish_feature_any(grad_dtype, pb, N, chunks, F, n_val, val_start, T, Sb, vb,
-                            out_grad_b, grad_scale, out_dot_b, s);
-  return rc;
+  FeatureSets sets{};
+  sets.set[0] = FeatureSet{pw, Sw, vw, out_grad_w, out_dot_w};
+  sets.set[1] = FeatureSet{pb, Sb, vb, out_grad_b, out_dot_b};
+  const int nsets = (out_dot_b != nullptr || out_grad_b != nullptr) ? 2 : 1;
+  return finish_feature_any(grad_dtype, sets, nsets, N, chunks, F, n_val, val_start, T,
+                            grad_scale, s);
 }
 
 // ------------------------------------------------------------------------------ embedding

@@ -14,7 +14,7 @@ import torch.nn as nn
 
 from .projection_utils import (choose_ki_ko, compute_projection_metadata,
                                get_projection_initializer)
-from .. import _overlap
+from .. import _overlap, async_io
 from .autograd_gradproj import create_projection_hooks
 from .supported_layers_gradproj import (compute_total_projection_size, find_matching_layers,
                                         get_layer_dimensions, get_layer_slice_ranges,
@@ -134,6 +134,7 @@ class GradProjLoraEngine:
                     delattr(layer, attr)
         self.hooks.clear()
         self.is_attached = False
+        async_io.writer.flush()   # projection files submitted so far are on disk
         print(f"Detached projection hooks from {len(self.matched_layers)} layers")
 
     def collect_batch(self, batch_indices: Optional[List[int]] = None) -> torch.Tensor:
@@ -167,12 +168,15 @@ class GradProjLoraEngine:
             with open(metadata_path, 'w') as f:
                 json.dump(self.metadata, f, indent=2)
             print(f"Saved metadata to {metadata_path}")
-        save_dict = {'proj': projection.cpu(), 'iter': self.iteration,
-                     'batch_size': projection.shape[0]}
+        # The host copy and the file write leave the step's critical path: pinned copy on a
+        # copy stream, torch.save on the writer thread once the copy is done.
+        events = []
+        save_dict = {'proj': async_io.tree_to_host_async(projection, events),
+                     'iter': self.iteration, 'batch_size': projection.shape[0]}
         if batch_indices is not None:
             save_dict['batch_idx'] = batch_indices
         save_path = self.proj_dir / f'proj_iter_{self.iteration:06d}.pt'
-        torch.save(save_dict, save_path)
+        async_io.writer.submit(save_dict, save_path, events)
         print(f"Saved projection [{projection.shape}] to {save_path}")
 
     def get_projection_metadata(self) -> dict:
@@ -214,7 +218,8 @@ class GradProjLoraEngine:
         self.projection_matrices.clear()
 
     def save_projections(self, iter_num: int):
-        pass
+        """Projections are saved by ``collect_batch``; this waits until they are on disk."""
+        async_io.writer.flush()
 
     def __repr__(self):
         return (f"GradProjLoraEngine(layers={len(self.matched_layers)}, "

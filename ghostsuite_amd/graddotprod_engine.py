@@ -17,6 +17,7 @@ import torch
 from torch import nn
 
 from . import _overlap
+from . import async_io
 from . import autograd_grad_sample_dotprod
 from . import transformers_support
 from . import supported_layers_grad_samplers_dotprod as _samplers
@@ -41,7 +42,8 @@ class GradDotProdEngine:
         self.dot_prod_save_path = dot_prod_save_path
         self.named_params = list((n, p) for (n, p) in module.named_parameters() if p.requires_grad)
         self._grad_creation_locked = False
-        self.dot_product_log = []
+        # Records are appended with their device->host copies in flight; reads wait for them.
+        self.dot_product_log = async_io.PendingLog()
         self.batch_idx_lst = []
 
         # Dummy-bias trick (reference :64-73): remember trainability, then let autograd skip
@@ -133,13 +135,16 @@ class GradDotProdEngine:
             if hasattr(param, 'grad_dot_prod_pair'):
                 delattr(param, 'grad_dot_prod_pair')
         if total is not None:
-            self.dot_product_log.append({
-                'dot_product': to_device(total, 'cpu'),
-                'X_train': to_device(self.X_train, 'cpu'),
-                'Y_train': to_device(self.Y_train, 'cpu'),
+            # Same record as the reference, but the host copies are asynchronous (pinned
+            # memory, copy stream): the step does not wait for the GPU here.
+            events = []
+            self.dot_product_log.append_pending({
+                'dot_product': async_io.tree_to_host_async(total, events),
+                'X_train': async_io.tree_to_host_async(self.X_train, events),
+                'Y_train': async_io.tree_to_host_async(self.Y_train, events),
                 'iter_num': self.iter_num,
                 'batch_idx': self.batch_idx,
-            })
+            }, events)
         else:
             warnings.warn("No gradient dot products computed for this iteration.")
 
@@ -149,7 +154,7 @@ class GradDotProdEngine:
             raise ValueError("No gradient dot products found to save for this iteration.")
         print(f"[INFO] Saving dot product log at iteration {iter_num} ...")
         file_path = os.path.join(self.dot_prod_save_path, f"dot_prod_log_iter_{iter_num}.pt")
-        torch.save(self.dot_product_log, file_path)
+        torch.save(self.dot_product_log.plain(), file_path)   # a plain list, as the reference
         self.dot_product_log.clear()
 
     def attach_and_store_valset(self, X_val, Y_val):

@@ -243,3 +243,56 @@ def test_side_stream_overlap_gives_identical_results(gpu):
     assert torch.equal(d_on, d_off)
     for a, b in zip(w_on, w_off):
         assert torch.equal(a, b)
+
+
+def test_async_host_copies_and_files_match_device_results(gpu, tmp_path):
+    """The dot log's host copies and the projection files are written off the critical
+    path; what a reader sees equals the device results, and the saved files are the
+    reference's plain formats (loadable with weights_only=True)."""
+    torch.manual_seed(40)
+    model = MLP((32, 64, 10)).to(gpu)
+    X = torch.randn(12, 32, generator=gen(41)).to(gpu)
+    Y = torch.randint(0, 10, (12,), generator=gen(42)).to(gpu)
+    eng = GradDotProdEngine(model, val_batch_size=4, precision="fp32",
+                            dot_prod_save_path=str(tmp_path))
+    eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+    device_totals = []
+    for step in range(3):
+        eng.attach_train_batch(X[:8], Y[:8], step, step)
+        F.cross_entropy(model(X), Y).backward()
+        dots = [p.grad_dot_prod.clone() for _, p in model.named_parameters()
+                if hasattr(p, "grad_dot_prod")]
+        device_totals.append(sum(dots).cpu())
+        eng.prepare_gradients()
+        eng.aggregate_and_log()
+        eng.clear_gradients()
+    assert len(eng.dot_product_log) == 3
+    for rec, want in zip(eng.dot_product_log, device_totals):
+        assert rec["dot_product"].device.type == "cpu"
+        assert_close(rec["dot_product"], want, 1e-6, "async log")
+        assert torch.equal(rec["X_train"], X[:8].cpu())
+    eng.save_dot_product_log(iter_num=7)
+    saved = torch.load(tmp_path / "dot_prod_log_iter_7.pt", weights_only=True)
+    assert type(saved) is list and len(saved) == 3
+    assert set(saved[0]) == {"dot_product", "X_train", "Y_train", "iter_num", "batch_idx"}
+    assert saved[2]["iter_num"] == 2 and saved[2]["dot_product"].dtype == torch.float32
+    eng.detach()
+
+    proj_dir = tmp_path / "proj"
+    net = nn.Sequential(nn.Linear(16, 24), nn.ReLU(), nn.Linear(24, 8)).to(gpu)
+    Xp = torch.randn(6, 16, generator=gen(43)).to(gpu)
+    peng = GradProjLoraEngine(net, proj_layers="0,2", proj_rank_total=16, proj_rank_min=2,
+                              proj_seed=3, proj_dtype="float16", proj_dir=str(proj_dir))
+    peng.attach()
+    outs = []
+    for it in range(2):
+        net.zero_grad()
+        net(Xp).square().mean().backward()
+        outs.append(peng.collect_batch(batch_indices=list(range(6))).cpu())
+    peng.detach()   # waits for the writer
+    for it, want in enumerate(outs):
+        d = torch.load(proj_dir / f"proj_iter_{it:06d}.pt", weights_only=True)
+        assert set(d) == {"proj", "iter", "batch_size", "batch_idx"}
+        assert d["proj"].dtype == torch.float16 and d["iter"] == it and d["batch_size"] == 6
+        assert torch.equal(d["proj"], want)
+    assert (proj_dir / "metadata.json").exists()

@@ -20,6 +20,7 @@ import torch.nn as nn
 
 from . import _overlap
 from .supported_layers_grad_samplers_dotprod import (
+    APPLIED,
     _supported_layers_dotprod,
     _create_or_accumulate_train_grad,
     options,
@@ -142,7 +143,9 @@ def _apply_train_grad(layer: nn.Module, val_batch_size: int, loss_reduction: str
             if hasattr(layer, 'weight') and layer.weight.initially_requires_grad:
                 grad_weight = compute_layer_train_grad(layer, layer.activations, layer.backprops,
                                                        val_batch_size, scale=scale)
-                if grad_weight is not None:
+                if grad_weight is APPLIED:
+                    pass   # the sampler added into param.train_grad itself
+                elif grad_weight is not None:
                     _create_or_accumulate_train_grad(layer.weight, grad_weight)
                 else:
                     raise ValueError(

@@ -21,6 +21,7 @@ import math
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from . import _native, _overlap
@@ -207,15 +208,29 @@ def _compute_embedding_dot_product(layer: nn.Embedding, A: torch.Tensor, B: torc
                                                      vocab=layer.weight.shape[0])
 
 
+# Returned by a train-grad sampler that has already added its gradient into
+# ``param.train_grad`` itself.
+APPLIED = object()
+
+
 def _compute_embedding_train_grad(layer: nn.Embedding, A: torch.Tensor, B: torch.Tensor,
                                   val_batch_size: int, scale: float = 1.0):
-    """scale * index_add of the train rows / n_train (reference :214-235)."""
+    """scale * index_add of the train rows / n_train (reference :214-235).  When the weight
+    already holds a train gradient (a tied lm_head's, computed earlier in backward) the rows
+    are added into it directly, which saves the reference's [vocab, d] zero-fill and the
+    full-table add; returns APPLIED then."""
     n_t = A.size(0) - val_batch_size
     if n_t <= 0:
         return None
+    ids = A[:n_t].long().reshape(-1)
+    rows = B[:n_t].reshape(-1, B.shape[-1])
+    prev = getattr(layer.weight, "train_grad", None)
+    if prev is not None and prev.shape == layer.weight.shape:
+        _overlap.join(prev.device)   # prev may come from the side stream
+        prev.index_add_(0, ids, rows.to(prev.dtype), alpha=scale / n_t)
+        return APPLIED
     grad = torch.zeros_like(layer.weight)
-    grad.index_add_(0, A[:n_t].long().reshape(-1),
-                    B[:n_t].reshape(-1, B.shape[-1]).to(grad.dtype))
+    grad.index_add_(0, ids, rows.to(grad.dtype))
     grad.mul_(scale / n_t)
     return grad
 
@@ -309,10 +324,66 @@ def _compute_Conv1D_train_grad(layer, A: torch.Tensor, B: torch.Tensor, val_batc
     return grad
 
 
+# Conv2d ###################################################################################
+
+def _conv2d_rows(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor, dtype: torch.dtype):
+    """im2col as token-major rows: A -> [N, L, C_in*kh*kw] (the unfold's feature order, which
+    is the order of weight.view(C_out, -1)), B -> [N, L, C_out]; L = output positions."""
+    if layer.groups != 1:
+        raise NotImplementedError("Conv2d with groups > 1 is not supported")
+    if isinstance(layer.padding, str):
+        raise NotImplementedError("Conv2d with string padding is not supported")
+    A_u = F.unfold(A.to(dtype), kernel_size=layer.kernel_size, dilation=layer.dilation,
+                   padding=layer.padding, stride=layer.stride)
+    A_rows = A_u.transpose(1, 2).contiguous()
+    B_rows = B.to(dtype).reshape(B.size(0), B.size(1), -1).transpose(1, 2).contiguous()
+    return A_rows, B_rows
+
+
+def _compute_conv2d_dot_product(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor,
+                                val_batch_size: int) -> None:
+    """Gradient dot-products of an nn.Conv2d (reference :513-560): unfold, then the presum
+    dot of the per-sample weight gradients, dot_i = <sum_l b_il a_il^T, sum_l bbar_l abar_l^T>
+    with abar, bbar the val sums, and the bias dot <sum_l b_il, sum_{j,l} b_jl>.
+
+    Both of the reference's branches aim at this presum quantity; its materialised branch
+    (:552-555) computes it, its ghost branch (:546-550) multiplies [d, d] by [p, p] blocks (it
+    raises unless C_in*kh*kw == C_out).  The switch is still cached on the layer."""
+    A = A.detach()
+    B = B.detach()
+    train_bs = A.size(0) - val_batch_size
+    if train_bs <= 0:
+        raise ValueError("No training samples to compute dot product")
+    dt = torch.float32 if options["precision"] == "fp32" else torch.bfloat16
+    A_rows, B_rows = _conv2d_rows(layer, A, B, dt)
+    # The reference's switch on the unfolded shapes: T = L, 2 L^2 <= weight.numel().
+    _should_use_ghost_computation(layer, A_rows.transpose(1, 2), B_rows.transpose(1, 2),
+                                  conv=True)
+    _linear_like_dot(layer, A_rows, B_rows, val_batch_size, False, dt)
+    if layer.bias is not None:
+        _bias_dot_and_grad(layer, B_rows, val_batch_size, dt)
+
+
+def _compute_conv2d_train_grad(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor,
+                               val_batch_size: int, scale: float = 1.0) -> torch.Tensor:
+    """scale * sum over train rows and positions of b a^T / n_train, viewed as the weight
+    (reference :563-592)."""
+    n_t = A.size(0) - val_batch_size
+    if n_t <= 0:
+        return None
+    dt = A.dtype if A.dtype in (torch.bfloat16, torch.float32) else torch.float32
+    A_rows, B_rows = _conv2d_rows(layer, A[:n_t], B[:n_t], dt)
+    grad = torch.mm(B_rows.reshape(-1, B_rows.shape[-1]).t(),
+                    A_rows.reshape(-1, A_rows.shape[-1]))
+    grad.mul_(scale / n_t)
+    return grad.view_as(layer.weight).to(layer.weight.dtype)
+
+
 _supported_layers_dotprod = {
     nn.Linear: (_compute_linear_dot_product, _compute_linear_train_grad),
     nn.Embedding: (_compute_embedding_dot_product, _compute_embedding_train_grad),
     nn.LayerNorm: (_compute_layernorm_dot_product, _compute_layernorm_train_grad),
+    nn.Conv2d: (_compute_conv2d_dot_product, _compute_conv2d_train_grad),
 }
 if _HFConv1D is not None:
     _supported_layers_dotprod[_HFConv1D] = (_compute_Conv1D_dot_product,

@@ -292,6 +292,40 @@ def conv1d_dot_ref(A: torch.Tensor, B: torch.Tensor, n_val: int, use_ghost: bool
     return w, b
 
 
+def conv2d_dot_ref(A: torch.Tensor, B: torch.Tensor, n_val: int, conv: dict,
+                   has_bias: bool = True):
+    """_compute_conv2d_dot_product, materialised branch (supported_layers_grad_samplers_dotprod.py
+    :513-560): bf16 unfold, per-sample grads einsum('bik,bpk->bpi'), the val presum grad
+    einsum('ik,pk->pi') of the val sums, then their dot; bias <sum_l b_il, sum_{j,l} b_jl>.
+    (The reference's ghost branch multiplies [d,d] by [p,p] blocks and is not restated.)"""
+    Ab, Bb = A.to(BF16), B.to(BF16)
+    n_t = Ab.size(0) - n_val
+    A_tr, A_va = torch.split(Ab, [n_t, n_val], dim=0)
+    B_tr, B_va = torch.split(Bb, [n_t, n_val], dim=0)
+    A_tr_u, A_va_u = F.unfold(A_tr, **conv), F.unfold(A_va, **conv)
+    B_tr_r = B_tr.reshape(n_t, B_tr.size(1), -1)
+    B_va_r = B_va.reshape(n_val, B_va.size(1), -1)
+    g_tr = torch.einsum('bik,bpk->bpi', A_tr_u, B_tr_r)
+    g_va = torch.einsum('ik,pk->pi', A_va_u.sum(dim=0), B_va_r.sum(dim=0))
+    w = torch.einsum('pi,bpi->b', g_va, g_tr)
+    b = None
+    if has_bias:
+        b = torch.einsum('p,bp->b', B_va_r.sum(dim=[0, 2]), B_tr_r.sum(dim=2))
+    return w.float(), None if b is None else b.float()
+
+
+def conv2d_dot_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, conv: dict):
+    """float64 presum dot of the Conv2d weight gradients: G_i = sum_l b_il a_il^T over the
+    unfolded positions, Gbar the same with the val sums of a and b."""
+    A64, B64 = A.double(), B.double()
+    n_t = A64.size(0) - n_val
+    A_u = F.unfold(A64, **conv)                            # [N, d, L]
+    B_r = B64.reshape(B64.size(0), B64.size(1), -1)        # [N, p, L]
+    G = torch.einsum('bdl,bpl->bpd', A_u[:n_t], B_r[:n_t])
+    Gbar = torch.einsum('dl,pl->pd', A_u[n_t:].sum(0), B_r[n_t:].sum(0))
+    return torch.einsum('bpd,pd->b', G, Gbar)
+
+
 # ------------------------------------------------------------------ GradProj
 def flatten_tokens(x: torch.Tensor) -> torch.Tensor:
     """_flatten_tokens (autograd_gradproj.py:11-37): [B, T, D]."""

@@ -21,3 +21,30 @@ def assert_close(x, y, tol, what=""):
     ok, worst = normwise_close(x, y, tol)
     assert ok, f"{what}: worst normwise error {worst:.3e} > {tol:.1e}\n got {x.reshape(-1)[:6]}\n want {y.reshape(-1)[:6]}"
     return worst
+
+
+def conv_net():
+    """Two Conv2d layers (stride, padding, dilation, rectangular kernels) and a Linear head."""
+    from torch import nn
+    return nn.Sequential(
+        nn.Conv2d(3, 6, kernel_size=3, padding=1, stride=2), nn.ReLU(),
+        nn.Conv2d(6, 4, kernel_size=(3, 2), dilation=(1, 2), padding=(1, 0)), nn.ReLU(),
+        nn.Flatten(), nn.Linear(4 * 4 * 2, 5))
+
+
+def run_conv_engine(model, X, Y, n_val, device, precision="fp32"):
+    """One GradDotProd step on `model`; returns ({name: dot}, {name: grad}) on the CPU."""
+    import torch.nn.functional as F
+    from ghostsuite_amd import GradDotProdEngine
+    eng = GradDotProdEngine(model, val_batch_size=n_val, use_dummy_bias=False,
+                            precision=precision)
+    eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+    eng.attach_train_batch(X[:-n_val], Y[:-n_val], 0, 0)
+    F.cross_entropy(model(X.to(device)), Y.to(device)).backward()
+    dots = {n: p.grad_dot_prod.detach().cpu().clone() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    eng.prepare_gradients()
+    grads = {n: p.grad.detach().cpu().clone() for n, p in model.named_parameters()}
+    eng.aggregate_and_log()
+    eng.detach()
+    return dots, grads

@@ -16,7 +16,7 @@ from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
 from ghostsuite_amd.workloads import MLP, CausalLM, LMConfig, synthetic_tokens
 from oracle import brute
 from oracle import ghost_ref as R
-from tests.helpers import BF16_TOL, FP32_TOL, assert_close, gen
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, conv_net, gen, run_conv_engine
 from tests.oracle_backend import use_oracle_backend
 
 
@@ -338,3 +338,24 @@ def test_gradproj_embedding_projection_matches_naive(tmp_path):
         naive = P_o @ W.t() @ P_i.t()
         # the reference does not multiply embedding projections by the batch size
         assert torch.allclose(got[b] * 3, naive, rtol=1e-4, atol=1e-6)
+
+
+# ------------------------------------------------------------------ Conv2d
+@pytest.mark.parametrize("n_val", [1, 3])
+def test_conv2d_engine_dots_and_grads(n_val):
+    torch.manual_seed(60)
+    model = conv_net()
+    ref = copy.deepcopy(model).double()
+    N = 7
+    X = torch.randn(N, 3, 8, 8, generator=gen(61))
+    Y = torch.randint(0, 5, (N,), generator=gen(62))
+    with use_oracle_backend() as ops:
+        dots, grads = run_conv_engine(model, X, Y, n_val, "cpu")
+        assert sum(1 for c in ops.calls if c[0] == "linear_dot") == 3
+    g = brute.per_sample_grads(ref, X.double(), Y, _ce_sum, 1.0 / N)
+    if n_val == 1:   # presum (Conv2d) and pairwise (Linear) coincide
+        for name, d in dots.items():
+            assert_close(d, brute.pairwise_dots(g[name], n_val), FP32_TOL, f"dot {name}")
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g[name], n_val, N), FP32_TOL, f"grad {name}")
+    assert model[0].use_ghost_computation == (2 * 16 ** 2 <= 6 * 3 * 9)

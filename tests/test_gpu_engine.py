@@ -296,3 +296,41 @@ def test_async_host_copies_and_files_match_device_results(gpu, tmp_path):
         assert d["proj"].dtype == torch.float16 and d["iter"] == it and d["batch_size"] == 6
         assert torch.equal(d["proj"], want)
     assert (proj_dir / "metadata.json").exists()
+
+
+@pytest.mark.parametrize("precision,tol", [("fp32", FP32_TOL), ("reference", BF16_TOL)])
+@pytest.mark.parametrize("n_val", [1, 3])
+def test_conv2d_engine_on_gpu(gpu, precision, tol, n_val):
+    """Conv2d samplers: unfold to token-major rows, presum dots on the Linear kernels, the
+    bias dot and train gradient from the bias kernel."""
+    from oracle import ghost_ref as R
+    from tests.helpers import conv_net, run_conv_engine
+    torch.manual_seed(60)
+    model = conv_net()
+    ref = copy.deepcopy(model).double()
+    N = 7
+    X = torch.randn(N, 3, 8, 8, generator=gen(61))
+    Y = torch.randint(0, 5, (N,), generator=gen(62))
+    model = model.to(gpu)
+    caps = {}
+    for idx in (0, 2):
+        model[idx].register_forward_hook(
+            lambda m, i, o, k=idx: caps.__setitem__(("A", k), i[0].detach().cpu()))
+        model[idx].register_full_backward_hook(
+            lambda m, gi, go, k=idx: caps.__setitem__(("B", k), go[0].detach().cpu()))
+    print(f"conv2d engine precision={precision} n_val={n_val}", flush=True)
+    dots, grads = run_conv_engine(model, X, Y, n_val, gpu, precision)
+    g = brute.per_sample_grads(ref, X.double(), Y,
+                               lambda m, x, y: F.cross_entropy(m(x), y, reduction="sum"),
+                               1.0 / N)
+    for idx in (0, 2):
+        layer = model[idx]
+        conv = dict(kernel_size=layer.kernel_size, dilation=layer.dilation,
+                    padding=layer.padding, stride=layer.stride)
+        want = R.conv2d_dot_exact(caps[("A", idx)], caps[("B", idx)], n_val, conv)
+        assert_close(dots[f"{idx}.weight"], want, tol, f"conv{idx} dot")
+        if n_val == 1:
+            # A, B captured from the fp32 GPU model: fp32-level agreement
+            assert_close(want, brute.pairwise_dots(g[f"{idx}.weight"], 1), 1e-5, "closed form")
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g[name], n_val, N), tol, f"grad {name}")

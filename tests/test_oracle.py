@@ -214,6 +214,53 @@ def test_embedding_projection_forms_match_per_sample_gradients():
     assert_close(R.kron_proj_exact(onehot, g, P_i, P_o, 1.0), naive, 1e-10, "one-hot dense")
 
 
+# ------------------------------------------------------------------ Conv2d
+CONV = dict(kernel_size=(3, 2), dilation=(1, 2), padding=(1, 0), stride=(2, 1))
+
+
+def test_conv2d_forms_match_per_sample_gradients():
+    N, n_val, C, H, W, P = 5, 1, 3, 7, 6, 4
+    layer = nn.Conv2d(C, P, **CONV).double()
+    X = randn((N, C, H, W), 51).double()
+    head = randn((P,), 52).double().view(1, P, 1, 1)
+
+    def loss(m, x, y):
+        return (torch.tanh(m(x)) * head).sum()
+
+    cap = Capture(layer)
+    layer.zero_grad()
+    (torch.tanh(layer(X)) * head).reshape(N, -1).sum(1).sum().backward()
+    A, B = cap.A, cap.B
+    g = brute.per_sample_grads(layer, X, X, loss, 1.0)
+    # n_val = 1: the presum dot is <g_i, g_val>
+    assert_close(R.conv2d_dot_exact(A, B, n_val, CONV), brute.pairwise_dots(g["weight"], n_val),
+                 1e-10, "conv2d weight")
+    w_ref, b_ref = R.conv2d_dot_ref(A.float(), B.float(), n_val, CONV)
+    assert_close(w_ref.double(), brute.pairwise_dots(g["weight"], n_val), BF16_TOL, "conv2d ref")
+    assert_close(b_ref.double(), brute.pairwise_dots(g["bias"], n_val), BF16_TOL, "conv2d bias")
+    assert_close(R.bias_dot_exact(B.double().flatten(2).transpose(1, 2), n_val),
+                 brute.pairwise_dots(g["bias"], n_val), 1e-10, "conv2d bias exact")
+
+
+def test_conv2d_presum_by_explicit_position_loops():
+    """n_val = 2: dot_i = sum_{l,m} <a_il, abar_m> <b_il, bbar_m> over unfolded positions."""
+    N, n_val, C, H, W, P = 4, 2, 2, 5, 4, 3
+    A = randn((N, C, H, W), 53).double()
+    Hout = (H + 2 * 1 - 1 * (3 - 1) - 1) // 2 + 1
+    Wout = (W + 2 * 0 - 2 * (2 - 1) - 1) // 1 + 1
+    B = randn((N, P, Hout, Wout), 54).double()
+    a = torch.nn.functional.unfold(A, **CONV)       # [N, d, L]
+    b = B.reshape(N, P, -1)
+    n_t = N - n_val
+    abar, bbar = a[n_t:].sum(0), b[n_t:].sum(0)
+    want = torch.zeros(n_t, dtype=torch.float64)
+    for i in range(n_t):
+        for l in range(a.shape[-1]):
+            for m in range(a.shape[-1]):
+                want[i] += (a[i, :, l] @ abar[:, m]) * (b[i, :, l] @ bbar[:, m])
+    assert_close(R.conv2d_dot_exact(A, B, n_val, CONV), want, 1e-10, "conv2d presum loops")
+
+
 def test_choose_ki_ko_known_answers():
     # GPT-2-medium shapes, k_total=256, k_min=8 (engine_manager defaults): values obtained
     # by hand from projection_utils.py:12-66.

@@ -89,6 +89,7 @@ struct GemmParams {
   int64_t z_ld;
   RowMap z_map;            // same rows as R1
   int z_vec_ok;
+  int64_t z_nbytes;        // extent of Z (buffer-resource range)
   // STORE
   void* C;
   int64_t c_ld;
@@ -604,6 +605,62 @@ __device__ __forceinline__ void rowdot_colsum(const GemmParams& p, f32x16_t (&ac
   }
 }
 
+// rowdot_colsum for the LDS-DMA kernel: after the mainloop the stage buffers are free, so
+// the Z tile [BN rows][BM cols] is brought in by wave-level DMA (16 contiguous bytes per
+// lane, each row's 16-byte chunk c at slot c ^ (row mod chunks-per-row)) and each lane then
+// reads its 4-element groups with one ds_read_b64.  Needs a full tile along M, 16-byte
+// aligned Z rows and Z below 4 GiB; `lds` holds at least BN * BM * 2 bytes.
+template <class C>
+__device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
+                                                  f32x16_t (&acc)[C::MI][C::NI], int64_t mt,
+                                                  int64_t nt, unsigned char* lds,
+                                                  float (&colsum)[C::NI]) {
+  constexpr int CPR = C::BM / 8;           // 16-byte chunks per Z row
+  constexpr int RPI = 64 / CPR;            // rows per wave-level DMA
+  constexpr int NW = C::WM * C::WN;
+  constexpr int NQ = C::BN / RPI / NW;     // DMAs per wave
+  static_assert(64 % CPR == 0 && (C::BN / RPI) % NW == 0, "Z tile split");
+  static_assert((CPR & (CPR - 1)) == 0, "chunks per row must be a power of two");
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z, p.z_nbytes);
+  const int sub = lane / CPR, sl = lane % CPR;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int r = RPI * (wid + NW * q) + sub;  // local row (train token) of this lane's chunk
+    const int c = sl ^ (r & (CPR - 1));
+    const int64_t f = nt * C::BN + r;
+    unsigned off = DMA_OOB;
+    if (f < p.z_map.total()) {
+      const int64_t seg = f / p.z_map.seglen;
+      const int64_t row = p.z_map.phys_row(seg, f - seg * p.z_map.seglen);
+      off = static_cast<unsigned>((row * p.z_ld + mt * C::BM + c * 8) * 2);
+    }
+    dma16(rz, off, lds + RPI * (wid + NW * q) * CPR * 16);
+  }
+  wait_vmcnt<0>();
+  raw_barrier();
+  const int half = (lane >> 5) * 8;
+#pragma unroll
+  for (int ni = 0; ni < C::NI; ++ni) {
+    const int nl = wn * 32 * C::NI + ni * 32 + (lane & 31);
+    const unsigned char* zrow = lds + nl * CPR * 16 + half;
+    float s = 0.f;
+#pragma unroll
+    for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c = wm * 4 * C::MI + mi * 4 + g;
+        union { uint2 v; uint16_t e[4]; } z;
+        z.v = *reinterpret_cast<const uint2*>(zrow + ((c ^ (nl & (CPR - 1))) * 16));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s += acc[mi][ni][4 * g + v] * bf16_to_f32(z.e[v]);
+      }
+    colsum[ni] = s;
+  }
+  raw_barrier();  // every wave's Z reads are done before the LDS is reused
+}
+
 // Combines column sums across the half-waves and the WM waves sharing columns, then writes
 // per-row partials P[p_row0 + mt][n] or, with tile_reduce, one partial P[p_row0 + mt][nt].
 template <class C>
@@ -685,7 +742,17 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
       mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc2);
       ghost_colsum<C>(p, acc, acc2, colsum);
     } else {
-      rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
+      constexpr bool fits = static_cast<int64_t>(C::BN) * C::BM * 2 <= D::STAGES * SB;
+      const bool zlds = fits && p.z_vec_ok && (mt + 1) * C::BM <= p.m_rows &&
+                        p.z_nbytes > 0 && p.z_nbytes < INT32_MAX;
+      if constexpr (fits) {
+        if (zlds)
+          rowdot_colsum_lds<C>(p, acc, mt, nt, s0, colsum);
+        else
+          rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
+      } else {
+        rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
+      }
     }
     static_assert(C::WM * C::BN * 4 <= SB, "partial scratch");
     write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
@@ -1211,6 +1278,7 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     r.z_ld = d_out;
     r.z_map = tr;
     r.z_vec_ok = aligned16(G) && (d_out * static_cast<int64_t>(esz)) % 16 == 0;
+    r.z_nbytes = g_bytes;
     rc = Launch<Tr, RC>::template run<EPI_ROWDOT>(r, r.L1.vec_ok && r.R1.vec_ok, s);
     if (rc) return rc;
   }

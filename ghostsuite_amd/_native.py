@@ -63,7 +63,15 @@ _SIGNATURES = {
                           _P, _I, _P, _SZ, _P]),
     "gs_kron_embed_proj": (_I, [_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _F,
                                 _P, _I, _P, _SZ, _P]),
+    "gs_linear_rowdot_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
+    "gs_linear_rowdot": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
+                              _P]),
 }
+
+# How the val-gradient algorithm forms V = G_val^T A_val: "library" (a hipBLASLt GEMM through
+# torch.mm on the operands as they lie, then gs_linear_rowdot) or "native" (the library's
+# own transposes and GEMM inside gs_linear_dot).  Per-pair outputs always use "native".
+V_GEMM = "library"
 
 
 def load_library() -> ctypes.CDLL:
@@ -171,6 +179,11 @@ class HipOps:
         n_t = N - n_val
         dt = _gs_dtype(A)
         lib = load_library()
+        if V_GEMM == "library" and not want_pair and n_t > 0 and 0 <= vs <= N - n_val and \
+                lib.gs_linear_dot_algo(dt, N, n_val, T, d_in, d_out, semantics, algo,
+                                       0) == ALGO_VALGRAD:
+            return self._valgrad_library(A, G, N, n_val, vs, T, d_in, d_out, semantics, dev,
+                                         dt), None
         ws_bytes = lib.gs_linear_dot_workspace(dt, N, n_val, T, d_in, d_out, semantics, algo,
                                                int(want_pair))
         if ws_bytes == 0:
@@ -185,6 +198,45 @@ class HipOps:
                                ws.data_ptr(), ws_bytes, _stream(dev))
         _check(rc, "gs_linear_dot")
         return out, pair
+
+    def _valgrad_library(self, A, G, N, n_val, vs, T, d_in, d_out, semantics, dev, dt):
+        """V = G_val^T A_val (presummed val rows for PRESUM) by torch.mm, then the fused
+        row-dot kernel over the train tokens."""
+        Av = A.view(N, T, d_in)[vs:vs + n_val]
+        Gv = G.view(N, T, d_out)[vs:vs + n_val]
+        if semantics == SEM_PRESUM:
+            Av, Gv = Av.sum(0), Gv.sum(0)
+        V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
+        return self.linear_rowdot(A, G, V, n_val, val_start=vs)
+
+    def linear_rowdot(self, A: torch.Tensor, G: torch.Tensor, V: torch.Tensor, n_val: int, *,
+                      val_start=None) -> torch.Tensor:
+        """dot_i = sum_t g_it^T V a_it over the train rows, V: [d_out, d_in]."""
+        dev = _require_device(A, G, V)
+        if not (A.dtype == G.dtype == V.dtype):
+            raise GhostHipError(f"A, G, V dtypes differ: {A.dtype} {G.dtype} {V.dtype}")
+        A = A.contiguous()
+        G = G.contiguous()
+        V = V.contiguous()
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T or tuple(V.shape) != (d_out, d_in):
+            raise GhostHipError(f"shapes disagree: A {tuple(A.shape)} G {tuple(G.shape)} "
+                                f"V {tuple(V.shape)}")
+        vs = N - n_val if val_start is None else int(val_start)
+        dt = _gs_dtype(A)
+        lib = load_library()
+        ws_bytes = lib.gs_linear_rowdot_workspace(dt, N, n_val, T, d_in, d_out)
+        if ws_bytes == 0:
+            raise GhostHipError(f"gs_linear_rowdot: invalid arguments N={N} n_val={n_val} T={T}")
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty(N - n_val, dtype=torch.float32, device=dev)
+        rc = lib.gs_linear_rowdot(A.data_ptr(), G.data_ptr(), V.data_ptr(), dt, N, n_val, vs, T,
+                                  d_in, d_out, out.data_ptr(), ws.data_ptr(), ws_bytes,
+                                  _stream(dev))
+        _check(rc, "gs_linear_rowdot")
+        return out
 
     def bias_dot(self, G: torch.Tensor, n_val: int, *, val_start=None,
                  grad_scale: Optional[float] = None, grad_dtype: Optional[torch.dtype] = None

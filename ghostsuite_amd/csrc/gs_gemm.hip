@@ -1142,6 +1142,35 @@ bool linear_args_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in
   return true;
 }
 
+// ROWDOT over the train tokens: P rows [p_row0, p_row0 + m tiles) get the per-tile (or
+// per-token) partials of sum_m (V a_t)[m] g_t[m].
+template <class Tr>
+int launch_rowdot(const void* A, const void* G, const void* V, int64_t N, int64_t n_val,
+                  int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, float* P,
+                  int64_t p_ld, int tile_reduce, int64_t p_row0, hipStream_t s) {
+  using RC = RowdotCfg<Tr>;
+  const size_t esz = sizeof(typename Tr::E);
+  const RowMap tr = train_rows(N, n_val, val_start, T);
+  GemmParams r{};
+  r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, esz,
+                      d_out * d_in * static_cast<int64_t>(esz));
+  r.R1 = make_operand(A, d_in, tr, 0, d_in, esz, N * T * d_in * static_cast<int64_t>(esz));
+  r.K1 = d_in;
+  r.m_tiles = ceil_div(d_out, RC::BM);
+  r.n_tiles = host_tiles<RC::BN>(r.R1);
+  r.m_rows = d_out;
+  r.P = P;
+  r.p_ld = p_ld;
+  r.tile_reduce = tile_reduce;
+  r.p_row0 = p_row0;
+  r.Z = G;
+  r.z_ld = d_out;
+  r.z_map = tr;
+  r.z_vec_ok = aligned16(G) && (d_out * static_cast<int64_t>(esz)) % 16 == 0;
+  r.z_nbytes = N * T * d_out * static_cast<int64_t>(esz);
+  return Launch<Tr, RC>::template run<EPI_ROWDOT>(r, r.L1.vec_ok && r.R1.vec_ok, s);
+}
+
 template <class Tr>
 int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t val_start,
                int64_t T, int64_t d_in, int64_t d_out, int semantics, int rounding,
@@ -1263,23 +1292,8 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     int rc = Launch<Tr, SC>::template run<EPI_STORE>(q, q.L1.vec_ok && q.R1.vec_ok, s);
     if (rc) return rc;
 
-    GemmParams r{};
-    r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, esz, d_out * d_in * esz);
-    r.R1 = make_operand(A, d_in, tr, 0, d_in, esz, a_bytes);
-    r.K1 = d_in;
-    r.m_tiles = n_mt;
-    r.n_tiles = host_tiles<RC::BN>(r.R1);
-    r.m_rows = d_out;
-    r.P = P;
-    r.p_ld = pl.p_ld;
-    r.tile_reduce = pl.tile_reduce;
-    r.p_row0 = j * n_mt;
-    r.Z = G;
-    r.z_ld = d_out;
-    r.z_map = tr;
-    r.z_vec_ok = aligned16(G) && (d_out * static_cast<int64_t>(esz)) % 16 == 0;
-    r.z_nbytes = g_bytes;
-    rc = Launch<Tr, RC>::template run<EPI_ROWDOT>(r, r.L1.vec_ok && r.R1.vec_ok, s);
+    rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
+                           pl.tile_reduce, j * n_mt, s);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s, P,
@@ -1337,4 +1351,71 @@ extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N,
                               out_dot, out_pair, pl, cv, s);
   return run_linear<TrF32>(A, G, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
                            out_dot, out_pair, pl, cv, s);
+}
+
+// ------------------------------------------------------------------ row-dot with a given V
+namespace gs {
+namespace {
+struct RowdotPlan {
+  int64_t n_mt, p_ld, cols;
+  int tile_reduce;
+};
+template <class Tr>
+RowdotPlan plan_rowdot(int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
+  using RC = RowdotCfg<Tr>;
+  RowdotPlan pl{};
+  const int64_t n_t = N - n_val;
+  pl.n_mt = ceil_div(d_out, RC::BM);
+  pl.tile_reduce = T % RC::BN == 0 ? 1 : 0;
+  pl.p_ld = pl.tile_reduce ? n_t * T / RC::BN : n_t * T;
+  pl.cols = pl.tile_reduce ? T / RC::BN : T;
+  return pl;
+}
+RowdotPlan plan_rowdot_any(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
+  return dtype == GS_DTYPE_F32 ? plan_rowdot<TrF32>(N, n_val, T, d_out)
+                               : plan_rowdot<TrBF16>(N, n_val, T, d_out);
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_rowdot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                             int64_t d_in, int64_t d_out) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
+    return 0;
+  const RowdotPlan pl = plan_rowdot_any(dtype, N, n_val, T, d_out);
+  Sizer sz;
+  sz.take<float>(pl.n_mt * pl.p_ld);
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_rowdot(const void* A, const void* G, const void* V, int dtype,
+                                int64_t N, int64_t n_val, int64_t val_start, int64_t T,
+                                int64_t d_in, int64_t d_out, float* out_dot, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_linear_rowdot: dtype must be bf16 or fp32");
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot: invalid shape");
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot: val block outside the batch");
+  if (A == nullptr || G == nullptr || V == nullptr || out_dot == nullptr)
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot: null pointer");
+  const RowdotPlan pl = plan_rowdot_any(dtype, N, n_val, T, d_out);
+  Sizer sz;
+  sz.take<float>(pl.n_mt * pl.p_ld);
+  if (workspace == nullptr || workspace_bytes < sz.used)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_rowdot: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  float* P = cv.take<float>(pl.n_mt * pl.p_ld);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n_t = N - n_val;
+  int rc = dtype == GS_DTYPE_BF16
+               ? launch_rowdot<TrBF16>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
+                                       pl.tile_reduce, 0, s)
+               : launch_rowdot<TrF32>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
+                                      pl.tile_reduce, 0, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s, P,
+                     int64_t{1}, pl.n_mt, pl.p_ld, pl.cols, n_t, nullptr, out_dot);
+  return check_launch("reduce_partials_kernel");
 }

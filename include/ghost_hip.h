@@ -94,6 +94,18 @@ int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_
                   int algo, int rounding, float* out_dot, float* out_pair, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* Row-dot with a caller-formed val gradient V = G_val^T A_val ([d_out, d_in], same dtype):
+ *   out_dot[i] = sum_t g_it^T V a_it over the train rows (the second half of the
+ *   VALGRAD algorithm of gs_linear_dot, for callers that form V with a library GEMM).
+ * Replaces the same reference function as gs_linear_dot
+ * (supported_layers_grad_samplers_dotprod.py:75-135); with V from the summed val rows it is
+ * the pairwise-sum dot, with V from the presummed val rows the presum dot. */
+size_t gs_linear_rowdot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
+                                  int64_t d_out);
+int gs_linear_rowdot(const void* A, const void* G, const void* V, int dtype, int64_t N,
+                     int64_t n_val, int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                     float* out_dot, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Bias dot product and bias train gradient ---------------------------------------
  * Replaces the bias part of _compute_linear_dot_product (:137-146), the bias part of
  * _compute_Conv1D_dot_product (:450-471) and _compute_train_grad_bias

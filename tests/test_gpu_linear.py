@@ -30,13 +30,24 @@ def _inputs(N, T, d_in, d_out, seed, dtype):
     return A, G
 
 
+@pytest.fixture(params=["library", "native"])
+def v_gemm(request):
+    saved = _native.V_GEMM
+    _native.V_GEMM = request.param
+    yield request.param
+    _native.V_GEMM = saved
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("algo", [_native.ALGO_GHOST, _native.ALGO_VALGRAD])
 @pytest.mark.parametrize("semantics", ["pairwise", "presum"])
-def test_linear_dot_matches_closed_form(gpu, shape, dtype, algo, semantics):
+def test_linear_dot_matches_closed_form(gpu, v_gemm, shape, dtype, algo, semantics):
     N, n_val, T, d_in, d_out = shape
-    print(f"linear_dot shape={shape} dtype={dtype} algo={algo} sem={semantics}", flush=True)
+    if algo == _native.ALGO_GHOST and v_gemm == "library":
+        pytest.skip("the V GEMM choice only affects VALGRAD")
+    print(f"linear_dot shape={shape} dtype={dtype} algo={algo} sem={semantics} v={v_gemm}",
+          flush=True)
     A, G = _inputs(N, T, d_in, d_out, 100 + N + T, dtype)
     sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
     dot, _ = _native.ops().linear_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem, algo=algo)
@@ -76,6 +87,25 @@ def test_ghost_reference_rounding_matches_reference_sequence(gpu, shape):
     torch.cuda.synchronize()
     want, _ = R.linear_dot_ref(A, G, n_val, use_ghost=True, has_bias=False)
     assert_close(dot.cpu(), want, 2e-3, "ref-rounding")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_linear_rowdot_with_given_v(gpu, shape, dtype):
+    """gs_linear_rowdot: sum_t g_it^T V a_it for a caller-formed V, at a val block in the
+    middle of the batch."""
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 300 + T, dtype)
+    V = randn((d_out, d_in), 301 + T, 1.0, dtype)
+    vs = 1 if N - n_val >= 1 else 0
+    print(f"rowdot shape={shape} dtype={dtype}", flush=True)
+    out = _native.ops().linear_rowdot(A.to(gpu), G.to(gpu), V.to(gpu), n_val, val_start=vs)
+    torch.cuda.synchronize()
+    tr = torch.cat([A[:vs], A[vs + n_val:]]).double().reshape(N - n_val, -1, d_in)
+    gt = torch.cat([G[:vs], G[vs + n_val:]]).double().reshape(N - n_val, -1, d_out)
+    want = torch.einsum('ntp,pd,ntd->n', gt, V.double(), tr)
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert_close(out.cpu(), want, tol, "rowdot")
 
 
 def test_linear_auto_picks_cheaper_algorithm(gpu):

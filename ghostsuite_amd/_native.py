@@ -68,9 +68,11 @@ _SIGNATURES = {
                               _P]),
 }
 
-# How the val-gradient algorithm forms V = G_val^T A_val: "library" (a hipBLASLt GEMM through
-# torch.mm on the operands as they lie, then gs_linear_rowdot) or "native" (the library's
-# own transposes and GEMM inside gs_linear_dot).  Per-pair outputs always use "native".
+# How the val-gradient algorithm forms V = G_val^T A_val for the pairwise semantics: "library"
+# (a hipBLASLt GEMM through torch.mm on the operands as they lie, then gs_linear_rowdot) or
+# "native" (the library's own transposes and GEMM inside gs_linear_dot).  The presum
+# semantics (V from T presummed rows, a short GEMM) and per-pair outputs use "native", which
+# measured faster there.
 V_GEMM = "library"
 
 
@@ -179,7 +181,8 @@ class HipOps:
         n_t = N - n_val
         dt = _gs_dtype(A)
         lib = load_library()
-        if V_GEMM == "library" and not want_pair and n_t > 0 and 0 <= vs <= N - n_val and \
+        if V_GEMM == "library" and not want_pair and semantics == SEM_PAIRWISE_SUM and \
+                n_t > 0 and 0 <= vs <= N - n_val and \
                 lib.gs_linear_dot_algo(dt, N, n_val, T, d_in, d_out, semantics, algo,
                                        0) == ALGO_VALGRAD:
             return self._valgrad_library(A, G, N, n_val, vs, T, d_in, d_out, semantics, dev,
@@ -206,6 +209,7 @@ class HipOps:
         Gv = G.view(N, T, d_out)[vs:vs + n_val]
         if semantics == SEM_PRESUM:
             Av, Gv = Av.sum(0), Gv.sum(0)
+        # sum over val rows and tokens of g a^T: one GEMM with K = n_val * T
         V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
         return self.linear_rowdot(A, G, V, n_val, val_start=vs)
 

@@ -77,6 +77,17 @@ class TimedOps:
         name = f"linear_{_native.ALGO_NAMES[algo]}[{d_in}x{d_out}]"
         return self._run(name, ("mfma", flops), self.inner.linear_dot, A, G, n_val, **k)
 
+    def linear_bias_dot(self, A, G, n_val, **k):
+        from ghostsuite_amd import _native
+        N, d_in, d_out = A.shape[0], A.shape[-1], G.shape[-1]
+        T = A.numel() // (N * d_in)
+        flops = 2.0 * (n_val * T + (N - n_val) * T) * d_in * d_out
+        out = self._run(f"linear_valgrad+bias[{d_in}x{d_out}]", ("mfma", flops),
+                        self.inner.linear_bias_dot, A, G, n_val, **k)
+        if out is None and self.enabled:
+            self.records.pop()   # not supported for this shape: nothing ran
+        return out
+
     def bias_dot(self, G, n_val, **k):
         return self._run("bias_dot", ("hbm", G.numel() * G.element_size()),
                          self.inner.bias_dot, G, n_val, **k)
@@ -357,6 +368,45 @@ def ghost_kernel_bench(dev, reps: int = 20, T: int = 1024):
             "valgrad_ms": ms_vg}
 
 
+def ghost_sweep(dev, reps: int = 10):
+    """BASELINE configs[1] sweep over T: the reference's switch (2T^2 <= d_in*d_out) picks the
+    ghost (pairwise-sum) branch up to T=1024 and the materialised (presum) branch at T=2048;
+    each semantics is timed with both algorithms."""
+    from ghostsuite_amd import _native
+    g = torch.Generator().manual_seed(1234)
+    N, n_val, d_in, d_out = 32, 8, 768, 3072
+    ops = _native.ops()
+    out = []
+    for T in (128, 512, 1024, 2048):
+        A = torch.randn(N, T, d_in, generator=g).to(dev, torch.bfloat16)
+        G = (torch.randn(N, T, d_out, generator=g) * 1e-3).to(dev, torch.bfloat16)
+        ghost_branch = 2 * T * T <= d_in * d_out
+        sem = _native.SEM_PAIRWISE_SUM if ghost_branch else _native.SEM_PRESUM
+        row = {"T": T, "reference_branch": "ghost" if ghost_branch else "materialised",
+               "semantics": "pairwise" if ghost_branch else "presum"}
+        for algo, name in ((_native.ALGO_GHOST, "ghost"), (_native.ALGO_VALGRAD, "valgrad")):
+            fn = lambda: ops.linear_dot(A, G, n_val, val_start=0, semantics=sem, algo=algo)
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                fn()
+            e.record()
+            torch.cuda.synchronize()
+            row[f"{name}_ms"] = s.elapsed_time(e) / reps
+        n_t, nv = N - n_val, (n_val if ghost_branch else 1)
+        ghost_flops = 2.0 * n_t * nv * T * T * (d_in + d_out)
+        row["ghost_TFLOPs"] = ghost_flops / row["ghost_ms"] / 1e9
+        row["auto"] = _native.ALGO_NAMES[ops.linear_algo(torch.bfloat16, N, n_val, T, d_in,
+                                                          d_out, sem, _native.ALGO_AUTO, False)]
+        out.append(row)
+        del A, G
+    return out
+
+
 # ------------------------------------------------------------------ CPU baseline
 def cpu_baseline(budget_s: float = 20.0):
     """The oracle's restatement of the reference op sequence (ghost dots + train grads) for
@@ -407,6 +457,8 @@ KERNEL_SHAPES = {
     # name: shape at which the kernel leg runs it (the GPT-2-small / GPT-2-medium bench shapes)
     "ghost_microbench": "linear_dot GHOST, A[32,1024,768] G[32,1024,3072] bf16, 8 val first",
     "valgrad_fc": "linear_dot VALGRAD pairwise, A[20,1024,768] G[20,1024,3072] bf16, 4 val",
+    "valgrad_bias_fc": "linear_bias_dot (weight + bias dots, bias grad), A[20,1024,768] "
+                       "G[20,1024,3072] bf16, 4 val",
     "bias_fc": "bias_dot, G[20,1024,3072] bf16, 4 val",
     "layernorm": "layernorm_dot + grads, X,G[20,1024,768] bf16, 4 val",
     "embedding_wte": "embedding_dot, ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
@@ -447,6 +499,9 @@ def kernels_leg(dev, reps: int = 10):
                                                            algo=_native.ALGO_GHOST))
     A2, G2 = A[:20].contiguous(), G[:20].contiguous()
     out["valgrad_fc"] = timeit(lambda: ops.linear_dot(A2, G2, 4, algo=_native.ALGO_VALGRAD))
+    out["valgrad_bias_fc"] = timeit(lambda: ops.linear_bias_dot(A2, G2, 4,
+                                                                algo=_native.ALGO_VALGRAD,
+                                                                grad_scale=1.25))
     out["bias_fc"] = timeit(lambda: ops.bias_dot(G2, 4, grad_scale=1.25))
     X = rnd(20, 1024, 768)
     GL = rnd(20, 1024, 768, s=1e-3)
@@ -520,6 +575,8 @@ def main():
     log("[bench] GPT-2 step done; ghost kernel microbench")
     gk = ghost_kernel_bench(dev)
     log(f"[bench] ghost kernel T=1024: {gk['ms']:.3f} ms, {gk['tflops']:.1f} TF/s")
+    sweep = ghost_sweep(dev)
+    log("[bench] configs[1] T sweep done")
     legs = [l for l in args.legs.split(",") if l and l != "none"]
     extra = {}
     import contextlib
@@ -576,7 +633,8 @@ def main():
                          "ms": gk["ms"], "achieved": gk["tflops"], "unit": "TFLOP/s",
                          "peak": PEAK_BF16 / 1e12, "frac": gk["frac"],
                          "traffic": measured_traffic("ghost"),
-                         "valgrad_same_semantics_ms": gk["valgrad_ms"]},
+                         "valgrad_same_semantics_ms": gk["valgrad_ms"],
+                         "T_sweep": sweep},
         "ops": {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["n"] / steps,
                     "avg_us": v["ms"] / v["n"] * 1e3,
                     ("TFLOP/s" if v["bound"] == "mfma" else "GB/s"):

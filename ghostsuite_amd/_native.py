@@ -64,6 +64,9 @@ _SIGNATURES = {
     "gs_kron_embed_proj": (_I, [_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _F,
                                 _P, _I, _P, _SZ, _P]),
     "gs_linear_rowdot_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
+    "gs_linear_rowdot_bias_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
+    "gs_linear_rowdot_bias": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
+                                   _P, _I, _F, _P, _SZ, _P]),
     "gs_linear_rowdot": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
                               _P]),
 }
@@ -212,6 +215,52 @@ class HipOps:
         # sum over val rows and tokens of g a^T: one GEMM with K = n_val * T
         V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
         return self.linear_rowdot(A, G, V, n_val, val_start=vs)
+
+    def linear_bias_dot(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
+                        semantics: int = SEM_PAIRWISE_SUM, algo: int = ALGO_AUTO,
+                        rounding: int = ROUND_FP32, grad_scale: Optional[float] = None,
+                        grad_dtype: Optional[torch.dtype] = None):
+        """Weight and bias dots of a Linear layer (and the bias train gradient when
+        grad_scale is given) in one pass when the shape allows it, i.e. the val-gradient
+        algorithm with the library V GEMM and gs_linear_rowdot_bias; otherwise None (the
+        caller then uses linear_dot and bias_dot).  Returns (dot, bias_dot, bias_grad)."""
+        dev = _require_device(A, G)
+        if A.dtype != G.dtype or A.dtype != torch.bfloat16 or V_GEMM != "library" or \
+                semantics != SEM_PAIRWISE_SUM or \
+                (grad_dtype or G.dtype) not in (torch.bfloat16, torch.float32):
+            return None
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        n_t = N - n_val
+        if n_t <= 0 or _tokens(G, N, d_out) != T:
+            return None
+        dt = _gs_dtype(A)
+        lib = load_library()
+        if lib.gs_linear_dot_algo(dt, N, n_val, T, d_in, d_out, semantics, algo,
+                                  0) != ALGO_VALGRAD:
+            return None
+        ws_bytes = lib.gs_linear_rowdot_bias_workspace(dt, N, n_val, T, d_in, d_out)
+        if ws_bytes == 0:
+            return None
+        A = A.contiguous()
+        G = G.contiguous()
+        vs = N - n_val
+        Av = A.view(N, T, d_in)[vs:]
+        Gv = G.view(N, T, d_out)[vs:]
+        V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
+        ws = _workspace(ws_bytes, dev)
+        out = torch.empty(n_t, dtype=torch.float32, device=dev)
+        bout = torch.empty(n_t, dtype=torch.float32, device=dev)
+        gdt = grad_dtype or G.dtype
+        grad = torch.empty(d_out, dtype=gdt, device=dev) if grad_scale is not None else None
+        rc = lib.gs_linear_rowdot_bias(A.data_ptr(), G.data_ptr(), V.data_ptr(), dt, N, n_val,
+                                       vs, T, d_in, d_out, out.data_ptr(),
+                                       bout.data_ptr(), _ptr(grad), _TORCH_TO_GS[gdt],
+                                       float(grad_scale or 0.0), ws.data_ptr(), ws_bytes,
+                                       _stream(dev))
+        _check(rc, "gs_linear_rowdot_bias")
+        return out, bout, grad
 
     def linear_rowdot(self, A: torch.Tensor, G: torch.Tensor, V: torch.Tensor, n_val: int, *,
                       val_start=None) -> torch.Tensor:

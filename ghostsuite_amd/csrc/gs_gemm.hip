@@ -90,6 +90,9 @@ struct GemmParams {
   RowMap z_map;            // same rows as R1
   int z_vec_ok;
   int64_t z_nbytes;        // extent of Z (buffer-resource range)
+  // ROWDOT with the bias folded in (LDS epilogue only): BP = column sums of the Z tile per
+  // N tile ([n_tiles][m_rows]); null when the bias is handled elsewhere.
+  float* BP;
   // STORE
   void* C;
   int64_t c_ld;
@@ -171,15 +174,16 @@ struct Streamer {
   }
 };
 
-// Tile configuration: WM x WN waves, each owning MI x NI MFMA 32x32 blocks.
-template <class Tr, int WM_, int WN_, int MI_, int NI_>
+// Tile configuration: WM x WN waves, each owning MI x NI MFMA 32x32 blocks; MW_ > 0 sets
+// the waves per SIMD the registers must allow (default: 2 for small wave tiles, else 1).
+template <class Tr, int WM_, int WN_, int MI_, int NI_, int MW_ = 0>
 struct Cfg {
   static constexpr int WM = WM_, WN = WN_, MI = MI_, NI = NI_;
   static constexpr int BM = 32 * MI * WM, BN = 32 * NI * WN, NT = 64 * WM * WN;
   static constexpr int LDR = Tr::BK + Tr::PAD;
   static constexpr int STAGE = (BM + BN) * LDR;  // elements per stage
   static constexpr size_t LDS_BYTES = 2 * STAGE * sizeof(typename Tr::E);
-  static constexpr int MIN_WAVES = (MI * NI <= 4) ? 2 : 1;  // waves per SIMD to fit registers
+  static constexpr int MIN_WAVES = MW_ > 0 ? MW_ : (MI * NI <= 4) ? 2 : 1;
 };
 
 template <class Tr, class C>
@@ -614,7 +618,7 @@ template <class C>
 __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
                                                   f32x16_t (&acc)[C::MI][C::NI], int64_t mt,
                                                   int64_t nt, unsigned char* lds,
-                                                  float (&colsum)[C::NI]) {
+                                                  float (&colsum)[C::NI], float* bsum) {
   constexpr int CPR = C::BM / 8;           // 16-byte chunks per Z row
   constexpr int RPI = 64 / CPR;            // rows per wave-level DMA
   constexpr int NW = C::WM * C::WN;
@@ -639,7 +643,7 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
     dma16(rz, off, lds + RPI * (wid + NW * q) * CPR * 16);
   }
   wait_vmcnt<0>();
-  raw_barrier();
+  __syncthreads();  // Z landed (every wave waited for its DMA)
   const int half = (lane >> 5) * 8;
 #pragma unroll
   for (int ni = 0; ni < C::NI; ++ni) {
@@ -658,6 +662,35 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
       }
     colsum[ni] = s;
   }
+  if (p.BP != nullptr) {
+    // Column sums of the tile over its BN token rows: LPR = BM / 4 lanes cover a row (one
+    // ds_read_b64 of 4 columns each), so a wave reads RPW rows at a time and the NW * RPW
+    // lane groups take every (NW * RPW)-th row; the group sums combine in a fixed order
+    // through `bsum` [NW * RPW][BM].
+    constexpr int LPR = C::BM / 4, RPW = 64 / LPR, GRP = NW * RPW;
+    static_assert(LPR <= 64 && 64 % LPR == 0 && C::BN % GRP == 0, "tile column-sum split");
+    const int q = lane % LPR, grp = wid * RPW + lane / LPR;
+    const int ch = q >> 1, hb = (q & 1) * 8;
+    float4 cs = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+    for (int r = grp; r < C::BN; r += GRP) {
+      union { uint2 v; uint16_t e[4]; } z;
+      z.v = *reinterpret_cast<const uint2*>(lds + r * CPR * 16 + ((ch ^ (r & (CPR - 1))) * 16) +
+                                            hb);
+      cs.x += bf16_to_f32(z.e[0]);
+      cs.y += bf16_to_f32(z.e[1]);
+      cs.z += bf16_to_f32(z.e[2]);
+      cs.w += bf16_to_f32(z.e[3]);
+    }
+    reinterpret_cast<float4*>(bsum)[grp * LPR + q] = cs;
+    __syncthreads();
+    for (int m = threadIdx.x; m < C::BM; m += C::NT) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < GRP; ++g) t += bsum[g * C::BM + m];
+      p.BP[nt * p.m_rows + mt * C::BM + m] = t;
+    }
+  }
   raw_barrier();  // every wave's Z reads are done before the LDS is reused
 }
 
@@ -666,6 +699,7 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
 template <class C>
 __device__ __forceinline__ void write_partials(const GemmParams& p, float (&colsum)[C::NI],
                                                int64_t mt, int64_t nt, float* red) {
+  float* P = p.P;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
 #pragma unroll
@@ -682,7 +716,7 @@ __device__ __forceinline__ void write_partials(const GemmParams& p, float (&cols
       for (int w = 0; w < C::WM; ++w) v += red[w * C::BN + c];
     }
     v = block_sum(v, tred);
-    if (tid == 0) p.P[(p.p_row0 + mt) * p.p_ld + nt] = v;
+    if (tid == 0) P[(p.p_row0 + mt) * p.p_ld + nt] = v;
     return;
   }
   for (int c = tid; c < C::BN; c += C::NT) {
@@ -690,7 +724,7 @@ __device__ __forceinline__ void write_partials(const GemmParams& p, float (&cols
 #pragma unroll
     for (int w = 0; w < C::WM; ++w) s += red[w * C::BN + c];
     const int64_t n = nt * C::BN + c;
-    if (n < p.p_ld) p.P[(p.p_row0 + mt) * p.p_ld + n] = s;
+    if (n < p.p_ld) P[(p.p_row0 + mt) * p.p_ld + n] = s;
   }
 }
 
@@ -746,10 +780,21 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
       const bool zlds = fits && p.z_vec_ok && (mt + 1) * C::BM <= p.m_rows &&
                         p.z_nbytes > 0 && p.z_nbytes < INT32_MAX;
       if constexpr (fits) {
-        if (zlds)
-          rowdot_colsum_lds<C>(p, acc, mt, nt, s0, colsum);
-        else
+        if (zlds) {
+          // The tile column-sum scratch sits behind the Z tile when the stages leave room.
+          constexpr int BSUM = C::NT / (C::BM / 4) * C::BM;
+          constexpr int ZB = C::BN * C::BM * 2;
+          float* bsum;
+          if constexpr (ZB + BSUM * 4 <= D::STAGES * SB) {
+            bsum = reinterpret_cast<float*>(s0 + ZB);
+          } else {
+            __shared__ __attribute__((aligned(16))) float bsum_own[BSUM];
+            bsum = bsum_own;
+          }
+          rowdot_colsum_lds<C>(p, acc, mt, nt, s0, colsum, bsum);
+        } else {
           rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
+        }
       } else {
         rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
       }
@@ -823,6 +868,31 @@ __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
   write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
 }
 
+// This thread's share of sum over r < rows, c < cols of P[(row0 + r) * p_ld + i * cols + c]:
+// threads form a (rows x cols) grid of min(cols, blockDim) columns, so a short row of
+// partials (one per N tile) still puts one load per thread in flight.  Fixed order.
+__device__ __forceinline__ float partial_share(const float* __restrict__ P, int64_t row0,
+                                               int64_t rows, int64_t p_ld, int64_t i,
+                                               int64_t cols) {
+  const int64_t cw = cols < blockDim.x ? cols : blockDim.x;
+  const int64_t rstep = blockDim.x / cw;
+  const int64_t rt = threadIdx.x / cw, ct = threadIdx.x % cw;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (rt >= rstep) return 0.f;
+  const float* base = P + row0 * p_ld + i * cols;
+  int64_t r = rt;
+  for (; r + 3 * rstep < rows; r += 4 * rstep)
+    for (int64_t c = ct; c < cols; c += cw) {
+      s0 += base[r * p_ld + c];
+      s1 += base[(r + rstep) * p_ld + c];
+      s2 += base[(r + 2 * rstep) * p_ld + c];
+      s3 += base[(r + 3 * rstep) * p_ld + c];
+    }
+  for (; r < rows; r += rstep)
+    for (int64_t c = ct; c < cols; c += cw) s0 += base[r * p_ld + c];
+  return (s0 + s1) + (s2 + s3);
+}
+
 // P[(g*rows_per_group + r) * p_ld + i*cols + c] summed over r < rows_per_group and c < cols
 // -> out_pair[g][i] (optional) and out_dot[i] = sum_g; one block per train sample, fixed order.
 __global__ void reduce_partials_kernel(const float* __restrict__ P, int64_t groups,
@@ -832,26 +902,127 @@ __global__ void reduce_partials_kernel(const float* __restrict__ P, int64_t grou
   const int64_t i = blockIdx.x;
   float dot = 0.f;
   for (int64_t g = 0; g < groups; ++g) {
-    // Four independent partial sums keep several loads in flight per thread.
-    float s4[4] = {0.f, 0.f, 0.f, 0.f};
-    int64_t r = 0;
-    for (; r + 4 <= rows_per_group; r += 4) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float* row = P + (g * rows_per_group + r + u) * p_ld + i * cols;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s4[u] += row[c];
-      }
-    }
-    for (; r < rows_per_group; ++r) {
-      const float* row = P + (g * rows_per_group + r) * p_ld + i * cols;
-      for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s4[0] += row[c];
-    }
-    float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    float s = partial_share(P, g * rows_per_group, rows_per_group, p_ld, i, cols);
     s = block_sum(s, red);
     if (out_pair != nullptr && threadIdx.x == 0) out_pair[g * n_train + i] = s;
     dot += s;
   }
   if (threadIdx.x == 0 && out_dot != nullptr) out_dot[i] = dot;
+}
+
+// Val column sums of G (the val bias gradient before scaling), stage 1: block (x, y) sums
+// val rows [y * VS_ROWS, +VS_ROWS) for columns [x * VS_COLS, +VS_COLS): wave w takes rows
+// w, w + 4, ... in batches of 16 (16 bytes per lane, a batch's loads issued before its
+// adds), and the four wave sums combine in a fixed order.  VP[y][f]; needs F % 8 == 0 and
+// 16-byte aligned rows.
+constexpr int VS_COLS = 512, VS_ROWS = 256, VS_BATCH = 16;
+__global__ void __launch_bounds__(256) val_colsum_kernel(const uint16_t* __restrict__ G,
+                                                         int64_t rows, int64_t F,
+                                                         float* __restrict__ VP) {
+  __shared__ float sm[4][VS_COLS];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * VS_COLS + lane * 8;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * VS_ROWS;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int bt = 0; bt < VS_ROWS / (4 * VS_BATCH); ++bt) {
+    uint4 x[VS_BATCH];
+#pragma unroll
+    for (int k = 0; k < VS_BATCH; ++k) {
+      const int64_t r = r0 + wid + 4 * (bt * VS_BATCH + k);
+      x[k] = (r < rows && f < F) ? *reinterpret_cast<const uint4*>(G + r * F + f)
+                                 : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int k = 0; k < VS_BATCH; ++k) {
+      const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[2 * e] += __uint_as_float(w[e] << 16);
+        a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sm[wid][lane * 8 + e] = a[e];
+  __syncthreads();
+  for (int c = threadIdx.x; c < VS_COLS; c += blockDim.x) {
+    const int64_t fc = static_cast<int64_t>(blockIdx.x) * VS_COLS + c;
+    if (fc < F)
+      VP[static_cast<int64_t>(blockIdx.y) * F + fc] = (sm[0][c] + sm[1][c]) + (sm[2][c] + sm[3][c]);
+  }
+}
+
+// Bias finish, column stage: block (x, i) owns columns [256 x, +256) of train sample i.
+// Per column m: vb[m] = sum of the VP rows, b[m] = sum of the tile column sums BP over the
+// sample's `tps` N tiles; Q[i][x] = sum_m vb[m] b[m] (the sample's bias-dot share of these
+// columns) and BS[i][m] = b[m] (for the train gradient).  Fixed order throughout.
+__global__ void __launch_bounds__(256) rowdot_bias_cols_kernel(
+    const float* __restrict__ VP, int64_t vp_rows, const float* __restrict__ BP, int64_t tps,
+    int64_t F, float* __restrict__ Q, int64_t q_ld, float* __restrict__ BS) {
+  __shared__ float red[4];
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t i = blockIdx.y;
+  float vb = 0.f, b = 0.f;
+  if (m < F) {
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+    int64_t s = 0;
+    for (; s + 4 <= vp_rows; s += 4) {
+      v0 += VP[s * F + m];
+      v1 += VP[(s + 1) * F + m];
+      v2 += VP[(s + 2) * F + m];
+      v3 += VP[(s + 3) * F + m];
+    }
+    for (; s < vp_rows; ++s) v0 += VP[s * F + m];
+    vb = (v0 + v1) + (v2 + v3);
+    const float* bp = BP + i * tps * F + m;
+    float b0 = 0.f, b1 = 0.f;
+    int64_t k = 0;
+    for (; k + 2 <= tps; k += 2) {
+      b0 += bp[k * F];
+      b1 += bp[(k + 1) * F];
+    }
+    if (k < tps) b0 += bp[k * F];
+    b = b0 + b1;
+    BS[i * F + m] = b;
+  }
+  const float q = block_sum(vb * b, red);
+  if (threadIdx.x == 0) Q[i * q_ld + blockIdx.x] = q;
+}
+
+// Bias finish, row stage: blocks [0, n_train) reduce the weight-dot partials P of train
+// sample i, blocks [n_train, 2 n_train) its bias-dot shares Q[i][0..q_ld), blocks beyond
+// take grad[f] = scale * sum over the train samples of BS[i][f] (all fixed order).
+template <class GE>
+__global__ void __launch_bounds__(256) rowdot_bias_rows_kernel(
+    const float* __restrict__ P, int64_t rows, int64_t p_ld, int64_t cols, int64_t n_train,
+    float* out_dot, const float* __restrict__ Q, int64_t q_ld, float* out_bdot,
+    const float* __restrict__ BS, int64_t F, GE* grad, float scale) {
+  __shared__ float red[16];
+  const int64_t b = blockIdx.x;
+  if (b < n_train) {
+    const float s = block_sum(partial_share(P, 0, rows, p_ld, b, cols), red);
+    if (threadIdx.x == 0) out_dot[b] = s;
+    return;
+  }
+  if (b < 2 * n_train) {
+    const int64_t i = b - n_train;
+    const float s = block_sum(partial_share(Q, i, 1, q_ld, 0, q_ld), red);
+    if (threadIdx.x == 0) out_bdot[i] = s;
+    return;
+  }
+  if (grad == nullptr) return;
+  const int64_t f = (b - 2 * n_train) * blockDim.x + threadIdx.x;
+  if (f >= F) return;
+  float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+  int64_t k = 0;
+  for (; k + 4 <= n_train; k += 4) {
+    t0 += BS[k * F + f];
+    t1 += BS[(k + 1) * F + f];
+    t2 += BS[(k + 2) * F + f];
+    t3 += BS[(k + 3) * F + f];
+  }
+  for (; k < n_train; ++k) t0 += BS[k * F + f];
+  grad[f] = from_f32<GE>(scale * ((t0 + t1) + (t2 + t3)));
 }
 
 // out[f][c] = row c of the row set, feature f (with `presum`: c = position, summed over all
@@ -982,6 +1153,14 @@ namespace {
 template <class C>
 using DmaFor = std::conditional_t<3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
                                   DmaCfg<C, GS_WIDE_DMA>>;
+// The row-dot kernel's stage geometry (GS_ROWDOT_DMACFG = row bytes, stages) or DmaFor.
+#ifdef GS_ROWDOT_DMACFG
+template <class C, int EPI>
+using DmaForEpi = std::conditional_t<EPI == EPI_ROWDOT, DmaCfg<C, GS_ROWDOT_DMACFG>, DmaFor<C>>;
+#else
+template <class C, int EPI>
+using DmaForEpi = DmaFor<C>;
+#endif
 #ifndef GS_ROWDOT_DMA
 #define GS_ROWDOT_DMA 1
 #endif
@@ -999,7 +1178,7 @@ struct Launch {
     if (blocks <= 0) return GS_OK;
     if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
-    using D = DmaFor<C>;
+    using D = DmaForEpi<C, EPI>;
     if constexpr (std::is_same<Tr, TrBF16>::value &&
                   D::STAGES * D::STAGE_BYTES <= 160 * 1024) {
       const bool on = EPI == EPI_GHOST || (EPI == EPI_ROWDOT && GS_ROWDOT_DMA) ||
@@ -1418,4 +1597,150 @@ extern "C" int gs_linear_rowdot(const void* A, const void* G, const void* V, int
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s, P,
                      int64_t{1}, pl.n_mt, pl.p_ld, pl.cols, n_t, nullptr, out_dot);
   return check_launch("reduce_partials_kernel");
+}
+
+// ------------------------------------------------------------------ row-dot + bias, fused
+namespace gs {
+namespace {
+// The fused path needs every ROWDOT tile on the LDS-DMA kernel with its LDS epilogue.
+bool rowdot_bias_ok(int dtype, const void* A, const void* G, const void* V, int64_t N,
+                    int64_t T, int64_t d_in, int64_t d_out) {
+  using RC = RowdotCfg<TrBF16>;
+  if (dtype != GS_DTYPE_BF16 || !GS_USE_DMA || !GS_ROWDOT_DMA) return false;
+  if (T % RC::BN != 0 || d_out % RC::BM != 0 || d_in % 8 != 0 || d_out % 8 != 0) return false;
+  const int64_t ga = N * T * d_in * 2, gg = N * T * d_out * 2, gv = d_out * d_in * 2;
+  if (ga >= INT32_MAX || gg >= INT32_MAX || gv >= INT32_MAX) return false;
+  if (A != nullptr && !(aligned16(A) && aligned16(G) && aligned16(V))) return false;
+  return true;
+}
+}  // namespace
+}  // namespace gs
+
+namespace gs {
+namespace {
+// Workspace layout of the fused row-dot + bias path.
+struct RowdotBiasPlan {
+  RowdotPlan pl;
+  int64_t n_t, n_tiles, tps, vp_rows, col_blocks;
+};
+RowdotBiasPlan plan_rowdot_bias(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
+  using RC = RowdotCfg<TrBF16>;
+  RowdotBiasPlan b;
+  b.pl = plan_rowdot_any(dtype, N, n_val, T, d_out);
+  b.n_t = N - n_val;
+  b.tps = T / RC::BN;
+  b.n_tiles = b.n_t * b.tps;
+  b.vp_rows = ceil_div(n_val * T, static_cast<int64_t>(VS_ROWS));
+  b.col_blocks = ceil_div(d_out, int64_t{256});
+  return b;
+}
+// P (weight-dot partials), BP (tile column sums), VP (val column sums), Q (bias-dot
+// shares per sample and column block), BS (train column sums per sample), in this order.
+void rowdot_bias_sizes(const RowdotBiasPlan& b, int64_t d_out, size_t (&n)[5]) {
+  n[0] = b.pl.n_mt * b.pl.p_ld;
+  n[1] = b.n_tiles * d_out;
+  n[2] = b.vp_rows * d_out;
+  n[3] = b.n_t * b.col_blocks;
+  n[4] = b.n_t * d_out;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                                  int64_t d_in, int64_t d_out) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
+    return 0;
+  if (!rowdot_bias_ok(dtype, nullptr, nullptr, nullptr, N, T, d_in, d_out)) return 0;
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  size_t n[5];
+  rowdot_bias_sizes(b, d_out, n);
+  Sizer sz;
+  for (size_t k : n) sz.take<float>(k);
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype,
+                                     int64_t N, int64_t n_val, int64_t val_start, int64_t T,
+                                     int64_t d_in, int64_t d_out, float* out_dot,
+                                     float* out_bias_dot, void* out_bias_grad, int grad_dtype,
+                                     float grad_scale, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: invalid shape");
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: val block outside the batch");
+  if (A == nullptr || G == nullptr || V == nullptr || out_dot == nullptr ||
+      out_bias_dot == nullptr)
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: null pointer");
+  if (grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_linear_rowdot_bias: grad_dtype must be bf16 or fp32");
+  if (!rowdot_bias_ok(dtype, A, G, V, N, T, d_in, d_out))
+    return fail(GS_ERR_UNSUPPORTED,
+                "gs_linear_rowdot_bias: needs bf16, 16-byte aligned operands below 2 GiB, "
+                "T a multiple of 256 and d_out a multiple of 256");
+  using RC = RowdotCfg<TrBF16>;
+  using RD = DmaForEpi<RC, EPI_ROWDOT>;
+  // Every tile must take the LDS epilogue, the only one that writes the tile column sums.
+  static_assert(static_cast<int64_t>(RC::BN) * RC::BM * 2 <= RD::STAGES * RD::STAGE_BYTES &&
+                    RD::STAGES * RD::STAGE_BYTES <= 160 * 1024,
+                "row-dot tile does not take the LDS epilogue");
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  if (workspace == nullptr ||
+      workspace_bytes < gs_linear_rowdot_bias_workspace(dtype, N, n_val, T, d_in, d_out) - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_rowdot_bias: workspace too small");
+  size_t n[5];
+  rowdot_bias_sizes(b, d_out, n);
+  Carver cv(workspace, workspace_bytes);
+  float* P = cv.take<float>(n[0]);
+  float* BP = cv.take<float>(n[1]);
+  float* VP = cv.take<float>(n[2]);
+  float* Q = cv.take<float>(n[3]);
+  float* BS = cv.take<float>(n[4]);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Val column sums of G (stage 1 of the val bias gradient).
+  const dim3 vgrid(static_cast<unsigned>(ceil_div(d_out, static_cast<int64_t>(VS_COLS))),
+                   static_cast<unsigned>(b.vp_rows));
+  hipLaunchKernelGGL(val_colsum_kernel, vgrid, dim3(256), 0, s,
+                     static_cast<const uint16_t*>(G) + val_start * T * d_out, n_val * T, d_out,
+                     VP);
+  int rc = check_launch("val_colsum_kernel");
+  if (rc) return rc;
+  const RowMap tr = train_rows(N, n_val, val_start, T);
+  GemmParams r{};
+  r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, 2, d_out * d_in * 2);
+  r.R1 = make_operand(A, d_in, tr, 0, d_in, 2, N * T * d_in * 2);
+  r.K1 = d_in;
+  r.m_tiles = b.pl.n_mt;
+  r.n_tiles = host_tiles<RC::BN>(r.R1);
+  r.m_rows = d_out;
+  r.P = P;
+  r.p_ld = b.pl.p_ld;
+  r.tile_reduce = b.pl.tile_reduce;
+  r.p_row0 = 0;
+  r.Z = G;
+  r.z_ld = d_out;
+  r.z_map = tr;
+  r.z_vec_ok = 1;
+  r.z_nbytes = N * T * d_out * 2;
+  r.BP = BP;
+  if (r.n_tiles != b.n_tiles || !b.pl.tile_reduce || !dma_ok(r.L1) || !dma_ok(r.R1))
+    return fail(GS_ERR_INVALID, "internal: row-dot tiles");
+  rc = Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
+  if (rc) return rc;
+  const dim3 cgrid(static_cast<unsigned>(b.col_blocks), static_cast<unsigned>(b.n_t));
+  hipLaunchKernelGGL(rowdot_bias_cols_kernel, cgrid, dim3(256), 0, s, VP, b.vp_rows, BP, b.tps,
+                     d_out, Q, b.col_blocks, BS);
+  rc = check_launch("rowdot_bias_cols_kernel");
+  if (rc) return rc;
+  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{256}) : 0;
+  const dim3 grid(static_cast<unsigned>(2 * b.n_t + gblocks));
+  if (grad_dtype == GS_DTYPE_F32)
+    hipLaunchKernelGGL(rowdot_bias_rows_kernel<float>, grid, dim3(256), 0, s, P, b.pl.n_mt,
+                       b.pl.p_ld, b.pl.cols, b.n_t, out_dot, Q, b.col_blocks, out_bias_dot, BS,
+                       d_out, static_cast<float*>(out_bias_grad), grad_scale);
+  else
+    hipLaunchKernelGGL(rowdot_bias_rows_kernel<uint16_t>, grid, dim3(256), 0, s, P, b.pl.n_mt,
+                       b.pl.p_ld, b.pl.cols, b.n_t, out_dot, Q, b.col_blocks, out_bias_dot, BS,
+                       d_out, static_cast<uint16_t*>(out_bias_grad), grad_scale);
+  return check_launch("rowdot_bias_rows_kernel");
 }

@@ -169,9 +169,36 @@ def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tens
     _should_use_ghost_computation(layer, A, B)
     pairwise = layer.use_ghost_computation
     if not _overwritten_later(layer):
-        _linear_like_dot(layer, A, B, val_batch_size, pairwise, _dot_dtype(A, pairwise))
+        dt = _dot_dtype(A, pairwise)
+        if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, pairwise, dt):
+            return
+        _linear_like_dot(layer, A, B, val_batch_size, pairwise, dt)
     if layer.bias is not None:
         _bias_dot_and_grad(layer, B, val_batch_size, _dot_dtype(B, False))
+
+
+def _fused_bias_dot(layer: nn.Module, A: torch.Tensor, B: torch.Tensor, val_batch_size: int,
+                    pairwise: bool, dtype: torch.dtype) -> bool:
+    """Weight dot, bias dot and bias train gradient from one pass over G, when the kernel
+    layer supports the shape (bf16 model, pairwise semantics, val-gradient algorithm).
+    Returns False when the separate weight and bias passes must run instead."""
+    if not pairwise or options["store_pairs"] or dtype != torch.bfloat16 or \
+            _dot_dtype(B, False) != torch.bfloat16:
+        return False
+    fused = ops().linear_bias_dot(
+        A.to(dtype), B.to(dtype), val_batch_size, semantics=_native.SEM_PAIRWISE_SUM,
+        algo=_ALGOS[options["linear_algo"]], rounding=_ROUNDINGS[options["rounding"]],
+        grad_scale=getattr(layer, "_gs_bias_grad_scale", None), grad_dtype=layer.bias.dtype)
+    if fused is None:
+        return False
+    dot, bias_dot, bias_grad = fused
+    layer.weight.grad_dot_prod = dot
+    layer.bias.grad_dot_prod = bias_dot
+    if bias_grad is not None:
+        layer._gs_bias_train_grad = bias_grad
+    if options["record_algorithms"]:
+        ALGO_LOG[getattr(layer, "name", id(layer))] = ("pairwise", "valgrad+bias")
+    return True
 
 
 def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tensor,

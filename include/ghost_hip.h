@@ -106,6 +106,25 @@ int gs_linear_rowdot(const void* A, const void* G, const void* V, int dtype, int
                      int64_t n_val, int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
                      float* out_dot, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Row-dot with the layer's bias folded into the same pass (reference: the weight and bias
+ * parts of _compute_linear_dot_product, :75-146, and _compute_train_grad_bias,
+ * autograd_grad_sample_dotprod.py:199-222):
+ *   out_dot[i]      = sum_t g_it^T V a_it                    (as gs_linear_rowdot)
+ *   out_bias_dot[i] = sum_t <g_it, vb>,   vb = sum over val rows and tokens of g (fp32)
+ *   out_bias_grad   = NULL, or grad_scale * sum over train rows and tokens of g ([d_out],
+ *                     grad_dtype)
+ * The row-dot epilogue sums each G tile it already holds in LDS over its tokens; those
+ * column sums give both bias terms, so the train rows of G are read once.
+ * Supported for bf16, 16-byte aligned operands below 2 GiB, T and d_out multiples of 256:
+ * the workspace query returns 0 otherwise (use gs_linear_rowdot + gs_bias_dot then). */
+size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                       int64_t d_in, int64_t d_out);
+int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype, int64_t N,
+                          int64_t n_val, int64_t val_start, int64_t T,
+                          int64_t d_in, int64_t d_out, float* out_dot, float* out_bias_dot,
+                          void* out_bias_grad, int grad_dtype, float grad_scale,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Bias dot product and bias train gradient ---------------------------------------
  * Replaces the bias part of _compute_linear_dot_product (:137-146), the bias part of
  * _compute_Conv1D_dot_product (:450-471) and _compute_train_grad_bias

@@ -27,6 +27,16 @@ class OracleOps:
                                       pair=True).float()
         return dot.to(A.device), pair
 
+    def linear_bias_dot(self, A, G, n_val, *, semantics=0, algo=0, rounding=0, grad_scale=None,
+                        grad_dtype=None):
+        """The fused weight + bias pass, as closed forms (pairwise semantics only)."""
+        if semantics != _native.SEM_PAIRWISE_SUM:
+            return None
+        self.calls.append(("linear_bias_dot", tuple(A.shape), tuple(G.shape)))
+        dot, _ = self.linear_dot(A, G, n_val, semantics=semantics)
+        bdot, grad = self.bias_dot(G, n_val, grad_scale=grad_scale, grad_dtype=grad_dtype)
+        return dot, bdot, grad
+
     def bias_dot(self, G, n_val, *, val_start=None, grad_scale=None, grad_dtype=None):
         self.calls.append(("bias_dot", tuple(G.shape)))
         dot = R.bias_dot_exact(G.float(), n_val, val_start).float()

@@ -140,3 +140,33 @@ def test_linear_rejects_bad_arguments(gpu):
         _native.ops().linear_dot(A, G.bfloat16(), 1)  # dtype mismatch
     with pytest.raises(_native.GhostHipError):
         _native.ops().linear_dot(A, G, 1, semantics=_native.SEM_PRESUM, want_pair=True)
+
+
+@pytest.mark.parametrize("shape", [(6, 2, 256, 128, 256), (5, 1, 512, 64, 512),
+                                   (4, 1, 256, 768, 768)])
+def test_linear_bias_fused_matches_closed_forms(gpu, shape):
+    """gs_linear_rowdot_bias: weight dot, bias dot and bias train gradient in one pass."""
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 400 + T, torch.bfloat16)
+    scale = N / (N - n_val) / 7.0
+    print(f"linear_bias_dot shape={shape}", flush=True)
+    res = _native.ops().linear_bias_dot(A.to(gpu), G.to(gpu), n_val,
+                                        algo=_native.ALGO_VALGRAD, grad_scale=scale,
+                                        grad_dtype=torch.float32)
+    assert res is not None
+    dot, bdot, bgrad = res
+    torch.cuda.synchronize()
+    assert_close(dot.cpu(), R.linear_dot_exact(A, G, n_val, "pairwise"), BF16_TOL, "weight dot")
+    assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
+    assert_close(bgrad.cpu(), R.bias_train_grad(G.double() * N, n_val) * (1 / 7.0), BF16_TOL,
+                 "bias grad")
+
+
+def test_linear_bias_fused_declines_unsupported_shapes(gpu):
+    ops = _native.ops()
+    A, G = _inputs(6, 100, 64, 256, 5, torch.bfloat16)        # T not a multiple of 256
+    assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None
+    A, G = _inputs(6, 256, 64, 200, 6, torch.bfloat16)        # d_out not a multiple of 256
+    assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None
+    A, G = _inputs(6, 256, 64, 256, 7, torch.float32)         # fp32 operands
+    assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None

@@ -64,6 +64,9 @@ _SIGNATURES = {
     "gs_kron_embed_proj": (_I, [_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _F,
                                 _P, _I, _P, _SZ, _P]),
     "gs_linear_rowdot_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
+    "gs_linear_val_gradient_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I]),
+    "gs_linear_val_gradient": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                                    _P, _SZ, _P]),
     "gs_linear_rowdot_bias_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
     "gs_linear_rowdot_bias": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
                                    _P, _I, _F, _P, _SZ, _P]),
@@ -216,17 +219,48 @@ class HipOps:
         V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
         return self.linear_rowdot(A, G, V, n_val, val_start=vs)
 
+    def linear_val_gradient(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
+                            val_start=None, semantics: int = SEM_PAIRWISE_SUM) -> torch.Tensor:
+        """The val term V [d_out, d_in] of the val-gradient algorithm (gs_linear_val_gradient):
+        sum over the val rows of g a^T, or with SEM_PRESUM the product of the val rows
+        presummed per token position."""
+        dev = _require_device(A, G)
+        if A.dtype != G.dtype:
+            raise GhostHipError(f"A and G dtypes differ: {A.dtype} vs {G.dtype}")
+        A = A.contiguous()
+        G = G.contiguous()
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T:
+            raise GhostHipError(f"A {tuple(A.shape)} and G {tuple(G.shape)} token counts differ")
+        vs = N - n_val if val_start is None else int(val_start)
+        dt = _gs_dtype(A)
+        lib = load_library()
+        ws_bytes = lib.gs_linear_val_gradient_workspace(dt, N, n_val, T, d_in, d_out, semantics)
+        if ws_bytes == 0:
+            raise GhostHipError(f"gs_linear_val_gradient: invalid arguments N={N} n_val={n_val} "
+                                f"T={T} d_in={d_in} d_out={d_out} semantics={semantics}")
+        ws = _workspace(ws_bytes, dev)
+        V = torch.empty((d_out, d_in), dtype=A.dtype, device=dev)
+        rc = lib.gs_linear_val_gradient(A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in,
+                                        d_out, semantics, V.data_ptr(), ws.data_ptr(), ws_bytes,
+                                        _stream(dev))
+        _check(rc, "gs_linear_val_gradient")
+        return V
+
     def linear_bias_dot(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
                         semantics: int = SEM_PAIRWISE_SUM, algo: int = ALGO_AUTO,
                         rounding: int = ROUND_FP32, grad_scale: Optional[float] = None,
                         grad_dtype: Optional[torch.dtype] = None):
         """Weight and bias dots of a Linear layer (and the bias train gradient when
-        grad_scale is given) in one pass when the shape allows it, i.e. the val-gradient
-        algorithm with the library V GEMM and gs_linear_rowdot_bias; otherwise None (the
-        caller then uses linear_dot and bias_dot).  Returns (dot, bias_dot, bias_grad)."""
+        grad_scale is given) in one pass over the train rows when the shape allows it: the
+        val-gradient algorithm with gs_linear_rowdot_bias, V from torch.mm (pairwise, library
+        V GEMM) or gs_linear_val_gradient.  Otherwise None (the caller then uses linear_dot
+        and bias_dot).  Returns (dot, bias_dot, bias_grad)."""
         dev = _require_device(A, G)
-        if A.dtype != G.dtype or A.dtype != torch.bfloat16 or V_GEMM != "library" or \
-                semantics != SEM_PAIRWISE_SUM or \
+        if A.dtype != G.dtype or A.dtype != torch.bfloat16 or \
+                semantics not in (SEM_PAIRWISE_SUM, SEM_PRESUM) or \
                 (grad_dtype or G.dtype) not in (torch.bfloat16, torch.float32):
             return None
         N = A.shape[0]
@@ -246,9 +280,12 @@ class HipOps:
         A = A.contiguous()
         G = G.contiguous()
         vs = N - n_val
-        Av = A.view(N, T, d_in)[vs:]
-        Gv = G.view(N, T, d_out)[vs:]
-        V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
+        if semantics == SEM_PAIRWISE_SUM and V_GEMM == "library":
+            Av = A.view(N, T, d_in)[vs:]
+            Gv = G.view(N, T, d_out)[vs:]
+            V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
+        else:
+            V = self.linear_val_gradient(A, G, n_val, val_start=vs, semantics=semantics)
         ws = _workspace(ws_bytes, dev)
         out = torch.empty(n_t, dtype=torch.float32, device=dev)
         bout = torch.empty(n_t, dtype=torch.float32, device=dev)

@@ -1350,6 +1350,50 @@ int launch_rowdot(const void* A, const void* G, const void* V, int64_t N, int64_
   return Launch<Tr, RC>::template run<EPI_ROWDOT>(r, r.L1.vec_ok && r.R1.vec_ok, s);
 }
 
+// Transposed val operands of the val-gradient GEMM: At [d_in][vcols], Gt [d_out][vcols]
+// (column c = val token c, or with `presum` position c summed over the val rows).
+template <class Tr>
+int transpose_val(const void* A, const void* G, int64_t d_in, int64_t d_out, const RowMap& va,
+                  int presum, int64_t vcols, typename Tr::E* At, typename Tr::E* Gt,
+                  hipStream_t s) {
+  using E = typename Tr::E;
+  const size_t esz = sizeof(E);
+  const dim3 ga(static_cast<unsigned>(ceil_div(d_in, 64)),
+                static_cast<unsigned>(ceil_div(vcols, 64)));
+  const dim3 gg(static_cast<unsigned>(ceil_div(d_out, 64)),
+                static_cast<unsigned>(ceil_div(vcols, 64)));
+  const int vec_a = aligned16(A) && aligned16(At) && (d_in * esz) % 16 == 0 &&
+                    (vcols * esz) % 16 == 0;
+  const int vec_g = aligned16(G) && aligned16(Gt) && (d_out * esz) % 16 == 0 &&
+                    (vcols * esz) % 16 == 0;
+  hipLaunchKernelGGL(transpose_rows_kernel<E>, ga, dim3(256), 0, s, static_cast<const E*>(A),
+                     d_in, va, d_in, presum, vec_a, At, vcols);
+  hipLaunchKernelGGL(transpose_rows_kernel<E>, gg, dim3(256), 0, s, static_cast<const E*>(G),
+                     d_out, va, d_out, presum, vec_g, Gt, vcols);
+  return check_launch("transpose_rows_kernel");
+}
+
+// V = Gt[:, k0 : k0 + kper] At[:, k0 : k0 + kper]^T -> V [d_out][d_in] (the STORE GEMM).
+template <class Tr>
+int store_v(const typename Tr::E* Gt, const typename Tr::E* At, int64_t vcols, int64_t k0,
+            int64_t kper, int64_t d_in, int64_t d_out, typename Tr::E* V, hipStream_t s) {
+  using SC = StoreCfg<Tr>;
+  const size_t esz = sizeof(typename Tr::E);
+  GemmParams q{};
+  q.L1 = make_operand(Gt + k0, vcols, plain_rows(d_out), 0, kper, esz,
+                      (d_out * vcols - k0) * static_cast<int64_t>(esz));
+  q.R1 = make_operand(At + k0, vcols, plain_rows(d_in), 0, kper, esz,
+                      (d_in * vcols - k0) * static_cast<int64_t>(esz));
+  q.K1 = kper;
+  q.m_tiles = host_tiles<SC::BM>(q.L1);
+  q.n_tiles = host_tiles<SC::BN>(q.R1);
+  q.m_rows = d_out;
+  q.n_cols = d_in;
+  q.C = V;
+  q.c_ld = d_in;
+  return Launch<Tr, SC>::template run<EPI_STORE>(q, q.L1.vec_ok && q.R1.vec_ok, s);
+}
+
 template <class Tr>
 int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t val_start,
                int64_t T, int64_t d_in, int64_t d_out, int semantics, int rounding,
@@ -1357,7 +1401,6 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   using E = typename Tr::E;
   using GC = GhostCfg<Tr>;
   using RC = RowdotCfg<Tr>;
-  using SC = StoreCfg<Tr>;
   const size_t esz = sizeof(E);
   const int64_t n_t = N - n_val;
   const RowMap tr = train_rows(N, n_val, val_start, T);
@@ -1436,41 +1479,14 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   E* V = reinterpret_cast<E*>(cv.take<char>(d_out * d_in * esz));
   float* P = cv.take<float>(pl.p_rows * pl.p_ld);
   const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
-  {
-    const dim3 ga(static_cast<unsigned>(ceil_div(d_in, 64)),
-                  static_cast<unsigned>(ceil_div(pl.vcols, 64)));
-    const dim3 gg(static_cast<unsigned>(ceil_div(d_out, 64)),
-                  static_cast<unsigned>(ceil_div(pl.vcols, 64)));
-    const int vec_a = aligned16(A) && aligned16(At) && (d_in * esz) % 16 == 0 &&
-                      (pl.vcols * esz) % 16 == 0;
-    const int vec_g = aligned16(G) && aligned16(Gt) && (d_out * esz) % 16 == 0 &&
-                      (pl.vcols * esz) % 16 == 0;
-    hipLaunchKernelGGL(transpose_rows_kernel<E>, ga, dim3(256), 0, s, static_cast<const E*>(A),
-                       d_in, va, d_in, presum, vec_a, At, pl.vcols);
-    hipLaunchKernelGGL(transpose_rows_kernel<E>, gg, dim3(256), 0, s, static_cast<const E*>(G),
-                       d_out, va, d_out, presum, vec_g, Gt, pl.vcols);
-    int rc = check_launch("transpose_rows_kernel");
-    if (rc) return rc;
-  }
+  int rc = transpose_val<Tr>(A, G, d_in, d_out, va, presum, pl.vcols, At, Gt, s);
+  if (rc) return rc;
   const int64_t n_mt = ceil_div(d_out, RC::BM);
   const int64_t vsteps = pl.groups;  // one V per val row for pairs, else one V
   const int64_t kper = pl.vcols / vsteps;
   for (int64_t j = 0; j < vsteps; ++j) {
-    GemmParams q{};
-    q.L1 = make_operand(Gt + j * kper, pl.vcols, plain_rows(d_out), 0, kper, esz,
-                        (d_out * pl.vcols - j * kper) * static_cast<int64_t>(esz));
-    q.R1 = make_operand(At + j * kper, pl.vcols, plain_rows(d_in), 0, kper, esz,
-                        (d_in * pl.vcols - j * kper) * static_cast<int64_t>(esz));
-    q.K1 = kper;
-    q.m_tiles = host_tiles<SC::BM>(q.L1);
-    q.n_tiles = host_tiles<SC::BN>(q.R1);
-    q.m_rows = d_out;
-    q.n_cols = d_in;
-    q.C = V;
-    q.c_ld = d_in;
-    int rc = Launch<Tr, SC>::template run<EPI_STORE>(q, q.L1.vec_ok && q.R1.vec_ok, s);
+    rc = store_v<Tr>(Gt, At, pl.vcols, j * kper, kper, d_in, d_out, V, s);
     if (rc) return rc;
-
     rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
                            pl.tile_reduce, j * n_mt, s);
     if (rc) return rc;
@@ -1530,6 +1546,56 @@ extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N,
                               out_dot, out_pair, pl, cv, s);
   return run_linear<TrF32>(A, G, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
                            out_dot, out_pair, pl, cv, s);
+}
+
+// ------------------------------------------------------------------ val gradient V
+extern "C" size_t gs_linear_val_gradient_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                                   int64_t d_in, int64_t d_out, int semantics) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, GS_ALGO_AUTO, 0)) return 0;
+  const int64_t vcols = (semantics == GS_SEM_PRESUM ? 1 : n_val) * T;
+  const size_t esz = elem_size(dtype);
+  Sizer sz;
+  sz.take<char>(d_in * vcols * esz);
+  sz.take<char>(d_out * vcols * esz);
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_val_gradient(const void* A, const void* G, int dtype, int64_t N,
+                                      int64_t n_val, int64_t val_start, int64_t T, int64_t d_in,
+                                      int64_t d_out, int semantics, void* V, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, GS_ALGO_AUTO, 0))
+    return fail(GS_ERR_INVALID, "gs_linear_val_gradient: invalid shape, dtype or semantics");
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, "gs_linear_val_gradient: val block outside the batch");
+  if (A == nullptr || G == nullptr || V == nullptr)
+    return fail(GS_ERR_INVALID, "gs_linear_val_gradient: null pointer");
+  if (workspace == nullptr ||
+      workspace_bytes < gs_linear_val_gradient_workspace(dtype, N, n_val, T, d_in, d_out,
+                                                         semantics) - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_val_gradient: workspace too small");
+  const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
+  const int64_t vcols = (presum ? 1 : n_val) * T;
+  const RowMap va = val_rows(n_val, val_start, T);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv(workspace, workspace_bytes);
+  const size_t esz = elem_size(dtype);
+  void* At = cv.take<char>(d_in * vcols * esz);
+  void* Gt = cv.take<char>(d_out * vcols * esz);
+  if (dtype == GS_DTYPE_BF16) {
+    using E = TrBF16::E;
+    int rc = transpose_val<TrBF16>(A, G, d_in, d_out, va, presum, vcols, static_cast<E*>(At),
+                                   static_cast<E*>(Gt), s);
+    if (rc) return rc;
+    return store_v<TrBF16>(static_cast<E*>(Gt), static_cast<E*>(At), vcols, 0, vcols, d_in,
+                           d_out, static_cast<E*>(V), s);
+  }
+  using E = TrF32::E;
+  int rc = transpose_val<TrF32>(A, G, d_in, d_out, va, presum, vcols, static_cast<E*>(At),
+                                static_cast<E*>(Gt), s);
+  if (rc) return rc;
+  return store_v<TrF32>(static_cast<E*>(Gt), static_cast<E*>(At), vcols, 0, vcols, d_in, d_out,
+                        static_cast<E*>(V), s);
 }
 
 // ------------------------------------------------------------------ row-dot with a given V

@@ -170,7 +170,8 @@ def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tens
     pairwise = layer.use_ghost_computation
     if not _overwritten_later(layer):
         dt = _dot_dtype(A, pairwise)
-        if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, pairwise, dt):
+        if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, pairwise, dt,
+                                                      _dot_dtype(B, False)):
             return
         _linear_like_dot(layer, A, B, val_batch_size, pairwise, dt)
     if layer.bias is not None:
@@ -178,15 +179,16 @@ def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tens
 
 
 def _fused_bias_dot(layer: nn.Module, A: torch.Tensor, B: torch.Tensor, val_batch_size: int,
-                    pairwise: bool, dtype: torch.dtype) -> bool:
-    """Weight dot, bias dot and bias train gradient from one pass over G, when the kernel
-    layer supports the shape (bf16 model, pairwise semantics, val-gradient algorithm).
-    Returns False when the separate weight and bias passes must run instead."""
-    if not pairwise or options["store_pairs"] or dtype != torch.bfloat16 or \
-            _dot_dtype(B, False) != torch.bfloat16:
+                    pairwise: bool, dtype: torch.dtype, bias_dtype: torch.dtype) -> bool:
+    """Weight dot, bias dot and bias train gradient from one pass over the train rows of B,
+    when the kernel layer supports the shape (bf16 dots, val-gradient algorithm).  Returns
+    False when the separate weight and bias passes must run instead."""
+    if (pairwise and options["store_pairs"]) or dtype != torch.bfloat16 or \
+            bias_dtype != torch.bfloat16:
         return False
+    sem = _native.SEM_PAIRWISE_SUM if pairwise else _native.SEM_PRESUM
     fused = ops().linear_bias_dot(
-        A.to(dtype), B.to(dtype), val_batch_size, semantics=_native.SEM_PAIRWISE_SUM,
+        A.to(dtype), B.to(dtype), val_batch_size, semantics=sem,
         algo=_ALGOS[options["linear_algo"]], rounding=_ROUNDINGS[options["rounding"]],
         grad_scale=getattr(layer, "_gs_bias_grad_scale", None), grad_dtype=layer.bias.dtype)
     if fused is None:
@@ -197,7 +199,8 @@ def _fused_bias_dot(layer: nn.Module, A: torch.Tensor, B: torch.Tensor, val_batc
     if bias_grad is not None:
         layer._gs_bias_train_grad = bias_grad
     if options["record_algorithms"]:
-        ALGO_LOG[getattr(layer, "name", id(layer))] = ("pairwise", "valgrad+bias")
+        ALGO_LOG[getattr(layer, "name", id(layer))] = ("pairwise" if pairwise else "presum",
+                                                       "valgrad+bias")
     return True
 
 
@@ -335,6 +338,8 @@ def _compute_Conv1D_dot_product(layer, A: torch.Tensor, B: torch.Tensor, val_bat
         raise ValueError("Currently we only expect 3D input tensors (batch, seq_len, features). "
                          "Extending this to 4D or higher requires additional handling.")
     dt = torch.float32 if options["precision"] == "fp32" else torch.bfloat16
+    if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, False, dt, dt):
+        return
     _linear_like_dot(layer, A, B, val_batch_size, False, dt)
     if layer.bias is not None:
         _bias_dot_and_grad(layer, B, val_batch_size, dt)

@@ -94,6 +94,21 @@ int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_
                   int algo, int rounding, float* out_dot, float* out_pair, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* The val term of a Linear layer's dot, V [d_out, d_in] (dtype; fp32 accumulation):
+ *   GS_SEM_PAIRWISE_SUM: V = sum over the val rows and tokens of g a^T
+ *   GS_SEM_PRESUM:       V = gbar^T abar, gbar / abar = the val rows summed over the val
+ *                        samples per token position (how the reference's materialised
+ *                        branch forms its val term)
+ * Reference: the val half of _compute_linear_dot_product
+ * (supported_layers_grad_samplers_dotprod.py:75-135); the V gs_linear_rowdot and
+ * gs_linear_rowdot_bias take. */
+size_t gs_linear_val_gradient_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                        int64_t d_in, int64_t d_out, int semantics);
+int gs_linear_val_gradient(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                           int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                           int semantics, void* V, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 /* Row-dot with a caller-formed val gradient V = G_val^T A_val ([d_out, d_in], same dtype):
  *   out_dot[i] = sum_t g_it^T V a_it over the train rows (the second half of the
  *   VALGRAD algorithm of gs_linear_dot, for callers that form V with a library GEMM).

@@ -109,6 +109,24 @@ def per_sample_linear_grads(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     return torch.einsum('ntp,ntd->npd', b, a)
 
 
+def val_term_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, semantics: str = "pairwise",
+                   val_start: Optional[int] = None) -> torch.Tensor:
+    """The val term V [d_out, d_in] (float64) the two semantics dot the train gradients with:
+    pairwise sum_j G_j (the summed per-sample val gradients), presum (sum_j b_j)^T (sum_j a_j)
+    (the materialised branch sums the val activations and backprops over the val samples
+    per token position before the product, supported_layers_grad_samplers_dotprod.py:108-135).
+    """
+    N = A.shape[0]
+    d, p = A.shape[-1], B.shape[-1]
+    _, va_a = split_rows(A.double().reshape(N, -1, d), n_val, val_start)
+    _, va_b = split_rows(B.double().reshape(N, -1, p), n_val, val_start)
+    if semantics == "pairwise":
+        return torch.einsum('ntp,ntd->pd', va_b, va_a)
+    if semantics == "presum":
+        return torch.einsum('tp,td->pd', va_b.sum(0), va_a.sum(0))
+    raise ValueError(semantics)
+
+
 def linear_dot_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, semantics: str = "pairwise",
                      val_start: Optional[int] = None, pair: bool = False):
     """Float64 closed forms.
@@ -122,17 +140,12 @@ def linear_dot_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, semantics: st
     tr_a, va_a = split_rows(A.double().reshape(N, -1, d), n_val, val_start)
     tr_b, va_b = split_rows(B.double().reshape(N, -1, p), n_val, val_start)
     G_tr = torch.einsum('ntp,ntd->npd', tr_b, tr_a)
-    if semantics == "pairwise":
+    if semantics == "pairwise" and pair:
         G_va = torch.einsum('ntp,ntd->npd', va_b, va_a)
-        if pair:
-            return torch.einsum('ipd,jpd->ji', G_tr, G_va)
-        return torch.einsum('ipd,pd->i', G_tr, G_va.sum(0))
-    if semantics == "presum":
-        if pair:
-            raise ValueError("presum has no per-pair form")
-        V = torch.einsum('tp,td->pd', va_b.sum(0), va_a.sum(0))
-        return torch.einsum('ipd,pd->i', G_tr, V)
-    raise ValueError(semantics)
+        return torch.einsum('ipd,jpd->ji', G_tr, G_va)
+    if semantics == "presum" and pair:
+        raise ValueError("presum has no per-pair form")
+    return torch.einsum('ipd,pd->i', G_tr, val_term_exact(A, B, n_val, semantics, val_start))
 
 
 def bias_dot_exact(B: torch.Tensor, n_val: int, val_start: Optional[int] = None) -> torch.Tensor:

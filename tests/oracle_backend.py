@@ -29,9 +29,7 @@ class OracleOps:
 
     def linear_bias_dot(self, A, G, n_val, *, semantics=0, algo=0, rounding=0, grad_scale=None,
                         grad_dtype=None):
-        """The fused weight + bias pass, as closed forms (pairwise semantics only)."""
-        if semantics != _native.SEM_PAIRWISE_SUM:
-            return None
+        """The fused weight + bias pass, as closed forms."""
         self.calls.append(("linear_bias_dot", tuple(A.shape), tuple(G.shape)))
         dot, _ = self.linear_dot(A, G, n_val, semantics=semantics)
         bdot, grad = self.bias_dot(G, n_val, grad_scale=grad_scale, grad_dtype=grad_dtype)

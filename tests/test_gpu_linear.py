@@ -142,21 +142,40 @@ def test_linear_rejects_bad_arguments(gpu):
         _native.ops().linear_dot(A, G, 1, semantics=_native.SEM_PRESUM, want_pair=True)
 
 
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_linear_val_gradient_matches_closed_form(gpu, shape, dtype, semantics):
+    N, n_val, T, d_in, d_out = shape
+    print(f"linear_val_gradient shape={shape} dtype={dtype} sem={semantics}", flush=True)
+    A, G = _inputs(N, T, d_in, d_out, 300 + N + T, dtype)
+    sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
+    V = _native.ops().linear_val_gradient(A.to(gpu), G.to(gpu), n_val, val_start=1,
+                                          semantics=sem)
+    torch.cuda.synchronize()
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert V.shape == (d_out, d_in) and V.dtype == dtype
+    assert_close(V.cpu().double(), R.val_term_exact(A, G, n_val, semantics, val_start=1), tol,
+                 f"val term {semantics}")
+
+
 @pytest.mark.parametrize("shape", [(6, 2, 256, 128, 256), (5, 1, 512, 64, 512),
                                    (4, 1, 256, 768, 768)])
-def test_linear_bias_fused_matches_closed_forms(gpu, shape):
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_linear_bias_fused_matches_closed_forms(gpu, shape, semantics):
     """gs_linear_rowdot_bias: weight dot, bias dot and bias train gradient in one pass."""
     N, n_val, T, d_in, d_out = shape
     A, G = _inputs(N, T, d_in, d_out, 400 + T, torch.bfloat16)
     scale = N / (N - n_val) / 7.0
-    print(f"linear_bias_dot shape={shape}", flush=True)
-    res = _native.ops().linear_bias_dot(A.to(gpu), G.to(gpu), n_val,
+    print(f"linear_bias_dot shape={shape} sem={semantics}", flush=True)
+    sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
+    res = _native.ops().linear_bias_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem,
                                         algo=_native.ALGO_VALGRAD, grad_scale=scale,
                                         grad_dtype=torch.float32)
     assert res is not None
     dot, bdot, bgrad = res
     torch.cuda.synchronize()
-    assert_close(dot.cpu(), R.linear_dot_exact(A, G, n_val, "pairwise"), BF16_TOL, "weight dot")
+    assert_close(dot.cpu(), R.linear_dot_exact(A, G, n_val, semantics), BF16_TOL, "weight dot")
     assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
     assert_close(bgrad.cpu(), R.bias_train_grad(G.double() * N, n_val) * (1 / 7.0), BF16_TOL,
                  "bias grad")

@@ -63,6 +63,9 @@ def test_linear_closed_forms_match_per_sample_gradients(shape):
     assert_close(R.linear_dot_exact(A, B, n_val, "pairwise", pair=True),
                  brute.pair_matrix(gw, n_val), 1e-10, "pair")
     assert_close(R.bias_dot_exact(B, n_val), brute.pairwise_dots(gb, n_val), 1e-10, "bias")
+    # the pairwise val term is the summed per-sample val gradient
+    assert_close(R.val_term_exact(A, B, n_val, "pairwise"), gw[N - n_val:].sum(0), 1e-10,
+                 "val term")
     # train gradient: sum over train rows of (N * g_i) / n_train
     assert_close(R.linear_train_grad(A, B * N, n_val), brute.train_mean(gw, n_val, N), 1e-10,
                  "train grad")
@@ -83,6 +86,10 @@ def test_presum_by_explicit_token_loops():
             for s in range(T):
                 want[i] += (A[i, t] @ abar[s]) * (B[i, t] @ bbar[s])
     assert_close(R.linear_dot_exact(A, B, n_val, "presum"), want, 1e-12, "presum loops")
+    V = torch.zeros(d_out, d_in, dtype=torch.float64)
+    for t in range(T):
+        V += torch.outer(bbar[t], abar[t])
+    assert_close(R.val_term_exact(A, B, n_val, "presum"), V, 1e-12, "presum val term")
     # presum == pairwise when there is one val row
     assert_close(R.linear_dot_exact(A[:4], B[:4], 1, "presum"),
                  R.linear_dot_exact(A[:4], B[:4], 1, "pairwise"), 1e-12, "n_val=1")

@@ -182,6 +182,124 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
   }
 }
 
+// Stage 1 for 16-byte aligned rows: RW token rows per wave at a time (LPR = 64 / RW lanes
+// per row, PC 16-byte chunks per lane), so a 768-feature bf16 row keeps all 64 lanes busy
+// with two rows in flight; the next rows' raw chunks are loaded while the current ones are
+// reduced.  Mean/rstd by shuffles inside each LPR-lane group (two passes over registers).
+// LN2_WAVES waves per block over LN_TOK_CHUNK tokens; the wave x row-group sums combine
+// through LDS [LN2_WAVES * RW][F] (x2) in a fixed order.
+constexpr int LN2_WAVES = 4;
+template <class E, int PC, int RW>
+__global__ void __launch_bounds__(64 * LN2_WAVES) ln_rows_kernel(
+    const E* __restrict__ X, const E* __restrict__ G, int64_t T, int64_t F, float eps,
+    int64_t chunks, float* __restrict__ part_w, float* __restrict__ part_b) {
+  constexpr int VE = 16 / sizeof(E), LPR = 64 / RW, NR = LN2_WAVES * RW;
+  extern __shared__ float sm[];  // [NR][F] for w, then [NR][F] for b
+  const int64_t n = blockIdx.y, c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int rh = lane / LPR, li = lane % LPR;
+  const int64_t t0 = c * LN_TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + LN_TOK_CHUNK);
+  float aw[PC][VE], ab[PC][VE];
+#pragma unroll
+  for (int k = 0; k < PC; ++k)
+#pragma unroll
+    for (int i = 0; i < VE; ++i) aw[k][i] = ab[k][i] = 0.f;
+  const float invF = 1.0f / static_cast<float>(F);
+  uint4 xr[PC], gr[PC], xq[PC], gq[PC];
+  auto load = [&](int64_t t, uint4 (&xd)[PC], uint4 (&gd)[PC]) {
+    const bool row_ok = t < t1;
+#pragma unroll
+    for (int k = 0; k < PC; ++k) {
+      const int64_t f = static_cast<int64_t>(li + LPR * k) * VE;
+      if (row_ok && f < F) {
+        xd[k] = *reinterpret_cast<const uint4*>(X + (n * T + t) * F + f);
+        gd[k] = *reinterpret_cast<const uint4*>(G + (n * T + t) * F + f);
+      } else {
+        xd[k] = make_uint4(0u, 0u, 0u, 0u);
+        gd[k] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  auto widen = [](const uint4& u, float (&v)[VE]) {
+    union { uint4 u; E e[VE]; } w;
+    w.u = u;
+#pragma unroll
+    for (int i = 0; i < VE; ++i) v[i] = to_f32<E>(w.e[i]);
+  };
+  auto group_sum = [](float v) {
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+  };
+  constexpr int STEP = LN2_WAVES * RW;  // token rows per block-wide pass
+  int64_t t = t0 + wid * RW + rh;
+  load(t, xr, gr);
+  for (int64_t base = t0; base < t1; base += STEP, t += STEP) {
+    load(t + STEP, xq, gq);
+    if (t < t1) {
+      float x[PC][VE];
+#pragma unroll
+      for (int k = 0; k < PC; ++k) widen(xr[k], x[k]);
+      float sx = 0.f;
+#pragma unroll
+      for (int k = 0; k < PC; ++k)
+#pragma unroll
+        for (int i = 0; i < VE; ++i) sx += x[k][i];
+      const float mean = group_sum(sx) * invF;
+      float var = 0.f;
+#pragma unroll
+      for (int k = 0; k < PC; ++k) {
+        if (static_cast<int64_t>(li + LPR * k) * VE < F) {
+#pragma unroll
+          for (int i = 0; i < VE; ++i) {
+            const float d = x[k][i] - mean;
+            var += d * d;
+          }
+        }
+      }
+      const float rstd = rsqrtf(group_sum(var) * invF + eps);
+#pragma unroll
+      for (int k = 0; k < PC; ++k) {
+        float g[VE];
+        widen(gr[k], g);
+#pragma unroll
+        for (int i = 0; i < VE; ++i) {
+          aw[k][i] += g[i] * ((x[k][i] - mean) * rstd);
+          ab[k][i] += g[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < PC; ++k) {
+      xr[k] = xq[k];
+      gr[k] = gq[k];
+    }
+  }
+  const int r = wid * RW + rh;
+#pragma unroll
+  for (int k = 0; k < PC; ++k) {
+    const int64_t f = static_cast<int64_t>(li + LPR * k) * VE;
+    if (f < F) {
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        sm[r * F + f + i] = aw[k][i];
+        sm[(NR + r) * F + f + i] = ab[k][i];
+      }
+    }
+  }
+  __syncthreads();
+  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+    float w = 0.f, b = 0.f;
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      w += sm[q * F + f];
+      b += sm[(NR + q) * F + f];
+    }
+    part_w[(n * chunks + c) * F + f] = w;
+    if (part_b != nullptr) part_b[(n * chunks + c) * F + f] = b;
+  }
+}
+
 // ---------------------------------------------------------------- stage 2/3 (shared)
 // One or two feature sets (bias: g; LayerNorm: g*xhat and g) share each launch; blockIdx.z
 // (totals) / blockIdx.y (finish) selects the set.
@@ -437,6 +555,16 @@ void launch_ln(const void* X, const void* G, int64_t N, int64_t T, int64_t F, fl
                      static_cast<const E*>(G), T, F, eps, chunks, vec, pw, pb);
 }
 
+template <class E, int PC, int RW>
+void launch_ln_rows(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
+                    int64_t chunks, float* pw, float* pb, hipStream_t s) {
+  const size_t lds = 2 * LN2_WAVES * RW * F * sizeof(float);
+  hipLaunchKernelGGL((ln_rows_kernel<E, PC, RW>),
+                     dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(N)),
+                     dim3(64 * LN2_WAVES), lds, s, static_cast<const E*>(X),
+                     static_cast<const E*>(G), T, F, eps, chunks, pw, pb);
+}
+
 template <class E>
 int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
                   int64_t chunks, float* pw, float* pb, hipStream_t s) {
@@ -444,6 +572,26 @@ int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F,
   const int64_t pc = cdiv(F, 64 * VE);
   const int vec = (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
                   (reinterpret_cast<uintptr_t>(G) % 16 == 0) && (F * sizeof(E)) % 16 == 0;
+  const int64_t fchunks = cdiv(F, VE);  // 16-byte chunks per row
+  const int64_t rw = fchunks <= 32 * 4 ? 2 : 1;
+  if (vec && 2 * LN2_WAVES * rw * F * static_cast<int64_t>(sizeof(float)) <= 64 * 1024) {
+    // Aligned rows: two rows per wave while 32 lanes x 4 chunks cover a row, else one.
+    if (fchunks <= 32 * 2)
+      launch_ln_rows<E, 2, 2>(X, G, N, T, F, eps, chunks, pw, pb, s);
+    else if (fchunks <= 32 * 3)
+      launch_ln_rows<E, 3, 2>(X, G, N, T, F, eps, chunks, pw, pb, s);
+    else if (fchunks <= 32 * 4)
+      launch_ln_rows<E, 4, 2>(X, G, N, T, F, eps, chunks, pw, pb, s);
+    else if (fchunks <= 64 * 4)
+      launch_ln_rows<E, 4, 1>(X, G, N, T, F, eps, chunks, pw, pb, s);
+    else if (fchunks <= 64 * 6)
+      launch_ln_rows<E, 6, 1>(X, G, N, T, F, eps, chunks, pw, pb, s);
+    else if (fchunks <= 64 * 8)
+      launch_ln_rows<E, 8, 1>(X, G, N, T, F, eps, chunks, pw, pb, s);
+    else
+      return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: feature count too large");
+    return check_launch("ln_rows_kernel");
+  }
   if (pc <= 1)
     launch_ln<E, 1>(X, G, N, T, F, eps, chunks, vec, pw, pb, s);
   else if (pc <= 2)

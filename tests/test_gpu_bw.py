@@ -41,7 +41,8 @@ def test_embedding_positions_and_all_equal_ids(gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100)])
+@pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100),
+                                   (3, 1, 130, 1024), (4, 2, 64, 1600)])
 def test_layernorm_dots_and_grads(gpu, dtype, shape):
     N, n_val, T, Fd = shape
     X = randn((N, T, Fd), 11 + T, 2.0, dtype) + 0.5

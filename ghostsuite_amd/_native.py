@@ -74,12 +74,12 @@ _SIGNATURES = {
                               _P]),
 }
 
-# How the val-gradient algorithm forms V = G_val^T A_val for the pairwise semantics: "library"
-# (a hipBLASLt GEMM through torch.mm on the operands as they lie, then gs_linear_rowdot) or
-# "native" (the library's own transposes and GEMM inside gs_linear_dot).  The presum
-# semantics (V from T presummed rows, a short GEMM) and per-pair outputs use "native", which
-# measured faster there.
-V_GEMM = "library"
+# How the val-gradient algorithm forms V = G_val^T A_val for the pairwise semantics: "native"
+# (the library's K-major GEMM on the val rows as they lie, inside gs_linear_dot /
+# gs_linear_val_gradient) or "library" (a hipBLASLt GEMM through torch.mm, then
+# gs_linear_rowdot).  The native GEMM measured faster at the GPT-2 shapes (38 vs 45 us for
+# the 3072 x 768 x 4096 val term); the presum semantics and per-pair outputs always use it.
+V_GEMM = "native"
 
 
 def load_library() -> ctypes.CDLL:

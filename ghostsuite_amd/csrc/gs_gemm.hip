@@ -1108,6 +1108,280 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
   }
 }
 
+// out_z[t][f] = sum over the nseg val rows of in_z[row(s, t)][f] for z = 0, 1 (blockIdx.z):
+// 16 bytes per thread, fp32 sums rounded once.  Rows 16-byte aligned, d % 8 == 0.
+struct PresumPair {
+  const uint16_t* in[2];
+  uint16_t* out[2];
+  int64_t d[2];
+};
+__global__ void __launch_bounds__(256) presum_rows_vec_kernel(PresumPair pp, RowMap map) {
+  const int z = blockIdx.z;
+  const int64_t d = pp.d[z];
+  const int64_t f = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  const int64_t t = blockIdx.y;
+  if (f >= d) return;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t sg = 0;
+  for (; sg + 4 <= map.nseg; sg += 4) {
+    uint4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      x[u] = *reinterpret_cast<const uint4*>(pp.in[z] + map.phys_row(sg + u, t) * d + f);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[2 * e] += __uint_as_float(w[e] << 16);
+        a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+      }
+    }
+  }
+  for (; sg < map.nseg; ++sg) {
+    const uint4 x = *reinterpret_cast<const uint4*>(pp.in[z] + map.phys_row(sg, t) * d + f);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[2 * e] += __uint_as_float(w[e] << 16);
+      a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+  uint4 o;
+  o.x = pack_bf16x2(a[0], a[1]);
+  o.y = pack_bf16x2(a[2], a[3]);
+  o.z = pack_bf16x2(a[4], a[5]);
+  o.w = pack_bf16x2(a[6], a[7]);
+  *reinterpret_cast<uint4*>(pp.out[z] + t * d + f) = o;
+}
+
+// ------------------------------------------------------------------ K-major (TN) GEMM
+// out[m][n] = sum over k rows of L[k][m] R[k][n], with both operands K-major: rows are k,
+// as the val rows of A and G lie in HBM, so neither is transposed in memory.  Each stage's
+// k-rows go to LDS unchanged by wave-level DMA (16-byte chunk c of k-row r at slot
+// c ^ swz(r)), and the MFMA fragments come out of LDS through the transpose read
+// ds_read_b64_tr_b16: within a 16-lane group, lane 4a+b receives element b of the 8-byte
+// reads of lanes a, a+4, a+8, a+12.  Lane l of a 32x32x16 fragment therefore points its two
+// reads at k-rows 8(l/32) + (l%16)/4 (+4) and columns 16((l/16)%2) + 4(l%4), and gets the
+// 8 k-values of column l%32.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
+
+template <class C, int BK, int NS>
+struct TnCfg {
+  static constexpr int NW = C::WM * C::WN;
+  static constexpr int CL = C::BM / 8, CR = C::BN / 8;  // 16-byte chunks per k-row
+  static constexpr int RL = C::BM * 2, RR = C::BN * 2;  // bytes per k-row
+  static constexpr int STAGES = NS, KB = BK, KSTEPS = BK / 16;
+  static constexpr int L_BYTES = BK * RL, STAGE_BYTES = BK * (RL + RR);
+  static constexpr int QL = L_BYTES / 1024 / NW, QR = BK * RR / 1024 / NW;  // DMAs per wave
+  static_assert(C::BM >= 64 && C::BN >= 64 && BK % 16 == 0, "TN tile");
+  static_assert((L_BYTES / 1024) % NW == 0 && (BK * RR / 1024) % NW == 0 && QL > 0 && QR > 0,
+                "TN DMA split");
+  // The 32 lanes of a transpose read cover k-rows r..r+3 (r % 4 == 0) x 4 chunks; the
+  // swizzle puts those 16 chunks in 16 distinct 16-byte bank groups of a 256-byte window.
+  template <int CH>
+  __device__ static constexpr int swz(int r) {
+    return CH >= 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+  }
+};
+
+struct TnParams {
+  const void* L;  // k-row 0 of the left operand (M columns, row stride ldl elements)
+  const void* R;  // k-row 0 of the right operand (N columns, row stride ldr elements)
+  int64_t ldl, ldr, l_nbytes, r_nbytes;
+  int64_t K, kper;  // k-rows in all, per split
+  int64_t M, N, m_tiles, n_tiles;
+  void* out;        // splits == 1: bf16 [M][N]; else fp32 partials [split][M][N]
+  int splits;
+};
+
+template <class C, class D>
+struct TnStreamer {
+  __amdgpu_buffer_rsrc_t rl, rr;
+  unsigned offl[D::QL], offr[D::QR];  // byte offset of the chunk in k-row 0, or DMA_OOB
+  int rowl[D::QL], rowr[D::QR];        // k-row within the stage
+  int64_t ldl2, ldr2;                  // row strides in bytes
+
+  __device__ __forceinline__ void init(const TnParams& p, int64_t mt, int64_t nt) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    rl = make_rsrc(p.L, p.l_nbytes);
+    rr = make_rsrc(p.R, p.r_nbytes);
+    ldl2 = p.ldl * 2;
+    ldr2 = p.ldr * 2;
+#pragma unroll
+    for (int q = 0; q < D::QL; ++q) {
+      const int byte = (wid + D::NW * q) * 1024 + lane * 16;  // within the L part of a stage
+      const int r = byte / D::RL, slot = (byte % D::RL) / 16;
+      const int c = slot ^ D::template swz<D::CL>(r);
+      const int64_t m = mt * C::BM + c * 8;
+      rowl[q] = r;
+      offl[q] = m < p.M ? static_cast<unsigned>(m * 2) : DMA_OOB;
+    }
+#pragma unroll
+    for (int q = 0; q < D::QR; ++q) {
+      const int byte = (wid + D::NW * q) * 1024 + lane * 16;
+      const int r = byte / D::RR, slot = (byte % D::RR) / 16;
+      const int c = slot ^ D::template swz<D::CR>(r);
+      const int64_t n = nt * C::BN + c * 8;
+      rowr[q] = r;
+      offr[q] = n < p.N ? static_cast<unsigned>(n * 2) : DMA_OOB;
+    }
+  }
+  __device__ __forceinline__ void issue(unsigned char* stage, int64_t k0, int64_t k_end) {
+    const int wid = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < D::QL; ++q) {
+      const int64_t k = k0 + rowl[q];
+      const unsigned off =
+          (k < k_end && offl[q] != DMA_OOB) ? static_cast<unsigned>(k * ldl2) + offl[q] : DMA_OOB;
+      dma16(rl, off, stage + (wid + D::NW * q) * 1024);
+    }
+#pragma unroll
+    for (int q = 0; q < D::QR; ++q) {
+      const int64_t k = k0 + rowr[q];
+      const unsigned off =
+          (k < k_end && offr[q] != DMA_OOB) ? static_cast<unsigned>(k * ldr2) + offr[q] : DMA_OOB;
+      dma16(rr, off, stage + D::L_BYTES + (wid + D::NW * q) * 1024);
+    }
+  }
+};
+
+__device__ __forceinline__ s16x4_t lds_tr16(const unsigned char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)(p));
+}
+
+template <class C, class D>
+__device__ __forceinline__ void tn_compute(const unsigned char* stage,
+                                           f32x16_t (&acc)[C::MI][C::NI]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  const int g = lane >> 4, a4 = (lane & 3) * 4, j = (lane >> 2) & 3;
+  const int row = 8 * (g >> 1) + j;  // k-row of this lane's first read within a k-step
+  const int colh = 16 * (g & 1) + a4;
+  // Byte offsets of fragment i (j) at k-step 0, first half; the swizzle depends on the
+  // k-row only through row % 4 (CH >= 16) or (row / 2) % 2, fixed per lane.
+  int offa[C::MI], offb[C::NI];
+#pragma unroll
+  for (int i = 0; i < C::MI; ++i) {
+    const int col = wm * 32 * C::MI + i * 32 + colh;
+    offa[i] = row * D::RL + (((col >> 3) ^ D::template swz<D::CL>(row)) * 16) + (col & 7) * 2;
+  }
+#pragma unroll
+  for (int jj = 0; jj < C::NI; ++jj) {
+    const int col = wn * 32 * C::NI + jj * 32 + colh;
+    offb[jj] = D::L_BYTES + row * D::RR + (((col >> 3) ^ D::template swz<D::CR>(row)) * 16) +
+               (col & 7) * 2;
+  }
+  constexpr int NB = 2;
+  bf16x8_t fa[NB][C::MI], fb[NB][C::NI];
+  auto load = [&](int buf, int ks) {
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i) {
+      const unsigned char* p = stage + offa[i] + ks * 16 * D::RL;
+      const s16x8_t v = __builtin_shufflevector(lds_tr16(p), lds_tr16(p + 4 * D::RL), 0, 1, 2,
+                                                3, 4, 5, 6, 7);
+      fa[buf][i] = __builtin_bit_cast(bf16x8_t, v);
+    }
+#pragma unroll
+    for (int jj = 0; jj < C::NI; ++jj) {
+      const unsigned char* p = stage + offb[jj] + ks * 16 * D::RR;
+      const s16x8_t v = __builtin_shufflevector(lds_tr16(p), lds_tr16(p + 4 * D::RR), 0, 1, 2,
+                                                3, 4, 5, 6, 7);
+      fb[buf][jj] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  };
+  load(0, 0);
+#pragma unroll
+  for (int ks = 0; ks < D::KSTEPS; ++ks) {
+    if (ks + 1 < D::KSTEPS) load((ks + 1) % NB, ks + 1);
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::NI; ++jj)
+        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks % NB][i], fb[ks % NB][jj],
+                                                             acc[i][jj], 0, 0, 0);
+  }
+}
+
+// acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same
+// schedule as mainloop_dma: constant vmcnt wait, barrier, loads of stage k + NS - 1, MFMAs).
+template <class C, class D>
+__device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
+                                            int64_t k_begin, int64_t k_end, unsigned char* lds,
+                                            f32x16_t (&acc)[C::MI][C::NI]) {
+  constexpr int NQ = D::QL + D::QR;
+  constexpr int AHEAD = D::STAGES - 1;
+  static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
+  TnStreamer<C, D> st;
+  st.init(p, mt, nt);
+  const int nk = static_cast<int>((k_end - k_begin + D::KB - 1) / D::KB);
+  auto slot = [&](int k) { return lds + (k % D::STAGES) * D::STAGE_BYTES; };
+#pragma unroll
+  for (int s = 0; s < AHEAD; ++s)
+    if (s < nk) st.issue(slot(s), k_begin + static_cast<int64_t>(s) * D::KB, k_end);
+  int kt = 0;
+  for (; kt + AHEAD < nk; ++kt) {
+    wait_vmcnt<(AHEAD - 1) * NQ>();
+    raw_barrier();
+    st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
+    tn_compute<C, D>(slot(kt), acc);
+  }
+  for (; kt < nk; ++kt) {
+    wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
+    raw_barrier();
+    tn_compute<C, D>(slot(kt), acc);
+  }
+  wait_vmcnt<0>();
+  raw_barrier();
+}
+
+// One output tile per (blockIdx.x, split blockIdx.y): bf16 out when there is one split,
+// else fp32 partials reduced by tn_reduce_kernel.
+template <class C, class D>
+__global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
+  int64_t mt, nt;
+  tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
+  const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * p.kper;
+  const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
+  f32x16_t acc[C::MI][C::NI];
+  zero_acc<TrBF16, C>(acc);
+  mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc);
+  GemmParams e{};
+  e.m_rows = p.M;
+  e.n_cols = p.N;
+  e.c_ld = p.N;
+  if (p.splits == 1) {
+    e.C = p.out;
+    store_epilogue<TrBF16, C>(e, acc, mt, nt);
+  } else {
+    e.C = static_cast<float*>(p.out) + static_cast<int64_t>(blockIdx.y) * p.M * p.N;
+    store_epilogue<TrF32, C>(e, acc, mt, nt);
+  }
+}
+
+// out[i] = bf16(sum over the splits of part[s][i]), fixed order, 4 elements per thread.
+__global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict__ part,
+                                                        int64_t count, int splits,
+                                                        uint16_t* __restrict__ out) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i >= count) return;
+  float4 s = *reinterpret_cast<const float4*>(part + i);
+  for (int k = 1; k < splits; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(part + k * count + i);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  uint2 o;
+  o.x = pack_bf16x2(s.x, s.y);
+  o.y = pack_bf16x2(s.z, s.w);
+  *reinterpret_cast<uint2*>(out + i) = o;
+}
+
 // ------------------------------------------------------------------------------ host side
 // Tile shapes per epilogue (overridable at build time for tuning sweeps).
 #ifndef GS_GHOST_TILE
@@ -1247,6 +1521,97 @@ struct LinearPlan {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The K-major val-term GEMM (tn_gemm_kernel): tile shape, stage geometry and split count
+// (GS_TN_SPLIT 0 = chosen by the estimate in tn_splits).
+#ifndef GS_TN_TILE
+#define GS_TN_TILE 2, 2, 2, 2
+#endif
+#ifndef GS_TN_STAGE
+#define GS_TN_STAGE 64, 2
+#endif
+#ifndef GS_TN_SPLIT
+#define GS_TN_SPLIT 0
+#endif
+#ifndef GS_USE_TN
+#define GS_USE_TN 1
+#endif
+using TnC = Cfg<TrBF16, GS_TN_TILE>;
+using TnD = TnCfg<TnC, GS_TN_STAGE>;
+
+bool tn_ok(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
+           int64_t N) {
+  if (!GS_USE_TN || K <= 0 || M <= 0 || N <= 0) return false;
+  if (ldl % 8 || ldr % 8 || M % 8 || N % 8) return false;
+  if (K * ldl * 2 >= INT32_MAX || K * ldr * 2 >= INT32_MAX) return false;
+  return L == nullptr || (aligned16(L) && aligned16(R));
+}
+
+// Splits of the k-rows: enough workgroups to cover the CUs against the fp32 partials'
+// extra write + read (estimated at 4 TF/s per CU and 4 TB/s).
+int tn_splits(int64_t K, int64_t M, int64_t N) {
+  const int64_t ksteps = ceil_div(K, static_cast<int64_t>(TnD::KB));
+  if (GS_TN_SPLIT > 0) return static_cast<int>(std::min<int64_t>(GS_TN_SPLIT, ksteps));
+  const double tiles = static_cast<double>(ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN));
+  int best = 1;
+  double best_t = 1e30;
+  for (int sp = 1; sp <= 8 && sp <= std::max<int64_t>(1, ksteps / 4); ++sp) {
+    const double t = 2.0 * M * N * K / (std::min(tiles * sp, 256.0) * 4e12) +
+                     (sp > 1 ? 8.0 * sp * M * N / 4e12 + 3e-6 : 0.0);
+    if (t < best_t) {
+      best_t = t;
+      best = sp;
+    }
+  }
+  return best;
+}
+int64_t tn_part_elems(int64_t K, int64_t M, int64_t N) {
+  const int sp = tn_splits(K, M, N);
+  return sp > 1 ? sp * M * N : 0;
+}
+
+// The K-major GEMM computes the val term for bf16 operands (after a presum for PRESUM);
+// else the val rows are transposed and the STORE GEMM runs.
+bool val_tn(int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, int presum) {
+  const int64_t K = (presum ? 1 : n_val) * T;
+  if (presum && T > 65535) return false;  // the presum grid takes one row of blocks per token
+  return dtype == GS_DTYPE_BF16 && tn_ok(nullptr, d_out, nullptr, d_in, K, d_out, d_in);
+}
+// out [M][N] bf16 = L^T R over K k-rows (L: [K][M] stride ldl, R: [K][N] stride ldr).
+int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
+              int64_t N, void* out, float* part, hipStream_t s) {
+  TnParams p{};
+  p.L = L;
+  p.R = R;
+  p.ldl = ldl;
+  p.ldr = ldr;
+  p.l_nbytes = K * ldl * 2;
+  p.r_nbytes = K * ldr * 2;
+  p.K = K;
+  p.M = M;
+  p.N = N;
+  p.m_tiles = ceil_div(M, TnC::BM);
+  p.n_tiles = ceil_div(N, TnC::BN);
+  int sp = tn_splits(K, M, N);
+  p.kper = ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
+           TnD::KB;
+  sp = static_cast<int>(ceil_div(K, p.kper));
+  p.splits = sp;
+  p.out = sp > 1 ? static_cast<void*>(part) : out;
+  if (sp > 1 && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
+  const int64_t tiles = p.m_tiles * p.n_tiles;
+  if (tiles > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
+  hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>),
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(sp)),
+                     dim3(TnC::NT), 0, s, p);
+  int rc = check_launch("tn_gemm_kernel");
+  if (rc || sp == 1) return rc;
+  const int64_t count = M * N;  // a multiple of 8 (N % 8 == 0)
+  hipLaunchKernelGGL(tn_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(count / 4, 256))),
+                     dim3(256), 0, s, part, count, sp, static_cast<uint16_t*>(out));
+  return check_launch("tn_reduce_kernel");
+}
+
+
 template <class Tr>
 LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
                        int semantics, int algo, int want_pair) {
@@ -1304,11 +1669,17 @@ void carve_linear(S& c, const LinearPlan& pl, int dtype, int64_t N, int64_t n_va
       c.template take<char>(T * d_out * esz);
     }
   } else {
+    // Transposed val rows (or, on the K-major path, the presummed rows), V, the partials,
+    // then the K-major GEMM's split partials.  Both paths carve the same prefix, so a call
+    // that cannot take the K-major path (unaligned pointers) still fits.
     c.template take<char>(d_in * pl.vcols * esz);
     c.template take<char>(d_out * pl.vcols * esz);
     c.template take<char>(d_out * d_in * esz);
   }
   c.template take<float>(pl.p_rows * pl.p_ld);
+  if (pl.algo != GS_ALGO_GHOST &&
+      val_tn(dtype, n_val, T, d_in, d_out, semantics == GS_SEM_PRESUM ? 1 : 0))
+    c.template take<float>(tn_part_elems(pl.vcols / pl.groups, d_out, d_in));
 }
 
 bool linear_args_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
@@ -1472,16 +1843,55 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     return check_launch("reduce_partials_kernel");
   }
 
-  // VALGRAD: transposed val operands, V = G_val^T A_val (per val row when pairs are wanted),
-  // then the fused row-dot GEMM over the train tokens.
+  // VALGRAD: V = G_val^T A_val (per val row when pairs are wanted), then the fused row-dot
+  // GEMM over the train tokens.  bf16: V by the K-major GEMM on the val rows as they lie.
+  const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
+  const int64_t n_mt = ceil_div(d_out, RC::BM);
+  if constexpr (std::is_same<Tr, TrBF16>::value) {
+    if (val_tn(GS_DTYPE_BF16, n_val, T, d_in, d_out, presum) && aligned16(A) && aligned16(G)) {
+      const E* La = static_cast<const E*>(A) + val_start * T * d_in;
+      const E* Lg = static_cast<const E*>(G) + val_start * T * d_out;
+      E* abar = reinterpret_cast<E*>(cv.take<char>(d_in * pl.vcols * esz));
+      E* gbar = reinterpret_cast<E*>(cv.take<char>(d_out * pl.vcols * esz));
+      E* V = reinterpret_cast<E*>(cv.take<char>(d_out * d_in * esz));
+      float* P = cv.take<float>(pl.p_rows * pl.p_ld);
+      const int64_t kper = pl.vcols / pl.groups;  // k-rows per V (one val row for pairs)
+      float* part = cv.take<float>(tn_part_elems(kper, d_out, d_in));
+      if (presum) {
+        PresumPair pp{};
+        pp.in[0] = static_cast<const E*>(A);
+        pp.in[1] = static_cast<const E*>(G);
+        pp.out[0] = abar;
+        pp.out[1] = gbar;
+        pp.d[0] = d_in;
+        pp.d[1] = d_out;
+        const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
+                        static_cast<unsigned>(T), 2);
+        hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp, va);
+        int rc = check_launch("presum_rows_vec_kernel");
+        if (rc) return rc;
+        La = abar;
+        Lg = gbar;
+      }
+      for (int64_t j = 0; j < pl.groups; ++j) {
+        int rc = launch_tn(Lg + j * kper * d_out, d_out, La + j * kper * d_in, d_in, kper, d_out,
+                           d_in, V, part, s);
+        if (rc) return rc;
+        rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
+                               pl.tile_reduce, j * n_mt, s);
+        if (rc) return rc;
+      }
+      hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0,
+                         s, P, pl.groups, n_mt, pl.p_ld, pl.cols, n_t, out_pair, out_dot);
+      return check_launch("reduce_partials_kernel");
+    }
+  }
   E* At = reinterpret_cast<E*>(cv.take<char>(d_in * pl.vcols * esz));
   E* Gt = reinterpret_cast<E*>(cv.take<char>(d_out * pl.vcols * esz));
   E* V = reinterpret_cast<E*>(cv.take<char>(d_out * d_in * esz));
   float* P = cv.take<float>(pl.p_rows * pl.p_ld);
-  const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
   int rc = transpose_val<Tr>(A, G, d_in, d_out, va, presum, pl.vcols, At, Gt, s);
   if (rc) return rc;
-  const int64_t n_mt = ceil_div(d_out, RC::BM);
   const int64_t vsteps = pl.groups;  // one V per val row for pairs, else one V
   const int64_t kper = pl.vcols / vsteps;
   for (int64_t j = 0; j < vsteps; ++j) {
@@ -1549,14 +1959,28 @@ extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N,
 }
 
 // ------------------------------------------------------------------ val gradient V
+namespace gs {
+namespace {
+// Transposed (or presummed) val rows, then the K-major GEMM's split partials; the prefix is
+// the same on both paths, so a call that cannot take the K-major path still fits.
+template <class S>
+void carve_val_gradient(S& c, int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
+                        int presum) {
+  const size_t esz = elem_size(dtype);
+  const int64_t vcols = (presum ? 1 : n_val) * T;
+  c.template take<char>(d_in * vcols * esz);
+  c.template take<char>(d_out * vcols * esz);
+  if (val_tn(dtype, n_val, T, d_in, d_out, presum))
+    c.template take<float>(tn_part_elems(vcols, d_out, d_in));
+}
+}  // namespace
+}  // namespace gs
+
 extern "C" size_t gs_linear_val_gradient_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
                                                    int64_t d_in, int64_t d_out, int semantics) {
   if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, GS_ALGO_AUTO, 0)) return 0;
-  const int64_t vcols = (semantics == GS_SEM_PRESUM ? 1 : n_val) * T;
-  const size_t esz = elem_size(dtype);
   Sizer sz;
-  sz.take<char>(d_in * vcols * esz);
-  sz.take<char>(d_out * vcols * esz);
+  carve_val_gradient(sz, dtype, n_val, T, d_in, d_out, semantics == GS_SEM_PRESUM ? 1 : 0);
   return sz.used + 256;
 }
 
@@ -1582,6 +2006,31 @@ extern "C" int gs_linear_val_gradient(const void* A, const void* G, int dtype, i
   const size_t esz = elem_size(dtype);
   void* At = cv.take<char>(d_in * vcols * esz);
   void* Gt = cv.take<char>(d_out * vcols * esz);
+  if (val_tn(dtype, n_val, T, d_in, d_out, presum) && aligned16(A) && aligned16(G)) {
+    using E = TrBF16::E;
+    const E* La = static_cast<const E*>(A) + val_start * T * d_in;
+    const E* Lg = static_cast<const E*>(G) + val_start * T * d_out;
+    if (presum) {
+      E* abar = static_cast<E*>(At);
+      E* gbar = static_cast<E*>(Gt);
+      PresumPair pp{};
+      pp.in[0] = static_cast<const E*>(A);
+      pp.in[1] = static_cast<const E*>(G);
+      pp.out[0] = abar;
+      pp.out[1] = gbar;
+      pp.d[0] = d_in;
+      pp.d[1] = d_out;
+      const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
+                      static_cast<unsigned>(T), 2);
+      hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp, va);
+      int rc = check_launch("presum_rows_vec_kernel");
+      if (rc) return rc;
+      La = abar;
+      Lg = gbar;
+    }
+    float* part = cv.take<float>(tn_part_elems(vcols, d_out, d_in));
+    return launch_tn(Lg, d_out, La, d_in, vcols, d_out, d_in, V, part, s);
+  }
   if (dtype == GS_DTYPE_BF16) {
     using E = TrBF16::E;
     int rc = transpose_val<TrBF16>(A, G, d_in, d_out, va, presum, vcols, static_cast<E*>(At),

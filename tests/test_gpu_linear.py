@@ -142,7 +142,7 @@ def test_linear_rejects_bad_arguments(gpu):
         _native.ops().linear_dot(A, G, 1, semantics=_native.SEM_PRESUM, want_pair=True)
 
 
-@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("shape", SHAPES + [(8, 4, 512, 256, 512), (5, 2, 1024, 768, 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("semantics", ["pairwise", "presum"])
 def test_linear_val_gradient_matches_closed_form(gpu, shape, dtype, semantics):

@@ -81,7 +81,8 @@ class TimedOps:
         from ghostsuite_amd import _native
         N, d_in, d_out = A.shape[0], A.shape[-1], G.shape[-1]
         T = A.numel() // (N * d_in)
-        flops = 2.0 * (n_val * T + (N - n_val) * T) * d_in * d_out
+        nv = n_val if k.get("semantics", 0) == _native.SEM_PAIRWISE_SUM else 1
+        flops = 2.0 * (nv * T + (N - n_val) * T) * d_in * d_out
         out = self._run(f"linear_valgrad+bias[{d_in}x{d_out}]", ("mfma", flops),
                         self.inner.linear_bias_dot, A, G, n_val, **k)
         if out is None and self.enabled:
@@ -290,7 +291,8 @@ def gradproj_bench(steps: int, warmup: int, dev):
 # ------------------------------------------------------------------ Pythia-1B shape
 def pythia_bench(steps: int, warmup: int, dev):
     """16 layers, d=2048, MLP 8192, T=2048, rotary, untied embed_out, bf16; 8 train + 2 val."""
-    from ghostsuite_amd import GradDotProdEngine
+    from ghostsuite_amd import GradDotProdEngine, _native
+    from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
     from ghostsuite_amd.workloads import CausalLM, PYTHIA_1B, synthetic_tokens
     n_train, n_val, T = 8, 2, 2048
     torch.manual_seed(0)
@@ -318,8 +320,10 @@ def pythia_bench(steps: int, warmup: int, dev):
         popt.step()
         popt.zero_grad(set_to_none=True)
 
-    out = {}
-    for name, fn in (("ghost", ghost_step), ("plain", plain_step)):
+    timed = TimedOps(_native.ops())
+    _native._install_backend(timed)
+
+    def timed_run(fn):
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
@@ -327,13 +331,35 @@ def pythia_bench(steps: int, warmup: int, dev):
         for i in range(steps):
             fn(i)
         torch.cuda.synchronize()
-        out[name] = (time.perf_counter() - t0) / steps
+        return (time.perf_counter() - t0) / steps
+
+    out = {"ghost": timed_run(ghost_step)}
+    # Per-op pass: dot kernels serialised on the autograd stream, bracketed by HIP events.
+    S.options["overlap"] = False
+    timed.enabled = True
+    out["serial"] = timed_run(ghost_step)
+    timed.enabled = False
+    S.options["overlap"] = True
+    ops = timed.summary()
+    _native._install_backend(None)
+    out["plain"] = timed_run(plain_step)
     eng.detach()
     del model, plain, opt, popt, eng
     torch.cuda.empty_cache()
+    per_op = {}
+    for name, a in sorted(ops.items(), key=lambda kv: -kv[1]["ms"]):
+        calls = a["n"] / (steps + warmup)
+        avg_ms = a["ms"] / a["n"]
+        rate = a["work"] / (avg_ms * 1e-3)
+        per_op[name] = {"ms_per_step": a["ms"] / (steps + warmup), "calls_per_step": calls,
+                        "avg_us": avg_ms * 1e3,
+                        ("TFLOP/s" if a["bound"] == "mfma" else "GB/s"): rate / 1e12
+                        if a["bound"] == "mfma" else rate / 1e9}
     return {"workload": "Pythia-1B shape GradDotProd, 8 train + 2 val, T=2048",
             "ms_per_step": out["ghost"] * 1e3, "plain_ms_per_step": out["plain"] * 1e3,
-            "samples_per_s": n_train / out["ghost"], "step_overhead": out["ghost"] / out["plain"]}
+            "ms_per_step_serialised_dots": out["serial"] * 1e3,
+            "samples_per_s": n_train / out["ghost"], "step_overhead": out["ghost"] / out["plain"],
+            "ops": per_op}
 
 
 # ------------------------------------------------------------------ ghost kernel microbench

@@ -2,12 +2,14 @@
 //
 //   out[b] = scale * sum_t (L g_bt)(R a_bt)^T        L: [kL, n_g], R: [kR, n_a]
 //
-// One workgroup takes one sample and a chunk of 64 tokens (16 per wave).  Each wave
-// streams its 16 token rows of G and A straight from HBM into MFMA operands
-// (v_mfma_f32_16x16x32_bf16 / v_mfma_f32_16x16x4f32), with the projection rows as the
-// other operand (small, L2-resident), so G and A are read exactly once.  The projected
-// rows (fp32) go to LDS and the 64-token outer-product sum is formed there; per-chunk
-// partials are reduced per sample in a fixed order.
+// One workgroup takes one sample and a chunk of 64 tokens; its 4 waves take interleaved
+// 64-feature pieces of all 64 token rows (so the workgroup reads 256 contiguous features of
+// every row at a time).  A wave streams its pieces of the G and A rows straight from HBM
+// into MFMA operands (v_mfma_f32_16x16x32_bf16 / v_mfma_f32_16x16x4f32) against the
+// projection rows (small, L2-resident), each projection fragment serving the 4 sixteen-row
+// groups, so G and A are read exactly once.  The wave shares (fp32) are summed in LDS, the
+// 64-token outer-product sum is formed there, and the per-chunk partials are reduced per
+// sample in a fixed order.
 //
 // 16x16 MFMA layout: lane l supplies row (l % 16) of A and column (l % 16) of B with its
 // k-slice chosen by l / 16; result element e of lane l is C[4*(l/16) + e][l % 16].
@@ -68,32 +70,50 @@ __device__ __forceinline__ uint4 lane_load(const typename Tr::E* row, int64_t k,
   return u.v;
 }
 
-// proj[t][k] (k < kp) for this wave's 16 token rows, accumulated in MFMA layout:
-// acc[nb][e] = C[token 4*(l/16)+e][k = 16*nb + l%16].
-template <class Tr>
-__device__ __forceinline__ void project_rows(const typename Tr::E* row, const typename Tr::E* P,
-                                             int64_t n, int64_t kP, int vec_ok, int vec_p,
-                                             f32x4_t (&acc)[2], int nblocks) {
+#ifndef GS_PJ_U
+#define GS_PJ_U 2
+#endif
+constexpr int PJ_WAVES = PJ_THREADS / 64;
+constexpr int PJ_TG = PJ_TOK / 16;  // 16-token MFMA row groups per workgroup
+
+// Partial projections over this wave's share of the features of the workgroup's PJ_TOK
+// token rows:
+// acc[tg][nb][e] = sum_f P[16*nb + l%16][f] * row(16*tg + 4*(l/16) + e)[f].  Every projection
+// fragment loaded is used by the PJ_TG row groups (one MFMA each).
+template <class Tr, int NB>
+__device__ __forceinline__ void project_rows(const typename Tr::E* const (&rows)[PJ_TG],
+                                             const typename Tr::E* P, int64_t n, int64_t kP,
+                                             int vec_ok, int vec_p, f32x4_t (&acc)[PJ_TG][NB]) {
   using E = typename Tr::E;
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;  // lane group: k-slice selector
   const E* prow0 = (lane & 15) < kP ? P + static_cast<int64_t>(lane & 15) * n : nullptr;
   const E* prow1 = 16 + (lane & 15) < kP ? P + static_cast<int64_t>(16 + (lane & 15)) * n : nullptr;
-  constexpr int U = 8;  // lane loads in flight per operand row
-  for (int64_t f0 = 0; f0 < n; f0 += static_cast<int64_t>(U) * Tr::KSTEP) {
-    uint4 a[U];
+  constexpr int U = GS_PJ_U;  // k-steps of loads in flight (x PJ_TG rows)
+  // The waves interleave in pieces of U k-steps, so a workgroup reads one contiguous run
+  // of PJ_WAVES pieces of every row at a time.
+  const int64_t f_step = static_cast<int64_t>(PJ_WAVES) * U * Tr::KSTEP;
+  for (int64_t f0 = (threadIdx.x >> 6) * U * Tr::KSTEP; f0 < n; f0 += f_step) {
+    uint4 a[U][PJ_TG];
 #pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = lane_load<Tr>(row, f0 + u * Tr::KSTEP + kg * Tr::VEC, n, vec_ok);
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int tg = 0; tg < PJ_TG; ++tg)
+        a[u][tg] = lane_load<Tr>(rows[tg], f0 + u * Tr::KSTEP + kg * Tr::VEC, n, vec_ok);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t k = f0 + u * Tr::KSTEP + kg * Tr::VEC;
       const uint4 b0 = lane_load<Tr>(prow0, k, n, vec_p);
 #pragma unroll
-      for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[0], a[u], b0, s);
-      if (nblocks > 1) {
+      for (int tg = 0; tg < PJ_TG; ++tg)
+#pragma unroll
+        for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[tg][0], a[u][tg], b0, s);
+      if constexpr (NB > 1) {
         const uint4 b1 = lane_load<Tr>(prow1, k, n, vec_p);
 #pragma unroll
-        for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[1], a[u], b1, s);
+        for (int tg = 0; tg < PJ_TG; ++tg)
+#pragma unroll
+          for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[tg][1], a[u][tg], b1, s);
       }
     }
   }
@@ -101,7 +121,10 @@ __device__ __forceinline__ void project_rows(const typename Tr::E* row, const ty
 
 // GATHER: the input side is an embedding, whose "projected input" for token id x is column
 // x of P_i, i.e. row x of R = P_i^T ([vocab, kR]); `ids` replaces A.
-template <class Tr, bool GATHER>
+// Workgroup = one sample x PJ_TOK tokens; wave w projects all PJ_TOK token rows over its
+// share of the features, the wave shares are summed in LDS (fixed order), then the
+// PJ_TOK-token outer-product sum is formed.
+template <class Tr, bool GATHER, int NB>
 __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
     const typename Tr::E* __restrict__ A, const int64_t* __restrict__ ids, int64_t vocab,
     const typename Tr::E* __restrict__ G, int64_t T, int64_t n_a, int64_t n_g,
@@ -109,45 +132,72 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
     int64_t kL, int vec_a, int vec_g, int vec_r, int vec_l, int64_t chunks,
     float* __restrict__ part) {
   using E = typename Tr::E;
-  __shared__ float sg[PJ_TOK][PJ_KMAX + 1];
-  __shared__ float sa[PJ_TOK][PJ_KMAX + 1];
+  // Wave slices combine in two steps through [PJ_WAVES / 2] slices of LDS.
+  constexpr int HW = PJ_WAVES / 2;
+  __shared__ float sg[HW][PJ_TOK][PJ_KMAX + 1];
+  __shared__ float sa[HW][PJ_TOK][PJ_KMAX + 1];
   const int64_t b = blockIdx.y, c = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int64_t t = c * PJ_TOK + wid * 16 + (lane & 15);  // this lane's operand row
-  const bool valid = t < T;
-  const E* grow = valid ? G + (b * T + t) * n_g : nullptr;
-  const int nbl = kL > 16 ? 2 : 1;
-
-  f32x4_t accg[2], acca[2];
+  const E* grows[PJ_TG];
+  const E* arows[PJ_TG];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) accg[i][e] = acca[i][e] = 0.f;
-  project_rows<Tr>(grow, L, n_g, kL, vec_g, vec_l, accg, nbl);
-  if constexpr (!GATHER) {
-    const E* arow = valid ? A + (b * T + t) * n_a : nullptr;
-    project_rows<Tr>(arow, R, n_a, kR, vec_a, vec_r, acca, kR > 16 ? 2 : 1);
+  for (int tg = 0; tg < PJ_TG; ++tg) {
+    const int64_t t = c * PJ_TOK + tg * 16 + (lane & 15);  // this lane's operand row
+    grows[tg] = t < T ? G + (b * T + t) * n_g : nullptr;
+    arows[tg] = (!GATHER && t < T) ? A + (b * T + t) * n_a : nullptr;
   }
-
+  f32x4_t accg[PJ_TG][NB], acca[PJ_TG][NB];
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
+  for (int tg = 0; tg < PJ_TG; ++tg)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int tok = wid * 16 + 4 * (lane >> 4) + e;
-      const int k = nb * 16 + (lane & 15);
-      sg[tok][k] = accg[nb][e];
-      if constexpr (!GATHER) sa[tok][k] = acca[nb][e];
-    }
-  if constexpr (GATHER) {
-    for (int x = threadIdx.x; x < PJ_TOK * PJ_KMAX; x += PJ_THREADS) {
-      const int tok = x / PJ_KMAX, q = x % PJ_KMAX;
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) accg[tg][i][e] = acca[tg][i][e] = 0.f;
+  project_rows<Tr, NB>(grows, L, n_g, kL, vec_g, vec_l, accg);
+  if constexpr (!GATHER) project_rows<Tr, NB>(arows, R, n_a, kR, vec_a, vec_r, acca);
+  // Waves HW.. park their slices, waves 0..HW-1 add their own, then slice 0 takes the sum
+  // of the HW slices (fixed order); the gather fills slice 0 of sa.
+  auto put = [&](bool add) {
+    const int sl = wid % HW;
+#pragma unroll
+    for (int tg = 0; tg < PJ_TG; ++tg)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int tok = tg * 16 + 4 * (lane >> 4) + e;
+          const int k = nb * 16 + (lane & 15);
+          const float g = nb < NB ? accg[tg][nb < NB ? nb : 0][e] : 0.f;
+          sg[sl][tok][k] = (add ? sg[sl][tok][k] : 0.f) + g;
+          if constexpr (!GATHER) {
+            const float a = nb < NB ? acca[tg][nb < NB ? nb : 0][e] : 0.f;
+            sa[sl][tok][k] = (add ? sa[sl][tok][k] : 0.f) + a;
+          }
+        }
+  };
+  if (wid >= HW) put(false);
+  __syncthreads();
+  if (wid < HW) put(true);
+  __syncthreads();
+  for (int x = threadIdx.x; x < PJ_TOK * PJ_KMAX; x += PJ_THREADS) {
+    const int tok = x / PJ_KMAX, q = x % PJ_KMAX;
+    float g = sg[0][tok][q];
+#pragma unroll
+    for (int w = 1; w < HW; ++w) g += sg[w][tok][q];
+    sg[0][tok][q] = g;
+    if constexpr (GATHER) {
       const int64_t tt = c * PJ_TOK + tok;
       float v = 0.f;
       if (tt < T && q < kR) {
         const int64_t id = ids[b * T + tt];
         if (id >= 0 && id < vocab) v = to_f32<E>(R[id * kR + q]);
       }
-      sa[tok][q] = v;
+      sa[0][tok][q] = v;
+    } else {
+      float a = sa[0][tok][q];
+#pragma unroll
+      for (int w = 1; w < HW; ++w) a += sa[w][tok][q];
+      sa[0][tok][q] = a;
     }
   }
   __syncthreads();
@@ -156,7 +206,7 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
   for (int64_t o = threadIdx.x; o < nout; o += PJ_THREADS) {
     const int p = static_cast<int>(o / kR), q = static_cast<int>(o % kR);
     float s = 0.f;
-    for (int64_t tk = 0; tk < nvalid; ++tk) s += sg[tk][p] * sa[tk][q];
+    for (int64_t tk = 0; tk < nvalid; ++tk) s += sg[0][tk][p] * sa[0][tk][q];
     part[(b * chunks + c) * nout + o] = s;
   }
 }
@@ -247,17 +297,20 @@ extern "C" int gs_kron_proj(const void* A, const void* G, int dtype, int64_t B, 
   const int vr = al16(R) && (n_a * static_cast<int64_t>(esz)) % 16 == 0;
   const int vl = al16(L) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
-  if (dtype == GS_DTYPE_BF16)
-    hipLaunchKernelGGL((kron_proj_kernel<PjBF16, false>), grid, dim3(PJ_THREADS), 0, s,
-                       static_cast<const uint16_t*>(A), nullptr, int64_t{0},
-                       static_cast<const uint16_t*>(G), T, n_a, n_g,
+  const bool two = kL > 16 || kR > 16;
+  if (dtype == GS_DTYPE_BF16) {
+    auto k = two ? kron_proj_kernel<PjBF16, false, 2> : kron_proj_kernel<PjBF16, false, 1>;
+    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, static_cast<const uint16_t*>(A),
+                       nullptr, int64_t{0}, static_cast<const uint16_t*>(G), T, n_a, n_g,
                        static_cast<const uint16_t*>(R), static_cast<const uint16_t*>(L), kR, kL,
                        va, vg, vr, vl, chunks, part);
-  else
-    hipLaunchKernelGGL((kron_proj_kernel<PjF32, false>), grid, dim3(PJ_THREADS), 0, s,
-                       static_cast<const float*>(A), nullptr, int64_t{0},
-                       static_cast<const float*>(G), T, n_a, n_g, static_cast<const float*>(R),
-                       static_cast<const float*>(L), kR, kL, va, vg, vr, vl, chunks, part);
+  } else {
+    auto k = two ? kron_proj_kernel<PjF32, false, 2> : kron_proj_kernel<PjF32, false, 1>;
+    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, static_cast<const float*>(A), nullptr,
+                       int64_t{0}, static_cast<const float*>(G), T, n_a, n_g,
+                       static_cast<const float*>(R), static_cast<const float*>(L), kR, kL, va,
+                       vg, vr, vl, chunks, part);
+  }
   int rc = check_launch("kron_proj_kernel");
   if (rc) return rc;
   return kron_finish(part, B, chunks, kL * kR, scale, out, out_dtype, s);
@@ -291,16 +344,20 @@ extern "C" int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, 
   const int vg = al16(G) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
   const int vl = al16(P_o) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
-  if (dtype == GS_DTYPE_BF16)
-    hipLaunchKernelGGL((kron_proj_kernel<PjBF16, true>), grid, dim3(PJ_THREADS), 0, s, nullptr,
-                       ids, vocab, static_cast<const uint16_t*>(G), T, int64_t{0}, n_g,
+  const bool two = k_o > 16;  // the gathered side needs no projection blocks
+  if (dtype == GS_DTYPE_BF16) {
+    auto k = two ? kron_proj_kernel<PjBF16, true, 2> : kron_proj_kernel<PjBF16, true, 1>;
+    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, nullptr, ids, vocab,
+                       static_cast<const uint16_t*>(G), T, int64_t{0}, n_g,
                        static_cast<const uint16_t*>(P_iT), static_cast<const uint16_t*>(P_o), k_i,
                        k_o, 0, vg, 0, vl, chunks, part);
-  else
-    hipLaunchKernelGGL((kron_proj_kernel<PjF32, true>), grid, dim3(PJ_THREADS), 0, s, nullptr,
-                       ids, vocab, static_cast<const float*>(G), T, int64_t{0}, n_g,
+  } else {
+    auto k = two ? kron_proj_kernel<PjF32, true, 2> : kron_proj_kernel<PjF32, true, 1>;
+    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, nullptr, ids, vocab,
+                       static_cast<const float*>(G), T, int64_t{0}, n_g,
                        static_cast<const float*>(P_iT), static_cast<const float*>(P_o), k_i, k_o,
                        0, vg, 0, vl, chunks, part);
+  }
   int rc = check_launch("kron_proj_kernel(gather)");
   if (rc) return rc;
   return kron_finish(part, B, chunks, k_o * k_i, scale, out, out_dtype, s);

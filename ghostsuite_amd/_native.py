@@ -72,6 +72,9 @@ _SIGNATURES = {
                                    _P, _I, _F, _P, _SZ, _P]),
     "gs_linear_rowdot": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
                               _P]),
+    "gs_linear_bias_dot_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I]),
+    "gs_linear_bias_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P,
+                                _I, _F, _P, _SZ, _P]),
 }
 
 # How the val-gradient algorithm forms V = G_val^T A_val for the pairwise semantics: "native"
@@ -255,9 +258,9 @@ class HipOps:
                         grad_dtype: Optional[torch.dtype] = None):
         """Weight and bias dots of a Linear layer (and the bias train gradient when
         grad_scale is given) in one pass over the train rows when the shape allows it: the
-        val-gradient algorithm with gs_linear_rowdot_bias, V from torch.mm (pairwise, library
-        V GEMM) or gs_linear_val_gradient.  Otherwise None (the caller then uses linear_dot
-        and bias_dot).  Returns (dot, bias_dot, bias_grad)."""
+        val-gradient algorithm through gs_linear_bias_dot, or, for the pairwise semantics with
+        the library V GEMM, torch.mm for V and gs_linear_rowdot_bias.  Otherwise None (the
+        caller then uses linear_dot and bias_dot).  Returns (dot, bias_dot, bias_grad)."""
         dev = _require_device(A, G)
         if A.dtype != G.dtype or A.dtype != torch.bfloat16 or \
                 semantics not in (SEM_PAIRWISE_SUM, SEM_PRESUM) or \
@@ -274,29 +277,36 @@ class HipOps:
         if lib.gs_linear_dot_algo(dt, N, n_val, T, d_in, d_out, semantics, algo,
                                   0) != ALGO_VALGRAD:
             return None
-        ws_bytes = lib.gs_linear_rowdot_bias_workspace(dt, N, n_val, T, d_in, d_out)
+        library_v = semantics == SEM_PAIRWISE_SUM and V_GEMM == "library"
+        ws_bytes = (lib.gs_linear_rowdot_bias_workspace(dt, N, n_val, T, d_in, d_out)
+                    if library_v else
+                    lib.gs_linear_bias_dot_workspace(dt, N, n_val, T, d_in, d_out, semantics))
         if ws_bytes == 0:
             return None
         A = A.contiguous()
         G = G.contiguous()
         vs = N - n_val
-        if semantics == SEM_PAIRWISE_SUM and V_GEMM == "library":
-            Av = A.view(N, T, d_in)[vs:]
-            Gv = G.view(N, T, d_out)[vs:]
-            V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
-        else:
-            V = self.linear_val_gradient(A, G, n_val, val_start=vs, semantics=semantics)
         ws = _workspace(ws_bytes, dev)
         out = torch.empty(n_t, dtype=torch.float32, device=dev)
         bout = torch.empty(n_t, dtype=torch.float32, device=dev)
         gdt = grad_dtype or G.dtype
         grad = torch.empty(d_out, dtype=gdt, device=dev) if grad_scale is not None else None
-        rc = lib.gs_linear_rowdot_bias(A.data_ptr(), G.data_ptr(), V.data_ptr(), dt, N, n_val,
-                                       vs, T, d_in, d_out, out.data_ptr(),
-                                       bout.data_ptr(), _ptr(grad), _TORCH_TO_GS[gdt],
-                                       float(grad_scale or 0.0), ws.data_ptr(), ws_bytes,
-                                       _stream(dev))
-        _check(rc, "gs_linear_rowdot_bias")
+        if library_v:
+            Av = A.view(N, T, d_in)[vs:]
+            Gv = G.view(N, T, d_out)[vs:]
+            V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
+            rc = lib.gs_linear_rowdot_bias(A.data_ptr(), G.data_ptr(), V.data_ptr(), dt, N,
+                                           n_val, vs, T, d_in, d_out, out.data_ptr(),
+                                           bout.data_ptr(), _ptr(grad), _TORCH_TO_GS[gdt],
+                                           float(grad_scale or 0.0), ws.data_ptr(), ws_bytes,
+                                           _stream(dev))
+            _check(rc, "gs_linear_rowdot_bias")
+        else:
+            rc = lib.gs_linear_bias_dot(A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in,
+                                        d_out, semantics, out.data_ptr(), bout.data_ptr(),
+                                        _ptr(grad), _TORCH_TO_GS[gdt], float(grad_scale or 0.0),
+                                        ws.data_ptr(), ws_bytes, _stream(dev))
+            _check(rc, "gs_linear_bias_dot")
         return out, bout, grad
 
     def linear_rowdot(self, A: torch.Tensor, G: torch.Tensor, V: torch.Tensor, n_val: int, *,

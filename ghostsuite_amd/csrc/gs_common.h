@@ -36,12 +36,15 @@ struct Carver {
 };
 
 // Sizes-only twin of Carver, used by the *_workspace() queries.
+// Counts what a Carver would take; take() returns a null pointer of the same type, so one
+// carving routine serves both.
 struct Sizer {
   size_t used = 0;
   template <class T>
-  void take(size_t n) {
+  T* take(size_t n) {
     used = align_up(used, 256);
     used += n * sizeof(T);
+    return nullptr;
   }
 };
 

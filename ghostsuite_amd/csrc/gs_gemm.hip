@@ -91,8 +91,13 @@ struct GemmParams {
   int z_vec_ok;
   int64_t z_nbytes;        // extent of Z (buffer-resource range)
   // ROWDOT with the bias folded in (LDS epilogue only): BP = column sums of the Z tile per
-  // N tile ([n_tiles][m_rows]); null when the bias is handled elsewhere.
+  // N tile ([n_tiles][m_rows]); with PB also the tile's bias-dot share
+  // sum_m vb[m] * colsum[m] (layout of P), vb[m] = sum of the vp_rows rows of vp.  Null
+  // when the bias is handled elsewhere.
   float* BP;
+  float* PB;
+  const float* vp;
+  int64_t vp_rows;
   // STORE
   void* C;
   int64_t c_ld;
@@ -629,6 +634,10 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
   const int wm = wid / C::WN, wn = wid % C::WN;
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z, p.z_nbytes);
   const int sub = lane / CPR, sl = lane % CPR;
+  // The tile's slice of the val bias gradient, loaded while the Z tile comes in.
+  float vbm = 0.f;
+  if (p.PB != nullptr && threadIdx.x < C::BM)
+    for (int64_t r = 0; r < p.vp_rows; ++r) vbm += p.vp[r * p.m_rows + mt * C::BM + threadIdx.x];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int r = RPI * (wid + NW * q) + sub;  // local row (train token) of this lane's chunk
@@ -684,11 +693,20 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
     }
     reinterpret_cast<float4*>(bsum)[grp * LPR + q] = cs;
     __syncthreads();
-    for (int m = threadIdx.x; m < C::BM; m += C::NT) {
+    static_assert(C::BM <= C::NT, "one thread per tile column");
+    float qb = 0.f;
+    if (threadIdx.x < C::BM) {
+      const int m = threadIdx.x;
       float t = 0.f;
 #pragma unroll
       for (int g = 0; g < GRP; ++g) t += bsum[g * C::BM + m];
       p.BP[nt * p.m_rows + mt * C::BM + m] = t;
+      qb = vbm * t;
+    }
+    if (p.PB != nullptr) {  // the tile's bias-dot share, fixed-order block sum
+      __shared__ float qred[C::NT / 64];
+      const float tot = block_sum(qb, qred);
+      if (threadIdx.x == 0) p.PB[(p.p_row0 + mt) * p.p_ld + nt] = tot;
     }
   }
   raw_barrier();  // every wave's Z reads are done before the LDS is reused
@@ -952,77 +970,43 @@ __global__ void __launch_bounds__(256) val_colsum_kernel(const uint16_t* __restr
   }
 }
 
-// Bias finish, column stage: block (x, i) owns columns [256 x, +256) of train sample i.
-// Per column m: vb[m] = sum of the VP rows, b[m] = sum of the tile column sums BP over the
-// sample's `tps` N tiles; Q[i][x] = sum_m vb[m] b[m] (the sample's bias-dot share of these
-// columns) and BS[i][m] = b[m] (for the train gradient).  Fixed order throughout.
-__global__ void __launch_bounds__(256) rowdot_bias_cols_kernel(
-    const float* __restrict__ VP, int64_t vp_rows, const float* __restrict__ BP, int64_t tps,
-    int64_t F, float* __restrict__ Q, int64_t q_ld, float* __restrict__ BS) {
-  __shared__ float red[4];
-  const int64_t m = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t i = blockIdx.y;
-  float vb = 0.f, b = 0.f;
-  if (m < F) {
-    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
-    int64_t s = 0;
-    for (; s + 4 <= vp_rows; s += 4) {
-      v0 += VP[s * F + m];
-      v1 += VP[(s + 1) * F + m];
-      v2 += VP[(s + 2) * F + m];
-      v3 += VP[(s + 3) * F + m];
-    }
-    for (; s < vp_rows; ++s) v0 += VP[s * F + m];
-    vb = (v0 + v1) + (v2 + v3);
-    const float* bp = BP + i * tps * F + m;
-    float b0 = 0.f, b1 = 0.f;
-    int64_t k = 0;
-    for (; k + 2 <= tps; k += 2) {
-      b0 += bp[k * F];
-      b1 += bp[(k + 1) * F];
-    }
-    if (k < tps) b0 += bp[k * F];
-    b = b0 + b1;
-    BS[i * F + m] = b;
-  }
-  const float q = block_sum(vb * b, red);
-  if (threadIdx.x == 0) Q[i * q_ld + blockIdx.x] = q;
-}
-
-// Bias finish, row stage: blocks [0, n_train) reduce the weight-dot partials P of train
-// sample i, blocks [n_train, 2 n_train) its bias-dot shares Q[i][0..q_ld), blocks beyond
-// take grad[f] = scale * sum over the train samples of BS[i][f] (all fixed order).
+// Finish of the row-dot with the bias folded in: blocks [0, n_train) reduce the weight-dot
+// partials P of train sample i, blocks [n_train, 2 n_train) its bias-dot shares PB (same
+// layout), blocks beyond take grad[f] = scale * sum over the N tiles of BP[tile][f] for 64
+// columns each, 4 row groups combined in LDS (all fixed order).
 template <class GE>
-__global__ void __launch_bounds__(256) rowdot_bias_rows_kernel(
-    const float* __restrict__ P, int64_t rows, int64_t p_ld, int64_t cols, int64_t n_train,
-    float* out_dot, const float* __restrict__ Q, int64_t q_ld, float* out_bdot,
-    const float* __restrict__ BS, int64_t F, GE* grad, float scale) {
-  __shared__ float red[16];
+__global__ void __launch_bounds__(256) rowdot_bias_finish_kernel(
+    const float* __restrict__ P, const float* __restrict__ PB, int64_t rows, int64_t p_ld,
+    int64_t cols, int64_t n_train, float* out_dot, float* out_bdot,
+    const float* __restrict__ BP, int64_t n_tiles, int64_t F, GE* grad, float scale) {
+  __shared__ float red[4][64];
   const int64_t b = blockIdx.x;
-  if (b < n_train) {
-    const float s = block_sum(partial_share(P, 0, rows, p_ld, b, cols), red);
-    if (threadIdx.x == 0) out_dot[b] = s;
-    return;
-  }
   if (b < 2 * n_train) {
-    const int64_t i = b - n_train;
-    const float s = block_sum(partial_share(Q, i, 1, q_ld, 0, q_ld), red);
-    if (threadIdx.x == 0) out_bdot[i] = s;
+    const bool is_bias = b >= n_train;
+    const int64_t i = is_bias ? b - n_train : b;
+    const float s = block_sum(partial_share(is_bias ? PB : P, 0, rows, p_ld, i, cols),
+                              &red[0][0]);
+    if (threadIdx.x == 0) (is_bias ? out_bdot : out_dot)[i] = s;
     return;
   }
   if (grad == nullptr) return;
-  const int64_t f = (b - 2 * n_train) * blockDim.x + threadIdx.x;
-  if (f >= F) return;
+  const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int64_t f = (b - 2 * n_train) * 64 + c;
   float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
-  int64_t k = 0;
-  for (; k + 4 <= n_train; k += 4) {
-    t0 += BS[k * F + f];
-    t1 += BS[(k + 1) * F + f];
-    t2 += BS[(k + 2) * F + f];
-    t3 += BS[(k + 3) * F + f];
+  if (f < F) {
+    int64_t k = rg;
+    for (; k + 12 < n_tiles; k += 16) {
+      t0 += BP[k * F + f];
+      t1 += BP[(k + 4) * F + f];
+      t2 += BP[(k + 8) * F + f];
+      t3 += BP[(k + 12) * F + f];
+    }
+    for (; k < n_tiles; k += 4) t0 += BP[k * F + f];
   }
-  for (; k < n_train; ++k) t0 += BS[k * F + f];
-  grad[f] = from_f32<GE>(scale * ((t0 + t1) + (t2 + t3)));
+  red[rg][c] = (t0 + t1) + (t2 + t3);
+  __syncthreads();
+  if (rg == 0 && f < F)
+    grad[f] = from_f32<GE>(scale * ((red[0][c] + red[1][c]) + (red[2][c] + red[3][c])));
 }
 
 // out[f][c] = row c of the row set, feature f (with `presum`: c = position, summed over all
@@ -1194,6 +1178,7 @@ struct TnParams {
   int64_t M, N, m_tiles, n_tiles;
   void* out;        // splits == 1: bf16 [M][N]; else fp32 partials [split][M][N]
   int splits;
+  float* vsum;      // null, or [split][M]: column sums of L over the split's k-rows
 };
 
 template <class C, class D>
@@ -1307,10 +1292,29 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
 
 // acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same
 // schedule as mainloop_dma: constant vmcnt wait, barrier, loads of stage k + NS - 1, MFMAs).
+// Column sums of a stage's L part: thread t owns the 4 columns of group t % (BM / 4) and
+// every (NT / (BM / 4))-th k-row from t / (BM / 4); zero-filled rows add nothing.
+template <class C, class D>
+__device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs)[4]) {
+  constexpr int CG = C::BM / 4, NRG = C::NT / CG;
+  static_assert(C::NT % CG == 0, "column groups");
+  const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
+  const int c = cg >> 1, hb = (cg & 1) * 8;
+#pragma unroll 4
+  for (int r = rg; r < D::KB; r += NRG) {
+    union { uint2 v; uint16_t e[4]; } z;
+    z.v = *reinterpret_cast<const uint2*>(stage + r * D::RL +
+                                          ((c ^ D::template swz<D::CL>(r)) * 16) + hb);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cs[e] += bf16_to_f32(z.e[e]);
+  }
+}
+
 template <class C, class D>
 __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
                                             int64_t k_begin, int64_t k_end, unsigned char* lds,
-                                            f32x16_t (&acc)[C::MI][C::NI]) {
+                                            f32x16_t (&acc)[C::MI][C::NI], bool colsum,
+                                            float (&cs)[4]) {
   constexpr int NQ = D::QL + D::QR;
   constexpr int AHEAD = D::STAGES - 1;
   static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
@@ -1327,11 +1331,13 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
     raw_barrier();
     st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
     tn_compute<C, D>(slot(kt), acc);
+    if (colsum) tn_colsum<C, D>(slot(kt), cs);
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
     tn_compute<C, D>(slot(kt), acc);
+    if (colsum) tn_colsum<C, D>(slot(kt), cs);
   }
   wait_vmcnt<0>();
   raw_barrier();
@@ -1348,7 +1354,27 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
   const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
-  mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc);
+  // The workgroups of N tile 0 also take the column sums of their L tile (the val rows of
+  // G: the val bias gradient), combined across the row groups in a fixed order.
+  const bool colsum = p.vsum != nullptr && nt == 0;
+  float cs[4] = {0.f, 0.f, 0.f, 0.f};
+  mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs);
+  if (colsum) {
+    constexpr int CG = C::BM / 4, NRG = C::NT / CG;
+    static_assert(NRG * C::BM * 4 <= D::STAGES * D::STAGE_BYTES, "column-sum scratch");
+    float* red = reinterpret_cast<float*>(lds);  // the stages are free after the mainloop
+    const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[rg * C::BM + 4 * cg + e] = cs[e];
+    __syncthreads();
+    for (int m = threadIdx.x; m < C::BM; m += C::NT) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < NRG; ++g) t += red[g * C::BM + m];
+      const int64_t col = mt * C::BM + m;
+      if (col < p.M) p.vsum[static_cast<int64_t>(blockIdx.y) * p.M + col] = t;
+    }
+  }
   GemmParams e{};
   e.m_rows = p.M;
   e.n_cols = p.N;
@@ -1548,7 +1574,11 @@ bool tn_ok(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, in
 
 // Splits of the k-rows: enough workgroups to cover the CUs against the fp32 partials'
 // extra write + read (estimated at 4 TF/s per CU and 4 TB/s).
-int tn_splits(int64_t K, int64_t M, int64_t N) {
+int64_t tn_kper(int64_t K, int sp) {
+  return ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
+         TnD::KB;
+}
+int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
   const int64_t ksteps = ceil_div(K, static_cast<int64_t>(TnD::KB));
   if (GS_TN_SPLIT > 0) return static_cast<int>(std::min<int64_t>(GS_TN_SPLIT, ksteps));
   const double tiles = static_cast<double>(ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN));
@@ -1564,6 +1594,10 @@ int tn_splits(int64_t K, int64_t M, int64_t N) {
   }
   return best;
 }
+// The split count a launch uses: the k-rows per split are rounded up to whole stages.
+int tn_splits(int64_t K, int64_t M, int64_t N) {
+  return static_cast<int>(ceil_div(K, tn_kper(K, tn_splits_raw(K, M, N))));
+}
 int64_t tn_part_elems(int64_t K, int64_t M, int64_t N) {
   const int sp = tn_splits(K, M, N);
   return sp > 1 ? sp * M * N : 0;
@@ -1578,7 +1612,7 @@ bool val_tn(int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, in
 }
 // out [M][N] bf16 = L^T R over K k-rows (L: [K][M] stride ldl, R: [K][N] stride ldr).
 int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
-              int64_t N, void* out, float* part, hipStream_t s) {
+              int64_t N, void* out, float* part, hipStream_t s, float* vsum = nullptr) {
   TnParams p{};
   p.L = L;
   p.R = R;
@@ -1591,11 +1625,10 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   p.N = N;
   p.m_tiles = ceil_div(M, TnC::BM);
   p.n_tiles = ceil_div(N, TnC::BN);
-  int sp = tn_splits(K, M, N);
-  p.kper = ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
-           TnD::KB;
-  sp = static_cast<int>(ceil_div(K, p.kper));
+  p.kper = tn_kper(K, tn_splits_raw(K, M, N));
+  const int sp = tn_splits(K, M, N);
   p.splits = sp;
+  p.vsum = vsum;
   p.out = sp > 1 ? static_cast<void*>(part) : out;
   if (sp > 1 && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
   const int64_t tiles = p.m_tiles * p.n_tiles;
@@ -2133,93 +2166,41 @@ bool rowdot_bias_ok(int dtype, const void* A, const void* G, const void* V, int6
 
 namespace gs {
 namespace {
-// Workspace layout of the fused row-dot + bias path.
+// Layout of the fused row-dot + bias pass: P (weight-dot partials), PB (bias-dot partials,
+// same layout), BP (tile column sums [n_tiles][d_out]).
 struct RowdotBiasPlan {
   RowdotPlan pl;
-  int64_t n_t, n_tiles, tps, vp_rows, col_blocks;
+  int64_t n_t, n_tiles;
 };
 RowdotBiasPlan plan_rowdot_bias(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
-  using RC = RowdotCfg<TrBF16>;
   RowdotBiasPlan b;
   b.pl = plan_rowdot_any(dtype, N, n_val, T, d_out);
   b.n_t = N - n_val;
-  b.tps = T / RC::BN;
-  b.n_tiles = b.n_t * b.tps;
-  b.vp_rows = ceil_div(n_val * T, static_cast<int64_t>(VS_ROWS));
-  b.col_blocks = ceil_div(d_out, int64_t{256});
+  b.n_tiles = b.n_t * T / RowdotCfg<TrBF16>::BN;
   return b;
 }
-// P (weight-dot partials), BP (tile column sums), VP (val column sums), Q (bias-dot
-// shares per sample and column block), BS (train column sums per sample), in this order.
-void rowdot_bias_sizes(const RowdotBiasPlan& b, int64_t d_out, size_t (&n)[5]) {
-  n[0] = b.pl.n_mt * b.pl.p_ld;
-  n[1] = b.n_tiles * d_out;
-  n[2] = b.vp_rows * d_out;
-  n[3] = b.n_t * b.col_blocks;
-  n[4] = b.n_t * d_out;
-}
-}  // namespace
-}  // namespace gs
-
-extern "C" size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
-                                                  int64_t d_in, int64_t d_out) {
-  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
-    return 0;
-  if (!rowdot_bias_ok(dtype, nullptr, nullptr, nullptr, N, T, d_in, d_out)) return 0;
-  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
-  size_t n[5];
-  rowdot_bias_sizes(b, d_out, n);
-  Sizer sz;
-  for (size_t k : n) sz.take<float>(k);
-  return sz.used + 256;
+template <class S>
+void carve_rowdot_bias(S& c, const RowdotBiasPlan& b, int64_t d_out, float** P, float** PB,
+                       float** BP) {
+  const size_t np = b.pl.n_mt * b.pl.p_ld;
+  *P = c.template take<float>(np);
+  *PB = c.template take<float>(np);
+  *BP = c.template take<float>(b.n_tiles * d_out);
 }
 
-extern "C" int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype,
-                                     int64_t N, int64_t n_val, int64_t val_start, int64_t T,
-                                     int64_t d_in, int64_t d_out, float* out_dot,
-                                     float* out_bias_dot, void* out_bias_grad, int grad_dtype,
-                                     float grad_scale, void* workspace, size_t workspace_bytes,
-                                     void* stream) {
-  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
-    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: invalid shape");
-  if (val_start < 0 || val_start + n_val > N)
-    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: val block outside the batch");
-  if (A == nullptr || G == nullptr || V == nullptr || out_dot == nullptr ||
-      out_bias_dot == nullptr)
-    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: null pointer");
-  if (grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32)
-    return fail(GS_ERR_DTYPE, "gs_linear_rowdot_bias: grad_dtype must be bf16 or fp32");
-  if (!rowdot_bias_ok(dtype, A, G, V, N, T, d_in, d_out))
-    return fail(GS_ERR_UNSUPPORTED,
-                "gs_linear_rowdot_bias: needs bf16, 16-byte aligned operands below 2 GiB, "
-                "T a multiple of 256 and d_out a multiple of 256");
+// ROWDOT over the train rows with the bias terms (vb = the vp_rows rows of vp summed), then
+// the finishing kernel.  Shapes were checked by rowdot_bias_ok.
+int launch_rowdot_bias(const void* A, const void* G, const void* V, const float* vp,
+                       int64_t vp_rows, int64_t N, int64_t n_val, int64_t val_start, int64_t T,
+                       int64_t d_in, int64_t d_out, const RowdotBiasPlan& b, float* P, float* PB,
+                       float* BP, float* out_dot, float* out_bias_dot, void* out_bias_grad,
+                       int grad_dtype, float grad_scale, hipStream_t s) {
   using RC = RowdotCfg<TrBF16>;
   using RD = DmaForEpi<RC, EPI_ROWDOT>;
-  // Every tile must take the LDS epilogue, the only one that writes the tile column sums.
+  // Every tile must take the LDS epilogue, the only one that writes the bias terms.
   static_assert(static_cast<int64_t>(RC::BN) * RC::BM * 2 <= RD::STAGES * RD::STAGE_BYTES &&
                     RD::STAGES * RD::STAGE_BYTES <= 160 * 1024,
                 "row-dot tile does not take the LDS epilogue");
-  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
-  if (workspace == nullptr ||
-      workspace_bytes < gs_linear_rowdot_bias_workspace(dtype, N, n_val, T, d_in, d_out) - 256)
-    return fail(GS_ERR_WORKSPACE, "gs_linear_rowdot_bias: workspace too small");
-  size_t n[5];
-  rowdot_bias_sizes(b, d_out, n);
-  Carver cv(workspace, workspace_bytes);
-  float* P = cv.take<float>(n[0]);
-  float* BP = cv.take<float>(n[1]);
-  float* VP = cv.take<float>(n[2]);
-  float* Q = cv.take<float>(n[3]);
-  float* BS = cv.take<float>(n[4]);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  // Val column sums of G (stage 1 of the val bias gradient).
-  const dim3 vgrid(static_cast<unsigned>(ceil_div(d_out, static_cast<int64_t>(VS_COLS))),
-                   static_cast<unsigned>(b.vp_rows));
-  hipLaunchKernelGGL(val_colsum_kernel, vgrid, dim3(256), 0, s,
-                     static_cast<const uint16_t*>(G) + val_start * T * d_out, n_val * T, d_out,
-                     VP);
-  int rc = check_launch("val_colsum_kernel");
-  if (rc) return rc;
   const RowMap tr = train_rows(N, n_val, val_start, T);
   GemmParams r{};
   r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, 2, d_out * d_in * 2);
@@ -2238,24 +2219,181 @@ extern "C" int gs_linear_rowdot_bias(const void* A, const void* G, const void* V
   r.z_vec_ok = 1;
   r.z_nbytes = N * T * d_out * 2;
   r.BP = BP;
+  r.PB = PB;
+  r.vp = vp;
+  r.vp_rows = vp_rows;
   if (r.n_tiles != b.n_tiles || !b.pl.tile_reduce || !dma_ok(r.L1) || !dma_ok(r.R1))
     return fail(GS_ERR_INVALID, "internal: row-dot tiles");
-  rc = Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
+  int rc = Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
   if (rc) return rc;
-  const dim3 cgrid(static_cast<unsigned>(b.col_blocks), static_cast<unsigned>(b.n_t));
-  hipLaunchKernelGGL(rowdot_bias_cols_kernel, cgrid, dim3(256), 0, s, VP, b.vp_rows, BP, b.tps,
-                     d_out, Q, b.col_blocks, BS);
-  rc = check_launch("rowdot_bias_cols_kernel");
-  if (rc) return rc;
-  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{256}) : 0;
+  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{64}) : 0;
   const dim3 grid(static_cast<unsigned>(2 * b.n_t + gblocks));
   if (grad_dtype == GS_DTYPE_F32)
-    hipLaunchKernelGGL(rowdot_bias_rows_kernel<float>, grid, dim3(256), 0, s, P, b.pl.n_mt,
-                       b.pl.p_ld, b.pl.cols, b.n_t, out_dot, Q, b.col_blocks, out_bias_dot, BS,
-                       d_out, static_cast<float*>(out_bias_grad), grad_scale);
+    hipLaunchKernelGGL(rowdot_bias_finish_kernel<float>, grid, dim3(256), 0, s, P, PB,
+                       b.pl.n_mt, b.pl.p_ld, b.pl.cols, b.n_t, out_dot, out_bias_dot, BP,
+                       b.n_tiles, d_out, static_cast<float*>(out_bias_grad), grad_scale);
   else
-    hipLaunchKernelGGL(rowdot_bias_rows_kernel<uint16_t>, grid, dim3(256), 0, s, P, b.pl.n_mt,
-                       b.pl.p_ld, b.pl.cols, b.n_t, out_dot, Q, b.col_blocks, out_bias_dot, BS,
-                       d_out, static_cast<uint16_t*>(out_bias_grad), grad_scale);
-  return check_launch("rowdot_bias_rows_kernel");
+    hipLaunchKernelGGL(rowdot_bias_finish_kernel<uint16_t>, grid, dim3(256), 0, s, P, PB,
+                       b.pl.n_mt, b.pl.p_ld, b.pl.cols, b.n_t, out_dot, out_bias_dot, BP,
+                       b.n_tiles, d_out, static_cast<uint16_t*>(out_bias_grad), grad_scale);
+  return check_launch("rowdot_bias_finish_kernel");
+}
+
+int check_bias_args(const char* who, const void* A, const void* G, float* out_dot,
+                    float* out_bias_dot, int grad_dtype, int64_t N, int64_t n_val,
+                    int64_t val_start) {
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, std::string(who) + ": val block outside the batch");
+  if (A == nullptr || G == nullptr || out_dot == nullptr || out_bias_dot == nullptr)
+    return fail(GS_ERR_INVALID, std::string(who) + ": null pointer");
+  if (grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, std::string(who) + ": grad_dtype must be bf16 or fp32");
+  return GS_OK;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                                  int64_t d_in, int64_t d_out) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
+    return 0;
+  if (!rowdot_bias_ok(dtype, nullptr, nullptr, nullptr, N, T, d_in, d_out)) return 0;
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  Sizer sz;
+  float *P, *PB, *BP;
+  carve_rowdot_bias(sz, b, d_out, &P, &PB, &BP);
+  sz.take<float>(ceil_div(n_val * T, static_cast<int64_t>(VS_ROWS)) * d_out);  // VP
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype,
+                                     int64_t N, int64_t n_val, int64_t val_start, int64_t T,
+                                     int64_t d_in, int64_t d_out, float* out_dot,
+                                     float* out_bias_dot, void* out_bias_grad, int grad_dtype,
+                                     float grad_scale, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
+    return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: invalid shape");
+  int rc = check_bias_args("gs_linear_rowdot_bias", A, G, out_dot, out_bias_dot, grad_dtype, N,
+                           n_val, val_start);
+  if (rc) return rc;
+  if (V == nullptr) return fail(GS_ERR_INVALID, "gs_linear_rowdot_bias: null pointer");
+  if (!rowdot_bias_ok(dtype, A, G, V, N, T, d_in, d_out))
+    return fail(GS_ERR_UNSUPPORTED,
+                "gs_linear_rowdot_bias: needs bf16, 16-byte aligned operands below 2 GiB, "
+                "T a multiple of 256 and d_out a multiple of 256");
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  if (workspace == nullptr ||
+      workspace_bytes < gs_linear_rowdot_bias_workspace(dtype, N, n_val, T, d_in, d_out) - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_rowdot_bias: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  float *P, *PB, *BP;
+  carve_rowdot_bias(cv, b, d_out, &P, &PB, &BP);
+  const int64_t vp_rows = ceil_div(n_val * T, static_cast<int64_t>(VS_ROWS));
+  float* VP = cv.take<float>(vp_rows * d_out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Val column sums of G (stage 1 of the val bias gradient).
+  const dim3 vgrid(static_cast<unsigned>(ceil_div(d_out, static_cast<int64_t>(VS_COLS))),
+                   static_cast<unsigned>(vp_rows));
+  hipLaunchKernelGGL(val_colsum_kernel, vgrid, dim3(256), 0, s,
+                     static_cast<const uint16_t*>(G) + val_start * T * d_out, n_val * T, d_out,
+                     VP);
+  rc = check_launch("val_colsum_kernel");
+  if (rc) return rc;
+  return launch_rowdot_bias(A, G, V, VP, vp_rows, N, n_val, val_start, T, d_in, d_out, b, P, PB,
+                            BP, out_dot, out_bias_dot, out_bias_grad, grad_dtype, grad_scale, s);
+}
+
+// ------------------------------------------------------------------ Linear + bias, one call
+namespace gs {
+namespace {
+// V and the val bias gradient from the K-major GEMM (its N-tile-0 workgroups take the column
+// sums of the val rows of G), then the row-dot + bias pass.
+bool bias_dot_ok(int dtype, const void* A, const void* G, int64_t N, int64_t n_val, int64_t T,
+                 int64_t d_in, int64_t d_out, int presum) {
+  return val_tn(dtype, n_val, T, d_in, d_out, presum) &&
+         rowdot_bias_ok(dtype, A, G, A, N, T, d_in, d_out);
+}
+template <class S>
+void carve_bias_dot(S& c, const RowdotBiasPlan& b, int64_t n_val, int64_t T, int64_t d_in,
+                    int64_t d_out, int presum, float** P, float** PB, float** BP, void** V,
+                    float** VS, float** part, void** abar, void** gbar) {
+  carve_rowdot_bias(c, b, d_out, P, PB, BP);
+  const int64_t K = (presum ? 1 : n_val) * T;
+  *V = c.template take<uint16_t>(d_out * d_in);
+  *VS = c.template take<float>(static_cast<int64_t>(tn_splits(K, d_out, d_in)) * d_out);
+  *part = c.template take<float>(tn_part_elems(K, d_out, d_in));
+  *abar = presum ? c.template take<uint16_t>(T * d_in) : nullptr;
+  *gbar = presum ? c.template take<uint16_t>(T * d_out) : nullptr;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_bias_dot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                               int64_t d_in, int64_t d_out, int semantics) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, GS_ALGO_AUTO, 0)) return 0;
+  const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
+  if (!bias_dot_ok(dtype, nullptr, nullptr, N, n_val, T, d_in, d_out, presum)) return 0;
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  Sizer sz;
+  float *P, *PB, *BP, *VS, *part;
+  void *V, *abar, *gbar;
+  carve_bias_dot(sz, b, n_val, T, d_in, d_out, presum, &P, &PB, &BP, &V, &VS, &part, &abar,
+                 &gbar);
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64_t N,
+                                  int64_t n_val, int64_t val_start, int64_t T, int64_t d_in,
+                                  int64_t d_out, int semantics, float* out_dot,
+                                  float* out_bias_dot, void* out_bias_grad, int grad_dtype,
+                                  float grad_scale, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, GS_ALGO_AUTO, 0))
+    return fail(GS_ERR_INVALID, "gs_linear_bias_dot: invalid shape, dtype or semantics");
+  int rc = check_bias_args("gs_linear_bias_dot", A, G, out_dot, out_bias_dot, grad_dtype, N,
+                           n_val, val_start);
+  if (rc) return rc;
+  const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
+  if (!bias_dot_ok(dtype, A, G, N, n_val, T, d_in, d_out, presum))
+    return fail(GS_ERR_UNSUPPORTED,
+                "gs_linear_bias_dot: needs bf16, 16-byte aligned operands below 2 GiB, "
+                "T a multiple of 256 and d_out a multiple of 256");
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  if (workspace == nullptr ||
+      workspace_bytes <
+          gs_linear_bias_dot_workspace(dtype, N, n_val, T, d_in, d_out, semantics) - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_bias_dot: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  float *P, *PB, *BP, *VS, *part;
+  void *V, *abar, *gbar;
+  carve_bias_dot(cv, b, n_val, T, d_in, d_out, presum, &P, &PB, &BP, &V, &VS, &part, &abar,
+                 &gbar);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  using E = TrBF16::E;
+  const E* La = static_cast<const E*>(A) + val_start * T * d_in;
+  const E* Lg = static_cast<const E*>(G) + val_start * T * d_out;
+  if (presum) {
+    PresumPair pp{};
+    pp.in[0] = static_cast<const E*>(A);
+    pp.in[1] = static_cast<const E*>(G);
+    pp.out[0] = static_cast<E*>(abar);
+    pp.out[1] = static_cast<E*>(gbar);
+    pp.d[0] = d_in;
+    pp.d[1] = d_out;
+    const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
+                    static_cast<unsigned>(T), 2);
+    hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp,
+                       val_rows(n_val, val_start, T));
+    rc = check_launch("presum_rows_vec_kernel");
+    if (rc) return rc;
+    La = static_cast<const E*>(abar);
+    Lg = static_cast<const E*>(gbar);
+  }
+  const int64_t K = (presum ? 1 : n_val) * T;
+  rc = launch_tn(Lg, d_out, La, d_in, K, d_out, d_in, V, part, s, VS);
+  if (rc) return rc;
+  return launch_rowdot_bias(A, G, V, VS, tn_splits(K, d_out, d_in), N, n_val, val_start, T,
+                            d_in, d_out, b, P, PB, BP, out_dot, out_bias_dot, out_bias_grad,
+                            grad_dtype, grad_scale, s);
 }

@@ -140,6 +140,21 @@ int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype
                           void* out_bias_grad, int grad_dtype, float grad_scale,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* The whole Linear sampler with a bias in one call (weight dot, bias dot, bias train
+ * gradient), for the semantics of gs_linear_dot: the K-major GEMM forms V (its N-tile-0
+ * workgroups also sum the val rows of G: the val bias gradient), then the row-dot + bias pass
+ * of gs_linear_rowdot_bias.  Reference: _compute_linear_dot_product weight and bias parts
+ * (supported_layers_grad_samplers_dotprod.py:75-146), Conv1D (:369-471), and
+ * _compute_train_grad_bias (autograd_grad_sample_dotprod.py:199-222).  Same shape limits as
+ * gs_linear_rowdot_bias (the workspace query returns 0 outside them; use gs_linear_dot and
+ * gs_bias_dot then). */
+size_t gs_linear_bias_dot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                    int64_t d_in, int64_t d_out, int semantics);
+int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                       int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, int semantics,
+                       float* out_dot, float* out_bias_dot, void* out_bias_grad, int grad_dtype,
+                       float grad_scale, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Bias dot product and bias train gradient ---------------------------------------
  * Replaces the bias part of _compute_linear_dot_product (:137-146), the bias part of
  * _compute_Conv1D_dot_product (:450-471) and _compute_train_grad_bias

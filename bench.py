@@ -195,6 +195,14 @@ def gpt2_bench(steps: int, warmup: int, dev):
     log(f"[bench] ghost step, serialised dot kernels: {t_serial * 1e3:.2f} ms")
     t_plain = run(plain_step, steps, warmup, "plain")
     log(f"[bench] plain step {t_plain * 1e3:.2f} ms")
+
+    def plain_train_step(i):   # plain backprop of the n_train rows only
+        loss = plain(X_tr, Y_tr)
+        loss.backward()
+        popt.step()
+        popt.zero_grad(set_to_none=True)
+
+    t_plain_train = run(plain_train_step, steps, warmup, "plain (train rows only)")
     _native._install_backend(None)
     engine.detach()
     algos = dict(S.ALGO_LOG)
@@ -202,7 +210,8 @@ def gpt2_bench(steps: int, warmup: int, dev):
     torch.cuda.empty_cache()
     return {
         "n_train": n_train, "n_val": n_val, "T": T,
-        "t_ghost": t_ghost, "t_serial": t_serial, "t_plain": t_plain, "ops": ops_summary,
+        "t_ghost": t_ghost, "t_serial": t_serial, "t_plain": t_plain,
+        "t_plain_train": t_plain_train, "ops": ops_summary,
         "algos": algos,
         "plain_tflop": __import__("ghostsuite_amd.workloads", fromlist=["x"]).lm_flops_per_step(
             cfg, n_train + n_val, T) / 1e12,
@@ -275,6 +284,13 @@ def gradproj_bench(steps: int, warmup: int, dev):
     t_plain, _ = timed_steps(plain_step)
     kp = ops.get("kron_proj", {"ms": 0.0, "n": 1, "work": 0})
     avg = kp["ms"] / max(kp["n"], 1)
+    # MFMA work of the projections: 2*B*T*(n_a*k_i + n_g*k_o) per layer (the outer products
+    # over tokens add 2*B*T*k_i*k_o), summed over the 96 layers of one step.
+    cfgm = GPT2_MEDIUM
+    kf = 0.0
+    dm, dff = cfgm.d_model, cfgm.d_mlp
+    for n_a, n_g in ((dm, 3 * dm), (dm, dm), (dm, dff), (dff, dm)):
+        kf += cfgm.n_layer * 2.0 * B * T * (16 * n_a + 16 * n_g + 16 * 16)
     bytes_per_step = kp["work"] * kp["n"] / steps if kp["n"] else 0
     del model, eng
     torch.cuda.empty_cache()
@@ -285,7 +301,9 @@ def gradproj_bench(steps: int, warmup: int, dev):
             "kron_ms_per_step": kp["ms"] / steps, "kron_calls_per_step": kp["n"] / steps,
             "kron_avg_us": avg * 1e3,
             "kron_hbm_GBps": (bytes_per_step / (kp["ms"] / steps * 1e-3) / 1e9) if kp["ms"] else None,
-            "kron_hbm_frac": (bytes_per_step / (kp["ms"] / steps * 1e-3) / PEAK_HBM) if kp["ms"] else None}
+            "kron_hbm_frac": (bytes_per_step / (kp["ms"] / steps * 1e-3) / PEAK_HBM) if kp["ms"] else None,
+            "kron_mfma_TFLOPs": (kf / (kp["ms"] / steps * 1e-3) / 1e12) if kp["ms"] else None,
+            "kron_mfma_frac": (kf / (kp["ms"] / steps * 1e-3) / 2.5e15) if kp["ms"] else None}
 
 
 # ------------------------------------------------------------------ Pythia-1B shape
@@ -655,6 +673,7 @@ def main():
                    "global_batch": res["n_train"] + res["n_val"], "seq_len": res["T"],
                    "parallelism": "single GPU"},
         "plain_ms_per_step": res["t_plain"] * 1e3,
+        "plain_train_rows_only_ms_per_step": res["t_plain_train"] * 1e3,
         "ms_per_step_serialised_dots": res["t_serial"] * 1e3,
         "step_overhead": res["t_ghost"] / res["t_plain"],
         "rows_per_s_total": (res["n_train"] + res["n_val"]) / res["t_ghost"],

@@ -620,28 +620,27 @@ __device__ __forceinline__ void rowdot_colsum(const GemmParams& p, f32x16_t (&ac
 // reads its 4-element groups with one ds_read_b64.  Needs a full tile along M, 16-byte
 // aligned Z rows and Z below 4 GiB; `lds` holds at least BN * BM * 2 bytes.
 template <class C>
-__device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
-                                                  f32x16_t (&acc)[C::MI][C::NI], int64_t mt,
-                                                  int64_t nt, unsigned char* lds,
-                                                  float (&colsum)[C::NI], float* bsum) {
-  constexpr int CPR = C::BM / 8;           // 16-byte chunks per Z row
-  constexpr int RPI = 64 / CPR;            // rows per wave-level DMA
-  constexpr int NW = C::WM * C::WN;
-  constexpr int NQ = C::BN / RPI / NW;     // DMAs per wave
+struct ZTile {
+  static constexpr int CPR = C::BM / 8;        // 16-byte chunks per Z row
+  static constexpr int RPI = 64 / CPR;         // rows per wave-level DMA
+  static constexpr int NW = C::WM * C::WN;
+  static constexpr int NQ = C::BN / RPI / NW;  // DMAs per wave
   static_assert(64 % CPR == 0 && (C::BN / RPI) % NW == 0, "Z tile split");
   static_assert((CPR & (CPR - 1)) == 0, "chunks per row must be a power of two");
+};
+
+// Issues the Z-tile DMAs (16 contiguous bytes per lane, RPI rows per wave-level DMA).
+template <class C>
+__device__ __forceinline__ void rowdot_issue_z(const GemmParams& p, int64_t mt, int64_t nt,
+                                               unsigned char* lds) {
+  using Z = ZTile<C>;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wm = wid / C::WN, wn = wid % C::WN;
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z, p.z_nbytes);
-  const int sub = lane / CPR, sl = lane % CPR;
-  // The tile's slice of the val bias gradient, loaded while the Z tile comes in.
-  float vbm = 0.f;
-  if (p.PB != nullptr && threadIdx.x < C::BM)
-    for (int64_t r = 0; r < p.vp_rows; ++r) vbm += p.vp[r * p.m_rows + mt * C::BM + threadIdx.x];
+  const int sub = lane / Z::CPR, sl = lane % Z::CPR;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int r = RPI * (wid + NW * q) + sub;  // local row (train token) of this lane's chunk
-    const int c = sl ^ (r & (CPR - 1));
+  for (int q = 0; q < Z::NQ; ++q) {
+    const int r = Z::RPI * (wid + Z::NW * q) + sub;  // local row (train token) of the chunk
+    const int c = sl ^ (r & (Z::CPR - 1));
     const int64_t f = nt * C::BN + r;
     unsigned off = DMA_OOB;
     if (f < p.z_map.total()) {
@@ -649,8 +648,24 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
       const int64_t row = p.z_map.phys_row(seg, f - seg * p.z_map.seglen);
       off = static_cast<unsigned>((row * p.z_ld + mt * C::BM + c * 8) * 2);
     }
-    dma16(rz, off, lds + RPI * (wid + NW * q) * CPR * 16);
+    dma16(rz, off, lds + Z::RPI * (wid + Z::NW * q) * Z::CPR * 16);
   }
+}
+
+template <class C>
+__device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
+                                                  f32x16_t (&acc)[C::MI][C::NI], int64_t mt,
+                                                  int64_t nt, unsigned char* lds,
+                                                  float (&colsum)[C::NI], float* bsum) {
+  constexpr int CPR = ZTile<C>::CPR;
+  constexpr int NW = ZTile<C>::NW;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  // The tile's slice of the val bias gradient, loaded while the Z tile comes in.
+  float vbm = 0.f;
+  if (p.PB != nullptr && threadIdx.x < C::BM)
+    for (int64_t r = 0; r < p.vp_rows; ++r) vbm += p.vp[r * p.m_rows + mt * C::BM + threadIdx.x];
+  rowdot_issue_z<C>(p, mt, nt, lds);
   wait_vmcnt<0>();
   __syncthreads();  // Z landed (every wave waited for its DMA)
   const int half = (lane >> 5) * 8;

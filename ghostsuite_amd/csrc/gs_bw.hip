@@ -487,6 +487,176 @@ __global__ void emb_dot_kernel(const int64_t* __restrict__ ids, const E* __restr
   if (threadIdx.x == 0) part[i * chunks + c] = tot;
 }
 
+// ---- sorted-segment path (at most EMB_SORT_MAX val tokens, ids below 2^19) --------------
+// The val tokens are ordered by the distinct keys (id << EMB_QBITS | index): a token's sorted
+// position is the number of smaller keys (every workgroup counts against all keys in LDS).  A
+// run of equal ids is a segment and table[id] = the run's first sorted position.  Each run's
+// rows are summed in index order (fp32, no atomics, nothing to zero-fill), and each train
+// token dots its row with its id's run sum.
+constexpr int EMB_SORT_MAX = 8192, EMB_QBITS = 13;
+constexpr uint32_t EMB_NOKEY = 0xFFFFFFFFu;
+
+__device__ __forceinline__ uint32_t emb_key(const int64_t* __restrict__ ids, const RowMap& val,
+                                            int64_t vocab, int i) {
+  const uint32_t len = static_cast<uint32_t>(val.seglen);  // n_vt < 2^13: 32-bit division
+  const uint32_t seg = static_cast<uint32_t>(i) / len;
+  const int64_t id = ids[val.phys_row(seg, static_cast<uint32_t>(i) - seg * len)];
+  return (id >= 0 && id < vocab) ? (static_cast<uint32_t>(id) << EMB_QBITS) |
+                                       static_cast<uint32_t>(i)
+                                 : EMB_NOKEY;
+}
+
+// keys[rank(i)] = key(i); val tokens whose id is out of range go last, in index order.  A
+// workgroup ranks EMB_RK keys, each counted against all keys by EMB_RP threads (one slice of
+// the keys each) and the slice counts combined through LDS.
+// ukeys[i] = key(i) for i < n4 (padded with no-keys to a multiple of 4), table[0, vocab) = -1.
+__global__ void __launch_bounds__(BW_THREADS) emb_key_kernel(
+    const int64_t* __restrict__ ids, RowMap val, int64_t vocab, int32_t* __restrict__ table,
+    uint32_t* __restrict__ ukeys) {
+  const int n = static_cast<int>(val.total()), n4 = (n + 3) / 4 * 4;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t x0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t x = x0; x < vocab; x += gstride) table[x] = -1;
+  for (int64_t j = x0; j < n4; j += gstride)
+    ukeys[j] = j < n ? emb_key(ids, val, vocab, static_cast<int>(j)) : EMB_NOKEY;
+}
+
+constexpr int EMB_RK = 16, EMB_RP = BW_THREADS / EMB_RK;
+__global__ void __launch_bounds__(BW_THREADS) emb_rank_kernel(const uint32_t* __restrict__ ukeys,
+                                                              int n,
+                                                              uint32_t* __restrict__ keys) {
+  __shared__ __attribute__((aligned(16))) uint32_t sk[EMB_SORT_MAX];
+  __shared__ int cnt[3][EMB_RP][EMB_RK];
+  const int n4 = (n + 3) / 4 * 4;
+  for (int j = threadIdx.x * 4; j < n4; j += blockDim.x * 4)
+    *reinterpret_cast<uint4*>(sk + j) = *reinterpret_cast<const uint4*>(ukeys + j);
+  __syncthreads();
+  const int kk = threadIdx.x % EMB_RK, part = threadIdx.x / EMB_RK;
+  const int i = blockIdx.x * EMB_RK + kk;
+  const uint32_t k = i < n ? sk[i] : EMB_NOKEY;
+  const int span = (n4 / 4 + EMB_RP - 1) / EMB_RP * 4;  // keys per slice, a multiple of 4
+  const int j0 = part * span, j1 = j0 + span < n4 ? j0 + span : n4;
+  int lt = 0, inv_before = 0, n_valid = 0;
+  for (int j = j0; j < j1; j += 4) {
+    const uint4 w = *reinterpret_cast<const uint4*>(sk + j);
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lt += v[e] < k;
+      n_valid += (j + e < n) & (v[e] != EMB_NOKEY);
+      inv_before += (j + e < i) & (v[e] == EMB_NOKEY);
+    }
+  }
+  cnt[0][part][kk] = lt;
+  cnt[1][part][kk] = inv_before;
+  cnt[2][part][kk] = n_valid;
+  __syncthreads();
+  if (part == 0 && i < n) {
+    int a = 0, b = 0, c = 0;
+    for (int q = 0; q < EMB_RP; ++q) {
+      a += cnt[0][q][kk];
+      b += cnt[1][q][kk];
+      c += cnt[2][q][kk];
+    }
+    keys[k != EMB_NOKEY ? a : c + b] = k;
+  }
+}
+
+// S[p][:] = sum of the val rows of the run starting at sorted position p (index order), and
+// table[id] = p for that run.
+template <class E>
+__global__ void __launch_bounds__(BW_THREADS) emb_segsum_kernel(
+    const E* __restrict__ G, RowMap val, int64_t d, const uint32_t* __restrict__ keys,
+    int32_t* __restrict__ table, float* __restrict__ S) {
+  constexpr int VE = Vec<E>::VE;
+  const int64_t p = blockIdx.x, n_vt = val.total();
+  const uint32_t kprev = p > 0 ? keys[p - 1] : EMB_NOKEY;
+  const uint32_t k0 = keys[p];
+  const uint32_t knext = p + 1 < n_vt ? keys[p + 1] : EMB_NOKEY;
+  if (k0 == EMB_NOKEY || (p > 0 && (kprev >> EMB_QBITS) == (k0 >> EMB_QBITS))) return;
+  const uint32_t id = k0 >> EMB_QBITS;
+  if (threadIdx.x == 0) table[id] = static_cast<int32_t>(p);
+  const int vec = (d * static_cast<int64_t>(sizeof(E))) % 16 == 0 &&
+                  (reinterpret_cast<uintptr_t>(G) % 16 == 0);
+  for (int64_t f = static_cast<int64_t>(threadIdx.x) * VE; f < d;
+       f += static_cast<int64_t>(blockDim.x) * VE) {
+    float a[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) a[e] = 0.f;
+    for (int64_t r = p; r < n_vt; ++r) {
+      const uint32_t k = r == p ? k0 : r == p + 1 ? knext : keys[r];
+      if (k == EMB_NOKEY || (k >> EMB_QBITS) != id) break;
+      const int64_t q = k & ((1u << EMB_QBITS) - 1);
+      const int64_t seg = q / val.seglen;
+      Vec<E> x;
+      x.load(G + val.phys_row(seg, q - seg * val.seglen) * d + f, vec && f + VE <= d, d - f);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) a[e] += x.v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < VE; ++e)
+      if (f + e < d) S[p * d + f + e] = a[e];
+  }
+}
+
+// part[i * chunks + c] = sum over train row i's tokens in chunk c of <g_it, S[table[x_it]]>:
+// the chunk's run positions are looked up first (one token per thread), then one token per
+// wave at a time with lanes over 16-byte feature chunks; fixed-order block sum.
+template <class E>
+__global__ void __launch_bounds__(BW_THREADS) emb_segdot_kernel(
+    const int64_t* __restrict__ ids, const E* __restrict__ G, RowMap train, int64_t d,
+    int64_t vocab, const int32_t* __restrict__ table, const float* __restrict__ S,
+    int64_t chunks, float* __restrict__ part) {
+  constexpr int VE = Vec<E>::VE;
+  static_assert(TOK_CHUNK <= BW_THREADS, "one lookup per thread");
+  __shared__ float red[BW_THREADS / 64];
+  __shared__ int32_t rs[TOK_CHUNK];
+  const int64_t i = blockIdx.y, c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t T = train.seglen;
+  const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
+  if (threadIdx.x < TOK_CHUNK) {
+    int32_t r = -1;
+    const int64_t t = t0 + threadIdx.x;
+    if (t < t1) {
+      const int64_t id = ids[train.phys_row(i, t)];
+      if (id >= 0 && id < vocab) r = table[id];
+    }
+    rs[threadIdx.x] = r;
+  }
+  __syncthreads();
+  const int vec = (d * static_cast<int64_t>(sizeof(E))) % 16 == 0 &&
+                  (reinterpret_cast<uintptr_t>(G) % 16 == 0) && d % 4 == 0;
+  float s = 0.f;
+  const int half = lane >> 5, hl = lane & 31;  // two tokens per wave, 32 lanes each
+  for (int64_t tb = t0 + 2 * wid; tb < t1; tb += 2 * (BW_THREADS / 64)) {
+    const int64_t t = tb + half;
+    const int32_t r = t < t1 ? rs[t - t0] : -1;
+    if (r < 0) continue;
+    const E* gr = G + train.phys_row(i, t) * d;
+    const float* sr = S + static_cast<int64_t>(r) * d;
+#pragma unroll 4
+    for (int64_t f = static_cast<int64_t>(hl) * VE; f < d; f += 32 * VE) {
+      Vec<E> x;
+      const bool full = vec && f + VE <= d;
+      x.load(gr + f, full, d - f);
+      if (full) {
+#pragma unroll
+        for (int e = 0; e < VE; e += 4) {
+          const float4 w = *reinterpret_cast<const float4*>(sr + f + e);
+          s += x.v[e] * w.x + x.v[e + 1] * w.y + x.v[e + 2] * w.z + x.v[e + 3] * w.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VE; ++e)
+          if (f + e < d) s += x.v[e] * sr[f + e];
+      }
+    }
+  }
+  const float tot = block_sum(s, red);
+  if (threadIdx.x == 0) part[i * chunks + c] = tot;
+}
+
 __global__ void sum_chunks_kernel(const float* __restrict__ part, int64_t chunks,
                                   float* __restrict__ out) {
   __shared__ float red[BW_THREADS / 64];
@@ -706,12 +876,24 @@ extern "C" int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t
 
 // ------------------------------------------------------------------------------ embedding
 namespace {
+// The sorted-segment path when the val tokens fit one sorting workgroup, else the
+// fixed-point path.
+bool emb_sorted(int64_t n_val, int64_t T, int64_t vocab) {
+  // (id << EMB_QBITS | index) must stay below the no-key value.
+  return n_val * T <= EMB_SORT_MAX && vocab < (int64_t{1} << (32 - EMB_QBITS));
+}
 template <class S>
 void carve_embedding(S& c, int64_t N, int64_t n_val, int64_t T, int64_t d, int64_t vocab) {
   const int64_t n_vt = n_val * T, n_t = N - n_val, chunks = cdiv(T, TOK_CHUNK);
   c.template take<int32_t>(vocab);
-  c.template take<unsigned>(EMB_SLOTS);
-  c.template take<unsigned long long>(n_vt * d);
+  if (emb_sorted(n_val, T, vocab)) {
+    c.template take<uint32_t>(n_vt);
+    c.template take<uint32_t>(cdiv(n_vt, 4) * 4);
+    c.template take<float>(n_vt * d);
+  } else {
+    c.template take<unsigned>(EMB_SLOTS);
+    c.template take<unsigned long long>(n_vt * d);
+  }
   c.template take<float>(n_t * chunks);
 }
 }  // namespace
@@ -742,12 +924,41 @@ extern "C" int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, in
   Carver cv(workspace, workspace_bytes);
   const int64_t n_vt = n_val * T, n_t = N - n_val, chunks = cdiv(T, TOK_CHUNK);
   int32_t* table = cv.take<int32_t>(vocab);
-  unsigned* slots = cv.take<unsigned>(EMB_SLOTS);
-  unsigned long long* fix = cv.take<unsigned long long>(n_vt * d);
-  float* part = cv.take<float>(n_t * chunks);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const RowMap va = val_rows(n_val, val_start, T);
   const RowMap tr = train_rows(N, n_val, val_start, T);
+  if (emb_sorted(n_val, T, vocab)) {
+    uint32_t* keys = cv.take<uint32_t>(n_vt);
+    uint32_t* ukeys = cv.take<uint32_t>(cdiv(n_vt, 4) * 4);
+    float* S = cv.take<float>(n_vt * d);
+    float* part = cv.take<float>(n_t * chunks);
+    hipLaunchKernelGGL(emb_key_kernel,
+                       dim3(static_cast<unsigned>(cdiv(std::max(vocab, n_vt), BW_THREADS))),
+                       dim3(BW_THREADS), 0, s, ids, va, vocab, table, ukeys);
+    hipLaunchKernelGGL(emb_rank_kernel, dim3(static_cast<unsigned>(cdiv(n_vt, EMB_RK))),
+                       dim3(BW_THREADS), 0, s, ukeys, static_cast<int>(n_vt), keys);
+    const dim3 gv(static_cast<unsigned>(n_vt));
+    const dim3 gt(static_cast<unsigned>(chunks), static_cast<unsigned>(n_t));
+    if (dtype == GS_DTYPE_BF16) {
+      const uint16_t* g = static_cast<const uint16_t*>(G);
+      hipLaunchKernelGGL(emb_segsum_kernel<uint16_t>, gv, dim3(128), 0, s, g, va, d, keys,
+                         table, S);
+      hipLaunchKernelGGL(emb_segdot_kernel<uint16_t>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, d,
+                         vocab, table, S, chunks, part);
+    } else {
+      const float* g = static_cast<const float*>(G);
+      hipLaunchKernelGGL(emb_segsum_kernel<float>, gv, dim3(128), 0, s, g, va, d, keys, table,
+                         S);
+      hipLaunchKernelGGL(emb_segdot_kernel<float>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, d,
+                         vocab, table, S, chunks, part);
+    }
+    hipLaunchKernelGGL(sum_chunks_kernel, dim3(static_cast<unsigned>(n_t)), dim3(BW_THREADS), 0,
+                       s, part, chunks, out_dot);
+    return check_launch("embedding kernels");
+  }
+  unsigned* slots = cv.take<unsigned>(EMB_SLOTS);
+  unsigned long long* fix = cv.take<unsigned long long>(n_vt * d);
+  float* part = cv.take<float>(n_t * chunks);
   const int64_t prep_n = std::max<int64_t>(vocab, n_vt * d);
   hipLaunchKernelGGL(emb_prep_kernel,
                      dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(prep_n, 256), 8192))),

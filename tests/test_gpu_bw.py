@@ -25,6 +25,18 @@ def test_embedding_dot(gpu, dtype, shape):
         assert_close(dot.cpu(), want, tol, "embedding dot")
 
 
+@pytest.mark.parametrize("shape", [(6, 3, 3000, 16, 100), (5, 2, 40, 24, 600_000)])
+def test_embedding_dot_fixed_point_path(gpu, shape):
+    """More than 8192 val tokens, or ids of 2^19 and above: the fixed-point segment path."""
+    N, n_val, T, d, vocab = shape
+    ids = torch.randint(0, vocab, (N, T), generator=gen(31 + T))
+    G = randn((N, T, d), 32 + T, 1e-3, torch.bfloat16)
+    print(f"embedding fixed-point shape={shape}", flush=True)
+    dot = _native.ops().embedding_dot(ids.to(gpu), G.to(gpu), n_val, vocab)
+    torch.cuda.synchronize()
+    assert_close(dot.cpu(), R.embedding_dot_exact(ids, G, n_val), BF16_TOL, "embedding dot")
+
+
 def test_embedding_positions_and_all_equal_ids(gpu):
     N, n_val, T, d = 8, 2, 40, 32
     G = randn((N, T, d), 9, 1e-3)

@@ -334,3 +334,62 @@ def test_conv2d_engine_on_gpu(gpu, precision, tol, n_val):
             assert_close(want, brute.pairwise_dots(g[f"{idx}.weight"], 1), 1e-5, "closed form")
     for name, gr in grads.items():
         assert_close(gr, brute.train_mean(g[name], n_val, N), tol, f"grad {name}")
+
+
+@pytest.mark.parametrize("n_v", [1, 2])
+def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
+    """Tile-aligned shapes (T and every d_out multiples of 256) route each Linear with a bias
+    through the fused weight + bias pass: dots against brute force, and dots and train grads
+    against the separate weight and bias passes on the same bf16 run."""
+    torch.manual_seed(21)
+    T, vocab = 256, 64
+    cfg = LMConfig(n_layer=1, n_head=4, d_model=256, d_mlp=512, vocab=vocab, n_ctx=T)
+    model = CausalLM(cfg).to(torch.bfloat16).float()   # references start from the bf16 weights
+    untied = copy.deepcopy(model)
+    untied.lm_head.weight = nn.Parameter(model.wte.weight.detach().clone())
+    untied = untied.double()
+    n_t = 3
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=22)
+    model = model.to(gpu, torch.bfloat16)
+
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True,
+                            record_algorithms=True, linear_algo="valgrad")
+
+    def run():
+        S.ALGO_LOG.clear()
+        eng.attach(opt)
+        eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+        model(X.to(gpu), Y.to(gpu)).backward()
+        torch.cuda.synchronize()
+        dots = {n: p.grad_dot_prod.float().cpu() for n, p in model.named_parameters()
+                if hasattr(p, "grad_dot_prod")}
+        eng.prepare_gradients()
+        grads = {n: p.grad.float().cpu() for n, p in model.named_parameters()
+                 if p.grad is not None and "dummy_bias" not in n}
+        eng.aggregate_and_log()
+        eng.clear_gradients()
+        eng.detach()
+        return dots, grads, dict(S.ALGO_LOG)
+
+    print(f"gpt2 fused-bias engine n_v={n_v}", flush=True)
+    dots, grads, log = run()
+    assert sorted(k for k, v in log.items() if v[1] == "valgrad+bias") == \
+        ["h.0.fc", "h.0.fc_out", "h.0.proj", "h.0.qkv"], log
+    monkeypatch.setattr(S, "_fused_bias_dot", lambda *a, **k: False)
+    dots2, grads2, log2 = run()
+    assert not any(v[1] == "valgrad+bias" for v in log2.values()), log2
+    semantics = {n: m.use_ghost_computation for n, m in model.named_modules()
+                 if hasattr(m, "use_ghost_computation")}
+    N = n_t + n_v
+    g_untied = brute.per_sample_grads(untied, X, Y, _lm_loss(T), 1.0 / (N * T))
+    for name, d in dots.items():
+        assert_close(d, dots2[name], 1e-2, f"fused vs separate dot {name}")
+        layer = name.rsplit(".", 1)[0]
+        if not semantics.get(layer, True) and n_v > 1:
+            continue   # presum: not a function of the per-sample gradients
+        assert_close(d, brute.pairwise_dots(g_untied[name], n_v), BF16_TOL, f"dot {name}")
+    block = [n for n in grads if n.startswith("h.")]
+    assert block and all(n in grads2 for n in block), (sorted(grads), sorted(grads2))
+    for name in block:
+        assert_close(grads[name], grads2[name], 1e-2, f"fused vs separate grad {name}")

@@ -15,7 +15,10 @@ namespace gs {
 
 constexpr int BW_THREADS = 256;
 constexpr int TOK_CHUNK = 32;     // tokens per stage-1 block (bias, embedding)
-constexpr int LN_TOK_CHUNK = 64;  // tokens per LayerNorm stage-1 block (8 per wave)
+#ifndef GS_LN_TOK
+#define GS_LN_TOK 64
+#endif
+constexpr int LN_TOK_CHUNK = GS_LN_TOK;  // tokens per LayerNorm stage-1 block
 
 template <class E>
 __device__ __forceinline__ float ld(const E* p) {
@@ -371,10 +374,21 @@ __global__ void __launch_bounds__(BW_THREADS) feature_finish_kernel(
   if (fs.grad == nullptr) return;
   const int64_t f = (b - n_train) * blockDim.x + threadIdx.x;
   if (f >= F) return;
-  float t = 0.f;
-  for (int64_t n = 0; n < N; ++n)
-    if (n < val_start || n >= val_start + n_val) t += fs.S[n * F + f];
-  static_cast<GE*>(fs.grad)[f] = from_f32<GE>(grad_scale * t);
+  // Train rows are [0, val_start) and [val_start + n_val, N); four running sums in a fixed
+  // order keep several loads in flight.
+  float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+  const int64_t ranges[2][2] = {{0, val_start}, {val_start + n_val, N}};
+  for (const auto& rg : ranges) {
+    int64_t n = rg[0];
+    for (; n + 4 <= rg[1]; n += 4) {
+      t0 += fs.S[n * F + f];
+      t1 += fs.S[(n + 1) * F + f];
+      t2 += fs.S[(n + 2) * F + f];
+      t3 += fs.S[(n + 3) * F + f];
+    }
+    for (; n < rg[1]; ++n) t0 += fs.S[n * F + f];
+  }
+  static_cast<GE*>(fs.grad)[f] = from_f32<GE>(grad_scale * ((t0 + t1) + (t2 + t3)));
 }
 
 // ---------------------------------------------------------------- embedding

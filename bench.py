@@ -503,6 +503,12 @@ KERNEL_SHAPES = {
     "valgrad_fc": "linear_dot VALGRAD pairwise, A[20,1024,768] G[20,1024,3072] bf16, 4 val",
     "valgrad_bias_fc": "linear_bias_dot (weight + bias dots, bias grad), A[20,1024,768] "
                        "G[20,1024,3072] bf16, 4 val",
+    "valgrad_bias_fc_out": "linear_bias_dot (weight + bias dots, bias grad), A[20,1024,3072] "
+                           "G[20,1024,768] bf16, 4 val",
+    "valgrad_bias_qkv": "linear_bias_dot presum (weight + bias dots, bias grad), A[20,1024,768] "
+                        "G[20,1024,2304] bf16, 4 val",
+    "valgrad_bias_proj": "linear_bias_dot presum (weight + bias dots, bias grad), "
+                         "A[20,1024,768] G[20,1024,768] bf16, 4 val",
     "bias_fc": "bias_dot, G[20,1024,3072] bf16, 4 val",
     "layernorm": "layernorm_dot + grads, X,G[20,1024,768] bf16, 4 val",
     "embedding_wte": "embedding_dot, ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
@@ -551,6 +557,15 @@ def kernels_leg(dev, reps: int = 10):
     out["valgrad_bias_fc"] = timeit(lambda: ops.linear_bias_dot(A2, G2, 4,
                                                                 algo=_native.ALGO_VALGRAD,
                                                                 grad_scale=1.25))
+    for key, a_src, g_src, sem in (
+            ("valgrad_bias_fc_out", G2, A2, _native.SEM_PAIRWISE_SUM),
+            ("valgrad_bias_qkv", A2, G2[..., :2304], _native.SEM_PRESUM),
+            ("valgrad_bias_proj", A2, A2, _native.SEM_PRESUM)):
+        a_op, g_op = a_src.contiguous(), (g_src * 1e-3 if g_src is A2 else g_src).contiguous()
+        out[key] = timeit(lambda: ops.linear_bias_dot(a_op, g_op, 4, semantics=sem,
+                                                      algo=_native.ALGO_VALGRAD,
+                                                      grad_scale=1.25))
+        del a_op, g_op
     out["bias_fc"] = timeit(lambda: ops.bias_dot(G2, 4, grad_scale=1.25))
     X = rnd(20, 1024, 768)
     GL = rnd(20, 1024, 768, s=1e-3)

@@ -338,24 +338,43 @@ __device__ __forceinline__ void raw_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// One wave-level DMA to a wave-uniform LDS byte address (M0 from SGPRs, no readfirstlane).
+__device__ __forceinline__ void dma16_at(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r)
+               : "memory");
+}
+// LDS byte address of a __shared__ object (the generic -> local conversion, done once).
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  typedef const __attribute__((address_space(3))) unsigned char* lds_ptr;
+  return static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr)p));
+}
+// Byte offset of a row outside the operand: adding any k offset below 2^31 keeps it at or
+// above 2^31, past every buffer range (operands on this path are below 2 GiB).
+constexpr unsigned DMA_OOB_ROW = 0x80000000u;
+
 template <class C, class D>
 struct DmaStreamer {
   __amdgpu_buffer_rsrc_t rl, rr;
-  unsigned offl[D::QL], offr[D::QR];  // row byte offset + chunk byte offset, or DMA_OOB
+  unsigned offl[D::QL], offr[D::QR];  // row byte offset + chunk byte offset, or DMA_OOB_ROW
   int kl[D::QL], kr[D::QR];            // this lane's k element offset within a stage
+  unsigned wl;                         // wave-uniform LDS offset of this wave's first L load
 
   __device__ __forceinline__ void init(const Operand& L, const Operand& R, int64_t mt,
                                        int64_t nt) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int sub = lane / D::CH, slot = lane % D::CH;
     rl = make_rsrc(L.base, L.nbytes);
     rr = make_rsrc(R.base, R.nbytes);
+    wl = static_cast<unsigned>(wid * D::RPL * D::ROW_BYTES);
 #pragma unroll
     for (int q = 0; q < D::QL; ++q) {
       const int r = D::RPL * (wid + D::NW * q) + sub;
       const int c = slot ^ D::swz(r);
       const int64_t pr = tile_row<C::BM>(L, mt, r);
-      offl[q] = pr < 0 ? DMA_OOB : static_cast<unsigned>(pr * L.ld * 2 + c * 16);
+      offl[q] = pr < 0 ? DMA_OOB_ROW : static_cast<unsigned>(pr * L.ld * 2 + c * 16);
       kl[q] = c * 8;
     }
 #pragma unroll
@@ -363,25 +382,29 @@ struct DmaStreamer {
       const int r = D::RPL * (wid + D::NW * q) + sub;  // row within the R block of the stage
       const int c = slot ^ D::swz(C::BM + r);
       const int64_t pr = tile_row<C::BN>(R, nt, r);
-      offr[q] = pr < 0 ? DMA_OOB : static_cast<unsigned>(pr * R.ld * 2 + c * 16);
+      offr[q] = pr < 0 ? DMA_OOB_ROW : static_cast<unsigned>(pr * R.ld * 2 + c * 16);
       kr[q] = c * 8;
     }
   }
-  __device__ __forceinline__ void issue(unsigned char* stage, int64_t k0, int64_t K) {
-    const int wid = threadIdx.x >> 6;
+  // Load q of a stage (q < QL: L rows, else R rows) at LDS byte address `stage`.  `full`
+  // (wave-uniform): the stage lies wholly inside K, so no lane needs the k bound.
+  __device__ __forceinline__ void one(unsigned stage, int64_t k0, int64_t K, bool full, int q) {
     const unsigned kb = static_cast<unsigned>(k0 * 2);
-#pragma unroll
-    for (int q = 0; q < D::QL; ++q) {
-      const bool kin = k0 + kl[q] < K;
-      const unsigned off = (kin && offl[q] != DMA_OOB) ? offl[q] + kb : DMA_OOB;
-      dma16(rl, off, stage + (wid + D::NW * q) * D::RPL * D::ROW_BYTES);
+    if (q < D::QL) {
+      unsigned off = offl[q] + kb;
+      if (!full && k0 + kl[q] >= K) off = DMA_OOB;
+      dma16_at(rl, off, stage + wl + q * D::NW * D::RPL * D::ROW_BYTES);
+    } else {
+      const int u = q - D::QL;
+      unsigned off = offr[u] + kb;
+      if (!full && k0 + kr[u] >= K) off = DMA_OOB;
+      dma16_at(rr, off, stage + (C::BM + D::NW * D::RPL * u) * D::ROW_BYTES + wl);
     }
+  }
+  __device__ __forceinline__ void issue(unsigned stage, int64_t k0, int64_t K) {
+    const bool full = k0 + D::KB <= K;
 #pragma unroll
-    for (int q = 0; q < D::QR; ++q) {
-      const bool kin = k0 + kr[q] < K;
-      const unsigned off = (kin && offr[q] != DMA_OOB) ? offr[q] + kb : DMA_OOB;
-      dma16(rr, off, stage + (C::BM + D::RPL * (wid + D::NW * q)) * D::ROW_BYTES);
-    }
+    for (int q = 0; q < D::QL + D::QR; ++q) one(stage, k0, K, full, q);
   }
 };
 
@@ -441,6 +464,7 @@ __device__ __forceinline__ void dma_compute(const unsigned char* stage,
 // so the compiler does not track it and one array costs no extra waits).
 struct DmaLds {
   unsigned char* base;
+  unsigned addr;  // LDS byte address of base
 };
 
 // Waits until at most `pending` (<= MAXP) stages of loads are still in flight.
@@ -473,14 +497,15 @@ __device__ __forceinline__ void mainloop_dma(const Operand& L, const Operand& R,
   st.init(L, R, mt, nt);
   const int nk = static_cast<int>((K + D::KB - 1) / D::KB);
   auto slot = [&](int k) { return l.base + (k % D::STAGES) * D::STAGE_BYTES; };
+  auto slot_at = [&](int k) { return l.addr + (k % D::STAGES) * D::STAGE_BYTES; };
 #pragma unroll
   for (int s = 0; s < AHEAD; ++s)
-    if (s < nk) st.issue(slot(s), static_cast<int64_t>(s) * D::KB, K);
+    if (s < nk) st.issue(slot_at(s), static_cast<int64_t>(s) * D::KB, K);
   int kt = 0;
   for (; kt + AHEAD < nk; ++kt) {
     wait_vmcnt<(AHEAD - 1) * NQ>();  // stage kt has landed
     raw_barrier();
-    st.issue(slot(kt + AHEAD), static_cast<int64_t>(kt + AHEAD) * D::KB, K);
+    st.issue(slot_at(kt + AHEAD), static_cast<int64_t>(kt + AHEAD) * D::KB, K);
     dma_compute<C, D>(slot(kt), acc);
   }
   // Tail: no more loads; the stages still in flight drain one by one.
@@ -793,7 +818,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
   constexpr int SB = D::STAGE_BYTES;
   static_assert(D::STAGES * SB <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) unsigned char s0[D::STAGES * SB];
-  const DmaLds l{s0};
+  const DmaLds l{s0, lds_addr(s0)};
   int64_t mt, nt;
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
   f32x16_t acc[C::MI][C::NI];
@@ -846,7 +871,7 @@ __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
   constexpr int SB = D::STAGE_BYTES;
   static_assert(D::STAGES * SB <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) unsigned char s0[D::STAGES * SB];
-  const DmaLds l{s0};
+  const DmaLds l{s0, lds_addr(s0)};
   int64_t mt, nt;
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
   f32x16_t acc[C::MI][C::NI];

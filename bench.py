@@ -594,7 +594,10 @@ def kernels_leg(dev, reps: int = 10):
 # bench op name -> kernel-leg entry at the same shape (profiles/traffic.json, from the
 # FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --mode kernels`)
 TRAFFIC_KEYS = {"linear_valgrad[768x3072]": "valgrad_fc",
-                "linear_valgrad+bias[768x3072]": "valgrad_bias_fc", "bias_dot": "bias_fc",
+                "linear_valgrad+bias[768x3072]": "valgrad_bias_fc",
+                "linear_valgrad+bias[3072x768]": "valgrad_bias_fc_out",
+                "linear_valgrad+bias[768x2304]": "valgrad_bias_qkv",
+                "linear_valgrad+bias[768x768]": "valgrad_bias_proj", "bias_dot": "bias_fc",
                 "layernorm_dot": "layernorm", "embedding_dot": "embedding_wte",
                 "kron_proj": "kron_fc", "kron_embed_proj": "kron_embed_wte",
                 "ghost": "ghost_microbench"}

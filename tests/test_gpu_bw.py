@@ -25,6 +25,20 @@ def test_embedding_dot(gpu, dtype, shape):
         assert_close(dot.cpu(), want, tol, "embedding dot")
 
 
+@pytest.mark.parametrize("shape", [(20, 4, 1024, 64, 50257), (5, 2, 4096, 24, 1000),
+                                   (6, 3, 1500, 40, 2)])
+def test_embedding_dot_sort_sizes(gpu, shape):
+    """The sorted-segment path at full size: 4096 val keys (the GPT-2 wte batch), the 8192-key
+    maximum with runs of ~8 equal ids, and 4500 keys in two long runs."""
+    N, n_val, T, d, vocab = shape
+    ids = torch.randint(0, vocab, (N, T), generator=gen(41 + T))
+    G = randn((N, T, d), 42 + T, 1e-3, torch.bfloat16)
+    print(f"embedding sort shape={shape}", flush=True)
+    dot = _native.ops().embedding_dot(ids.to(gpu), G.to(gpu), n_val, vocab)
+    torch.cuda.synchronize()
+    assert_close(dot.cpu(), R.embedding_dot_exact(ids, G, n_val), BF16_TOL, "embedding dot")
+
+
 @pytest.mark.parametrize("shape", [(6, 3, 3000, 16, 100), (5, 2, 40, 24, 600_000)])
 def test_embedding_dot_fixed_point_path(gpu, shape):
     """More than 8192 val tokens, or ids of 2^19 and above: the fixed-point segment path."""

@@ -89,6 +89,37 @@ def test_ghost_reference_rounding_matches_reference_sequence(gpu, shape):
     assert_close(dot.cpu(), want, 2e-3, "ref-rounding")
 
 
+@pytest.mark.parametrize("shape,pair", [((32, 8, 1024, 64, 96), False),   # per-tile partials
+                                        ((20, 5, 600, 40, 72), False),    # per-token, K tails
+                                        ((40, 10, 512, 32, 48), True)])   # per val row
+def test_ghost_many_tiles(gpu, shape, pair):
+    """Grids of 400-3000 tiles (several waves of workgroups per CU, both partial layouts, K
+    tails, per-val-row tiles): bf16 dots (and per-pair values) against the float64 closed
+    form."""
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 500 + T, torch.bfloat16)
+    print(f"ghost many tiles shape={shape} pair={pair}", flush=True)
+    dot, prs = _native.ops().linear_dot(A.to(gpu), G.to(gpu), n_val, algo=_native.ALGO_GHOST,
+                                        want_pair=pair)
+    torch.cuda.synchronize()
+    Af, Gf = A.float(), G.float()
+    assert_close(dot.cpu(), R.linear_dot_exact(Af, Gf, n_val, "pairwise"), BF16_TOL, "dot")
+    if pair:
+        assert_close(prs.cpu(), R.linear_dot_exact(Af, Gf, n_val, "pairwise", pair=True),
+                     BF16_TOL, "pair")
+
+
+def test_ghost_many_tiles_reference_rounding(gpu):
+    N, n_val, T, d_in, d_out = 20, 5, 600, 40, 72
+    A, G = _inputs(N, T, d_in, d_out, 77, torch.float32)
+    dot, _ = _native.ops().linear_dot(A.to(gpu).bfloat16(), G.to(gpu).bfloat16(), n_val,
+                                      algo=_native.ALGO_GHOST,
+                                      rounding=_native.ROUND_REF_BF16)
+    torch.cuda.synchronize()
+    want, _ = R.linear_dot_ref(A, G, n_val, use_ghost=True, has_bias=False)
+    assert_close(dot.cpu(), want, 2e-3, "ref-rounding")
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_linear_rowdot_with_given_v(gpu, shape, dtype):

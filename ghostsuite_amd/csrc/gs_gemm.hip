@@ -20,6 +20,7 @@
 // k-slice selected by l / 32; result element e of lane l is C[8*(e/4) + 4*(l/32) + e%4][l%32].
 
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "gs_common.h"
@@ -1613,8 +1614,9 @@ bool tn_ok(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, in
 }
 
 // Splits of the k-rows: enough workgroups to cover the CUs against the fp32 partials'
-// extra write + read (estimated at 1.5 TF/s per CU, the rate measured for the 128 x 128 tile
-// at the GPT-2 shapes, and 4 TB/s).
+// extra write + read.  Estimate: whole waves of 256 workgroups, each workgroup's share of the
+// flops at 1.5 TF/s (the rate measured for the 128 x 128 tile at the GPT-2 shapes), plus the
+// partials at 4 TB/s.
 int64_t tn_kper(int64_t K, int sp) {
   return ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
          TnD::KB;
@@ -1626,7 +1628,8 @@ int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
   int best = 1;
   double best_t = 1e30;
   for (int sp = 1; sp <= 8 && sp <= std::max<int64_t>(1, ksteps / 4); ++sp) {
-    const double t = 2.0 * M * N * K / (std::min(tiles * sp, 256.0) * 1.5e12) +
+    const double waves = std::ceil(tiles * sp / 256.0);
+    const double t = waves * 2.0 * M * N * K / (tiles * sp * 1.5e12) +
                      (sp > 1 ? 8.0 * sp * M * N / 4e12 + 3e-6 : 0.0);
     if (t < best_t) {
       best_t = t;

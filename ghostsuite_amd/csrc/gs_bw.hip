@@ -508,7 +508,11 @@ __global__ void emb_dot_kernel(const int64_t* __restrict__ ids, const E* __restr
 // rows are summed in index order (fp32, no atomics, nothing to zero-fill), and each train
 // token dots its row with its id's run sum.
 constexpr int EMB_SORT_MAX = 8192, EMB_QBITS = 13;
-constexpr uint32_t EMB_NOKEY = 0xFFFFFFFFu;
+// A val token whose id is out of range gets the key EMB_NOKEY | index: above every valid key
+// (ids below 2^19 - 1), distinct, and in index order, so every key has its own rank.
+// EMB_PAD (above all of them) pads the key array.
+constexpr uint32_t EMB_NOKEY = 0xFFFFE000u, EMB_PAD = 0xFFFFFFFFu;
+__device__ __forceinline__ bool emb_nokey(uint32_t k) { return k >= EMB_NOKEY; }
 
 __device__ __forceinline__ uint32_t emb_key(const int64_t* __restrict__ ids, const RowMap& val,
                                             int64_t vocab, int i) {
@@ -517,7 +521,7 @@ __device__ __forceinline__ uint32_t emb_key(const int64_t* __restrict__ ids, con
   const int64_t id = ids[val.phys_row(seg, static_cast<uint32_t>(i) - seg * len)];
   return (id >= 0 && id < vocab) ? (static_cast<uint32_t>(id) << EMB_QBITS) |
                                        static_cast<uint32_t>(i)
-                                 : EMB_NOKEY;
+                                 : EMB_NOKEY | static_cast<uint32_t>(i);
 }
 
 // keys[rank(i)] = key(i); val tokens whose id is out of range go last, in index order.  A
@@ -532,7 +536,7 @@ __global__ void __launch_bounds__(BW_THREADS) emb_key_kernel(
   const int64_t x0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   for (int64_t x = x0; x < vocab; x += gstride) table[x] = -1;
   for (int64_t j = x0; j < n4; j += gstride)
-    ukeys[j] = j < n ? emb_key(ids, val, vocab, static_cast<int>(j)) : EMB_NOKEY;
+    ukeys[j] = j < n ? emb_key(ids, val, vocab, static_cast<int>(j)) : EMB_PAD;
 }
 
 constexpr int EMB_RK = 16, EMB_RP = BW_THREADS / EMB_RK;
@@ -540,56 +544,46 @@ __global__ void __launch_bounds__(BW_THREADS) emb_rank_kernel(const uint32_t* __
                                                               int n,
                                                               uint32_t* __restrict__ keys) {
   __shared__ __attribute__((aligned(16))) uint32_t sk[EMB_SORT_MAX];
-  __shared__ int cnt[3][EMB_RP][EMB_RK];
+  __shared__ int cnt[EMB_RP][EMB_RK];
   const int n4 = (n + 3) / 4 * 4;
   for (int j = threadIdx.x * 4; j < n4; j += blockDim.x * 4)
     *reinterpret_cast<uint4*>(sk + j) = *reinterpret_cast<const uint4*>(ukeys + j);
   __syncthreads();
   const int kk = threadIdx.x % EMB_RK, part = threadIdx.x / EMB_RK;
   const int i = blockIdx.x * EMB_RK + kk;
-  const uint32_t k = i < n ? sk[i] : EMB_NOKEY;
+  const uint32_t k = i < n ? sk[i] : EMB_PAD;
   const int span = (n4 / 4 + EMB_RP - 1) / EMB_RP * 4;  // keys per slice, a multiple of 4
   const int j0 = part * span, j1 = j0 + span < n4 ? j0 + span : n4;
-  int lt = 0, inv_before = 0, n_valid = 0;
+  int lt = 0;  // keys are distinct, so the rank is the number of smaller keys
   for (int j = j0; j < j1; j += 4) {
     const uint4 w = *reinterpret_cast<const uint4*>(sk + j);
-    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      lt += v[e] < k;
-      n_valid += (j + e < n) & (v[e] != EMB_NOKEY);
-      inv_before += (j + e < i) & (v[e] == EMB_NOKEY);
-    }
+    lt += (w.x < k) + (w.y < k) + (w.z < k) + (w.w < k);
   }
-  cnt[0][part][kk] = lt;
-  cnt[1][part][kk] = inv_before;
-  cnt[2][part][kk] = n_valid;
+  cnt[part][kk] = lt;
   __syncthreads();
   if (part == 0 && i < n) {
-    int a = 0, b = 0, c = 0;
-    for (int q = 0; q < EMB_RP; ++q) {
-      a += cnt[0][q][kk];
-      b += cnt[1][q][kk];
-      c += cnt[2][q][kk];
-    }
-    keys[k != EMB_NOKEY ? a : c + b] = k;
+    int a = 0;
+    for (int q = 0; q < EMB_RP; ++q) a += cnt[q][kk];
+    keys[a] = k;
   }
 }
 
-// S[p][:] = sum of the val rows of the run starting at sorted position p (index order), and
-// table[id] = p for that run.
+// S[p][:] = sum of the val rows of the run starting at sorted position p (index order) when the
+// run has two or more tokens, and table[id] = p for every run.
 template <class E>
 __global__ void __launch_bounds__(BW_THREADS) emb_segsum_kernel(
     const E* __restrict__ G, RowMap val, int64_t d, const uint32_t* __restrict__ keys,
     int32_t* __restrict__ table, float* __restrict__ S) {
   constexpr int VE = Vec<E>::VE;
   const int64_t p = blockIdx.x, n_vt = val.total();
-  const uint32_t kprev = p > 0 ? keys[p - 1] : EMB_NOKEY;
+  const uint32_t kprev = p > 0 ? keys[p - 1] : EMB_PAD;
   const uint32_t k0 = keys[p];
-  const uint32_t knext = p + 1 < n_vt ? keys[p + 1] : EMB_NOKEY;
-  if (k0 == EMB_NOKEY || (p > 0 && (kprev >> EMB_QBITS) == (k0 >> EMB_QBITS))) return;
+  const uint32_t knext = p + 1 < n_vt ? keys[p + 1] : EMB_PAD;
+  if (emb_nokey(k0) || (p > 0 && (kprev >> EMB_QBITS) == (k0 >> EMB_QBITS))) return;
   const uint32_t id = k0 >> EMB_QBITS;
   if (threadIdx.x == 0) table[id] = static_cast<int32_t>(p);
+  // A one-token run needs no sum: the train tokens read that val row itself.
+  if (emb_nokey(knext) || (knext >> EMB_QBITS) != id) return;
   const int vec = (d * static_cast<int64_t>(sizeof(E))) % 16 == 0 &&
                   (reinterpret_cast<uintptr_t>(G) % 16 == 0);
   for (int64_t f = static_cast<int64_t>(threadIdx.x) * VE; f < d;
@@ -599,7 +593,7 @@ __global__ void __launch_bounds__(BW_THREADS) emb_segsum_kernel(
     for (int e = 0; e < VE; ++e) a[e] = 0.f;
     for (int64_t r = p; r < n_vt; ++r) {
       const uint32_t k = r == p ? k0 : r == p + 1 ? knext : keys[r];
-      if (k == EMB_NOKEY || (k >> EMB_QBITS) != id) break;
+      if (emb_nokey(k) || (k >> EMB_QBITS) != id) break;
       const int64_t q = k & ((1u << EMB_QBITS) - 1);
       const int64_t seg = q / val.seglen;
       Vec<E> x;
@@ -613,30 +607,42 @@ __global__ void __launch_bounds__(BW_THREADS) emb_segsum_kernel(
   }
 }
 
-// part[i * chunks + c] = sum over train row i's tokens in chunk c of <g_it, S[table[x_it]]>:
-// the chunk's run positions are looked up first (one token per thread), then one token per
-// wave at a time with lanes over 16-byte feature chunks; fixed-order block sum.
+// part[i * chunks + c] = sum over train row i's tokens in chunk c of <g_it, run sum of x_it>:
+// the chunk's runs are looked up first (one token per thread): a run of two or more tokens is
+// read from S, a one-token run straight from that val token's row of G.  Then one token per
+// half-wave at a time with lanes over 16-byte feature chunks; fixed-order block sum.
 template <class E>
 __global__ void __launch_bounds__(BW_THREADS) emb_segdot_kernel(
-    const int64_t* __restrict__ ids, const E* __restrict__ G, RowMap train, int64_t d,
-    int64_t vocab, const int32_t* __restrict__ table, const float* __restrict__ S,
-    int64_t chunks, float* __restrict__ part) {
+    const int64_t* __restrict__ ids, const E* __restrict__ G, RowMap train, RowMap val, int64_t d,
+    int64_t vocab, const uint32_t* __restrict__ keys, const int32_t* __restrict__ table,
+    const float* __restrict__ S, int64_t chunks, float* __restrict__ part) {
   constexpr int VE = Vec<E>::VE;
   static_assert(TOK_CHUNK <= BW_THREADS, "one lookup per thread");
   __shared__ float red[BW_THREADS / 64];
-  __shared__ int32_t rs[TOK_CHUNK];
+  __shared__ int64_t src[TOK_CHUNK];  // >= 0: row of S; < 0: -1 - (row of G); INT64_MIN: none
   const int64_t i = blockIdx.y, c = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int64_t T = train.seglen;
+  const int64_t T = train.seglen, n_vt = val.total();
   const int64_t t0 = c * TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + TOK_CHUNK);
   if (threadIdx.x < TOK_CHUNK) {
-    int32_t r = -1;
+    int64_t sr = INT64_MIN;
     const int64_t t = t0 + threadIdx.x;
     if (t < t1) {
       const int64_t id = ids[train.phys_row(i, t)];
-      if (id >= 0 && id < vocab) r = table[id];
+      const int32_t r = (id >= 0 && id < vocab) ? table[id] : -1;
+      if (r >= 0) {
+        const uint32_t k = keys[r];
+        const uint32_t kn = r + 1 < n_vt ? keys[r + 1] : EMB_PAD;
+        if (!emb_nokey(kn) && (kn >> EMB_QBITS) == (k >> EMB_QBITS)) {
+          sr = r;
+        } else {
+          const int64_t q = k & ((1u << EMB_QBITS) - 1);
+          const int64_t seg = q / val.seglen;
+          sr = -1 - val.phys_row(seg, q - seg * val.seglen);
+        }
+      }
     }
-    rs[threadIdx.x] = r;
+    src[threadIdx.x] = sr;
   }
   __syncthreads();
   const int vec = (d * static_cast<int64_t>(sizeof(E))) % 16 == 0 &&
@@ -645,25 +651,38 @@ __global__ void __launch_bounds__(BW_THREADS) emb_segdot_kernel(
   const int half = lane >> 5, hl = lane & 31;  // two tokens per wave, 32 lanes each
   for (int64_t tb = t0 + 2 * wid; tb < t1; tb += 2 * (BW_THREADS / 64)) {
     const int64_t t = tb + half;
-    const int32_t r = t < t1 ? rs[t - t0] : -1;
-    if (r < 0) continue;
+    const int64_t sr = t < t1 ? src[t - t0] : INT64_MIN;
+    if (sr == INT64_MIN) continue;
     const E* gr = G + train.phys_row(i, t) * d;
-    const float* sr = S + static_cast<int64_t>(r) * d;
+    if (sr >= 0) {
+      const float* srow = S + sr * d;
 #pragma unroll 4
-    for (int64_t f = static_cast<int64_t>(hl) * VE; f < d; f += 32 * VE) {
-      Vec<E> x;
-      const bool full = vec && f + VE <= d;
-      x.load(gr + f, full, d - f);
-      if (full) {
+      for (int64_t f = static_cast<int64_t>(hl) * VE; f < d; f += 32 * VE) {
+        Vec<E> x;
+        const bool full = vec && f + VE <= d;
+        x.load(gr + f, full, d - f);
+        if (full) {
 #pragma unroll
-        for (int e = 0; e < VE; e += 4) {
-          const float4 w = *reinterpret_cast<const float4*>(sr + f + e);
-          s += x.v[e] * w.x + x.v[e + 1] * w.y + x.v[e + 2] * w.z + x.v[e + 3] * w.w;
+          for (int e = 0; e < VE; e += 4) {
+            const float4 w = *reinterpret_cast<const float4*>(srow + f + e);
+            s += x.v[e] * w.x + x.v[e + 1] * w.y + x.v[e + 2] * w.z + x.v[e + 3] * w.w;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VE; ++e)
+            if (f + e < d) s += x.v[e] * srow[f + e];
         }
-      } else {
+      }
+    } else {
+      const E* vrow = G + (-1 - sr) * d;
+#pragma unroll 4
+      for (int64_t f = static_cast<int64_t>(hl) * VE; f < d; f += 32 * VE) {
+        Vec<E> x, y;
+        const bool full = vec && f + VE <= d;
+        x.load(gr + f, full, d - f);
+        y.load(vrow + f, full, d - f);
 #pragma unroll
-        for (int e = 0; e < VE; ++e)
-          if (f + e < d) s += x.v[e] * sr[f + e];
+        for (int e = 0; e < VE; ++e) s += x.v[e] * y.v[e];
       }
     }
   }
@@ -893,7 +912,7 @@ namespace {
 // The sorted-segment path when the val tokens fit one sorting workgroup, else the
 // fixed-point path.
 bool emb_sorted(int64_t n_val, int64_t T, int64_t vocab) {
-  // (id << EMB_QBITS | index) must stay below the no-key value.
+  // (id << EMB_QBITS | index) must stay below the no-keys: ids below 2^19 - 1.
   return n_val * T <= EMB_SORT_MAX && vocab < (int64_t{1} << (32 - EMB_QBITS));
 }
 template <class S>
@@ -957,14 +976,14 @@ extern "C" int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, in
       const uint16_t* g = static_cast<const uint16_t*>(G);
       hipLaunchKernelGGL(emb_segsum_kernel<uint16_t>, gv, dim3(128), 0, s, g, va, d, keys,
                          table, S);
-      hipLaunchKernelGGL(emb_segdot_kernel<uint16_t>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, d,
-                         vocab, table, S, chunks, part);
+      hipLaunchKernelGGL(emb_segdot_kernel<uint16_t>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, va,
+                         d, vocab, keys, table, S, chunks, part);
     } else {
       const float* g = static_cast<const float*>(G);
       hipLaunchKernelGGL(emb_segsum_kernel<float>, gv, dim3(128), 0, s, g, va, d, keys, table,
                          S);
-      hipLaunchKernelGGL(emb_segdot_kernel<float>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, d,
-                         vocab, table, S, chunks, part);
+      hipLaunchKernelGGL(emb_segdot_kernel<float>, gt, dim3(BW_THREADS), 0, s, ids, g, tr, va,
+                         d, vocab, keys, table, S, chunks, part);
     }
     hipLaunchKernelGGL(sum_chunks_kernel, dim3(static_cast<unsigned>(n_t)), dim3(BW_THREADS), 0,
                        s, part, chunks, out_dot);

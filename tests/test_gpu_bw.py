@@ -39,6 +39,25 @@ def test_embedding_dot_sort_sizes(gpu, shape):
     assert_close(dot.cpu(), R.embedding_dot_exact(ids, G, n_val), BF16_TOL, "embedding dot")
 
 
+@pytest.mark.parametrize("shape", [(8, 2, 300, 24, 50), (20, 4, 1024, 16, 50257)])
+def test_embedding_dot_out_of_range_ids(gpu, shape):
+    """Ids outside [0, vocab) (negative or too large) take no part, as val or train tokens:
+    the dot equals the closed form with those tokens' gradient rows zeroed."""
+    N, n_val, T, d, vocab = shape
+    ids = torch.randint(0, vocab, (N, T), generator=gen(51 + T))
+    bad = torch.rand(N, T, generator=gen(52 + T)) < 0.1
+    ids[bad] = torch.where(torch.rand(N, T, generator=gen(53 + T)) < 0.5,
+                           torch.full((N, T), -3), torch.full((N, T), vocab + 7))[bad]
+    G = randn((N, T, d), 54 + T, 1e-3, torch.bfloat16)
+    print(f"embedding out-of-range ids shape={shape}", flush=True)
+    dot = _native.ops().embedding_dot(ids.to(gpu), G.to(gpu), n_val, vocab)
+    torch.cuda.synchronize()
+    Gz = G.clone()
+    Gz[bad] = 0
+    assert_close(dot.cpu(), R.embedding_dot_exact(ids.clamp(0, vocab - 1), Gz, n_val), BF16_TOL,
+                 "embedding dot")
+
+
 @pytest.mark.parametrize("shape", [(6, 3, 3000, 16, 100), (5, 2, 40, 24, 600_000)])
 def test_embedding_dot_fixed_point_path(gpu, shape):
     """More than 8192 val tokens, or ids of 2^19 and above: the fixed-point segment path."""

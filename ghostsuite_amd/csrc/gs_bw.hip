@@ -539,7 +539,10 @@ __global__ void __launch_bounds__(BW_THREADS) emb_key_kernel(
     ukeys[j] = j < n ? emb_key(ids, val, vocab, static_cast<int>(j)) : EMB_PAD;
 }
 
-constexpr int EMB_RK = 16, EMB_RP = BW_THREADS / EMB_RK;
+#ifndef GS_EMB_RK
+#define GS_EMB_RK 4
+#endif
+constexpr int EMB_RK = GS_EMB_RK, EMB_RP = BW_THREADS / EMB_RK;
 __global__ void __launch_bounds__(BW_THREADS) emb_rank_kernel(const uint32_t* __restrict__ ukeys,
                                                               int n,
                                                               uint32_t* __restrict__ keys) {

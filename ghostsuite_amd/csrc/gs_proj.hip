@@ -2,8 +2,8 @@
 //
 //   out[b] = scale * sum_t (L g_bt)(R a_bt)^T        L: [kL, n_g], R: [kR, n_a]
 //
-// One workgroup takes one sample and a chunk of 64 tokens; its 4 waves take interleaved
-// 64-feature pieces of all 64 token rows (so the workgroup reads 256 contiguous features of
+// One workgroup takes one sample and a chunk of 64 tokens; its 8 waves take interleaved
+// 32-feature pieces of all 64 token rows (so the workgroup reads 256 contiguous features of
 // every row at a time).  A wave streams its pieces of the G and A rows straight from HBM
 // into MFMA operands (v_mfma_f32_16x16x32_bf16 / v_mfma_f32_16x16x4f32) against the
 // projection rows (small, L2-resident), each projection fragment serving the 4 sixteen-row
@@ -26,8 +26,14 @@ namespace gs {
 typedef __bf16 bf16x8p_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int PJ_TOK = 64;      // tokens per workgroup
-constexpr int PJ_THREADS = 256;
+#ifndef GS_PJ_TOK
+#define GS_PJ_TOK 64
+#endif
+#ifndef GS_PJ_THREADS
+#define GS_PJ_THREADS 512
+#endif
+constexpr int PJ_TOK = GS_PJ_TOK;  // tokens per workgroup
+constexpr int PJ_THREADS = GS_PJ_THREADS;
 constexpr int PJ_KMAX = 32;     // projection rows supported per side
 
 struct PjBF16 {
@@ -71,7 +77,7 @@ __device__ __forceinline__ uint4 lane_load(const typename Tr::E* row, int64_t k,
 }
 
 #ifndef GS_PJ_U
-#define GS_PJ_U 2
+#define GS_PJ_U 1
 #endif
 constexpr int PJ_WAVES = PJ_THREADS / 64;
 constexpr int PJ_TG = PJ_TOK / 16;  // 16-token MFMA row groups per workgroup

@@ -647,26 +647,36 @@ __device__ __forceinline__ void rowdot_colsum(const GemmParams& p, f32x16_t (&ac
 // aligned Z rows and Z below 4 GiB; `lds` holds at least BN * BM * 2 bytes.
 template <class C>
 struct ZTile {
-  static constexpr int CPR = C::BM / 8;        // 16-byte chunks per Z row
-  static constexpr int RPI = 64 / CPR;         // rows per wave-level DMA
+  static constexpr int CPR = C::BM / 8;              // 16-byte chunks per Z row
   static constexpr int NW = C::WM * C::WN;
-  static constexpr int NQ = C::BN / RPI / NW;  // DMAs per wave
-  static_assert(64 % CPR == 0 && (C::BN / RPI) % NW == 0, "Z tile split");
-  static_assert((CPR & (CPR - 1)) == 0, "chunks per row must be a power of two");
+  static constexpr int NQ = C::BN * CPR / (64 * NW);  // wave-level DMAs per wave
+  static_assert((C::BN * CPR) % (64 * NW) == 0, "Z tile split");
+  static_assert(CPR % 8 == 0, "Z rows of whole 128-byte groups");
+  // LDS slot of chunk c of tile row r (and, the map being an involution, the chunk held by
+  // slot c): XOR-swizzled over all CPR chunks when CPR is a power of two, else within groups
+  // of 8, so that one chunk of 32 consecutive rows spreads over the LDS banks.
+  __device__ static constexpr int slot(int c, int r) {
+    if constexpr ((CPR & (CPR - 1)) == 0)
+      return c ^ (r & (CPR - 1));
+    else
+      return (c & ~7) | ((c & 7) ^ (r & 7));
+  }
 };
 
-// Issues the Z-tile DMAs (16 contiguous bytes per lane, RPI rows per wave-level DMA).
+// Issues the Z-tile DMAs: wave-level DMA j fills LDS bytes [1024 j, 1024 j + 1024), i.e. the
+// 64 linear chunk slots 64 j + lane of the row-major [BN][CPR] tile; each lane fetches the
+// chunk its slot holds.
 template <class C>
 __device__ __forceinline__ void rowdot_issue_z(const GemmParams& p, int64_t mt, int64_t nt,
                                                unsigned char* lds) {
   using Z = ZTile<C>;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(p.Z, p.z_nbytes);
-  const int sub = lane / Z::CPR, sl = lane % Z::CPR;
 #pragma unroll
   for (int q = 0; q < Z::NQ; ++q) {
-    const int r = Z::RPI * (wid + Z::NW * q) + sub;  // local row (train token) of the chunk
-    const int c = sl ^ (r & (Z::CPR - 1));
+    const int li = (wid + Z::NW * q) * 64 + lane;
+    const int r = li / Z::CPR;                 // local row (train token) of the slot
+    const int c = Z::slot(li % Z::CPR, r);     // chunk of that row the slot holds
     const int64_t f = nt * C::BN + r;
     unsigned off = DMA_OOB;
     if (f < p.z_map.total()) {
@@ -674,7 +684,7 @@ __device__ __forceinline__ void rowdot_issue_z(const GemmParams& p, int64_t mt, 
       const int64_t row = p.z_map.phys_row(seg, f - seg * p.z_map.seglen);
       off = static_cast<unsigned>((row * p.z_ld + mt * C::BM + c * 8) * 2);
     }
-    dma16(rz, off, lds + Z::RPI * (wid + Z::NW * q) * Z::CPR * 16);
+    dma16(rz, off, lds + (wid + Z::NW * q) * 1024);
   }
 }
 
@@ -684,7 +694,6 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
                                                   int64_t nt, unsigned char* lds,
                                                   float (&colsum)[C::NI], float* bsum) {
   constexpr int CPR = ZTile<C>::CPR;
-  constexpr int NW = ZTile<C>::NW;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
   // The tile's slice of the val bias gradient, loaded while the Z tile comes in.
@@ -706,33 +715,33 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
       for (int g = 0; g < 4; ++g) {
         const int c = wm * 4 * C::MI + mi * 4 + g;
         union { uint2 v; uint16_t e[4]; } z;
-        z.v = *reinterpret_cast<const uint2*>(zrow + ((c ^ (nl & (CPR - 1))) * 16));
+        z.v = *reinterpret_cast<const uint2*>(zrow + ZTile<C>::slot(c, nl) * 16);
 #pragma unroll
         for (int v = 0; v < 4; ++v) s += acc[mi][ni][4 * g + v] * bf16_to_f32(z.e[v]);
       }
     colsum[ni] = s;
   }
   if (p.BP != nullptr) {
-    // Column sums of the tile over its BN token rows: LPR = BM / 4 lanes cover a row (one
-    // ds_read_b64 of 4 columns each), so a wave reads RPW rows at a time and the NW * RPW
-    // lane groups take every (NW * RPW)-th row; the group sums combine in a fixed order
-    // through `bsum` [NW * RPW][BM].
-    constexpr int LPR = C::BM / 4, RPW = 64 / LPR, GRP = NW * RPW;
-    static_assert(LPR <= 64 && 64 % LPR == 0 && C::BN % GRP == 0, "tile column-sum split");
-    const int q = lane % LPR, grp = wid * RPW + lane / LPR;
+    // Column sums of the tile over its BN token rows: thread t < GRP * CG takes column group
+    // q = t % CG (4 columns, one ds_read_b64) of every GRP-th row starting at t / CG; the
+    // group sums combine in a fixed order through `bsum` [GRP][BM].
+    constexpr int CG = C::BM / 4, GRP = C::NT / CG;
+    const int q = threadIdx.x % CG, grp = threadIdx.x / CG;
     const int ch = q >> 1, hb = (q & 1) * 8;
-    float4 cs = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (grp < GRP) {
+      float4 cs = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 8
-    for (int r = grp; r < C::BN; r += GRP) {
-      union { uint2 v; uint16_t e[4]; } z;
-      z.v = *reinterpret_cast<const uint2*>(lds + r * CPR * 16 + ((ch ^ (r & (CPR - 1))) * 16) +
-                                            hb);
-      cs.x += bf16_to_f32(z.e[0]);
-      cs.y += bf16_to_f32(z.e[1]);
-      cs.z += bf16_to_f32(z.e[2]);
-      cs.w += bf16_to_f32(z.e[3]);
+      for (int r = grp; r < C::BN; r += GRP) {
+        union { uint2 v; uint16_t e[4]; } z;
+        z.v = *reinterpret_cast<const uint2*>(lds + r * CPR * 16 + ZTile<C>::slot(ch, r) * 16 +
+                                              hb);
+        cs.x += bf16_to_f32(z.e[0]);
+        cs.y += bf16_to_f32(z.e[1]);
+        cs.z += bf16_to_f32(z.e[2]);
+        cs.w += bf16_to_f32(z.e[3]);
+      }
+      reinterpret_cast<float4*>(bsum)[grp * CG + q] = cs;
     }
-    reinterpret_cast<float4*>(bsum)[grp * LPR + q] = cs;
     __syncthreads();
     static_assert(C::BM <= C::NT, "one thread per tile column");
     float qb = 0.f;
@@ -1588,6 +1597,31 @@ struct LinearPlan {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Row-dot tile height (d_out rows per tile; 256 tokens wide either way): 256, or 192 where it
+// divides d_out and fills whole waves of 256 workgroups better (fc_out / proj with d_out 768:
+// 256 tiles instead of 192; qkv with 2304: 768 instead of 576).  `full`: every tile must be
+// whole along d_out (the fused bias pass), so 256 only when it divides d_out.
+#ifndef GS_ROWDOT192
+#define GS_ROWDOT192 1
+#endif
+using RowdotCfg192 = Cfg<TrBF16, 2, 4, 3, 2>;
+template <class Tr>
+int64_t rowdot_bm(int64_t d_out, int64_t n_tiles, bool full) {
+  constexpr int64_t B = RowdotCfg<Tr>::BM, B2 = RowdotCfg192::BM;
+  if constexpr (!std::is_same<Tr, TrBF16>::value) {
+    return B;
+  } else {
+    const bool ok2 = GS_ROWDOT192 && d_out % B2 == 0;
+    if (!ok2) return B;
+    if (full && d_out % B != 0) return B2;
+    auto fill = [&](int64_t bm) {
+      const double t = static_cast<double>(ceil_div(d_out, bm) * n_tiles);
+      return t / (std::ceil(t / 256.0) * 256.0);
+    };
+    return fill(B2) > fill(B) + 1e-9 ? B2 : B;
+  }
+}
+
 // The K-major val-term GEMM (tn_gemm_kernel): tile shape, stage geometry and split count
 // (GS_TN_SPLIT 0 = chosen by the estimate in tn_splits).
 #ifndef GS_TN_TILE
@@ -1692,8 +1726,9 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
 template <class Tr>
 LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
                        int semantics, int algo, int want_pair) {
-  constexpr int64_t GBM = GhostCfg<Tr>::BM, RBM = RowdotCfg<Tr>::BM;
+  constexpr int64_t GBM = GhostCfg<Tr>::BM;
   const int64_t n_t = N - n_val;
+  const int64_t RBM = rowdot_bm<Tr>(d_out, ceil_div(n_t * T, RowdotCfg<Tr>::BN), false);
   const int64_t nv_eff = semantics == GS_SEM_PRESUM ? 1 : n_val;  // val rows after presum
   LinearPlan pl{};
   // MFMA flops including tile padding.
@@ -1771,11 +1806,10 @@ bool linear_args_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in
 
 // ROWDOT over the train tokens: P rows [p_row0, p_row0 + m tiles) get the per-tile (or
 // per-token) partials of sum_m (V a_t)[m] g_t[m].
-template <class Tr>
-int launch_rowdot(const void* A, const void* G, const void* V, int64_t N, int64_t n_val,
-                  int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, float* P,
-                  int64_t p_ld, int tile_reduce, int64_t p_row0, hipStream_t s) {
-  using RC = RowdotCfg<Tr>;
+template <class Tr, class RC>
+int launch_rowdot_cfg(const void* A, const void* G, const void* V, int64_t N, int64_t n_val,
+                      int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, float* P,
+                      int64_t p_ld, int tile_reduce, int64_t p_row0, hipStream_t s) {
   const size_t esz = sizeof(typename Tr::E);
   const RowMap tr = train_rows(N, n_val, val_start, T);
   GemmParams r{};
@@ -1796,6 +1830,19 @@ int launch_rowdot(const void* A, const void* G, const void* V, int64_t N, int64_
   r.z_vec_ok = aligned16(G) && (d_out * static_cast<int64_t>(esz)) % 16 == 0;
   r.z_nbytes = N * T * d_out * static_cast<int64_t>(esz);
   return Launch<Tr, RC>::template run<EPI_ROWDOT>(r, r.L1.vec_ok && r.R1.vec_ok, s);
+}
+template <class Tr>
+int launch_rowdot(const void* A, const void* G, const void* V, int64_t N, int64_t n_val,
+                  int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, float* P,
+                  int64_t p_ld, int tile_reduce, int64_t p_row0, hipStream_t s) {
+  if constexpr (std::is_same<Tr, TrBF16>::value) {
+    const int64_t ntr = ceil_div((N - n_val) * T, RowdotCfg<Tr>::BN);
+    if (rowdot_bm<Tr>(d_out, ntr, false) == RowdotCfg192::BM)
+      return launch_rowdot_cfg<Tr, RowdotCfg192>(A, G, V, N, n_val, val_start, T, d_in, d_out, P,
+                                                 p_ld, tile_reduce, p_row0, s);
+  }
+  return launch_rowdot_cfg<Tr, RowdotCfg<Tr>>(A, G, V, N, n_val, val_start, T, d_in, d_out, P,
+                                              p_ld, tile_reduce, p_row0, s);
 }
 
 // Transposed val operands of the val-gradient GEMM: At [d_in][vcols], Gt [d_out][vcols]
@@ -1848,7 +1895,6 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
                float* out_dot, float* out_pair, const LinearPlan& pl, Carver& cv, hipStream_t s) {
   using E = typename Tr::E;
   using GC = GhostCfg<Tr>;
-  using RC = RowdotCfg<Tr>;
   const size_t esz = sizeof(E);
   const int64_t n_t = N - n_val;
   const RowMap tr = train_rows(N, n_val, val_start, T);
@@ -1923,7 +1969,7 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   // VALGRAD: V = G_val^T A_val (per val row when pairs are wanted), then the fused row-dot
   // GEMM over the train tokens.  bf16: V by the K-major GEMM on the val rows as they lie.
   const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
-  const int64_t n_mt = ceil_div(d_out, RC::BM);
+  const int64_t n_mt = pl.p_rows / pl.groups;  // row-dot M tiles (the plan's tile height)
   if constexpr (std::is_same<Tr, TrBF16>::value) {
     if (val_tn(GS_DTYPE_BF16, n_val, T, d_in, d_out, presum) && aligned16(A) && aligned16(G)) {
       const E* La = static_cast<const E*>(A) + val_start * T * d_in;
@@ -2132,19 +2178,20 @@ struct RowdotPlan {
   int tile_reduce;
 };
 template <class Tr>
-RowdotPlan plan_rowdot(int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
+RowdotPlan plan_rowdot(int64_t N, int64_t n_val, int64_t T, int64_t d_out, bool full) {
   using RC = RowdotCfg<Tr>;
   RowdotPlan pl{};
   const int64_t n_t = N - n_val;
-  pl.n_mt = ceil_div(d_out, RC::BM);
+  pl.n_mt = ceil_div(d_out, rowdot_bm<Tr>(d_out, ceil_div(n_t * T, RC::BN), full));
   pl.tile_reduce = T % RC::BN == 0 ? 1 : 0;
   pl.p_ld = pl.tile_reduce ? n_t * T / RC::BN : n_t * T;
   pl.cols = pl.tile_reduce ? T / RC::BN : T;
   return pl;
 }
-RowdotPlan plan_rowdot_any(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
-  return dtype == GS_DTYPE_F32 ? plan_rowdot<TrF32>(N, n_val, T, d_out)
-                               : plan_rowdot<TrBF16>(N, n_val, T, d_out);
+RowdotPlan plan_rowdot_any(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out,
+                           bool full = false) {
+  return dtype == GS_DTYPE_F32 ? plan_rowdot<TrF32>(N, n_val, T, d_out, full)
+                               : plan_rowdot<TrBF16>(N, n_val, T, d_out, full);
 }
 }  // namespace
 }  // namespace gs
@@ -2199,7 +2246,8 @@ bool rowdot_bias_ok(int dtype, const void* A, const void* G, const void* V, int6
                     int64_t T, int64_t d_in, int64_t d_out) {
   using RC = RowdotCfg<TrBF16>;
   if (dtype != GS_DTYPE_BF16 || !GS_USE_DMA || !GS_ROWDOT_DMA) return false;
-  if (T % RC::BN != 0 || d_out % RC::BM != 0 || d_in % 8 != 0 || d_out % 8 != 0) return false;
+  const bool whole = d_out % RC::BM == 0 || (GS_ROWDOT192 && d_out % RowdotCfg192::BM == 0);
+  if (T % RC::BN != 0 || !whole || d_in % 8 != 0 || d_out % 8 != 0) return false;
   const int64_t ga = N * T * d_in * 2, gg = N * T * d_out * 2, gv = d_out * d_in * 2;
   if (ga >= INT32_MAX || gg >= INT32_MAX || gv >= INT32_MAX) return false;
   if (A != nullptr && !(aligned16(A) && aligned16(G) && aligned16(V))) return false;
@@ -2218,7 +2266,7 @@ struct RowdotBiasPlan {
 };
 RowdotBiasPlan plan_rowdot_bias(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
   RowdotBiasPlan b;
-  b.pl = plan_rowdot_any(dtype, N, n_val, T, d_out);
+  b.pl = plan_rowdot_any(dtype, N, n_val, T, d_out, true);
   b.n_t = N - n_val;
   b.n_tiles = b.n_t * T / RowdotCfg<TrBF16>::BN;
   return b;
@@ -2240,11 +2288,20 @@ int launch_rowdot_bias(const void* A, const void* G, const void* V, const float*
                        float* BP, float* out_dot, float* out_bias_dot, void* out_bias_grad,
                        int grad_dtype, float grad_scale, hipStream_t s) {
   using RC = RowdotCfg<TrBF16>;
-  using RD = DmaForEpi<RC, EPI_ROWDOT>;
   // Every tile must take the LDS epilogue, the only one that writes the bias terms.
+  using RD = DmaForEpi<RC, EPI_ROWDOT>;
+  using RD2 = DmaForEpi<RowdotCfg192, EPI_ROWDOT>;
   static_assert(static_cast<int64_t>(RC::BN) * RC::BM * 2 <= RD::STAGES * RD::STAGE_BYTES &&
                     RD::STAGES * RD::STAGE_BYTES <= 160 * 1024,
                 "row-dot tile does not take the LDS epilogue");
+  static_assert(static_cast<int64_t>(RowdotCfg192::BN) * RowdotCfg192::BM * 2 <=
+                        RD2::STAGES * RD2::STAGE_BYTES &&
+                    RD2::STAGES * RD2::STAGE_BYTES <= 160 * 1024,
+                "row-dot tile does not take the LDS epilogue");
+  static_assert(RowdotCfg192::BN == RC::BN, "both row-dot tiles are BN tokens wide");
+  const bool bm192 = b.pl.n_mt * RowdotCfg192::BM == d_out;
+  if (!bm192 && b.pl.n_mt * RC::BM != d_out)
+    return fail(GS_ERR_INVALID, "internal: row-dot tile height");
   const RowMap tr = train_rows(N, n_val, val_start, T);
   GemmParams r{};
   r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, 2, d_out * d_in * 2);
@@ -2268,7 +2325,8 @@ int launch_rowdot_bias(const void* A, const void* G, const void* V, const float*
   r.vp_rows = vp_rows;
   if (r.n_tiles != b.n_tiles || !b.pl.tile_reduce || !dma_ok(r.L1) || !dma_ok(r.R1))
     return fail(GS_ERR_INVALID, "internal: row-dot tiles");
-  int rc = Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
+  int rc = bm192 ? Launch<TrBF16, RowdotCfg192>::template run<EPI_ROWDOT>(r, true, s)
+                 : Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
   if (rc) return rc;
   const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{64}) : 0;
   const dim3 grid(static_cast<unsigned>(2 * b.n_t + gblocks));
@@ -2325,7 +2383,7 @@ extern "C" int gs_linear_rowdot_bias(const void* A, const void* G, const void* V
   if (!rowdot_bias_ok(dtype, A, G, V, N, T, d_in, d_out))
     return fail(GS_ERR_UNSUPPORTED,
                 "gs_linear_rowdot_bias: needs bf16, 16-byte aligned operands below 2 GiB, "
-                "T a multiple of 256 and d_out a multiple of 256");
+                "T a multiple of 256 and d_out a multiple of 192 or 256");
   const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
   if (workspace == nullptr ||
       workspace_bytes < gs_linear_rowdot_bias_workspace(dtype, N, n_val, T, d_in, d_out) - 256)
@@ -2402,7 +2460,7 @@ extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64
   if (!bias_dot_ok(dtype, A, G, N, n_val, T, d_in, d_out, presum))
     return fail(GS_ERR_UNSUPPORTED,
                 "gs_linear_bias_dot: needs bf16, 16-byte aligned operands below 2 GiB, "
-                "T a multiple of 256 and d_out a multiple of 256");
+                "T a multiple of 256 and d_out a multiple of 192 or 256");
   const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
   if (workspace == nullptr ||
       workspace_bytes <

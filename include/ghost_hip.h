@@ -130,7 +130,7 @@ int gs_linear_rowdot(const void* A, const void* G, const void* V, int dtype, int
  *                     grad_dtype)
  * The row-dot epilogue sums each G tile it already holds in LDS over its tokens; those
  * column sums give both bias terms, so the train rows of G are read once.
- * Supported for bf16, 16-byte aligned operands below 2 GiB, T and d_out multiples of 256:
+ * Supported for bf16, 16-byte aligned operands below 2 GiB, T a multiple of 256 and d_out of 192 or 256:
  * the workspace query returns 0 otherwise (use gs_linear_rowdot + gs_bias_dot then). */
 size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
                                        int64_t d_in, int64_t d_out);

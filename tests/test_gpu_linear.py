@@ -214,11 +214,33 @@ def test_linear_bias_fused_matches_closed_forms(gpu, v_gemm, shape, semantics):
                  "bias grad")
 
 
+@pytest.mark.parametrize("shape", [(20, 4, 1024, 64, 768), (20, 4, 1024, 32, 2304)])
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_rowdot_192_row_tiles(gpu, shape, semantics):
+    """d_out 768 and 2304 over 64 train-token tiles: the row-dot takes 192-row tiles (256 and
+    768 workgroups instead of 192 and 576), for the plain dot and the fused bias pass."""
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 600 + d_out, torch.bfloat16)
+    sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
+    print(f"rowdot 192 shape={shape} sem={semantics}", flush=True)
+    ops = _native.ops()
+    dot, _ = ops.linear_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem, algo=_native.ALGO_VALGRAD)
+    dot2, bdot, bgrad = ops.linear_bias_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem,
+                                            algo=_native.ALGO_VALGRAD,
+                                            grad_scale=N / (N - n_val), grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    want = R.linear_dot_exact(A, G, n_val, semantics)
+    assert_close(dot.cpu(), want, BF16_TOL, "weight dot")
+    assert_close(dot2.cpu(), want, BF16_TOL, "weight dot (fused)")
+    assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
+    assert_close(bgrad.cpu(), R.bias_train_grad(G.double() * N, n_val), BF16_TOL, "bias grad")
+
+
 def test_linear_bias_fused_declines_unsupported_shapes(gpu):
     ops = _native.ops()
     A, G = _inputs(6, 100, 64, 256, 5, torch.bfloat16)        # T not a multiple of 256
     assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None
-    A, G = _inputs(6, 256, 64, 200, 6, torch.bfloat16)        # d_out not a multiple of 256
+    A, G = _inputs(6, 256, 64, 200, 6, torch.bfloat16)        # d_out not a multiple of 192/256
     assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None
     A, G = _inputs(6, 256, 64, 256, 7, torch.float32)         # fp32 operands
     assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None

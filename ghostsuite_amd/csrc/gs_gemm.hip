@@ -60,7 +60,9 @@ struct TrF32 {
   }
 };
 
-enum { EPI_GHOST = 0, EPI_ROWDOT = 1, EPI_STORE = 2 };
+// EPI_ROWDOT_KS: ROWDOT whose R operand is the train rows of G (the pass runs over K = d_out),
+// so the bias column sums come from the R stages of the mainloop instead of the Z tile.
+enum { EPI_GHOST = 0, EPI_ROWDOT = 1, EPI_STORE = 2, EPI_ROWDOT_KS = 3 };
 
 // One operand of a GEMM: rows picked by a RowMap from a row-major [*, ld] tensor.
 // per_seg: tiles never straddle segments (tile = (segment, position block)); otherwise
@@ -99,6 +101,12 @@ struct GemmParams {
   float* PB;
   const float* vp;
   int64_t vp_rows;
+  // ROWDOT_KS: kbp = column sums of the R rows of each stage over this workgroup's share of
+  // the token tile ([m_tiles * n_tiles][K1], row mt * n_tiles + nt; the m_tiles workgroups
+  // of a token tile split its BN rows), kpb = the tile's bias-dot share
+  // sum_k vb[k] * kbp[row][k] (layout of P), vb from vp as above.
+  float* kbp;
+  float* kpb;
   // STORE
   void* C;
   int64_t c_ld;
@@ -487,18 +495,142 @@ __device__ __forceinline__ void wait_stages(int64_t pending) {
 // barrier that opens stage kt (every wave has finished reading that slot, stage kt - 1, by
 // then).  The steady-state loop body is one basic block: a constant vmcnt wait, barrier,
 // loads, MFMAs.
+// K-side column sums (EPI_ROWDOT_KS): every stage's R rows [r0, r1) summed per feature k.
+// Wave w sums rows r0 + w, r0 + w + NW, ... for feature `lane` into wsum[kt % 3][w][lane]
+// (ks_load before the stage's MFMAs, ks_stage after them).  Two stages later (after two
+// barriers) the wave reads the NW wave sums of features 8w .. 8w + 7 of that stage
+// (ks_read, before the MFMAs) and one stage after that adds them in wave order and stores
+// them to row[k] (ks_store, right after the barrier, well ahead of the next vmcnt wait).  The
+// last three stages are flushed after the mainloop by lanes 0-7, 8-15 and 16-23.
+struct KsState {
+  float* row;   // this workgroup's row of kbp (K floats)
+  float* wsum;  // LDS [3][NW][64]
+  int r0, r1;   // R rows of each stage this workgroup sums
+};
+// Rows go in passes of 8 per wave (8 NW rows per workgroup); rows past r1 read a row inside
+// the stage and add nothing.
 template <class C, class D>
-__device__ __forceinline__ void mainloop_dma(const Operand& L, const Operand& R, int64_t mt,
+__device__ __forceinline__ void ks_load(const unsigned char* stage, const KsState& ks, int base,
+                                        uint32_t (&v)[8]) {
+  constexpr int NW = C::WM * C::WN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int c = (lane >> 3) & (D::CH - 1), e = (lane & 7) * 2;
+  const int rsafe = ks.r0 < ks.r1 ? ks.r0 : 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = base + wid + NW * j;
+    const int sr = C::BM + (r < ks.r1 ? r : rsafe);
+    v[j] = *reinterpret_cast<const uint16_t*>(stage + sr * D::ROW_BYTES +
+                                              ((c ^ D::swz(sr)) * 16) + e);
+  }
+}
+template <class C, class D>
+__device__ __forceinline__ void ks_stage(const unsigned char* stage, const KsState& ks, int buf,
+                                         const uint32_t (&v0)[8]) {
+  constexpr int NW = C::WM * C::WN;
+  static_assert(D::KB <= 64 && D::KB == 8 * NW, "one feature per lane, 8 per wave");
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  // Every LDS access of this wave so far has completed, the previous stage's wsum write
+  // included (read after the next barrier).
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (ks.r0 + wid + NW * j < ks.r1) s += __uint_as_float(v0[j] << 16);
+  for (int base = ks.r0 + 8 * NW; base < ks.r1; base += 8 * NW) {
+    uint32_t v[8];
+    ks_load<C, D>(stage, ks, base, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (base + wid + NW * j < ks.r1) s += __uint_as_float(v[j] << 16);
+  }
+  ks.wsum[(buf * NW + wid) * 64 + lane] = lane < D::KB ? s : 0.f;
+}
+template <class C, class D>
+__device__ __forceinline__ void ks_read(const KsState& ks, int buf, float (&f)[C::WM * C::WN]) {
+  constexpr int NW = C::WM * C::WN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) f[w] = ks.wsum[(buf * NW + w) * 64 + 8 * wid + (lane & 7)];
+}
+template <class C, class D>
+__device__ __forceinline__ float ks_store(const KsState& ks, const float (&f)[C::WM * C::WN],
+                                          int64_t k0, int64_t K, int lane0) {
+  constexpr int NW = C::WM * C::WN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += f[w];
+  const int64_t k = k0 + 8 * wid + (lane & 7);
+  if (lane >= lane0 && lane < lane0 + 8 && k < K) ks.row[k] = t;
+  return t;
+}
+// After the mainloop (its LDS writes waited for, then a barrier): lanes 8g .. 8g + 7 flush
+// stage nk - 1 - g, g < 3; returns that sum (0 in the other lanes).
+template <class C, class D>
+__device__ __forceinline__ float ks_final(const KsState& ks, int64_t nk, int64_t K) {
+  constexpr int NW = C::WM * C::WN;
+  const int g = (threadIdx.x & 63) >> 3;
+  const int64_t st = nk - 1 - g;
+  float f[NW];
+  ks_read<C, D>(ks, static_cast<int>(((st % 3) + 3) % 3), f);
+  if (g >= 3 || st < 0) return 0.f;
+  return ks_store<C, D>(ks, f, st * D::KB, K, 8 * g);
+}
+// This wave's share of the tile's bias-dot: the sum over the features it flushed of
+// kbp[row][k] * vb[k], vb[k] = the sum of the vp_rows rows of vp.  Stages are taken from the
+// last one down, so lanes 0-23 start on the three stages ks_final flushed and use their sums
+// from `last` (those stores may still be in flight); the earlier stores were waited for before
+// the mainloop's last barrier.
+// Loads go in passes of 8 per lane, all issued before the first product.
+template <class C, class D>
+__device__ __forceinline__ float ks_bias_share(const GemmParams& p, const float* row,
+                                               float last) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t K = p.K1, nk = (K + D::KB - 1) / D::KB, total = nk * 8;
+  float q = 0.f;
+  for (int64_t base = 0; base < total; base += 8 * 64) {
+    float bp[8], vb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = base + lane + 64 * u;
+      const int64_t k = (nk - 1 - (i >> 3)) * D::KB + 8 * wid + (i & 7);
+      const bool ok = i < total && k < K;
+      bp[u] = ok ? (i < 24 ? last : row[k]) : 0.f;
+      vb[u] = ok ? p.vp[k] : 0.f;
+    }
+    for (int64_t r = 1; r < p.vp_rows; ++r) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t i = base + lane + 64 * u;
+        const int64_t k = (nk - 1 - (i >> 3)) * D::KB + 8 * wid + (i & 7);
+        if (i < total && k < K) vb[u] += p.vp[r * K + k];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) q += bp[u] * vb[u];
+  }
+  return q;
+}
+
+// With KS the two-stage ring's constant wait is vmcnt(0), which also covers the column-sum
+// stores; returns this lane's sum from ks_final (0 without KS).
+template <class C, class D, bool KS = false>
+__device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R, int64_t mt,
                                              int64_t nt, int64_t K, const DmaLds& l,
-                                             f32x16_t (&acc)[C::MI][C::NI]) {
+                                             f32x16_t (&acc)[C::MI][C::NI],
+                                             const KsState* ks = nullptr) {
   constexpr int NQ = D::QL + D::QR;
   constexpr int AHEAD = D::STAGES - 1;  // stages in flight ahead of the one computed
   static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
+  static_assert(!KS || D::STAGES == 2, "K-side sums assume the two-stage ring");
   DmaStreamer<C, D> st;
   st.init(L, R, mt, nt);
   const int nk = static_cast<int>((K + D::KB - 1) / D::KB);
   auto slot = [&](int k) { return l.base + (k % D::STAGES) * D::STAGE_BYTES; };
   auto slot_at = [&](int k) { return l.addr + (k % D::STAGES) * D::STAGE_BYTES; };
+  float kf[C::WM * C::WN];  // KS: wave sums read for the store one stage later
+  uint32_t kv[8];           // KS: the stage's first row reads
 #pragma unroll
   for (int s = 0; s < AHEAD; ++s)
     if (s < nk) st.issue(slot_at(s), static_cast<int64_t>(s) * D::KB, K);
@@ -507,16 +639,41 @@ __device__ __forceinline__ void mainloop_dma(const Operand& L, const Operand& R,
     wait_vmcnt<(AHEAD - 1) * NQ>();  // stage kt has landed
     raw_barrier();
     st.issue(slot_at(kt + AHEAD), static_cast<int64_t>(kt + AHEAD) * D::KB, K);
+    if constexpr (KS) {
+      if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
+      if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
+      ks_load<C, D>(slot(kt), *ks, ks->r0, kv);
+      // Keep these reads out of the MFMA stream's fragment-read schedule.
+      __builtin_amdgcn_sched_barrier(0);
+    }
     dma_compute<C, D>(slot(kt), acc);
+    if constexpr (KS) {
+      __builtin_amdgcn_sched_barrier(0);
+      ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
+    }
   }
   // Tail: no more loads; the stages still in flight drain one by one.
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
+    if constexpr (KS) {
+      if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
+      if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
+      ks_load<C, D>(slot(kt), *ks, ks->r0, kv);
+      // Keep these reads out of the MFMA stream's fragment-read schedule.
+      __builtin_amdgcn_sched_barrier(0);
+    }
     dma_compute<C, D>(slot(kt), acc);
+    if constexpr (KS) {
+      __builtin_amdgcn_sched_barrier(0);
+      ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
+    }
   }
+  if constexpr (KS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   wait_vmcnt<0>();
   raw_barrier();
+  if constexpr (KS) return ks_final<C, D>(*ks, nk, K);
+  return 0.f;
 }
 
 // Maps the launch index to (m tile, n tile): consecutive workgroups of one XCD get
@@ -688,19 +845,24 @@ __device__ __forceinline__ void rowdot_issue_z(const GemmParams& p, int64_t mt, 
   }
 }
 
-template <class C>
+// KS: the bias terms come from the mainloop's K-side sums (ks_row, ks_last); the tile's
+// bias-dot share is read back while the Z tile comes in, and the Z-tile sums are skipped.
+template <class C, class D, bool KS>
 __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
                                                   f32x16_t (&acc)[C::MI][C::NI], int64_t mt,
                                                   int64_t nt, unsigned char* lds,
-                                                  float (&colsum)[C::NI], float* bsum) {
+                                                  float (&colsum)[C::NI], float* bsum,
+                                                  const float* ks_row, float ks_last) {
   constexpr int CPR = ZTile<C>::CPR;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
   // The tile's slice of the val bias gradient, loaded while the Z tile comes in.
   float vbm = 0.f;
-  if (p.PB != nullptr && threadIdx.x < C::BM)
+  if (!KS && p.PB != nullptr && threadIdx.x < C::BM)
     for (int64_t r = 0; r < p.vp_rows; ++r) vbm += p.vp[r * p.m_rows + mt * C::BM + threadIdx.x];
   rowdot_issue_z<C>(p, mt, nt, lds);
+  float ksq = 0.f;
+  if constexpr (KS) ksq = ks_bias_share<C, D>(p, ks_row, ks_last);
   wait_vmcnt<0>();
   __syncthreads();  // Z landed (every wave waited for its DMA)
   const int half = (lane >> 5) * 8;
@@ -721,7 +883,11 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
       }
     colsum[ni] = s;
   }
-  if (p.BP != nullptr) {
+  if constexpr (KS) {
+    __shared__ float kred[C::NT / 64];
+    const float tot = block_sum(ksq, kred);
+    if (threadIdx.x == 0) p.kpb[(p.p_row0 + mt) * p.p_ld + nt] = tot;
+  } else if (p.BP != nullptr) {
     // Column sums of the tile over its BN token rows: thread t < GRP * CG takes column group
     // q = t % CG (4 columns, one ds_read_b64) of every GRP-th row starting at t / CG; the
     // group sums combine in a fixed order through `bsum` [GRP][BM].
@@ -833,7 +999,21 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
-  mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
+  float ks_last = 0.f;
+  const float* ks_row = nullptr;
+  if constexpr (EPI == EPI_ROWDOT_KS) {
+    // The m_tiles workgroups of a token tile split its BN rows for the K-side sums.
+    __shared__ float ks_wsum[3 * C::WM * C::WN * 64];
+    const int64_t rpw = (C::BN + p.m_tiles - 1) / p.m_tiles;
+    const int64_t r0 = mt * rpw < C::BN ? mt * rpw : C::BN;
+    const int64_t r1 = r0 + rpw < C::BN ? r0 + rpw : C::BN;
+    float* row = p.kbp + (mt * p.n_tiles + nt) * p.K1;
+    const KsState ks{row, ks_wsum, static_cast<int>(r0), static_cast<int>(r1)};
+    ks_row = row;
+    ks_last = mainloop_dma<C, D, true>(p.L1, p.R1, mt, nt, p.K1, l, acc, &ks);
+  } else {
+    mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
+  }
   if constexpr (EPI == EPI_STORE) {
     store_epilogue<TrBF16, C>(p, acc, mt, nt);
   } else {
@@ -843,6 +1023,10 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
       zero_acc<TrBF16, C>(acc2);
       mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc2);
       ghost_colsum<C>(p, acc, acc2, colsum);
+    } else if constexpr (EPI == EPI_ROWDOT_KS) {
+      // Every tile is whole along M and takes the LDS epilogue (checked by the host).
+      static_assert(static_cast<int64_t>(C::BN) * C::BM * 2 <= D::STAGES * SB, "Z tile in LDS");
+      rowdot_colsum_lds<C, D, true>(p, acc, mt, nt, s0, colsum, nullptr, ks_row, ks_last);
     } else {
       constexpr bool fits = static_cast<int64_t>(C::BN) * C::BM * 2 <= D::STAGES * SB;
       const bool zlds = fits && p.z_vec_ok && (mt + 1) * C::BM <= p.m_rows &&
@@ -859,7 +1043,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
             __shared__ __attribute__((aligned(16))) float bsum_own[BSUM];
             bsum = bsum_own;
           }
-          rowdot_colsum_lds<C>(p, acc, mt, nt, s0, colsum, bsum);
+          rowdot_colsum_lds<C, D, false>(p, acc, mt, nt, s0, colsum, bsum, nullptr, 0.f);
         } else {
           rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
         }
@@ -1024,6 +1208,7 @@ __global__ void __launch_bounds__(256) val_colsum_kernel(const uint16_t* __restr
 // partials P of train sample i, blocks [n_train, 2 n_train) its bias-dot shares PB (same
 // layout), blocks beyond take grad[f] = scale * sum over the N tiles of BP[tile][f] for 64
 // columns each, 4 row groups combined in LDS (all fixed order).
+constexpr int FINISH_GF = 16;  // bias-gradient features per finishing block
 template <class GE>
 __global__ void __launch_bounds__(256) rowdot_bias_finish_kernel(
     const float* __restrict__ P, const float* __restrict__ PB, int64_t rows, int64_t p_ld,
@@ -1040,23 +1225,31 @@ __global__ void __launch_bounds__(256) rowdot_bias_finish_kernel(
     return;
   }
   if (grad == nullptr) return;
-  const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
-  const int64_t f = (b - 2 * n_train) * 64 + c;
+  // Grad blocks: FINISH_GF features each, FINISH_RG row groups of BP rows, fixed-order sums.
+  constexpr int GF = FINISH_GF, RG = 256 / GF;
+  __shared__ float gred[RG][GF];
+  const int c = threadIdx.x % GF, rg = threadIdx.x / GF;
+  const int64_t f = (b - 2 * n_train) * GF + c;
   float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
   if (f < F) {
     int64_t k = rg;
-    for (; k + 12 < n_tiles; k += 16) {
+#pragma unroll 2
+    for (; k + 3 * RG < n_tiles; k += 4 * RG) {
       t0 += BP[k * F + f];
-      t1 += BP[(k + 4) * F + f];
-      t2 += BP[(k + 8) * F + f];
-      t3 += BP[(k + 12) * F + f];
+      t1 += BP[(k + RG) * F + f];
+      t2 += BP[(k + 2 * RG) * F + f];
+      t3 += BP[(k + 3 * RG) * F + f];
     }
-    for (; k < n_tiles; k += 4) t0 += BP[k * F + f];
+    for (; k < n_tiles; k += RG) t0 += BP[k * F + f];
   }
-  red[rg][c] = (t0 + t1) + (t2 + t3);
+  gred[rg][c] = (t0 + t1) + (t2 + t3);
   __syncthreads();
-  if (rg == 0 && f < F)
-    grad[f] = from_f32<GE>(scale * ((red[0][c] + red[1][c]) + (red[2][c] + red[3][c])));
+  if (rg == 0 && f < F) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) t += gred[g][c];
+    grad[f] = from_f32<GE>(scale * t);
+  }
 }
 
 // out[f][c] = row c of the row set, feature f (with `presum`: c = position, summed over all
@@ -1228,7 +1421,9 @@ struct TnParams {
   int64_t M, N, m_tiles, n_tiles;
   void* out;        // splits == 1: bf16 [M][N]; else fp32 partials [split][M][N]
   int splits;
-  float* vsum;      // null, or [split][M]: column sums of L over the split's k-rows
+  float* vsum;      // null, or [split][vparts][M]: column sums of L over the split's k-rows
+  int vsum_r;       // 1: vsum holds the column sums of R instead ([split][vparts][N])
+  int vparts;       // the tiles along the other side (N, or M with vsum_r) split the k-rows
 };
 
 template <class C, class D>
@@ -1342,29 +1537,34 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
 
 // acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same
 // schedule as mainloop_dma: constant vmcnt wait, barrier, loads of stage k + NS - 1, MFMAs).
-// Column sums of a stage's L part: thread t owns the 4 columns of group t % (BM / 4) and
-// every (NT / (BM / 4))-th k-row from t / (BM / 4); zero-filled rows add nothing.
-template <class C, class D>
-__device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs)[4]) {
-  constexpr int CG = C::BM / 4, NRG = C::NT / CG;
-  static_assert(C::NT % CG == 0, "column groups");
+// Column sums of a stage's L part (RS: its R part): thread t owns the 4 columns of group
+// t % (W / 4) and every (NT / (W / 4))-th k-row from t / (W / 4), W the part's tile width;
+// zero-filled rows add nothing.
+// The vparts workgroups along the other side share the work: part p takes the k-rows
+// rg + NRG j with j = p mod vparts.
+template <class C, class D, bool RS>
+__device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs)[4], int part,
+                                          int vparts) {
+  constexpr int W = RS ? C::BN : C::BM, CG = W / 4, NRG = C::NT / CG;
+  constexpr int RB = RS ? D::RR : D::RL, CH = RS ? D::CR : D::CL, OFF = RS ? D::L_BYTES : 0;
+  static_assert(C::NT % CG == 0 && D::KB % NRG == 0, "column groups");
   const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
   const int c = cg >> 1, hb = (cg & 1) * 8;
-#pragma unroll 4
-  for (int r = rg; r < D::KB; r += NRG) {
+  for (int j = part; j < D::KB / NRG; j += vparts) {
+    const int r = rg + NRG * j;
     union { uint2 v; uint16_t e[4]; } z;
-    z.v = *reinterpret_cast<const uint2*>(stage + r * D::RL +
-                                          ((c ^ D::template swz<D::CL>(r)) * 16) + hb);
+    z.v = *reinterpret_cast<const uint2*>(stage + OFF + r * RB +
+                                          ((c ^ D::template swz<CH>(r)) * 16) + hb);
 #pragma unroll
     for (int e = 0; e < 4; ++e) cs[e] += bf16_to_f32(z.e[e]);
   }
 }
 
-template <class C, class D>
+template <class C, class D, bool RS>
 __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
                                             int64_t k_begin, int64_t k_end, unsigned char* lds,
                                             f32x16_t (&acc)[C::MI][C::NI], bool colsum,
-                                            float (&cs)[4]) {
+                                            float (&cs)[4], int part) {
   constexpr int NQ = D::QL + D::QR;
   constexpr int AHEAD = D::STAGES - 1;
   static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
@@ -1381,13 +1581,13 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
     raw_barrier();
     st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
     tn_compute<C, D>(slot(kt), acc);
-    if (colsum) tn_colsum<C, D>(slot(kt), cs);
+    if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
     tn_compute<C, D>(slot(kt), acc);
-    if (colsum) tn_colsum<C, D>(slot(kt), cs);
+    if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
   }
   wait_vmcnt<0>();
   raw_barrier();
@@ -1404,11 +1604,18 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
   const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
-  // The workgroups of N tile 0 also take the column sums of their L tile (the val rows of
-  // G: the val bias gradient), combined across the row groups in a fixed order.
-  const bool colsum = p.vsum != nullptr && nt == 0;
+  // The workgroups also take the column sums of their L tile (the val rows of G: the val
+  // bias gradient), or with vsum_r of their R tile (G on the right when the GEMM forms V^T):
+  // the workgroups along the other side (part = nt, or mt) split each stage's k-rows, and
+  // the row groups combine in a fixed order.
+  static_assert(C::BM == C::BN, "one column-sum layout for both sides");
+  const int part = static_cast<int>(p.vsum_r ? mt : nt);
+  const bool colsum = p.vsum != nullptr && part < p.vparts;
   float cs[4] = {0.f, 0.f, 0.f, 0.f};
-  mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs);
+  if (p.vsum_r)
+    mainloop_tn<C, D, true>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs, part);
+  else
+    mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs, part);
   if (colsum) {
     constexpr int CG = C::BM / 4, NRG = C::NT / CG;
     static_assert(NRG * C::BM * 4 <= D::STAGES * D::STAGE_BYTES, "column-sum scratch");
@@ -1417,12 +1624,14 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[rg * C::BM + 4 * cg + e] = cs[e];
     __syncthreads();
+    const int64_t ext = p.vsum_r ? p.N : p.M, t0 = (p.vsum_r ? nt : mt) * C::BM;
     for (int m = threadIdx.x; m < C::BM; m += C::NT) {
       float t = 0.f;
 #pragma unroll
       for (int g = 0; g < NRG; ++g) t += red[g * C::BM + m];
-      const int64_t col = mt * C::BM + m;
-      if (col < p.M) p.vsum[static_cast<int64_t>(blockIdx.y) * p.M + col] = t;
+      const int64_t col = t0 + m;
+      if (col < ext)
+        p.vsum[(static_cast<int64_t>(blockIdx.y) * p.vparts + part) * ext + col] = t;
     }
   }
   GemmParams e{};
@@ -1439,10 +1648,36 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
 }
 
 // out[i] = bf16(sum over the splits of part[s][i]), fixed order, 4 elements per thread.
+// With vsum ([vs_rows][vs_n]) its rows are also summed into row 0, in place.
 __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict__ part,
                                                         int64_t count, int splits,
-                                                        uint16_t* __restrict__ out) {
+                                                        uint16_t* __restrict__ out, float* vsum,
+                                                        int64_t vs_n, int64_t vs_rows) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (vsum != nullptr && i < vs_n) {
+    // Rows k = j mod 4 into four running sums (loads in flight together), then combined.
+    float4 t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t k = 0; k < vs_rows; k += 4) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (k + j < vs_rows) {
+          const float4 v = *reinterpret_cast<const float4*>(vsum + (k + j) * vs_n + i);
+          t[j].x += v.x;
+          t[j].y += v.y;
+          t[j].z += v.z;
+          t[j].w += v.w;
+        }
+      }
+    }
+    float4 r;
+    r.x = (t[0].x + t[1].x) + (t[2].x + t[3].x);
+    r.y = (t[0].y + t[1].y) + (t[2].y + t[3].y);
+    r.z = (t[0].z + t[1].z) + (t[2].z + t[3].z);
+    r.w = (t[0].w + t[1].w) + (t[2].w + t[3].w);
+    *reinterpret_cast<float4*>(vsum + i) = r;
+  }
   if (i >= count) return;
   float4 s = *reinterpret_cast<const float4*>(part + i);
   for (int k = 1; k < splits; ++k) {
@@ -1506,7 +1741,8 @@ using DmaFor = std::conditional_t<3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCf
 // The row-dot kernel's stage geometry (GS_ROWDOT_DMACFG = row bytes, stages) or DmaFor.
 #ifdef GS_ROWDOT_DMACFG
 template <class C, int EPI>
-using DmaForEpi = std::conditional_t<EPI == EPI_ROWDOT, DmaCfg<C, GS_ROWDOT_DMACFG>, DmaFor<C>>;
+using DmaForEpi = std::conditional_t<EPI == EPI_ROWDOT || EPI == EPI_ROWDOT_KS,
+                                     DmaCfg<C, GS_ROWDOT_DMACFG>, DmaFor<C>>;
 #else
 template <class C, int EPI>
 using DmaForEpi = DmaFor<C>;
@@ -1531,7 +1767,8 @@ struct Launch {
     using D = DmaForEpi<C, EPI>;
     if constexpr (std::is_same<Tr, TrBF16>::value &&
                   D::STAGES * D::STAGE_BYTES <= 160 * 1024) {
-      const bool on = EPI == EPI_GHOST || (EPI == EPI_ROWDOT && GS_ROWDOT_DMA) ||
+      const bool on = EPI == EPI_GHOST ||
+                      ((EPI == EPI_ROWDOT || EPI == EPI_ROWDOT_KS) && GS_ROWDOT_DMA) ||
                       (EPI == EPI_STORE && GS_STORE_DMA);
       const bool dma = GS_USE_DMA && on && aligned &&
                        dma_ok(p.L1) && dma_ok(p.R1) &&
@@ -1541,8 +1778,12 @@ struct Launch {
         return check_launch("gemm_dma_kernel");
       }
     }
-    if (aligned) return go(gemm_nt_kernel<Tr, C, true, EPI>, grid, block, p, s);
-    return go(gemm_nt_kernel<Tr, C, false, EPI>, grid, block, p, s);
+    if constexpr (EPI == EPI_ROWDOT_KS) {
+      return fail(GS_ERR_INVALID, "internal: the K-side row-dot needs the LDS-DMA kernel");
+    } else {
+      if (aligned) return go(gemm_nt_kernel<Tr, C, true, EPI>, grid, block, p, s);
+      return go(gemm_nt_kernel<Tr, C, false, EPI>, grid, block, p, s);
+    }
   }
   // Raises the dynamic-LDS limit of each kernel once (the stage buffers exceed 64 KiB).
   static int go(void (*k)(GemmParams), dim3 grid, dim3 block, GemmParams& p, hipStream_t s) {
@@ -1586,6 +1827,7 @@ int64_t host_tiles(const Operand& o) {
 
 struct LinearPlan {
   int algo;        // GS_ALGO_GHOST or GS_ALGO_VALGRAD
+  int swap;        // VALGRAD: the row-dot runs over K = d_out (V^T, R = G rows, Z = A rows)
   int ghost_flat;  // GHOST left side tiled flat (dot only, pairwise)
   int64_t p_rows;  // rows of the partial buffer
   int64_t groups;  // groups in the final reduction
@@ -1689,8 +1931,13 @@ bool val_tn(int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, in
   return dtype == GS_DTYPE_BF16 && tn_ok(nullptr, d_out, nullptr, d_in, K, d_out, d_in);
 }
 // out [M][N] bf16 = L^T R over K k-rows (L: [K][M] stride ldl, R: [K][N] stride ldr).
+// vsum (optional): [splits][parts][M] column sums of L (parts: the first N tiles, at most
+// TN_VPARTS), or with vsum_r [splits][parts][N] those of R (the first M tiles); their total
+// ends in row 0.
+constexpr int64_t TN_VPARTS = 4;
 int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
-              int64_t N, void* out, float* part, hipStream_t s, float* vsum = nullptr) {
+              int64_t N, void* out, float* part, hipStream_t s, float* vsum = nullptr,
+              bool vsum_r = false) {
   TnParams p{};
   p.L = L;
   p.R = R;
@@ -1707,6 +1954,9 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   const int sp = tn_splits(K, M, N);
   p.splits = sp;
   p.vsum = vsum;
+  p.vsum_r = vsum_r ? 1 : 0;
+  p.vparts = static_cast<int>(std::min<int64_t>(
+      TN_VPARTS, vsum_r ? ceil_div(M, TnC::BM) : ceil_div(N, TnC::BN)));
   p.out = sp > 1 ? static_cast<void*>(part) : out;
   if (sp > 1 && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
   const int64_t tiles = p.m_tiles * p.n_tiles;
@@ -1715,20 +1965,36 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(sp)),
                      dim3(TnC::NT), 0, s, p);
   int rc = check_launch("tn_gemm_kernel");
-  if (rc || sp == 1) return rc;
-  const int64_t count = M * N;  // a multiple of 8 (N % 8 == 0)
-  hipLaunchKernelGGL(tn_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(count / 4, 256))),
-                     dim3(256), 0, s, part, count, sp, static_cast<uint16_t*>(out));
+  const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts : 1;
+  if (rc || (sp == 1 && vs_rows == 1)) return rc;
+  const int64_t count = sp > 1 ? M * N : 0;  // a multiple of 8 (N % 8 == 0)
+  const int64_t vs_n = vsum_r ? N : M;
+  hipLaunchKernelGGL(tn_reduce_kernel,
+                     dim3(static_cast<unsigned>(ceil_div(std::max(count, vs_n) / 4, 256))),
+                     dim3(256), 0, s, part, count, sp, static_cast<uint16_t*>(out), vsum, vs_n,
+                     vs_rows);
   return check_launch("tn_reduce_kernel");
 }
 
 
+// The VALGRAD row-dot contracts over the longer feature dimension (bf16): with d_out > d_in
+// it computes sum_t <a_t, V^T g_t>, whose GEMM has the longer K and the narrower Z.
+#ifndef GS_ROWDOT_SWAP
+#define GS_ROWDOT_SWAP 1
+#endif
+template <class Tr>
+bool rowdot_swap(int64_t d_in, int64_t d_out) {
+  return GS_ROWDOT_SWAP && std::is_same<Tr, TrBF16>::value && d_out > d_in && d_in % 8 == 0 &&
+         d_out % 8 == 0;
+}
 template <class Tr>
 LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
                        int semantics, int algo, int want_pair) {
   constexpr int64_t GBM = GhostCfg<Tr>::BM;
   const int64_t n_t = N - n_val;
-  const int64_t RBM = rowdot_bm<Tr>(d_out, ceil_div(n_t * T, RowdotCfg<Tr>::BN), false);
+  const bool swap = rowdot_swap<Tr>(d_in, d_out);
+  const int64_t dm = swap ? d_in : d_out, dk = swap ? d_out : d_in;  // row-dot M extent, K
+  const int64_t RBM = rowdot_bm<Tr>(dm, ceil_div(n_t * T, RowdotCfg<Tr>::BN), false);
   const int64_t nv_eff = semantics == GS_SEM_PRESUM ? 1 : n_val;  // val rows after presum
   LinearPlan pl{};
   // MFMA flops including tile padding.
@@ -1736,7 +2002,7 @@ LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_
   const double ghost_m = flat ? static_cast<double>(ceil_div(nv_eff * T, GBM) * GBM)
                               : static_cast<double>(nv_eff * ceil_div(T, GBM) * GBM);
   const double ghost = 2.0 * n_t * T * ghost_m * (d_in + d_out);
-  const double rowdot = 2.0 * n_t * T * ceil_div(d_out, RBM) * RBM * d_in;
+  const double rowdot = 2.0 * n_t * T * ceil_div(dm, RBM) * RBM * dk;
   const double vgemm = 2.0 * nv_eff * T * d_out * d_in;
   const double valgrad = vgemm + rowdot * (want_pair ? n_val : 1);
   pl.algo = algo;
@@ -1748,7 +2014,8 @@ LinearPlan plan_linear(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_
     pl.groups = flat ? 1 : nv_eff;
     bn = GhostCfg<Tr>::BN;
   } else {
-    const int64_t n_mt = ceil_div(d_out, RBM);
+    const int64_t n_mt = ceil_div(dm, RBM);
+    pl.swap = swap ? 1 : 0;
     pl.groups = want_pair ? n_val : 1;
     pl.p_rows = pl.groups * n_mt;
     pl.vcols = nv_eff * T;
@@ -1997,11 +2264,20 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
         Lg = gbar;
       }
       for (int64_t j = 0; j < pl.groups; ++j) {
-        int rc = launch_tn(Lg + j * kper * d_out, d_out, La + j * kper * d_in, d_in, kper, d_out,
-                           d_in, V, part, s);
-        if (rc) return rc;
-        rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
-                               pl.tile_reduce, j * n_mt, s);
+        int rc;
+        if (pl.swap) {  // V^T [d_in][d_out] = A_val^T G_val; sum_t <a_t, V^T g_t>
+          rc = launch_tn(La + j * kper * d_in, d_in, Lg + j * kper * d_out, d_out, kper, d_in,
+                         d_out, V, part, s);
+          if (rc) return rc;
+          rc = launch_rowdot<Tr>(G, A, V, N, n_val, val_start, T, d_out, d_in, P, pl.p_ld,
+                                 pl.tile_reduce, j * n_mt, s);
+        } else {
+          rc = launch_tn(Lg + j * kper * d_out, d_out, La + j * kper * d_in, d_in, kper, d_out,
+                         d_in, V, part, s);
+          if (rc) return rc;
+          rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
+                                 pl.tile_reduce, j * n_mt, s);
+        }
         if (rc) return rc;
       }
       hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0,
@@ -2018,10 +2294,17 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   const int64_t vsteps = pl.groups;  // one V per val row for pairs, else one V
   const int64_t kper = pl.vcols / vsteps;
   for (int64_t j = 0; j < vsteps; ++j) {
-    rc = store_v<Tr>(Gt, At, pl.vcols, j * kper, kper, d_in, d_out, V, s);
-    if (rc) return rc;
-    rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
-                           pl.tile_reduce, j * n_mt, s);
+    if (pl.swap) {
+      rc = store_v<Tr>(At, Gt, pl.vcols, j * kper, kper, d_out, d_in, V, s);
+      if (rc) return rc;
+      rc = launch_rowdot<Tr>(G, A, V, N, n_val, val_start, T, d_out, d_in, P, pl.p_ld,
+                             pl.tile_reduce, j * n_mt, s);
+    } else {
+      rc = store_v<Tr>(Gt, At, pl.vcols, j * kper, kper, d_in, d_out, V, s);
+      if (rc) return rc;
+      rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
+                             pl.tile_reduce, j * n_mt, s);
+    }
     if (rc) return rc;
   }
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(n_t)), dim3(256), 0, s, P,
@@ -2260,15 +2543,30 @@ namespace gs {
 namespace {
 // Layout of the fused row-dot + bias pass: P (weight-dot partials), PB (bias-dot partials,
 // same layout), BP (tile column sums [n_tiles][d_out]).
+// The fused pass contracts over the longer feature dimension.  With d_out > d_in (swap) it
+// runs over K = d_out: L = V^T [d_in][d_out], R = the train rows of G, Z = the train rows of
+// A, and the bias column sums come from the R stages (EPI_ROWDOT_KS), so the M tiles span d_in.
+#ifndef GS_BIAS_SWAP
+#define GS_BIAS_SWAP 1
+#endif
 struct RowdotBiasPlan {
   RowdotPlan pl;
   int64_t n_t, n_tiles;
+  int swap;
+  int64_t bp_rows;  // rows of BP: n_tiles, or with swap m tiles x n_tiles
 };
-RowdotBiasPlan plan_rowdot_bias(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_out) {
+bool bias_swap(int dtype, int64_t N, int64_t T, int64_t d_in, int64_t d_out) {
+  return GS_BIAS_SWAP && d_out > d_in &&
+         rowdot_bias_ok(dtype, nullptr, nullptr, nullptr, N, T, d_out, d_in);
+}
+RowdotBiasPlan plan_rowdot_bias(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
+                                int64_t d_out, bool allow_swap) {
   RowdotBiasPlan b;
-  b.pl = plan_rowdot_any(dtype, N, n_val, T, d_out, true);
+  b.swap = allow_swap && bias_swap(dtype, N, T, d_in, d_out) ? 1 : 0;
+  b.pl = plan_rowdot_any(dtype, N, n_val, T, b.swap ? d_in : d_out, true);
   b.n_t = N - n_val;
   b.n_tiles = b.n_t * T / RowdotCfg<TrBF16>::BN;
+  b.bp_rows = b.swap ? b.pl.n_mt * b.n_tiles : b.n_tiles;
   return b;
 }
 template <class S>
@@ -2277,7 +2575,7 @@ void carve_rowdot_bias(S& c, const RowdotBiasPlan& b, int64_t d_out, float** P, 
   const size_t np = b.pl.n_mt * b.pl.p_ld;
   *P = c.template take<float>(np);
   *PB = c.template take<float>(np);
-  *BP = c.template take<float>(b.n_tiles * d_out);
+  *BP = c.template take<float>(b.bp_rows * d_out);
 }
 
 // ROWDOT over the train rows with the bias terms (vb = the vp_rows rows of vp summed), then
@@ -2299,45 +2597,58 @@ int launch_rowdot_bias(const void* A, const void* G, const void* V, const float*
                     RD2::STAGES * RD2::STAGE_BYTES <= 160 * 1024,
                 "row-dot tile does not take the LDS epilogue");
   static_assert(RowdotCfg192::BN == RC::BN, "both row-dot tiles are BN tokens wide");
-  const bool bm192 = b.pl.n_mt * RowdotCfg192::BM == d_out;
-  if (!bm192 && b.pl.n_mt * RC::BM != d_out)
+  // dk: the contracted feature dimension, dm: the M extent (the Z width).
+  const bool sw = b.swap != 0;
+  const int64_t dk = sw ? d_out : d_in, dm = sw ? d_in : d_out;
+  const bool bm192 = b.pl.n_mt * RowdotCfg192::BM == dm;
+  if (!bm192 && b.pl.n_mt * RC::BM != dm)
     return fail(GS_ERR_INVALID, "internal: row-dot tile height");
   const RowMap tr = train_rows(N, n_val, val_start, T);
   GemmParams r{};
-  r.L1 = make_operand(V, d_in, plain_rows(d_out), 0, d_in, 2, d_out * d_in * 2);
-  r.R1 = make_operand(A, d_in, tr, 0, d_in, 2, N * T * d_in * 2);
-  r.K1 = d_in;
+  r.L1 = make_operand(V, dk, plain_rows(dm), 0, dk, 2, dm * dk * 2);
+  r.R1 = make_operand(sw ? G : A, dk, tr, 0, dk, 2, N * T * dk * 2);
+  r.K1 = dk;
   r.m_tiles = b.pl.n_mt;
   r.n_tiles = host_tiles<RC::BN>(r.R1);
-  r.m_rows = d_out;
+  r.m_rows = dm;
   r.P = P;
   r.p_ld = b.pl.p_ld;
   r.tile_reduce = b.pl.tile_reduce;
   r.p_row0 = 0;
-  r.Z = G;
-  r.z_ld = d_out;
+  r.Z = sw ? A : G;
+  r.z_ld = dm;
   r.z_map = tr;
   r.z_vec_ok = 1;
-  r.z_nbytes = N * T * d_out * 2;
-  r.BP = BP;
-  r.PB = PB;
+  r.z_nbytes = N * T * dm * 2;
+  if (sw) {
+    r.kbp = BP;
+    r.kpb = PB;
+  } else {
+    r.BP = BP;
+    r.PB = PB;
+  }
   r.vp = vp;
   r.vp_rows = vp_rows;
   if (r.n_tiles != b.n_tiles || !b.pl.tile_reduce || !dma_ok(r.L1) || !dma_ok(r.R1))
     return fail(GS_ERR_INVALID, "internal: row-dot tiles");
-  int rc = bm192 ? Launch<TrBF16, RowdotCfg192>::template run<EPI_ROWDOT>(r, true, s)
-                 : Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
+  int rc;
+  if (sw)
+    rc = bm192 ? Launch<TrBF16, RowdotCfg192>::template run<EPI_ROWDOT_KS>(r, true, s)
+               : Launch<TrBF16, RC>::template run<EPI_ROWDOT_KS>(r, true, s);
+  else
+    rc = bm192 ? Launch<TrBF16, RowdotCfg192>::template run<EPI_ROWDOT>(r, true, s)
+               : Launch<TrBF16, RC>::template run<EPI_ROWDOT>(r, true, s);
   if (rc) return rc;
-  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{64}) : 0;
+  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{FINISH_GF}) : 0;
   const dim3 grid(static_cast<unsigned>(2 * b.n_t + gblocks));
   if (grad_dtype == GS_DTYPE_F32)
     hipLaunchKernelGGL(rowdot_bias_finish_kernel<float>, grid, dim3(256), 0, s, P, PB,
                        b.pl.n_mt, b.pl.p_ld, b.pl.cols, b.n_t, out_dot, out_bias_dot, BP,
-                       b.n_tiles, d_out, static_cast<float*>(out_bias_grad), grad_scale);
+                       b.bp_rows, d_out, static_cast<float*>(out_bias_grad), grad_scale);
   else
     hipLaunchKernelGGL(rowdot_bias_finish_kernel<uint16_t>, grid, dim3(256), 0, s, P, PB,
                        b.pl.n_mt, b.pl.p_ld, b.pl.cols, b.n_t, out_dot, out_bias_dot, BP,
-                       b.n_tiles, d_out, static_cast<uint16_t*>(out_bias_grad), grad_scale);
+                       b.bp_rows, d_out, static_cast<uint16_t*>(out_bias_grad), grad_scale);
   return check_launch("rowdot_bias_finish_kernel");
 }
 
@@ -2360,7 +2671,7 @@ extern "C" size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t 
   if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, GS_SEM_PAIRWISE_SUM, GS_ALGO_AUTO, 0))
     return 0;
   if (!rowdot_bias_ok(dtype, nullptr, nullptr, nullptr, N, T, d_in, d_out)) return 0;
-  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_in, d_out, false);
   Sizer sz;
   float *P, *PB, *BP;
   carve_rowdot_bias(sz, b, d_out, &P, &PB, &BP);
@@ -2384,7 +2695,7 @@ extern "C" int gs_linear_rowdot_bias(const void* A, const void* G, const void* V
     return fail(GS_ERR_UNSUPPORTED,
                 "gs_linear_rowdot_bias: needs bf16, 16-byte aligned operands below 2 GiB, "
                 "T a multiple of 256 and d_out a multiple of 192 or 256");
-  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_in, d_out, false);
   if (workspace == nullptr ||
       workspace_bytes < gs_linear_rowdot_bias_workspace(dtype, N, n_val, T, d_in, d_out) - 256)
     return fail(GS_ERR_WORKSPACE, "gs_linear_rowdot_bias: workspace too small");
@@ -2414,7 +2725,9 @@ namespace {
 bool bias_dot_ok(int dtype, const void* A, const void* G, int64_t N, int64_t n_val, int64_t T,
                  int64_t d_in, int64_t d_out, int presum) {
   return val_tn(dtype, n_val, T, d_in, d_out, presum) &&
-         rowdot_bias_ok(dtype, A, G, A, N, T, d_in, d_out);
+         (rowdot_bias_ok(dtype, A, G, A, N, T, d_in, d_out) ||
+          (bias_swap(dtype, N, T, d_in, d_out) &&
+           rowdot_bias_ok(dtype, A, G, A, N, T, d_out, d_in)));
 }
 template <class S>
 void carve_bias_dot(S& c, const RowdotBiasPlan& b, int64_t n_val, int64_t T, int64_t d_in,
@@ -2423,7 +2736,8 @@ void carve_bias_dot(S& c, const RowdotBiasPlan& b, int64_t n_val, int64_t T, int
   carve_rowdot_bias(c, b, d_out, P, PB, BP);
   const int64_t K = (presum ? 1 : n_val) * T;
   *V = c.template take<uint16_t>(d_out * d_in);
-  *VS = c.template take<float>(static_cast<int64_t>(tn_splits(K, d_out, d_in)) * d_out);
+  *VS = c.template take<float>(static_cast<int64_t>(tn_splits(K, d_out, d_in)) *
+                               std::min<int64_t>(TN_VPARTS, ceil_div(d_in, TnC::BN)) * d_out);
   *part = c.template take<float>(tn_part_elems(K, d_out, d_in));
   *abar = presum ? c.template take<uint16_t>(T * d_in) : nullptr;
   *gbar = presum ? c.template take<uint16_t>(T * d_out) : nullptr;
@@ -2436,7 +2750,7 @@ extern "C" size_t gs_linear_bias_dot_workspace(int dtype, int64_t N, int64_t n_v
   if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, GS_ALGO_AUTO, 0)) return 0;
   const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
   if (!bias_dot_ok(dtype, nullptr, nullptr, N, n_val, T, d_in, d_out, presum)) return 0;
-  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_in, d_out, true);
   Sizer sz;
   float *P, *PB, *BP, *VS, *part;
   void *V, *abar, *gbar;
@@ -2460,8 +2774,9 @@ extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64
   if (!bias_dot_ok(dtype, A, G, N, n_val, T, d_in, d_out, presum))
     return fail(GS_ERR_UNSUPPORTED,
                 "gs_linear_bias_dot: needs bf16, 16-byte aligned operands below 2 GiB, "
-                "T a multiple of 256 and d_out a multiple of 192 or 256");
-  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_out);
+                "T a multiple of 256 and d_out a multiple of 192 or 256 (or d_out > d_in "
+                "and d_in such a multiple)");
+  const RowdotBiasPlan b = plan_rowdot_bias(dtype, N, n_val, T, d_in, d_out, true);
   if (workspace == nullptr ||
       workspace_bytes <
           gs_linear_bias_dot_workspace(dtype, N, n_val, T, d_in, d_out, semantics) - 256)
@@ -2493,9 +2808,12 @@ extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64
     Lg = static_cast<const E*>(gbar);
   }
   const int64_t K = (presum ? 1 : n_val) * T;
-  rc = launch_tn(Lg, d_out, La, d_in, K, d_out, d_in, V, part, s, VS);
+  // V [d_out][d_in] = G_val^T A_val, or with swap V^T [d_in][d_out] = A_val^T G_val; VS holds
+  // the column sums of G_val either way.
+  rc = b.swap ? launch_tn(La, d_in, Lg, d_out, K, d_in, d_out, V, part, s, VS, true)
+              : launch_tn(Lg, d_out, La, d_in, K, d_out, d_in, V, part, s, VS);
   if (rc) return rc;
-  return launch_rowdot_bias(A, G, V, VS, tn_splits(K, d_out, d_in), N, n_val, val_start, T,
+  return launch_rowdot_bias(A, G, V, VS, 1, N, n_val, val_start, T,
                             d_in, d_out, b, P, PB, BP, out_dot, out_bias_dot, out_bias_grad,
                             grad_dtype, grad_scale, s);
 }

@@ -130,8 +130,9 @@ int gs_linear_rowdot(const void* A, const void* G, const void* V, int dtype, int
  *                     grad_dtype)
  * The row-dot epilogue sums each G tile it already holds in LDS over its tokens; those
  * column sums give both bias terms, so the train rows of G are read once.
- * Supported for bf16, 16-byte aligned operands below 2 GiB, T a multiple of 256 and d_out of 192 or 256:
- * the workspace query returns 0 otherwise (use gs_linear_rowdot + gs_bias_dot then). */
+ * Supported for bf16, 16-byte aligned operands below 2 GiB, T a multiple of 256 and d_out a
+ * multiple of 192 or 256: the workspace query returns 0 otherwise (use gs_linear_rowdot +
+ * gs_bias_dot then). */
 size_t gs_linear_rowdot_bias_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
                                        int64_t d_in, int64_t d_out);
 int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype, int64_t N,
@@ -141,13 +142,16 @@ int gs_linear_rowdot_bias(const void* A, const void* G, const void* V, int dtype
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* The whole Linear sampler with a bias in one call (weight dot, bias dot, bias train
- * gradient), for the semantics of gs_linear_dot: the K-major GEMM forms V (its N-tile-0
- * workgroups also sum the val rows of G: the val bias gradient), then the row-dot + bias pass
- * of gs_linear_rowdot_bias.  Reference: _compute_linear_dot_product weight and bias parts
+ * gradient), for the semantics of gs_linear_dot: the K-major GEMM forms V (its workgroups
+ * also sum the val rows of G: the val bias gradient), then the row-dot + bias pass of
+ * gs_linear_rowdot_bias.  With d_out > d_in the pass contracts over d_out instead
+ * (sum_t <a_it, V^T g_it>, V^T formed by the K-major GEMM) and takes the bias column sums of
+ * G from its mainloop.  Reference: _compute_linear_dot_product weight and bias parts
  * (supported_layers_grad_samplers_dotprod.py:75-146), Conv1D (:369-471), and
- * _compute_train_grad_bias (autograd_grad_sample_dotprod.py:199-222).  Same shape limits as
- * gs_linear_rowdot_bias (the workspace query returns 0 outside them; use gs_linear_dot and
- * gs_bias_dot then). */
+ * _compute_train_grad_bias (autograd_grad_sample_dotprod.py:199-222).  Supported for bf16,
+ * 16-byte aligned operands below 2 GiB, T a multiple of 256 and d_out a multiple of 192 or
+ * 256, or d_out > d_in with d_in such a multiple (the workspace query returns 0 otherwise; use
+ * gs_linear_dot and gs_bias_dot then). */
 size_t gs_linear_bias_dot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
                                     int64_t d_in, int64_t d_out, int semantics);
 int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,

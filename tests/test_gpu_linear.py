@@ -30,6 +30,14 @@ def _inputs(N, T, d_in, d_out, seed, dtype):
     return A, G
 
 
+@pytest.fixture
+def v_gemm_native():
+    saved = _native.V_GEMM
+    _native.V_GEMM = "native"
+    yield
+    _native.V_GEMM = saved
+
+
 @pytest.fixture(params=["library", "native"])
 def v_gemm(request):
     saved = _native.V_GEMM
@@ -142,7 +150,8 @@ def test_linear_rowdot_with_given_v(gpu, shape, dtype):
 def test_linear_auto_picks_cheaper_algorithm(gpu):
     ops = _native.ops()
     # microbench T=1024: ghost 1.5 TF vs val-gradient 0.15 TF
-    assert ops.linear_algo(torch.bfloat16, 32, 8, 1024, 768, 3072, 0, 0, False) == _native.ALGO_VALGRAD
+    assert ops.linear_algo(torch.bfloat16, 32, 8, 1024, 768, 3072, 0, 0,
+                           False) == _native.ALGO_VALGRAD
     # tiny T with big layers: ghost
     assert ops.linear_algo(torch.bfloat16, 20, 4, 4, 1024, 4096, 0, 0, False) == _native.ALGO_GHOST
 
@@ -232,6 +241,43 @@ def test_rowdot_192_row_tiles(gpu, shape, semantics):
     want = R.linear_dot_exact(A, G, n_val, semantics)
     assert_close(dot.cpu(), want, BF16_TOL, "weight dot")
     assert_close(dot2.cpu(), want, BF16_TOL, "weight dot (fused)")
+    assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
+    assert_close(bgrad.cpu(), R.bias_train_grad(G.double() * N, n_val), BF16_TOL, "bias grad")
+
+
+@pytest.mark.parametrize("shape", [(12, 4, 256, 768, 3072), (6, 2, 256, 256, 1000),
+                                   (6, 2, 512, 1280, 1536)])
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_valgrad_over_d_out(gpu, v_gemm_native, shape, semantics):
+    """d_out > d_in: the val-gradient row-dot runs over K = d_out (V^T, Z = the train rows of
+    A) and the fused bias pass sums the train rows of G inside its mainloop.  192-row tiles
+    over d_in 768 (each token tile's rows split 64/64/64/64 over 4 workgroups); one 256-row
+    tile (all 256 rows in one workgroup) with a K tail of 40; five 256-row tiles (rows split
+    52/52/52/52/48).  Val rows first and last; per-pair values for the pairwise sum."""
+    N, n_val, T, d_in, d_out = shape
+    A, G = _inputs(N, T, d_in, d_out, 700 + d_in, torch.bfloat16)
+    sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
+    ops = _native.ops()
+    for val_start in (N - n_val, 0):
+        print(f"valgrad over d_out shape={shape} sem={semantics} val_start={val_start}",
+              flush=True)
+        pair = semantics == "pairwise"
+        dot, prs = ops.linear_dot(A.to(gpu), G.to(gpu), n_val, val_start=val_start,
+                                  semantics=sem, algo=_native.ALGO_VALGRAD, want_pair=pair)
+        torch.cuda.synchronize()
+        want = R.linear_dot_exact(A, G, n_val, semantics, val_start=val_start)
+        assert_close(dot.cpu(), want, BF16_TOL, "weight dot")
+        if pair:
+            assert_close(prs.cpu(), R.linear_dot_exact(A, G, n_val, "pairwise",
+                                                       val_start=val_start, pair=True),
+                         BF16_TOL, "pair")
+    # The fused weight + bias pass (gs_linear_bias_dot, val rows last).
+    dot2, bdot, bgrad = ops.linear_bias_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem,
+                                            algo=_native.ALGO_VALGRAD,
+                                            grad_scale=N / (N - n_val), grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(dot2.cpu(), R.linear_dot_exact(A, G, n_val, semantics), BF16_TOL,
+                 "weight dot (fused)")
     assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
     assert_close(bgrad.cpu(), R.bias_train_grad(G.double() * N, n_val), BF16_TOL, "bias grad")
 

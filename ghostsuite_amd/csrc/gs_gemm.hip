@@ -506,12 +506,14 @@ struct KsState {
   float* row;   // this workgroup's row of kbp (K floats)
   float* wsum;  // LDS [3][NW][64]
   int r0, r1;   // R rows of each stage this workgroup sums
+  int off[8];   // this lane's byte offsets (within a stage) of its first-pass rows
+  bool whole;   // the first pass has 8 rows for every wave
 };
 // Rows go in passes of 8 per wave (8 NW rows per workgroup); rows past r1 read a row inside
 // the stage and add nothing.
+// Byte offsets within a stage of this lane's reads of rows base + wid + NW j.
 template <class C, class D>
-__device__ __forceinline__ void ks_load(const unsigned char* stage, const KsState& ks, int base,
-                                        uint32_t (&v)[8]) {
+__device__ __forceinline__ void ks_offsets(const KsState& ks, int base, int (&off)[8]) {
   constexpr int NW = C::WM * C::WN;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int c = (lane >> 3) & (D::CH - 1), e = (lane & 7) * 2;
@@ -520,9 +522,21 @@ __device__ __forceinline__ void ks_load(const unsigned char* stage, const KsStat
   for (int j = 0; j < 8; ++j) {
     const int r = base + wid + NW * j;
     const int sr = C::BM + (r < ks.r1 ? r : rsafe);
-    v[j] = *reinterpret_cast<const uint16_t*>(stage + sr * D::ROW_BYTES +
-                                              ((c ^ D::swz(sr)) * 16) + e);
+    off[j] = sr * D::ROW_BYTES + ((c ^ D::swz(sr)) * 16) + e;
   }
+}
+template <class C, class D>
+__device__ __forceinline__ void ks_load_at(const unsigned char* stage, const int (&off)[8],
+                                           uint32_t (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const uint16_t*>(stage + off[j]);
+}
+template <class C, class D>
+__device__ __forceinline__ void ks_load(const unsigned char* stage, const KsState& ks, int base,
+                                        uint32_t (&v)[8]) {
+  int off[8];
+  ks_offsets<C, D>(ks, base, off);
+  ks_load_at<C, D>(stage, off, v);
 }
 template <class C, class D>
 __device__ __forceinline__ void ks_stage(const unsigned char* stage, const KsState& ks, int buf,
@@ -534,9 +548,14 @@ __device__ __forceinline__ void ks_stage(const unsigned char* stage, const KsSta
   // included (read after the next barrier).
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   float s = 0.f;
+  if (ks.whole) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (ks.r0 + wid + NW * j < ks.r1) s += __uint_as_float(v0[j] << 16);
+    for (int j = 0; j < 8; ++j) s += __uint_as_float(v0[j] << 16);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (ks.r0 + wid + NW * j < ks.r1) s += __uint_as_float(v0[j] << 16);
+  }
   for (int base = ks.r0 + 8 * NW; base < ks.r1; base += 8 * NW) {
     uint32_t v[8];
     ks_load<C, D>(stage, ks, base, v);
@@ -642,7 +661,7 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
     if constexpr (KS) {
       if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
       if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
-      ks_load<C, D>(slot(kt), *ks, ks->r0, kv);
+      ks_load_at<C, D>(slot(kt), ks->off, kv);
       // Keep these reads out of the MFMA stream's fragment-read schedule.
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -659,7 +678,7 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
     if constexpr (KS) {
       if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
       if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
-      ks_load<C, D>(slot(kt), *ks, ks->r0, kv);
+      ks_load_at<C, D>(slot(kt), ks->off, kv);
       // Keep these reads out of the MFMA stream's fragment-read schedule.
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1008,7 +1027,9 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
     const int64_t r0 = mt * rpw < C::BN ? mt * rpw : C::BN;
     const int64_t r1 = r0 + rpw < C::BN ? r0 + rpw : C::BN;
     float* row = p.kbp + (mt * p.n_tiles + nt) * p.K1;
-    const KsState ks{row, ks_wsum, static_cast<int>(r0), static_cast<int>(r1)};
+    KsState ks{row, ks_wsum, static_cast<int>(r0), static_cast<int>(r1), {},
+               r1 - r0 >= 8 * C::WM * C::WN};
+    ks_offsets<C, D>(ks, ks.r0, ks.off);
     ks_row = row;
     ks_last = mainloop_dma<C, D, true>(p.L1, p.R1, mt, nt, p.K1, l, acc, &ks);
   } else {

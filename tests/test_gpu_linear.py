@@ -246,14 +246,16 @@ def test_rowdot_192_row_tiles(gpu, shape, semantics):
 
 
 @pytest.mark.parametrize("shape", [(12, 4, 256, 768, 3072), (6, 2, 256, 256, 1000),
-                                   (6, 2, 512, 1280, 1536)])
+                                   (6, 2, 512, 1280, 1536), (82, 2, 256, 768, 1024)])
 @pytest.mark.parametrize("semantics", ["pairwise", "presum"])
 def test_valgrad_over_d_out(gpu, v_gemm_native, shape, semantics):
     """d_out > d_in: the val-gradient row-dot runs over K = d_out (V^T, Z = the train rows of
     A) and the fused bias pass sums the train rows of G inside its mainloop.  192-row tiles
     over d_in 768 (each token tile's rows split 64/64/64/64 over 4 workgroups); one 256-row
-    tile (all 256 rows in one workgroup) with a K tail of 40; five 256-row tiles (rows split
-    52/52/52/52/48).  Val rows first and last; per-pair values for the pairwise sum."""
+    tile (all 256 rows in one workgroup, four passes of 64) with a K tail of 40; five 256-row
+    tiles (rows split 52/52/52/52/48); three 256-row tiles over 80 token tiles (rows split
+    86/86/84: a whole first pass and a partial second one).  Val rows first and last; per-pair
+    values for the pairwise sum."""
     N, n_val, T, d_in, d_out = shape
     A, G = _inputs(N, T, d_in, d_out, 700 + d_in, torch.bfloat16)
     sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM

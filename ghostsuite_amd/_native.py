@@ -252,7 +252,7 @@ class HipOps:
         _check(rc, "gs_linear_val_gradient")
         return V
 
-    def linear_bias_dot(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
+    def linear_bias_dot(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *, val_start=None,
                         semantics: int = SEM_PAIRWISE_SUM, algo: int = ALGO_AUTO,
                         rounding: int = ROUND_FP32, grad_scale: Optional[float] = None,
                         grad_dtype: Optional[torch.dtype] = None):
@@ -260,7 +260,8 @@ class HipOps:
         grad_scale is given) in one pass over the train rows when the shape allows it: the
         val-gradient algorithm through gs_linear_bias_dot, or, for the pairwise semantics with
         the library V GEMM, torch.mm for V and gs_linear_rowdot_bias.  Otherwise None (the
-        caller then uses linear_dot and bias_dot).  Returns (dot, bias_dot, bias_grad)."""
+        caller then uses linear_dot and bias_dot).  The val rows are [val_start, val_start +
+        n_val) (default: the last n_val rows).  Returns (dot, bias_dot, bias_grad)."""
         dev = _require_device(A, G)
         if A.dtype != G.dtype or A.dtype != torch.bfloat16 or \
                 semantics not in (SEM_PAIRWISE_SUM, SEM_PRESUM) or \
@@ -270,7 +271,8 @@ class HipOps:
         d_in, d_out = A.shape[-1], G.shape[-1]
         T = _tokens(A, N, d_in)
         n_t = N - n_val
-        if n_t <= 0 or _tokens(G, N, d_out) != T:
+        vs = N - n_val if val_start is None else int(val_start)
+        if n_t <= 0 or _tokens(G, N, d_out) != T or not 0 <= vs <= N - n_val:
             return None
         dt = _gs_dtype(A)
         lib = load_library()
@@ -285,15 +287,14 @@ class HipOps:
             return None
         A = A.contiguous()
         G = G.contiguous()
-        vs = N - n_val
         ws = _workspace(ws_bytes, dev)
         out = torch.empty(n_t, dtype=torch.float32, device=dev)
         bout = torch.empty(n_t, dtype=torch.float32, device=dev)
         gdt = grad_dtype or G.dtype
         grad = torch.empty(d_out, dtype=gdt, device=dev) if grad_scale is not None else None
         if library_v:
-            Av = A.view(N, T, d_in)[vs:]
-            Gv = G.view(N, T, d_out)[vs:]
+            Av = A.view(N, T, d_in)[vs:vs + n_val]
+            Gv = G.view(N, T, d_out)[vs:vs + n_val]
             V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
             rc = lib.gs_linear_rowdot_bias(A.data_ptr(), G.data_ptr(), V.data_ptr(), dt, N,
                                            n_val, vs, T, d_in, d_out, out.data_ptr(),

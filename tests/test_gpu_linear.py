@@ -273,15 +273,19 @@ def test_valgrad_over_d_out(gpu, v_gemm_native, shape, semantics):
             assert_close(prs.cpu(), R.linear_dot_exact(A, G, n_val, "pairwise",
                                                        val_start=val_start, pair=True),
                          BF16_TOL, "pair")
-    # The fused weight + bias pass (gs_linear_bias_dot, val rows last).
-    dot2, bdot, bgrad = ops.linear_bias_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem,
-                                            algo=_native.ALGO_VALGRAD,
-                                            grad_scale=N / (N - n_val), grad_dtype=torch.float32)
-    torch.cuda.synchronize()
-    assert_close(dot2.cpu(), R.linear_dot_exact(A, G, n_val, semantics), BF16_TOL,
-                 "weight dot (fused)")
-    assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
-    assert_close(bgrad.cpu(), R.bias_train_grad(G.double() * N, n_val), BF16_TOL, "bias grad")
+    # The fused weight + bias pass (gs_linear_bias_dot), val rows last and in the middle.
+    for val_start in (N - n_val, 1):
+        dot2, bdot, bgrad = ops.linear_bias_dot(A.to(gpu), G.to(gpu), n_val, val_start=val_start,
+                                                semantics=sem, algo=_native.ALGO_VALGRAD,
+                                                grad_scale=N / (N - n_val),
+                                                grad_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert_close(dot2.cpu(), R.linear_dot_exact(A, G, n_val, semantics, val_start=val_start),
+                     BF16_TOL, "weight dot (fused)")
+        assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val, val_start=val_start), BF16_TOL,
+                     "bias dot")
+        tr = torch.cat([G[:val_start], G[val_start + n_val:]]).double()
+        assert_close(bgrad.cpu(), tr.sum((0, 1)) * N / (N - n_val), BF16_TOL, "bias grad")
 
 
 def test_linear_bias_fused_declines_unsupported_shapes(gpu):

@@ -509,9 +509,9 @@ struct KsState {
   int off[8];   // this lane's byte offsets (within a stage) of its first-pass rows
   bool whole;   // the first pass has 8 rows for every wave
 };
-// Rows go in passes of 8 per wave (8 NW rows per workgroup); rows past r1 read a row inside
-// the stage and add nothing.
-// Byte offsets within a stage of this lane's reads of rows base + wid + NW j.
+// Rows go in passes of 8 per wave (8 NW rows per workgroup): byte offsets within a stage of
+// this lane's reads of rows base + wid + NW j; rows past r1 read a row inside the stage (and
+// ks_stage adds nothing for them).
 template <class C, class D>
 __device__ __forceinline__ void ks_offsets(const KsState& ks, int base, int (&off)[8]) {
   constexpr int NW = C::WM * C::WN;

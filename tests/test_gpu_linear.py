@@ -288,6 +288,36 @@ def test_valgrad_over_d_out(gpu, v_gemm_native, shape, semantics):
         assert_close(bgrad.cpu(), tr.sum((0, 1)) * N / (N - n_val), BF16_TOL, "bias grad")
 
 
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_valgrad_over_d_out_unaligned_operands(gpu, semantics):
+    """bf16 operands 2 bytes past a 16-byte boundary (through the C ABI; the wrapper would copy
+    them): the val-gradient pass takes the transposed-operand path (STORE GEMM for V^T,
+    element loads in the row-dot and its epilogue), still over K = d_out."""
+    N, n_val, T, d_in, d_out = 6, 2, 64, 64, 160
+    A, G = _inputs(N, T, d_in, d_out, 900, torch.bfloat16)
+    sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
+    lib = _native.load_library()
+    bufs = []
+    for t in (A, G):
+        b = torch.zeros(t.numel() + 8, dtype=torch.bfloat16, device=gpu)
+        b[1:1 + t.numel()] = t.reshape(-1).to(gpu)
+        bufs.append(b)
+    dev = torch.device(gpu)
+    ws_bytes = lib.gs_linear_dot_workspace(_native.DTYPE_BF16, N, n_val, T, d_in, d_out, sem,
+                                           _native.ALGO_VALGRAD, 0)
+    assert ws_bytes > 0
+    ws = _native._workspace(ws_bytes, dev)
+    out = torch.empty(N - n_val, dtype=torch.float32, device=gpu)
+    print(f"valgrad unaligned sem={semantics}", flush=True)
+    rc = lib.gs_linear_dot(bufs[0].data_ptr() + 2, bufs[1].data_ptr() + 2, _native.DTYPE_BF16,
+                           N, n_val, N - n_val, T, d_in, d_out, sem, _native.ALGO_VALGRAD,
+                           _native.ROUND_FP32, out.data_ptr(), None, ws.data_ptr(), ws_bytes,
+                           _native._stream(dev))
+    assert rc == 0, lib.gs_last_error()
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), R.linear_dot_exact(A, G, n_val, semantics), BF16_TOL, "dot")
+
+
 def test_linear_bias_fused_declines_unsupported_shapes(gpu):
     ops = _native.ops()
     A, G = _inputs(6, 100, 64, 256, 5, torch.bfloat16)        # T not a multiple of 256

@@ -544,17 +544,12 @@ __device__ __forceinline__ void ks_stage(const unsigned char* stage, const KsSta
   constexpr int NW = C::WM * C::WN;
   static_assert(D::KB <= 64 && D::KB == 8 * NW, "one feature per lane, 8 per wave");
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  // Every LDS access of this wave so far has completed, the previous stage's wsum write
-  // included (read after the next barrier).
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // First pass branch-free (selects), so the adds can share the MFMAs' basic block.
   float s = 0.f;
-  if (ks.whole) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += __uint_as_float(v0[j] << 16);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (ks.r0 + wid + NW * j < ks.r1) s += __uint_as_float(v0[j] << 16);
+  for (int j = 0; j < 8; ++j) {
+    const float x = __uint_as_float(v0[j] << 16);
+    s += (ks.whole || ks.r0 + wid + NW * j < ks.r1) ? x : 0.f;
   }
   for (int base = ks.r0 + 8 * NW; base < ks.r1; base += 8 * NW) {
     uint32_t v[8];
@@ -563,6 +558,9 @@ __device__ __forceinline__ void ks_stage(const unsigned char* stage, const KsSta
     for (int j = 0; j < 8; ++j)
       if (base + wid + NW * j < ks.r1) s += __uint_as_float(v[j] << 16);
   }
+  // Every LDS access of this wave so far has completed, the previous stage's wsum write
+  // included (read after the next barrier).
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   ks.wsum[(buf * NW + wid) * 64 + lane] = lane < D::KB ? s : 0.f;
 }
 template <class C, class D>
@@ -666,10 +664,8 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
       __builtin_amdgcn_sched_barrier(0);
     }
     dma_compute<C, D>(slot(kt), acc);
-    if constexpr (KS) {
-      __builtin_amdgcn_sched_barrier(0);
-      ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
-    }
+    // The adds of ks_stage may interleave with the MFMAs above (they read only kv).
+    if constexpr (KS) ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
   }
   // Tail: no more loads; the stages still in flight drain one by one.
   for (; kt < nk; ++kt) {
@@ -683,10 +679,8 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
       __builtin_amdgcn_sched_barrier(0);
     }
     dma_compute<C, D>(slot(kt), acc);
-    if constexpr (KS) {
-      __builtin_amdgcn_sched_barrier(0);
-      ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
-    }
+    // The adds of ks_stage may interleave with the MFMAs above (they read only kv).
+    if constexpr (KS) ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
   }
   if constexpr (KS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   wait_vmcnt<0>();

@@ -299,6 +299,9 @@ constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
 #ifndef GS_WIDE_DMA
 #define GS_WIDE_DMA 128, 2
 #endif
+#ifndef GS_TN_SCHED
+#define GS_TN_SCHED 1
+#endif
 #ifndef GS_PF
 #define GS_PF 1
 #endif
@@ -1548,6 +1551,22 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
         acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks % NB][i], fb[ks % NB][jj],
                                                              acc[i][jj], 0, 0, 0);
   }
+#if GS_TN_SCHED
+  // Instruction order: the first k-step's transpose reads, then each k-step's MFMAs with the
+  // next k-step's reads (two per fragment) spread between them.
+  constexpr int RD = 2 * (C::MI + C::NI), M = C::MI * C::NI;
+  static_assert(RD % M == 0, "reads per MFMA");
+  __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+#pragma unroll
+  for (int ks = 0; ks + 1 < D::KSTEPS; ++ks) {
+#pragma unroll
+    for (int g = 0; g < M; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, RD / M, 0);
+    }
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, M, 0);
+#endif
 }
 
 // acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same

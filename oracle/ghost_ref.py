@@ -100,15 +100,6 @@ def linear_pair_ref(A: torch.Tensor, B: torch.Tensor, n_val: int) -> torch.Tenso
     return out
 
 
-def per_sample_linear_grads(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    """G_n = sum_t b_nt a_nt^T  [N, d_out, d_in] in float64 (the textbook per-sample grad)."""
-    N = A.shape[0]
-    d, p = A.shape[-1], B.shape[-1]
-    a = A.double().reshape(N, -1, d)
-    b = B.double().reshape(N, -1, p)
-    return torch.einsum('ntp,ntd->npd', b, a)
-
-
 def val_term_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, semantics: str = "pairwise",
                    val_start: Optional[int] = None) -> torch.Tensor:
     """The val term V [d_out, d_in] (float64) the two semantics dot the train gradients with:
@@ -146,6 +137,34 @@ def linear_dot_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, semantics: st
     if semantics == "presum" and pair:
         raise ValueError("presum has no per-pair form")
     return torch.einsum('ipd,pd->i', G_tr, val_term_exact(A, B, n_val, semantics, val_start))
+
+
+def linear_dot_valterm_exact(A: torch.Tensor, B: torch.Tensor, n_val: int,
+                             semantics: str = "pairwise",
+                             val_start: Optional[int] = None) -> torch.Tensor:
+    """The linear_dot_exact vector through the val term: dot_i = sum_t b_it^T V a_it with V
+    from val_term_exact, since <sum_t b_it a_it^T, V>_F = sum_t b_it^T V a_it.  Float64,
+    with 2-D products only and one train row at a time, so that it runs at full model sizes
+    on whichever device holds A and B (no [n_train, d_out, d_in] tensor is formed)."""
+    N = A.shape[0]
+    d, p = A.shape[-1], B.shape[-1]
+    a = A.reshape(N, -1, d)
+    b = B.reshape(N, -1, p)
+    vs = N - n_val if val_start is None else val_start
+    va_a = a[vs:vs + n_val].double()
+    va_b = b[vs:vs + n_val].double()
+    if semantics == "pairwise":
+        V = torch.mm(va_b.reshape(-1, p).t(), va_a.reshape(-1, d))
+    elif semantics == "presum":
+        V = torch.mm(va_b.sum(0).t(), va_a.sum(0))
+    else:
+        raise ValueError(semantics)
+    del va_a, va_b
+    rows = [i for i in range(N) if not vs <= i < vs + n_val]
+    out = torch.empty(len(rows), dtype=torch.float64, device=A.device)
+    for k, i in enumerate(rows):
+        out[k] = (torch.mm(b[i].double(), V) * a[i].double()).sum()
+    return out
 
 
 def bias_dot_exact(B: torch.Tensor, n_val: int, val_start: Optional[int] = None) -> torch.Tensor:
@@ -375,6 +394,26 @@ def kron_proj_exact(A: torch.Tensor, B: torch.Tensor, P_i: torch.Tensor, P_o: to
         # Conv1D: rows of P_i act on the output-grad side, P_o on the input side.
         return scale * torch.einsum('ip,bpd,od->bio', P_i.double(), Gs, P_o.double())
     return scale * torch.einsum('op,bpd,id->boi', P_o.double(), Gs, P_i.double())
+
+
+def kron_proj_projfirst_exact(A: torch.Tensor, B: torch.Tensor, P_i: torch.Tensor,
+                              P_o: torch.Tensor, scale: float,
+                              conv1d: bool = False) -> torch.Tensor:
+    """kron_proj_exact with the projections applied first: per sample
+    scale * (B_b P_o^T)^T (A_b P_i^T) = scale * P_o (sum_t b a^T) P_i^T (Conv1D: P_i on the
+    output-grad side, [k_i, k_o]).  Float64, 2-D products one sample at a time, so that it
+    runs at full model sizes on whichever device holds A and B."""
+    A3 = flatten_tokens(A)
+    B3 = flatten_tokens(B)
+    Pl, Pr = (P_i, P_o) if conv1d else (P_o, P_i)
+    Pl = Pl.double().to(A3.device)
+    Pr = Pr.double().to(A3.device)
+    outs = []
+    for b in range(A3.shape[0]):
+        left = torch.mm(B3[b].double(), Pl.t())     # [T, k_o] (Conv1D: [T, k_i])
+        right = torch.mm(A3[b].double(), Pr.t())    # [T, k_i] (Conv1D: [T, k_o])
+        outs.append(scale * torch.mm(left.t(), right))
+    return torch.stack(outs)
 
 
 def kron_embed_proj_ref(ids: torch.Tensor, g: torch.Tensor, P_i: torch.Tensor,

@@ -1,0 +1,355 @@
+"""GPU parity at the stated size of every BASELINE configuration, through the reference API
+and the C ABI, against the oracle's closed forms.
+
+  configs[0]  MLP 512-1024-1024-10, fp32, 64 train + 16 val rows, 10 SGD steps
+  configs[1]  Linear microbench A[32, T, 768], G[32, T, 3072], 8 val rows first,
+              T in {128, 512, 1024, 2048}, both algorithms
+  configs[2]  GPT-2-small, 12 layers, bf16, 16 + 4 rows, T = 1024: every hooked module's
+              dots and every .grad of one step
+  configs[3]  GradProj on the GPT-2-medium shape, B = 32, T = 1024, k = 16 x 16
+  configs[4]  Pythia-1B shape, 8 + 2 rows, T = 2048: every hooked module (embed_out's
+              output gradient is 2.06 GB) and every .grad of one step
+
+The expected values are the oracle's float64 closed forms evaluated on the tensors the
+samplers received (captured by hooks of this test), on the GPU where the sizes need it
+(2-D float64 products only).  Tolerances: bf16 operands 2e-2 normwise, fp32 operands 1e-4
+normwise (|x - y| <= tol * max(|y|, rms(y))); routing (which parameter receives which
+result) exact.
+"""
+import copy
+
+import pytest
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ghostsuite_amd import GradDotProdEngine, GradProjLoraEngine, _native
+from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+from ghostsuite_amd.workloads import (CausalLM, GPT2_MEDIUM, GPT2_SMALL, MLP, PYTHIA_1B,
+                                      synthetic_tokens)
+from oracle import brute
+from oracle import ghost_ref as R
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, gen, randn
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+
+
+@pytest.fixture(autouse=True)
+def _reset_options():
+    saved = dict(S.options)
+    yield
+    S.options.clear()
+    S.options.update(saved)
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+class HookCapture:
+    """Keeps every sampled module's input and output gradient (the A and B its sampler
+    receives), by hooks registered after the engine's."""
+
+    def __init__(self, model, types, names=None):
+        self.A, self.B, self.handles = {}, {}, []
+        for name, m in model.named_modules():
+            if type(m) in types and (names is None or name in names):
+                self.handles.append(m.register_forward_hook(self._fwd(name)))
+                self.handles.append(m.register_full_backward_hook(self._bwd(name)))
+
+    def _fwd(self, name):
+        def hook(m, inp, out):
+            self.A[name] = inp[0].detach()
+        return hook
+
+    def _bwd(self, name):
+        def hook(m, gin, gout):
+            self.B[name] = gout[0].detach()
+        return hook
+
+    def remove(self):
+        for h in self.handles:
+            h.remove()
+
+
+def _param_names(model):
+    return {id(p): n for n, p in model.named_parameters()}
+
+
+def _train_rows(x, n_t):
+    return x[:n_t].reshape(-1, x.shape[-1])
+
+
+def _expected_lm(model, cap, n_t, n_v):
+    """{param name: expected dot} and {param name: expected .grad}, float64 on the device."""
+    N = n_t + n_v
+    s = N / n_t   # the train grads average the N-scaled backprops over the train rows
+    names = _param_names(model)
+    dots, grads = {}, {}
+
+    def add(name, g):
+        grads[name] = grads[name] + g if name in grads else g
+
+    for mname, m in model.named_modules():
+        if mname not in cap.A:
+            continue
+        A, B = cap.A[mname], cap.B[mname]
+        wname = names[id(m.weight)]
+        if isinstance(m, nn.Linear):
+            tied = wname != f"{mname}.weight"
+            if not tied:
+                sem = "pairwise" if m.use_ghost_computation else "presum"
+                dots[wname] = R.linear_dot_valterm_exact(A, B, n_v, sem)
+            add(wname, s * torch.mm(_train_rows(B, n_t).double().t(),
+                                    _train_rows(A, n_t).double()))
+            if m.bias is not None:
+                dots[names[id(m.bias)]] = R.bias_dot_exact(B, n_v)
+                add(names[id(m.bias)], s * _train_rows(B, n_t).double().sum(0))
+        elif isinstance(m, nn.Embedding):
+            dots[wname] = R.embedding_dot_exact(A, B, n_v)
+            g = torch.zeros(m.weight.shape, dtype=torch.float64, device=B.device)
+            g.index_add_(0, A[:n_t].reshape(-1).long(), _train_rows(B, n_t).double())
+            add(wname, s * g)
+        elif isinstance(m, nn.LayerNorm):
+            dw, db = R.layernorm_dot_exact(A, B, n_v, m.eps)
+            dots[wname], dots[names[id(m.bias)]] = dw, db
+            xh = F.layer_norm(_train_rows(A, n_t).double(), (A.shape[-1],), eps=m.eps)
+            add(wname, s * (_train_rows(B, n_t).double() * xh).sum(0))
+            add(names[id(m.bias)], s * _train_rows(B, n_t).double().sum(0))
+    return dots, grads
+
+
+def _lm_step(model, X, Y, n_t, n_v, **options):
+    """One GradDotProd step through the engine (the reference's step order); returns the
+    per-parameter dots, the .grad values, the logged aggregate and the capture."""
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True, **options)
+    eng.attach(opt)
+    cap = HookCapture(model, tuple(S._supported_layers_dotprod))
+    eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+    model(X, Y).backward()
+    torch.cuda.synchronize()
+    dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    eng.prepare_gradients()
+    grads = {n: p.grad for n, p in model.named_parameters()
+             if p.grad is not None and "dummy_bias" not in n}
+    eng.aggregate_and_log()
+    total = eng.dot_product_log[-1]["dot_product"]
+    cap.remove()
+    return eng, dots, grads, total, cap
+
+
+def _check_lm(model, dots, grads, total, cap, n_t, n_v):
+    want_dots, want_grads = _expected_lm(model, cap, n_t, n_v)
+    assert sorted(dots) == sorted(want_dots), (sorted(dots), sorted(want_dots))
+    for name in sorted(want_dots):
+        _say(f"  dot {name}")
+        assert_close(dots[name], want_dots[name], BF16_TOL, f"dot {name}")
+    assert_close(total, sum(want_dots.values()), BF16_TOL, "logged aggregate")
+    trainable = sorted(n for n, p in model.named_parameters()
+                       if p.initially_requires_grad and "dummy_bias" not in n)
+    assert sorted(grads) == trainable and sorted(want_grads) == trainable
+    for name in trainable:
+        _say(f"  grad {name}")
+        assert_close(grads[name], want_grads[name], BF16_TOL, f"grad {name}")
+
+
+# ------------------------------------------------------------------ configs[1]
+@pytest.mark.parametrize("T", [128, 512, 1024, 2048])
+def test_config1_linear_microbench(gpu, T):
+    """A[32, T, 768] ~ N(0, 1), G[32, T, 3072] ~ N(0, 1e-3^2), bf16, the first 8 rows val.
+    The reference's switch picks pairwise for T <= 1024 and presum at T = 2048; both
+    semantics run through both algorithms at every T."""
+    n_val, d_in, d_out = 8, 768, 3072
+    A = randn((32, T, d_in), 1234, 1.0, BF16).to(gpu)
+    G = randn((32, T, d_out), 1235, 1e-3, BF16).to(gpu)
+    assert R.should_use_ghost(T, d_in * d_out) == (T <= 1024)
+    for sem_name, sem in (("pairwise", _native.SEM_PAIRWISE_SUM),
+                          ("presum", _native.SEM_PRESUM)):
+        want = R.linear_dot_valterm_exact(A, G, n_val, sem_name, val_start=0)
+        for algo in (_native.ALGO_GHOST, _native.ALGO_VALGRAD):
+            _say(f"config1 T={T} sem={sem_name} algo={_native.ALGO_NAMES[algo]}")
+            dot, _ = _native.ops().linear_dot(A, G, n_val, val_start=0, semantics=sem,
+                                              algo=algo)
+            torch.cuda.synchronize()
+            assert_close(dot, want, BF16_TOL, f"T={T} {sem_name} {algo}")
+
+
+def test_config1_reference_sequence_t1024(gpu):
+    """The reference's own bf16 op sequence of the ghost branch (bf16 Gram products, bf16
+    Hadamard product, fp32 sums; 2-D products on the GPU) at the T = 1024 microbench, with
+    the reference layout (val last): the default kernels at 2e-2, the ghost kernel in its
+    reference-rounding mode at 2e-3."""
+    n_val, T = 8, 1024
+    A = randn((32, T, 768), 1240, 1.0, BF16).to(gpu)
+    G = randn((32, T, 3072), 1241, 1e-3, BF16).to(gpu)
+    want, _ = R.linear_dot_ref(A, G, n_val, use_ghost=True, has_bias=False)
+    torch.cuda.synchronize()
+    for algo in (_native.ALGO_GHOST, _native.ALGO_VALGRAD):
+        _say(f"config1 reference sequence algo={_native.ALGO_NAMES[algo]}")
+        dot, _ = _native.ops().linear_dot(A, G, n_val, algo=algo)
+        torch.cuda.synchronize()
+        assert_close(dot, want, BF16_TOL, f"ref sequence {algo}")
+    dot, _ = _native.ops().linear_dot(A, G, n_val, algo=_native.ALGO_GHOST,
+                                      rounding=_native.ROUND_REF_BF16)
+    torch.cuda.synchronize()
+    assert_close(dot, want, 2e-3, "ghost reference rounding")
+
+
+# ------------------------------------------------------------------ configs[0]
+@pytest.mark.parametrize("precision,tol", [("fp32", FP32_TOL), ("reference", BF16_TOL)])
+def test_config0_mlp_ten_steps(gpu, precision, tol):
+    """Linear 512 -> 1024 -> ReLU -> 1024 -> ReLU -> 10, fp32, 64 train + 16 val rows,
+    x ~ N(0, 1), labels uniform over 10 classes, mean cross-entropy, SGD lr 0.1, 10 steps:
+    every layer's dots per step and the weights after every step against per-sample
+    gradients of a float64 copy (one backward per sample)."""
+    torch.manual_seed(0)
+    model = MLP((512, 1024, 1024, 10))
+    ref = copy.deepcopy(model).double()
+    model = model.to(gpu)
+    n_t, n_v = 64, 16
+    N = n_t + n_v
+    X = torch.randn(N, 512, generator=gen(1))
+    Y = torch.randint(0, 10, (N,), generator=gen(2))
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False,
+                            precision=precision)
+    eng.attach(opt)
+    Xd, Yd = X.to(gpu), Y.to(gpu)
+    for step in range(10):
+        _say(f"config0 precision={precision} step {step}")
+        eng.attach_train_batch(Xd[:n_t], Yd[:n_t], step, 0)
+        opt.zero_grad(set_to_none=True)
+        F.cross_entropy(model(Xd), Yd).backward()
+        torch.cuda.synchronize()
+        dots = {n: p.grad_dot_prod.cpu() for n, p in model.named_parameters()}
+        eng.prepare_gradients()
+        opt.step()
+        eng.aggregate_and_log()
+        eng.clear_gradients()
+        g = brute.per_sample_grads(
+            ref, X.double(), Y, lambda m, x, y: F.cross_entropy(m(x), y, reduction="sum"),
+            1.0 / N)
+        for name, gr in g.items():
+            # T = 1: every layer takes the ghost branch (pairwise sums); bias dots are in
+            # the model dtype in both precisions
+            t = tol if name.endswith("weight") else FP32_TOL
+            assert_close(dots[name], brute.pairwise_dots(gr, n_v), t, f"step {step} {name}")
+        assert_close(eng.dot_product_log[-1]["dot_product"],
+                     sum(brute.pairwise_dots(gr, n_v) for gr in g.values()), tol,
+                     f"step {step} aggregate")
+        with torch.no_grad():
+            for name, p in ref.named_parameters():
+                p -= 0.1 * brute.train_mean(g[name], n_v, N)
+        for (n1, p1), (_, p2) in zip(model.named_parameters(), ref.named_parameters()):
+            assert_close(p1.detach().cpu(), p2.detach(), 1e-4, f"step {step} weights {n1}")
+    eng.detach()
+
+
+# ------------------------------------------------------------------ configs[2]
+def test_config2_gpt2_small_full_step(gpu):
+    """GPT-2-small (12 layers, d = 768, vocab 50257, tied lm_head), N(0, 0.02) weights,
+    bf16, 16 train + 4 val rows of uniform token ids, T = 1024, next-token cross-entropy:
+    all 76 hooked modules' dots (the tied lm_head's is overwritten by wte's, as in the
+    reference) and every .grad after one step."""
+    torch.manual_seed(0)
+    n_t, n_v, T = 16, 4, 1024
+    with torch.device(gpu):
+        model = CausalLM(GPT2_SMALL).to(BF16)
+    X, Y = synthetic_tokens(n_t + n_v, T, GPT2_SMALL.vocab, seed=5, device=gpu)
+    _say("config2 step")
+    eng, dots, grads, total, cap = _lm_step(model, X, Y, n_t, n_v)
+    hooked = sum(1 for m in model.modules() if type(m) in S._supported_layers_dotprod)
+    assert hooked == 76 and len(cap.A) == 76
+    sem = {n: m.use_ghost_computation for n, m in model.named_modules()
+           if hasattr(m, "use_ghost_computation")}
+    assert sem["h.0.fc"] and sem["h.0.fc_out"] and not sem["h.0.qkv"] and not sem["h.0.proj"]
+    _check_lm(model, dots, grads, total, cap, n_t, n_v)
+    eng.detach()
+
+
+# ------------------------------------------------------------------ configs[4]
+def test_config4_pythia_full_step(gpu):
+    """Pythia-1B shape (16 layers, d = 2048, MLP 8192, rotary, untied embed_out over
+    vocab 50304), bf16, 8 train + 2 val rows, T = 2048: every hooked module's dots and every
+    .grad after one step.  embed_out's output gradient [10, 2048, 50304] bf16 is 2.06 GB."""
+    torch.manual_seed(0)
+    n_t, n_v, T = 8, 2, 2048
+    with torch.device(gpu):
+        model = CausalLM(PYTHIA_1B).to(BF16)
+    X, Y = synthetic_tokens(n_t + n_v, T, PYTHIA_1B.vocab, seed=9, device=gpu)
+    _say("config4 step")
+    eng, dots, grads, total, cap = _lm_step(model, X, Y, n_t, n_v)
+    assert cap.B["lm_head"].numel() * 2 > 2 * 10 ** 9
+    sem = {n: m.use_ghost_computation for n, m in model.named_modules()
+           if hasattr(m, "use_ghost_computation")}
+    assert sem["h.0.qkv"] and not sem["h.0.proj"] and sem["h.0.fc"] and sem["lm_head"]
+    _check_lm(model, dots, grads, total, cap, n_t, n_v)
+    eng.detach()
+
+
+# ------------------------------------------------------------------ configs[3]
+def test_config3_gradproj_gpt2_medium(gpu, tmp_path):
+    """GPT-2-medium shape (24 layers, d = 1024, MLP 4096), bf16, B = 32, T = 1024, a
+    16 x 16 Kronecker projection on each of the 96 block Linear layers (seed 42, fp16
+    output): each layer's projection against the float64 projection-first closed form
+    (with the bf16 projections the kernels use), and the concatenation in sorted layer-name
+    order."""
+    torch.manual_seed(0)
+    B, T = 32, 1024
+    with torch.device(gpu):
+        model = CausalLM(GPT2_MEDIUM).to(BF16)
+    X, Y = synthetic_tokens(B, T, GPT2_MEDIUM.vocab, seed=77, device=gpu)
+    eng = GradProjLoraEngine(model, proj_layers="h.", proj_rank_total=256, proj_rank_min=8,
+                             proj_seed=42, proj_dtype="float16", proj_dir=str(tmp_path),
+                             proj_dims_override=(16, 16))
+    assert len(eng.matched_layers) == 96
+    eng.attach()
+    cap = HookCapture(model, (nn.Linear,), names=set(eng.matched_layers))
+    _say("config3 step")
+    model(X, Y).backward()
+    torch.cuda.synchronize()
+    per_layer = {n: l._ghost_grad_proj.clone() for n, l in eng.matched_layers.items()}
+    full = eng.collect_batch()
+    torch.cuda.synchronize()
+    cap.remove()
+    wants = {}
+    for name in sorted(eng.matched_layers):
+        _say(f"  proj {name}")
+        P_i, P_o = eng.projection_matrices[name]
+        want = R.kron_proj_projfirst_exact(cap.A[name], cap.B[name], P_i.to(BF16),
+                                           P_o.to(BF16), float(B))
+        assert_close(per_layer[name], want, BF16_TOL, f"proj {name}")
+        wants[name] = want.reshape(B, -1)
+    assert_close(full.double(), torch.cat([wants[n] for n in sorted(wants)], dim=1), BF16_TOL,
+                 "collected batch")
+    assert full.dtype == torch.float16 and full.shape == (B, 96 * 256)
+    eng.detach()
+
+
+# ------------------------------------------------------------------ operands above 2 GiB
+def test_linear_operand_above_2gib(gpu):
+    """An output gradient of 2.47 GB (12 x 2048 x 50304 bf16), past the 2^31-byte reach of
+    the buffer-resource loads: the val-gradient and bias passes take their other kernels;
+    dots against the float64 closed forms."""
+    N, n_val, T, d_in, d_out = 12, 2, 2048, 256, 50304
+    A = randn((N, T, d_in), 71, 1.0, BF16).to(gpu)
+    G = randn((N, T, d_out), 72, 1e-3, BF16).to(gpu)
+    assert G.numel() * 2 > 2 ** 31
+    want = R.linear_dot_valterm_exact(A, G, n_val, "pairwise")
+    _say("above-2GiB linear_dot")
+    dot, _ = _native.ops().linear_dot(A, G, n_val, algo=_native.ALGO_VALGRAD)
+    torch.cuda.synchronize()
+    assert_close(dot, want, BF16_TOL, "linear_dot > 2 GiB")
+    _say("above-2GiB linear_bias_dot")
+    out = _native.ops().linear_bias_dot(A, G, n_val, grad_scale=1.0)
+    if out is not None:
+        torch.cuda.synchronize()
+        assert_close(out[0], want, BF16_TOL, "fused dot > 2 GiB")
+        assert_close(out[1], R.bias_dot_exact(G, n_val), BF16_TOL, "fused bias > 2 GiB")
+    bdot, _ = _native.ops().bias_dot(G, n_val)
+    torch.cuda.synchronize()
+    assert_close(bdot, R.bias_dot_exact(G, n_val), BF16_TOL, "bias_dot > 2 GiB")

@@ -106,6 +106,25 @@ def test_linear_homogeneity_and_val_layouts():
     assert_close(R.linear_dot_exact(A[perm], B[perm], n_val, val_start=0), base, 1e-12, "layout")
 
 
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+@pytest.mark.parametrize("val_start", [None, 0, 2])
+def test_linear_val_term_form_equals_closed_form(semantics, val_start):
+    """The full-size form (train rows against the val term, one row at a time) against the
+    per-sample-gradient closed form; a transposed val term (V^T in place of V, only
+    possible with d_in == d_out) is rejected."""
+    N, n_val, T, d_in, d_out = 7, 3, 5, 6, 4
+    A = randn((N, T, d_in), 51).double()
+    B = randn((N, T, d_out), 52).double()
+    want = R.linear_dot_exact(A, B, n_val, semantics, val_start=val_start)
+    assert_close(R.linear_dot_valterm_exact(A, B, n_val, semantics, val_start=val_start), want,
+                 1e-12, "val-term form")
+    Asq = randn((N, T, 4), 53).double()
+    V = R.val_term_exact(Asq, B, n_val, semantics)
+    wrong = torch.stack([(B[i] @ V.t() * Asq[i]).sum() for i in range(N - n_val)])
+    ok, _ = R.normwise_close(wrong, R.linear_dot_valterm_exact(Asq, B, n_val, semantics), 1e-3)
+    assert not ok
+
+
 @pytest.mark.parametrize("T", [1, 6])
 def test_linear_reference_sequence_within_bf16_tolerance(T):
     N, n_val, d_in, d_out = 8, 2, 32, 24
@@ -197,6 +216,8 @@ def test_kron_projection_matches_naive_projection(conv1d):
     assert_close(R.kron_proj_exact(A, B, P_i, P_o, float(N), conv1d=conv1d), naive, 1e-10,
                  "exact")
     assert_close(R.kron_proj_ref(A, B, P_i, P_o, conv1d=conv1d).double(), naive, 1e-6, "ref")
+    assert_close(R.kron_proj_projfirst_exact(A, B, P_i, P_o, float(N), conv1d=conv1d), naive,
+                 1e-10, "projection first")
 
 
 def test_embedding_projection_forms_match_per_sample_gradients():

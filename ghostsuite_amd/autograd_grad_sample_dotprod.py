@@ -70,7 +70,9 @@ def add_hooks(model: nn.Module, val_batch_size: int, loss_reduction: str = 'mean
     for lin in linears:
         emb = embeddings_by_weight.get(id(lin.weight))
         if emb is not None:
-            lin._gs_tied_embedding = emb
+            # A plain attribute, not a registered submodule: the model's modules and
+            # state_dict keys stay as they were.
+            lin.__dict__["_gs_tied_embedding"] = emb
     handles.append(model.register_forward_pre_hook(_new_step))
     model.__dict__.setdefault("autograd_grad_sample_hooks", []).extend(handles)
 
@@ -119,6 +121,13 @@ def _prepare_sample_grad_or_dotprod(layer: nn.Module, grad_output: Tuple[torch.T
         if acts is not None and acts.dtype != backprops.dtype and acts.is_floating_point():
             common = torch.promote_types(acts.dtype, backprops.dtype)
             compute_layer_dotprod(layer, acts.to(common), backprops.to(common),
+                                  val_batch_size=val_batch_size)
+        elif acts is not None and acts.dtype != backprops.dtype and \
+                options["reference_id_promotion"]:
+            # The reference promotes integer token ids to the backprops' dtype too (:116-123),
+            # which rounds ids >= 256 in a bf16 model before its sampler casts them back.
+            common = torch.promote_types(acts.dtype, backprops.dtype)
+            compute_layer_dotprod(layer, acts.to(common).long(), backprops,
                                   val_batch_size=val_batch_size)
         else:
             compute_layer_dotprod(layer, acts, backprops, val_batch_size=val_batch_size)

@@ -5,7 +5,8 @@ prepare_gradients, clear_gradients, aggregate_and_log, save_dot_product_log,
 attach_and_store_valset, attach_train_batch, the dot_product_log record format).  Extra
 keyword arguments set the sampler options of
 ``supported_layers_grad_samplers_dotprod.options`` (precision, linear_algo, rounding,
-store_pairs, skip_overwritten_tied_dots, record_algorithms, overlap).
+store_pairs, skip_overwritten_tied_dots, record_algorithms, overlap,
+reference_id_promotion); each engine starts from the defaults.
 """
 from __future__ import annotations
 
@@ -34,6 +35,9 @@ class GradDotProdEngine:
         unknown = set(sampler_options) - set(_samplers.options)
         if unknown:
             raise TypeError(f"unknown GradDotProdEngine options: {sorted(unknown)}")
+        # Options apply per engine: nothing an earlier engine set carries over.
+        _samplers.options.clear()
+        _samplers.options.update(_samplers.DEFAULT_OPTIONS)
         _samplers.options.update(sampler_options)
 
         self.module = module

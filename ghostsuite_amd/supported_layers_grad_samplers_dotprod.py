@@ -33,7 +33,8 @@ try:  # HF Conv1D is a registry key only when transformers is importable
 except Exception:  # pragma: no cover - transformers absent
     _HFConv1D = None
 
-# Engine-wide knobs (set through GradDotProdEngine(**options) or directly).
+# Engine-wide knobs.  Each GradDotProdEngine resets them to DEFAULT_OPTIONS and applies its
+# keyword arguments; they can also be changed directly between steps.
 #   precision:     'reference' -- bf16 operands for the ghost/pairwise path (the reference
 #                  casts A, B to bf16, :92-93), original dtype for presum (:104-105);
 #                  'fp32' -- no down-casts (fp32 operands everywhere).
@@ -45,6 +46,9 @@ except Exception:  # pragma: no cover - transformers absent
 #   skip_overwritten_tied_dots: skip a tied Linear weight's dot when the Embedding that
 #                  shares the weight runs later in backward and overwrites it (:130 vs :211)
 #   record_algorithms: keep {layer name: algorithm} in ``ALGO_LOG``
+#   reference_id_promotion: pass an Embedding's token ids through the backprops' dtype
+#                  before its dot, as the reference's hook does (ids >= 256 round in a bf16
+#                  model); off by default: the ids are used as given
 options = {
     "precision": "reference",
     "linear_algo": "auto",
@@ -54,7 +58,9 @@ options = {
     "record_algorithms": False,
     # Run the dot kernels on a side stream, overlapped with the rest of backward.
     "overlap": True,
+    "reference_id_promotion": False,
 }
+DEFAULT_OPTIONS = dict(options)
 ALGO_LOG: dict = {}
 
 _ALGOS = {"auto": _native.ALGO_AUTO, "ghost": _native.ALGO_GHOST, "valgrad": _native.ALGO_VALGRAD}

@@ -20,8 +20,10 @@ Pinning (how each oracle function is checked; see tests/test_oracle.py):
     n_val == 1; homogeneity; Kronecker identity; embedding mask x Gram);
   - known answers from reading the reference (choose_ki_ko on GPT-2 shapes, the 2T^2 rule
     on the BASELINE shapes);
-  - committed golden fixtures (tests/golden/) generated from these functions on seeded
-    inputs so drift in torch's bf16 CPU kernels is caught.
+  - golden vectors written by the reference's own functions (tests/golden/make_golden.py,
+    run in the build container only; tests/golden/reference_vectors.pt holds inputs and
+    outputs): the *_ref op sequences reproduce them bit for bit, which pins every bf16
+    rounding point, and the exact forms sit within the bf16 tolerance.
 The reference itself is pure Python with no compiled part: oracle/_ref has nothing to
 build.
 """

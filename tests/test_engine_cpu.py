@@ -359,3 +359,45 @@ def test_conv2d_engine_dots_and_grads(n_val):
     for name, gr in grads.items():
         assert_close(gr, brute.train_mean(g[name], n_val, N), FP32_TOL, f"grad {name}")
     assert model[0].use_ghost_computation == (2 * 16 ** 2 <= 6 * 3 * 9)
+
+
+def test_options_do_not_carry_over_between_engines():
+    S = __import__("ghostsuite_amd.supported_layers_grad_samplers_dotprod",
+                   fromlist=["options"])
+    with use_oracle_backend():
+        GradDotProdEngine(MLP((4, 3)), val_batch_size=1, precision="fp32", overlap=False)
+        assert S.options["precision"] == "fp32" and S.options["overlap"] is False
+        GradDotProdEngine(MLP((4, 3)), val_batch_size=1)
+        assert S.options == S.DEFAULT_OPTIONS
+
+
+@pytest.mark.parametrize("promote", [False, True])
+def test_embedding_id_promotion(promote):
+    """The reference's hook promotes an Embedding's int64 ids to the backprops' dtype
+    (autograd_grad_sample_dotprod.py:116-123); in a bf16 model ids >= 256 round (1023 ->
+    1024, 50000 -> 49920) before its sampler casts them back to long.  By default this
+    package uses the ids as given; reference_id_promotion=True reproduces the rounding.
+    The two values differ on such ids."""
+    from oracle import ghost_ref as R
+    vocab, d, T = 1100, 8, 6
+    emb = nn.Embedding(vocab, d).to(torch.bfloat16)
+    ids = torch.tensor([[1023, 300, 5, 700, 1023, 17], [1024, 301, 5, 701, 1022, 18],
+                        [1023, 1021, 6, 700, 299, 17]])
+    n_v = 1
+    with use_oracle_backend():
+        eng = GradDotProdEngine(emb, val_batch_size=n_v, use_dummy_bias=False,
+                                reference_id_promotion=promote)
+        eng.attach(torch.optim.SGD(emb.parameters(), lr=0.0))
+        head = torch.randn(3, T, d, generator=gen(70)).to(torch.bfloat16)
+        (emb(ids).float() * head.float()).sum().backward()
+        got = emb.weight.grad_dot_prod.clone()
+        eng.detach()
+    B = head.float()
+    exact = R.embedding_dot_exact(ids, B, n_v)
+    rounded_ids = ids.to(torch.bfloat16).long()
+    bucketed = R.embedding_dot_exact(rounded_ids, B, n_v)
+    assert not torch.allclose(exact, bucketed)
+    assert_close(got, bucketed if promote else exact, 1e-6, "promotion")
+    # the reference's own op sequence on the promoted ids is the bucketed value
+    assert_close(R.embedding_dot_ref(ids.to(torch.bfloat16), B, n_v, vocab), bucketed,
+                 BF16_TOL, "reference sequence")

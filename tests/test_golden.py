@@ -1,0 +1,161 @@
+"""The oracle and the host logic against vectors written by the reference's own functions
+(tests/golden/make_golden.py; inputs and outputs only, loaded with weights_only=True).
+
+  - the oracle's reference op sequences (*_ref) reproduce the reference's bf16 rounding
+    sequence bit for bit on the same inputs (CPU, one thread, the torch build the vectors
+    were written with; a later torch release may move a last bit, and the check then
+    degrades to one bf16 step per entry, reported in the assertion);
+  - the exact closed forms sit within the bf16 tolerance of the reference's outputs (2e-2
+    normwise) and within 1e-5 where the reference computes in fp32;
+  - the engine's routing, aggregation and tied-weight overwrite match the reference
+    engine's over two SGD steps (the kernel layer here is the oracle's CPU stand-in);
+  - the Gaussian projection matrices equal the reference's on the CPU generator.
+"""
+import os
+
+import pytest
+import torch
+
+from oracle import ghost_ref as R
+from tests.helpers import BF16_TOL, assert_close
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+VECTORS = os.path.join(HERE, "reference_vectors.pt")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return torch.load(VECTORS, weights_only=True)
+
+
+def _bitwise_or_one_step(got, want, what):
+    """Equal bits, else every entry within one bf16 rounding step (2^-8 relative)."""
+    got = got.float()
+    want = want.float()
+    if torch.equal(got, want):
+        return
+    rel = ((got - want).abs() / want.abs().clamp_min(1e-30)).max().item()
+    assert rel <= 2.0 ** -8, f"{what}: not bit-equal, worst relative difference {rel:.3e}"
+
+
+def _cases(golden, prefix):
+    return {k: v for k, v in golden["samplers"].items() if k.startswith(prefix)}
+
+
+def test_vectors_present_and_from_the_reference(golden):
+    meta = golden["meta"]
+    assert set(meta["sha256"]) >= {"ghostEngines/supported_layers_grad_samplers_dotprod.py",
+                                   "ghostEngines/graddotprod_engine.py"}
+    assert len(golden["samplers"]) == 22 and len(golden["projection"]) == 3
+
+
+def test_linear_reference_sequence_bits(golden):
+    torch.set_num_threads(1)
+    for name, c in _cases(golden, "linear_").items():
+        ghost = "_ghost_" in name
+        w, b = R.linear_dot_ref(c["A"], c["B"], c["n_val"], use_ghost=ghost)
+        _bitwise_or_one_step(w, c["dot"], f"{name} weight")
+        _bitwise_or_one_step(b, c["bias_dot"], f"{name} bias")
+        sem = "pairwise" if ghost else "presum"
+        tol = BF16_TOL if (ghost or c["A"].dtype == torch.bfloat16) else 1e-5
+        assert_close(R.linear_dot_exact(c["A"], c["B"], c["n_val"], sem), c["dot"], tol,
+                     f"{name} exact")
+        assert_close(R.bias_dot_exact(c["B"], c["n_val"]), c["bias_dot"],
+                     BF16_TOL if c["B"].dtype == torch.bfloat16 else 1e-5, f"{name} bias exact")
+
+
+def test_embedding_reference_sequence_bits(golden):
+    torch.set_num_threads(1)
+    for name, c in _cases(golden, "embedding_").items():
+        got = R.embedding_dot_ref(c["ids"], c["B"], c["n_val"], c["vocab"])
+        _bitwise_or_one_step(got, c["dot"], name)
+        assert_close(R.embedding_dot_exact(c["ids"], c["B"], c["n_val"]), c["dot"], BF16_TOL,
+                     f"{name} exact")
+
+
+def test_layernorm_reference_sequence_bits(golden):
+    torch.set_num_threads(1)
+    for name, c in _cases(golden, "layernorm_").items():
+        w, b = R.layernorm_dot_ref(c["A"], c["B"], c["n_val"], c["eps"])
+        _bitwise_or_one_step(w, c["dot"], f"{name} weight")
+        _bitwise_or_one_step(b, c["bias_dot"], f"{name} bias")
+        ew, eb = R.layernorm_dot_exact(c["A"], c["B"], c["n_val"], c["eps"])
+        assert_close(ew, c["dot"], BF16_TOL, f"{name} exact weight")
+        assert_close(eb, c["bias_dot"], BF16_TOL, f"{name} exact bias")
+
+
+def test_conv1d_reference_sequence_bits(golden):
+    torch.set_num_threads(1)
+    cases = _cases(golden, "conv1d_")
+    if not cases:
+        pytest.skip("vectors written without transformers")
+    for name, c in cases.items():
+        w, b = R.conv1d_dot_ref(c["A"], c["B"], c["n_val"], use_ghost="_ghost_" in name)
+        _bitwise_or_one_step(w, c["dot"], f"{name} weight")
+        _bitwise_or_one_step(b, c["bias_dot"], f"{name} bias")
+        assert_close(R.linear_dot_exact(c["A"], c["B"], c["n_val"], "presum"), c["dot"],
+                     BF16_TOL, f"{name} exact")
+
+
+def test_planted_rounding_mistake_is_caught(golden):
+    """Dropping the bf16 rounding of the Gram products (fp32 matmuls in place of bf16 ones)
+    changes the bits of the reference sequence's output."""
+    c = golden["samplers"]["linear_ghost_3d_fp32"]
+    A, B, n_val = c["A"], c["B"], c["n_val"]
+    n_t = A.shape[0] - n_val
+    a = A.to(torch.bfloat16).float()
+    b = B.to(torch.bfloat16).float()
+    a_dot = a[:n_t].reshape(-1, a.shape[-1]) @ a[n_t:].reshape(-1, a.shape[-1]).T
+    b_dot = b[:n_t].reshape(-1, b.shape[-1]) @ b[n_t:].reshape(-1, b.shape[-1]).T
+    wrong = (a_dot * b_dot).sum(1).reshape(n_t, -1).sum(1)
+    assert not torch.equal(wrong, c["dot"])
+
+
+def test_projection_matrices_equal_reference(golden):
+    from ghostsuite_amd.gradProjection.projection_utils import init_projection_matrix_gaussian
+    for name, c in golden["projection"].items():
+        P = init_projection_matrix_gaussian(c["rows"], c["cols"], dtype=torch.float32,
+                                            device=torch.device("cpu"), seed=c["seed"])
+        assert torch.equal(P, c["P"]), name
+
+
+def test_engine_routing_matches_reference_engine(golden):
+    """TiedNet (Embedding -> LayerNorm -> Linear -> tanh -> Linear tied to the Embedding),
+    4 train + 2 val rows, two SGD steps in the reference's step order, through this
+    package's engine on the oracle's CPU kernel layer: the same parameters carry dots (the
+    Embedding's replaces the tied Linear's), the logged aggregate, .grad and the weights
+    after each step."""
+    from ghostsuite_amd import GradDotProdEngine
+    from tests.golden.make_golden import tied_net_state
+    from tests.oracle_backend import use_oracle_backend
+    g = golden["engine_tied"]
+    net = tied_net_state()
+    for k, v in net.state_dict().items():
+        assert torch.equal(v, g["init"][k]), k
+    X, Y, n_v = g["X"], g["Y"], g["n_val"]
+    n_t = X.shape[0] - n_v
+    opt = torch.optim.SGD(net.parameters(), lr=g["lr"])
+    with use_oracle_backend():
+        eng = GradDotProdEngine(net, val_batch_size=n_v, use_dummy_bias=False)
+        eng.attach(opt)
+        for it, want in enumerate(g["steps"]):
+            eng.attach_train_batch(X[:n_t], Y[:n_t], it, it)
+            loss = torch.nn.functional.cross_entropy(net(X).reshape(-1, 13), Y.reshape(-1))
+            opt.zero_grad()
+            loss.backward()
+            dots = {n: p.grad_dot_prod.detach().clone() for n, p in net.named_parameters()
+                    if hasattr(p, "grad_dot_prod")}
+            assert sorted(dots) == sorted(want["dots"]), (sorted(dots), sorted(want["dots"]))
+            for n in dots:
+                assert_close(dots[n], want["dots"][n], BF16_TOL, f"step {it} dot {n}")
+            eng.prepare_gradients()
+            for n, p in net.named_parameters():
+                assert_close(p.grad, want["grads"][n], 1e-5, f"step {it} grad {n}")
+            opt.step()
+            eng.aggregate_and_log()
+            eng.clear_gradients()
+            assert_close(eng.dot_product_log[-1]["dot_product"], want["logged"], BF16_TOL,
+                         f"step {it} logged")
+        eng.detach()
+    for k, v in net.state_dict().items():
+        assert_close(v, g["final"][k], 1e-5, f"final {k}")

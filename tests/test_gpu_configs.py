@@ -146,15 +146,15 @@ def _check_lm(model, dots, grads, total, cap, n_t, n_v):
     want_dots, want_grads = _expected_lm(model, cap, n_t, n_v)
     assert sorted(dots) == sorted(want_dots), (sorted(dots), sorted(want_dots))
     for name in sorted(want_dots):
-        _say(f"  dot {name}")
-        assert_close(dots[name], want_dots[name], BF16_TOL, f"dot {name}")
-    assert_close(total, sum(want_dots.values()), BF16_TOL, "logged aggregate")
+        worst = assert_close(dots[name], want_dots[name], BF16_TOL, f"dot {name}")
+        _say(f"  dot {name}: worst {worst:.2e}")
+    assert_close(total, sum(want_dots.values()).cpu(), BF16_TOL, "logged aggregate")
     trainable = sorted(n for n, p in model.named_parameters()
                        if p.initially_requires_grad and "dummy_bias" not in n)
     assert sorted(grads) == trainable and sorted(want_grads) == trainable
     for name in trainable:
-        _say(f"  grad {name}")
-        assert_close(grads[name], want_grads[name], BF16_TOL, f"grad {name}")
+        worst = assert_close(grads[name], want_grads[name], BF16_TOL, f"grad {name}")
+        _say(f"  grad {name}: worst {worst:.2e}")
 
 
 # ------------------------------------------------------------------ configs[1]

@@ -55,6 +55,9 @@ _SIGNATURES = {
     "gs_embedding_dot_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "gs_embedding_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
                               _P]),
+    "gs_embedding_train_grad_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+    "gs_embedding_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P,
+                                     _I, _I, _P, _SZ, _P]),
     "gs_layernorm_dot_workspace": (_SZ, [_I64, _I64, _I64]),
     "gs_layernorm_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _F, _P, _P, _P, _P,
                               _I, _F, _P, _SZ, _P]),
@@ -76,13 +79,6 @@ _SIGNATURES = {
     "gs_linear_bias_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P,
                                 _I, _F, _P, _SZ, _P]),
 }
-
-# How the val-gradient algorithm forms V = G_val^T A_val for the pairwise semantics: "native"
-# (the library's K-major GEMM on the val rows as they lie, inside gs_linear_dot /
-# gs_linear_val_gradient) or "library" (a hipBLASLt GEMM through torch.mm, then
-# gs_linear_rowdot).  The native GEMM measured faster at the GPT-2 shapes (38 vs 45 us for
-# the 3072 x 768 x 4096 val term); the presum semantics and per-pair outputs always use it.
-V_GEMM = "native"
 
 
 def load_library() -> ctypes.CDLL:
@@ -190,12 +186,6 @@ class HipOps:
         n_t = N - n_val
         dt = _gs_dtype(A)
         lib = load_library()
-        if V_GEMM == "library" and not want_pair and semantics == SEM_PAIRWISE_SUM and \
-                n_t > 0 and 0 <= vs <= N - n_val and \
-                lib.gs_linear_dot_algo(dt, N, n_val, T, d_in, d_out, semantics, algo,
-                                       0) == ALGO_VALGRAD:
-            return self._valgrad_library(A, G, N, n_val, vs, T, d_in, d_out, semantics, dev,
-                                         dt), None
         ws_bytes = lib.gs_linear_dot_workspace(dt, N, n_val, T, d_in, d_out, semantics, algo,
                                                int(want_pair))
         if ws_bytes == 0:
@@ -210,17 +200,6 @@ class HipOps:
                                ws.data_ptr(), ws_bytes, _stream(dev))
         _check(rc, "gs_linear_dot")
         return out, pair
-
-    def _valgrad_library(self, A, G, N, n_val, vs, T, d_in, d_out, semantics, dev, dt):
-        """V = G_val^T A_val (presummed val rows for PRESUM) by torch.mm, then the fused
-        row-dot kernel over the train tokens."""
-        Av = A.view(N, T, d_in)[vs:vs + n_val]
-        Gv = G.view(N, T, d_out)[vs:vs + n_val]
-        if semantics == SEM_PRESUM:
-            Av, Gv = Av.sum(0), Gv.sum(0)
-        # sum over val rows and tokens of g a^T: one GEMM with K = n_val * T
-        V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
-        return self.linear_rowdot(A, G, V, n_val, val_start=vs)
 
     def linear_val_gradient(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
                             val_start=None, semantics: int = SEM_PAIRWISE_SUM) -> torch.Tensor:
@@ -257,11 +236,10 @@ class HipOps:
                         rounding: int = ROUND_FP32, grad_scale: Optional[float] = None,
                         grad_dtype: Optional[torch.dtype] = None):
         """Weight and bias dots of a Linear layer (and the bias train gradient when
-        grad_scale is given) in one pass over the train rows when the shape allows it: the
-        val-gradient algorithm through gs_linear_bias_dot, or, for the pairwise semantics with
-        the library V GEMM, torch.mm for V and gs_linear_rowdot_bias.  Otherwise None (the
-        caller then uses linear_dot and bias_dot).  The val rows are [val_start, val_start +
-        n_val) (default: the last n_val rows).  Returns (dot, bias_dot, bias_grad)."""
+        grad_scale is given) in one pass over the train rows when the shape allows it (the
+        val-gradient algorithm through gs_linear_bias_dot).  Otherwise None (the caller then
+        uses linear_dot and bias_dot).  The val rows are [val_start, val_start + n_val)
+        (default: the last n_val rows).  Returns (dot, bias_dot, bias_grad)."""
         dev = _require_device(A, G)
         if A.dtype != G.dtype or A.dtype != torch.bfloat16 or \
                 semantics not in (SEM_PAIRWISE_SUM, SEM_PRESUM) or \
@@ -279,10 +257,7 @@ class HipOps:
         if lib.gs_linear_dot_algo(dt, N, n_val, T, d_in, d_out, semantics, algo,
                                   0) != ALGO_VALGRAD:
             return None
-        library_v = semantics == SEM_PAIRWISE_SUM and V_GEMM == "library"
-        ws_bytes = (lib.gs_linear_rowdot_bias_workspace(dt, N, n_val, T, d_in, d_out)
-                    if library_v else
-                    lib.gs_linear_bias_dot_workspace(dt, N, n_val, T, d_in, d_out, semantics))
+        ws_bytes = lib.gs_linear_bias_dot_workspace(dt, N, n_val, T, d_in, d_out, semantics)
         if ws_bytes == 0:
             return None
         A = A.contiguous()
@@ -292,22 +267,48 @@ class HipOps:
         bout = torch.empty(n_t, dtype=torch.float32, device=dev)
         gdt = grad_dtype or G.dtype
         grad = torch.empty(d_out, dtype=gdt, device=dev) if grad_scale is not None else None
-        if library_v:
-            Av = A.view(N, T, d_in)[vs:vs + n_val]
-            Gv = G.view(N, T, d_out)[vs:vs + n_val]
-            V = torch.mm(Gv.reshape(-1, d_out).t(), Av.reshape(-1, d_in)).contiguous()
-            rc = lib.gs_linear_rowdot_bias(A.data_ptr(), G.data_ptr(), V.data_ptr(), dt, N,
-                                           n_val, vs, T, d_in, d_out, out.data_ptr(),
-                                           bout.data_ptr(), _ptr(grad), _TORCH_TO_GS[gdt],
-                                           float(grad_scale or 0.0), ws.data_ptr(), ws_bytes,
-                                           _stream(dev))
-            _check(rc, "gs_linear_rowdot_bias")
-        else:
-            rc = lib.gs_linear_bias_dot(A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in,
-                                        d_out, semantics, out.data_ptr(), bout.data_ptr(),
-                                        _ptr(grad), _TORCH_TO_GS[gdt], float(grad_scale or 0.0),
-                                        ws.data_ptr(), ws_bytes, _stream(dev))
-            _check(rc, "gs_linear_bias_dot")
+        rc = lib.gs_linear_bias_dot(A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in,
+                                    d_out, semantics, out.data_ptr(), bout.data_ptr(),
+                                    _ptr(grad), _TORCH_TO_GS[gdt], float(grad_scale or 0.0),
+                                    ws.data_ptr(), ws_bytes, _stream(dev))
+        _check(rc, "gs_linear_bias_dot")
+        return out, bout, grad
+
+    def linear_rowdot_bias(self, A: torch.Tensor, G: torch.Tensor, V: torch.Tensor, n_val: int,
+                           *, val_start=None, grad_scale: Optional[float] = None,
+                           grad_dtype: Optional[torch.dtype] = None):
+        """gs_linear_rowdot_bias with a caller-formed V [d_out, d_in] (bf16): the weight dot
+        sum_t g^T V a, the bias dot and (with grad_scale) the bias train gradient of the train
+        rows in one pass.  None when the shape is outside the fused pass's limits.  Returns
+        (dot, bias_dot, bias_grad)."""
+        dev = _require_device(A, G, V)
+        if not (A.dtype == G.dtype == V.dtype == torch.bfloat16):
+            return None
+        A = A.contiguous()
+        G = G.contiguous()
+        V = V.contiguous()
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T or tuple(V.shape) != (d_out, d_in):
+            raise GhostHipError(f"shapes disagree: A {tuple(A.shape)} G {tuple(G.shape)} "
+                                f"V {tuple(V.shape)}")
+        vs = N - n_val if val_start is None else int(val_start)
+        lib = load_library()
+        ws_bytes = lib.gs_linear_rowdot_bias_workspace(DTYPE_BF16, N, n_val, T, d_in, d_out)
+        if ws_bytes == 0:
+            return None
+        ws = _workspace(ws_bytes, dev)
+        n_t = N - n_val
+        out = torch.empty(n_t, dtype=torch.float32, device=dev)
+        bout = torch.empty(n_t, dtype=torch.float32, device=dev)
+        gdt = grad_dtype or G.dtype
+        grad = torch.empty(d_out, dtype=gdt, device=dev) if grad_scale is not None else None
+        rc = lib.gs_linear_rowdot_bias(A.data_ptr(), G.data_ptr(), V.data_ptr(), DTYPE_BF16, N,
+                                       n_val, vs, T, d_in, d_out, out.data_ptr(), bout.data_ptr(),
+                                       _ptr(grad), _TORCH_TO_GS[gdt], float(grad_scale or 0.0),
+                                       ws.data_ptr(), ws_bytes, _stream(dev))
+        _check(rc, "gs_linear_rowdot_bias")
         return out, bout, grad
 
     def linear_rowdot(self, A: torch.Tensor, G: torch.Tensor, V: torch.Tensor, n_val: int, *,
@@ -381,6 +382,33 @@ class HipOps:
                                   vocab, out.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
         _check(rc, "gs_embedding_dot")
         return out
+
+    def embedding_train_grad(self, ids: torch.Tensor, G: torch.Tensor, n_val: int,
+                             scale: float, out: torch.Tensor, *, accumulate: bool = False,
+                             val_start=None) -> None:
+        """out[v] (+)= scale * sum of the train rows of G whose token id is v
+        (gs_embedding_train_grad); out: [vocab, d] bf16 or fp32, written in place."""
+        dev = _require_device(ids, G, out)
+        ids = ids.to(torch.int64).contiguous()
+        G = G.contiguous()
+        N, d = G.shape[0], G.shape[-1]
+        T = ids.numel() // N
+        if _tokens(G, N, d) != T or out.dim() != 2 or out.shape[1] != d or \
+                not out.is_contiguous():
+            raise GhostHipError(f"embedding_train_grad: ids {tuple(ids.shape)}, G "
+                                f"{tuple(G.shape)} and out {tuple(out.shape)} disagree")
+        vocab = out.shape[0]
+        vs = N - n_val if val_start is None else int(val_start)
+        lib = load_library()
+        ws_bytes = lib.gs_embedding_train_grad_workspace(N, n_val, T, vocab)
+        if ws_bytes == 0:
+            raise GhostHipError(f"gs_embedding_train_grad: invalid arguments N={N} n_val={n_val}")
+        ws = _workspace(ws_bytes, dev)
+        rc = lib.gs_embedding_train_grad(ids.data_ptr(), G.data_ptr(), _gs_dtype(G), N, n_val,
+                                         vs, T, d, vocab, float(scale), out.data_ptr(),
+                                         _gs_dtype(out), int(accumulate), ws.data_ptr(),
+                                         ws_bytes, _stream(dev))
+        _check(rc, "gs_embedding_train_grad")
 
     def layernorm_dot(self, X: torch.Tensor, G: torch.Tensor, n_val: int, eps: float, *,
                       val_start=None, want_dot: bool = True, want_bias: bool = True,

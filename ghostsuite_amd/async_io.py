@@ -6,9 +6,11 @@ gradproj_engine.py:274-301 does ``projection.cpu()`` and ``torch.save`` inside
 ``collect_batch``), so the host waits for the GPU to finish the step before it can enqueue
 the next one.  Here:
 
-- ``to_host_async(t)`` enqueues the copy on a dedicated copy stream (default priority) into
-  freshly allocated pinned memory, after that stream waits for the current stream, and
-  returns the host tensor plus the event that completes it.
+- ``to_host_async(t)`` snapshots ``t`` on the current stream (a device clone, so that later
+  in-place writes to ``t`` by the caller cannot reach the copy), then enqueues the copy of the
+  snapshot on a dedicated copy stream (default priority) into freshly allocated pinned memory,
+  after that stream waits for the current stream, and returns the host tensor plus the event
+  that completes it.
 - ``PendingLog`` is a ``list`` of per-step records whose tensors may still be in flight; every
   read of the records (indexing, iteration, pickling, ``clear``) first waits for the pending
   copies, so readers always see finished values, exactly what the reference's list holds.
@@ -49,9 +51,10 @@ def to_host_async(t: torch.Tensor) -> Tuple[torch.Tensor, Optional[torch.cuda.Ev
         return (t.detach().clone() if isinstance(t, torch.Tensor) else t), None
     idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
     cs = _copy_stream(idx)
-    cs.wait_stream(torch.cuda.current_stream(idx))
     host = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
-    src = t.detach()
+    with torch.cuda.device(idx):
+        src = t.detach().clone()   # ordered before anything the caller enqueues on t later
+    cs.wait_stream(torch.cuda.current_stream(idx))
     with torch.cuda.stream(cs):
         host.copy_(src, non_blocking=True)
         ev = torch.cuda.Event()

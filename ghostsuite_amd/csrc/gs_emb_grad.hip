@@ -1,0 +1,251 @@
+// Embedding train gradient, gfx950:
+//
+//   grad[v] = scale * sum over the train tokens t with id_t = v of g_t        grad: [vocab, d]
+//
+// The train tokens are grouped by id without float atomics, so the result is the same bits
+// on every run: a histogram and an exclusive scan of the counts give each id its range of a
+// token list; integer atomics place the tokens in their ranges (in any order); each token then
+// finds its place in index order by counting the smaller token indices in its range.  One wave
+// per vocabulary row sums the rows of its tokens in index order in fp32 and writes the row
+// once, scaled and converted to the grad dtype.  Overwrite mode writes every row (zeros where
+// no token has the id), which replaces a zero-fill, a scatter-add and a full-table scale;
+// accumulate mode adds the touched rows into what `grad` holds (a tied weight whose Linear
+// train gradient is already there) and leaves the other rows alone.
+
+#include <algorithm>
+
+#include "gs_common.h"
+
+namespace gs {
+namespace {
+
+constexpr int EG_THREADS = 256;
+constexpr int EG_SCAN_THREADS = 1024;
+
+// cnt[v] = fill[v] = 0.
+__global__ void __launch_bounds__(EG_THREADS) eg_clear_kernel(int32_t* __restrict__ cnt,
+                                                              int32_t* __restrict__ fill,
+                                                              int64_t vocab) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; v < vocab;
+       v += stride) {
+    cnt[v] = 0;
+    fill[v] = 0;
+  }
+}
+
+// The id of train token q (tokens numbered in train-row order), or -1 when out of range.
+__device__ __forceinline__ int64_t eg_id(const int64_t* __restrict__ ids, const RowMap& tr,
+                                         int64_t vocab, int64_t q) {
+  const int64_t seg = q / tr.seglen;
+  const int64_t id = ids[tr.phys_row(seg, q - seg * tr.seglen)];
+  return (id >= 0 && id < vocab) ? id : -1;
+}
+
+__global__ void __launch_bounds__(EG_THREADS) eg_count_kernel(const int64_t* __restrict__ ids,
+                                                              RowMap tr, int64_t vocab,
+                                                              int32_t* __restrict__ cnt) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (q >= tr.total()) return;
+  const int64_t id = eg_id(ids, tr, vocab, q);
+  if (id >= 0) atomicAdd(cnt + id, 1);
+}
+
+// off = exclusive prefix sum of cnt over [0, vocab), one workgroup: thread t sums a contiguous
+// run of entries, the run totals are scanned in LDS, then each run is written out.
+__global__ void __launch_bounds__(EG_SCAN_THREADS) eg_scan_kernel(const int32_t* __restrict__ cnt,
+                                                                  int64_t vocab,
+                                                                  int32_t* __restrict__ off) {
+  __shared__ int32_t tot[EG_SCAN_THREADS];
+  const int64_t per = (vocab + EG_SCAN_THREADS - 1) / EG_SCAN_THREADS;
+  const int64_t v0 = threadIdx.x * per, v1 = std::min<int64_t>(vocab, v0 + per);
+  int32_t s = 0;
+  for (int64_t v = v0; v < v1; ++v) s += cnt[v];
+  tot[threadIdx.x] = s;
+  __syncthreads();
+  // Hillis-Steele inclusive scan of the run totals.
+  for (int d = 1; d < EG_SCAN_THREADS; d <<= 1) {
+    const int32_t add = threadIdx.x >= d ? tot[threadIdx.x - d] : 0;
+    __syncthreads();
+    tot[threadIdx.x] += add;
+    __syncthreads();
+  }
+  int32_t run = threadIdx.x > 0 ? tot[threadIdx.x - 1] : 0;
+  for (int64_t v = v0; v < v1; ++v) {
+    off[v] = run;
+    run += cnt[v];
+  }
+}
+
+// list[off[id] + k] = q for some k in [0, cnt[id]) (the order inside a range is arbitrary).
+__global__ void __launch_bounds__(EG_THREADS) eg_place_kernel(const int64_t* __restrict__ ids,
+                                                              RowMap tr, int64_t vocab,
+                                                              const int32_t* __restrict__ off,
+                                                              int32_t* __restrict__ fill,
+                                                              int32_t* __restrict__ list) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (q >= tr.total()) return;
+  const int64_t id = eg_id(ids, tr, vocab, q);
+  if (id < 0) return;
+  const int32_t k = atomicAdd(fill + id, 1);
+  list[off[id] + k] = static_cast<int32_t>(q);
+}
+
+// sorted[off[id] + r] = q with r = the number of tokens of the same id before q: each range
+// of `sorted` lists its tokens in index order.
+__global__ void __launch_bounds__(EG_THREADS) eg_order_kernel(const int64_t* __restrict__ ids,
+                                                              RowMap tr, int64_t vocab,
+                                                              const int32_t* __restrict__ off,
+                                                              const int32_t* __restrict__ cnt,
+                                                              const int32_t* __restrict__ list,
+                                                              int32_t* __restrict__ sorted) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (q >= tr.total()) return;
+  const int64_t id = eg_id(ids, tr, vocab, q);
+  if (id < 0) return;
+  const int32_t s = off[id], n = cnt[id];
+  int32_t r = 0;
+  for (int32_t k = 0; k < n; ++k) r += list[s + k] < static_cast<int32_t>(q) ? 1 : 0;
+  sorted[s + r] = static_cast<int32_t>(q);
+}
+
+template <class E>
+struct EgVec {
+  static constexpr int VE = 16 / sizeof(E);
+};
+
+// One wave per vocabulary row v (4 rows per workgroup): lanes own 16-byte feature chunks of
+// the row (VE elements, several passes when d > 64 VE); each lane sums its chunk over the
+// row's tokens in index order (fp32) and writes scale * sum (plus the old value when
+// accumulating).  `vec`: G's rows are 16-byte aligned, so whole chunks load at once.
+template <class E, class GE>
+__global__ void __launch_bounds__(EG_THREADS) eg_rows_kernel(
+    const E* __restrict__ G, RowMap tr, int64_t d, int64_t vocab, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ cnt, const int32_t* __restrict__ sorted, float scale,
+    int accumulate, int vec, GE* __restrict__ grad) {
+  constexpr int VE = EgVec<E>::VE;
+  const int lane = threadIdx.x & 63;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * (EG_THREADS / 64) + (threadIdx.x >> 6);
+  if (v >= vocab) return;
+  const int32_t n = cnt[v];
+  if (n == 0 && accumulate) return;
+  const int32_t s = off[v];
+  GE* out = grad + v * d;
+  for (int64_t f0 = static_cast<int64_t>(lane) * VE; f0 < d; f0 += 64 * VE) {
+    const bool full = vec && f0 + VE <= d;
+    float acc[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] = 0.f;
+    for (int32_t k = 0; k < n; ++k) {
+      const int64_t q = sorted[s + k];
+      const int64_t seg = q / tr.seglen;
+      const E* row = G + tr.phys_row(seg, q - seg * tr.seglen) * d + f0;
+      if (full) {
+        union { uint4 u; E e[VE]; } w;
+        w.u = *reinterpret_cast<const uint4*>(row);
+#pragma unroll
+        for (int i = 0; i < VE; ++i) acc[i] += to_f32<E>(w.e[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VE; ++i)
+          if (f0 + i < d) acc[i] += to_f32<E>(row[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      if (f0 + i >= d) break;
+      float x = n > 0 ? scale * acc[i] : 0.f;
+      if (accumulate) x += to_f32<GE>(out[f0 + i]);
+      out[f0 + i] = from_f32<GE>(x);
+    }
+  }
+}
+
+int64_t eg_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <class S>
+void carve_emb_grad(S& c, int64_t M, int64_t vocab, int32_t** cnt, int32_t** fill,
+                    int32_t** off, int32_t** list, int32_t** sorted) {
+  *cnt = c.template take<int32_t>(vocab);
+  *fill = c.template take<int32_t>(vocab);
+  *off = c.template take<int32_t>(vocab);
+  *list = c.template take<int32_t>(M);
+  *sorted = c.template take<int32_t>(M);
+}
+
+template <class E, class GE>
+int launch_rows(const void* G, const RowMap& tr, int64_t d, int64_t vocab, const int32_t* off,
+                const int32_t* cnt, const int32_t* sorted, float scale, int accumulate, int vec,
+                void* grad, hipStream_t s) {
+  hipLaunchKernelGGL((eg_rows_kernel<E, GE>),
+                     dim3(static_cast<unsigned>(eg_cdiv(vocab, EG_THREADS / 64))),
+                     dim3(EG_THREADS), 0, s, static_cast<const E*>(G), tr, d, vocab, off, cnt,
+                     sorted, scale, accumulate, vec, static_cast<GE*>(grad));
+  return check_launch("eg_rows_kernel");
+}
+
+}  // namespace
+}  // namespace gs
+
+using namespace gs;
+
+extern "C" size_t gs_embedding_train_grad_workspace(int64_t N, int64_t n_val, int64_t T,
+                                                    int64_t vocab) {
+  if (N <= 0 || n_val < 0 || n_val >= N || T <= 0 || vocab <= 0) return 0;
+  Sizer sz;
+  int32_t *cnt, *fill, *off, *list, *sorted;
+  carve_emb_grad(sz, (N - n_val) * T, vocab, &cnt, &fill, &off, &list, &sorted);
+  return sz.used + 256;
+}
+
+extern "C" int gs_embedding_train_grad(const int64_t* ids, const void* G, int dtype, int64_t N,
+                                       int64_t n_val, int64_t val_start, int64_t T, int64_t d,
+                                       int64_t vocab, float scale, void* grad, int grad_dtype,
+                                       int accumulate, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_embedding_train_grad: dtype must be bf16 or fp32");
+  if (grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_embedding_train_grad: grad_dtype must be bf16 or fp32");
+  if (ids == nullptr || G == nullptr || grad == nullptr || N <= 0 || n_val < 0 || n_val >= N ||
+      val_start < 0 || val_start + n_val > N || T <= 0 || d <= 0 || vocab <= 0)
+    return fail(GS_ERR_INVALID, "gs_embedding_train_grad: invalid arguments");
+  const int64_t M = (N - n_val) * T;
+  if (M >= INT32_MAX || vocab >= INT32_MAX)
+    return fail(GS_ERR_UNSUPPORTED, "gs_embedding_train_grad: 2^31 or more tokens or ids");
+  Sizer sz;
+  int32_t *cnt, *fill, *off, *list, *sorted;
+  carve_emb_grad(sz, M, vocab, &cnt, &fill, &off, &list, &sorted);
+  if (workspace == nullptr || workspace_bytes < sz.used)
+    return fail(GS_ERR_WORKSPACE, "gs_embedding_train_grad: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  carve_emb_grad(cv, M, vocab, &cnt, &fill, &off, &list, &sorted);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const RowMap tr = train_rows(N, n_val, val_start, T);
+  const unsigned vb = static_cast<unsigned>(std::min<int64_t>(eg_cdiv(vocab, EG_THREADS), 4096));
+  const unsigned tb = static_cast<unsigned>(eg_cdiv(M, EG_THREADS));
+  hipLaunchKernelGGL(eg_clear_kernel, dim3(vb), dim3(EG_THREADS), 0, s, cnt, fill, vocab);
+  hipLaunchKernelGGL(eg_count_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, cnt);
+  hipLaunchKernelGGL(eg_scan_kernel, dim3(1), dim3(EG_SCAN_THREADS), 0, s, cnt, vocab, off);
+  hipLaunchKernelGGL(eg_place_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, off,
+                     fill, list);
+  hipLaunchKernelGGL(eg_order_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, off,
+                     cnt, list, sorted);
+  int rc = check_launch("embedding train-gradient grouping kernels");
+  if (rc) return rc;
+  const size_t esz = elem_size(dtype);
+  const int vec = (reinterpret_cast<uintptr_t>(G) % 16 == 0) &&
+                  (d * static_cast<int64_t>(esz)) % 16 == 0;
+  const int acc = accumulate ? 1 : 0;
+  if (dtype == GS_DTYPE_BF16)
+    return grad_dtype == GS_DTYPE_BF16
+               ? launch_rows<uint16_t, uint16_t>(G, tr, d, vocab, off, cnt, sorted, scale, acc,
+                                                 vec, grad, s)
+               : launch_rows<uint16_t, float>(G, tr, d, vocab, off, cnt, sorted, scale, acc,
+                                              vec, grad, s);
+  return grad_dtype == GS_DTYPE_BF16
+             ? launch_rows<float, uint16_t>(G, tr, d, vocab, off, cnt, sorted, scale, acc, vec,
+                                            grad, s)
+             : launch_rows<float, float>(G, tr, d, vocab, off, cnt, sorted, scale, acc, vec,
+                                         grad, s);
+}

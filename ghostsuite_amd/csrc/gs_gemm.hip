@@ -2070,29 +2070,56 @@ LinearPlan plan_any(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in
   return plan_linear<TrBF16>(N, n_val, T, d_in, d_out, semantics, algo, want_pair);
 }
 
+// Workspace of run_linear, in the order it carves.  `tn`: VALGRAD forms V by the K-major
+// GEMM (bf16, aligned operands): the presummed val rows (PRESUM only), V, the partials, the
+// GEMM's split partials.  Otherwise the transposed val rows, V, the partials.
 template <class S>
-void carve_linear(S& c, const LinearPlan& pl, int dtype, int64_t N, int64_t n_val, int64_t T,
-                  int64_t d_in, int64_t d_out, int semantics) {
+void carve_linear(S& c, const LinearPlan& pl, int dtype, int64_t T, int64_t d_in,
+                  int64_t d_out, int semantics, bool tn) {
   const size_t esz = elem_size(dtype);
-  (void)N;
-  (void)n_val;
   if (pl.algo == GS_ALGO_GHOST) {
     if (semantics == GS_SEM_PRESUM) {
       c.template take<char>(T * d_in * esz);
       c.template take<char>(T * d_out * esz);
     }
+    c.template take<float>(pl.p_rows * pl.p_ld);
+  } else if (tn) {
+    if (semantics == GS_SEM_PRESUM) {
+      c.template take<char>(T * d_in * esz);
+      c.template take<char>(T * d_out * esz);
+    }
+    c.template take<char>(d_out * d_in * esz);
+    c.template take<float>(pl.p_rows * pl.p_ld);
+    c.template take<float>(tn_part_elems(pl.vcols / pl.groups, d_out, d_in));
   } else {
-    // Transposed val rows (or, on the K-major path, the presummed rows), V, the partials,
-    // then the K-major GEMM's split partials.  Both paths carve the same prefix, so a call
-    // that cannot take the K-major path (unaligned pointers) still fits.
     c.template take<char>(d_in * pl.vcols * esz);
     c.template take<char>(d_out * pl.vcols * esz);
     c.template take<char>(d_out * d_in * esz);
+    c.template take<float>(pl.p_rows * pl.p_ld);
   }
-  c.template take<float>(pl.p_rows * pl.p_ld);
-  if (pl.algo != GS_ALGO_GHOST &&
-      val_tn(dtype, n_val, T, d_in, d_out, semantics == GS_SEM_PRESUM ? 1 : 0))
-    c.template take<float>(tn_part_elems(pl.vcols / pl.groups, d_out, d_in));
+}
+// Whether run_linear's VALGRAD takes the K-major GEMM for these operands.
+bool linear_tn(int dtype, const LinearPlan& pl, int64_t n_val, int64_t T, int64_t d_in,
+               int64_t d_out, int semantics, const void* A, const void* G) {
+  return pl.algo != GS_ALGO_GHOST && dtype == GS_DTYPE_BF16 &&
+         val_tn(dtype, n_val, T, d_in, d_out, semantics == GS_SEM_PRESUM ? 1 : 0) &&
+         aligned16(A) && aligned16(G);
+}
+// Bytes a call needs: exact when the operands are known, else the larger of the two layouts.
+size_t linear_bytes(int dtype, const LinearPlan& pl, int64_t n_val, int64_t T, int64_t d_in,
+                    int64_t d_out, int semantics, const void* A, const void* G) {
+  Sizer a, b;
+  if (A != nullptr) {
+    carve_linear(a, pl, dtype, T, d_in, d_out, semantics,
+                 linear_tn(dtype, pl, n_val, T, d_in, d_out, semantics, A, G));
+    return a.used;
+  }
+  carve_linear(a, pl, dtype, T, d_in, d_out, semantics, false);
+  const bool tn_possible = pl.algo != GS_ALGO_GHOST && dtype == GS_DTYPE_BF16 &&
+                           val_tn(dtype, n_val, T, d_in, d_out,
+                                  semantics == GS_SEM_PRESUM ? 1 : 0);
+  if (tn_possible) carve_linear(b, pl, dtype, T, d_in, d_out, semantics, true);
+  return std::max(a.used, b.used);
 }
 
 bool linear_args_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
@@ -2272,11 +2299,11 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
   const int presum = semantics == GS_SEM_PRESUM ? 1 : 0;
   const int64_t n_mt = pl.p_rows / pl.groups;  // row-dot M tiles (the plan's tile height)
   if constexpr (std::is_same<Tr, TrBF16>::value) {
-    if (val_tn(GS_DTYPE_BF16, n_val, T, d_in, d_out, presum) && aligned16(A) && aligned16(G)) {
+    if (linear_tn(GS_DTYPE_BF16, pl, n_val, T, d_in, d_out, semantics, A, G)) {
       const E* La = static_cast<const E*>(A) + val_start * T * d_in;
       const E* Lg = static_cast<const E*>(G) + val_start * T * d_out;
-      E* abar = reinterpret_cast<E*>(cv.take<char>(d_in * pl.vcols * esz));
-      E* gbar = reinterpret_cast<E*>(cv.take<char>(d_out * pl.vcols * esz));
+      E* abar = presum ? reinterpret_cast<E*>(cv.take<char>(T * d_in * esz)) : nullptr;
+      E* gbar = presum ? reinterpret_cast<E*>(cv.take<char>(T * d_out * esz)) : nullptr;
       E* V = reinterpret_cast<E*>(cv.take<char>(d_out * d_in * esz));
       float* P = cv.take<float>(pl.p_rows * pl.p_ld);
       const int64_t kper = pl.vcols / pl.groups;  // k-rows per V (one val row for pairs)
@@ -2356,9 +2383,7 @@ extern "C" size_t gs_linear_dot_workspace(int dtype, int64_t N, int64_t n_val, i
                                           int want_pair) {
   if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair)) return 0;
   const LinearPlan pl = plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair);
-  Sizer sz;
-  carve_linear(sz, pl, dtype, N, n_val, T, d_in, d_out, semantics);
-  return sz.used + 256;
+  return linear_bytes(dtype, pl, n_val, T, d_in, d_out, semantics, nullptr, nullptr) + 256;
 }
 
 extern "C" int gs_linear_dot_algo(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,
@@ -2368,34 +2393,54 @@ extern "C" int gs_linear_dot_algo(int dtype, int64_t N, int64_t n_val, int64_t T
   return plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair).algo;
 }
 
+namespace gs {
+namespace {
+int check_linear_args(const char* who, const void* A, const void* G, int dtype, int64_t N,
+                      int64_t n_val, int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                      int semantics, int algo, int rounding, const float* out_dot,
+                      int want_pair) {
+  const std::string w(who);
+  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, w + ": dtype must be bf16 or fp32");
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair))
+    return fail(GS_ERR_INVALID, w + ": invalid shape, semantics or algorithm");
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, w + ": val block outside the batch");
+  if (A == nullptr || G == nullptr || out_dot == nullptr)
+    return fail(GS_ERR_INVALID, w + ": null pointer");
+  if (rounding != GS_ROUND_FP32 && rounding != GS_ROUND_REF_BF16)
+    return fail(GS_ERR_INVALID, w + ": invalid rounding");
+  return GS_OK;
+}
+int run_linear_any(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                   int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, int semantics,
+                   int rounding, float* out_dot, float* out_pair, const LinearPlan& pl,
+                   Carver& cv, hipStream_t s) {
+  if (dtype == GS_DTYPE_BF16)
+    return run_linear<TrBF16>(A, G, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
+                              out_dot, out_pair, pl, cv, s);
+  return run_linear<TrF32>(A, G, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
+                           out_dot, out_pair, pl, cv, s);
+}
+}  // namespace
+}  // namespace gs
+
 extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
                              int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
                              int semantics, int algo, int rounding, float* out_dot,
                              float* out_pair, void* workspace, size_t workspace_bytes,
                              void* stream) {
   const int want_pair = out_pair != nullptr;
-  if (dtype != GS_DTYPE_BF16 && dtype != GS_DTYPE_F32)
-    return fail(GS_ERR_DTYPE, "gs_linear_dot: dtype must be bf16 or fp32");
-  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair))
-    return fail(GS_ERR_INVALID, "gs_linear_dot: invalid shape, semantics or algorithm");
-  if (val_start < 0 || val_start + n_val > N)
-    return fail(GS_ERR_INVALID, "gs_linear_dot: val block outside the batch");
-  if (A == nullptr || G == nullptr || out_dot == nullptr)
-    return fail(GS_ERR_INVALID, "gs_linear_dot: null pointer");
-  if (rounding != GS_ROUND_FP32 && rounding != GS_ROUND_REF_BF16)
-    return fail(GS_ERR_INVALID, "gs_linear_dot: invalid rounding");
+  int rc = check_linear_args("gs_linear_dot", A, G, dtype, N, n_val, val_start, T, d_in, d_out,
+                             semantics, algo, rounding, out_dot, want_pair);
+  if (rc) return rc;
   const LinearPlan pl = plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair);
-  Sizer sz;
-  carve_linear(sz, pl, dtype, N, n_val, T, d_in, d_out, semantics);
-  if (workspace == nullptr || workspace_bytes < sz.used)
+  if (workspace == nullptr ||
+      workspace_bytes < linear_bytes(dtype, pl, n_val, T, d_in, d_out, semantics, A, G))
     return fail(GS_ERR_WORKSPACE, "gs_linear_dot: workspace too small");
   Carver cv(workspace, workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == GS_DTYPE_BF16)
-    return run_linear<TrBF16>(A, G, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
-                              out_dot, out_pair, pl, cv, s);
-  return run_linear<TrF32>(A, G, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
-                           out_dot, out_pair, pl, cv, s);
+  return run_linear_any(A, G, dtype, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
+                        out_dot, out_pair, pl, cv, static_cast<hipStream_t>(stream));
 }
 
 // ------------------------------------------------------------------ val gradient V

@@ -2,6 +2,9 @@
 //
 //   out[b] = scale * sum_t (L g_bt)(R a_bt)^T        L: [kL, n_g], R: [kR, n_a]
 //
+// Projections with more than 64 rows on a side run as several launches over 64-row slices of
+// the projection matrices, each writing its block of the [kL, kR] partials.
+//
 // One workgroup takes one sample and a chunk of 64 tokens; its 8 waves take interleaved
 // 32-feature pieces of all 64 token rows (so the workgroup reads 256 contiguous features of
 // every row at a time).  A wave streams its pieces of the G and A rows straight from HBM
@@ -34,7 +37,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 #endif
 constexpr int PJ_TOK = GS_PJ_TOK;  // tokens per workgroup
 constexpr int PJ_THREADS = GS_PJ_THREADS;
-constexpr int PJ_KMAX = 32;     // projection rows supported per side
+constexpr int PJ_KMAX = 64;     // projection rows per side of one launch
 
 struct PjBF16 {
   using E = uint16_t;
@@ -93,8 +96,11 @@ __device__ __forceinline__ void project_rows(const typename Tr::E* const (&rows)
   using E = typename Tr::E;
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 4;  // lane group: k-slice selector
-  const E* prow0 = (lane & 15) < kP ? P + static_cast<int64_t>(lane & 15) * n : nullptr;
-  const E* prow1 = 16 + (lane & 15) < kP ? P + static_cast<int64_t>(16 + (lane & 15)) * n : nullptr;
+  const E* prow[NB];         // this lane's projection row in each 16-row block
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+    prow[nb] = 16 * nb + (lane & 15) < kP ? P + static_cast<int64_t>(16 * nb + (lane & 15)) * n
+                                          : nullptr;
   constexpr int U = GS_PJ_U;  // k-steps of loads in flight (x PJ_TG rows)
   // The waves interleave in pieces of U k-steps, so a workgroup reads one contiguous run
   // of PJ_WAVES pieces of every row at a time.
@@ -109,39 +115,43 @@ __device__ __forceinline__ void project_rows(const typename Tr::E* const (&rows)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t k = f0 + u * Tr::KSTEP + kg * Tr::VEC;
-      const uint4 b0 = lane_load<Tr>(prow0, k, n, vec_p);
 #pragma unroll
-      for (int tg = 0; tg < PJ_TG; ++tg)
-#pragma unroll
-        for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[tg][0], a[u][tg], b0, s);
-      if constexpr (NB > 1) {
-        const uint4 b1 = lane_load<Tr>(prow1, k, n, vec_p);
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint4 bq = lane_load<Tr>(prow[nb], k, n, vec_p);
 #pragma unroll
         for (int tg = 0; tg < PJ_TG; ++tg)
 #pragma unroll
-          for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[tg][1], a[u][tg], b1, s);
+          for (int s = 0; s < Tr::SUB; ++s) Tr::mma(acc[tg][nb], a[u][tg], bq, s);
       }
     }
   }
 }
 
+// Where a launch writes: its [kL, kR] block of the per-(sample, chunk) partials
+// part[(b * chunks + c) * kl_tot * kr_tot + (l0 + p) * kr_tot + r0 + q].
+struct PjSlice {
+  int64_t kl_tot, kr_tot, l0, r0;
+};
+
 // GATHER: the input side is an embedding, whose "projected input" for token id x is column
-// x of P_i, i.e. row x of R = P_i^T ([vocab, kR]); `ids` replaces A.
+// x of P_i, i.e. row x of R = P_i^T ([vocab, ldr], this launch's kR columns); `ids` replaces A.
 // Workgroup = one sample x PJ_TOK tokens; wave w projects all PJ_TOK token rows over its
 // share of the features, the wave shares are summed in LDS (fixed order), then the
-// PJ_TOK-token outer-product sum is formed.
+// PJ_TOK-token outer-product sum is formed.  NB: 16-row projection blocks per side
+// (kL, kR <= 16 * NB).
 template <class Tr, bool GATHER, int NB>
 __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
     const typename Tr::E* __restrict__ A, const int64_t* __restrict__ ids, int64_t vocab,
     const typename Tr::E* __restrict__ G, int64_t T, int64_t n_a, int64_t n_g,
     const typename Tr::E* __restrict__ R, const typename Tr::E* __restrict__ L, int64_t kR,
-    int64_t kL, int vec_a, int vec_g, int vec_r, int vec_l, int64_t chunks,
-    float* __restrict__ part) {
+    int64_t kL, int64_t ldr, int vec_a, int vec_g, int vec_r, int vec_l, int64_t chunks,
+    PjSlice sl, float* __restrict__ part) {
   using E = typename Tr::E;
+  constexpr int KM = 16 * NB;  // LDS width: projection rows per side
   // Wave slices combine in two steps through [PJ_WAVES / 2] slices of LDS.
   constexpr int HW = PJ_WAVES / 2;
-  __shared__ float sg[HW][PJ_TOK][PJ_KMAX + 1];
-  __shared__ float sa[HW][PJ_TOK][PJ_KMAX + 1];
+  __shared__ float sg[HW][PJ_TOK][KM + 1];
+  __shared__ float sa[HW][PJ_TOK][KM + 1];
   const int64_t b = blockIdx.y, c = blockIdx.x;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const E* grows[PJ_TG];
@@ -164,29 +174,25 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
   // Waves HW.. park their slices, waves 0..HW-1 add their own, then slice 0 takes the sum
   // of the HW slices (fixed order); the gather fills slice 0 of sa.
   auto put = [&](bool add) {
-    const int sl = wid % HW;
+    const int ws = wid % HW;
 #pragma unroll
     for (int tg = 0; tg < PJ_TG; ++tg)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int tok = tg * 16 + 4 * (lane >> 4) + e;
           const int k = nb * 16 + (lane & 15);
-          const float g = nb < NB ? accg[tg][nb < NB ? nb : 0][e] : 0.f;
-          sg[sl][tok][k] = (add ? sg[sl][tok][k] : 0.f) + g;
-          if constexpr (!GATHER) {
-            const float a = nb < NB ? acca[tg][nb < NB ? nb : 0][e] : 0.f;
-            sa[sl][tok][k] = (add ? sa[sl][tok][k] : 0.f) + a;
-          }
+          sg[ws][tok][k] = (add ? sg[ws][tok][k] : 0.f) + accg[tg][nb][e];
+          if constexpr (!GATHER) sa[ws][tok][k] = (add ? sa[ws][tok][k] : 0.f) + acca[tg][nb][e];
         }
   };
   if (wid >= HW) put(false);
   __syncthreads();
   if (wid < HW) put(true);
   __syncthreads();
-  for (int x = threadIdx.x; x < PJ_TOK * PJ_KMAX; x += PJ_THREADS) {
-    const int tok = x / PJ_KMAX, q = x % PJ_KMAX;
+  for (int x = threadIdx.x; x < PJ_TOK * KM; x += PJ_THREADS) {
+    const int tok = x / KM, q = x % KM;
     float g = sg[0][tok][q];
 #pragma unroll
     for (int w = 1; w < HW; ++w) g += sg[w][tok][q];
@@ -196,7 +202,7 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
       float v = 0.f;
       if (tt < T && q < kR) {
         const int64_t id = ids[b * T + tt];
-        if (id >= 0 && id < vocab) v = to_f32<E>(R[id * kR + q]);
+        if (id >= 0 && id < vocab) v = to_f32<E>(R[id * ldr + q]);
       }
       sa[0][tok][q] = v;
     } else {
@@ -209,11 +215,12 @@ __global__ void __launch_bounds__(PJ_THREADS) kron_proj_kernel(
   __syncthreads();
   const int64_t nvalid = std::min<int64_t>(PJ_TOK, T - c * PJ_TOK);
   const int64_t nout = kL * kR;
+  float* dst = part + (b * chunks + c) * sl.kl_tot * sl.kr_tot + sl.l0 * sl.kr_tot + sl.r0;
   for (int64_t o = threadIdx.x; o < nout; o += PJ_THREADS) {
     const int p = static_cast<int>(o / kR), q = static_cast<int>(o % kR);
     float s = 0.f;
     for (int64_t tk = 0; tk < nvalid; ++tk) s += sg[0][tk][p] * sa[0][tk][q];
-    part[(b * chunks + c) * nout + o] = s;
+    dst[p * sl.kr_tot + q] = s;
   }
 }
 
@@ -238,6 +245,47 @@ __global__ void kron_reduce_kernel(const float* __restrict__ part, int64_t chunk
 namespace {
 int64_t pj_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// One launch over rows [l0, l0 + kl) of L and [r0, r0 + kr) of R (each at most PJ_KMAX).
+template <class Tr, bool GATHER>
+int launch_pj_slice(const typename Tr::E* A, const int64_t* ids, int64_t vocab,
+                    const typename Tr::E* G, int64_t B, int64_t T, int64_t n_a, int64_t n_g,
+                    const typename Tr::E* R, const typename Tr::E* L, int64_t kr, int64_t kl,
+                    int64_t ldr, int va, int vg, int vr, int vl, int64_t chunks, PjSlice sl,
+                    float* part, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
+  const int64_t km = std::max(kl, kr);  // LDS width (a gathered side occupies it too)
+  auto k = km > 32   ? kron_proj_kernel<Tr, GATHER, 4>
+           : km > 16 ? kron_proj_kernel<Tr, GATHER, 2>
+                     : kron_proj_kernel<Tr, GATHER, 1>;
+  hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, A, ids, vocab, G, T, n_a, n_g, R, L, kr,
+                     kl, ldr, va, vg, vr, vl, chunks, sl, part);
+  return check_launch(GATHER ? "kron_proj_kernel(gather)" : "kron_proj_kernel");
+}
+
+// All slices of a [kL_tot, kR_tot] projection: L rows and R rows (or, gathering, R columns)
+// in pieces of PJ_KMAX.
+template <class Tr, bool GATHER>
+int launch_pj(const void* A, const int64_t* ids, int64_t vocab, const void* G, int64_t B,
+              int64_t T, int64_t n_a, int64_t n_g, const void* R, const void* L, int64_t kR,
+              int64_t kL, int va, int vg, int vr, int vl, int64_t chunks, float* part,
+              hipStream_t s) {
+  using E = typename Tr::E;
+  for (int64_t l0 = 0; l0 < kL; l0 += PJ_KMAX) {
+    for (int64_t r0 = 0; r0 < kR; r0 += PJ_KMAX) {
+      const int64_t kl = std::min<int64_t>(PJ_KMAX, kL - l0);
+      const int64_t kr = std::min<int64_t>(PJ_KMAX, kR - r0);
+      const E* Ls = static_cast<const E*>(L) + l0 * n_g;
+      const E* Rs = GATHER ? static_cast<const E*>(R) + r0 : static_cast<const E*>(R) + r0 * n_a;
+      const PjSlice sl{kL, kR, l0, r0};
+      const int rc = launch_pj_slice<Tr, GATHER>(
+          static_cast<const E*>(A), ids, vocab, static_cast<const E*>(G), B, T, n_a, n_g, Rs, Ls,
+          kr, kl, GATHER ? kR : n_a, va, vg, vr, vl, chunks, sl, part, s);
+      if (rc) return rc;
+    }
+  }
+  return GS_OK;
+}
 
 // Fixed-order per-sample sum of the chunk partials, scaled and converted to the output type.
 int kron_finish(const float* part, int64_t B, int64_t chunks, int64_t nout, float scale,
@@ -283,8 +331,6 @@ extern "C" int gs_kron_proj(const void* A, const void* G, int dtype, int64_t B, 
     return fail(GS_ERR_INVALID, "gs_kron_proj: invalid arguments");
   if (layout != GS_PROJ_KO_KI && layout != GS_PROJ_KI_KO)
     return fail(GS_ERR_INVALID, "gs_kron_proj: invalid layout");
-  if (k_i > PJ_KMAX || k_o > PJ_KMAX)
-    return fail(GS_ERR_UNSUPPORTED, "gs_kron_proj: k_i and k_o must be <= 32");
   // KO_KI: L = P_o (applied to G), R = P_i (applied to A).  KI_KO swaps the matrices.
   const void* L = layout == GS_PROJ_KO_KI ? P_o : P_i;
   const void* R = layout == GS_PROJ_KO_KI ? P_i : P_o;
@@ -302,22 +348,11 @@ extern "C" int gs_kron_proj(const void* A, const void* G, int dtype, int64_t B, 
   const int vg = al16(G) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
   const int vr = al16(R) && (n_a * static_cast<int64_t>(esz)) % 16 == 0;
   const int vl = al16(L) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
-  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
-  const bool two = kL > 16 || kR > 16;
-  if (dtype == GS_DTYPE_BF16) {
-    auto k = two ? kron_proj_kernel<PjBF16, false, 2> : kron_proj_kernel<PjBF16, false, 1>;
-    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, static_cast<const uint16_t*>(A),
-                       nullptr, int64_t{0}, static_cast<const uint16_t*>(G), T, n_a, n_g,
-                       static_cast<const uint16_t*>(R), static_cast<const uint16_t*>(L), kR, kL,
-                       va, vg, vr, vl, chunks, part);
-  } else {
-    auto k = two ? kron_proj_kernel<PjF32, false, 2> : kron_proj_kernel<PjF32, false, 1>;
-    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, static_cast<const float*>(A), nullptr,
-                       int64_t{0}, static_cast<const float*>(G), T, n_a, n_g,
-                       static_cast<const float*>(R), static_cast<const float*>(L), kR, kL, va,
-                       vg, vr, vl, chunks, part);
-  }
-  int rc = check_launch("kron_proj_kernel");
+  int rc = dtype == GS_DTYPE_BF16
+               ? launch_pj<PjBF16, false>(A, nullptr, 0, G, B, T, n_a, n_g, R, L, kR, kL, va, vg,
+                                          vr, vl, chunks, part, s)
+               : launch_pj<PjF32, false>(A, nullptr, 0, G, B, T, n_a, n_g, R, L, kR, kL, va, vg,
+                                         vr, vl, chunks, part, s);
   if (rc) return rc;
   return kron_finish(part, B, chunks, kL * kR, scale, out, out_dtype, s);
 }
@@ -336,8 +371,6 @@ extern "C" int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, 
   if (B <= 0 || T <= 0 || n_g <= 0 || vocab <= 0 || k_i <= 0 || k_o <= 0 || ids == nullptr ||
       G == nullptr || P_iT == nullptr || P_o == nullptr || out == nullptr)
     return fail(GS_ERR_INVALID, "gs_kron_embed_proj: invalid arguments");
-  if (k_i > PJ_KMAX || k_o > PJ_KMAX)
-    return fail(GS_ERR_UNSUPPORTED, "gs_kron_embed_proj: k_i and k_o must be <= 32");
   const int64_t chunks = pj_cdiv(T, PJ_TOK);
   if (workspace == nullptr || workspace_bytes < gs_kron_proj_workspace(B, T, k_i, k_o) - 256)
     return fail(GS_ERR_WORKSPACE, "gs_kron_embed_proj: workspace too small");
@@ -349,22 +382,11 @@ extern "C" int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, 
   const size_t esz = elem_size(dtype);
   const int vg = al16(G) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
   const int vl = al16(P_o) && (n_g * static_cast<int64_t>(esz)) % 16 == 0;
-  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(B));
-  const bool two = k_o > 16;  // the gathered side needs no projection blocks
-  if (dtype == GS_DTYPE_BF16) {
-    auto k = two ? kron_proj_kernel<PjBF16, true, 2> : kron_proj_kernel<PjBF16, true, 1>;
-    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, nullptr, ids, vocab,
-                       static_cast<const uint16_t*>(G), T, int64_t{0}, n_g,
-                       static_cast<const uint16_t*>(P_iT), static_cast<const uint16_t*>(P_o), k_i,
-                       k_o, 0, vg, 0, vl, chunks, part);
-  } else {
-    auto k = two ? kron_proj_kernel<PjF32, true, 2> : kron_proj_kernel<PjF32, true, 1>;
-    hipLaunchKernelGGL(k, grid, dim3(PJ_THREADS), 0, s, nullptr, ids, vocab,
-                       static_cast<const float*>(G), T, int64_t{0}, n_g,
-                       static_cast<const float*>(P_iT), static_cast<const float*>(P_o), k_i, k_o,
-                       0, vg, 0, vl, chunks, part);
-  }
-  int rc = check_launch("kron_proj_kernel(gather)");
+  int rc = dtype == GS_DTYPE_BF16
+               ? launch_pj<PjBF16, true>(nullptr, ids, vocab, G, B, T, 0, n_g, P_iT, P_o, k_i,
+                                         k_o, 0, vg, 0, vl, chunks, part, s)
+               : launch_pj<PjF32, true>(nullptr, ids, vocab, G, B, T, 0, n_g, P_iT, P_o, k_i,
+                                        k_o, 0, vg, 0, vl, chunks, part, s);
   if (rc) return rc;
   return kron_finish(part, B, chunks, k_o * k_i, scale, out, out_dtype, s);
 }

@@ -221,9 +221,14 @@ def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tenso
     B_tr = B[:n_t].reshape(-1, B.shape[-1])
     if B_tr.dtype != A_tr.dtype:
         B_tr = B_tr.to(A_tr.dtype)
-    grad = torch.mm(B_tr.t(), A_tr)
-    grad.mul_(scale / n_t)
-    return grad
+    return _scaled_mm(B_tr.t(), A_tr, scale / n_t)
+
+
+def _scaled_mm(x: torch.Tensor, y: torch.Tensor, alpha: float) -> torch.Tensor:
+    """alpha * x @ y with alpha applied in the GEMM's fp32 epilogue: one rounding to the
+    output dtype and no second pass over the result."""
+    return torch.addmm(torch.zeros((), dtype=x.dtype, device=x.device), x, y, beta=0.0,
+                       alpha=alpha)
 
 
 # Embedding Layer ###########################################################################
@@ -251,23 +256,26 @@ APPLIED = object()
 
 def _compute_embedding_train_grad(layer: nn.Embedding, A: torch.Tensor, B: torch.Tensor,
                                   val_batch_size: int, scale: float = 1.0):
-    """scale * index_add of the train rows / n_train (reference :214-235).  When the weight
-    already holds a train gradient (a tied lm_head's, computed earlier in backward) the rows
-    are added into it directly, which saves the reference's [vocab, d] zero-fill and the
-    full-table add; returns APPLIED then."""
+    """scale * (sum of the train rows per token id) / n_train (reference :214-235), summed
+    in fp32 and rounded once to the weight dtype (the reference accumulates with index_add_
+    in the weight dtype).  The kernel writes every row of a fresh gradient once (no
+    zero-fill and full-table scale); when the weight already holds a train gradient (a tied
+    lm_head's, computed earlier in backward) it adds the touched rows into that tensor and
+    this returns APPLIED."""
     n_t = A.size(0) - val_batch_size
     if n_t <= 0:
         return None
-    ids = A[:n_t].long().reshape(-1)
-    rows = B[:n_t].reshape(-1, B.shape[-1])
+    B = B.detach()
+    if B.dtype not in (torch.bfloat16, torch.float32):
+        B = B.float()
     prev = getattr(layer.weight, "train_grad", None)
     if prev is not None and prev.shape == layer.weight.shape:
         _overlap.join(prev.device)   # prev may come from the side stream
-        prev.index_add_(0, ids, rows.to(prev.dtype), alpha=scale / n_t)
+        ops().embedding_train_grad(A.detach(), B, val_batch_size, scale / n_t, prev,
+                                   accumulate=True)
         return APPLIED
-    grad = torch.zeros_like(layer.weight)
-    grad.index_add_(0, ids, rows.to(grad.dtype))
-    grad.mul_(scale / n_t)
+    grad = torch.empty_like(layer.weight)
+    ops().embedding_train_grad(A.detach(), B, val_batch_size, scale / n_t, grad)
     return grad
 
 
@@ -357,9 +365,7 @@ def _compute_Conv1D_train_grad(layer, A: torch.Tensor, B: torch.Tensor, val_batc
     n_t = A.size(0) - val_batch_size
     A_tr = A[:n_t].reshape(-1, A.shape[-1])
     B_tr = B[:n_t].reshape(-1, B.shape[-1]).to(A_tr.dtype)
-    grad = torch.mm(A_tr.t(), B_tr)
-    grad.mul_(scale / n_t)
-    return grad
+    return _scaled_mm(A_tr.t(), B_tr, scale / n_t)
 
 
 # Conv2d ###################################################################################
@@ -411,9 +417,8 @@ def _compute_conv2d_train_grad(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tenso
         return None
     dt = A.dtype if A.dtype in (torch.bfloat16, torch.float32) else torch.float32
     A_rows, B_rows = _conv2d_rows(layer, A[:n_t], B[:n_t], dt)
-    grad = torch.mm(B_rows.reshape(-1, B_rows.shape[-1]).t(),
-                    A_rows.reshape(-1, A_rows.shape[-1]))
-    grad.mul_(scale / n_t)
+    grad = _scaled_mm(B_rows.reshape(-1, B_rows.shape[-1]).t(),
+                      A_rows.reshape(-1, A_rows.shape[-1]), scale / n_t)
     return grad.view_as(layer.weight).to(layer.weight.dtype)
 
 

@@ -222,7 +222,7 @@ def embedding_dot_exact(ids: torch.Tensor, B: torch.Tensor, n_val: int,
     n_t = tr_i.shape[0]
     vi = va_i.reshape(-1)
     vb = va_b.reshape(-1, d)
-    out = torch.empty(n_t, dtype=torch.float64)
+    out = torch.empty(n_t, dtype=torch.float64, device=B.device)
     for i in range(n_t):
         mask = (tr_i[i][:, None] == vi[None, :]).double()       # [T, n_val*T]
         gram = tr_b[i] @ vb.T                                     # [T, n_val*T]
@@ -445,6 +445,24 @@ def kron_embed_proj_exact(ids: torch.Tensor, g: torch.Tensor, P_i: torch.Tensor,
     W.scatter_add_(2, ids2.unsqueeze(1).expand(bs, g3.shape[-1], ids2.shape[1]),
                    g3.transpose(1, 2))
     return scale * torch.einsum('od,bdv,iv->boi', P_o.double(), W, P_i.double())
+
+
+def kron_embed_proj_projfirst_exact(ids: torch.Tensor, g: torch.Tensor, P_i: torch.Tensor,
+                                    P_o: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """kron_embed_proj_exact with the projections applied first: per sample
+    scale * (G_b P_o^T)^T P_i[:, ids_b]^T.  Float64, 2-D products one sample at a time, on
+    whichever device holds g (no [vocab]-wide per-sample gradient is formed)."""
+    bs = ids.shape[0]
+    ids2 = ids.reshape(bs, -1).long()
+    g3 = g.reshape(bs, ids2.shape[1], g.shape[-1])
+    P_iT = P_i.double().to(g3.device).t()
+    P_o = P_o.double().to(g3.device)
+    outs = []
+    for b in range(bs):
+        left = torch.mm(g3[b].double(), P_o.t())      # [T, k_o]
+        right = P_iT[ids2[b].to(g3.device)]           # [T, k_i]
+        outs.append(scale * torch.mm(left.t(), right))
+    return torch.stack(outs)
 
 
 def choose_ki_ko(n_i: int, n_o: int, k_total: int, k_min: int = 1):

@@ -49,6 +49,22 @@ class OracleOps:
         self.calls.append(("embedding_dot", tuple(G.shape)))
         return R.embedding_dot_exact(ids, G.float(), n_val, val_start).float()
 
+    def embedding_train_grad(self, ids, G, n_val, scale, out, *, accumulate=False,
+                             val_start=None):
+        self.calls.append(("embedding_train_grad", tuple(G.shape)))
+        N, d = G.shape[0], G.shape[-1]
+        tr_i, _ = R.split_rows(ids.reshape(N, -1).long(), n_val, val_start)
+        tr_g, _ = R.split_rows(G.double().reshape(N, -1, d), n_val, val_start)
+        g = torch.zeros(out.shape, dtype=torch.float64)
+        g.index_add_(0, tr_i.reshape(-1), tr_g.reshape(-1, d))
+        g *= scale
+        if accumulate:
+            touched = torch.zeros(out.shape[0], dtype=torch.bool)
+            touched[tr_i.reshape(-1)] = True
+            out[touched] = (out[touched].double() + g[touched]).to(out.dtype)
+        else:
+            out.copy_(g.to(out.dtype))
+
     def layernorm_dot(self, X, G, n_val, eps, *, val_start=None, want_dot=True, want_bias=True,
                       grad_scale=None, grad_dtype=None):
         self.calls.append(("layernorm_dot", tuple(X.shape)))

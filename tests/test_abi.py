@@ -46,7 +46,7 @@ def test_invalid_arguments_return_status_and_message():
                             None, 0, None) == -1
     assert lib.gs_kron_proj(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 1, 1, 4, 4,
                             ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 40, 4, 0, 1.0,
-                            ctypes.c_void_p(16), 1, None, 0, None) == -5  # k > 32
+                            ctypes.c_void_p(16), 1, None, 0, None) == -3  # k = 40: needs ws
     assert lib.gs_layernorm_dot(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 4, 1, 3, 2, 4096,
                                 1e-5, None, None, None, None, 1, 1.0, None, 0, None) == -5
 
@@ -74,3 +74,4 @@ def test_cpu_tensors_are_rejected_loudly():
     import torch
     with pytest.raises(_native.GhostHipError, match="ROCm GPU"):
         _native.HipOps().linear_dot(torch.zeros(4, 3, 8), torch.zeros(4, 3, 8), 1)
+

@@ -85,6 +85,60 @@ def test_embedding_positions_and_all_equal_ids(gpu):
     assert_close(dot2.cpu(), tr.sum(1) @ va.sum((0, 1)), FP32_TOL, "all-equal ids")
 
 
+def _emb_grad_exact(ids, G, n_val, vs, vocab, scale):
+    N, d = G.shape[0], G.shape[-1]
+    tr_i, _ = R.split_rows(ids.reshape(N, -1).long(), n_val, vs)
+    tr_g, _ = R.split_rows(G.double().reshape(N, -1, d), n_val, vs)
+    keep = (tr_i >= 0) & (tr_i < vocab)
+    g = torch.zeros(vocab, d, dtype=torch.float64)
+    g.index_add_(0, tr_i[keep], tr_g[keep])
+    touched = torch.zeros(vocab, dtype=torch.bool)
+    touched[tr_i[keep]] = True
+    return g * scale, touched
+
+
+@pytest.mark.parametrize("gdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [
+    # N, n_val, T, d, vocab
+    (6, 2, 5, 24, 11),            # many tokens per id
+    (20, 4, 1024, 768, 50257),    # GPT-2 wte: 16 train rows of 1024 tokens
+    (10, 2, 2048, 2048, 50304),   # Pythia wte
+    (7, 3, 33, 20, 3000),         # d not a multiple of 8: scalar loads
+    (5, 1, 1024, 64, 1),          # every token the same id: one 4096-token segment
+])
+def test_embedding_train_grad(gpu, gdt, odt, shape):
+    """gs_embedding_train_grad against float64 index_add of the train rows: overwrite mode
+    (every row written, zeros where no train token has the id) and accumulate mode (only the
+    touched rows change), val block in the middle, out-of-range ids skipped, bit-identical on
+    a second run."""
+    N, n_val, T, d, vocab = shape
+    ids = torch.randint(0, vocab, (N, T), generator=gen(80 + T))
+    ids[0, :3] = -1
+    ids[-1, -2:] = vocab + 5
+    G = randn((N, T, d), 81 + T, 1e-2, gdt)
+    vs = 1 if N - n_val > 1 else 0
+    scale = N / (N - n_val)
+    print(f"embedding train grad shape={shape} G {gdt} out {odt}", flush=True)
+    idd, Gd = ids.to(gpu), G.to(gpu)
+    out = torch.full((vocab, d), float("nan"), dtype=odt, device=gpu)
+    _native.ops().embedding_train_grad(idd, Gd, n_val, scale, out, val_start=vs)
+    want, touched = _emb_grad_exact(ids, G, n_val, vs, vocab, scale)
+    tol = 1e-2 if odt == torch.bfloat16 else FP32_TOL
+    got = out.cpu()
+    assert_close(got, want, tol, "overwrite")
+    assert torch.all(got[~touched] == 0)
+    again = torch.empty_like(out)
+    _native.ops().embedding_train_grad(idd, Gd, n_val, scale, again, val_start=vs)
+    assert torch.equal(again, out)
+    prev = randn((vocab, d), 82, 1e-2, odt)
+    acc = prev.to(gpu)
+    _native.ops().embedding_train_grad(idd, Gd, n_val, scale, acc, accumulate=True, val_start=vs)
+    got = acc.cpu()
+    assert torch.equal(got[~touched], prev[~touched])
+    assert_close(got, prev.double() + want, tol, "accumulate")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100),
                                    (3, 1, 130, 1024), (4, 2, 64, 1600)])
@@ -113,6 +167,12 @@ def test_layernorm_dots_and_grads(gpu, dtype, shape):
     (4, 130, 256, 512, 16, 16),
     (2, 64, 96, 384, 28, 9),
     (2, 3, 1, 10, 1, 8),
+    # the reference's own rank settings (choose_ki_ko, projection_utils.py:12-66):
+    (3, 100, 768, 3072, 43, 12),     # fc at rank 512, k_min 8
+    (3, 100, 3072, 768, 11, 47),     # fc_out at rank 512
+    (2, 70, 1024, 4096, 64, 16),     # fc at rank 1024 (64-row slice boundary)
+    (2, 70, 1024, 50257, 157, 8),    # lm_head at rank 512: three 64-row slices of P_i
+    (2, 33, 200, 300, 70, 130),      # more than 64 rows on both sides
 ])
 @pytest.mark.parametrize("conv1d", [False, True])
 def test_kron_projection(gpu, dtype, conf, conv1d):
@@ -144,6 +204,9 @@ def test_kron_projection(gpu, dtype, conf, conv1d):
     (4, 130, 50257, 768, 16, 16),    # GPT-2 vocabulary, two token chunks + a tail
     (2, 64, 1000, 100, 32, 32),      # d not a multiple of 8: scalar G loads
     (5, 1, 7, 8, 1, 3),
+    (3, 130, 50257, 768, 4, 64),     # wte at the reference's default rank 256, k_min 4
+    (2, 70, 50257, 1024, 8, 128),    # wte at rank 1024: two 64-row slices of P_o
+    (2, 40, 3000, 96, 100, 5),       # gathered side wider than 64 columns
 ])
 def test_kron_embedding_projection(gpu, dtype, conf):
     B, T, V, d, k_i, k_o = conf

@@ -87,10 +87,12 @@ def _expected_lm(model, cap, n_t, n_v):
     N = n_t + n_v
     s = N / n_t   # the train grads average the N-scaled backprops over the train rows
     names = _param_names(model)
-    dots, grads = {}, {}
+    dots, grads, mags = {}, {}, {}
 
     def add(name, g):
+        # mags: the sum of the contributions' magnitudes (a tied weight gets two)
         grads[name] = grads[name] + g if name in grads else g
+        mags[name] = mags[name] + g.abs() if name in mags else g.abs()
 
     for mname, m in model.named_modules():
         if mname not in cap.A:
@@ -118,7 +120,17 @@ def _expected_lm(model, cap, n_t, n_v):
             xh = F.layer_norm(_train_rows(A, n_t).double(), (A.shape[-1],), eps=m.eps)
             add(wname, s * (_train_rows(B, n_t).double() * xh).sum(0))
             add(names[id(m.bias)], s * _train_rows(B, n_t).double().sum(0))
-    return dots, grads
+    return dots, grads, mags
+
+
+def _close_to_sum(got, want, mag, tol, what):
+    """|got - want| <= tol * max(mag, rms(want)) elementwise, mag = the summed magnitudes of
+    the addends: the rounding bound of a sum of separately rounded contributions."""
+    got = got.double()
+    rms = want.pow(2).mean().sqrt().item()
+    worst = ((got - want).abs() / torch.clamp(mag, min=max(rms, 1e-300))).max().item()
+    assert worst <= tol, f"{what}: worst error {worst:.3e} of the addends' size > {tol:.1e}"
+    return worst
 
 
 def _lm_step(model, X, Y, n_t, n_v, **options):
@@ -143,7 +155,12 @@ def _lm_step(model, X, Y, n_t, n_v, **options):
 
 
 def _check_lm(model, dots, grads, total, cap, n_t, n_v):
-    want_dots, want_grads = _expected_lm(model, cap, n_t, n_v)
+    want_dots, want_grads, mags = _expected_lm(model, cap, n_t, n_v)
+    contributions = {}
+    for mname, m in model.named_modules():
+        if mname in cap.A:
+            pid = _param_names(model)[id(m.weight)]
+            contributions[pid] = contributions.get(pid, 0) + 1
     assert sorted(dots) == sorted(want_dots), (sorted(dots), sorted(want_dots))
     for name in sorted(want_dots):
         worst = assert_close(dots[name], want_dots[name], BF16_TOL, f"dot {name}")
@@ -153,7 +170,11 @@ def _check_lm(model, dots, grads, total, cap, n_t, n_v):
                        if p.initially_requires_grad and "dummy_bias" not in n)
     assert sorted(grads) == trainable and sorted(want_grads) == trainable
     for name in trainable:
-        worst = assert_close(grads[name], want_grads[name], BF16_TOL, f"grad {name}")
+        if contributions.get(name, 1) > 1:   # a tied weight: Linear + Embedding train grads
+            worst = _close_to_sum(grads[name], want_grads[name], mags[name], BF16_TOL,
+                                  f"grad {name}")
+        else:
+            worst = assert_close(grads[name], want_grads[name], BF16_TOL, f"grad {name}")
         _say(f"  grad {name}: worst {worst:.2e}")
 
 
@@ -327,6 +348,48 @@ def test_config3_gradproj_gpt2_medium(gpu, tmp_path):
     assert_close(full.double(), torch.cat([wants[n] for n in sorted(wants)], dim=1), BF16_TOL,
                  "collected batch")
     assert full.dtype == torch.float16 and full.shape == (B, 96 * 256)
+    eng.detach()
+
+
+def test_config3_gradproj_reference_ranks(gpu, tmp_path):
+    """The same model and batch with the projection sizes the reference's choose_ki_ko picks
+    at its documented --proj_rank_total 512, k_min 8 (Examples/GradProj_LM/README.md:67),
+    embeddings included: (39, 13) qkv, (23, 22) proj, (43, 12) fc, (11, 47) fc_out, (8, 64)
+    wte, (23, 22) wpe; every layer against the float64 projection-first closed forms."""
+    torch.manual_seed(0)
+    B, T = 32, 1024
+    with torch.device(gpu):
+        model = CausalLM(GPT2_MEDIUM).to(BF16)
+    X, Y = synthetic_tokens(B, T, GPT2_MEDIUM.vocab, seed=78, device=gpu)
+    eng = GradProjLoraEngine(model, proj_layers="h.,wte,wpe", proj_rank_total=512,
+                             proj_rank_min=8, proj_seed=42, proj_dtype="float16",
+                             proj_dir=str(tmp_path), include_embeddings=True)
+    dims = eng.projection_dims
+    assert dims["h.0.qkv"] == (39, 13) and dims["h.0.fc"] == (43, 12)
+    assert dims["h.0.fc_out"] == (11, 47) and dims["wte"] == (8, 64)
+    eng.attach()
+    cap = HookCapture(model, (nn.Linear, nn.Embedding), names=set(eng.matched_layers))
+    _say("config3 reference ranks step")
+    model(X, Y).backward()
+    torch.cuda.synchronize()
+    per_layer = {n: l._ghost_grad_proj.clone() for n, l in eng.matched_layers.items()}
+    full = eng.collect_batch()
+    torch.cuda.synchronize()
+    cap.remove()
+    wants = {}
+    for name in sorted(eng.matched_layers):
+        P_i, P_o = eng.projection_matrices[name]
+        if isinstance(eng.matched_layers[name], nn.Embedding):
+            want = R.kron_embed_proj_projfirst_exact(cap.A[name], cap.B[name], P_i.to(BF16),
+                                                     P_o.to(BF16))
+        else:
+            want = R.kron_proj_projfirst_exact(cap.A[name], cap.B[name], P_i.to(BF16),
+                                               P_o.to(BF16), float(B))
+        worst = assert_close(per_layer[name], want, BF16_TOL, f"proj {name}")
+        _say(f"  proj {name} {tuple(per_layer[name].shape[1:])}: worst {worst:.2e}")
+        wants[name] = want.reshape(B, -1)
+    assert_close(full.double(), torch.cat([wants[n] for n in sorted(wants)], dim=1), BF16_TOL,
+                 "collected batch")
     eng.detach()
 
 

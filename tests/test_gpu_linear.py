@@ -30,32 +30,13 @@ def _inputs(N, T, d_in, d_out, seed, dtype):
     return A, G
 
 
-@pytest.fixture
-def v_gemm_native():
-    saved = _native.V_GEMM
-    _native.V_GEMM = "native"
-    yield
-    _native.V_GEMM = saved
-
-
-@pytest.fixture(params=["library", "native"])
-def v_gemm(request):
-    saved = _native.V_GEMM
-    _native.V_GEMM = request.param
-    yield request.param
-    _native.V_GEMM = saved
-
-
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("algo", [_native.ALGO_GHOST, _native.ALGO_VALGRAD])
 @pytest.mark.parametrize("semantics", ["pairwise", "presum"])
-def test_linear_dot_matches_closed_form(gpu, v_gemm, shape, dtype, algo, semantics):
+def test_linear_dot_matches_closed_form(gpu, shape, dtype, algo, semantics):
     N, n_val, T, d_in, d_out = shape
-    if algo == _native.ALGO_GHOST and v_gemm == "library":
-        pytest.skip("the V GEMM choice only affects VALGRAD")
-    print(f"linear_dot shape={shape} dtype={dtype} algo={algo} sem={semantics} v={v_gemm}",
-          flush=True)
+    print(f"linear_dot shape={shape} dtype={dtype} algo={algo} sem={semantics}", flush=True)
     A, G = _inputs(N, T, d_in, d_out, 100 + N + T, dtype)
     sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
     dot, _ = _native.ops().linear_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem, algo=algo)
@@ -202,18 +183,24 @@ def test_linear_val_gradient_matches_closed_form(gpu, shape, dtype, semantics):
 @pytest.mark.parametrize("shape", [(6, 2, 256, 128, 256), (5, 1, 512, 64, 512),
                                    (4, 1, 256, 768, 768)])
 @pytest.mark.parametrize("semantics", ["pairwise", "presum"])
-def test_linear_bias_fused_matches_closed_forms(gpu, v_gemm, shape, semantics):
-    """gs_linear_rowdot_bias: weight dot, bias dot and bias train gradient in one pass."""
+@pytest.mark.parametrize("caller_v", [False, True])
+def test_linear_bias_fused_matches_closed_forms(gpu, caller_v, shape, semantics):
+    """Weight dot, bias dot and bias train gradient in one pass: gs_linear_bias_dot, and
+    gs_linear_rowdot_bias with a V the caller formed (here a float64 val term rounded to
+    bf16)."""
     N, n_val, T, d_in, d_out = shape
     A, G = _inputs(N, T, d_in, d_out, 400 + T, torch.bfloat16)
     scale = N / (N - n_val) / 7.0
-    if semantics == "presum" and v_gemm == "library":
-        pytest.skip("the V GEMM choice only affects the pairwise semantics")
-    print(f"linear_bias_dot shape={shape} sem={semantics} v={v_gemm}", flush=True)
+    print(f"linear_bias_dot shape={shape} sem={semantics} caller_v={caller_v}", flush=True)
     sem = _native.SEM_PAIRWISE_SUM if semantics == "pairwise" else _native.SEM_PRESUM
-    res = _native.ops().linear_bias_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem,
-                                        algo=_native.ALGO_VALGRAD, grad_scale=scale,
-                                        grad_dtype=torch.float32)
+    if caller_v:
+        V = R.val_term_exact(A, G, n_val, semantics).to(torch.bfloat16)
+        res = _native.ops().linear_rowdot_bias(A.to(gpu), G.to(gpu), V.to(gpu), n_val,
+                                               grad_scale=scale, grad_dtype=torch.float32)
+    else:
+        res = _native.ops().linear_bias_dot(A.to(gpu), G.to(gpu), n_val, semantics=sem,
+                                            algo=_native.ALGO_VALGRAD, grad_scale=scale,
+                                            grad_dtype=torch.float32)
     assert res is not None
     dot, bdot, bgrad = res
     torch.cuda.synchronize()
@@ -248,7 +235,7 @@ def test_rowdot_192_row_tiles(gpu, shape, semantics):
 @pytest.mark.parametrize("shape", [(12, 4, 256, 768, 3072), (6, 2, 256, 256, 1000),
                                    (6, 2, 512, 1280, 1536), (82, 2, 256, 768, 1024)])
 @pytest.mark.parametrize("semantics", ["pairwise", "presum"])
-def test_valgrad_over_d_out(gpu, v_gemm_native, shape, semantics):
+def test_valgrad_over_d_out(gpu, shape, semantics):
     """d_out > d_in: the val-gradient row-dot runs over K = d_out (V^T, Z = the train rows of
     A) and the fused bias pass sums the train rows of G inside its mainloop.  192-row tiles
     over d_in 768 (each token tile's rows split 64/64/64/64 over 4 workgroups); one 256-row

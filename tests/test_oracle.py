@@ -240,6 +240,8 @@ def test_embedding_projection_forms_match_per_sample_gradients():
     # an embedding is a Linear layer on one-hot inputs: the dense identity gives the same
     onehot = torch.nn.functional.one_hot(ids, V).double()
     assert_close(R.kron_proj_exact(onehot, g, P_i, P_o, 1.0), naive, 1e-10, "one-hot dense")
+    assert_close(R.kron_embed_proj_projfirst_exact(ids, g, P_i, P_o), naive, 1e-10,
+                 "projection first")
 
 
 # ------------------------------------------------------------------ Conv2d

@@ -50,6 +50,10 @@ _SIGNATURES = {
     "gs_linear_dot_algo": (_I, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I, _I]),
     "gs_linear_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I,
                            _P, _P, _P, _SZ, _P]),
+    "gs_linear_dot_noalloc_bytes": (_SZ, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                                         _I]),
+    "gs_linear_dot_noalloc": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I,
+                                   _I, _P, _P, _P]),
     "gs_bias_dot_workspace": (_SZ, [_I64, _I64, _I64]),
     "gs_bias_dot": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _P, _I, _F, _P, _SZ, _P]),
     "gs_embedding_dot_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
@@ -200,6 +204,34 @@ class HipOps:
                                ws.data_ptr(), ws_bytes, _stream(dev))
         _check(rc, "gs_linear_dot")
         return out, pair
+
+    def linear_dot_noalloc(self, A: torch.Tensor, G: torch.Tensor, n_val: int,
+                           out: torch.Tensor, pair: Optional[torch.Tensor] = None, *,
+                           val_start=None, semantics: int = SEM_PAIRWISE_SUM,
+                           algo: int = ALGO_AUTO, rounding: int = ROUND_FP32) -> None:
+        """gs_linear_dot_noalloc into caller-given outputs (out [n_train], pair [n_val,
+        n_train] or None); nothing is allocated (A and G must be contiguous)."""
+        _require_device(A, G, out, pair)
+        if not (A.is_contiguous() and G.is_contiguous() and out.is_contiguous()):
+            raise GhostHipError("linear_dot_noalloc: A, G and out must be contiguous")
+        if A.dtype != G.dtype:
+            raise GhostHipError(f"A and G dtypes differ: {A.dtype} vs {G.dtype}")
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T:
+            raise GhostHipError(f"A {tuple(A.shape)} and G {tuple(G.shape)} token counts differ")
+        n_t = N - n_val
+        if out.dtype != torch.float32 or out.numel() != n_t or \
+                (pair is not None and (pair.dtype != torch.float32 or
+                                       pair.numel() != n_val * n_t)):
+            raise GhostHipError("linear_dot_noalloc: outputs must be fp32 [n_train] and "
+                                "[n_val, n_train]")
+        vs = N - n_val if val_start is None else int(val_start)
+        rc = load_library().gs_linear_dot_noalloc(
+            A.data_ptr(), G.data_ptr(), _gs_dtype(A), N, n_val, vs, T, d_in, d_out, semantics,
+            algo, rounding, out.data_ptr(), _ptr(pair), _stream(A.device))
+        _check(rc, "gs_linear_dot_noalloc")
 
     def linear_val_gradient(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
                             val_start=None, semantics: int = SEM_PAIRWISE_SUM) -> torch.Tensor:

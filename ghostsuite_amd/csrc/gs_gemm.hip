@@ -20,6 +20,7 @@
 // k-slice selected by l / 32; result element e of lane l is C[8*(e/4) + 4*(l/32) + e%4][l%32].
 
 #include <algorithm>
+#include <mutex>
 #include <cmath>
 #include <type_traits>
 
@@ -2441,6 +2442,86 @@ extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N,
   Carver cv(workspace, workspace_bytes);
   return run_linear_any(A, G, dtype, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
                         out_dot, out_pair, pl, cv, static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------ allocation-free variant
+// gs_linear_dot_noalloc's scratch memory: a file-scope device array, one copy on every GPU
+// the library runs on, held until the process ends.  Host code never uses the array's name
+// as an address (on the host it is only a stand-in for the symbol): the device address comes
+// from hipGetSymbolAddress, looked up once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[GS_LINEAR_NOALLOC_SCRATCH_BYTES];
+
+namespace gs {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the current device, which must be the stream's device.
+int scratch_address(hipStream_t s, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(GS_ERR_LAUNCH, std::string("hipGetDevice: ") +
+                                                      hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(GS_ERR_UNSUPPORTED, "gs_linear_dot_noalloc: device index above 63");
+  if (s != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(s, &sdev);
+    if (e != hipSuccess) return fail(GS_ERR_LAUNCH, std::string("hipStreamGetDevice: ") +
+                                                        hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(GS_ERR_INVALID,
+                  "gs_linear_dot_noalloc: the stream belongs to another device than the "
+                  "current one");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(GS_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") +
+                                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GS_OK;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_dot_noalloc_bytes(const void* A, const void* G, int dtype,
+                                              int64_t N, int64_t n_val, int64_t T, int64_t d_in,
+                                              int64_t d_out, int semantics, int algo,
+                                              int want_pair) {
+  if (!linear_args_ok(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair)) return 0;
+  const LinearPlan pl = plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair);
+  return linear_bytes(dtype, pl, n_val, T, d_in, d_out, semantics, A, G);
+}
+
+extern "C" int gs_linear_dot_noalloc(const void* A, const void* G, int dtype, int64_t N,
+                                     int64_t n_val, int64_t val_start, int64_t T, int64_t d_in,
+                                     int64_t d_out, int semantics, int algo, int rounding,
+                                     float* out_dot, float* out_pair, void* stream) {
+  const int want_pair = out_pair != nullptr;
+  int rc = check_linear_args("gs_linear_dot_noalloc", A, G, dtype, N, n_val, val_start, T,
+                             d_in, d_out, semantics, algo, rounding, out_dot, want_pair);
+  if (rc) return rc;
+  const LinearPlan pl = plan_any(dtype, N, n_val, T, d_in, d_out, semantics, algo, want_pair);
+  const size_t need = linear_bytes(dtype, pl, n_val, T, d_in, d_out, semantics, A, G);
+  if (need > GS_LINEAR_NOALLOC_SCRATCH_BYTES)
+    return fail(GS_ERR_UNSUPPORTED,
+                "gs_linear_dot_noalloc: the call needs " + std::to_string(need) +
+                    " bytes of scratch, above the fixed " +
+                    std::to_string(GS_LINEAR_NOALLOC_SCRATCH_BYTES) +
+                    " (use gs_linear_dot with a workspace)");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ptr = nullptr;
+  rc = scratch_address(s, &ptr);
+  if (rc) return rc;
+  Carver cv(ptr, GS_LINEAR_NOALLOC_SCRATCH_BYTES);
+  return run_linear_any(A, G, dtype, N, n_val, val_start, T, d_in, d_out, semantics, rounding,
+                        out_dot, out_pair, pl, cv, s);
 }
 
 // ------------------------------------------------------------------ val gradient V

@@ -94,6 +94,27 @@ int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_
                   int algo, int rounding, float* out_dot, float* out_pair, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of gs_linear_dot.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, semantics, kernels and results
+ * as gs_linear_dot, without (workspace, workspace_bytes): the scratch memory is a fixed
+ * device array of GS_LINEAR_NOALLOC_SCRATCH_BYTES inside the library, one copy per GPU, held
+ * until the process ends.  The call allocates nothing and frees nothing.
+ *   - `stream` must belong to the current device (NULL = its default stream).
+ *   - A call that needs more scratch than the array holds returns GS_ERR_UNSUPPORTED
+ *     (gs_linear_dot_noalloc_bytes tells the need; use gs_linear_dot with a workspace then).
+ *   - Every call on one GPU uses the same array and leaves its contents behind (nothing in
+ *     it needs to start at zero).  Calls that overlap on one GPU -- on two streams, or from
+ *     two threads without ordering -- race on it: serialise them. */
+#define GS_LINEAR_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+size_t gs_linear_dot_noalloc_bytes(const void* A, const void* G, int dtype, int64_t N,
+                                   int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
+                                   int semantics, int algo, int want_pair);
+int gs_linear_dot_noalloc(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                          int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                          int semantics, int algo, int rounding, float* out_dot,
+                          float* out_pair, void* stream);
+
 /* The val term of a Linear layer's dot, V [d_out, d_in] (dtype; fp32 accumulation):
  *   GS_SEM_PAIRWISE_SUM: V = sum over the val rows and tokens of g a^T
  *   GS_SEM_PRESUM:       V = gbar^T abar, gbar / abar = the val rows summed over the val

@@ -75,3 +75,25 @@ def test_cpu_tensors_are_rejected_loudly():
     with pytest.raises(_native.GhostHipError, match="ROCm GPU"):
         _native.HipOps().linear_dot(torch.zeros(4, 3, 8), torch.zeros(4, 3, 8), 1)
 
+
+def test_noalloc_rejects_calls_beyond_its_scratch_before_touching_the_device():
+    """gs_linear_dot_noalloc checks its fixed scratch size on the host: a call that needs
+    more (the GPT-2 lm_head shape, 472 MiB) fails with GS_ERR_UNSUPPORTED and a message
+    naming the need, before any HIP call."""
+    lib = _native.load_library()
+    P16 = ctypes.c_void_p(256)
+    need = lib.gs_linear_dot_noalloc_bytes(P16, P16, 0, 20, 4, 1024, 768, 50257, 0, 2, 0)
+    assert need > (128 << 20)
+    rc = lib.gs_linear_dot_noalloc(P16, P16, 0, 20, 4, 16, 1024, 768, 50257, 0, 2, 0, P16,
+                                   None, None)
+    assert rc == -5
+    assert b"scratch" in lib.gs_last_error() and str(need).encode() in lib.gs_last_error()
+    # argument checks as gs_linear_dot's
+    assert lib.gs_linear_dot_noalloc(None, None, 0, 4, 1, 3, 4, 8, 8, 0, 0, 0, None, None,
+                                     None) == -1
+    assert lib.gs_linear_dot_noalloc(P16, P16, 7, 4, 1, 3, 4, 8, 8, 0, 0, 0, P16, None,
+                                     None) == -2
+    # the GPT-2-small block layers fit
+    for d_in, d_out, sem in ((768, 2304, 1), (768, 768, 1), (768, 3072, 0), (3072, 768, 0)):
+        assert 0 < lib.gs_linear_dot_noalloc_bytes(P16, P16, 0, 20, 4, 1024, d_in, d_out, sem,
+                                                   0, 0) <= (128 << 20)

@@ -58,8 +58,19 @@ class TimedOps:
         self.records.append((name, work, s, e))
         return out
 
+    def __getattr__(self, name):
+        # entry points without their own timing pass straight through
+        return getattr(self.inner, name)
+
     def linear_algo(self, *a, **k):
         return self.inner.linear_algo(*a, **k)
+
+    def embedding_train_grad(self, ids, G, n_val, scale, out, **k):
+        n_tr = (G.shape[0] - n_val) * (G.numel() // G.shape[0])
+        nbytes = (n_tr * G.element_size() + ids.numel() * 8 +
+                  out.numel() * out.element_size() * (2 if k.get("accumulate") else 1))
+        return self._run("embedding_train_grad", ("hbm", nbytes),
+                         self.inner.embedding_train_grad, ids, G, n_val, scale, out, **k)
 
     def linear_dot(self, A, G, n_val, **k):
         from ghostsuite_amd import _native
@@ -452,49 +463,105 @@ def ghost_sweep(dev, reps: int = 10):
 
 
 # ------------------------------------------------------------------ CPU baseline
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(budget_s: float = 20.0):
-    """The oracle's restatement of the reference op sequence (ghost dots + train grads) for
-    the hooked layers of one GPT-2-small block at the bench batch (N=20, T=1024, bf16), on
-    the host cores, scaled to 12 blocks; reported as train rows per second."""
+    """A whole GPT-2-small GradDotProd step (16 train + 4 val rows, T=1024, bf16) through
+    the reference's op sequence on the host cores: the oracle's restatement of every hooked
+    sampler (dots and train gradients: 48 block Linear layers, 25 LayerNorms, wte and wpe,
+    and the tied lm_head's ghost dot, which the reference computes before wte overwrites
+    it) plus the model's forward and input-gradient backward (the reference freezes the
+    weights and supplies their gradients from the hooks).  Timed on bounded samples, each
+    scaled by how its cost grows with the batch; reported as train rows per second."""
     from oracle import ghost_ref as R
+    from ghostsuite_amd.workloads import CausalLM, GPT2_SMALL, synthetic_tokens
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    N, n_val, T, d, m = 20, 4, 1024, 768, 3072
+    N, n_val, T, d, m, V = 20, 4, 1024, 768, 3072, GPT2_SMALL.vocab
+    n_t = N - n_val
     g = torch.Generator().manual_seed(0)
     bf = torch.bfloat16
 
     def rnd(*shape, s=1.0):
         return (torch.randn(*shape, generator=g) * s).to(bf)
 
+    def timed(fn, warm=False):
+        if warm:
+            fn()   # first-call allocations, for the short parts
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    parts = {}
     layers = [("qkv", d, 3 * d), ("proj", d, d), ("fc", d, m), ("fc_out", m, d)]
     acts = {n: (rnd(N, T, a), rnd(N, T, b, s=1e-3)) for n, a, b in layers}
-    ln_in = rnd(N, T, d)
-    ln_g = rnd(N, T, d, s=1e-3)
+    ln_in, ln_g = rnd(N, T, d), rnd(N, T, d, s=1e-3)
 
     def one_block():
         for name, a, b in layers:
             A, B = acts[name]
-            use_ghost = R.should_use_ghost(T, a * b)
-            R.linear_dot_ref(A, B, n_val, use_ghost)
+            R.linear_dot_ref(A, B, n_val, R.should_use_ghost(T, a * b))
             R.linear_train_grad(A, B * N, n_val)
         for _ in range(2):
             R.layernorm_dot_ref(ln_in, ln_g, n_val, 1e-5)
             R.layernorm_train_grad(ln_in, ln_g * N, n_val, 1e-5)
 
-    t0 = time.perf_counter()
-    one_block()
-    t_block = time.perf_counter() - t0
-    reps = 1
-    while time.perf_counter() - t0 + t_block < budget_s and reps < 3:
-        one_block()
-        reps += 1
-    t_block = (time.perf_counter() - t0) / reps
-    t_step = 12 * t_block
-    return {"value": 16.0 / t_step, "unit": "samples/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle reference-op sequence (Linear ghost/materialised dots + train "
-                       f"grads, 2 LayerNorm dots + grads) of one GPT-2-small block at N=20, "
-                       f"T=1024, bf16, x{reps} reps, {t_block:.2f} s/block, scaled to 12 "
-                       f"blocks; model fwd/bwd not included")}
+    parts["block_samplers_x12"] = 12 * timed(one_block, warm=True)
+    del acts
+    ids = torch.randint(0, V, (N, T), generator=g)
+    pos = torch.arange(T).repeat(N, 1)
+
+    def embeddings_and_ln_f():
+        for x, vocab in ((ids, V), (pos, T)):
+            R.embedding_dot_ref(x, ln_g, n_val, vocab)
+            R.embedding_train_grad(x, ln_g * N, n_val, (vocab, d))
+        R.layernorm_dot_ref(ln_in, ln_g, n_val, 1e-5)
+        R.layernorm_train_grad(ln_in, ln_g * N, n_val, 1e-5)
+
+    parts["embeddings_ln_f"] = timed(embeddings_and_ln_f, warm=True)
+    # lm_head ghost dot + train grad: cost grows with the train rows; sampled on 2 of 16.
+    k_tr = 2
+    A_lm = rnd(k_tr + n_val, T, d)
+    B_lm = rnd(k_tr + n_val, T, V, s=1e-4)
+    parts["lm_head_dot_and_grad"] = (n_t / k_tr) * timed(
+        lambda: (R.linear_dot_ref(A_lm, B_lm, n_val, True, has_bias=False),
+                 R.linear_train_grad(A_lm, B_lm * N, n_val)))
+    del A_lm, B_lm
+    # forward + input-gradient backward of the model: grows with the rows; sampled on 2.
+    torch.manual_seed(0)
+    model = CausalLM(GPT2_SMALL).to(bf)
+    for p in model.parameters():
+        p.requires_grad_(False)
+    X, Y = synthetic_tokens(1, T, V, seed=3)
+
+    def fwd_bwd():
+        x = model.wte(X).detach().requires_grad_(True)   # the dummy bias's role: a graph
+        h = x + model.wpe(torch.arange(T).repeat(1, 1))
+        for blk in model.h:
+            h = blk(h)
+        logits = model.lm_head(model.ln_f(h))
+        loss = torch.nn.functional.cross_entropy(logits.float().view(-1, V), Y.reshape(-1))
+        loss.backward()
+
+    parts["model_fwd_bwd"] = N * timed(fwd_bwd)
+    t_step = sum(parts.values())
+    return {"value": n_t / t_step, "unit": "samples/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "s_per_step": t_step,
+            "s_per_step_parts": {k: round(v, 3) for k, v in parts.items()},
+            "sample": ("oracle restatement of the reference's op sequence (torch CPU, bf16) for "
+                       "one GPT-2-small step at 16+4 rows, T=1024: one block's 4 Linear + 2 "
+                       "LayerNorm samplers timed at full size x12; wte, wpe, ln_f samplers at "
+                       "full size; the lm_head ghost dot + train grad on 2 of the 16 train rows "
+                       "x8; model forward + input-gradient backward on 1 row x20")}
 
 
 KERNEL_SHAPES = {
@@ -697,7 +764,19 @@ def main():
         "step_overhead": res["t_ghost"] / res["t_plain"],
         "rows_per_s_total": (res["n_train"] + res["n_val"]) / res["t_ghost"],
         "hot_path_ms_per_step": hot_ms,
+        "step_overhead_vs_train_rows_only": res["t_ghost"] / res["t_plain_train"],
+        "step_overhead_serialised_dots": res["t_serial"] / res["t_plain"],
         "roofline": roof,
+        "notes": {
+            "roofline_traffic": "HBM bytes per launch from profiles/traffic.json: rocprofv3 "
+                                "FETCH_SIZE / WRITE_SIZE runs of `bench.py --mode kernels` at "
+                                "the same shape, scaled by the 1 GiB copy calibration; not "
+                                "measured in this run",
+            "tied_lm_head_dot": "not computed: the reference computes the tied lm_head's "
+                                "ghost dot and then overwrites it with wte's "
+                                "(supported_layers_grad_samplers_dotprod.py:130 vs :211), so "
+                                "the outputs are identical without it",
+        },
         "ghost_kernel": {"shape": "A[32,1024,768] G[32,1024,3072] bf16, 8 val rows first",
                          "ms": gk["ms"], "achieved": gk["tflops"], "unit": "TFLOP/s",
                          "peak": PEAK_BF16 / 1e12, "frac": gk["frac"],

@@ -579,6 +579,10 @@ KERNEL_SHAPES = {
     "bias_fc": "bias_dot, G[20,1024,3072] bf16, 4 val",
     "layernorm": "layernorm_dot + grads, X,G[20,1024,768] bf16, 4 val",
     "embedding_wte": "embedding_dot, ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
+    "embedding_grad_tied": "embedding_train_grad accumulate (into a tied lm_head grad), "
+                           "ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
+    "embedding_grad_untied": "embedding_train_grad overwrite (every row written), ids[20,1024] "
+                             "vocab 50257, G[20,1024,768] bf16, 4 val",
     "kron_fc": "kron_proj, A[32,1024,1024] G[32,1024,4096] bf16, k=16x16",
     "kron_embed_wte": "kron_embed_proj, ids[32,1024] vocab 50257, G[32,1024,1024] bf16, k=16x16",
     "copy_1GiB": "device copy of 1 GiB (HBM calibration)",
@@ -639,6 +643,12 @@ def kernels_leg(dev, reps: int = 10):
     out["layernorm"] = timeit(lambda: ops.layernorm_dot(X, GL, 4, 1e-5, grad_scale=1.25))
     ids = torch.randint(0, 50257, (20, 1024), generator=g).to(dev)
     out["embedding_wte"] = timeit(lambda: ops.embedding_dot(ids, GL, 4, 50257))
+    tab = torch.zeros(50257, 768, dtype=torch.bfloat16, device=dev)
+    out["embedding_grad_tied"] = timeit(lambda: ops.embedding_train_grad(
+        ids, GL, 4, 1.25, tab, accumulate=True))
+    out["embedding_grad_untied"] = timeit(lambda: ops.embedding_train_grad(ids, GL, 4, 1.25,
+                                                                           tab))
+    del tab
     del A, G, A2, G2, X, GL
     Ak = rnd(32, 1024, 1024)
     Gk = rnd(32, 1024, 4096, s=1e-3)

@@ -3,14 +3,16 @@
 //   grad[v] = scale * sum over the train tokens t with id_t = v of g_t        grad: [vocab, d]
 //
 // The train tokens are grouped by id without float atomics, so the result is the same bits
-// on every run: a histogram and an exclusive scan of the counts give each id its range of a
-// token list; integer atomics place the tokens in their ranges (in any order); each token then
-// finds its place in index order by counting the smaller token indices in its range.  One wave
-// per vocabulary row sums the rows of its tokens in index order in fp32 and writes the row
-// once, scaled and converted to the grad dtype.  Overwrite mode writes every row (zeros where
-// no token has the id), which replaces a zero-fill, a scatter-add and a full-table scale;
-// accumulate mode adds the touched rows into what `grad` holds (a tied weight whose Linear
-// train gradient is already there) and leaves the other rows alone.
+// on every run: integer atomics count each id's tokens and find its first token, which
+// reserves the id's range of a token list from a bump cursor; the tokens are placed in their
+// ranges (in any order), then each finds its place in index order by counting the smaller
+// token indices in its range.  One wave per vocabulary row sums the rows of its tokens in
+// index order in fp32 and writes the row once, scaled and converted to the grad dtype.
+// Overwrite mode writes every row (zeros where no train token has the id), which replaces a
+// zero-fill, a scatter-add and a full-table scale; accumulate mode adds the touched rows into
+// what `grad` holds (a tied weight whose Linear train gradient is already there) and leaves
+// the other rows alone.  Where a range sits in the list depends on the order the atomics ran
+// in; only its contents and their order enter the sums.
 
 #include <algorithm>
 
@@ -20,17 +22,20 @@ namespace gs {
 namespace {
 
 constexpr int EG_THREADS = 256;
-constexpr int EG_SCAN_THREADS = 1024;
 
-// cnt[v] = fill[v] = 0.
+// cnt[v] = fill[v] = 0, first[v] = INT32_MAX, *cursor = 0.
 __global__ void __launch_bounds__(EG_THREADS) eg_clear_kernel(int32_t* __restrict__ cnt,
                                                               int32_t* __restrict__ fill,
+                                                              int32_t* __restrict__ first,
+                                                              int32_t* __restrict__ cursor,
                                                               int64_t vocab) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; v < vocab;
-       v += stride) {
+  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (v0 == 0) *cursor = 0;
+  for (int64_t v = v0; v < vocab; v += stride) {
     cnt[v] = 0;
     fill[v] = 0;
+    first[v] = INT32_MAX;
   }
 }
 
@@ -42,45 +47,37 @@ __device__ __forceinline__ int64_t eg_id(const int64_t* __restrict__ ids, const 
   return (id >= 0 && id < vocab) ? id : -1;
 }
 
+// cnt[id] = tokens with the id, first[id] = the smallest such token index.
 __global__ void __launch_bounds__(EG_THREADS) eg_count_kernel(const int64_t* __restrict__ ids,
                                                               RowMap tr, int64_t vocab,
-                                                              int32_t* __restrict__ cnt) {
+                                                              int32_t* __restrict__ cnt,
+                                                              int32_t* __restrict__ first) {
   const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (q >= tr.total()) return;
   const int64_t id = eg_id(ids, tr, vocab, q);
-  if (id >= 0) atomicAdd(cnt + id, 1);
+  if (id < 0) return;
+  atomicAdd(cnt + id, 1);
+  atomicMin(first + id, static_cast<int32_t>(q));
 }
 
-// off = exclusive prefix sum of cnt over [0, vocab), one workgroup: thread t sums a contiguous
-// run of entries, the run totals are scanned in LDS, then each run is written out.
-__global__ void __launch_bounds__(EG_SCAN_THREADS) eg_scan_kernel(const int32_t* __restrict__ cnt,
-                                                                  int64_t vocab,
-                                                                  int32_t* __restrict__ off) {
-  __shared__ int32_t tot[EG_SCAN_THREADS];
-  const int64_t per = (vocab + EG_SCAN_THREADS - 1) / EG_SCAN_THREADS;
-  const int64_t v0 = threadIdx.x * per, v1 = std::min<int64_t>(vocab, v0 + per);
-  int32_t s = 0;
-  for (int64_t v = v0; v < v1; ++v) s += cnt[v];
-  tot[threadIdx.x] = s;
-  __syncthreads();
-  // Hillis-Steele inclusive scan of the run totals.
-  for (int d = 1; d < EG_SCAN_THREADS; d <<= 1) {
-    const int32_t add = threadIdx.x >= d ? tot[threadIdx.x - d] : 0;
-    __syncthreads();
-    tot[threadIdx.x] += add;
-    __syncthreads();
-  }
-  int32_t run = threadIdx.x > 0 ? tot[threadIdx.x - 1] : 0;
-  for (int64_t v = v0; v < v1; ++v) {
-    off[v] = run;
-    run += cnt[v];
-  }
+// base[id] = the start of the id's range in the token list, reserved by its first token.
+__global__ void __launch_bounds__(EG_THREADS) eg_alloc_kernel(const int64_t* __restrict__ ids,
+                                                              RowMap tr, int64_t vocab,
+                                                              const int32_t* __restrict__ cnt,
+                                                              const int32_t* __restrict__ first,
+                                                              int32_t* __restrict__ cursor,
+                                                              int32_t* __restrict__ base) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (q >= tr.total()) return;
+  const int64_t id = eg_id(ids, tr, vocab, q);
+  if (id < 0 || first[id] != static_cast<int32_t>(q)) return;
+  base[id] = atomicAdd(cursor, cnt[id]);
 }
 
-// list[off[id] + k] = q for some k in [0, cnt[id]) (the order inside a range is arbitrary).
+// list[base[id] + k] = q for some k in [0, cnt[id]) (the order inside a range is arbitrary).
 __global__ void __launch_bounds__(EG_THREADS) eg_place_kernel(const int64_t* __restrict__ ids,
                                                               RowMap tr, int64_t vocab,
-                                                              const int32_t* __restrict__ off,
+                                                              const int32_t* __restrict__ base,
                                                               int32_t* __restrict__ fill,
                                                               int32_t* __restrict__ list) {
   const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -88,14 +85,14 @@ __global__ void __launch_bounds__(EG_THREADS) eg_place_kernel(const int64_t* __r
   const int64_t id = eg_id(ids, tr, vocab, q);
   if (id < 0) return;
   const int32_t k = atomicAdd(fill + id, 1);
-  list[off[id] + k] = static_cast<int32_t>(q);
+  list[base[id] + k] = static_cast<int32_t>(q);
 }
 
-// sorted[off[id] + r] = q with r = the number of tokens of the same id before q: each range
+// sorted[base[id] + r] = q with r = the number of tokens of the same id before q: each range
 // of `sorted` lists its tokens in index order.
 __global__ void __launch_bounds__(EG_THREADS) eg_order_kernel(const int64_t* __restrict__ ids,
                                                               RowMap tr, int64_t vocab,
-                                                              const int32_t* __restrict__ off,
+                                                              const int32_t* __restrict__ base,
                                                               const int32_t* __restrict__ cnt,
                                                               const int32_t* __restrict__ list,
                                                               int32_t* __restrict__ sorted) {
@@ -103,7 +100,7 @@ __global__ void __launch_bounds__(EG_THREADS) eg_order_kernel(const int64_t* __r
   if (q >= tr.total()) return;
   const int64_t id = eg_id(ids, tr, vocab, q);
   if (id < 0) return;
-  const int32_t s = off[id], n = cnt[id];
+  const int32_t s = base[id], n = cnt[id];
   int32_t r = 0;
   for (int32_t k = 0; k < n; ++k) r += list[s + k] < static_cast<int32_t>(q) ? 1 : 0;
   sorted[s + r] = static_cast<int32_t>(q);
@@ -120,8 +117,9 @@ struct EgVec {
 // accumulating).  `vec`: G's rows are 16-byte aligned, so whole chunks load at once.
 template <class E, class GE>
 __global__ void __launch_bounds__(EG_THREADS) eg_rows_kernel(
-    const E* __restrict__ G, RowMap tr, int64_t d, int64_t vocab, const int32_t* __restrict__ off,
-    const int32_t* __restrict__ cnt, const int32_t* __restrict__ sorted, float scale,
+    const E* __restrict__ G, RowMap tr, int64_t d, int64_t vocab,
+    const int32_t* __restrict__ base, const int32_t* __restrict__ cnt,
+    const int32_t* __restrict__ sorted, float scale,
     int accumulate, int vec, GE* __restrict__ grad) {
   constexpr int VE = EgVec<E>::VE;
   const int lane = threadIdx.x & 63;
@@ -129,7 +127,7 @@ __global__ void __launch_bounds__(EG_THREADS) eg_rows_kernel(
   if (v >= vocab) return;
   const int32_t n = cnt[v];
   if (n == 0 && accumulate) return;
-  const int32_t s = off[v];
+  const int32_t s = n > 0 ? base[v] : 0;   // base[v] is set only for ids present
   GE* out = grad + v * d;
   for (int64_t f0 = static_cast<int64_t>(lane) * VE; f0 < d; f0 += 64 * VE) {
     const bool full = vec && f0 + VE <= d;
@@ -165,21 +163,24 @@ int64_t eg_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 template <class S>
 void carve_emb_grad(S& c, int64_t M, int64_t vocab, int32_t** cnt, int32_t** fill,
-                    int32_t** off, int32_t** list, int32_t** sorted) {
+                    int32_t** first, int32_t** base, int32_t** cursor, int32_t** list,
+                    int32_t** sorted) {
   *cnt = c.template take<int32_t>(vocab);
   *fill = c.template take<int32_t>(vocab);
-  *off = c.template take<int32_t>(vocab);
+  *first = c.template take<int32_t>(vocab);
+  *base = c.template take<int32_t>(vocab);
+  *cursor = c.template take<int32_t>(1);
   *list = c.template take<int32_t>(M);
   *sorted = c.template take<int32_t>(M);
 }
 
 template <class E, class GE>
-int launch_rows(const void* G, const RowMap& tr, int64_t d, int64_t vocab, const int32_t* off,
+int launch_rows(const void* G, const RowMap& tr, int64_t d, int64_t vocab, const int32_t* base,
                 const int32_t* cnt, const int32_t* sorted, float scale, int accumulate, int vec,
                 void* grad, hipStream_t s) {
   hipLaunchKernelGGL((eg_rows_kernel<E, GE>),
                      dim3(static_cast<unsigned>(eg_cdiv(vocab, EG_THREADS / 64))),
-                     dim3(EG_THREADS), 0, s, static_cast<const E*>(G), tr, d, vocab, off, cnt,
+                     dim3(EG_THREADS), 0, s, static_cast<const E*>(G), tr, d, vocab, base, cnt,
                      sorted, scale, accumulate, vec, static_cast<GE*>(grad));
   return check_launch("eg_rows_kernel");
 }
@@ -193,8 +194,9 @@ extern "C" size_t gs_embedding_train_grad_workspace(int64_t N, int64_t n_val, in
                                                     int64_t vocab) {
   if (N <= 0 || n_val < 0 || n_val >= N || T <= 0 || vocab <= 0) return 0;
   Sizer sz;
-  int32_t *cnt, *fill, *off, *list, *sorted;
-  carve_emb_grad(sz, (N - n_val) * T, vocab, &cnt, &fill, &off, &list, &sorted);
+  int32_t *cnt, *fill, *first, *base, *cursor, *list, *sorted;
+  carve_emb_grad(sz, (N - n_val) * T, vocab, &cnt, &fill, &first, &base, &cursor, &list,
+                 &sorted);
   return sz.used + 256;
 }
 
@@ -214,22 +216,25 @@ extern "C" int gs_embedding_train_grad(const int64_t* ids, const void* G, int dt
   if (M >= INT32_MAX || vocab >= INT32_MAX)
     return fail(GS_ERR_UNSUPPORTED, "gs_embedding_train_grad: 2^31 or more tokens or ids");
   Sizer sz;
-  int32_t *cnt, *fill, *off, *list, *sorted;
-  carve_emb_grad(sz, M, vocab, &cnt, &fill, &off, &list, &sorted);
+  int32_t *cnt, *fill, *first, *base, *cursor, *list, *sorted;
+  carve_emb_grad(sz, M, vocab, &cnt, &fill, &first, &base, &cursor, &list, &sorted);
   if (workspace == nullptr || workspace_bytes < sz.used)
     return fail(GS_ERR_WORKSPACE, "gs_embedding_train_grad: workspace too small");
   Carver cv(workspace, workspace_bytes);
-  carve_emb_grad(cv, M, vocab, &cnt, &fill, &off, &list, &sorted);
+  carve_emb_grad(cv, M, vocab, &cnt, &fill, &first, &base, &cursor, &list, &sorted);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const RowMap tr = train_rows(N, n_val, val_start, T);
   const unsigned vb = static_cast<unsigned>(std::min<int64_t>(eg_cdiv(vocab, EG_THREADS), 4096));
   const unsigned tb = static_cast<unsigned>(eg_cdiv(M, EG_THREADS));
-  hipLaunchKernelGGL(eg_clear_kernel, dim3(vb), dim3(EG_THREADS), 0, s, cnt, fill, vocab);
-  hipLaunchKernelGGL(eg_count_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, cnt);
-  hipLaunchKernelGGL(eg_scan_kernel, dim3(1), dim3(EG_SCAN_THREADS), 0, s, cnt, vocab, off);
-  hipLaunchKernelGGL(eg_place_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, off,
+  hipLaunchKernelGGL(eg_clear_kernel, dim3(vb), dim3(EG_THREADS), 0, s, cnt, fill, first, cursor,
+                     vocab);
+  hipLaunchKernelGGL(eg_count_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, cnt,
+                     first);
+  hipLaunchKernelGGL(eg_alloc_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, cnt,
+                     first, cursor, base);
+  hipLaunchKernelGGL(eg_place_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, base,
                      fill, list);
-  hipLaunchKernelGGL(eg_order_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, off,
+  hipLaunchKernelGGL(eg_order_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, base,
                      cnt, list, sorted);
   int rc = check_launch("embedding train-gradient grouping kernels");
   if (rc) return rc;
@@ -239,13 +244,13 @@ extern "C" int gs_embedding_train_grad(const int64_t* ids, const void* G, int dt
   const int acc = accumulate ? 1 : 0;
   if (dtype == GS_DTYPE_BF16)
     return grad_dtype == GS_DTYPE_BF16
-               ? launch_rows<uint16_t, uint16_t>(G, tr, d, vocab, off, cnt, sorted, scale, acc,
+               ? launch_rows<uint16_t, uint16_t>(G, tr, d, vocab, base, cnt, sorted, scale, acc,
                                                  vec, grad, s)
-               : launch_rows<uint16_t, float>(G, tr, d, vocab, off, cnt, sorted, scale, acc,
+               : launch_rows<uint16_t, float>(G, tr, d, vocab, base, cnt, sorted, scale, acc,
                                               vec, grad, s);
   return grad_dtype == GS_DTYPE_BF16
-             ? launch_rows<float, uint16_t>(G, tr, d, vocab, off, cnt, sorted, scale, acc, vec,
+             ? launch_rows<float, uint16_t>(G, tr, d, vocab, base, cnt, sorted, scale, acc, vec,
                                             grad, s)
-             : launch_rows<float, float>(G, tr, d, vocab, off, cnt, sorted, scale, acc, vec,
+             : launch_rows<float, float>(G, tr, d, vocab, base, cnt, sorted, scale, acc, vec,
                                          grad, s);
 }

@@ -393,3 +393,70 @@ def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
     assert block and all(n in grads2 for n in block), (sorted(grads), sorted(grads2))
     for name in block:
         assert_close(grads[name], grads2[name], 1e-2, f"fused vs separate grad {name}")
+
+
+def test_manager_step_contract_on_gpu(gpu, tmp_path):
+    """The reference's training step (Examples/GradDotProd_LM/training_loop.py:99-166) through
+    GhostEngineManager on the GPU: attach_train_batch -> save metrics on their interval ->
+    prepare_forward_input -> forward/backward -> prepare_gradients -> optimizer step ->
+    aggregate_and_log -> clear_gradients -> zero_grad, with config.ghost_options reaching
+    the engine (fp32 dots here).  Over four steps: every logged dot vector and the weights
+    against per-sample gradients of float64 copies; then the files the loop leaves
+    (valset.pt, dot_prod_log_iter_2.pt, and dot_prod_log_iter_-1.pt from cleanup)."""
+    import types
+    from ghostsuite_amd import GhostEngineManager
+    torch.manual_seed(50)
+    T, vocab, n_t, n_v, lr = 16, 64, 4, 2, 0.05
+    cfg_m = LMConfig(n_layer=2, n_head=2, d_model=32, d_mlp=64, vocab=vocab, n_ctx=T)
+    model = CausalLM(cfg_m)
+    ref = copy.deepcopy(model).double()       # tied, follows the same SGD updates
+    model = model.to(gpu)
+    Xv, Yv = synthetic_tokens(n_v, T, vocab, seed=51)
+    opt = torch.optim.SGD(model.parameters(), lr=lr)
+    cfg = types.SimpleNamespace(method="GradDotProd", result_dir=str(tmp_path),
+                                val_batch_size=n_v, dot_prod_save_interval=2,
+                                ghost_options={"precision": "fp32"})
+    mgr = GhostEngineManager(cfg, model, opt, {"master_process": True, "device": gpu},
+                             (Xv.to(gpu), Yv.to(gpu)))
+    assert S.options["precision"] == "fp32"
+    N = n_t + n_v
+    for it in range(4):
+        print(f"manager step {it}", flush=True)
+        X, Y = synthetic_tokens(n_t, T, vocab, seed=60 + it)
+        mgr.attach_train_batch(X.to(gpu), Y.to(gpu), it, list(range(it * n_t, (it + 1) * n_t)))
+        if it > 0 and mgr.should_save_metrics(it):
+            mgr.save_metrics(it)
+        Xf, Yf = mgr.prepare_forward_input(X.to(gpu), Y.to(gpu))
+        assert torch.equal(Xf[n_t:].cpu(), Xv)
+        model(Xf, Yf).backward()
+        mgr.prepare_gradients()
+        opt.step()
+        mgr.aggregate_and_log()
+        mgr.clear_gradients()
+        opt.zero_grad(set_to_none=True)
+        # expected: per-sample gradients on the same concatenated batch
+        Xc, Yc = torch.cat((X, Xv)), torch.cat((Y, Yv))
+        untied = copy.deepcopy(ref)
+        untied.lm_head.weight = nn.Parameter(ref.wte.weight.detach().clone())
+        g_untied = brute.per_sample_grads(untied, Xc, Yc, _lm_loss(T), 1.0 / (N * T))
+        g_tied = brute.per_sample_grads(ref, Xc, Yc, _lm_loss(T), 1.0 / (N * T))
+        names = [n for n, _ in ref.named_parameters()]
+        want = sum(brute.pairwise_dots(g_untied[n], n_v) for n in names)
+        assert_close(mgr.engine.dot_product_log[-1]["dot_product"], want, FP32_TOL,
+                     f"step {it} logged dots")
+        with torch.no_grad():
+            for n, p in ref.named_parameters():
+                p -= lr * brute.train_mean(g_tied[n], n_v, N)
+        for (n, p), (_, q) in zip(model.named_parameters(), ref.named_parameters()):
+            if "dummy_bias" not in n:
+                assert_close(p.detach().cpu(), q.detach(), FP32_TOL, f"step {it} weight {n}")
+    mgr.cleanup()
+    d = tmp_path / "grad_dotprods"
+    vs = torch.load(d / "valset.pt", weights_only=True)
+    assert torch.equal(vs["X_val"], Xv) and torch.equal(vs["Y_val"], Yv)
+    log2 = torch.load(d / "dot_prod_log_iter_2.pt", weights_only=True)
+    assert [r["iter_num"] for r in log2] == [0, 1]
+    assert log2[1]["batch_idx"] == [4, 5, 6, 7] and log2[0]["dot_product"].shape == (n_t,)
+    rest = torch.load(d / "dot_prod_log_iter_-1.pt", weights_only=True)
+    assert [r["iter_num"] for r in rest] == [2, 3]
+    assert not hasattr(model, "autograd_grad_sample_hooks")

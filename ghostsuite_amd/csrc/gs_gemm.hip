@@ -1628,14 +1628,36 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
   raw_barrier();
 }
 
-// One output tile per (blockIdx.x, split blockIdx.y): bf16 out when there is one split,
-// else fp32 partials reduced by tn_reduce_kernel.
+// Work item of this workgroup: (split, mt, nt).  The items are ordered split-major, then by
+// blocks of the side with more tiles, the other side innermost, and each XCD takes a
+// contiguous run of them (workgroup w runs on XCD w mod 8): the workgroups resident on one
+// XCD share a few column blocks of both operands for one k-range in its L2, instead of every
+// XCD streaming most of both operands.
+__device__ __forceinline__ void tn_item(const TnParams& p, int64_t& mt, int64_t& nt,
+                                        int64_t& split) {
+  constexpr int64_t XCDS = 8;
+  const int64_t total = static_cast<int64_t>(gridDim.x), w = blockIdx.x;
+  const int64_t i = total % XCDS == 0 ? (w % XCDS) * (total / XCDS) + w / XCDS : w;
+  const int64_t tiles = p.m_tiles * p.n_tiles;
+  split = i / tiles;
+  const int64_t r = i - split * tiles;
+  if (p.m_tiles <= p.n_tiles) {
+    nt = r / p.m_tiles;
+    mt = r - nt * p.m_tiles;
+  } else {
+    mt = r / p.n_tiles;
+    nt = r - mt * p.n_tiles;
+  }
+}
+
+// One output tile per work item: bf16 out when there is one split, else fp32 partials
+// reduced by tn_reduce_kernel.
 template <class C, class D>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
-  int64_t mt, nt;
-  tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
-  const int64_t k_begin = static_cast<int64_t>(blockIdx.y) * p.kper;
+  int64_t mt, nt, split;
+  tn_item(p, mt, nt, split);
+  const int64_t k_begin = split * p.kper;
   const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
@@ -1665,8 +1687,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
 #pragma unroll
       for (int g = 0; g < NRG; ++g) t += red[g * C::BM + m];
       const int64_t col = t0 + m;
-      if (col < ext)
-        p.vsum[(static_cast<int64_t>(blockIdx.y) * p.vparts + part) * ext + col] = t;
+      if (col < ext) p.vsum[(split * p.vparts + part) * ext + col] = t;
     }
   }
   GemmParams e{};
@@ -1677,7 +1698,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
     e.C = p.out;
     store_epilogue<TrBF16, C>(e, acc, mt, nt);
   } else {
-    e.C = static_cast<float*>(p.out) + static_cast<int64_t>(blockIdx.y) * p.M * p.N;
+    e.C = static_cast<float*>(p.out) + split * p.M * p.N;
     store_epilogue<TrF32, C>(e, acc, mt, nt);
   }
 }
@@ -1994,10 +2015,9 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
       TN_VPARTS, vsum_r ? ceil_div(M, TnC::BM) : ceil_div(N, TnC::BN)));
   p.out = sp > 1 ? static_cast<void*>(part) : out;
   if (sp > 1 && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
-  const int64_t tiles = p.m_tiles * p.n_tiles;
-  if (tiles > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-  hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>),
-                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(sp)),
+  const int64_t items = p.m_tiles * p.n_tiles * sp;
+  if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
+  hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
                      dim3(TnC::NT), 0, s, p);
   int rc = check_launch("tn_gemm_kernel");
   const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts : 1;

@@ -1401,32 +1401,6 @@ __global__ void __launch_bounds__(256) presum_rows_vec_kernel(PresumPair pp, Row
   *reinterpret_cast<uint4*>(pp.out[z] + t * d + f) = o;
 }
 
-// n counters = 0 (the folded reductions' arrival counters; a kernel rather than a memset,
-// so that callers may capture the op in a graph).
-__global__ void __launch_bounds__(256) zero_u32_kernel(unsigned* __restrict__ c, int64_t n) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    c[i] = 0u;
-}
-
-// Arrival at a folded reduction: every thread's stores are made visible device-wide, then one
-// thread counts the workgroup in; true (in every thread) for the last of `total` arrivals,
-// which resets the counter and may then read what the others wrote.
-__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned total) {
-  __shared__ unsigned last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(counter, 1u);
-    last = prev + 1u == total ? 1u : 0u;
-    if (last) *counter = 0u;
-  }
-  __syncthreads();
-  const bool is_last = last != 0u;
-  if (is_last) __threadfence();
-  return is_last;
-}
-
 // ------------------------------------------------------------------ K-major (TN) GEMM
 // out[m][n] = sum over k rows of L[k][m] R[k][n], with both operands K-major: rows are k,
 // as the val rows of A and G lie in HBM, so neither is transposed in memory.  Each stage's
@@ -1469,12 +1443,6 @@ struct TnParams {
   float* vsum;      // null, or [split][vparts][M]: column sums of L over the split's k-rows
   int vsum_r;       // 1: vsum holds the column sums of R instead ([split][vparts][N])
   int vparts;       // the tiles along the other side (N, or M with vsum_r) split the k-rows
-  // Folded reduction (cnt != null): the last workgroup to finish a tile sums its splits'
-  // partials into V; the last contributor of a column-sum tile folds vsum into row 0.
-  // cnt [m_tiles * n_tiles] and vcnt [column-sum tiles] start at zero and are left at zero.
-  unsigned* cnt;
-  unsigned* vcnt;
-  void* V;          // bf16 [M][N] when folding
 };
 
 template <class C, class D>
@@ -1727,53 +1695,11 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
   e.n_cols = p.N;
   e.c_ld = p.N;
   if (p.splits == 1) {
-    e.C = p.cnt != nullptr ? p.V : p.out;
+    e.C = p.out;
     store_epilogue<TrBF16, C>(e, acc, mt, nt);
   } else {
     e.C = static_cast<float*>(p.out) + split * p.M * p.N;
     store_epilogue<TrF32, C>(e, acc, mt, nt);
-  }
-  if (p.cnt == nullptr) return;
-  // Folded split reduction: the tile's last workgroup sums the partials in split order.
-  if (p.splits > 1 &&
-      arrive_last(p.cnt + mt * p.n_tiles + nt, static_cast<unsigned>(p.splits))) {
-    const float* part = static_cast<const float*>(p.out);
-    uint16_t* V = static_cast<uint16_t*>(p.V);
-    const int64_t cnt_all = p.M * p.N;
-    for (int x = threadIdx.x; x < C::BM * C::BN / 4; x += C::NT) {
-      const int64_t m = mt * C::BM + x / (C::BN / 4);
-      const int64_t n = nt * C::BN + (x % (C::BN / 4)) * 4;
-      if (m >= p.M || n >= p.N) continue;   // N % 8 == 0: a group of 4 is whole or absent
-      const int64_t i = m * p.N + n;
-      float4 t = *reinterpret_cast<const float4*>(part + i);
-      for (int k = 1; k < p.splits; ++k) {
-        const float4 v = *reinterpret_cast<const float4*>(part + k * cnt_all + i);
-        t.x += v.x;
-        t.y += v.y;
-        t.z += v.z;
-        t.w += v.w;
-      }
-      uint2 o;
-      o.x = pack_bf16x2(t.x, t.y);
-      o.y = pack_bf16x2(t.z, t.w);
-      *reinterpret_cast<uint2*>(V + i) = o;
-    }
-  }
-  // Folded column sums: the last of the column tile's contributors adds the rows
-  // (split, part) in order into row 0.
-  const int vrows = p.splits * p.vparts;
-  if (colsum && vrows > 1) {
-    const int64_t ct = p.vsum_r ? nt : mt;
-    if (arrive_last(p.vcnt + ct, static_cast<unsigned>(vrows))) {
-      const int64_t ext = p.vsum_r ? p.N : p.M;
-      for (int m = threadIdx.x; m < C::BM; m += C::NT) {
-        const int64_t col = ct * C::BM + m;
-        if (col >= ext) continue;
-        float t = 0.f;
-        for (int r = 0; r < vrows; ++r) t += p.vsum[r * ext + col];
-        p.vsum[col] = t;
-      }
-    }
   }
 }
 
@@ -2063,16 +1989,11 @@ bool val_tn(int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, in
 // out [M][N] bf16 = L^T R over K k-rows (L: [K][M] stride ldl, R: [K][N] stride ldr).
 // vsum (optional): [splits][parts][M] column sums of L (parts: the first N tiles, at most
 // TN_VPARTS), or with vsum_r [splits][parts][N] those of R (the first M tiles); their total
-// ends in row 0.  cnt (optional, tn_counters() entries): the splits and column-sum parts are
-// reduced inside tn_gemm_kernel by the last workgroup to arrive (counters zeroed by a small
-// kernel first), else by tn_reduce_kernel.
+// ends in row 0.
 constexpr int64_t TN_VPARTS = 4;
-int64_t tn_counters(int64_t M, int64_t N) {
-  return ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN) + ceil_div(std::max(M, N), TnC::BM);
-}
 int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
               int64_t N, void* out, float* part, hipStream_t s, float* vsum = nullptr,
-              bool vsum_r = false, unsigned* cnt = nullptr) {
+              bool vsum_r = false) {
   TnParams p{};
   p.L = L;
   p.R = R;
@@ -2096,20 +2017,11 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   if (sp > 1 && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
   const int64_t items = p.m_tiles * p.n_tiles * sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-  const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts : 1;
-  if (cnt != nullptr && (sp > 1 || vs_rows > 1)) {
-    p.cnt = cnt;
-    p.vcnt = cnt + p.m_tiles * p.n_tiles;
-    p.V = out;
-    const int64_t nc = tn_counters(M, N);
-    hipLaunchKernelGGL(zero_u32_kernel,
-                       dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(nc, 256), 64))),
-                       dim3(256), 0, s, cnt, nc);
-  }
   hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
                      dim3(TnC::NT), 0, s, p);
   int rc = check_launch("tn_gemm_kernel");
-  if (rc || p.cnt != nullptr || (sp == 1 && vs_rows == 1)) return rc;
+  const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts : 1;
+  if (rc || (sp == 1 && vs_rows == 1)) return rc;
   const int64_t count = sp > 1 ? M * N : 0;  // a multiple of 8 (N % 8 == 0)
   const int64_t vs_n = vsum_r ? N : M;
   hipLaunchKernelGGL(tn_reduce_kernel,
@@ -2200,7 +2112,6 @@ void carve_linear(S& c, const LinearPlan& pl, int dtype, int64_t T, int64_t d_in
     c.template take<char>(d_out * d_in * esz);
     c.template take<float>(pl.p_rows * pl.p_ld);
     c.template take<float>(tn_part_elems(pl.vcols / pl.groups, d_out, d_in));
-    c.template take<unsigned>(tn_counters(d_out, d_in));
   } else {
     c.template take<char>(d_in * pl.vcols * esz);
     c.template take<char>(d_out * pl.vcols * esz);
@@ -2418,7 +2329,6 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
       float* P = cv.take<float>(pl.p_rows * pl.p_ld);
       const int64_t kper = pl.vcols / pl.groups;  // k-rows per V (one val row for pairs)
       float* part = cv.take<float>(tn_part_elems(kper, d_out, d_in));
-      unsigned* tcnt = cv.take<unsigned>(tn_counters(d_out, d_in));
       if (presum) {
         PresumPair pp{};
         pp.in[0] = static_cast<const E*>(A);
@@ -2439,13 +2349,13 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
         int rc;
         if (pl.swap) {  // V^T [d_in][d_out] = A_val^T G_val; sum_t <a_t, V^T g_t>
           rc = launch_tn(La + j * kper * d_in, d_in, Lg + j * kper * d_out, d_out, kper, d_in,
-                         d_out, V, part, s, nullptr, false, tcnt);
+                         d_out, V, part, s);
           if (rc) return rc;
           rc = launch_rowdot<Tr>(G, A, V, N, n_val, val_start, T, d_out, d_in, P, pl.p_ld,
                                  pl.tile_reduce, j * n_mt, s);
         } else {
           rc = launch_tn(Lg + j * kper * d_out, d_out, La + j * kper * d_in, d_in, kper, d_out,
-                         d_in, V, part, s, nullptr, false, tcnt);
+                         d_in, V, part, s);
           if (rc) return rc;
           rc = launch_rowdot<Tr>(A, G, V, N, n_val, val_start, T, d_in, d_out, P, pl.p_ld,
                                  pl.tile_reduce, j * n_mt, s);
@@ -2646,10 +2556,8 @@ void carve_val_gradient(S& c, int dtype, int64_t n_val, int64_t T, int64_t d_in,
   const int64_t vcols = (presum ? 1 : n_val) * T;
   c.template take<char>(d_in * vcols * esz);
   c.template take<char>(d_out * vcols * esz);
-  if (val_tn(dtype, n_val, T, d_in, d_out, presum)) {
+  if (val_tn(dtype, n_val, T, d_in, d_out, presum))
     c.template take<float>(tn_part_elems(vcols, d_out, d_in));
-    c.template take<unsigned>(tn_counters(d_out, d_in));
-  }
 }
 }  // namespace
 }  // namespace gs
@@ -2707,8 +2615,7 @@ extern "C" int gs_linear_val_gradient(const void* A, const void* G, int dtype, i
       Lg = gbar;
     }
     float* part = cv.take<float>(tn_part_elems(vcols, d_out, d_in));
-    unsigned* tcnt = cv.take<unsigned>(tn_counters(d_out, d_in));
-    return launch_tn(Lg, d_out, La, d_in, vcols, d_out, d_in, V, part, s, nullptr, false, tcnt);
+    return launch_tn(Lg, d_out, La, d_in, vcols, d_out, d_in, V, part, s);
   }
   if (dtype == GS_DTYPE_BF16) {
     using E = TrBF16::E;
@@ -3005,7 +2912,7 @@ bool bias_dot_ok(int dtype, const void* A, const void* G, int64_t N, int64_t n_v
 template <class S>
 void carve_bias_dot(S& c, const RowdotBiasPlan& b, int64_t n_val, int64_t T, int64_t d_in,
                     int64_t d_out, int presum, float** P, float** PB, float** BP, void** V,
-                    float** VS, float** part, void** abar, void** gbar, unsigned** tcnt) {
+                    float** VS, float** part, void** abar, void** gbar) {
   carve_rowdot_bias(c, b, d_out, P, PB, BP);
   const int64_t K = (presum ? 1 : n_val) * T;
   *V = c.template take<uint16_t>(d_out * d_in);
@@ -3014,7 +2921,6 @@ void carve_bias_dot(S& c, const RowdotBiasPlan& b, int64_t n_val, int64_t T, int
   *part = c.template take<float>(tn_part_elems(K, d_out, d_in));
   *abar = presum ? c.template take<uint16_t>(T * d_in) : nullptr;
   *gbar = presum ? c.template take<uint16_t>(T * d_out) : nullptr;
-  *tcnt = c.template take<unsigned>(tn_counters(d_out, d_in));
 }
 }  // namespace
 }  // namespace gs
@@ -3028,9 +2934,8 @@ extern "C" size_t gs_linear_bias_dot_workspace(int dtype, int64_t N, int64_t n_v
   Sizer sz;
   float *P, *PB, *BP, *VS, *part;
   void *V, *abar, *gbar;
-  unsigned* tcnt;
   carve_bias_dot(sz, b, n_val, T, d_in, d_out, presum, &P, &PB, &BP, &V, &VS, &part, &abar,
-                 &gbar, &tcnt);
+                 &gbar);
   return sz.used + 256;
 }
 
@@ -3059,9 +2964,8 @@ extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64
   Carver cv(workspace, workspace_bytes);
   float *P, *PB, *BP, *VS, *part;
   void *V, *abar, *gbar;
-  unsigned* tcnt;
   carve_bias_dot(cv, b, n_val, T, d_in, d_out, presum, &P, &PB, &BP, &V, &VS, &part, &abar,
-                 &gbar, &tcnt);
+                 &gbar);
   hipStream_t s = static_cast<hipStream_t>(stream);
   using E = TrBF16::E;
   const E* La = static_cast<const E*>(A) + val_start * T * d_in;
@@ -3086,8 +2990,8 @@ extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64
   const int64_t K = (presum ? 1 : n_val) * T;
   // V [d_out][d_in] = G_val^T A_val, or with swap V^T [d_in][d_out] = A_val^T G_val; VS holds
   // the column sums of G_val either way.
-  rc = b.swap ? launch_tn(La, d_in, Lg, d_out, K, d_in, d_out, V, part, s, VS, true, tcnt)
-              : launch_tn(Lg, d_out, La, d_in, K, d_out, d_in, V, part, s, VS, false, tcnt);
+  rc = b.swap ? launch_tn(La, d_in, Lg, d_out, K, d_in, d_out, V, part, s, VS, true)
+              : launch_tn(Lg, d_out, La, d_in, K, d_out, d_in, V, part, s, VS);
   if (rc) return rc;
   return launch_rowdot_bias(A, G, V, VS, 1, N, n_val, val_start, T,
                             d_in, d_out, b, P, PB, BP, out_dot, out_bias_dot, out_bias_grad,

@@ -64,8 +64,9 @@ __global__ void __launch_bounds__(EG_THREADS) eg_count_kernel(const int64_t* __r
 }
 
 // base[id] = the start of the id's range in the token list, reserved by its first token;
-// segs[j] = the ids present (in reservation order), *nseg = their number.  The reservations
-// of a wave go through one atomic per counter (the wave's prefix sums place its lanes).
+// segs[j] = the ids present (in reservation order), cursor[1] = their number.  A workgroup's
+// reservations go through one 64-bit atomic on the packed (ranges, ids) cursor; prefix sums
+// over the workgroup place its lanes.
 __global__ void __launch_bounds__(EG_THREADS) eg_alloc_kernel(const int64_t* __restrict__ ids,
                                                               RowMap tr, int64_t vocab,
                                                               const int32_t* __restrict__ cnt,
@@ -73,14 +74,16 @@ __global__ void __launch_bounds__(EG_THREADS) eg_alloc_kernel(const int64_t* __r
                                                               int32_t* __restrict__ cursor,
                                                               int32_t* __restrict__ base,
                                                               int32_t* __restrict__ segs) {
+  constexpr int NW = EG_THREADS / 64;
+  __shared__ int32_t wn[NW], wo[NW];
+  __shared__ unsigned long long blk;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int64_t id = -1;
   if (q < tr.total()) id = eg_id(ids, tr, vocab, q);
   const bool mine = id >= 0 && first[id] == static_cast<int32_t>(q);
-  int32_t n = mine ? cnt[id] : 0, one = mine ? 1 : 0;
-  // inclusive prefix sums over the wave
-  int32_t pn = n, po = one;
+  const int32_t n = mine ? cnt[id] : 0, one = mine ? 1 : 0;
+  int32_t pn = n, po = one;  // inclusive prefix sums over the wave
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const int32_t a = __shfl_up(pn, off, 64), b = __shfl_up(po, off, 64);
@@ -89,16 +92,30 @@ __global__ void __launch_bounds__(EG_THREADS) eg_alloc_kernel(const int64_t* __r
       po += b;
     }
   }
-  int32_t b_n = 0, b_o = 0;
-  if (lane == 63 && po > 0) {
-    b_n = atomicAdd(cursor, pn);
-    b_o = atomicAdd(cursor + 1, po);
+  if (lane == 63) {
+    wn[wid] = pn;
+    wo[wid] = po;
   }
-  b_n = __shfl(b_n, 63, 64);
-  b_o = __shfl(b_o, 63, 64);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long tn = 0, to = 0;
+    for (int w = 0; w < NW; ++w) {
+      tn += static_cast<unsigned>(wn[w]);
+      to += static_cast<unsigned>(wo[w]);
+    }
+    blk = to > 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(cursor), tn | (to << 32))
+                 : 0ull;
+  }
+  __syncthreads();
   if (mine) {
-    base[id] = b_n + pn - n;
-    segs[b_o + po - 1] = static_cast<int32_t>(id);
+    int32_t bn = static_cast<int32_t>(blk & 0xffffffffull);
+    int32_t bo = static_cast<int32_t>(blk >> 32);
+    for (int w = 0; w < wid; ++w) {
+      bn += wn[w];
+      bo += wo[w];
+    }
+    base[id] = bn + pn - n;
+    segs[bo + po - 1] = static_cast<int32_t>(id);
   }
 }
 

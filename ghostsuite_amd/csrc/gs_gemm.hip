@@ -308,25 +308,31 @@ constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
 #endif
 
 // Geometry of one LDS-DMA pipeline over the tile of config C: each stage holds ROWB bytes
-// (ROWB / 2 bf16 of K) of every L and R row, NS stage buffers.  A wave-level load moves
-// 1 KiB = RPL rows.
-template <class C, int ROWB, int NS>
+// (ROWB / 2 bf16 of K) of every L and R row.  The L rows cycle through NS slots and the R
+// rows through NSR >= NS slots (a deeper ring for the operand streamed from HBM keeps more
+// of its bytes in flight); the L ring sits at byte 0 and the R ring behind it.  A wave-level
+// load moves 1 KiB = RPL rows.
+template <class C, int ROWB, int NS, int NSR = NS>
 struct DmaCfg {
   static constexpr int NW = C::WM * C::WN;
-  static constexpr int ROW_BYTES = ROWB, STAGES = NS;
+  static constexpr int ROW_BYTES = ROWB, STAGES = NS, RSTAGES = NSR;
   static constexpr int CH = ROWB / 16;   // 16-byte chunks per row
   static constexpr int RPL = 64 / CH;    // rows per wave-level load
   static constexpr int KB = ROWB / 2;    // k elements per stage
   static constexpr int KSTEPS = KB / 16; // MFMA k-steps per stage
   static_assert(ROWB == 64 || ROWB == 128, "64- or 128-byte stage rows");
-  static_assert(NS >= 2 && NS <= 8, "2 to 8 stages");
+  static_assert(NS >= 2 && NSR >= NS && NSR <= 8, "2 to 8 stages, the R ring at least as deep");
   static_assert((C::BM / RPL) % NW == 0 && (C::BN / RPL) % NW == 0,
                 "row groups must split over waves");
+  static_assert(C::BM % 32 == 0, "R rows keep the swizzle phase of the stacked layout");
   static constexpr int QL = C::BM / RPL / NW, QR = C::BN / RPL / NW;  // loads per wave
-  static constexpr int STAGE_BYTES = (C::BM + C::BN) * ROWB;
+  static constexpr int L_SLOT = C::BM * ROWB, R_SLOT = C::BN * ROWB;  // bytes of one slot
+  static constexpr int R_RING = NS * L_SLOT;                          // offset of the R ring
+  static constexpr int LDS_BYTES = NS * L_SLOT + NSR * R_SLOT;
   // Physical slot of logical chunk c of row r is c ^ swz(r): the 16 consecutive rows a
   // 16-lane ds_read_b128 group reads (one logical chunk each) then occupy 16 distinct
-  // 16-byte bank groups of the 256-byte bank window.  swz depends on r mod 32 only.
+  // 16-byte bank groups of the 256-byte bank window.  swz depends on r mod 32 only; R row r
+  // uses swz(BM + r).
   __device__ static constexpr int swz(int r) { return CH == 8 ? (r >> 1) & 7 : (r >> 2) & 3; }
 };
 
@@ -399,36 +405,38 @@ struct DmaStreamer {
       kr[q] = c * 8;
     }
   }
-  // Load q of a stage (q < QL: L rows, else R rows) at LDS byte address `stage`.  `full`
-  // (wave-uniform): the stage lies wholly inside K, so no lane needs the k bound.
-  __device__ __forceinline__ void one(unsigned stage, int64_t k0, int64_t K, bool full, int q) {
+  // The L (or R) rows of the stage starting at k0 into the slot at LDS byte address `slot`.
+  // `full` (wave-uniform): the stage lies wholly inside K, so no lane needs the k bound.
+  __device__ __forceinline__ void issue_l(unsigned slot, int64_t k0, int64_t K) {
+    const bool full = k0 + D::KB <= K;
     const unsigned kb = static_cast<unsigned>(k0 * 2);
-    if (q < D::QL) {
+#pragma unroll
+    for (int q = 0; q < D::QL; ++q) {
       unsigned off = offl[q] + kb;
       if (!full && k0 + kl[q] >= K) off = DMA_OOB;
-      dma16_at(rl, off, stage + wl + q * D::NW * D::RPL * D::ROW_BYTES);
-    } else {
-      const int u = q - D::QL;
-      unsigned off = offr[u] + kb;
-      if (!full && k0 + kr[u] >= K) off = DMA_OOB;
-      dma16_at(rr, off, stage + (C::BM + D::NW * D::RPL * u) * D::ROW_BYTES + wl);
+      dma16_at(rl, off, slot + wl + q * D::NW * D::RPL * D::ROW_BYTES);
     }
   }
-  __device__ __forceinline__ void issue(unsigned stage, int64_t k0, int64_t K) {
+  __device__ __forceinline__ void issue_r(unsigned slot, int64_t k0, int64_t K) {
     const bool full = k0 + D::KB <= K;
+    const unsigned kb = static_cast<unsigned>(k0 * 2);
 #pragma unroll
-    for (int q = 0; q < D::QL + D::QR; ++q) one(stage, k0, K, full, q);
+    for (int u = 0; u < D::QR; ++u) {
+      unsigned off = offr[u] + kb;
+      if (!full && k0 + kr[u] >= K) off = DMA_OOB;
+      dma16_at(rr, off, slot + wl + u * D::NW * D::RPL * D::ROW_BYTES);
+    }
   }
 };
 
 template <class C, class D>
-__device__ __forceinline__ void dma_compute(const unsigned char* stage,
+__device__ __forceinline__ void dma_compute(const unsigned char* lslot, const unsigned char* rslot,
                                             f32x16_t (&acc)[C::MI][C::NI]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
   const int lo = D::swz(lane & 31), hi = lane >> 5;  // fragment rows start at multiples of 32
-  const unsigned char* lt = stage + (wm * 32 * C::MI + (lane & 31)) * D::ROW_BYTES;
-  const unsigned char* rt = stage + (C::BM + wn * 32 * C::NI + (lane & 31)) * D::ROW_BYTES;
+  const unsigned char* lt = lslot + (wm * 32 * C::MI + (lane & 31)) * D::ROW_BYTES;
+  const unsigned char* rt = rslot + (wn * 32 * C::NI + (lane & 31)) * D::ROW_BYTES;
   constexpr int NB = GS_PF + 1;  // fragment buffers: reads run GS_PF k-steps ahead
   bf16x8_t a[NB][C::MI], b[NB][C::NI];
   auto load = [&](int buf, int ks) {
@@ -473,14 +481,28 @@ __device__ __forceinline__ void dma_compute(const unsigned char* stage,
 #endif
 }
 
-// The stage buffers: one __shared__ array of STAGES * STAGE_BYTES (the DMA is inline asm,
-// so the compiler does not track it and one array costs no extra waits).
+// The stage buffers: one __shared__ array of LDS_BYTES (the DMA is inline asm, so the
+// compiler does not track it and one array costs no extra waits).
 struct DmaLds {
   unsigned char* base;
   unsigned addr;  // LDS byte address of base
 };
 
-// Waits until at most `pending` (<= MAXP) stages of loads are still in flight.
+// Waits until at most `pending` loads of this wave are still in flight (rounded down to
+// the nearest constant <= MAXP; vmcnt takes an immediate).
+template <int MAXP>
+__device__ __forceinline__ void wait_atmost(int pending) {
+  if constexpr (MAXP > 0) {
+    if (pending >= MAXP) {
+      wait_vmcnt<MAXP>();
+      return;
+    }
+    wait_atmost<MAXP - 1>(pending);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+// Waits until at most `pending` (<= MAXP) stages of NQ loads each are still in flight.
 template <int NQ, int MAXP>
 __device__ __forceinline__ void wait_stages(int64_t pending) {
   if constexpr (MAXP > 0) {
@@ -494,27 +516,29 @@ __device__ __forceinline__ void wait_stages(int64_t pending) {
   }
 }
 
-// acc += L_tile R_tile^T over K, bf16 operands through the LDS-DMA ring.  Stage kt lives
-// in slot kt % STAGES; the loads of stage kt + STAGES - 1 are issued right after the
-// barrier that opens stage kt (every wave has finished reading that slot, stage kt - 1, by
-// then).  The steady-state loop body is one basic block: a constant vmcnt wait, barrier,
-// loads, MFMAs.
+// acc += L_tile R_tile^T over K, bf16 operands through the LDS-DMA rings.  The L rows of
+// stage kt live in L slot kt % STAGES and its R rows in R slot kt % RSTAGES; right after the
+// barrier that opens stage kt, the L rows of stage kt + STAGES - 1 and the R rows of stage
+// kt + RSTAGES - 1 are issued (each into the slot of stage kt - 1, which every wave has
+// finished reading by then).  The steady-state loop body is one basic block: a constant
+// vmcnt wait, barrier, loads, MFMAs.
 // K-side column sums (EPI_ROWDOT_KS): every stage's R rows [r0, r1) summed per feature k.
 // Wave w sums rows r0 + w, r0 + w + NW, ... for feature `lane` into wsum[kt % 3][w][lane]
 // (ks_load before the stage's MFMAs, ks_stage after them).  Two stages later (after two
 // barriers) the wave reads the NW wave sums of features 8w .. 8w + 7 of that stage
 // (ks_read, before the MFMAs) and one stage after that adds them in wave order and stores
-// them to row[k] (ks_store, right after the barrier, well ahead of the next vmcnt wait).  The
-// last three stages are flushed after the mainloop by lanes 0-7, 8-15 and 16-23.
+// them to row[k] (ks_store, right after the barrier and before that iteration's loads, so the
+// loads the next wait leaves in flight are all issued after it).  The last three stages are
+// flushed after the mainloop by lanes 0-7, 8-15 and 16-23.
 struct KsState {
   float* row;   // this workgroup's row of kbp (K floats)
   float* wsum;  // LDS [3][NW][64]
   int r0, r1;   // R rows of each stage this workgroup sums
-  int off[8];   // this lane's byte offsets (within a stage) of its first-pass rows
+  int off[8];   // this lane's byte offsets (within an R slot) of its first-pass rows
   bool whole;   // the first pass has 8 rows for every wave
 };
-// Rows go in passes of 8 per wave (8 NW rows per workgroup): byte offsets within a stage of
-// this lane's reads of rows base + wid + NW j; rows past r1 read a row inside the stage (and
+// Rows go in passes of 8 per wave (8 NW rows per workgroup): byte offsets within an R slot of
+// this lane's reads of rows base + wid + NW j; rows past r1 read a row inside the slot (and
 // ks_stage adds nothing for them).
 template <class C, class D>
 __device__ __forceinline__ void ks_offsets(const KsState& ks, int base, int (&off)[8]) {
@@ -525,8 +549,8 @@ __device__ __forceinline__ void ks_offsets(const KsState& ks, int base, int (&of
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int r = base + wid + NW * j;
-    const int sr = C::BM + (r < ks.r1 ? r : rsafe);
-    off[j] = sr * D::ROW_BYTES + ((c ^ D::swz(sr)) * 16) + e;
+    const int sr = r < ks.r1 ? r : rsafe;
+    off[j] = sr * D::ROW_BYTES + ((c ^ D::swz(C::BM + sr)) * 16) + e;
   }
 }
 template <class C, class D>
@@ -634,57 +658,85 @@ __device__ __forceinline__ float ks_bias_share(const GemmParams& p, const float*
   return q;
 }
 
-// With KS the two-stage ring's constant wait is vmcnt(0), which also covers the column-sum
-// stores; returns this lane's sum from ks_final (0 without KS).
+// Loads of this wave issued after the later of stage kt's L and R loads (iteration i issues
+// the L rows of stage i + AL and then the R rows of stage i + AR, AL <= AR, stages below nk
+// only; the prologue runs iterations -AR .. -1).
+template <class D>
+__device__ __forceinline__ int dma_pending(int kt, int nk) {
+  constexpr int AL = D::STAGES - 1, AR = D::RSTAGES - 1;
+  int n = 0, i = kt - AR;
+  if constexpr (AL < AR) {
+    i = kt - AL;  // the L rows of stage kt come later; the R rows of its iteration follow
+    if (i + AR < nk) n += D::QR;
+  }
+  for (++i; i < kt; ++i) n += (i + AL < nk ? D::QL : 0) + (i + AR < nk ? D::QR : 0);
+  return n;
+}
+
+// Returns this lane's sum from ks_final with KS (0 without).
 template <class C, class D, bool KS = false>
 __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R, int64_t mt,
                                              int64_t nt, int64_t K, const DmaLds& l,
                                              f32x16_t (&acc)[C::MI][C::NI],
                                              const KsState* ks = nullptr) {
   constexpr int NQ = D::QL + D::QR;
-  constexpr int AHEAD = D::STAGES - 1;  // stages in flight ahead of the one computed
-  static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
-  static_assert(!KS || D::STAGES == 2, "K-side sums assume the two-stage ring");
+  constexpr int AL = D::STAGES - 1, AR = D::RSTAGES - 1;  // stages each ring runs ahead
+  // Steady state: after the L loads of stage kt come the R loads of its iteration and AL - 1
+  // whole iterations (AL < AR), or AR - 1 whole iterations after its R loads (AL == AR).
+  constexpr int PEND = AL < AR ? D::QR + (AL - 1) * NQ : (AR - 1) * NQ;
+  static_assert(PEND < 64, "vmcnt range");
   DmaStreamer<C, D> st;
   st.init(L, R, mt, nt);
   const int nk = static_cast<int>((K + D::KB - 1) / D::KB);
-  auto slot = [&](int k) { return l.base + (k % D::STAGES) * D::STAGE_BYTES; };
-  auto slot_at = [&](int k) { return l.addr + (k % D::STAGES) * D::STAGE_BYTES; };
+  auto lslot = [&](int k) { return l.base + (k % D::STAGES) * D::L_SLOT; };
+  auto rslot = [&](int k) { return l.base + D::R_RING + (k % D::RSTAGES) * D::R_SLOT; };
+  auto issue = [&](int i) {  // iteration i's loads, where they exist
+    const int sl = i + AL, sr = i + AR;
+    if (sl >= 0 && sl < nk)
+      st.issue_l(l.addr + (sl % D::STAGES) * D::L_SLOT, static_cast<int64_t>(sl) * D::KB, K);
+    if (sr >= 0 && sr < nk)
+      st.issue_r(l.addr + D::R_RING + (sr % D::RSTAGES) * D::R_SLOT,
+                 static_cast<int64_t>(sr) * D::KB, K);
+  };
   float kf[C::WM * C::WN];  // KS: wave sums read for the store one stage later
   uint32_t kv[8];           // KS: the stage's first row reads
 #pragma unroll
-  for (int s = 0; s < AHEAD; ++s)
-    if (s < nk) st.issue(slot_at(s), static_cast<int64_t>(s) * D::KB, K);
+  for (int i = -AR; i < 0; ++i) issue(i);
+  // One iteration after its wait: the column-sum store (before the loads), the loads (both
+  // rings in the steady state), then the stage's MFMAs.
+  auto body = [&](int kt, auto steady) {
+    if constexpr (KS) {
+      if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
+    }
+    if constexpr (decltype(steady)::value) {
+      st.issue_l(l.addr + ((kt + AL) % D::STAGES) * D::L_SLOT,
+                 static_cast<int64_t>(kt + AL) * D::KB, K);
+      st.issue_r(l.addr + D::R_RING + ((kt + AR) % D::RSTAGES) * D::R_SLOT,
+                 static_cast<int64_t>(kt + AR) * D::KB, K);
+    } else {
+      issue(kt);
+    }
+    if constexpr (KS) {
+      if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
+      ks_load_at<C, D>(rslot(kt), ks->off, kv);
+      // Keep these reads out of the MFMA stream's fragment-read schedule.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    dma_compute<C, D>(lslot(kt), rslot(kt), acc);
+    // The adds of ks_stage may interleave with the MFMAs above (they read only kv).
+    if constexpr (KS) ks_stage<C, D>(rslot(kt), *ks, kt % 3, kv);
+  };
   int kt = 0;
-  for (; kt + AHEAD < nk; ++kt) {
-    wait_vmcnt<(AHEAD - 1) * NQ>();  // stage kt has landed
+  for (; kt + AR < nk; ++kt) {
+    wait_vmcnt<PEND>();  // stage kt has landed
     raw_barrier();
-    st.issue(slot_at(kt + AHEAD), static_cast<int64_t>(kt + AHEAD) * D::KB, K);
-    if constexpr (KS) {
-      if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
-      if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
-      ks_load_at<C, D>(slot(kt), ks->off, kv);
-      // Keep these reads out of the MFMA stream's fragment-read schedule.
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    dma_compute<C, D>(slot(kt), acc);
-    // The adds of ks_stage may interleave with the MFMAs above (they read only kv).
-    if constexpr (KS) ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
+    body(kt, std::true_type{});
   }
-  // Tail: no more loads; the stages still in flight drain one by one.
+  // Tail: the rings stop loading one after the other and drain.
   for (; kt < nk; ++kt) {
-    wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
+    wait_atmost<PEND>(dma_pending<D>(kt, nk));
     raw_barrier();
-    if constexpr (KS) {
-      if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
-      if (kt >= 2) ks_read<C, D>(*ks, (kt - 2) % 3, kf);
-      ks_load_at<C, D>(slot(kt), ks->off, kv);
-      // Keep these reads out of the MFMA stream's fragment-read schedule.
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    dma_compute<C, D>(slot(kt), acc);
-    // The adds of ks_stage may interleave with the MFMAs above (they read only kv).
-    if constexpr (KS) ks_stage<C, D>(slot(kt), *ks, kt % 3, kv);
+    body(kt, std::false_type{});
   }
   if constexpr (KS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   wait_vmcnt<0>();
@@ -864,11 +916,12 @@ __device__ __forceinline__ void rowdot_issue_z(const GemmParams& p, int64_t mt, 
 
 // KS: the bias terms come from the mainloop's K-side sums (ks_row, ks_last); the tile's
 // bias-dot share is read back while the Z tile comes in, and the Z-tile sums are skipped.
+// `red`: NT / 64 floats of LDS outside the Z tile and bsum, for the block sums.
 template <class C, class D, bool KS>
 __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
                                                   f32x16_t (&acc)[C::MI][C::NI], int64_t mt,
                                                   int64_t nt, unsigned char* lds,
-                                                  float (&colsum)[C::NI], float* bsum,
+                                                  float (&colsum)[C::NI], float* bsum, float* red,
                                                   const float* ks_row, float ks_last) {
   constexpr int CPR = ZTile<C>::CPR;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -901,8 +954,7 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
     colsum[ni] = s;
   }
   if constexpr (KS) {
-    __shared__ float kred[C::NT / 64];
-    const float tot = block_sum(ksq, kred);
+    const float tot = block_sum(ksq, red);
     if (threadIdx.x == 0) p.kpb[(p.p_row0 + mt) * p.p_ld + nt] = tot;
   } else if (p.BP != nullptr) {
     // Column sums of the tile over its BN token rows: thread t < GRP * CG takes column group
@@ -937,8 +989,7 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
       qb = vbm * t;
     }
     if (p.PB != nullptr) {  // the tile's bias-dot share, fixed-order block sum
-      __shared__ float qred[C::NT / 64];
-      const float tot = block_sum(qb, qred);
+      const float tot = block_sum(qb, red);
       if (threadIdx.x == 0) p.PB[(p.p_row0 + mt) * p.p_ld + nt] = tot;
     }
   }
@@ -947,6 +998,7 @@ __device__ __forceinline__ void rowdot_colsum_lds(const GemmParams& p,
 
 // Combines column sums across the half-waves and the WM waves sharing columns, then writes
 // per-row partials P[p_row0 + mt][n] or, with tile_reduce, one partial P[p_row0 + mt][nt].
+// `red`: WM BN + NT / 64 floats of LDS.
 template <class C>
 __device__ __forceinline__ void write_partials(const GemmParams& p, float (&colsum)[C::NI],
                                                int64_t mt, int64_t nt, float* red) {
@@ -960,7 +1012,7 @@ __device__ __forceinline__ void write_partials(const GemmParams& p, float (&cols
   }
   __syncthreads();
   if (p.tile_reduce) {
-    __shared__ float tred[C::NT / 64];
+    float* tred = red + C::WM * C::BN;
     float v = 0.f;
     for (int c = tid; c < C::BN; c += C::NT) {
 #pragma unroll
@@ -1001,6 +1053,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_nt_kernel(GemmParams
     } else {
       rowdot_colsum<Tr, C>(p, acc, mt, nt, colsum);
     }
+    static_assert((C::WM * C::BN + C::NT / 64) * 4 <= C::LDS_BYTES, "partial scratch");
     write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(smem_raw));
   }
 }
@@ -1008,9 +1061,9 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_nt_kernel(GemmParams
 // bf16, 16-byte aligned operands below 4 GiB: the LDS-DMA mainloop.
 template <class C, class D, int EPI>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParams p) {
-  constexpr int SB = D::STAGE_BYTES;
-  static_assert(D::STAGES * SB <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) unsigned char s0[D::STAGES * SB];
+  constexpr int SB = D::LDS_BYTES;
+  static_assert(SB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) unsigned char s0[SB];
   const DmaLds l{s0, lds_addr(s0)};
   int64_t mt, nt;
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
@@ -1044,25 +1097,36 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
       ghost_colsum<C>(p, acc, acc2, colsum);
     } else if constexpr (EPI == EPI_ROWDOT_KS) {
       // Every tile is whole along M and takes the LDS epilogue (checked by the host).
-      static_assert(static_cast<int64_t>(C::BN) * C::BM * 2 <= D::STAGES * SB, "Z tile in LDS");
-      rowdot_colsum_lds<C, D, true>(p, acc, mt, nt, s0, colsum, nullptr, ks_row, ks_last);
+      constexpr int ZB = C::BN * C::BM * 2, RED = C::NT / 64;
+      static_assert(ZB <= SB, "Z tile in LDS");
+      float* red;
+      if constexpr (ZB + RED * 4 <= SB) {
+        red = reinterpret_cast<float*>(s0 + ZB);
+      } else {
+        __shared__ float red_own[RED];
+        red = red_own;
+      }
+      rowdot_colsum_lds<C, D, true>(p, acc, mt, nt, s0, colsum, nullptr, red, ks_row, ks_last);
     } else {
-      constexpr bool fits = static_cast<int64_t>(C::BN) * C::BM * 2 <= D::STAGES * SB;
+      constexpr bool fits = static_cast<int64_t>(C::BN) * C::BM * 2 <= SB;
       const bool zlds = fits && p.z_vec_ok && (mt + 1) * C::BM <= p.m_rows &&
                         p.z_nbytes > 0 && p.z_nbytes < INT32_MAX;
       if constexpr (fits) {
         if (zlds) {
-          // The tile column-sum scratch sits behind the Z tile when the stages leave room.
-          constexpr int BSUM = C::NT / (C::BM / 4) * C::BM;
+          // The tile column-sum scratch and the block-sum scratch sit behind the Z tile when
+          // the stages leave room.
+          constexpr int BSUM = C::NT / (C::BM / 4) * C::BM, RED = C::NT / 64;
           constexpr int ZB = C::BN * C::BM * 2;
-          float* bsum;
-          if constexpr (ZB + BSUM * 4 <= D::STAGES * SB) {
+          float *bsum, *red;
+          if constexpr (ZB + (BSUM + RED) * 4 <= SB) {
             bsum = reinterpret_cast<float*>(s0 + ZB);
+            red = bsum + BSUM;
           } else {
-            __shared__ __attribute__((aligned(16))) float bsum_own[BSUM];
+            __shared__ __attribute__((aligned(16))) float bsum_own[BSUM + RED];
             bsum = bsum_own;
+            red = bsum_own + BSUM;
           }
-          rowdot_colsum_lds<C, D, false>(p, acc, mt, nt, s0, colsum, bsum, nullptr, 0.f);
+          rowdot_colsum_lds<C, D, false>(p, acc, mt, nt, s0, colsum, bsum, red, nullptr, 0.f);
         } else {
           rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
         }
@@ -1070,7 +1134,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
         rowdot_colsum<TrBF16, C>(p, acc, mt, nt, colsum);
       }
     }
-    static_assert(C::WM * C::BN * 4 <= SB, "partial scratch");
+    static_assert((C::WM * C::BN + C::NT / 64) * 4 <= SB, "partial scratch");
     write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
   }
 }
@@ -1081,9 +1145,9 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
 // rounds both Gram matrices to bf16 (its a_dot / b_dot are bf16 matmul outputs).
 template <class C, class D>
 __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
-  constexpr int SB = D::STAGE_BYTES;
-  static_assert(D::STAGES * SB <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(16))) unsigned char s0[D::STAGES * SB];
+  constexpr int SB = D::LDS_BYTES;
+  static_assert(SB <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) unsigned char s0[SB];
   const DmaLds l{s0, lds_addr(s0)};
   int64_t mt, nt;
   tile_of_block(p.m_tiles, p.n_tiles, mt, nt);
@@ -1135,7 +1199,7 @@ __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
     hadamard(std::true_type{});
   else
     hadamard(std::false_type{});
-  static_assert(C::WM * C::BN * 4 <= SB, "partial scratch");
+  static_assert((C::WM * C::BN + C::NT / 64) * 4 <= SB, "partial scratch");
   write_partials<C>(p, colsum, mt, nt, reinterpret_cast<float*>(s0));
 }
 
@@ -1761,7 +1825,7 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
 #define GS_STORE_TILE 2, 2, 1, 1
 #endif
 // bf16 GHOST through ghost_stash_kernel: 256x256 tiles, 8 waves of 128x64 (2x4 waves),
-// 128-byte stage rows, 2 stages (128 KiB of LDS).
+// 128-byte stage rows, 2 L slots and 3 R slots (160 KiB of LDS).
 #ifndef GS_GHOST_STASH
 #define GS_GHOST_STASH 1
 #endif
@@ -1769,7 +1833,7 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
 #define GS_STASH_TILE 2, 4, 4, 2
 #endif
 #ifndef GS_STASH_DMA
-#define GS_STASH_DMA 128, 2
+#define GS_STASH_DMA 128, 2, 3
 #endif
 // fp32 operands (precision checks, fp32 models) keep the small 128 x 128 tile.
 template <class Tr, int... Tile>
@@ -1789,19 +1853,28 @@ namespace {
 #ifndef GS_USE_DMA
 #define GS_USE_DMA 1
 #endif
-// Stage geometry of gemm_dma_kernel: three 128-byte-row stages when they fit in LDS,
-// else GS_WIDE_DMA.
-template <class C>
-using DmaFor = std::conditional_t<3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
-                                  DmaCfg<C, GS_WIDE_DMA>>;
-// The row-dot kernel's stage geometry (GS_ROWDOT_DMACFG = row bytes, stages) or DmaFor.
+// Stage geometry of gemm_dma_kernel: three 128-byte-row stages when they fit in LDS; else
+// two L slots and three R slots (GS_RDEEP) when those fit beside the epilogue's own LDS
+// (`extra` bytes); else GS_WIDE_DMA.
+#ifndef GS_RDEEP
+#define GS_RDEEP 1
+#endif
+template <class C, int extra = 0>
+using DmaFor = std::conditional_t<
+    3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
+    std::conditional_t<GS_RDEEP && (2 * C::BM + 3 * C::BN) * 128 + extra <= 160 * 1024,
+                       DmaCfg<C, 128, 2, 3>, DmaCfg<C, GS_WIDE_DMA>>>;
+// The row-dot kernel's stage geometry (GS_ROWDOT_DMACFG = row bytes, stages) or DmaFor; the
+// K-side sums keep 3 NW x 64 floats of LDS beside the rings.
+template <class C, int EPI>
+using DmaForAuto = DmaFor<C, EPI == EPI_ROWDOT_KS ? 3 * C::WM * C::WN * 64 * 4 : 0>;
 #ifdef GS_ROWDOT_DMACFG
 template <class C, int EPI>
 using DmaForEpi = std::conditional_t<EPI == EPI_ROWDOT || EPI == EPI_ROWDOT_KS,
-                                     DmaCfg<C, GS_ROWDOT_DMACFG>, DmaFor<C>>;
+                                     DmaCfg<C, GS_ROWDOT_DMACFG>, DmaForAuto<C, EPI>>;
 #else
 template <class C, int EPI>
-using DmaForEpi = DmaFor<C>;
+using DmaForEpi = DmaForAuto<C, EPI>;
 #endif
 #ifndef GS_ROWDOT_DMA
 #define GS_ROWDOT_DMA 1
@@ -1822,7 +1895,7 @@ struct Launch {
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
     using D = DmaForEpi<C, EPI>;
     if constexpr (std::is_same<Tr, TrBF16>::value &&
-                  D::STAGES * D::STAGE_BYTES <= 160 * 1024) {
+                  D::LDS_BYTES <= 160 * 1024) {
       const bool on = EPI == EPI_GHOST ||
                       ((EPI == EPI_ROWDOT || EPI == EPI_ROWDOT_KS) && GS_ROWDOT_DMA) ||
                       (EPI == EPI_STORE && GS_STORE_DMA);
@@ -1902,7 +1975,14 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 #ifndef GS_ROWDOT192
 #define GS_ROWDOT192 1
 #endif
-using RowdotCfg192 = Cfg<TrBF16, 2, 4, 3, 2>;
+#ifndef GS_ROWDOT192_TILE
+#define GS_ROWDOT192_TILE 2, 4, 3, 2
+#endif
+using RowdotCfg192 = Cfg<TrBF16, GS_ROWDOT192_TILE>;
+// The K-side-sum row-dot (one feature per lane, 8 per wave) keeps 8 waves.
+using RowdotCfg192K = Cfg<TrBF16, 2, 4, 3, 2>;
+static_assert(RowdotCfg192K::BM == RowdotCfg192::BM && RowdotCfg192K::BN == RowdotCfg192::BN,
+              "both 192-row tiles share the tile shape");
 template <class Tr>
 int64_t rowdot_bm(int64_t d_out, int64_t n_tiles, bool full) {
   constexpr int64_t B = RowdotCfg<Tr>::BM, B2 = RowdotCfg192::BM;
@@ -2769,12 +2849,12 @@ int launch_rowdot_bias(const void* A, const void* G, const void* V, const float*
   // Every tile must take the LDS epilogue, the only one that writes the bias terms.
   using RD = DmaForEpi<RC, EPI_ROWDOT>;
   using RD2 = DmaForEpi<RowdotCfg192, EPI_ROWDOT>;
-  static_assert(static_cast<int64_t>(RC::BN) * RC::BM * 2 <= RD::STAGES * RD::STAGE_BYTES &&
-                    RD::STAGES * RD::STAGE_BYTES <= 160 * 1024,
+  static_assert(static_cast<int64_t>(RC::BN) * RC::BM * 2 <= RD::LDS_BYTES &&
+                    RD::LDS_BYTES <= 160 * 1024,
                 "row-dot tile does not take the LDS epilogue");
   static_assert(static_cast<int64_t>(RowdotCfg192::BN) * RowdotCfg192::BM * 2 <=
-                        RD2::STAGES * RD2::STAGE_BYTES &&
-                    RD2::STAGES * RD2::STAGE_BYTES <= 160 * 1024,
+                        RD2::LDS_BYTES &&
+                    RD2::LDS_BYTES <= 160 * 1024,
                 "row-dot tile does not take the LDS epilogue");
   static_assert(RowdotCfg192::BN == RC::BN, "both row-dot tiles are BN tokens wide");
   // dk: the contracted feature dimension, dm: the M extent (the Z width).
@@ -2813,7 +2893,7 @@ int launch_rowdot_bias(const void* A, const void* G, const void* V, const float*
     return fail(GS_ERR_INVALID, "internal: row-dot tiles");
   int rc;
   if (sw)
-    rc = bm192 ? Launch<TrBF16, RowdotCfg192>::template run<EPI_ROWDOT_KS>(r, true, s)
+    rc = bm192 ? Launch<TrBF16, RowdotCfg192K>::template run<EPI_ROWDOT_KS>(r, true, s)
                : Launch<TrBF16, RC>::template run<EPI_ROWDOT_KS>(r, true, s);
   else
     rc = bm192 ? Launch<TrBF16, RowdotCfg192>::template run<EPI_ROWDOT>(r, true, s)

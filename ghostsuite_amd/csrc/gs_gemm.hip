@@ -1705,13 +1705,12 @@ __device__ __forceinline__ void tn_item(const TnParams& p, int64_t& mt, int64_t&
   const int64_t tiles = p.m_tiles * p.n_tiles;
   split = i / tiles;
   const int64_t r = i - split * tiles;
-  if (p.m_tiles <= p.n_tiles) {
-    nt = r / p.m_tiles;
-    mt = r - nt * p.m_tiles;
-  } else {
-    mt = r / p.n_tiles;
-    nt = r - mt * p.n_tiles;
-  }
+  // Selects rather than branches, so (mt, nt) stay in registers.
+  const bool m_inner = p.m_tiles <= p.n_tiles;
+  const int64_t inner = m_inner ? p.m_tiles : p.n_tiles;
+  const int64_t outer_i = r / inner, inner_i = r - outer_i * inner;
+  mt = m_inner ? inner_i : outer_i;
+  nt = m_inner ? outer_i : inner_i;
 }
 
 // One output tile per work item: bf16 out when there is one split, else fp32 partials

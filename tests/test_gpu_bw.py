@@ -141,16 +141,23 @@ def test_embedding_train_grad(gpu, gdt, odt, shape):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100),
-                                   (3, 1, 130, 1024), (4, 2, 64, 1600)])
-def test_layernorm_dots_and_grads(gpu, dtype, shape):
+                                   (3, 1, 130, 1024), (4, 2, 64, 1600), (20, 4, 1024, 768),
+                                   (10, 2, 2048, 2048), (5, 2, 9, 6)])
+@pytest.mark.parametrize("mid", [False, True])
+def test_layernorm_dots_and_grads(gpu, dtype, shape, mid):
+    """LayerNorm dots and grads against float64; `mid`: the val block between train rows
+    (the oracle sees the same samples with the val block moved to the end)."""
     N, n_val, T, Fd = shape
     X = randn((N, T, Fd), 11 + T, 2.0, dtype) + 0.5
     G = randn((N, T, Fd), 12 + T, 1e-3, dtype)
     n_t = N - n_val
-    print(f"layernorm shape={shape} dtype={dtype}", flush=True)
-    dw, db, gw, gb = _native.ops().layernorm_dot(X.to(gpu), G.to(gpu), n_val, 1e-5,
+    vs = 1 if mid else N - n_val
+    print(f"layernorm shape={shape} dtype={dtype} val_start={vs}", flush=True)
+    dw, db, gw, gb = _native.ops().layernorm_dot(X.to(gpu), G.to(gpu), n_val, 1e-5, val_start=vs,
                                                  grad_scale=N / n_t, grad_dtype=torch.float32)
     torch.cuda.synchronize()
+    X = torch.cat([X[:vs], X[vs + n_val:], X[vs:vs + n_val]])  # val rows last
+    G = torch.cat([G[:vs], G[vs + n_val:], G[vs:vs + n_val]])
     ww, wb = R.layernorm_dot_exact(X, G, n_val, 1e-5)
     tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
     assert_close(dw.cpu(), ww, tol, "ln weight dot")

@@ -138,17 +138,25 @@ def test_linear_auto_picks_cheaper_algorithm(gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(6, 2, 5, 40), (10, 3, 130, 96), (80, 16, 1, 10)])
-def test_bias_dot_and_grad(gpu, dtype, shape):
+@pytest.mark.parametrize("shape", [(6, 2, 5, 40), (10, 3, 130, 96), (80, 16, 1, 10),
+                                   (6, 2, 40, 3072), (4, 1, 33, 1030), (20, 4, 1024, 768),
+                                   (10, 2, 2048, 8192)])
+@pytest.mark.parametrize("mid", [False, True])
+def test_bias_dot_and_grad(gpu, dtype, shape, mid):
+    """Bias dots and train grad against float64; `mid`: the val block between train rows
+    (the oracle sees the same samples with the val block moved to the end)."""
     N, n_val, T, d = shape
     G = randn((N, T, d), 5 + T, 1e-3, dtype)
     scale = N / (N - n_val)
-    dot, grad = _native.ops().bias_dot(G.to(gpu), n_val, grad_scale=scale,
+    vs = 1 if mid else N - n_val
+    print(f"bias shape={shape} dtype={dtype} val_start={vs}", flush=True)
+    dot, grad = _native.ops().bias_dot(G.to(gpu), n_val, val_start=vs, grad_scale=scale,
                                        grad_dtype=torch.float32)
     torch.cuda.synchronize()
+    Go = torch.cat([G[:vs], G[vs + n_val:], G[vs:vs + n_val]])  # val rows last
     tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
-    assert_close(dot.cpu(), R.bias_dot_exact(G, n_val), tol, "bias dot")
-    want_grad = R.bias_train_grad(G.double() * N, n_val)
+    assert_close(dot.cpu(), R.bias_dot_exact(Go, n_val), tol, "bias dot")
+    want_grad = R.bias_train_grad(Go.double() * N, n_val)
     assert_close(grad.cpu(), want_grad, tol, "bias grad")
 
 

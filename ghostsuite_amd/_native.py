@@ -24,6 +24,7 @@ SEM_PAIRWISE_SUM, SEM_PRESUM = 0, 1
 ALGO_AUTO, ALGO_GHOST, ALGO_VALGRAD = 0, 1, 2
 ROUND_FP32, ROUND_REF_BF16 = 0, 1
 PROJ_KO_KI, PROJ_KI_KO = 0, 1
+ERR_UNSUPPORTED = -5  # gs_status GS_ERR_UNSUPPORTED: a valid request outside the kernels' limits
 ABI_VERSION = 1
 
 _TORCH_TO_GS = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32, torch.float16: DTYPE_F16}
@@ -74,6 +75,9 @@ _SIGNATURES = {
     "gs_linear_val_gradient_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I]),
     "gs_linear_val_gradient": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
                                     _P, _SZ, _P]),
+    "gs_linear_train_grad_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
+    "gs_linear_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I,
+                                  _I, _P, _SZ, _P]),
     "gs_linear_rowdot_bias_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
     "gs_linear_rowdot_bias": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
                                    _P, _I, _F, _P, _SZ, _P]),
@@ -262,6 +266,41 @@ class HipOps:
                                         _stream(dev))
         _check(rc, "gs_linear_val_gradient")
         return V
+
+    def linear_train_grad(self, A: torch.Tensor, G: torch.Tensor, n_val: int, scale: float, *,
+                          val_start=None, out_dtype: Optional[torch.dtype] = None,
+                          conv1d: bool = False) -> Optional[torch.Tensor]:
+        """scale * sum over the train rows of g a^T as [d_out, d_in] (Linear weight), or
+        a g^T as [d_in, d_out] with conv1d (gs_linear_train_grad); None for the cases the
+        kernel does not take (non-bf16 operands, unaligned rows, feature counts not multiples
+        of 8, operands past 2 GiB)."""
+        dev = _require_device(A, G)
+        if A.dtype != G.dtype:
+            raise GhostHipError(f"A and G dtypes differ: {A.dtype} vs {G.dtype}")
+        A = A.contiguous()
+        G = G.contiguous()
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T:
+            raise GhostHipError(f"A {tuple(A.shape)} and G {tuple(G.shape)} token counts differ")
+        vs = N - n_val if val_start is None else int(val_start)
+        dt = _gs_dtype(A)
+        lib = load_library()
+        ws_bytes = lib.gs_linear_train_grad_workspace(dt, N, n_val, T, d_in, d_out)
+        if ws_bytes == 0:
+            return None
+        odt = out_dtype or A.dtype
+        shape = (d_in, d_out) if conv1d else (d_out, d_in)
+        out = torch.empty(shape, dtype=odt, device=dev)
+        ws = _workspace(ws_bytes, dev)
+        rc = lib.gs_linear_train_grad(A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in,
+                                      d_out, float(scale), out.data_ptr(), _gs_dtype(out),
+                                      1 if conv1d else 0, ws.data_ptr(), ws_bytes, _stream(dev))
+        if rc == ERR_UNSUPPORTED:
+            return None
+        _check(rc, "gs_linear_train_grad")
+        return out
 
     def linear_bias_dot(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *, val_start=None,
                         semantics: int = SEM_PAIRWISE_SUM, algo: int = ALGO_AUTO,

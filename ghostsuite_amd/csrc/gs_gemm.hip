@@ -777,7 +777,7 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[C::MI][C::NI]) {
 // C = acc written to p.C (row-major, ld p.c_ld), bounded by p.m_rows x p.n_cols.
 template <class Tr, class C>
 __device__ __forceinline__ void store_epilogue(const GemmParams& p, f32x16_t (&acc)[C::MI][C::NI],
-                                               int64_t mt, int64_t nt) {
+                                               int64_t mt, int64_t nt, float scale = 1.f) {
   using E = typename Tr::E;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
@@ -791,7 +791,8 @@ __device__ __forceinline__ void store_epilogue(const GemmParams& p, f32x16_t (&a
       for (int e = 0; e < 16; ++e) {
         const int64_t m =
             mt * C::BM + wm * 32 * C::MI + mi * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < p.m_rows && n < p.n_cols) out[m * p.c_ld + n] = from_f32<E>(acc[mi][ni][e]);
+        if (m < p.m_rows && n < p.n_cols)
+          out[m * p.c_ld + n] = from_f32<E>(scale * acc[mi][ni][e]);
       }
     }
 }
@@ -1502,11 +1503,14 @@ struct TnParams {
   int64_t ldl, ldr, l_nbytes, r_nbytes;
   int64_t K, kper;  // k-rows in all, per split
   int64_t M, N, m_tiles, n_tiles;
-  void* out;        // splits == 1: bf16 [M][N]; else fp32 partials [split][M][N]
-  int splits;
+  void* out;        // part_out == 0: [M][N] (bf16, or fp32 with out_f32); else fp32 partials
+  int part_out;     //   [split][M][N], scaled and rounded by tn_reduce_kernel
+  float alpha;      // part_out == 0: the scale applied before the one rounding
+  int out_f32;
   float* vsum;      // null, or [split][vparts][M]: column sums of L over the split's k-rows
   int vsum_r;       // 1: vsum holds the column sums of R instead ([split][vparts][N])
   int vparts;       // the tiles along the other side (N, or M with vsum_r) split the k-rows
+  int64_t gap_at, gap;  // logical k-rows >= gap_at lie gap rows further on (a skipped block)
 };
 
 template <class C, class D>
@@ -1515,6 +1519,7 @@ struct TnStreamer {
   unsigned offl[D::QL], offr[D::QR];  // byte offset of the chunk in k-row 0, or DMA_OOB
   int rowl[D::QL], rowr[D::QR];        // k-row within the stage
   int64_t ldl2, ldr2;                  // row strides in bytes
+  int64_t gap_at, gap;                 // the skipped k-row block (TnParams)
 
   __device__ __forceinline__ void init(const TnParams& p, int64_t mt, int64_t nt) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -1522,6 +1527,8 @@ struct TnStreamer {
     rr = make_rsrc(p.R, p.r_nbytes);
     ldl2 = p.ldl * 2;
     ldr2 = p.ldr * 2;
+    gap_at = p.gap_at;
+    gap = p.gap;
 #pragma unroll
     for (int q = 0; q < D::QL; ++q) {
       const int byte = (wid + D::NW * q) * 1024 + lane * 16;  // within the L part of a stage
@@ -1545,16 +1552,18 @@ struct TnStreamer {
     const int wid = threadIdx.x >> 6;
 #pragma unroll
     for (int q = 0; q < D::QL; ++q) {
-      const int64_t k = k0 + rowl[q];
-      const unsigned off =
-          (k < k_end && offl[q] != DMA_OOB) ? static_cast<unsigned>(k * ldl2) + offl[q] : DMA_OOB;
+      const int64_t k = k0 + rowl[q], kp = k >= gap_at ? k + gap : k;
+      const unsigned off = (k < k_end && offl[q] != DMA_OOB)
+                               ? static_cast<unsigned>(kp * ldl2) + offl[q]
+                               : DMA_OOB;
       dma16(rl, off, stage + (wid + D::NW * q) * 1024);
     }
 #pragma unroll
     for (int q = 0; q < D::QR; ++q) {
-      const int64_t k = k0 + rowr[q];
-      const unsigned off =
-          (k < k_end && offr[q] != DMA_OOB) ? static_cast<unsigned>(k * ldr2) + offr[q] : DMA_OOB;
+      const int64_t k = k0 + rowr[q], kp = k >= gap_at ? k + gap : k;
+      const unsigned off = (k < k_end && offr[q] != DMA_OOB)
+                               ? static_cast<unsigned>(kp * ldr2) + offr[q]
+                               : DMA_OOB;
       dma16(rr, off, stage + D::L_BYTES + (wid + D::NW * q) * 1024);
     }
   }
@@ -1713,8 +1722,8 @@ __device__ __forceinline__ void tn_item(const TnParams& p, int64_t& mt, int64_t&
   nt = m_inner ? outer_i : inner_i;
 }
 
-// One output tile per work item: bf16 out when there is one split, else fp32 partials
-// reduced by tn_reduce_kernel.
+// One output tile per work item: bf16 out, or fp32 partials (several splits or an output
+// option) reduced by tn_reduce_kernel.
 template <class C, class D>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
@@ -1757,20 +1766,24 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
   e.m_rows = p.M;
   e.n_cols = p.N;
   e.c_ld = p.N;
-  if (p.splits == 1) {
+  if (!p.part_out) {
     e.C = p.out;
-    store_epilogue<TrBF16, C>(e, acc, mt, nt);
+    if (p.out_f32)
+      store_epilogue<TrF32, C>(e, acc, mt, nt, p.alpha);
+    else
+      store_epilogue<TrBF16, C>(e, acc, mt, nt, p.alpha);
   } else {
     e.C = static_cast<float*>(p.out) + split * p.M * p.N;
     store_epilogue<TrF32, C>(e, acc, mt, nt);
   }
 }
 
-// out[i] = bf16(sum over the splits of part[s][i]), fixed order, 4 elements per thread.
-// With vsum ([vs_rows][vs_n]) its rows are also summed into row 0, in place.
+// out[i] = alpha * (sum over the splits of part[s][i]) in fixed order, rounded once to bf16
+// (or stored as fp32 with out_f32), 4 elements per thread.  With vsum ([vs_rows][vs_n]) its
+// rows are also summed into row 0, in place.
 __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict__ part,
-                                                        int64_t count, int splits,
-                                                        uint16_t* __restrict__ out, float* vsum,
+                                                        int64_t count, int splits, void* out,
+                                                        float alpha, int out_f32, float* vsum,
                                                         int64_t vs_n, int64_t vs_rows) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (vsum != nullptr && i < vs_n) {
@@ -1806,10 +1819,18 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
     s.z += v.z;
     s.w += v.w;
   }
+  s.x *= alpha;
+  s.y *= alpha;
+  s.z *= alpha;
+  s.w *= alpha;
+  if (out_f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + i) = s;
+    return;
+  }
   uint2 o;
   o.x = pack_bf16x2(s.x, s.y);
   o.y = pack_bf16x2(s.z, s.w);
-  *reinterpret_cast<uint2*>(out + i) = o;
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = o;
 }
 
 // ------------------------------------------------------------------------------ host side
@@ -2024,10 +2045,12 @@ bool tn_ok(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, in
   return L == nullptr || (aligned16(L) && aligned16(R));
 }
 
-// Splits of the k-rows: enough workgroups to cover the CUs against the fp32 partials'
-// extra write + read.  Estimate: whole waves of 256 workgroups, each workgroup's share of the
-// flops at 1.5 TF/s (the rate measured for the 128 x 128 tile at the GPT-2 shapes), plus the
-// partials at 4 TB/s.
+// Splits of the k-rows: enough workgroups to cover the CUs against the fp32 partials' extra
+// write + read.  Estimate: two workgroups fit on a CU (512 slots), so the launch takes
+// ceil(items / 512) rounds of one workgroup's k-rows at ~2 TF/s per workgroup when the CUs
+// hold two (~3.2 TF/s alone, at most 256 items), plus the partials at 4 TB/s and the reduction
+// launch (rates measured for the 128 x 128 tile at the GPT-2 shapes: train gradients with
+// 16k k-rows take 3-4 splits at fc / qkv, 7 at proj).
 int64_t tn_kper(int64_t K, int sp) {
   return ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
          TnD::KB;
@@ -2035,12 +2058,14 @@ int64_t tn_kper(int64_t K, int sp) {
 int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
   const int64_t ksteps = ceil_div(K, static_cast<int64_t>(TnD::KB));
   if (GS_TN_SPLIT > 0) return static_cast<int>(std::min<int64_t>(GS_TN_SPLIT, ksteps));
-  const double tiles = static_cast<double>(ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN));
+  const int64_t tiles = ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN);
   int best = 1;
   double best_t = 1e30;
-  for (int sp = 1; sp <= 8 && sp <= std::max<int64_t>(1, ksteps / 4); ++sp) {
-    const double waves = std::ceil(tiles * sp / 256.0);
-    const double t = waves * 2.0 * M * N * K / (tiles * sp * 1.5e12) +
+  for (int sp = 1; sp <= 16 && sp <= std::max<int64_t>(1, ksteps / 4); ++sp) {
+    const int64_t items = tiles * sp;
+    const double rounds = std::ceil(static_cast<double>(items) / 512.0);
+    const double rate = items <= 256 ? 3.2e12 : 2.0e12;
+    const double t = rounds * 2.0 * TnC::BM * TnC::BN * tn_kper(K, sp) / rate +
                      (sp > 1 ? 8.0 * sp * M * N / 4e12 + 3e-6 : 0.0);
     if (t < best_t) {
       best_t = t;
@@ -2070,16 +2095,27 @@ bool val_tn(int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, in
 // TN_VPARTS), or with vsum_r [splits][parts][N] those of R (the first M tiles); their total
 // ends in row 0.
 constexpr int64_t TN_VPARTS = 4;
+// Output options of launch_tn beyond the plain bf16 product: a scale applied before the one
+// rounding, fp32 output, and a block of `gap` k-rows skipped at logical row gap_at (the
+// operands then span K + gap rows).
+struct TnOut {
+  float alpha = 1.f;
+  int out_f32 = 0;
+  int64_t gap_at = INT64_MAX, gap = 0;
+};
 int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
               int64_t N, void* out, float* part, hipStream_t s, float* vsum = nullptr,
-              bool vsum_r = false) {
+              bool vsum_r = false, const TnOut& o = TnOut{}) {
   TnParams p{};
   p.L = L;
   p.R = R;
   p.ldl = ldl;
   p.ldr = ldr;
-  p.l_nbytes = K * ldl * 2;
-  p.r_nbytes = K * ldr * 2;
+  const int64_t rows = o.gap_at < K ? K + o.gap : K;
+  p.l_nbytes = rows * ldl * 2;
+  p.r_nbytes = rows * ldr * 2;
+  p.gap_at = o.gap_at;
+  p.gap = o.gap;
   p.K = K;
   p.M = M;
   p.N = N;
@@ -2087,25 +2123,28 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   p.n_tiles = ceil_div(N, TnC::BN);
   p.kper = tn_kper(K, tn_splits_raw(K, M, N));
   const int sp = tn_splits(K, M, N);
-  p.splits = sp;
   p.vsum = vsum;
   p.vsum_r = vsum_r ? 1 : 0;
   p.vparts = static_cast<int>(std::min<int64_t>(
       TN_VPARTS, vsum_r ? ceil_div(M, TnC::BM) : ceil_div(N, TnC::BN)));
-  p.out = sp > 1 ? static_cast<void*>(part) : out;
-  if (sp > 1 && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
+  const bool via_part = sp > 1;
+  p.part_out = via_part ? 1 : 0;
+  p.alpha = o.alpha;
+  p.out_f32 = o.out_f32;
+  p.out = via_part ? static_cast<void*>(part) : out;
+  if (via_part && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
   const int64_t items = p.m_tiles * p.n_tiles * sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
   hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
                      dim3(TnC::NT), 0, s, p);
   int rc = check_launch("tn_gemm_kernel");
   const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts : 1;
-  if (rc || (sp == 1 && vs_rows == 1)) return rc;
-  const int64_t count = sp > 1 ? M * N : 0;  // a multiple of 8 (N % 8 == 0)
+  if (rc || (!via_part && vs_rows == 1)) return rc;
+  const int64_t count = via_part ? M * N : 0;  // a multiple of 8 (N % 8 == 0)
   const int64_t vs_n = vsum_r ? N : M;
   hipLaunchKernelGGL(tn_reduce_kernel,
                      dim3(static_cast<unsigned>(ceil_div(std::max(count, vs_n) / 4, 256))),
-                     dim3(256), 0, s, part, count, sp, static_cast<uint16_t*>(out), vsum, vs_n,
+                     dim3(256), 0, s, part, count, sp, out, o.alpha, o.out_f32, vsum, vs_n,
                      vs_rows);
   return check_launch("tn_reduce_kernel");
 }
@@ -2737,6 +2776,82 @@ RowdotPlan plan_rowdot_any(int dtype, int64_t N, int64_t n_val, int64_t T, int64
 }
 }  // namespace
 }  // namespace gs
+
+// ------------------------------------------------------------------ Linear train gradient
+namespace gs {
+namespace {
+// The train-gradient GEMM contracts over the train tokens, the row dimension of A and G as
+// they lie: the K-major GEMM of the val term, over logical k-rows [0, n_train T) with the
+// val block skipped.  layout 0: out [d_out][d_in] = G^T A (Linear weight), 1: [d_in][d_out]
+// = A^T G (HF Conv1D weight).
+struct TrainGradPlan {
+  const void *L, *R;
+  int64_t ldl, ldr, K, M, N;
+  TnOut o;
+};
+bool plan_train_grad(const void* A, const void* G, int64_t N, int64_t n_val, int64_t val_start,
+                     int64_t T, int64_t d_in, int64_t d_out, int layout, float scale,
+                     int out_dtype, TrainGradPlan& t) {
+  t.K = (N - n_val) * T;
+  t.o.alpha = scale;
+  t.o.out_f32 = out_dtype == GS_DTYPE_F32 ? 1 : 0;
+  t.o.gap_at = val_start * T < t.K ? val_start * T : INT64_MAX;
+  t.o.gap = t.o.gap_at < t.K ? n_val * T : 0;
+  const bool g_left = layout == 0;
+  t.L = g_left ? G : A;
+  t.R = g_left ? A : G;
+  t.ldl = g_left ? d_out : d_in;
+  t.ldr = g_left ? d_in : d_out;
+  t.M = t.ldl;
+  t.N = t.ldr;
+  // tn_ok bounds the byte offsets of every k-row the operands span (train and val rows).
+  return tn_ok(t.L, t.ldl, t.R, t.ldr, N * T, t.M, t.N);
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_train_grad_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                                 int64_t d_in, int64_t d_out) {
+  if (dtype != GS_DTYPE_BF16 || N <= 0 || n_val < 0 || n_val >= N || T <= 0 || d_in <= 0 ||
+      d_out <= 0)
+    return 0;
+  const int64_t K = (N - n_val) * T;
+  if (!tn_ok(nullptr, d_out, nullptr, d_in, N * T, d_out, d_in)) return 0;
+  Sizer sz;
+  sz.take<float>(tn_part_elems(K, d_out, d_in));  // fp32 split partials
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_train_grad(const void* A, const void* G, int dtype, int64_t N,
+                                    int64_t n_val, int64_t val_start, int64_t T, int64_t d_in,
+                                    int64_t d_out, float scale, void* out, int out_dtype,
+                                    int layout, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  if (N <= 0 || n_val < 0 || n_val >= N || T <= 0 || d_in <= 0 || d_out <= 0)
+    return fail(GS_ERR_INVALID, "gs_linear_train_grad: invalid shape");
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, "gs_linear_train_grad: val block outside the batch");
+  if (A == nullptr || G == nullptr || out == nullptr)
+    return fail(GS_ERR_INVALID, "gs_linear_train_grad: null pointer");
+  if (layout != 0 && layout != 1)
+    return fail(GS_ERR_INVALID, "gs_linear_train_grad: layout must be 0 or 1");
+  if (out_dtype != GS_DTYPE_BF16 && out_dtype != GS_DTYPE_F32)
+    return fail(GS_ERR_DTYPE, "gs_linear_train_grad: out_dtype must be bf16 or fp32");
+  if (dtype != GS_DTYPE_BF16)
+    return fail(GS_ERR_UNSUPPORTED, "gs_linear_train_grad: bf16 operands only");
+  TrainGradPlan t;
+  if (!plan_train_grad(A, G, N, n_val, val_start, T, d_in, d_out, layout, scale, out_dtype, t))
+    return fail(GS_ERR_UNSUPPORTED,
+                "gs_linear_train_grad: needs 16-byte aligned operands below 2 GiB and feature "
+                "counts that are multiples of 8");
+  const size_t need = gs_linear_train_grad_workspace(dtype, N, n_val, T, d_in, d_out);
+  if (workspace == nullptr || workspace_bytes < need - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_train_grad: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  float* part = cv.take<float>(tn_part_elems(t.K, t.M, t.N));
+  return launch_tn(t.L, t.ldl, t.R, t.ldr, t.K, t.M, t.N, out, part,
+                   static_cast<hipStream_t>(stream), nullptr, false, t.o);
+}
 
 extern "C" size_t gs_linear_rowdot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
                                              int64_t d_in, int64_t d_out) {

@@ -217,11 +217,39 @@ def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tenso
     n_t = A.size(0) - val_batch_size
     if n_t <= 0:
         return None
+    grad = _native_train_grad(A, B, val_batch_size, scale / n_t, False)
+    if grad is not None:
+        return grad
     A_tr = A[:n_t].reshape(-1, A.shape[-1])
     B_tr = B[:n_t].reshape(-1, B.shape[-1])
     if B_tr.dtype != A_tr.dtype:
         B_tr = B_tr.to(A_tr.dtype)
     return _scaled_mm(B_tr.t(), A_tr, scale / n_t)
+
+
+# Output tiles (128 x 128) below which the K-major train-gradient GEMM beats hipBLASLt:
+# with fewer tiles than CUs the product is a long-K, small-output GEMM that the K-major kernel
+# splits over the token rows (GPT-2-small: fc / fc_out 96-100 us against 152-160 us through
+# torch.addmm, proj 46-48 against 98), while outputs of 256 tiles and more (Pythia-1B layers,
+# the 50k-row lm_head) run faster through hipBLASLt (e.g. 2048x8192: 506 against 572 us).
+_TRAIN_GRAD_MAX_TILES = 256
+
+
+def _native_train_grad(A: torch.Tensor, B: torch.Tensor, val_batch_size: int, alpha: float,
+                       conv1d: bool) -> Optional[torch.Tensor]:
+    """The weight's train gradient from the K-major GEMM over the train rows as they lie
+    (gs_linear_train_grad: fp32 accumulation, alpha before the one rounding, in A's dtype);
+    None where that kernel does not apply (fp32 operands, unaligned or >2 GiB rows) or where
+    hipBLASLt is faster (outputs of _TRAIN_GRAD_MAX_TILES tiles and more)."""
+    if A.dtype != torch.bfloat16 or A.dim() < 2:
+        return None
+    tiles = math.ceil(A.shape[-1] / 128) * math.ceil(B.shape[-1] / 128)
+    if tiles >= _TRAIN_GRAD_MAX_TILES:
+        return None
+    B = B if B.dtype == A.dtype else B.to(A.dtype)
+    return ops().linear_train_grad(A, B, val_batch_size, alpha,
+                                   val_start=A.size(0) - val_batch_size, out_dtype=A.dtype,
+                                   conv1d=conv1d)
 
 
 def _scaled_mm(x: torch.Tensor, y: torch.Tensor, alpha: float) -> torch.Tensor:
@@ -363,6 +391,9 @@ def _compute_Conv1D_train_grad(layer, A: torch.Tensor, B: torch.Tensor, val_batc
                                scale: float = 1.0) -> torch.Tensor:
     """scale * sum_train A^T B / n_train, [d_in, d_out] (reference :474-506)."""
     n_t = A.size(0) - val_batch_size
+    grad = _native_train_grad(A, B, val_batch_size, scale / n_t, True)
+    if grad is not None:
+        return grad
     A_tr = A[:n_t].reshape(-1, A.shape[-1])
     B_tr = B[:n_t].reshape(-1, B.shape[-1]).to(A_tr.dtype)
     return _scaled_mm(A_tr.t(), B_tr, scale / n_t)

@@ -130,6 +130,22 @@ int gs_linear_val_gradient(const void* A, const void* G, int dtype, int64_t N, i
                            int semantics, void* V, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Train gradient of a Linear / HF Conv1D weight from the train rows (the val block
+ * [val_start, val_start + n_val) skipped), fp32 accumulation, scale applied before the one
+ * rounding to out_dtype (GS_DTYPE_BF16 or GS_DTYPE_F32):
+ *   layout 0: out [d_out, d_in] = scale * sum over train rows and tokens of g a^T (Linear)
+ *   layout 1: out [d_in, d_out] = scale * sum of a g^T (HF Conv1D)
+ * bf16 operands, 16-byte aligned, d_in and d_out multiples of 8, every row of A and G below
+ * 2 GiB of offset; other cases return GS_ERR_UNSUPPORTED (workspace query: 0).
+ * Reference: _compute_linear_train_grad (supported_layers_grad_samplers_dotprod.py:155-173)
+ * and _compute_Conv1D_train_grad (:474-506), with scale = 1 / n_train there. */
+size_t gs_linear_train_grad_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                      int64_t d_in, int64_t d_out);
+int gs_linear_train_grad(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                         int64_t val_start, int64_t T, int64_t d_in, int64_t d_out, float scale,
+                         void* out, int out_dtype, int layout, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* Row-dot with a caller-formed val gradient V = G_val^T A_val ([d_out, d_in], same dtype):
  *   out_dot[i] = sum_t g_it^T V a_it over the train rows (the second half of the
  *   VALGRAD algorithm of gs_linear_dot, for callers that form V with a library GEMM).

@@ -35,6 +35,16 @@ class OracleOps:
         bdot, grad = self.bias_dot(G, n_val, grad_scale=grad_scale, grad_dtype=grad_dtype)
         return dot, bdot, grad
 
+    def linear_train_grad(self, A, G, n_val, scale, *, val_start=None, out_dtype=None,
+                          conv1d=False):
+        self.calls.append(("linear_train_grad", tuple(A.shape), tuple(G.shape)))
+        N = A.shape[0]
+        a, _ = R.split_rows(A.double().reshape(N, -1, A.shape[-1]), n_val, val_start)
+        g, _ = R.split_rows(G.double().reshape(N, -1, G.shape[-1]), n_val, val_start)
+        a, g = a.reshape(-1, a.shape[-1]), g.reshape(-1, g.shape[-1])
+        w = (a.t() @ g) if conv1d else (g.t() @ a)
+        return (w * scale).to(out_dtype or A.dtype)
+
     def bias_dot(self, G, n_val, *, val_start=None, grad_scale=None, grad_dtype=None):
         self.calls.append(("bias_dot", tuple(G.shape)))
         dot = R.bias_dot_exact(G.float(), n_val, val_start).float()

@@ -321,3 +321,71 @@ def test_linear_bias_fused_declines_unsupported_shapes(gpu):
     assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None
     A, G = _inputs(6, 256, 64, 256, 7, torch.float32)         # fp32 operands
     assert ops.linear_bias_dot(A.to(gpu), G.to(gpu), 2, algo=_native.ALGO_VALGRAD) is None
+
+
+def _train_grad_want(A, G, n_val, vs, scale, conv1d, dev):
+    """float64 reference on the device: scale * sum over the train rows of g a^T (or a g^T)."""
+    N = A.shape[0]
+    keep = [i for i in range(N) if not vs <= i < vs + n_val]
+    a = A[keep].to(dev, torch.float64).reshape(-1, A.shape[-1])
+    g = G[keep].to(dev, torch.float64).reshape(-1, G.shape[-1])
+    w = (a.t() @ g) if conv1d else (g.t() @ a)
+    return (w * scale).cpu()
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", [
+    # N, n_val, T, d_in, d_out, val position
+    (6, 2, 33, 40, 24, "last"), (6, 2, 33, 40, 24, "first"), (6, 2, 33, 40, 24, "mid"),
+    (3, 1, 1, 8, 16, "mid"), (5, 1, 300, 136, 264, "mid"),
+    (20, 4, 1024, 768, 3072, "last"), (20, 4, 1024, 3072, 768, "last"),
+    (20, 4, 1024, 768, 2304, "mid"), (20, 4, 1024, 768, 768, "first"),
+    (10, 2, 2048, 2048, 8192, "last"),
+])
+@pytest.mark.parametrize("conv1d", [False, True])
+def test_linear_train_grad(gpu, out_dtype, case, conv1d):
+    """gs_linear_train_grad (K-major GEMM over the train rows, val block skipped) against a
+    float64 product; at bf16 output the one rounding is the only error."""
+    N, n_val, T, d_in, d_out, pos = case
+    vs = {"last": N - n_val, "first": 0, "mid": 1}[pos]
+    A = randn((N, T, d_in), 90 + T, 1.0, torch.bfloat16)
+    G = randn((N, T, d_out), 91 + T, 1e-3, torch.bfloat16)
+    scale = 1.25 / (N - n_val)
+    print(f"train grad case={case} out={out_dtype} conv1d={conv1d}", flush=True)
+    out = _native.ops().linear_train_grad(A.to(gpu), G.to(gpu), n_val, scale, val_start=vs,
+                                          out_dtype=out_dtype, conv1d=conv1d)
+    assert out is not None and out.dtype == out_dtype
+    assert tuple(out.shape) == ((d_in, d_out) if conv1d else (d_out, d_in))
+    want = _train_grad_want(A, G, n_val, vs, scale, conv1d, gpu)
+    tol = 1e-2 if out_dtype == torch.bfloat16 else FP32_TOL
+    assert_close(out.cpu(), want, tol, "train grad")
+
+
+def test_linear_train_grad_declines_and_sampler_falls_back(gpu):
+    """Cases outside the kernel return None (fp32 operands, feature counts not multiples of 8);
+    the Linear sampler then takes the addmm path, and at a supported shape its result is the
+    kernel's."""
+    from ghostsuite_amd.supported_layers_grad_samplers_dotprod import _compute_linear_train_grad
+    ops = _native.ops()
+    A = randn((4, 16, 40), 95, 1.0, torch.float32).to(gpu)
+    G = randn((4, 16, 24), 96, 1e-3, torch.float32).to(gpu)
+    assert ops.linear_train_grad(A, G, 1, 0.5) is None
+    A2 = randn((4, 16, 12), 97, 1.0, torch.bfloat16).to(gpu)
+    G2 = randn((4, 16, 24), 98, 1e-3, torch.bfloat16).to(gpu)
+    assert ops.linear_train_grad(A2, G2, 1, 0.5) is None
+    layer = torch.nn.Linear(12, 24)
+    for a, g in ((A, G), (A2, G2)):
+        got = _compute_linear_train_grad(layer, a, g, 1, scale=2.0)
+        want = _train_grad_want(a.cpu(), g.cpu(), 1, 3, 2.0 / 3, False, gpu)
+        assert_close(got.float().cpu(), want, 1e-2, "sampler fallback")
+    A3 = randn((4, 32, 40), 99, 1.0, torch.bfloat16).to(gpu)
+    G3 = randn((4, 32, 24), 100, 1e-3, torch.bfloat16).to(gpu)
+    got = _compute_linear_train_grad(torch.nn.Linear(40, 24), A3, G3, 1, scale=2.0)
+    assert torch.equal(got, ops.linear_train_grad(A3, G3, 1, 2.0 / 3))
+    # 256 output tiles and more: hipBLASLt through addmm (faster there).
+    from ghostsuite_amd.supported_layers_grad_samplers_dotprod import _scaled_mm
+    A4 = randn((3, 8, 2048), 101, 1.0, torch.bfloat16).to(gpu)
+    G4 = randn((3, 8, 2048), 102, 1e-3, torch.bfloat16).to(gpu)
+    got = _compute_linear_train_grad(torch.nn.Linear(2048, 2048), A4, G4, 1, scale=2.0)
+    want = _scaled_mm(G4[:2].reshape(-1, 2048).t(), A4[:2].reshape(-1, 2048), 1.0)
+    assert torch.equal(got, want)

@@ -144,35 +144,49 @@ def _apply_train_grad(layer: nn.Module, val_batch_size: int, loss_reduction: str
             f"Layer {layer.__class__.__name__} is not supported for training gradient "
             "computation. Ensure it is included in the _supported_layers_dotprod dictionary.")
     scale = getattr(layer, "backprops_scale", 1.0)
+    # The train-gradient kernels join the layer's dot kernels on the side stream: both read
+    # only this layer's activations and backprops, and the end-of-backward join orders
+    # param.train_grad before the optimizer reads it.
+    side = _overlap.on_side_stream(layer.__dict__.get("activations"),
+                                   layer.__dict__.get("backprops")) \
+        if options["overlap"] else contextlib.nullcontext()
     try:
-        if isinstance(layer, nn.LayerNorm):
-            compute_layer_train_grad(layer, layer.activations, layer.backprops, val_batch_size,
-                                     scale=scale)
-        else:
-            if hasattr(layer, 'weight') and layer.weight.initially_requires_grad:
-                grad_weight = compute_layer_train_grad(layer, layer.activations, layer.backprops,
-                                                       val_batch_size, scale=scale)
-                if grad_weight is APPLIED:
-                    pass   # the sampler added into param.train_grad itself
-                elif grad_weight is not None:
-                    _create_or_accumulate_train_grad(layer.weight, grad_weight)
-                else:
-                    raise ValueError(
-                        f"Layer {layer.__class__.__name__} returned None for weight gradient. "
-                        "Ensure the compute_layer_train_grad function is implemented correctly.")
-            if hasattr(layer, 'bias') and layer.bias is not None and \
-                    layer.bias.initially_requires_grad:
-                grad_bias = layer.__dict__.pop("_gs_bias_train_grad", None)
-                if grad_bias is None:
-                    grad_bias = _compute_train_grad_bias(layer.backprops, val_batch_size,
-                                                         loss_reduction=loss_reduction)
-                    if scale != 1.0:
-                        grad_bias = grad_bias * scale
-                _create_or_accumulate_train_grad(layer.bias, grad_bias)
+        with side:
+            _apply_train_grad_body(layer, compute_layer_train_grad, val_batch_size, scale,
+                                   loss_reduction)
     finally:
         for attr in ('activations', 'backprops', 'backprops_scale', '_gs_bias_train_grad',
                      '_gs_ln_train_grads', '_gs_bias_grad_scale', '_gs_ln_grad_scale'):
             layer.__dict__.pop(attr, None)
+
+
+def _apply_train_grad_body(layer: nn.Module, compute_layer_train_grad, val_batch_size: int,
+                           scale: float, loss_reduction: str):
+    """The train gradients of one layer (weight, then bias) into ``param.train_grad``."""
+    if isinstance(layer, nn.LayerNorm):
+        compute_layer_train_grad(layer, layer.activations, layer.backprops, val_batch_size,
+                                 scale=scale)
+    else:
+        if hasattr(layer, 'weight') and layer.weight.initially_requires_grad:
+            grad_weight = compute_layer_train_grad(layer, layer.activations, layer.backprops,
+                                                   val_batch_size, scale=scale)
+            if grad_weight is APPLIED:
+                pass   # the sampler added into param.train_grad itself
+            elif grad_weight is not None:
+                _create_or_accumulate_train_grad(layer.weight, grad_weight)
+            else:
+                raise ValueError(
+                    f"Layer {layer.__class__.__name__} returned None for weight gradient. "
+                    "Ensure the compute_layer_train_grad function is implemented correctly.")
+        if hasattr(layer, 'bias') and layer.bias is not None and \
+                layer.bias.initially_requires_grad:
+            grad_bias = layer.__dict__.pop("_gs_bias_train_grad", None)
+            if grad_bias is None:
+                grad_bias = _compute_train_grad_bias(layer.backprops, val_batch_size,
+                                                     loss_reduction=loss_reduction)
+                if scale != 1.0:
+                    grad_bias = grad_bias * scale
+            _create_or_accumulate_train_grad(layer.bias, grad_bias)
 
 
 def _compute_train_grad_bias(B: torch.Tensor, val_batch_size: int,

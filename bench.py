@@ -66,9 +66,12 @@ class TimedOps:
         return self.inner.linear_algo(*a, **k)
 
     def embedding_train_grad(self, ids, G, n_val, scale, out, **k):
-        n_tr = (G.shape[0] - n_val) * (G.numel() // G.shape[0])
-        nbytes = (n_tr * G.element_size() + ids.numel() * 8 +
-                  out.numel() * out.element_size() * (2 if k.get("accumulate") else 1))
+        # train rows of G and their ids, plus the table rows written: every row (overwrite),
+        # or read + written for at most one row per train token (accumulate)
+        n_tok = (G.shape[0] - n_val) * (ids.numel() // G.shape[0])
+        row = out.shape[-1] * out.element_size()
+        rows = 2 * min(out.shape[0], n_tok) if k.get("accumulate") else out.shape[0]
+        nbytes = n_tok * (G.shape[-1] * G.element_size() + 8) + rows * row
         return self._run("embedding_train_grad", ("hbm", nbytes),
                          self.inner.embedding_train_grad, ids, G, n_val, scale, out, **k)
 
@@ -98,6 +101,16 @@ class TimedOps:
                         self.inner.linear_bias_dot, A, G, n_val, **k)
         if out is None and self.enabled:
             self.records.pop()   # not supported for this shape: nothing ran
+        return out
+
+    def linear_train_grad(self, A, G, n_val, scale, **k):
+        N, d_in, d_out = A.shape[0], A.shape[-1], G.shape[-1]
+        T = A.numel() // (N * d_in)
+        flops = 2.0 * (N - n_val) * T * d_in * d_out
+        out = self._run(f"linear_train_grad[{d_in}x{d_out}]", ("mfma", flops),
+                        self.inner.linear_train_grad, A, G, n_val, scale, **k)
+        if out is None and self.enabled:
+            self.records.pop()   # not taken by the kernel: the sampler's addmm runs instead
         return out
 
     def bias_dot(self, G, n_val, **k):
@@ -576,6 +589,10 @@ KERNEL_SHAPES = {
                         "G[20,1024,2304] bf16, 4 val",
     "valgrad_bias_proj": "linear_bias_dot presum (weight + bias dots, bias grad), "
                          "A[20,1024,768] G[20,1024,768] bf16, 4 val",
+    "train_grad_fc": "linear_train_grad (fc weight's train gradient), A[20,1024,768] "
+                     "G[20,1024,3072] bf16, 16 train rows",
+    "train_grad_proj": "linear_train_grad (proj weight's train gradient), A[20,1024,768] "
+                       "G[20,1024,768] bf16, 16 train rows",
     "bias_fc": "bias_dot, G[20,1024,3072] bf16, 4 val",
     "layernorm": "layernorm_dot + grads, X,G[20,1024,768] bf16, 4 val",
     "embedding_wte": "embedding_dot, ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
@@ -637,6 +654,10 @@ def kernels_leg(dev, reps: int = 10):
                                                       algo=_native.ALGO_VALGRAD,
                                                       grad_scale=1.25))
         del a_op, g_op
+    out["train_grad_fc"] = timeit(lambda: ops.linear_train_grad(A2, G2, 4, 1.25 / 16))
+    GP = (A2 * 1e-3).contiguous()
+    out["train_grad_proj"] = timeit(lambda: ops.linear_train_grad(A2, GP, 4, 1.25 / 16))
+    del GP
     out["bias_fc"] = timeit(lambda: ops.bias_dot(G2, 4, grad_scale=1.25))
     X = rnd(20, 1024, 768)
     GL = rnd(20, 1024, 768, s=1e-3)

@@ -303,6 +303,83 @@ __global__ void __launch_bounds__(64 * LN2_WAVES) ln_rows_kernel(
   }
 }
 
+// ---------------------------------------------------------------- LayerNorm, wide rows
+// Rows wider than the register-resident kernels hold (F > LN_REG_MAX_F): a first pass writes
+// each token row's mean and rstd (one wave per row; the sum, then the squared deviations
+// from the mean, as the register kernels form them), then the feature pass takes one
+// (sample, token chunk, feature block) per workgroup, a thread per 16-byte feature chunk
+// walking the chunk's tokens, and writes the same per-(sample, chunk) partials.
+constexpr int64_t LN_REG_MAX_F = 2048;
+constexpr int LNS_WAVES = 4;
+template <class E>
+__global__ void __launch_bounds__(64 * LNS_WAVES) ln_row_stats_kernel(
+    const E* __restrict__ X, int64_t rows, int64_t F, float eps, int vec,
+    float2* __restrict__ stats) {
+  constexpr int VE = Vec<E>::VE;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * LNS_WAVES + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const E* xr = X + r * F;
+  const float invF = 1.0f / static_cast<float>(F);
+  float s = 0.f;
+  for (int64_t f = static_cast<int64_t>(lane) * VE; f < F; f += 64 * VE) {
+    Vec<E> x;
+    x.load(xr + f, vec && f + VE <= F, F - f);
+#pragma unroll
+    for (int i = 0; i < VE; ++i) s += x.v[i];
+  }
+  const float mean = wave_sum(s) * invF;
+  float q = 0.f;
+  for (int64_t f = static_cast<int64_t>(lane) * VE; f < F; f += 64 * VE) {
+    Vec<E> x;
+    x.load(xr + f, vec && f + VE <= F, F - f);
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      const float d = x.v[i] - mean;
+      q += f + i < F ? d * d : 0.f;
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) * invF + eps);
+  if (lane == 0) stats[r] = make_float2(mean, rstd);
+}
+
+template <class E>
+__global__ void __launch_bounds__(BW_THREADS) ln_feat_kernel(
+    const E* __restrict__ X, const E* __restrict__ G, int64_t T, int64_t F, int64_t chunks,
+    int vec, const float2* __restrict__ stats, float* __restrict__ part_w,
+    float* __restrict__ part_b) {
+  constexpr int VE = Vec<E>::VE;
+  const int64_t n = blockIdx.y, c = blockIdx.x;
+  const int64_t f = (static_cast<int64_t>(blockIdx.z) * BW_THREADS + threadIdx.x) * VE;
+  if (f >= F) return;
+  const int64_t t0 = c * LN_TOK_CHUNK, t1 = std::min<int64_t>(T, t0 + LN_TOK_CHUNK);
+  const bool full = vec && f + VE <= F;
+  float aw[VE], ab[VE];
+#pragma unroll
+  for (int i = 0; i < VE; ++i) aw[i] = ab[i] = 0.f;
+#pragma unroll 4
+  for (int64_t t = t0; t < t1; ++t) {
+    const int64_t row = n * T + t;
+    const float2 st = stats[row];
+    Vec<E> x, g;
+    x.load(X + row * F + f, full, F - f);
+    g.load(G + row * F + f, full, F - f);
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      aw[i] += g.v[i] * ((x.v[i] - st.x) * st.y);
+      ab[i] += g.v[i];
+    }
+  }
+  float* dw = part_w + (n * chunks + c) * F + f;
+  float* db = part_b != nullptr ? part_b + (n * chunks + c) * F + f : nullptr;
+#pragma unroll
+  for (int i = 0; i < VE; ++i) {
+    if (f + i >= F) break;
+    dw[i] = aw[i];
+    if (db != nullptr) db[i] = ab[i];
+  }
+}
+
 // ---------------------------------------------------------------- stage 2/3 (shared)
 // One or two feature sets (bias: g; LayerNorm: g*xhat and g) share each launch; blockIdx.z
 // (totals) / blockIdx.y (finish) selects the set.
@@ -772,6 +849,25 @@ void launch_ln_rows(const void* X, const void* G, int64_t N, int64_t T, int64_t 
 }
 
 template <class E>
+int launch_ln_wide(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
+                   int64_t chunks, float* pw, float* pb, float2* stats, hipStream_t s) {
+  constexpr int VE = Vec<E>::VE;
+  const int vec = (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
+                  (reinterpret_cast<uintptr_t>(G) % 16 == 0) && (F * sizeof(E)) % 16 == 0;
+  const int64_t rows = N * T, fblocks = cdiv(F, int64_t{BW_THREADS} * VE);
+  if (fblocks > 65535) return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: grid too large");
+  hipLaunchKernelGGL(ln_row_stats_kernel<E>, dim3(static_cast<unsigned>(cdiv(rows, LNS_WAVES))),
+                     dim3(64 * LNS_WAVES), 0, s, static_cast<const E*>(X), rows, F, eps, vec,
+                     stats);
+  hipLaunchKernelGGL(ln_feat_kernel<E>,
+                     dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(N),
+                          static_cast<unsigned>(fblocks)),
+                     dim3(BW_THREADS), 0, s, static_cast<const E*>(X), static_cast<const E*>(G),
+                     T, F, chunks, vec, stats, pw, pb);
+  return check_launch("ln_row_stats_kernel / ln_feat_kernel");
+}
+
+template <class E>
 int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F, float eps,
                   int64_t chunks, float* pw, float* pb, hipStream_t s) {
   constexpr int VE = 16 / sizeof(E);
@@ -870,6 +966,7 @@ extern "C" size_t gs_layernorm_dot_workspace(int64_t N, int64_t T, int64_t F) {
   if (N <= 0 || T <= 0 || F <= 0) return 0;
   Sizer sz;
   carve_feature(sz, N, T, F, 1);
+  if (F > LN_REG_MAX_F) sz.take<float2>(N * T);  // per-row mean / rstd
   return sz.used + 256;
 }
 
@@ -884,13 +981,15 @@ extern "C" int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t
     return fail(GS_ERR_DTYPE, "gs_layernorm_dot: grad_dtype must be bf16 or fp32");
   if (!batch_ok(N, n_val, val_start, T, F) || X == nullptr || G == nullptr)
     return fail(GS_ERR_INVALID, "gs_layernorm_dot: invalid arguments");
-  if (F > 2048) return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: F > 2048 not supported");
   Sizer sz;
   carve_feature(sz, N, T, F, 1);
+  if (F > LN_REG_MAX_F) sz.take<float2>(N * T);
   if (workspace == nullptr || workspace_bytes < sz.used)
     return fail(GS_ERR_WORKSPACE, "gs_layernorm_dot: workspace too small");
   Carver cv(workspace, workspace_bytes);
   const int64_t chunks = cdiv(T, LN_TOK_CHUNK);
+  if (N > 65535 || chunks > 65535)  // grid y / x of the stage-1 kernels
+    return fail(GS_ERR_UNSUPPORTED, "gs_layernorm_dot: more than 65535 samples or token chunks");
   float* pw = cv.take<float>(N * chunks * F);
   float* pb = cv.take<float>(N * chunks * F);
   float* Sw = cv.take<float>(N * F);
@@ -898,9 +997,17 @@ extern "C" int gs_layernorm_dot(const void* X, const void* G, int dtype, int64_t
   float* vw = cv.take<float>(F);
   float* vb = cv.take<float>(F);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = dtype == GS_DTYPE_BF16
-               ? launch_ln_any<uint16_t>(X, G, N, T, F, eps, chunks, pw, pb, s)
-               : launch_ln_any<float>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  int rc;
+  if (F > LN_REG_MAX_F) {
+    float2* stats = cv.take<float2>(N * T);
+    rc = dtype == GS_DTYPE_BF16
+             ? launch_ln_wide<uint16_t>(X, G, N, T, F, eps, chunks, pw, pb, stats, s)
+             : launch_ln_wide<float>(X, G, N, T, F, eps, chunks, pw, pb, stats, s);
+  } else {
+    rc = dtype == GS_DTYPE_BF16
+             ? launch_ln_any<uint16_t>(X, G, N, T, F, eps, chunks, pw, pb, s)
+             : launch_ln_any<float>(X, G, N, T, F, eps, chunks, pw, pb, s);
+  }
   if (rc) return rc;
   FeatureSets sets{};
   sets.set[0] = FeatureSet{pw, Sw, vw, out_grad_w, out_dot_w};

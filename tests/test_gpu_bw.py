@@ -142,7 +142,11 @@ def test_embedding_train_grad(gpu, gdt, odt, shape):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100),
                                    (3, 1, 130, 1024), (4, 2, 64, 1600), (20, 4, 1024, 768),
-                                   (10, 2, 2048, 2048), (5, 2, 9, 6)])
+                                   (10, 2, 2048, 2048), (5, 2, 9, 6),
+                                   # wider than the register-resident kernels: row statistics
+                                   # first, then the feature pass
+                                   (3, 1, 70, 2560), (4, 2, 33, 4100), (2, 1, 130, 8192),
+                                   (3, 1, 5, 2049)])
 @pytest.mark.parametrize("mid", [False, True])
 def test_layernorm_dots_and_grads(gpu, dtype, shape, mid):
     """LayerNorm dots and grads against float64; `mid`: the val block between train rows

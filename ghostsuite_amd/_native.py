@@ -75,6 +75,9 @@ _SIGNATURES = {
     "gs_linear_val_gradient_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I]),
     "gs_linear_val_gradient": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
                                     _P, _SZ, _P]),
+    "gs_linear_dot_train_grad_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I]),
+    "gs_linear_dot_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                                      _P, _I, _F, _P, _P, _I, _F, _P, _SZ, _P]),
     "gs_linear_train_grad_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
     "gs_linear_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I,
                                   _I, _P, _SZ, _P]),
@@ -266,6 +269,55 @@ class HipOps:
                                         _stream(dev))
         _check(rc, "gs_linear_val_gradient")
         return V
+
+    def linear_dot_train_grad(self, A: torch.Tensor, G: torch.Tensor, n_val: int, *,
+                              val_start=None, semantics: int = SEM_PAIRWISE_SUM,
+                              grad_scale: Optional[float] = None,
+                              grad_dtype: Optional[torch.dtype] = None, bias: bool = False,
+                              bias_grad_scale: Optional[float] = None,
+                              bias_grad_dtype: Optional[torch.dtype] = None):
+        """Weight dots and weight train gradient in one pass over the train rows
+        (gs_linear_dot_train_grad), with the bias dots and bias train gradient when `bias`.
+        Returns (dot, grad, bias_dot, bias_grad), entries not asked for None; None for the
+        cases the kernels do not take (non-bf16, unaligned, T not a multiple of 64, feature
+        counts not multiples of 8)."""
+        dev = _require_device(A, G)
+        if A.dtype != G.dtype:
+            raise GhostHipError(f"A and G dtypes differ: {A.dtype} vs {G.dtype}")
+        A = A.contiguous()
+        G = G.contiguous()
+        N = A.shape[0]
+        d_in, d_out = A.shape[-1], G.shape[-1]
+        T = _tokens(A, N, d_in)
+        if _tokens(G, N, d_out) != T:
+            raise GhostHipError(f"A {tuple(A.shape)} and G {tuple(G.shape)} token counts differ")
+        vs = N - n_val if val_start is None else int(val_start)
+        dt = _gs_dtype(A)
+        lib = load_library()
+        ws_bytes = lib.gs_linear_dot_train_grad_workspace(dt, N, n_val, T, d_in, d_out,
+                                                          semantics, 1 if bias else 0)
+        if ws_bytes == 0:
+            return None
+        ws = _workspace(ws_bytes, dev)
+        n_t = N - n_val
+        dot = torch.empty(n_t, dtype=torch.float32, device=dev)
+        grad = None
+        if grad_scale is not None:
+            grad = torch.empty((d_out, d_in), dtype=grad_dtype or A.dtype, device=dev)
+        bdot = torch.empty(n_t, dtype=torch.float32, device=dev) if bias else None
+        bgrad = None
+        if bias and bias_grad_scale is not None:
+            bgrad = torch.empty(d_out, dtype=bias_grad_dtype or A.dtype, device=dev)
+        rc = lib.gs_linear_dot_train_grad(
+            A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in, d_out, semantics,
+            dot.data_ptr(), _ptr(grad), _gs_dtype(grad) if grad is not None else DTYPE_BF16,
+            float(grad_scale or 0.0), _ptr(bdot), _ptr(bgrad),
+            _gs_dtype(bgrad) if bgrad is not None else DTYPE_BF16, float(bias_grad_scale or 0.0),
+            ws.data_ptr(), ws_bytes, _stream(dev))
+        if rc == ERR_UNSUPPORTED:
+            return None
+        _check(rc, "gs_linear_dot_train_grad")
+        return dot, grad, bdot, bgrad
 
     def linear_train_grad(self, A: torch.Tensor, G: torch.Tensor, n_val: int, scale: float, *,
                           val_start=None, out_dtype: Optional[torch.dtype] = None,

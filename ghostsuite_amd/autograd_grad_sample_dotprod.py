@@ -156,7 +156,8 @@ def _apply_train_grad(layer: nn.Module, val_batch_size: int, loss_reduction: str
                                    loss_reduction)
     finally:
         for attr in ('activations', 'backprops', 'backprops_scale', '_gs_bias_train_grad',
-                     '_gs_ln_train_grads', '_gs_bias_grad_scale', '_gs_ln_grad_scale'):
+                     '_gs_weight_train_grad', '_gs_ln_train_grads', '_gs_bias_grad_scale',
+                     '_gs_ln_grad_scale'):
             layer.__dict__.pop(attr, None)
 
 

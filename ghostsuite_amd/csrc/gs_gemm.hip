@@ -309,7 +309,7 @@ constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
 
 // Geometry of one LDS-DMA pipeline over the tile of config C: each stage holds ROWB bytes
 // (ROWB / 2 bf16 of K) of every L and R row.  The L rows cycle through NS slots and the R
-// rows through NSR >= NS slots (a deeper ring for the operand streamed from HBM keeps more
+// rows through NSR slots (a deeper ring for the operand whose loads take longer keeps more
 // of its bytes in flight); the L ring sits at byte 0 and the R ring behind it.  A wave-level
 // load moves 1 KiB = RPL rows.
 template <class C, int ROWB, int NS, int NSR = NS>
@@ -321,7 +321,7 @@ struct DmaCfg {
   static constexpr int KB = ROWB / 2;    // k elements per stage
   static constexpr int KSTEPS = KB / 16; // MFMA k-steps per stage
   static_assert(ROWB == 64 || ROWB == 128, "64- or 128-byte stage rows");
-  static_assert(NS >= 2 && NSR >= NS && NSR <= 8, "2 to 8 stages, the R ring at least as deep");
+  static_assert(NS >= 2 && NSR >= 2 && NS <= 8 && NSR <= 8, "2 to 8 slots per ring");
   static_assert((C::BM / RPL) % NW == 0 && (C::BN / RPL) % NW == 0,
                 "row groups must split over waves");
   static_assert(C::BM % 32 == 0, "R rows keep the swizzle phase of the stacked layout");
@@ -658,18 +658,28 @@ __device__ __forceinline__ float ks_bias_share(const GemmParams& p, const float*
   return q;
 }
 
-// Loads of this wave issued after the later of stage kt's L and R loads (iteration i issues
-// the L rows of stage i + AL and then the R rows of stage i + AR, AL <= AR, stages below nk
-// only; the prologue runs iterations -AR .. -1).
+// The two rings of a DMA pipeline in issue order: each iteration i loads stage i + A1 of the
+// shallower ring ("first", the L ring on a tie) and then stage i + A2 of the deeper one.
+template <class D>
+struct DmaOrder {
+  static constexpr int AL = D::STAGES - 1, AR = D::RSTAGES - 1;
+  static constexpr bool L_FIRST = AL <= AR;
+  static constexpr int A1 = L_FIRST ? AL : AR, A2 = L_FIRST ? AR : AL;
+  static constexpr int Q1 = L_FIRST ? D::QL : D::QR, Q2 = L_FIRST ? D::QR : D::QL;
+  static constexpr int NQ = D::QL + D::QR;
+  // Steady state: after the later of stage kt's loads (the first ring's, issued at iteration
+  // kt - A1) come the second ring's loads of that iteration (A1 < A2) and A1 - 1 whole
+  // iterations.
+  static constexpr int PEND = (A1 < A2 ? Q2 : 0) + (A1 - 1) * NQ;
+};
+// The same count near the end, where iterations issue only stages below nk (the prologue
+// runs iterations -A2 .. -1).
 template <class D>
 __device__ __forceinline__ int dma_pending(int kt, int nk) {
-  constexpr int AL = D::STAGES - 1, AR = D::RSTAGES - 1;
-  int n = 0, i = kt - AR;
-  if constexpr (AL < AR) {
-    i = kt - AL;  // the L rows of stage kt come later; the R rows of its iteration follow
-    if (i + AR < nk) n += D::QR;
-  }
-  for (++i; i < kt; ++i) n += (i + AL < nk ? D::QL : 0) + (i + AR < nk ? D::QR : 0);
+  using O = DmaOrder<D>;
+  int n = 0, i = kt - O::A1;
+  if (O::A1 < O::A2 && i + O::A2 < nk) n += O::Q2;
+  for (++i; i < kt; ++i) n += (i + O::A1 < nk ? O::Q1 : 0) + (i + O::A2 < nk ? O::Q2 : 0);
   return n;
 }
 
@@ -679,29 +689,37 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
                                              int64_t nt, int64_t K, const DmaLds& l,
                                              f32x16_t (&acc)[C::MI][C::NI],
                                              const KsState* ks = nullptr) {
-  constexpr int NQ = D::QL + D::QR;
-  constexpr int AL = D::STAGES - 1, AR = D::RSTAGES - 1;  // stages each ring runs ahead
-  // Steady state: after the L loads of stage kt come the R loads of its iteration and AL - 1
-  // whole iterations (AL < AR), or AR - 1 whole iterations after its R loads (AL == AR).
-  constexpr int PEND = AL < AR ? D::QR + (AL - 1) * NQ : (AR - 1) * NQ;
+  using O = DmaOrder<D>;
+  constexpr int AL = O::AL, AR = O::AR;  // stages each ring runs ahead
+  constexpr int PEND = O::PEND;
   static_assert(PEND < 64, "vmcnt range");
   DmaStreamer<C, D> st;
   st.init(L, R, mt, nt);
   const int nk = static_cast<int>((K + D::KB - 1) / D::KB);
   auto lslot = [&](int k) { return l.base + (k % D::STAGES) * D::L_SLOT; };
   auto rslot = [&](int k) { return l.base + D::R_RING + (k % D::RSTAGES) * D::R_SLOT; };
-  auto issue = [&](int i) {  // iteration i's loads, where they exist
+  auto load_l = [&](int sl) {
+    st.issue_l(l.addr + (sl % D::STAGES) * D::L_SLOT, static_cast<int64_t>(sl) * D::KB, K);
+  };
+  auto load_r = [&](int sr) {
+    st.issue_r(l.addr + D::R_RING + (sr % D::RSTAGES) * D::R_SLOT,
+               static_cast<int64_t>(sr) * D::KB, K);
+  };
+  auto issue = [&](int i) {  // iteration i's loads, where they exist, in DmaOrder
     const int sl = i + AL, sr = i + AR;
-    if (sl >= 0 && sl < nk)
-      st.issue_l(l.addr + (sl % D::STAGES) * D::L_SLOT, static_cast<int64_t>(sl) * D::KB, K);
-    if (sr >= 0 && sr < nk)
-      st.issue_r(l.addr + D::R_RING + (sr % D::RSTAGES) * D::R_SLOT,
-                 static_cast<int64_t>(sr) * D::KB, K);
+    const bool l_ok = sl >= 0 && sl < nk, r_ok = sr >= 0 && sr < nk;
+    if constexpr (O::L_FIRST) {
+      if (l_ok) load_l(sl);
+      if (r_ok) load_r(sr);
+    } else {
+      if (r_ok) load_r(sr);
+      if (l_ok) load_l(sl);
+    }
   };
   float kf[C::WM * C::WN];  // KS: wave sums read for the store one stage later
   uint32_t kv[8];           // KS: the stage's first row reads
 #pragma unroll
-  for (int i = -AR; i < 0; ++i) issue(i);
+  for (int i = -O::A2; i < 0; ++i) issue(i);
   // One iteration after its wait: the column-sum store (before the loads), the loads (both
   // rings in the steady state), then the stage's MFMAs.
   auto body = [&](int kt, auto steady) {
@@ -709,10 +727,13 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
       if (kt >= 3) ks_store<C, D>(*ks, kf, static_cast<int64_t>(kt - 3) * D::KB, K, 0);
     }
     if constexpr (decltype(steady)::value) {
-      st.issue_l(l.addr + ((kt + AL) % D::STAGES) * D::L_SLOT,
-                 static_cast<int64_t>(kt + AL) * D::KB, K);
-      st.issue_r(l.addr + D::R_RING + ((kt + AR) % D::RSTAGES) * D::R_SLOT,
-                 static_cast<int64_t>(kt + AR) * D::KB, K);
+      if constexpr (O::L_FIRST) {
+        load_l(kt + AL);
+        load_r(kt + AR);
+      } else {
+        load_r(kt + AR);
+        load_l(kt + AL);
+      }
     } else {
       issue(kt);
     }
@@ -727,7 +748,7 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
     if constexpr (KS) ks_stage<C, D>(rslot(kt), *ks, kt % 3, kv);
   };
   int kt = 0;
-  for (; kt + AR < nk; ++kt) {
+  for (; kt + O::A2 < nk; ++kt) {
     wait_vmcnt<PEND>();  // stage kt has landed
     raw_barrier();
     body(kt, std::true_type{});
@@ -1336,6 +1357,97 @@ __global__ void __launch_bounds__(256) rowdot_bias_finish_kernel(
   }
 }
 
+// After tgdot_kernel: blocks b < n_t take weight dot b from its `shares` wave shares.  Then
+// n_t * fb bias blocks: block (i, k) takes features m = 256 k + thread of sample i, the
+// sample's column sum of G at m (its cs_rows partial rows of csum) times vb[m] (the vp_rows
+// rows of VP, val column sums from val_colsum_kernel), block-summed into bpart[i][k]
+// (tgdot_bias_sum_kernel adds the fb parts).  The rest form the bias train gradient,
+// FINISH_GF features per block, over all n_t * cs_rows partial rows.  Fixed order throughout.
+constexpr int TG_FIN_F = 256;  // features per bias block
+template <class GE>
+__global__ void __launch_bounds__(256) tgdot_finish_kernel(
+    const float* __restrict__ pdot, int64_t shares, int64_t n_t, const float* __restrict__ csum,
+    int64_t cs_rows, int64_t M, const float* __restrict__ VP, int64_t vp_rows, float* out_dot,
+    float* bpart, int64_t fb, GE* bgrad, float bscale) {
+  __shared__ float red[4];
+  const int64_t b = blockIdx.x;
+  if (b < n_t) {
+    float s0 = 0.f, s1 = 0.f;
+    int64_t r = threadIdx.x;
+    for (; r + 256 < shares; r += 512) {
+      s0 += pdot[r * n_t + b];
+      s1 += pdot[(r + 256) * n_t + b];
+    }
+    if (r < shares) s0 += pdot[r * n_t + b];
+    const float s = block_sum(s0 + s1, red);
+    if (threadIdx.x == 0) out_dot[b] = s;
+    return;
+  }
+  const int64_t nb = bpart != nullptr ? n_t * fb : 0;
+  if (b < n_t + nb) {
+    const int64_t i = (b - n_t) / fb, k = (b - n_t) - i * fb;
+    const int64_t m = k * TG_FIN_F + threadIdx.x;
+    float s = 0.f;
+    if (m < M) {
+      const float* rows = csum + i * cs_rows * M + m;
+      float c[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      int64_t r = 0;
+      for (; r + 7 < cs_rows; r += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] += rows[(r + u) * M];
+      }
+      for (; r < cs_rows; ++r) c[0] += rows[r * M];
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      r = 0;
+      for (; r + 3 < vp_rows; r += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] += VP[(r + u) * M + m];
+      }
+      for (; r < vp_rows; ++r) v[0] += VP[r * M + m];
+      s = (((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]))) *
+          ((v[0] + v[1]) + (v[2] + v[3]));
+    }
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) bpart[i * fb + k] = s;
+    return;
+  }
+  if (bgrad == nullptr) return;
+  constexpr int GF = FINISH_GF, RG = 256 / GF;
+  __shared__ float gred[RG][GF];
+  const int c = threadIdx.x % GF, rg = threadIdx.x / GF;
+  const int64_t f = (b - n_t - nb) * GF + c, nrows = n_t * cs_rows;
+  float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+  if (f < M) {
+    int64_t k = rg;
+    for (; k + 3 * RG < nrows; k += 4 * RG) {
+      t0 += csum[k * M + f];
+      t1 += csum[(k + RG) * M + f];
+      t2 += csum[(k + 2 * RG) * M + f];
+      t3 += csum[(k + 3 * RG) * M + f];
+    }
+    for (; k < nrows; k += RG) t0 += csum[k * M + f];
+  }
+  gred[rg][c] = (t0 + t1) + (t2 + t3);
+  __syncthreads();
+  if (rg == 0 && f < M) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) t += gred[g][c];
+    bgrad[f] = from_f32<GE>(bscale * t);
+  }
+}
+
+// out_bdot[i] = the sum of bpart[i][0 .. fb) in order; one thread per sample.
+__global__ void __launch_bounds__(256) tgdot_bias_sum_kernel(const float* __restrict__ bpart,
+                                                             int64_t n_t, int64_t fb,
+                                                             float* out_bdot) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_t) return;
+  float s = 0.f;
+  for (int64_t k = 0; k < fb; ++k) s += bpart[i * fb + k];
+  out_bdot[i] = s;
+}
+
 // out[f][c] = row c of the row set, feature f (with `presum`: c = position, summed over all
 // segments in fp32).  64 x 64 tiles: 16-byte loads along features, a padded LDS tile, and
 // 16-byte stores along c.  Requires d % 8 == 0 and 16-byte aligned rows when `vec`.
@@ -1668,11 +1780,16 @@ __device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs
   }
 }
 
-template <class C, class D, bool RS>
+struct NoStageHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
+// `hook(kt)` runs after stage kt's MFMAs and column sums (the stage-end hook of tgdot_kernel).
+template <class C, class D, bool RS, class Hook = NoStageHook>
 __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
                                             int64_t k_begin, int64_t k_end, unsigned char* lds,
                                             f32x16_t (&acc)[C::MI][C::NI], bool colsum,
-                                            float (&cs)[4], int part) {
+                                            float (&cs)[4], int part, Hook hook = Hook{}) {
   constexpr int NQ = D::QL + D::QR;
   constexpr int AHEAD = D::STAGES - 1;
   static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
@@ -1690,12 +1807,14 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
     st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
     tn_compute<C, D>(slot(kt), acc);
     if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
+    hook(kt);
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
     tn_compute<C, D>(slot(kt), acc);
     if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
+    hook(kt);
   }
   wait_vmcnt<0>();
   raw_barrier();
@@ -1776,6 +1895,107 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
     e.C = static_cast<float*>(p.out) + split * p.M * p.N;
     store_epilogue<TrF32, C>(e, acc, mt, nt);
   }
+}
+
+// Row-dot and train gradient from one K-major GEMM over the train rows.  Per train sample i,
+// sum_t g_it^T V a_it = <V, G_i^T A_i>, and the train gradient is the sum over i of the same
+// G_i^T A_i, so a work item (split, mt, nt) accumulates G^T A over the whole samples of its
+// split (L = G's train rows, R = A's, logical k-rows with the val block skipped): at every
+// sample boundary (T k-rows, a multiple of the stage height) each wave forms <acc, V tile>
+// against the V tile it holds in registers and stores the growth since the previous boundary
+// as that sample's share; acc runs on and ends as the split's train-gradient partial.  With
+// csum the column sums of the L tile (G: the bias terms) are flushed per sample as well:
+// thread partials straight to memory, no barrier inside the stage ring.
+struct TgParams {
+  TnParams tn;          // k-rows per split (kper) a multiple of T; out: fp32 partials
+  const uint16_t* Vt;   // V^T: [N][M] bf16
+  int64_t T, n_t;       // k-rows per sample, train samples
+  float* pdot;          // [m_tiles * n_tiles][NW][n_t] wave shares of the weight dots
+  float* csum;          // null, or [n_t][vparts][NRG][M] per-sample column-sum partials of L
+};
+
+template <class C, class D>
+__global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) {
+  const TnParams& p = q.tn;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
+  int64_t mt, nt, split;
+  tn_item(p, mt, nt, split);
+  const int64_t k_begin = split * p.kper;
+  const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN, wn = wid % C::WN;
+  f32x16_t acc[C::MI][C::NI];
+  zero_acc<TrBF16, C>(acc);
+  float s_prev = 0.f;  // <acc, V tile> of this wave at the previous boundary
+  // This lane's V elements, loaded once and held for the work item: for block (i, j) and
+  // row group g, the 4 consecutive rows m(i, g) .. m(i, g) + 3 of column n(j), one 8-byte
+  // load of V^T row n (M and N are multiples of 8, so a group is wholly inside or outside
+  // the matrix).
+  uint2 vr[C::MI][C::NI][4];
+  {
+    const int64_t m_lane = mt * C::BM + wm * 32 * C::MI + 4 * (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < C::NI; ++j) {
+      const int64_t n = nt * C::BN + wn * 32 * C::NI + j * 32 + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t m = m_lane + i * 32 + 8 * g;
+          vr[i][j][g] = (n < p.N && m < p.M)
+                            ? *reinterpret_cast<const uint2*>(q.Vt + n * p.M + m)
+                            : make_uint2(0u, 0u);
+        }
+    }
+  }
+  static_assert(C::BM == C::BN, "one column-sum layout for both sides");
+  constexpr int CG = C::BM / 4, NRG = C::NT / CG;
+  const int part = static_cast<int>(nt);
+  const bool colsum = q.csum != nullptr && part < p.vparts;
+  float cs[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t tile = mt * p.n_tiles + nt;
+  // Stages left in the current sample (wave-uniform; no division in the stage loop).
+  const int sps = static_cast<int>(q.T / D::KB);
+  int left = sps;
+  int64_t sample = k_begin / q.T;
+  auto boundary = [&](int) {
+    if (--left != 0) return;
+    left = sps;
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint2 w = vr[i][j][g];
+          d += acc[i][j][4 * g] * __uint_as_float(w.x << 16) +
+               acc[i][j][4 * g + 1] * __uint_as_float(w.x & 0xFFFF0000u) +
+               acc[i][j][4 * g + 2] * __uint_as_float(w.y << 16) +
+               acc[i][j][4 * g + 3] * __uint_as_float(w.y & 0xFFFF0000u);
+        }
+    d = wave_sum(d);
+    if (lane == 0) q.pdot[(tile * (C::WM * C::WN) + wid) * q.n_t + sample] = d - s_prev;
+    s_prev = d;
+    if (colsum) {
+      const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
+      const int64_t col = mt * C::BM + 4 * cg;
+      float* dst = q.csum + ((sample * p.vparts + part) * NRG + rg) * p.M + col;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (col + e < p.M) dst[e] = cs[e];
+        cs[e] = 0.f;
+      }
+    }
+    ++sample;
+  };
+  mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs, part, boundary);
+  GemmParams e{};
+  e.m_rows = p.M;
+  e.n_cols = p.N;
+  e.c_ld = p.N;
+  e.C = static_cast<float*>(p.out) + split * p.M * p.N;
+  store_epilogue<TrF32, C>(e, acc, mt, nt);
 }
 
 // out[i] = alpha * (sum over the splits of part[s][i]) in fixed order, rounded once to bf16
@@ -1874,16 +2094,18 @@ namespace {
 #define GS_USE_DMA 1
 #endif
 // Stage geometry of gemm_dma_kernel: three 128-byte-row stages when they fit in LDS; else
-// two L slots and three R slots (GS_RDEEP) when those fit beside the epilogue's own LDS
-// (`extra` bytes); else GS_WIDE_DMA.
+// a third slot for one ring (GS_RDEEP 1: the R ring, 2: the L ring) when it fits beside the
+// epilogue's own LDS (`extra` bytes); else GS_WIDE_DMA.
 #ifndef GS_RDEEP
 #define GS_RDEEP 1
 #endif
+template <class C>
+using DmaDeep = std::conditional_t<GS_RDEEP == 2, DmaCfg<C, 128, 3, 2>, DmaCfg<C, 128, 2, 3>>;
 template <class C, int extra = 0>
 using DmaFor = std::conditional_t<
     3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
-    std::conditional_t<GS_RDEEP && (2 * C::BM + 3 * C::BN) * 128 + extra <= 160 * 1024,
-                       DmaCfg<C, 128, 2, 3>, DmaCfg<C, GS_WIDE_DMA>>>;
+    std::conditional_t<GS_RDEEP && DmaDeep<C>::LDS_BYTES + extra <= 160 * 1024, DmaDeep<C>,
+                       DmaCfg<C, GS_WIDE_DMA>>>;
 // The row-dot kernel's stage geometry (GS_ROWDOT_DMACFG = row bytes, stages) or DmaFor; the
 // K-side sums keep 3 NW x 64 floats of LDS beside the rings.
 template <class C, int EPI>
@@ -2851,6 +3073,212 @@ extern "C" int gs_linear_train_grad(const void* A, const void* G, int dtype, int
   float* part = cv.take<float>(tn_part_elems(t.K, t.M, t.N));
   return launch_tn(t.L, t.ldl, t.R, t.ldr, t.K, t.M, t.N, out, part,
                    static_cast<hipStream_t>(stream), nullptr, false, t.o);
+}
+
+// ------------------------------------------------------ weight dots + train gradient, one GEMM
+namespace gs {
+namespace {
+constexpr int TG_NRG = TnC::NT / (TnC::BM / 4);  // column-sum row groups of a workgroup
+struct TgPlan {
+  int presum;
+  int64_t vk;                // k-rows of the V GEMM (val rows, or T after the presum)
+  int64_t n_val, n_t, K;     // val and train samples, train k-rows
+  int64_t spl, sp;           // samples per split, splits
+  int64_t m_tiles, n_tiles, vparts;
+};
+bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
+           int semantics) {
+  if (dtype != GS_DTYPE_BF16 || n_val <= 0 || n_val >= N || T % TnD::KB != 0) return false;
+  if (semantics != GS_SEM_PAIRWISE_SUM && semantics != GS_SEM_PRESUM) return false;
+  if (!val_tn(dtype, n_val, T, d_in, d_out, semantics == GS_SEM_PRESUM)) return false;
+  return tn_ok(nullptr, d_out, nullptr, d_in, N * T, d_out, d_in);
+}
+TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, int semantics,
+               bool bias) {
+  TgPlan t{};
+  t.presum = semantics == GS_SEM_PRESUM ? 1 : 0;
+  t.vk = (t.presum ? 1 : n_val) * T;
+  t.n_val = n_val;
+  t.n_t = N - n_val;
+  t.K = t.n_t * T;
+  t.m_tiles = ceil_div(d_out, TnC::BM);
+  t.n_tiles = ceil_div(d_in, TnC::BN);
+  // Splits of whole samples, as many as the split estimate asks for where samples allow.
+  t.spl = ceil_div(t.n_t, static_cast<int64_t>(tn_splits_raw(t.K, d_out, d_in)));
+  t.sp = ceil_div(t.n_t, t.spl);
+  t.vparts = bias ? std::min<int64_t>(TN_VPARTS, t.n_tiles) : 0;
+  return t;
+}
+struct TgBufs {
+  uint16_t *abar, *gbar, *V;
+  float *vpart, *vp, *pdot, *csum, *bpart, *tgpart;
+};
+template <class S>
+TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
+  TgBufs b{};
+  b.abar = t.presum ? c.template take<uint16_t>(T * d_in) : nullptr;
+  b.gbar = t.presum ? c.template take<uint16_t>(T * d_out) : nullptr;
+  b.V = c.template take<uint16_t>(d_out * d_in);  // V^T, [d_in][d_out]
+  b.vpart = c.template take<float>(tn_part_elems(t.vk, d_out, d_in));
+  // Val column sums of G: the V GEMM's own partials for the pairwise semantics (its operands
+  // are the val rows as they lie); for the presum, whose V operands are rounded to bf16,
+  // val_colsum_kernel over the val rows.
+  const int64_t vp_rows = t.presum ? ceil_div(t.n_val * T, int64_t{VS_ROWS})
+                                   : tn_splits(t.vk, d_in, d_out) *
+                                         std::min<int64_t>(TN_VPARTS, t.n_tiles);
+  b.vp = t.vparts ? c.template take<float>(vp_rows * d_out) : nullptr;
+  b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * t.n_t);
+  b.csum = t.vparts ? c.template take<float>(t.n_t * t.vparts * TG_NRG * d_out) : nullptr;
+  b.bpart = t.vparts ? c.template take<float>(t.n_t * ceil_div(d_out, int64_t{TG_FIN_F}))
+                     : nullptr;
+  b.tgpart = c.template take<float>(t.sp * d_out * d_in);
+  return b;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" size_t gs_linear_dot_train_grad_workspace(int dtype, int64_t N, int64_t n_val,
+                                                     int64_t T, int64_t d_in, int64_t d_out,
+                                                     int semantics, int with_bias) {
+  if (N <= 0 || T <= 0 || d_in <= 0 || d_out <= 0) return 0;
+  if (!tg_ok(dtype, N, n_val, T, d_in, d_out, semantics)) return 0;
+  const TgPlan t = plan_tg(N, n_val, T, d_in, d_out, semantics, with_bias != 0);
+  Sizer sz;
+  carve_tg(sz, t, T, d_in, d_out);
+  return sz.used + 256;
+}
+
+extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype, int64_t N,
+                                        int64_t n_val, int64_t val_start, int64_t T,
+                                        int64_t d_in, int64_t d_out, int semantics,
+                                        float* out_dot, void* out_grad, int grad_dtype,
+                                        float grad_scale, float* out_bias_dot,
+                                        void* out_bias_grad, int bias_grad_dtype,
+                                        float bias_grad_scale, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  if (N <= 0 || T <= 0 || d_in <= 0 || d_out <= 0 || n_val <= 0 || n_val >= N)
+    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: invalid shape");
+  if (val_start < 0 || val_start + n_val > N)
+    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: val block outside the batch");
+  if (A == nullptr || G == nullptr || out_dot == nullptr)
+    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: null pointer");
+  if (semantics != GS_SEM_PAIRWISE_SUM && semantics != GS_SEM_PRESUM)
+    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: invalid semantics");
+  if ((out_grad != nullptr && grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32) ||
+      (out_bias_grad != nullptr && bias_grad_dtype != GS_DTYPE_BF16 &&
+       bias_grad_dtype != GS_DTYPE_F32))
+    return fail(GS_ERR_DTYPE, "gs_linear_dot_train_grad: gradient dtypes must be bf16 or fp32");
+  if (!tg_ok(dtype, N, n_val, T, d_in, d_out, semantics) || !aligned16(A) || !aligned16(G))
+    return fail(GS_ERR_UNSUPPORTED,
+                "gs_linear_dot_train_grad: needs bf16, 16-byte aligned operands below 2 GiB, "
+                "T a multiple of 64 and feature counts that are multiples of 8");
+  const bool bias = out_bias_dot != nullptr || out_bias_grad != nullptr;
+  const TgPlan t = plan_tg(N, n_val, T, d_in, d_out, semantics, bias);
+  if (workspace == nullptr ||
+      workspace_bytes < gs_linear_dot_train_grad_workspace(dtype, N, n_val, T, d_in, d_out,
+                                                           semantics, bias ? 1 : 0) - 256)
+    return fail(GS_ERR_WORKSPACE, "gs_linear_dot_train_grad: workspace too small");
+  Carver cv(workspace, workspace_bytes);
+  const TgBufs b = carve_tg(cv, t, T, d_in, d_out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  using E = TrBF16::E;
+  const E* Ap = static_cast<const E*>(A);
+  const E* Gp = static_cast<const E*>(G);
+  const E* La = Ap + val_start * T * d_in;
+  const E* Lg = Gp + val_start * T * d_out;
+  // V^T = A_val^T G_val (or the product of the val rows presummed per position); with a bias,
+  // the val rows' column sums of G in fp32 from the rows as they lie: from the V GEMM's
+  // workgroups (pairwise; their total ends in row 0) or val_colsum_kernel (presum).
+  if (t.presum) {
+    PresumPair pp{};
+    pp.in[0] = Ap;
+    pp.in[1] = Gp;
+    pp.out[0] = b.abar;
+    pp.out[1] = b.gbar;
+    pp.d[0] = d_in;
+    pp.d[1] = d_out;
+    const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
+                    static_cast<unsigned>(T), 2);
+    hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp,
+                       val_rows(n_val, val_start, T));
+    int rc = check_launch("presum_rows_vec_kernel");
+    if (rc) return rc;
+    La = b.abar;
+    Lg = b.gbar;
+  }
+  int rc = launch_tn(La, d_in, Lg, d_out, t.vk, d_in, d_out, b.V, b.vpart, s,
+                     t.presum ? nullptr : b.vp, true);
+  if (rc) return rc;
+  int64_t vp_rows = 1;  // rows of b.vp the finishing kernel sums
+  if (b.vp != nullptr && t.presum) {
+    vp_rows = ceil_div(n_val * T, int64_t{VS_ROWS});
+    const dim3 vgrid(static_cast<unsigned>(ceil_div(d_out, int64_t{VS_COLS})),
+                     static_cast<unsigned>(vp_rows));
+    hipLaunchKernelGGL(val_colsum_kernel, vgrid, dim3(256), 0, s, Gp + val_start * T * d_out,
+                       n_val * T, d_out, b.vp);
+    rc = check_launch("val_colsum_kernel");
+    if (rc) return rc;
+  }
+  // The train rows: dots at every sample boundary, train-gradient partials per split.
+  TgParams q{};
+  TnParams& p = q.tn;
+  p.L = G;
+  p.R = A;
+  p.ldl = d_out;
+  p.ldr = d_in;
+  p.l_nbytes = N * T * d_out * 2;
+  p.r_nbytes = N * T * d_in * 2;
+  p.gap_at = val_start * T < t.K ? val_start * T : INT64_MAX;
+  p.gap = p.gap_at < t.K ? n_val * T : 0;
+  p.K = t.K;
+  p.kper = t.spl * T;
+  p.M = d_out;
+  p.N = d_in;
+  p.m_tiles = t.m_tiles;
+  p.n_tiles = t.n_tiles;
+  p.out = b.tgpart;
+  p.part_out = 1;
+  p.alpha = 1.f;
+  p.vparts = static_cast<int>(t.vparts);
+  q.Vt = b.V;
+  q.T = T;
+  q.n_t = t.n_t;
+  q.pdot = b.pdot;
+  q.csum = b.csum;
+  const int64_t items = t.m_tiles * t.n_tiles * t.sp;
+  if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
+  hipLaunchKernelGGL((tgdot_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
+                     dim3(TnC::NT), 0, s, q);
+  rc = check_launch("tgdot_kernel");
+  if (rc) return rc;
+  if (out_grad != nullptr) {
+    const int64_t count = d_out * d_in;  // a multiple of 8
+    hipLaunchKernelGGL(tn_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(count / 4, 256))),
+                       dim3(256), 0, s, b.tgpart, count, static_cast<int>(t.sp), out_grad,
+                       grad_scale, grad_dtype == GS_DTYPE_F32 ? 1 : 0, nullptr, int64_t{0},
+                       int64_t{1});
+    rc = check_launch("tn_reduce_kernel");
+    if (rc) return rc;
+  }
+  const int64_t shares = t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN);
+  const int64_t cs_rows = t.vparts * TG_NRG;
+  const int64_t fb = ceil_div(d_out, int64_t{TG_FIN_F});
+  float* bpart = out_bias_dot != nullptr ? b.bpart : nullptr;
+  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{FINISH_GF}) : 0;
+  const dim3 grid(static_cast<unsigned>(t.n_t + (bpart != nullptr ? t.n_t * fb : 0) + gblocks));
+  if (bias_grad_dtype == GS_DTYPE_F32)
+    hipLaunchKernelGGL(tgdot_finish_kernel<float>, grid, dim3(256), 0, s, b.pdot, shares, t.n_t,
+                       b.csum, cs_rows, d_out, b.vp, vp_rows, out_dot, bpart, fb,
+                       static_cast<float*>(out_bias_grad), bias_grad_scale);
+  else
+    hipLaunchKernelGGL(tgdot_finish_kernel<uint16_t>, grid, dim3(256), 0, s, b.pdot, shares,
+                       t.n_t, b.csum, cs_rows, d_out, b.vp, vp_rows, out_dot, bpart, fb,
+                       static_cast<uint16_t*>(out_bias_grad), bias_grad_scale);
+  rc = check_launch("tgdot_finish_kernel");
+  if (rc || bpart == nullptr) return rc;
+  hipLaunchKernelGGL(tgdot_bias_sum_kernel, dim3(static_cast<unsigned>(ceil_div(t.n_t, int64_t{256}))),
+                     dim3(256), 0, s, bpart, t.n_t, fb, out_bias_dot);
+  return check_launch("tgdot_bias_sum_kernel");
 }
 
 extern "C" size_t gs_linear_rowdot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,

@@ -176,12 +176,53 @@ def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tens
     pairwise = layer.use_ghost_computation
     if not _overwritten_later(layer):
         dt = _dot_dtype(A, pairwise)
+        if _fused_dot_train_grad(layer, A, B, val_batch_size, pairwise, dt):
+            return
         if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, pairwise, dt,
                                                       _dot_dtype(B, False)):
             return
         _linear_like_dot(layer, A, B, val_batch_size, pairwise, dt)
     if layer.bias is not None:
         _bias_dot_and_grad(layer, B, val_batch_size, _dot_dtype(B, False))
+
+
+def _fused_dot_train_grad(layer: nn.Module, A: torch.Tensor, B: torch.Tensor,
+                          val_batch_size: int, pairwise: bool, dtype: torch.dtype) -> bool:
+    """Weight dot and weight train gradient (and with a bias its dot and train gradient) from
+    one K-major pass over the train rows: per train row, sum_t g^T V a = <V, G_i^T A_i>, and
+    the train gradient is the sum of the same G_i^T A_i (gs_linear_dot_train_grad).  Taken
+    for bf16 layers on the val-gradient algorithm whose weight trains; the train gradients
+    are parked for _apply_train_grad.  Returns False when the other paths must run."""
+    scale = getattr(layer, "_gs_bias_grad_scale", None)
+    bias = layer.bias is not None
+    if scale is None or dtype != torch.bfloat16 or A.dtype != torch.bfloat16 or \
+            (pairwise and options["store_pairs"]) or \
+            not getattr(layer.weight, "initially_requires_grad", False) or \
+            (bias and (layer.bias.dtype != torch.bfloat16 or
+                       not getattr(layer.bias, "initially_requires_grad", False))):
+        return False
+    Bc = B.to(dtype) if B.dtype != dtype else B
+    N, d_in, d_out = A.shape[0], A.shape[-1], Bc.shape[-1]
+    T = A.numel() // (N * d_in)
+    sem = _native.SEM_PAIRWISE_SUM if pairwise else _native.SEM_PRESUM
+    if ops().linear_algo(dtype, N, val_batch_size, T, d_in, d_out, sem,
+                         _ALGOS[options["linear_algo"]], False) != _native.ALGO_VALGRAD:
+        return False
+    res = ops().linear_dot_train_grad(A, Bc, val_batch_size, semantics=sem, grad_scale=scale,
+                                      grad_dtype=A.dtype, bias=bias, bias_grad_scale=scale,
+                                      bias_grad_dtype=layer.bias.dtype if bias else None)
+    if res is None:
+        return False
+    dot, grad, bias_dot, bias_grad = res
+    layer.weight.grad_dot_prod = dot
+    layer._gs_weight_train_grad = grad
+    if bias:
+        layer.bias.grad_dot_prod = bias_dot
+        layer._gs_bias_train_grad = bias_grad
+    if options["record_algorithms"]:
+        ALGO_LOG[getattr(layer, "name", id(layer))] = ("pairwise" if pairwise else "presum",
+                                                       "valgrad+train_grad")
+    return True
 
 
 def _fused_bias_dot(layer: nn.Module, A: torch.Tensor, B: torch.Tensor, val_batch_size: int,
@@ -217,6 +258,9 @@ def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tenso
     n_t = A.size(0) - val_batch_size
     if n_t <= 0:
         return None
+    parked = layer.__dict__.pop("_gs_weight_train_grad", None)
+    if parked is not None:   # formed with the dots (_fused_dot_train_grad), same scale
+        return parked
     grad = _native_train_grad(A, B, val_batch_size, scale / n_t, False)
     if grad is not None:
         return grad

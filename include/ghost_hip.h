@@ -130,6 +130,29 @@ int gs_linear_val_gradient(const void* A, const void* G, int dtype, int64_t N, i
                            int semantics, void* V, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* A Linear layer's weight dots and weight train gradient from one pass over the train rows
+ * (and, with out_bias_dot / out_bias_grad, its bias dots and bias train gradient):
+ *   out_dot[i]      = sum over train row i's tokens of g^T V a, V the val term of
+ *                     gs_linear_val_gradient (semantics as there)
+ *   out_grad        = grad_scale * sum over the train rows of g a^T, [d_out, d_in], grad_dtype
+ *   out_bias_dot[i] = sum_t <g_it, the val rows' column sum of G>
+ *   out_bias_grad   = bias_grad_scale * the train rows' column sum of G, bias_grad_dtype
+ * out_grad, out_bias_dot, out_bias_grad may be null.  bf16 operands, 16-byte aligned, T a
+ * multiple of 64, d_in and d_out multiples of 8, n_val >= 1, operands below 2 GiB; other
+ * cases return GS_ERR_UNSUPPORTED (workspace query: 0).  with_bias: 1 when a bias output is
+ * passed.  Reference: _compute_linear_dot_product (supported_layers_grad_samplers_dotprod.py
+ * :75-146) and _compute_linear_train_grad (:155-173) with _compute_train_grad_bias
+ * (autograd_grad_sample_dotprod.py:199-222). */
+size_t gs_linear_dot_train_grad_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                          int64_t d_in, int64_t d_out, int semantics,
+                                          int with_bias);
+int gs_linear_dot_train_grad(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                             int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                             int semantics, float* out_dot, void* out_grad, int grad_dtype,
+                             float grad_scale, float* out_bias_dot, void* out_bias_grad,
+                             int bias_grad_dtype, float bias_grad_scale, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Train gradient of a Linear / HF Conv1D weight from the train rows (the val block
  * [val_start, val_start + n_val) skipped), fp32 accumulation, scale applied before the one
  * rounding to out_dtype (GS_DTYPE_BF16 or GS_DTYPE_F32):

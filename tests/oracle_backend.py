@@ -35,6 +35,22 @@ class OracleOps:
         bdot, grad = self.bias_dot(G, n_val, grad_scale=grad_scale, grad_dtype=grad_dtype)
         return dot, bdot, grad
 
+    def linear_dot_train_grad(self, A, G, n_val, *, val_start=None, semantics=0,
+                              grad_scale=None, grad_dtype=None, bias=False,
+                              bias_grad_scale=None, bias_grad_dtype=None):
+        """The fused weight dot + train gradient (+ bias dot and gradient), as closed forms."""
+        self.calls.append(("linear_dot_train_grad", tuple(A.shape), tuple(G.shape)))
+        dot, _ = self.linear_dot(A, G, n_val, val_start=val_start, semantics=semantics)
+        grad = None
+        if grad_scale is not None:
+            grad = self.linear_train_grad(A, G, n_val, grad_scale, val_start=val_start,
+                                          out_dtype=grad_dtype)
+        bdot = bgrad = None
+        if bias:
+            bdot, bgrad = self.bias_dot(G, n_val, val_start=val_start,
+                                        grad_scale=bias_grad_scale, grad_dtype=bias_grad_dtype)
+        return dot, grad, bdot, bgrad
+
     def linear_train_grad(self, A, G, n_val, scale, *, val_start=None, out_dtype=None,
                           conv1d=False):
         self.calls.append(("linear_train_grad", tuple(A.shape), tuple(G.shape)))

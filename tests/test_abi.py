@@ -47,8 +47,9 @@ def test_invalid_arguments_return_status_and_message():
     assert lib.gs_kron_proj(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 1, 1, 4, 4,
                             ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 40, 4, 0, 1.0,
                             ctypes.c_void_p(16), 1, None, 0, None) == -3  # k = 40: needs ws
+    # F = 4096 takes the wide-row path: a well-formed request that needs its workspace
     assert lib.gs_layernorm_dot(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 4, 1, 3, 2, 4096,
-                                1e-5, None, None, None, None, 1, 1.0, None, 0, None) == -5
+                                1e-5, None, None, None, None, 1, 1.0, None, 0, None) == -3
 
 
 def test_workspace_queries():

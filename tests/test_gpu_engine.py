@@ -373,12 +373,22 @@ def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
         return dots, grads, dict(S.ALGO_LOG)
 
     print(f"gpt2 fused-bias engine n_v={n_v}", flush=True)
+    linears = ["h.0.fc", "h.0.fc_out", "h.0.proj", "h.0.qkv"]
+    # default: weight + bias dots and both train grads from one pass over the train rows
     dots, grads, log = run()
-    assert sorted(k for k, v in log.items() if v[1] == "valgrad+bias") == \
-        ["h.0.fc", "h.0.fc_out", "h.0.proj", "h.0.qkv"], log
+    assert sorted(k for k, v in log.items() if v[1] == "valgrad+train_grad") == linears, log
+    # without it: the fused weight + bias dot pass, train grad separately
+    monkeypatch.setattr(S, "_fused_dot_train_grad", lambda *a, **k: False)
+    dots1, grads1, log1 = run()
+    assert sorted(k for k, v in log1.items() if v[1] == "valgrad+bias") == linears, log1
+    # without both: separate weight and bias passes
     monkeypatch.setattr(S, "_fused_bias_dot", lambda *a, **k: False)
     dots2, grads2, log2 = run()
-    assert not any(v[1] == "valgrad+bias" for v in log2.values()), log2
+    assert not any(v[1] in ("valgrad+bias", "valgrad+train_grad") for v in log2.values()), log2
+    for name, d in dots1.items():
+        assert_close(d, dots2[name], 1e-2, f"fused bias vs separate dot {name}")
+    for name in grads1:
+        assert_close(grads1[name], grads2[name], 1e-2, f"fused bias vs separate grad {name}")
     semantics = {n: m.use_ghost_computation for n, m in model.named_modules()
                  if hasattr(m, "use_ghost_computation")}
     N = n_t + n_v

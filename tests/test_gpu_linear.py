@@ -389,3 +389,58 @@ def test_linear_train_grad_declines_and_sampler_falls_back(gpu):
     got = _compute_linear_train_grad(torch.nn.Linear(2048, 2048), A4, G4, 1, scale=2.0)
     want = _scaled_mm(G4[:2].reshape(-1, 2048).t(), A4[:2].reshape(-1, 2048), 1.0)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("case", [
+    # N, n_val, T, d_in, d_out, semantics, val position, bias
+    (6, 2, 64, 40, 24, "pairwise", "last", True),
+    (6, 2, 64, 40, 24, "presum", "mid", True),
+    (6, 2, 128, 136, 264, "pairwise", "first", False),
+    (3, 2, 64, 16, 8, "presum", "last", True),           # one train row
+    (7, 1, 192, 264, 136, "pairwise", "mid", True),
+    (20, 4, 1024, 768, 3072, "pairwise", "last", True),  # GPT-2-small fc
+    (20, 4, 1024, 3072, 768, "pairwise", "last", True),  # fc_out
+    (20, 4, 1024, 768, 2304, "presum", "last", True),    # qkv
+    (20, 4, 1024, 768, 768, "presum", "mid", True),      # proj
+    (10, 2, 2048, 2048, 8192, "pairwise", "last", True),  # Pythia-1B fc
+])
+@pytest.mark.parametrize("grad_dtype", [torch.bfloat16, torch.float32])
+def test_linear_dot_train_grad(gpu, case, grad_dtype):
+    """gs_linear_dot_train_grad (one K-major pass over the train rows: dots at the sample
+    boundaries, the train gradient from the same accumulators, per-sample column sums of G
+    for the bias) against float64: dots through the val-term form, the weight and bias
+    train gradients as closed forms."""
+    N, n_val, T, d_in, d_out, sem, pos, bias = case
+    vs = {"last": N - n_val, "first": 0, "mid": 1}[pos]
+    A = randn((N, T, d_in), 110 + T, 1.0, torch.bfloat16)
+    G = randn((N, T, d_out), 111 + T, 1e-3, torch.bfloat16)
+    n_t = N - n_val
+    semantics = _native.SEM_PAIRWISE_SUM if sem == "pairwise" else _native.SEM_PRESUM
+    print(f"dot+train grad case={case} grad={grad_dtype}", flush=True)
+    Ad, Gd = A.to(gpu), G.to(gpu)
+    res = _native.ops().linear_dot_train_grad(
+        Ad, Gd, n_val, val_start=vs, semantics=semantics, grad_scale=1.5 / n_t,
+        grad_dtype=grad_dtype, bias=bias, bias_grad_scale=0.75 / n_t, bias_grad_dtype=grad_dtype)
+    assert res is not None
+    dot, grad, bdot, bgrad = res
+    want_dot = R.linear_dot_valterm_exact(Ad, Gd, n_val, sem, val_start=vs).cpu()
+    assert_close(dot.cpu(), want_dot, BF16_TOL, "weight dot")
+    tol = 1e-2 if grad_dtype == torch.bfloat16 else FP32_TOL
+    assert_close(grad.float().cpu(), _train_grad_want(A, G, n_val, vs, 1.5 / n_t, False, gpu),
+                 tol, "weight train grad")
+    if bias:
+        assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val, vs), BF16_TOL, "bias dot")
+        tr, _ = R.split_rows(G.double().reshape(N, T, d_out), n_val, vs)
+        assert_close(bgrad.float().cpu(), tr.sum((0, 1)) * (0.75 / n_t), tol, "bias train grad")
+    else:
+        assert bdot is None and bgrad is None
+
+
+def test_linear_dot_train_grad_declines(gpu):
+    ops = _native.ops()
+    A, G = _inputs(6, 100, 64, 256, 5, torch.bfloat16)        # T not a multiple of 64
+    assert ops.linear_dot_train_grad(A.to(gpu), G.to(gpu), 2, grad_scale=1.0) is None
+    A, G = _inputs(6, 64, 12, 256, 6, torch.bfloat16)         # d_in not a multiple of 8
+    assert ops.linear_dot_train_grad(A.to(gpu), G.to(gpu), 2, grad_scale=1.0) is None
+    A, G = _inputs(6, 64, 64, 256, 7, torch.float32)          # fp32 operands
+    assert ops.linear_dot_train_grad(A.to(gpu), G.to(gpu), 2, grad_scale=1.0) is None

@@ -1628,7 +1628,11 @@ struct TnParams {
 template <class C, class D>
 struct TnStreamer {
   __amdgpu_buffer_rsrc_t rl, rr;
-  unsigned offl[D::QL], offr[D::QR];  // byte offset of the chunk in k-row 0, or DMA_OOB
+  // Byte offset of the lane's chunk relative to its stage's first k-row (row r of the stage
+  // times the row stride, plus the column), or DMA_OOB_ROW for columns outside the operand:
+  // a stage adds one wave-uniform base, and an out-of-range chunk stays at or above 2^31,
+  // past the buffer (the operands are below 2 GiB).
+  unsigned offl[D::QL], offr[D::QR];
   int rowl[D::QL], rowr[D::QR];        // k-row within the stage
   int64_t ldl2, ldr2;                  // row strides in bytes
   int64_t gap_at, gap;                 // the skipped k-row block (TnParams)
@@ -1648,7 +1652,7 @@ struct TnStreamer {
       const int c = slot ^ D::template swz<D::CL>(r);
       const int64_t m = mt * C::BM + c * 8;
       rowl[q] = r;
-      offl[q] = m < p.M ? static_cast<unsigned>(m * 2) : DMA_OOB;
+      offl[q] = m < p.M ? static_cast<unsigned>(r * ldl2 + m * 2) : DMA_OOB_ROW;
     }
 #pragma unroll
     for (int q = 0; q < D::QR; ++q) {
@@ -1657,26 +1661,29 @@ struct TnStreamer {
       const int c = slot ^ D::template swz<D::CR>(r);
       const int64_t n = nt * C::BN + c * 8;
       rowr[q] = r;
-      offr[q] = n < p.N ? static_cast<unsigned>(n * 2) : DMA_OOB;
+      offr[q] = n < p.N ? static_cast<unsigned>(r * ldr2 + n * 2) : DMA_OOB_ROW;
     }
   }
+  // The stage of logical k-rows [k0, k0 + KB): rows at or past k_end land as zeros, rows at
+  // or past gap_at come from gap rows further on.  Per stage only wave-uniform 32-bit values
+  // change: the base offset of row k0, the first row taking the gap and the first row past
+  // k_end (all byte offsets below 2^31: the operands are below 2 GiB).
   __device__ __forceinline__ void issue(unsigned char* stage, int64_t k0, int64_t k_end) {
     const int wid = threadIdx.x >> 6;
+    const int64_t kp0 = k0 >= gap_at ? k0 + gap : k0;
+    const int e_rel = k_end - k0 < D::KB ? static_cast<int>(k_end - k0) : D::KB;
+    const int g_rel = k0 < gap_at && gap_at - k0 < D::KB ? static_cast<int>(gap_at - k0) : D::KB;
+    const unsigned bl = static_cast<unsigned>(kp0 * ldl2), gl = static_cast<unsigned>(gap * ldl2);
+    const unsigned br = static_cast<unsigned>(kp0 * ldr2), gr = static_cast<unsigned>(gap * ldr2);
 #pragma unroll
     for (int q = 0; q < D::QL; ++q) {
-      const int64_t k = k0 + rowl[q], kp = k >= gap_at ? k + gap : k;
-      const unsigned off = (k < k_end && offl[q] != DMA_OOB)
-                               ? static_cast<unsigned>(kp * ldl2) + offl[q]
-                               : DMA_OOB;
-      dma16(rl, off, stage + (wid + D::NW * q) * 1024);
+      const unsigned off = offl[q] + bl + (rowl[q] >= g_rel ? gl : 0u);
+      dma16(rl, rowl[q] < e_rel ? off : DMA_OOB, stage + (wid + D::NW * q) * 1024);
     }
 #pragma unroll
     for (int q = 0; q < D::QR; ++q) {
-      const int64_t k = k0 + rowr[q], kp = k >= gap_at ? k + gap : k;
-      const unsigned off = (k < k_end && offr[q] != DMA_OOB)
-                               ? static_cast<unsigned>(kp * ldr2) + offr[q]
-                               : DMA_OOB;
-      dma16(rr, off, stage + D::L_BYTES + (wid + D::NW * q) * 1024);
+      const unsigned off = offr[q] + br + (rowr[q] >= g_rel ? gr : 0u);
+      dma16(rr, rowr[q] < e_rel ? off : DMA_OOB, stage + D::L_BYTES + (wid + D::NW * q) * 1024);
     }
   }
 };
@@ -1684,6 +1691,16 @@ struct TnStreamer {
 __device__ __forceinline__ s16x4_t lds_tr16(const unsigned char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4_t*)(p));
+}
+
+// One k-step of the TN schedule: each of the M MFMAs followed by its share of the RD
+// transpose reads of the next k-step, spread as evenly as they divide.
+template <int RD, int M, int G>
+__device__ __forceinline__ void tn_sched_kstep() {
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  constexpr int n = (RD * (G + 1)) / M - (RD * G) / M;
+  if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+  if constexpr (G + 1 < M) tn_sched_kstep<RD, M, G + 1>();
 }
 
 template <class C, class D>
@@ -1741,18 +1758,43 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
   // Instruction order: the first k-step's transpose reads, then each k-step's MFMAs with the
   // next k-step's reads (two per fragment) spread between them.
   constexpr int RD = 2 * (C::MI + C::NI), M = C::MI * C::NI;
-  static_assert(RD % M == 0, "reads per MFMA");
   __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
 #pragma unroll
-  for (int ks = 0; ks + 1 < D::KSTEPS; ++ks) {
-#pragma unroll
-    for (int g = 0; g < M; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, RD / M, 0);
-    }
-  }
+  for (int ks = 0; ks + 1 < D::KSTEPS; ++ks) tn_sched_kstep<RD, M, 0>();
   __builtin_amdgcn_sched_group_barrier(0x008, M, 0);
 #endif
+}
+
+// rc[i] = the column sums over a stage's k-rows of this wave's L fragment i, read back from
+// the stage through the same transpose reads as the MFMA operands (lane l: column l % 32 of
+// fragment i, half of each k-step's rows; lanes l and l + 32 together cover the stage), two
+// bf16 values per dot2 against (1, 1).
+template <class C, class D>
+__device__ __forceinline__ void tn_lsum(const unsigned char* stage, float (&rc)[C::MI]) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);  // (1, 1)
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / C::WN;
+  const int g = lane >> 4, a4 = (lane & 3) * 4, j = (lane >> 2) & 3;
+  const int row = 8 * (g >> 1) + j;
+  const int colh = 16 * (g & 1) + a4;
+#pragma unroll
+  for (int i = 0; i < C::MI; ++i) {
+    const int col = wm * 32 * C::MI + i * 32 + colh;
+    const int off = row * D::RL + (((col >> 3) ^ D::template swz<D::CL>(row)) * 16) + (col & 7) * 2;
+    float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D::KSTEPS; ++ks) {
+      const unsigned char* p = stage + off + ks * 16 * D::RL;
+      const uint2 lo = __builtin_bit_cast(uint2, lds_tr16(p));
+      const uint2 hi = __builtin_bit_cast(uint2, lds_tr16(p + 4 * D::RL));
+      t0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo.x), one, t0, false);
+      t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo.y), one, t1, false);
+      t0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi.x), one, t0, false);
+      t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi.y), one, t1, false);
+    }
+    rc[i] = t0 + t1;
+  }
 }
 
 // acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same
@@ -1781,10 +1823,11 @@ __device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs
 }
 
 struct NoStageHook {
-  __device__ __forceinline__ void operator()(int) const {}
+  __device__ __forceinline__ void operator()(int, const unsigned char*) const {}
 };
 
-// `hook(kt)` runs after stage kt's MFMAs and column sums (the stage-end hook of tgdot_kernel).
+// `hook(kt, stage)` runs after stage kt's MFMAs and column sums, with the stage still in
+// LDS (the stage-end hook of tgdot_kernel).
 template <class C, class D, bool RS, class Hook = NoStageHook>
 __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
                                             int64_t k_begin, int64_t k_end, unsigned char* lds,
@@ -1807,14 +1850,14 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
     st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
     tn_compute<C, D>(slot(kt), acc);
     if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
-    hook(kt);
+    hook(kt, slot(kt));
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
     tn_compute<C, D>(slot(kt), acc);
     if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
-    hook(kt);
+    hook(kt, slot(kt));
   }
   wait_vmcnt<0>();
   raw_barrier();
@@ -1899,22 +1942,24 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
 
 // Row-dot and train gradient from one K-major GEMM over the train rows.  Per train sample i,
 // sum_t g_it^T V a_it = <V, G_i^T A_i>, and the train gradient is the sum over i of the same
-// G_i^T A_i, so a work item (split, mt, nt) accumulates G^T A over the whole samples of its
-// split (L = G's train rows, R = A's, logical k-rows with the val block skipped): at every
-// sample boundary (T k-rows, a multiple of the stage height) each wave forms <acc, V tile>
-// against the V tile it holds in registers and stores the growth since the previous boundary
-// as that sample's share; acc runs on and ends as the split's train-gradient partial.  With
-// csum the column sums of the L tile (G: the bias terms) are flushed per sample as well:
-// thread partials straight to memory, no barrier inside the stage ring.
+// G_i^T A_i, so a work item (split, mt, nt) accumulates G^T A over the k-rows of its split
+// (L = G's train rows, R = A's, logical k-rows with the val block skipped): at every sample
+// boundary (T k-rows, a multiple of the stage height) and at a split's end inside a sample,
+// each wave forms <acc, V tile> against the V tile it holds in registers and stores the
+// growth since the previous boundary as its share of that sample; acc runs on and ends as
+// the split's train-gradient partial.  With CS the column sums of the L tile (G: the bias
+// terms) are taken per stage as well, after the stage's MFMAs, spread over the workgroups.
 struct TgParams {
-  TnParams tn;          // k-rows per split (kper) a multiple of T; out: fp32 partials
+  TnParams tn;          // k-rows per split (kper) a multiple of the stage height, >= T;
+                        // out: fp32 partials
   const uint16_t* Vt;   // V^T: [N][M] bf16
-  int64_t T, n_t;       // k-rows per sample, train samples
-  float* pdot;          // [m_tiles * n_tiles][NW][n_t] wave shares of the weight dots
-  float* csum;          // null, or [n_t][vparts][NRG][M] per-sample column-sum partials of L
+  int64_t T, n_t;       // k-rows per sample (a multiple of the stage height), train samples
+  float* pdot;          // [m_tiles * n_tiles][NW][2 slots][n_t] wave shares of the weight dots
+  float* csum;          // with CS: [n_t][2 T / stage height][M] column sums of L, two rows
+                        // (halves of the stage's k-rows) per stage
 };
 
-template <class C, class D>
+template <class C, class D, bool CS>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) {
   const TnParams& p = q.tn;
   __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
@@ -1922,7 +1967,8 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   tn_item(p, mt, nt, split);
   const int64_t k_begin = split * p.kper;
   const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const int wm = wid / C::WN, wn = wid % C::WN;
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
@@ -1948,19 +1994,25 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
         }
     }
   }
-  static_assert(C::BM == C::BN, "one column-sum layout for both sides");
-  constexpr int CG = C::BM / 4, NRG = C::NT / CG;
-  const int part = static_cast<int>(nt);
-  const bool colsum = q.csum != nullptr && part < p.vparts;
-  float cs[4] = {0.f, 0.f, 0.f, 0.f};
+  // Column sums of L (G's train rows: the bias terms), with CS: every workgroup along N
+  // takes a share, so no work item runs longer than the others.  After the MFMAs of the
+  // stages kt with kt mod (n_tiles * WN) == nt * WN + wn, wave (nt, wn) reads its L fragments
+  // back from the stage and sums them (the two waves wm = 0, 1 cover the m-tile's columns
+  // once), then stores the sums in the rows of (stage within its sample) of that sample:
+  // every (sample, stage, column) is written once.
+  const int cs_every = static_cast<int>(p.n_tiles) * C::WN;
+  int cs_left = static_cast<int>(nt) * C::WN + wn;  // stages until this wave's next sum
   const int64_t tile = mt * p.n_tiles + nt;
-  // Stages left in the current sample (wave-uniform; no division in the stage loop).
+  // Stages left in the current sample (wave-uniform; no division in the stage loop).  A
+  // split may start or end inside a sample (kper >= T, so a sample meets at most two
+  // splits): the share of the part before a split's end goes to slot 0, the part after a
+  // split's start to slot 1; a sample wholly inside a split writes its share to slot 0 and
+  // zeros to slot 1, so every slot is written exactly once.
   const int sps = static_cast<int>(q.T / D::KB);
-  int left = sps;
   int64_t sample = k_begin / q.T;
-  auto boundary = [&](int) {
-    if (--left != 0) return;
-    left = sps;
+  int left = static_cast<int>(((sample + 1) * q.T - k_begin) / D::KB);
+  bool started = sample * q.T == k_begin;  // the current sample starts inside this split
+  auto flush = [&](bool ended) {
     float d = 0.f;
 #pragma unroll
     for (int i = 0; i < C::MI; ++i)
@@ -1975,21 +2027,40 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
                acc[i][j][4 * g + 3] * __uint_as_float(w.y & 0xFFFF0000u);
         }
     d = wave_sum(d);
-    if (lane == 0) q.pdot[(tile * (C::WM * C::WN) + wid) * q.n_t + sample] = d - s_prev;
-    s_prev = d;
-    if (colsum) {
-      const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
-      const int64_t col = mt * C::BM + 4 * cg;
-      float* dst = q.csum + ((sample * p.vparts + part) * NRG + rg) * p.M + col;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (col + e < p.M) dst[e] = cs[e];
-        cs[e] = 0.f;
-      }
+    const int slot = started ? 0 : 1;
+    const bool whole = started && ended;
+    float* pd = q.pdot + (tile * (C::WM * C::WN) + wid) * 2 * q.n_t + sample;
+    if (lane == 0) {
+      pd[slot * q.n_t] = d - s_prev;
+      if (whole) pd[q.n_t] = 0.f;
     }
+    s_prev = d;
+  };
+  auto hook = [&](int, const unsigned char* stage) {
+    if constexpr (CS) {
+      if (cs_left == 0) {
+        cs_left = cs_every;
+        float rc[C::MI];
+        tn_lsum<C, D>(stage, rc);
+        // lanes l and l + 32 hold halves of the same column: rows 2 s and 2 s + 1
+        float* dst = q.csum + (sample * 2 * sps + 2 * (sps - left) + (lane >> 5)) * p.M;
+#pragma unroll
+        for (int i = 0; i < C::MI; ++i) {
+          const int64_t col = mt * C::BM + wm * 32 * C::MI + i * 32 + (lane & 31);
+          if (col < p.M) dst[col] = rc[i];
+        }
+      }
+      --cs_left;
+    }
+    if (--left != 0) return;
+    flush(true);
+    left = sps;
+    started = true;
     ++sample;
   };
-  mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs, part, boundary);
+  float cs[4];
+  mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, false, cs, 0, hook);
+  if (k_end < (sample + 1) * q.T && k_end > sample * q.T) flush(false);  // ends inside a sample
   GemmParams e{};
   e.m_rows = p.M;
   e.n_cols = p.N;
@@ -3078,12 +3149,11 @@ extern "C" int gs_linear_train_grad(const void* A, const void* G, int dtype, int
 // ------------------------------------------------------ weight dots + train gradient, one GEMM
 namespace gs {
 namespace {
-constexpr int TG_NRG = TnC::NT / (TnC::BM / 4);  // column-sum row groups of a workgroup
 struct TgPlan {
   int presum;
   int64_t vk;                // k-rows of the V GEMM (val rows, or T after the presum)
   int64_t n_val, n_t, K;     // val and train samples, train k-rows
-  int64_t spl, sp;           // samples per split, splits
+  int64_t kper, sp;          // k-rows per split (at least one sample), splits
   int64_t m_tiles, n_tiles, vparts;
 };
 bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
@@ -3103,9 +3173,12 @@ TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
   t.K = t.n_t * T;
   t.m_tiles = ceil_div(d_out, TnC::BM);
   t.n_tiles = ceil_div(d_in, TnC::BN);
-  // Splits of whole samples, as many as the split estimate asks for where samples allow.
-  t.spl = ceil_div(t.n_t, static_cast<int64_t>(tn_splits_raw(t.K, d_out, d_in)));
-  t.sp = ceil_div(t.n_t, t.spl);
+  // The train-gradient GEMM's splits, at least one sample long (a sample then meets at most
+  // two splits).
+  t.sp = tn_splits(t.K, d_out, d_in);
+  t.kper = tn_kper(t.K, static_cast<int>(t.sp));
+  if (t.kper < T) t.kper = T;
+  t.sp = ceil_div(t.K, t.kper);
   t.vparts = bias ? std::min<int64_t>(TN_VPARTS, t.n_tiles) : 0;
   return t;
 }
@@ -3127,8 +3200,8 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
                                    : tn_splits(t.vk, d_in, d_out) *
                                          std::min<int64_t>(TN_VPARTS, t.n_tiles);
   b.vp = t.vparts ? c.template take<float>(vp_rows * d_out) : nullptr;
-  b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * t.n_t);
-  b.csum = t.vparts ? c.template take<float>(t.n_t * t.vparts * TG_NRG * d_out) : nullptr;
+  b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2 * t.n_t);
+  b.csum = t.vparts ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * d_out) : nullptr;
   b.bpart = t.vparts ? c.template take<float>(t.n_t * ceil_div(d_out, int64_t{TG_FIN_F}))
                      : nullptr;
   b.tgpart = c.template take<float>(t.sp * d_out * d_in);
@@ -3231,7 +3304,7 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
   p.gap_at = val_start * T < t.K ? val_start * T : INT64_MAX;
   p.gap = p.gap_at < t.K ? n_val * T : 0;
   p.K = t.K;
-  p.kper = t.spl * T;
+  p.kper = t.kper;
   p.M = d_out;
   p.N = d_in;
   p.m_tiles = t.m_tiles;
@@ -3247,8 +3320,12 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
   q.csum = b.csum;
   const int64_t items = t.m_tiles * t.n_tiles * t.sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-  hipLaunchKernelGGL((tgdot_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
-                     dim3(TnC::NT), 0, s, q);
+  if (q.csum != nullptr)
+    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, true>), dim3(static_cast<unsigned>(items)),
+                       dim3(TnC::NT), 0, s, q);
+  else
+    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, false>), dim3(static_cast<unsigned>(items)),
+                       dim3(TnC::NT), 0, s, q);
   rc = check_launch("tgdot_kernel");
   if (rc) return rc;
   if (out_grad != nullptr) {
@@ -3260,8 +3337,8 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
     rc = check_launch("tn_reduce_kernel");
     if (rc) return rc;
   }
-  const int64_t shares = t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN);
-  const int64_t cs_rows = t.vparts * TG_NRG;
+  const int64_t shares = t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2;
+  const int64_t cs_rows = 2 * (T / TnD::KB);  // csum rows per sample: two per stage
   const int64_t fb = ceil_div(d_out, int64_t{TG_FIN_F});
   float* bpart = out_bias_dot != nullptr ? b.bpart : nullptr;
   const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{FINISH_GF}) : 0;

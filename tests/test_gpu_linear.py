@@ -403,6 +403,11 @@ def test_linear_train_grad_declines_and_sampler_falls_back(gpu):
     (20, 4, 1024, 768, 2304, "presum", "last", True),    # qkv
     (20, 4, 1024, 768, 768, "presum", "mid", True),      # proj
     (10, 2, 2048, 2048, 8192, "pairwise", "last", True),  # Pythia-1B fc
+    # splits that start and end inside samples (k-rows per split 1.33 and 2.6 samples), and
+    # a split estimate below one sample (raised to one sample per split)
+    (9, 1, 192, 512, 512, "presum", "last", True),
+    (12, 2, 320, 1024, 1024, "pairwise", "first", True),
+    (5, 1, 1024, 136, 264, "pairwise", "mid", True),
 ])
 @pytest.mark.parametrize("grad_dtype", [torch.bfloat16, torch.float32])
 def test_linear_dot_train_grad(gpu, case, grad_dtype):

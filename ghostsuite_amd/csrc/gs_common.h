@@ -118,6 +118,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave-wide sum through DPP row shifts and row broadcasts (no LDS traffic): lane 15 of each
+// 16-lane row gathers its row, row broadcasts carry the rows up to lane 63, whose value is
+// returned (wave-uniform).
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               ROW_MASK, BANK_MASK, true));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  float s = v + dpp_f32<0x111, 0xf, 0xf>(v);  // row_shr:1
+  s += dpp_f32<0x112, 0xf, 0xf>(v);           // row_shr:2
+  s += dpp_f32<0x113, 0xf, 0xf>(v);           // row_shr:3: lane l holds v[l-3 .. l] of its row
+  s += dpp_f32<0x114, 0xf, 0xe>(s);           // row_shr:4, banks 1-3
+  s += dpp_f32<0x118, 0xf, 0xc>(s);           // row_shr:8, banks 2-3: lane 15 holds the row
+  s += dpp_f32<0x142, 0xa, 0xf>(s);           // row_bcast:15 into rows 1 and 3
+  s += dpp_f32<0x143, 0xc, 0xf>(s);           // row_bcast:31 into rows 2 and 3: lane 63 = total
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 63));
+}
+
 // Block-wide sum; `red` must hold blockDim.x/64 floats.  Result is valid in every thread.
 __device__ __forceinline__ float block_sum(float v, float* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;

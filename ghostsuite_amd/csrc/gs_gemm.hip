@@ -1357,20 +1357,20 @@ __global__ void __launch_bounds__(256) rowdot_bias_finish_kernel(
   }
 }
 
-// After tgdot_kernel: blocks b < n_t take weight dot b from its `shares` wave shares.  Then
-// n_t * fb bias blocks: block (i, k) takes features m = 256 k + thread of sample i, the
-// sample's column sum of G at m (its cs_rows partial rows of csum) times vb[m] (the vp_rows
-// rows of VP, val column sums from val_colsum_kernel), block-summed into bpart[i][k]
-// (tgdot_bias_sum_kernel adds the fb parts).  The rest form the bias train gradient,
-// FINISH_GF features per block, over all n_t * cs_rows partial rows.  Fixed order throughout.
-constexpr int TG_FIN_F = 256;  // features per bias block
+// After tgdot_kernel, three independent block ranges of one launch, fixed order throughout:
+// blocks b < n_t take weight dot b from its `shares` wave shares and, with pbias, bias dot b
+// from its `bshares` shares; then (with bgrad) the bias train gradient, FINISH_GF features
+// per block, over the n_t * cs_rows column-sum rows of csum; then (with grad) the train
+// gradient: grad[i] = gscale * (the sum over the sp splits of part[s][i]), rounded once (or
+// stored as fp32 with grad_f32), 4 elements per thread.
 template <class GE>
 __global__ void __launch_bounds__(256) tgdot_finish_kernel(
-    const float* __restrict__ pdot, int64_t shares, int64_t n_t, const float* __restrict__ csum,
-    int64_t cs_rows, int64_t M, const float* __restrict__ VP, int64_t vp_rows, float* out_dot,
-    float* bpart, int64_t fb, GE* bgrad, float bscale) {
+    const float* __restrict__ pdot, int64_t shares, int64_t n_t, const float* __restrict__ pbias,
+    int64_t bshares, const float* __restrict__ csum, int64_t cs_rows, int64_t M, float* out_dot,
+    float* out_bdot, GE* bgrad, float bscale, int64_t gblocks, const float* __restrict__ part,
+    int64_t count, int sp, void* grad, float gscale, int grad_f32) {
   __shared__ float red[4];
-  const int64_t b = blockIdx.x;
+  int64_t b = blockIdx.x;
   if (b < n_t) {
     float s0 = 0.f, s1 = 0.f;
     int64_t r = threadIdx.x;
@@ -1381,71 +1381,69 @@ __global__ void __launch_bounds__(256) tgdot_finish_kernel(
     if (r < shares) s0 += pdot[r * n_t + b];
     const float s = block_sum(s0 + s1, red);
     if (threadIdx.x == 0) out_dot[b] = s;
+    if (pbias == nullptr) return;
+    const float* pb = pbias + b * bshares;
+    float t0 = 0.f, t1 = 0.f;
+    r = threadIdx.x;
+    for (; r + 256 < bshares; r += 512) {
+      t0 += pb[r];
+      t1 += pb[r + 256];
+    }
+    if (r < bshares) t0 += pb[r];
+    const float t = block_sum(t0 + t1, red);
+    if (threadIdx.x == 0) out_bdot[b] = t;
     return;
   }
-  const int64_t nb = bpart != nullptr ? n_t * fb : 0;
-  if (b < n_t + nb) {
-    const int64_t i = (b - n_t) / fb, k = (b - n_t) - i * fb;
-    const int64_t m = k * TG_FIN_F + threadIdx.x;
-    float s = 0.f;
-    if (m < M) {
-      const float* rows = csum + i * cs_rows * M + m;
-      float c[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      int64_t r = 0;
-      for (; r + 7 < cs_rows; r += 8) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) c[u] += rows[(r + u) * M];
+  b -= n_t;
+  if (b < gblocks) {
+    constexpr int GF = FINISH_GF, RG = 256 / GF;
+    __shared__ float gred[RG][GF];
+    const int c = threadIdx.x % GF, rg = threadIdx.x / GF;
+    const int64_t f = b * GF + c, nrows = n_t * cs_rows;
+    float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
+    if (f < M) {
+      int64_t k = rg;
+      for (; k + 3 * RG < nrows; k += 4 * RG) {
+        t0 += csum[k * M + f];
+        t1 += csum[(k + RG) * M + f];
+        t2 += csum[(k + 2 * RG) * M + f];
+        t3 += csum[(k + 3 * RG) * M + f];
       }
-      for (; r < cs_rows; ++r) c[0] += rows[r * M];
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      r = 0;
-      for (; r + 3 < vp_rows; r += 4) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] += VP[(r + u) * M + m];
-      }
-      for (; r < vp_rows; ++r) v[0] += VP[r * M + m];
-      s = (((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]))) *
-          ((v[0] + v[1]) + (v[2] + v[3]));
+      for (; k < nrows; k += RG) t0 += csum[k * M + f];
     }
-    s = block_sum(s, red);
-    if (threadIdx.x == 0) bpart[i * fb + k] = s;
+    gred[rg][c] = (t0 + t1) + (t2 + t3);
+    __syncthreads();
+    if (rg == 0 && f < M) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) t += gred[g][c];
+      bgrad[f] = from_f32<GE>(bscale * t);
+    }
     return;
   }
-  if (bgrad == nullptr) return;
-  constexpr int GF = FINISH_GF, RG = 256 / GF;
-  __shared__ float gred[RG][GF];
-  const int c = threadIdx.x % GF, rg = threadIdx.x / GF;
-  const int64_t f = (b - n_t - nb) * GF + c, nrows = n_t * cs_rows;
-  float t0 = 0.f, t1 = 0.f, t2 = 0.f, t3 = 0.f;
-  if (f < M) {
-    int64_t k = rg;
-    for (; k + 3 * RG < nrows; k += 4 * RG) {
-      t0 += csum[k * M + f];
-      t1 += csum[(k + RG) * M + f];
-      t2 += csum[(k + 2 * RG) * M + f];
-      t3 += csum[(k + 3 * RG) * M + f];
-    }
-    for (; k < nrows; k += RG) t0 += csum[k * M + f];
+  b -= gblocks;
+  const int64_t i = (b * 256 + threadIdx.x) * 4;
+  if (i >= count) return;
+  float4 v = *reinterpret_cast<const float4*>(part + i);
+  for (int k = 1; k < sp; ++k) {
+    const float4 w = *reinterpret_cast<const float4*>(part + k * count + i);
+    v.x += w.x;
+    v.y += w.y;
+    v.z += w.z;
+    v.w += w.w;
   }
-  gred[rg][c] = (t0 + t1) + (t2 + t3);
-  __syncthreads();
-  if (rg == 0 && f < M) {
-    float t = 0.f;
-#pragma unroll
-    for (int g = 0; g < RG; ++g) t += gred[g][c];
-    bgrad[f] = from_f32<GE>(bscale * t);
+  v.x *= gscale;
+  v.y *= gscale;
+  v.z *= gscale;
+  v.w *= gscale;
+  if (grad_f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(grad) + i) = v;
+    return;
   }
-}
-
-// out_bdot[i] = the sum of bpart[i][0 .. fb) in order; one thread per sample.
-__global__ void __launch_bounds__(256) tgdot_bias_sum_kernel(const float* __restrict__ bpart,
-                                                             int64_t n_t, int64_t fb,
-                                                             float* out_bdot) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n_t) return;
-  float s = 0.f;
-  for (int64_t k = 0; k < fb; ++k) s += bpart[i * fb + k];
-  out_bdot[i] = s;
+  uint2 o;
+  o.x = pack_bf16x2(v.x, v.y);
+  o.y = pack_bf16x2(v.z, v.w);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(grad) + i) = o;
 }
 
 // out[f][c] = row c of the row set, feature f (with `presum`: c = position, summed over all
@@ -1703,9 +1701,12 @@ __device__ __forceinline__ void tn_sched_kstep() {
   if constexpr (G + 1 < M) tn_sched_kstep<RD, M, G + 1>();
 }
 
-template <class C, class D>
+// With KEEP the L fragments of all the stage's k-steps stay in keep[ks][i] afterwards (lane
+// l: L column l % 32 of fragment i, 8 of the k-step's 16 k-rows).
+template <class C, class D, bool KEEP = false>
 __device__ __forceinline__ void tn_compute(const unsigned char* stage,
-                                           f32x16_t (&acc)[C::MI][C::NI]) {
+                                           f32x16_t (&acc)[C::MI][C::NI],
+                                           bf16x8_t (*keep)[C::MI] = nullptr) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
   const int g = lane >> 4, a4 = (lane & 3) * 4, j = (lane >> 2) & 3;
@@ -1726,14 +1727,15 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
                (col & 7) * 2;
   }
   constexpr int NB = 2;
-  bf16x8_t fa[NB][C::MI], fb[NB][C::NI];
+  bf16x8_t fa_own[NB][C::MI], fb[NB][C::NI];
+  bf16x8_t (*fa)[C::MI] = KEEP ? keep : fa_own;  // with KEEP indexed by k-step
   auto load = [&](int buf, int ks) {
 #pragma unroll
     for (int i = 0; i < C::MI; ++i) {
       const unsigned char* p = stage + offa[i] + ks * 16 * D::RL;
       const s16x8_t v = __builtin_shufflevector(lds_tr16(p), lds_tr16(p + 4 * D::RL), 0, 1, 2,
                                                 3, 4, 5, 6, 7);
-      fa[buf][i] = __builtin_bit_cast(bf16x8_t, v);
+      fa[KEEP ? ks : buf][i] = __builtin_bit_cast(bf16x8_t, v);
     }
 #pragma unroll
     for (int jj = 0; jj < C::NI; ++jj) {
@@ -1751,8 +1753,9 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
     for (int i = 0; i < C::MI; ++i)
 #pragma unroll
       for (int jj = 0; jj < C::NI; ++jj)
-        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks % NB][i], fb[ks % NB][jj],
-                                                             acc[i][jj], 0, 0, 0);
+        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[KEEP ? ks : ks % NB][i],
+                                                             fb[ks % NB][jj], acc[i][jj], 0, 0,
+                                                             0);
   }
 #if GS_TN_SCHED
   // Instruction order: the first k-step's transpose reads, then each k-step's MFMAs with the
@@ -1765,33 +1768,23 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
 #endif
 }
 
-// rc[i] = the column sums over a stage's k-rows of this wave's L fragment i, read back from
-// the stage through the same transpose reads as the MFMA operands (lane l: column l % 32 of
-// fragment i, half of each k-step's rows; lanes l and l + 32 together cover the stage), two
-// bf16 values per dot2 against (1, 1).
+// rc[i] = the column sums over a stage's k-rows of this wave's L fragment i, from the
+// fragments tn_compute kept (lane l: column l % 32, half of each k-step's rows; lanes l and
+// l + 32 together cover the stage), two bf16 values per dot2 against (1, 1).
 template <class C, class D>
-__device__ __forceinline__ void tn_lsum(const unsigned char* stage, float (&rc)[C::MI]) {
+__device__ __forceinline__ void tn_lsum(bf16x8_t (*keep)[C::MI], float (&rc)[C::MI]) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);  // (1, 1)
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wm = wid / C::WN;
-  const int g = lane >> 4, a4 = (lane & 3) * 4, j = (lane >> 2) & 3;
-  const int row = 8 * (g >> 1) + j;
-  const int colh = 16 * (g & 1) + a4;
 #pragma unroll
   for (int i = 0; i < C::MI; ++i) {
-    const int col = wm * 32 * C::MI + i * 32 + colh;
-    const int off = row * D::RL + (((col >> 3) ^ D::template swz<D::CL>(row)) * 16) + (col & 7) * 2;
     float t0 = 0.f, t1 = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D::KSTEPS; ++ks) {
-      const unsigned char* p = stage + off + ks * 16 * D::RL;
-      const uint2 lo = __builtin_bit_cast(uint2, lds_tr16(p));
-      const uint2 hi = __builtin_bit_cast(uint2, lds_tr16(p + 4 * D::RL));
-      t0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo.x), one, t0, false);
-      t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo.y), one, t1, false);
-      t0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi.x), one, t0, false);
-      t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi.y), one, t1, false);
+      const uint4 w = __builtin_bit_cast(uint4, keep[ks][i]);
+      t0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), one, t0, false);
+      t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), one, t1, false);
+      t0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), one, t0, false);
+      t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), one, t1, false);
     }
     rc[i] = t0 + t1;
   }
@@ -1825,14 +1818,23 @@ __device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs
 struct NoStageHook {
   __device__ __forceinline__ void operator()(int, const unsigned char*) const {}
 };
+// The MFMAs of one stage.
+template <class C, class D>
+struct TnPlainCompute {
+  __device__ __forceinline__ void operator()(const unsigned char* stage,
+                                             f32x16_t (&acc)[C::MI][C::NI]) const {
+    tn_compute<C, D>(stage, acc);
+  }
+};
 
-// `hook(kt, stage)` runs after stage kt's MFMAs and column sums, with the stage still in
-// LDS (the stage-end hook of tgdot_kernel).
-template <class C, class D, bool RS, class Hook = NoStageHook>
+// `cmp(stage, acc)` does a stage's MFMAs; `hook(kt, stage)` runs after them and the column
+// sums, with the stage still in LDS (the stage-end hook of tgdot_kernel).
+template <class C, class D, bool RS, class Hook = NoStageHook, class Cmp = TnPlainCompute<C, D>>
 __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
                                             int64_t k_begin, int64_t k_end, unsigned char* lds,
                                             f32x16_t (&acc)[C::MI][C::NI], bool colsum,
-                                            float (&cs)[4], int part, Hook hook = Hook{}) {
+                                            float (&cs)[4], int part, Hook hook = Hook{},
+                                            Cmp cmp = Cmp{}) {
   constexpr int NQ = D::QL + D::QR;
   constexpr int AHEAD = D::STAGES - 1;
   static_assert(NQ * (AHEAD - 1) < 64, "vmcnt range");
@@ -1848,14 +1850,14 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
     wait_vmcnt<(AHEAD - 1) * NQ>();
     raw_barrier();
     st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
-    tn_compute<C, D>(slot(kt), acc);
+    cmp(slot(kt), acc);
     if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
     hook(kt, slot(kt));
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
-    tn_compute<C, D>(slot(kt), acc);
+    cmp(slot(kt), acc);
     if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
     hook(kt, slot(kt));
   }
@@ -1957,6 +1959,9 @@ struct TgParams {
   float* pdot;          // [m_tiles * n_tiles][NW][2 slots][n_t] wave shares of the weight dots
   float* csum;          // with CS: [n_t][2 T / stage height][M] column sums of L, two rows
                         // (halves of the stage's k-rows) per stage
+  const float* vb;      // with CS: [M] the val rows' column sums of L (G)
+  float* pbias;         // with CS: [n_t][T / stage height][m_tiles][WM] bias-dot shares:
+                        //   a stage's column sums of one wave's columns dotted with vb
 };
 
 template <class C, class D, bool CS>
@@ -1996,12 +2001,18 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   }
   // Column sums of L (G's train rows: the bias terms), with CS: every workgroup along N
   // takes a share, so no work item runs longer than the others.  After the MFMAs of the
-  // stages kt with kt mod (n_tiles * WN) == nt * WN + wn, wave (nt, wn) reads its L fragments
-  // back from the stage and sums them (the two waves wm = 0, 1 cover the m-tile's columns
+  // stages kt with kt mod (n_tiles * WN) == nt * WN + wn, wave (nt, wn) sums the L fragments
+  // the MFMAs used, still in registers (the two waves wm = 0, 1 cover the m-tile's columns
   // once), then stores the sums in the rows of (stage within its sample) of that sample:
   // every (sample, stage, column) is written once.
   const int cs_every = static_cast<int>(p.n_tiles) * C::WN;
   int cs_left = static_cast<int>(nt) * C::WN + wn;  // stages until this wave's next sum
+  float vbr[C::MI];  // vb at this lane's columns (the bias-dot shares)
+#pragma unroll
+  for (int i = 0; i < C::MI; ++i) {
+    const int64_t col = mt * C::BM + wm * 32 * C::MI + i * 32 + (lane & 31);
+    vbr[i] = CS && col < p.M ? q.vb[col] : 0.f;
+  }
   const int64_t tile = mt * p.n_tiles + nt;
   // Stages left in the current sample (wave-uniform; no division in the stage loop).  A
   // split may start or end inside a sample (kper >= T, so a sample meets at most two
@@ -2026,7 +2037,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
                acc[i][j][4 * g + 2] * __uint_as_float(w.y << 16) +
                acc[i][j][4 * g + 3] * __uint_as_float(w.y & 0xFFFF0000u);
         }
-    d = wave_sum(d);
+    d = wave_sum_dpp(d);
     const int slot = started ? 0 : 1;
     const bool whole = started && ended;
     float* pd = q.pdot + (tile * (C::WM * C::WN) + wid) * 2 * q.n_t + sample;
@@ -2036,19 +2047,25 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
     }
     s_prev = d;
   };
-  auto hook = [&](int, const unsigned char* stage) {
+  bf16x8_t keep[D::KSTEPS][C::MI];  // with CS: the stage's L fragments, kept by tn_compute
+  auto hook = [&](int, const unsigned char*) {
     if constexpr (CS) {
       if (cs_left == 0) {
         cs_left = cs_every;
         float rc[C::MI];
-        tn_lsum<C, D>(stage, rc);
+        tn_lsum<C, D>(keep, rc);
+        const int64_t row = sample * sps + (sps - left);  // stage within its sample
         // lanes l and l + 32 hold halves of the same column: rows 2 s and 2 s + 1
-        float* dst = q.csum + (sample * 2 * sps + 2 * (sps - left) + (lane >> 5)) * p.M;
+        float* dst = q.csum + (2 * row + (lane >> 5)) * p.M;
+        float bd = 0.f;
 #pragma unroll
         for (int i = 0; i < C::MI; ++i) {
           const int64_t col = mt * C::BM + wm * 32 * C::MI + i * 32 + (lane & 31);
           if (col < p.M) dst[col] = rc[i];
+          bd += rc[i] * vbr[i];
         }
+        bd = wave_sum_dpp(bd);
+        if (lane == 0) q.pbias[(row * p.m_tiles + mt) * C::WM + wm] = bd;
       }
       --cs_left;
     }
@@ -2059,7 +2076,14 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
     ++sample;
   };
   float cs[4];
-  mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, false, cs, 0, hook);
+  if constexpr (CS) {
+    auto cmp = [&](const unsigned char* stage, f32x16_t (&a)[C::MI][C::NI]) {
+      tn_compute<C, D, true>(stage, a, keep);
+    };
+    mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, false, cs, 0, hook, cmp);
+  } else {
+    mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, false, cs, 0, hook);
+  }
   if (k_end < (sample + 1) * q.T && k_end > sample * q.T) flush(false);  // ends inside a sample
   GemmParams e{};
   e.m_rows = p.M;
@@ -2395,6 +2419,8 @@ struct TnOut {
   float alpha = 1.f;
   int out_f32 = 0;
   int64_t gap_at = INT64_MAX, gap = 0;
+  float* vrows = nullptr;  // column-sum rows written before the launch (no vsum): the
+  int64_t vrows_n = 0;     //   reduction also folds these vrows_n rows into row 0
 };
 int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
               int64_t N, void* out, float* part, hipStream_t s, float* vsum = nullptr,
@@ -2431,13 +2457,15 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
                      dim3(TnC::NT), 0, s, p);
   int rc = check_launch("tn_gemm_kernel");
-  const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts : 1;
-  if (rc || (!via_part && vs_rows == 1)) return rc;
+  float* vs = vsum != nullptr ? vsum : o.vrows;
+  const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts
+                                          : (o.vrows != nullptr ? o.vrows_n : 1);
+  if (rc || (!via_part && vs_rows <= 1)) return rc;
   const int64_t count = via_part ? M * N : 0;  // a multiple of 8 (N % 8 == 0)
   const int64_t vs_n = vsum_r ? N : M;
   hipLaunchKernelGGL(tn_reduce_kernel,
                      dim3(static_cast<unsigned>(ceil_div(std::max(count, vs_n) / 4, 256))),
-                     dim3(256), 0, s, part, count, sp, out, o.alpha, o.out_f32, vsum, vs_n,
+                     dim3(256), 0, s, part, count, sp, out, o.alpha, o.out_f32, vs, vs_n,
                      vs_rows);
   return check_launch("tn_reduce_kernel");
 }
@@ -3184,7 +3212,7 @@ TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
 }
 struct TgBufs {
   uint16_t *abar, *gbar, *V;
-  float *vpart, *vp, *pdot, *csum, *bpart, *tgpart;
+  float *vpart, *vp, *pdot, *csum, *pbias, *tgpart;
 };
 template <class S>
 TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
@@ -3202,7 +3230,7 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
   b.vp = t.vparts ? c.template take<float>(vp_rows * d_out) : nullptr;
   b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2 * t.n_t);
   b.csum = t.vparts ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * d_out) : nullptr;
-  b.bpart = t.vparts ? c.template take<float>(t.n_t * ceil_div(d_out, int64_t{TG_FIN_F}))
+  b.pbias = t.vparts ? c.template take<float>(t.n_t * (T / TnD::KB) * t.m_tiles * TnC::WM)
                      : nullptr;
   b.tgpart = c.template take<float>(t.sp * d_out * d_in);
   return b;
@@ -3279,19 +3307,22 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
     La = b.abar;
     Lg = b.gbar;
   }
-  int rc = launch_tn(La, d_in, Lg, d_out, t.vk, d_in, d_out, b.V, b.vpart, s,
-                     t.presum ? nullptr : b.vp, true);
-  if (rc) return rc;
-  int64_t vp_rows = 1;  // rows of b.vp the finishing kernel sums
+  // With the presum and a bias, val_colsum_kernel writes the val column sums of G as partial
+  // rows and the V GEMM's reduction folds them into row 0.
+  TnOut vo;
   if (b.vp != nullptr && t.presum) {
-    vp_rows = ceil_div(n_val * T, int64_t{VS_ROWS});
+    vo.vrows = b.vp;
+    vo.vrows_n = ceil_div(n_val * T, int64_t{VS_ROWS});
     const dim3 vgrid(static_cast<unsigned>(ceil_div(d_out, int64_t{VS_COLS})),
-                     static_cast<unsigned>(vp_rows));
+                     static_cast<unsigned>(vo.vrows_n));
     hipLaunchKernelGGL(val_colsum_kernel, vgrid, dim3(256), 0, s, Gp + val_start * T * d_out,
                        n_val * T, d_out, b.vp);
-    rc = check_launch("val_colsum_kernel");
+    int rc = check_launch("val_colsum_kernel");
     if (rc) return rc;
   }
+  int rc = launch_tn(La, d_in, Lg, d_out, t.vk, d_in, d_out, b.V, b.vpart, s,
+                     t.presum ? nullptr : b.vp, true, vo);
+  if (rc) return rc;
   // The train rows: dots at every sample boundary, train-gradient partials per split.
   TgParams q{};
   TnParams& p = q.tn;
@@ -3318,6 +3349,8 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
   q.n_t = t.n_t;
   q.pdot = b.pdot;
   q.csum = b.csum;
+  q.vb = b.vp;
+  q.pbias = b.pbias;
   const int64_t items = t.m_tiles * t.n_tiles * t.sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
   if (q.csum != nullptr)
@@ -3328,34 +3361,26 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
                        dim3(TnC::NT), 0, s, q);
   rc = check_launch("tgdot_kernel");
   if (rc) return rc;
-  if (out_grad != nullptr) {
-    const int64_t count = d_out * d_in;  // a multiple of 8
-    hipLaunchKernelGGL(tn_reduce_kernel, dim3(static_cast<unsigned>(ceil_div(count / 4, 256))),
-                       dim3(256), 0, s, b.tgpart, count, static_cast<int>(t.sp), out_grad,
-                       grad_scale, grad_dtype == GS_DTYPE_F32 ? 1 : 0, nullptr, int64_t{0},
-                       int64_t{1});
-    rc = check_launch("tn_reduce_kernel");
-    if (rc) return rc;
-  }
+  // One launch: the dots, the bias train gradient and the train-gradient reduction.
   const int64_t shares = t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2;
-  const int64_t cs_rows = 2 * (T / TnD::KB);  // csum rows per sample: two per stage
-  const int64_t fb = ceil_div(d_out, int64_t{TG_FIN_F});
-  float* bpart = out_bias_dot != nullptr ? b.bpart : nullptr;
+  const int64_t sps = T / TnD::KB;
+  const int64_t bshares = sps * t.m_tiles * TnC::WM;
+  const float* pbias = out_bias_dot != nullptr ? b.pbias : nullptr;
   const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{FINISH_GF}) : 0;
-  const dim3 grid(static_cast<unsigned>(t.n_t + (bpart != nullptr ? t.n_t * fb : 0) + gblocks));
+  const int64_t count = out_grad != nullptr ? d_out * d_in : 0;  // a multiple of 8
+  const dim3 grid(static_cast<unsigned>(t.n_t + gblocks + ceil_div(count / 4, int64_t{256})));
+  const int gf32 = grad_dtype == GS_DTYPE_F32 ? 1 : 0;
   if (bias_grad_dtype == GS_DTYPE_F32)
     hipLaunchKernelGGL(tgdot_finish_kernel<float>, grid, dim3(256), 0, s, b.pdot, shares, t.n_t,
-                       b.csum, cs_rows, d_out, b.vp, vp_rows, out_dot, bpart, fb,
-                       static_cast<float*>(out_bias_grad), bias_grad_scale);
+                       pbias, bshares, b.csum, 2 * sps, d_out, out_dot, out_bias_dot,
+                       static_cast<float*>(out_bias_grad), bias_grad_scale, gblocks, b.tgpart,
+                       count, static_cast<int>(t.sp), out_grad, grad_scale, gf32);
   else
     hipLaunchKernelGGL(tgdot_finish_kernel<uint16_t>, grid, dim3(256), 0, s, b.pdot, shares,
-                       t.n_t, b.csum, cs_rows, d_out, b.vp, vp_rows, out_dot, bpart, fb,
-                       static_cast<uint16_t*>(out_bias_grad), bias_grad_scale);
-  rc = check_launch("tgdot_finish_kernel");
-  if (rc || bpart == nullptr) return rc;
-  hipLaunchKernelGGL(tgdot_bias_sum_kernel, dim3(static_cast<unsigned>(ceil_div(t.n_t, int64_t{256}))),
-                     dim3(256), 0, s, bpart, t.n_t, fb, out_bias_dot);
-  return check_launch("tgdot_bias_sum_kernel");
+                       t.n_t, pbias, bshares, b.csum, 2 * sps, d_out, out_dot, out_bias_dot,
+                       static_cast<uint16_t*>(out_bias_grad), bias_grad_scale, gblocks,
+                       b.tgpart, count, static_cast<int>(t.sp), out_grad, grad_scale, gf32);
+  return check_launch("tgdot_finish_kernel");
 }
 
 extern "C" size_t gs_linear_rowdot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,

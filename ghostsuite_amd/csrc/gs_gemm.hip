@@ -1617,9 +1617,11 @@ struct TnParams {
   int part_out;     //   [split][M][N], scaled and rounded by tn_reduce_kernel
   float alpha;      // part_out == 0: the scale applied before the one rounding
   int out_f32;
-  float* vsum;      // null, or [split][vparts][M]: column sums of L over the split's k-rows
+  float* vsum;      // null, or [split][vparts][M]: column sums of L over the split's k-rows,
+                    //   rows the reduction folds into row 0
   int vsum_r;       // 1: vsum holds the column sums of R instead ([split][vparts][N])
-  int vparts;       // the tiles along the other side (N, or M with vsum_r) split the k-rows
+  int vparts;       // the first vparts tiles along the other side (N, or M with vsum_r)
+                    //   share the column sums
   int64_t gap_at, gap;  // logical k-rows >= gap_at lie gap rows further on (a skipped block)
 };
 
@@ -1701,12 +1703,13 @@ __device__ __forceinline__ void tn_sched_kstep() {
   if constexpr (G + 1 < M) tn_sched_kstep<RD, M, G + 1>();
 }
 
-// With KEEP the L fragments of all the stage's k-steps stay in keep[ks][i] afterwards (lane
-// l: L column l % 32 of fragment i, 8 of the k-step's 16 k-rows).
-template <class C, class D, bool KEEP = false>
+// With KEEP = 1 (2) the L (R) fragments of all the stage's k-steps stay in keep[ks][i]
+// afterwards (lane l: column l % 32 of fragment i, 8 of the k-step's 16 k-rows; keep has
+// MI (NI) fragments per k-step).
+template <class C, class D, int KEEP = 0>
 __device__ __forceinline__ void tn_compute(const unsigned char* stage,
                                            f32x16_t (&acc)[C::MI][C::NI],
-                                           bf16x8_t (*keep)[C::MI] = nullptr) {
+                                           bf16x8_t (*keep)[KEEP == 2 ? C::NI : C::MI] = nullptr) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / C::WN, wn = wid % C::WN;
   const int g = lane >> 4, a4 = (lane & 3) * 4, j = (lane >> 2) & 3;
@@ -1727,22 +1730,27 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
                (col & 7) * 2;
   }
   constexpr int NB = 2;
-  bf16x8_t fa_own[NB][C::MI], fb[NB][C::NI];
-  bf16x8_t (*fa)[C::MI] = KEEP ? keep : fa_own;  // with KEEP indexed by k-step
+  constexpr bool KL = KEEP == 1, KR = KEEP == 2;
+  bf16x8_t fa_own[NB][C::MI], fb_own[NB][C::NI];
+  // The kept side is indexed by k-step, the other by double buffer.
+  bf16x8_t (*fa)[C::MI] = fa_own;
+  bf16x8_t (*fb)[C::NI] = fb_own;
+  if constexpr (KL) fa = reinterpret_cast<bf16x8_t (*)[C::MI]>(keep);
+  if constexpr (KR) fb = reinterpret_cast<bf16x8_t (*)[C::NI]>(keep);
   auto load = [&](int buf, int ks) {
 #pragma unroll
     for (int i = 0; i < C::MI; ++i) {
       const unsigned char* p = stage + offa[i] + ks * 16 * D::RL;
       const s16x8_t v = __builtin_shufflevector(lds_tr16(p), lds_tr16(p + 4 * D::RL), 0, 1, 2,
                                                 3, 4, 5, 6, 7);
-      fa[KEEP ? ks : buf][i] = __builtin_bit_cast(bf16x8_t, v);
+      fa[KL ? ks : buf][i] = __builtin_bit_cast(bf16x8_t, v);
     }
 #pragma unroll
     for (int jj = 0; jj < C::NI; ++jj) {
       const unsigned char* p = stage + offb[jj] + ks * 16 * D::RR;
       const s16x8_t v = __builtin_shufflevector(lds_tr16(p), lds_tr16(p + 4 * D::RR), 0, 1, 2,
                                                 3, 4, 5, 6, 7);
-      fb[buf][jj] = __builtin_bit_cast(bf16x8_t, v);
+      fb[KR ? ks : buf][jj] = __builtin_bit_cast(bf16x8_t, v);
     }
   };
   load(0, 0);
@@ -1753,9 +1761,9 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
     for (int i = 0; i < C::MI; ++i)
 #pragma unroll
       for (int jj = 0; jj < C::NI; ++jj)
-        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[KEEP ? ks : ks % NB][i],
-                                                             fb[ks % NB][jj], acc[i][jj], 0, 0,
-                                                             0);
+        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[KL ? ks : ks % NB][i],
+                                                             fb[KR ? ks : ks % NB][jj],
+                                                             acc[i][jj], 0, 0, 0);
   }
 #if GS_TN_SCHED
   // Instruction order: the first k-step's transpose reads, then each k-step's MFMAs with the
@@ -1768,16 +1776,16 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
 #endif
 }
 
-// rc[i] = the column sums over a stage's k-rows of this wave's L fragment i, from the
-// fragments tn_compute kept (lane l: column l % 32, half of each k-step's rows; lanes l and
-// l + 32 together cover the stage), two bf16 values per dot2 against (1, 1).
-template <class C, class D>
-__device__ __forceinline__ void tn_lsum(bf16x8_t (*keep)[C::MI], float (&rc)[C::MI]) {
+// rc[i] (+)= the column sums over a stage's k-rows of this wave's fragment i, from the F
+// fragments per k-step tn_compute kept (lane l: column l % 32, half of each k-step's rows;
+// lanes l and l + 32 together cover the stage), two bf16 values per dot2 against (1, 1).
+template <class D, int F, bool ADD = false>
+__device__ __forceinline__ void tn_fsum(bf16x8_t (*keep)[F], float (&rc)[F]) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);  // (1, 1)
 #pragma unroll
-  for (int i = 0; i < C::MI; ++i) {
-    float t0 = 0.f, t1 = 0.f;
+  for (int i = 0; i < F; ++i) {
+    float t0 = ADD ? rc[i] : 0.f, t1 = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D::KSTEPS; ++ks) {
       const uint4 w = __builtin_bit_cast(uint4, keep[ks][i]);
@@ -1787,31 +1795,6 @@ __device__ __forceinline__ void tn_lsum(bf16x8_t (*keep)[C::MI], float (&rc)[C::
       t1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), one, t1, false);
     }
     rc[i] = t0 + t1;
-  }
-}
-
-// acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same
-// schedule as mainloop_dma: constant vmcnt wait, barrier, loads of stage k + NS - 1, MFMAs).
-// Column sums of a stage's L part (RS: its R part): thread t owns the 4 columns of group
-// t % (W / 4) and every (NT / (W / 4))-th k-row from t / (W / 4), W the part's tile width;
-// zero-filled rows add nothing.
-// The vparts workgroups along the other side share the work: part p takes the k-rows
-// rg + NRG j with j = p mod vparts.
-template <class C, class D, bool RS>
-__device__ __forceinline__ void tn_colsum(const unsigned char* stage, float (&cs)[4], int part,
-                                          int vparts) {
-  constexpr int W = RS ? C::BN : C::BM, CG = W / 4, NRG = C::NT / CG;
-  constexpr int RB = RS ? D::RR : D::RL, CH = RS ? D::CR : D::CL, OFF = RS ? D::L_BYTES : 0;
-  static_assert(C::NT % CG == 0 && D::KB % NRG == 0, "column groups");
-  const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
-  const int c = cg >> 1, hb = (cg & 1) * 8;
-  for (int j = part; j < D::KB / NRG; j += vparts) {
-    const int r = rg + NRG * j;
-    union { uint2 v; uint16_t e[4]; } z;
-    z.v = *reinterpret_cast<const uint2*>(stage + OFF + r * RB +
-                                          ((c ^ D::template swz<CH>(r)) * 16) + hb);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) cs[e] += bf16_to_f32(z.e[e]);
   }
 }
 
@@ -1827,13 +1810,14 @@ struct TnPlainCompute {
   }
 };
 
-// `cmp(stage, acc)` does a stage's MFMAs; `hook(kt, stage)` runs after them and the column
-// sums, with the stage still in LDS (the stage-end hook of tgdot_kernel).
-template <class C, class D, bool RS, class Hook = NoStageHook, class Cmp = TnPlainCompute<C, D>>
+// acc += over k-rows [k_begin, k_end) of L^T R, through an NS-stage LDS-DMA ring (the same
+// schedule as mainloop_dma: constant vmcnt wait, barrier, loads of stage k + NS - 1, MFMAs).
+// `cmp(stage, acc)` does a stage's MFMAs; `hook(kt, stage)` runs after them, with the stage
+// still in LDS.
+template <class C, class D, class Hook = NoStageHook, class Cmp = TnPlainCompute<C, D>>
 __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64_t nt,
                                             int64_t k_begin, int64_t k_end, unsigned char* lds,
-                                            f32x16_t (&acc)[C::MI][C::NI], bool colsum,
-                                            float (&cs)[4], int part, Hook hook = Hook{},
+                                            f32x16_t (&acc)[C::MI][C::NI], Hook hook = Hook{},
                                             Cmp cmp = Cmp{}) {
   constexpr int NQ = D::QL + D::QR;
   constexpr int AHEAD = D::STAGES - 1;
@@ -1851,14 +1835,12 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
     raw_barrier();
     st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
     cmp(slot(kt), acc);
-    if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
     hook(kt, slot(kt));
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);
     raw_barrier();
     cmp(slot(kt), acc);
-    if (colsum) tn_colsum<C, D, RS>(slot(kt), cs, part, p.vparts);
     hook(kt, slot(kt));
   }
   wait_vmcnt<0>();
@@ -1888,7 +1870,7 @@ __device__ __forceinline__ void tn_item(const TnParams& p, int64_t& mt, int64_t&
 
 // One output tile per work item: bf16 out, or fp32 partials (several splits or an output
 // option) reduced by tn_reduce_kernel.
-template <class C, class D>
+template <class C, class D, int CSM>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
   int64_t mt, nt, split;
@@ -1897,33 +1879,54 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tn_gemm_kernel(TnParams p
   const int64_t k_end = k_begin + p.kper < p.K ? k_begin + p.kper : p.K;
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
-  // The workgroups also take the column sums of their L tile (the val rows of G: the val
-  // bias gradient), or with vsum_r of their R tile (G on the right when the GEMM forms V^T):
-  // the workgroups along the other side (part = nt, or mt) split each stage's k-rows, and
-  // the row groups combine in a fixed order.
-  static_assert(C::BM == C::BN, "one column-sum layout for both sides");
-  const int part = static_cast<int>(p.vsum_r ? mt : nt);
-  const bool colsum = p.vsum != nullptr && part < p.vparts;
-  float cs[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.vsum_r)
-    mainloop_tn<C, D, true>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs, part);
-  else
-    mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, colsum, cs, part);
-  if (colsum) {
-    constexpr int CG = C::BM / 4, NRG = C::NT / CG;
-    static_assert(NRG * C::BM * 4 <= D::STAGES * D::STAGE_BYTES, "column-sum scratch");
-    float* red = reinterpret_cast<float*>(lds);  // the stages are free after the mainloop
-    const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
+  if constexpr (CSM == 0) {
+    mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc);
+  } else {
+    // The workgroups also take the column sums of their L (CSM 1) or R (CSM 2) tile: the val
+    // rows of G, for the val bias terms.  The first vparts tiles along the other side (part)
+    // and the waves sharing the columns (w: wn for L, wm for R) take turns by stage: wave
+    // (part, w) adds the fragments the stage's MFMAs used, still in registers, at the stages
+    // kt with kt mod (vparts * W) == part * W + w.  At the end the workgroup combines its
+    // waves' sums in LDS in a fixed order into one row: vsum [split][part][ext], folded by
+    // the reduction.
+    constexpr int F = CSM == 1 ? C::MI : C::NI, W = CSM == 1 ? C::WN : C::WM;
+    constexpr int BW = CSM == 1 ? C::BM : C::BN;  // columns of the tile
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wid / C::WN, wn = wid % C::WN, w = CSM == 1 ? wn : wm;
+    const int part = static_cast<int>(CSM == 1 ? nt : mt), every = p.vparts * W;
+    const bool colsum = part < p.vparts;
+    int left = colsum ? part * W + w : -1;  // stages until this wave's next turn
+    bf16x8_t keep[D::KSTEPS][F];
+    float rc[F];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[rg * C::BM + 4 * cg + e] = cs[e];
-    __syncthreads();
-    const int64_t ext = p.vsum_r ? p.N : p.M, t0 = (p.vsum_r ? nt : mt) * C::BM;
-    for (int m = threadIdx.x; m < C::BM; m += C::NT) {
-      float t = 0.f;
+    for (int i = 0; i < F; ++i) rc[i] = 0.f;
+    auto cmp = [&](const unsigned char* stage, f32x16_t (&a)[C::MI][C::NI]) {
+      tn_compute<C, D, CSM>(stage, a, keep);
+    };
+    auto hook = [&](int, const unsigned char*) {
+      if (left == 0) {
+        left = every;
+        tn_fsum<D, F, true>(keep, rc);
+      }
+      --left;
+    };
+    mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc, hook, cmp);
+    if (colsum) {  // workgroup-uniform; the stages are free after the mainloop
+      static_assert(W * 2 * BW * 4 <= D::STAGES * D::STAGE_BYTES, "column-sum scratch");
+      float* red = reinterpret_cast<float*>(lds);  // [w][lane half][BW]
+      const int c0 = (CSM == 1 ? wm * C::MI : wn * C::NI) * 32 + (lane & 31);
 #pragma unroll
-      for (int g = 0; g < NRG; ++g) t += red[g * C::BM + m];
-      const int64_t col = t0 + m;
-      if (col < ext) p.vsum[(split * p.vparts + part) * ext + col] = t;
+      for (int i = 0; i < F; ++i) red[(w * 2 + (lane >> 5)) * BW + c0 + i * 32] = rc[i];
+      __syncthreads();
+      const int64_t ext = CSM == 1 ? p.M : p.N;
+      for (int c = threadIdx.x; c < BW; c += C::NT) {
+        float t = 0.f;
+#pragma unroll
+        for (int r = 0; r < 2 * W; ++r) t += red[r * BW + c];
+        const int64_t col = (CSM == 1 ? mt : nt) * BW + c;
+        if (col < ext) p.vsum[(split * p.vparts + part) * ext + col] = t;
+      }
     }
   }
   GemmParams e{};
@@ -2053,7 +2056,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
       if (cs_left == 0) {
         cs_left = cs_every;
         float rc[C::MI];
-        tn_lsum<C, D>(keep, rc);
+        tn_fsum<D, C::MI>(keep, rc);
         const int64_t row = sample * sps + (sps - left);  // stage within its sample
         // lanes l and l + 32 hold halves of the same column: rows 2 s and 2 s + 1
         float* dst = q.csum + (2 * row + (lane >> 5)) * p.M;
@@ -2075,14 +2078,13 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
     started = true;
     ++sample;
   };
-  float cs[4];
   if constexpr (CS) {
     auto cmp = [&](const unsigned char* stage, f32x16_t (&a)[C::MI][C::NI]) {
-      tn_compute<C, D, true>(stage, a, keep);
+      tn_compute<C, D, 1>(stage, a, keep);
     };
-    mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, false, cs, 0, hook, cmp);
+    mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc, hook, cmp);
   } else {
-    mainloop_tn<C, D, false>(p, mt, nt, k_begin, k_end, lds, acc, false, cs, 0, hook);
+    mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc, hook);
   }
   if (k_end < (sample + 1) * q.T && k_end > sample * q.T) flush(false);  // ends inside a sample
   GemmParams e{};
@@ -2408,10 +2410,14 @@ bool val_tn(int dtype, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, in
   return dtype == GS_DTYPE_BF16 && tn_ok(nullptr, d_out, nullptr, d_in, K, d_out, d_in);
 }
 // out [M][N] bf16 = L^T R over K k-rows (L: [K][M] stride ldl, R: [K][N] stride ldr).
-// vsum (optional): [splits][parts][M] column sums of L (parts: the first N tiles, at most
-// TN_VPARTS), or with vsum_r [splits][parts][N] those of R (the first M tiles); their total
-// ends in row 0.
-constexpr int64_t TN_VPARTS = 4;
+// vsum (optional): tn_vsum_rows rows of column sums of L ([M] each), or with vsum_r of R
+// ([N] each); their total ends in row 0.
+int64_t tn_vparts(int64_t M, int64_t N, bool vsum_r) {
+  return std::min<int64_t>(4, vsum_r ? ceil_div(M, TnC::BM) : ceil_div(N, TnC::BN));
+}
+int64_t tn_vsum_rows(int64_t K, int64_t M, int64_t N, bool vsum_r) {
+  return static_cast<int64_t>(tn_splits(K, M, N)) * tn_vparts(M, N, vsum_r);
+}
 // Output options of launch_tn beyond the plain bf16 product: a scale applied before the one
 // rounding, fp32 output, and a block of `gap` k-rows skipped at logical row gap_at (the
 // operands then span K + gap rows).
@@ -2444,8 +2450,7 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   const int sp = tn_splits(K, M, N);
   p.vsum = vsum;
   p.vsum_r = vsum_r ? 1 : 0;
-  p.vparts = static_cast<int>(std::min<int64_t>(
-      TN_VPARTS, vsum_r ? ceil_div(M, TnC::BM) : ceil_div(N, TnC::BN)));
+  p.vparts = static_cast<int>(tn_vparts(M, N, vsum_r));
   const bool via_part = sp > 1;
   p.part_out = via_part ? 1 : 0;
   p.alpha = o.alpha;
@@ -2454,11 +2459,16 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   if (via_part && part == nullptr) return fail(GS_ERR_INVALID, "internal: TN partials");
   const int64_t items = p.m_tiles * p.n_tiles * sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-  hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD>), dim3(static_cast<unsigned>(items)),
-                     dim3(TnC::NT), 0, s, p);
+  const dim3 grid(static_cast<unsigned>(items));
+  if (vsum == nullptr)
+    hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD, 0>), grid, dim3(TnC::NT), 0, s, p);
+  else if (!vsum_r)
+    hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD, 1>), grid, dim3(TnC::NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((tn_gemm_kernel<TnC, TnD, 2>), grid, dim3(TnC::NT), 0, s, p);
   int rc = check_launch("tn_gemm_kernel");
   float* vs = vsum != nullptr ? vsum : o.vrows;
-  const int64_t vs_rows = vsum != nullptr ? static_cast<int64_t>(sp) * p.vparts
+  const int64_t vs_rows = vsum != nullptr ? tn_vsum_rows(K, M, N, vsum_r)
                                           : (o.vrows != nullptr ? o.vrows_n : 1);
   if (rc || (!via_part && vs_rows <= 1)) return rc;
   const int64_t count = via_part ? M * N : 0;  // a multiple of 8 (N % 8 == 0)
@@ -3182,7 +3192,7 @@ struct TgPlan {
   int64_t vk;                // k-rows of the V GEMM (val rows, or T after the presum)
   int64_t n_val, n_t, K;     // val and train samples, train k-rows
   int64_t kper, sp;          // k-rows per split (at least one sample), splits
-  int64_t m_tiles, n_tiles, vparts;
+  int64_t m_tiles, n_tiles, bias;  // bias: the bias terms are wanted
 };
 bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
            int semantics) {
@@ -3207,7 +3217,7 @@ TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
   t.kper = tn_kper(t.K, static_cast<int>(t.sp));
   if (t.kper < T) t.kper = T;
   t.sp = ceil_div(t.K, t.kper);
-  t.vparts = bias ? std::min<int64_t>(TN_VPARTS, t.n_tiles) : 0;
+  t.bias = bias ? 1 : 0;
   return t;
 }
 struct TgBufs {
@@ -3225,12 +3235,11 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
   // are the val rows as they lie); for the presum, whose V operands are rounded to bf16,
   // val_colsum_kernel over the val rows.
   const int64_t vp_rows = t.presum ? ceil_div(t.n_val * T, int64_t{VS_ROWS})
-                                   : tn_splits(t.vk, d_in, d_out) *
-                                         std::min<int64_t>(TN_VPARTS, t.n_tiles);
-  b.vp = t.vparts ? c.template take<float>(vp_rows * d_out) : nullptr;
+                                   : tn_vsum_rows(t.vk, d_in, d_out, true);
+  b.vp = t.bias ? c.template take<float>(vp_rows * d_out) : nullptr;
   b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2 * t.n_t);
-  b.csum = t.vparts ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * d_out) : nullptr;
-  b.pbias = t.vparts ? c.template take<float>(t.n_t * (T / TnD::KB) * t.m_tiles * TnC::WM)
+  b.csum = t.bias ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * d_out) : nullptr;
+  b.pbias = t.bias ? c.template take<float>(t.n_t * (T / TnD::KB) * t.m_tiles * TnC::WM)
                      : nullptr;
   b.tgpart = c.template take<float>(t.sp * d_out * d_in);
   return b;
@@ -3343,7 +3352,6 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
   p.out = b.tgpart;
   p.part_out = 1;
   p.alpha = 1.f;
-  p.vparts = static_cast<int>(t.vparts);
   q.Vt = b.V;
   q.T = T;
   q.n_t = t.n_t;
@@ -3640,8 +3648,9 @@ void carve_bias_dot(S& c, const RowdotBiasPlan& b, int64_t n_val, int64_t T, int
   carve_rowdot_bias(c, b, d_out, P, PB, BP);
   const int64_t K = (presum ? 1 : n_val) * T;
   *V = c.template take<uint16_t>(d_out * d_in);
-  *VS = c.template take<float>(static_cast<int64_t>(tn_splits(K, d_out, d_in)) *
-                               std::min<int64_t>(TN_VPARTS, ceil_div(d_in, TnC::BN)) * d_out);
+  *VS = c.template take<float>((b.swap ? tn_vsum_rows(K, d_in, d_out, true)
+                                       : tn_vsum_rows(K, d_out, d_in, false)) *
+                               d_out);
   *part = c.template take<float>(tn_part_elems(K, d_out, d_in));
   *abar = presum ? c.template take<uint16_t>(T * d_in) : nullptr;
   *gbar = presum ? c.template take<uint16_t>(T * d_out) : nullptr;

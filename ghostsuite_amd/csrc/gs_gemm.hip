@@ -1530,50 +1530,87 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 }
 
 // out_z[t][f] = sum over the nseg val rows of in_z[row(s, t)][f] for z = 0, 1 (blockIdx.z):
-// 16 bytes per thread, fp32 sums rounded once.  Rows 16-byte aligned, d % 8 == 0.
+// fp32 sums rounded once.  A block takes PS_F * 8 features (16 bytes per thread) of PS_T
+// positions, PS_P position lanes per feature chunk; with colsum the z = 1 blocks also write
+// the fp32 sums over their positions, one row per block row: colsum [ceil(T / PS_T)][d[1]]
+// (the val rows' column sums, combined in a fixed order).  Rows 16-byte aligned, d % 8 == 0.
+constexpr int PS_F = 32, PS_P = 8, PS_T = 32;
 struct PresumPair {
   const uint16_t* in[2];
   uint16_t* out[2];
   int64_t d[2];
+  float* colsum;
 };
 __global__ void __launch_bounds__(256) presum_rows_vec_kernel(PresumPair pp, RowMap map) {
+  static_assert(PS_F * PS_P == 256, "block shape");
+  __shared__ float red[PS_P][PS_F * 8];
   const int z = blockIdx.z;
   const int64_t d = pp.d[z];
-  const int64_t f = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
-  const int64_t t = blockIdx.y;
-  if (f >= d) return;
-  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  int64_t sg = 0;
-  for (; sg + 4 <= map.nseg; sg += 4) {
-    uint4 x[4];
+  const int fc = threadIdx.x % PS_F, pl = threadIdx.x / PS_F;
+  const int64_t f = (static_cast<int64_t>(blockIdx.x) * PS_F + fc) * 8;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * PS_T;
+  const int64_t t1 = t0 + PS_T < map.seglen ? t0 + PS_T : map.seglen;
+  const bool cs_on = z == 1 && pp.colsum != nullptr;  // block-uniform
+  float cs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (f < d) {
+    for (int64_t t = t0 + pl; t < t1; t += PS_P) {
+      float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      int64_t sg = 0;
+      for (; sg + 4 <= map.nseg; sg += 4) {
+        uint4 x[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      x[u] = *reinterpret_cast<const uint4*>(pp.in[z] + map.phys_row(sg + u, t) * d + f);
+        for (int u = 0; u < 4; ++u)
+          x[u] = *reinterpret_cast<const uint4*>(pp.in[z] + map.phys_row(sg + u, t) * d + f);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        a[2 * e] += __uint_as_float(w[e] << 16);
-        a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+          for (int e = 0; e < 4; ++e) {
+            a[2 * e] += __uint_as_float(w[e] << 16);
+            a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+          }
+        }
       }
-    }
-  }
-  for (; sg < map.nseg; ++sg) {
-    const uint4 x = *reinterpret_cast<const uint4*>(pp.in[z] + map.phys_row(sg, t) * d + f);
-    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+      for (; sg < map.nseg; ++sg) {
+        const uint4 x = *reinterpret_cast<const uint4*>(pp.in[z] + map.phys_row(sg, t) * d + f);
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      a[2 * e] += __uint_as_float(w[e] << 16);
-      a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+        for (int e = 0; e < 4; ++e) {
+          a[2 * e] += __uint_as_float(w[e] << 16);
+          a[2 * e + 1] += __uint_as_float(w[e] & 0xffff0000u);
+        }
+      }
+      uint4 o;
+      o.x = pack_bf16x2(a[0], a[1]);
+      o.y = pack_bf16x2(a[2], a[3]);
+      o.z = pack_bf16x2(a[4], a[5]);
+      o.w = pack_bf16x2(a[6], a[7]);
+      *reinterpret_cast<uint4*>(pp.out[z] + t * d + f) = o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cs[e] += a[e];
     }
   }
-  uint4 o;
-  o.x = pack_bf16x2(a[0], a[1]);
-  o.y = pack_bf16x2(a[2], a[3]);
-  o.z = pack_bf16x2(a[4], a[5]);
-  o.w = pack_bf16x2(a[6], a[7]);
-  *reinterpret_cast<uint4*>(pp.out[z] + t * d + f) = o;
+  if (!cs_on) return;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[pl][fc * 8 + e] = cs[e];
+  __syncthreads();
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * PS_F * 8 + threadIdx.x;
+  if (col < d) {
+    float t = 0.f;
+#pragma unroll
+    for (int r = 0; r < PS_P; ++r) t += red[r][threadIdx.x];
+    pp.colsum[blockIdx.y * d + col] = t;
+  }
+}
+// The presum of the val rows of A (in[0], d[0] features) and G (in[1], d[1]); with colsum
+// also the val column sums of G as presum_rows(T) partial rows.
+int64_t presum_rows(int64_t T) { return (T + PS_T - 1) / PS_T; }
+int launch_presum(const PresumPair& pp, const RowMap& map, hipStream_t s) {
+  const int64_t dmax = std::max(pp.d[0], pp.d[1]);
+  const dim3 grid(static_cast<unsigned>((dmax + PS_F * 8 - 1) / (PS_F * 8)),
+                  static_cast<unsigned>(presum_rows(map.seglen)), 2);
+  hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp, map);
+  return check_launch("presum_rows_vec_kernel");
 }
 
 // ------------------------------------------------------------------ K-major (TN) GEMM
@@ -2786,10 +2823,7 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
         pp.out[1] = gbar;
         pp.d[0] = d_in;
         pp.d[1] = d_out;
-        const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
-                        static_cast<unsigned>(T), 2);
-        hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp, va);
-        int rc = check_launch("presum_rows_vec_kernel");
+        int rc = launch_presum(pp, va, s);
         if (rc) return rc;
         La = abar;
         Lg = gbar;
@@ -3055,10 +3089,7 @@ extern "C" int gs_linear_val_gradient(const void* A, const void* G, int dtype, i
       pp.out[1] = gbar;
       pp.d[0] = d_in;
       pp.d[1] = d_out;
-      const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
-                      static_cast<unsigned>(T), 2);
-      hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp, va);
-      int rc = check_launch("presum_rows_vec_kernel");
+      int rc = launch_presum(pp, va, s);
       if (rc) return rc;
       La = abar;
       Lg = gbar;
@@ -3232,10 +3263,9 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
   b.V = c.template take<uint16_t>(d_out * d_in);  // V^T, [d_in][d_out]
   b.vpart = c.template take<float>(tn_part_elems(t.vk, d_out, d_in));
   // Val column sums of G: the V GEMM's own partials for the pairwise semantics (its operands
-  // are the val rows as they lie); for the presum, whose V operands are rounded to bf16,
-  // val_colsum_kernel over the val rows.
-  const int64_t vp_rows = t.presum ? ceil_div(t.n_val * T, int64_t{VS_ROWS})
-                                   : tn_vsum_rows(t.vk, d_in, d_out, true);
+  // are the val rows as they lie); for the presum, whose V operands are rounded to bf16, the
+  // presum kernel's fp32 sums.
+  const int64_t vp_rows = t.presum ? presum_rows(T) : tn_vsum_rows(t.vk, d_in, d_out, true);
   b.vp = t.bias ? c.template take<float>(vp_rows * d_out) : nullptr;
   b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2 * t.n_t);
   b.csum = t.bias ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * d_out) : nullptr;
@@ -3298,7 +3328,9 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
   const E* Lg = Gp + val_start * T * d_out;
   // V^T = A_val^T G_val (or the product of the val rows presummed per position); with a bias,
   // the val rows' column sums of G in fp32 from the rows as they lie: from the V GEMM's
-  // workgroups (pairwise; their total ends in row 0) or val_colsum_kernel (presum).
+  // workgroups (pairwise) or the presum kernel (presum), as partial rows the V GEMM's
+  // reduction folds into row 0.
+  TnOut vo;
   if (t.presum) {
     PresumPair pp{};
     pp.in[0] = Ap;
@@ -3307,27 +3339,15 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
     pp.out[1] = b.gbar;
     pp.d[0] = d_in;
     pp.d[1] = d_out;
-    const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
-                    static_cast<unsigned>(T), 2);
-    hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp,
-                       val_rows(n_val, val_start, T));
-    int rc = check_launch("presum_rows_vec_kernel");
+    pp.colsum = b.vp;
+    int rc = launch_presum(pp, val_rows(n_val, val_start, T), s);
     if (rc) return rc;
     La = b.abar;
     Lg = b.gbar;
-  }
-  // With the presum and a bias, val_colsum_kernel writes the val column sums of G as partial
-  // rows and the V GEMM's reduction folds them into row 0.
-  TnOut vo;
-  if (b.vp != nullptr && t.presum) {
-    vo.vrows = b.vp;
-    vo.vrows_n = ceil_div(n_val * T, int64_t{VS_ROWS});
-    const dim3 vgrid(static_cast<unsigned>(ceil_div(d_out, int64_t{VS_COLS})),
-                     static_cast<unsigned>(vo.vrows_n));
-    hipLaunchKernelGGL(val_colsum_kernel, vgrid, dim3(256), 0, s, Gp + val_start * T * d_out,
-                       n_val * T, d_out, b.vp);
-    int rc = check_launch("val_colsum_kernel");
-    if (rc) return rc;
+    if (b.vp != nullptr) {
+      vo.vrows = b.vp;
+      vo.vrows_n = presum_rows(T);
+    }
   }
   int rc = launch_tn(La, d_in, Lg, d_out, t.vk, d_in, d_out, b.V, b.vpart, s,
                      t.presum ? nullptr : b.vp, true, vo);
@@ -3711,11 +3731,7 @@ extern "C" int gs_linear_bias_dot(const void* A, const void* G, int dtype, int64
     pp.out[1] = static_cast<E*>(gbar);
     pp.d[0] = d_in;
     pp.d[1] = d_out;
-    const dim3 grid(static_cast<unsigned>(ceil_div(std::max(d_in, d_out) / 8, int64_t{256})),
-                    static_cast<unsigned>(T), 2);
-    hipLaunchKernelGGL(presum_rows_vec_kernel, grid, dim3(256), 0, s, pp,
-                       val_rows(n_val, val_start, T));
-    rc = check_launch("presum_rows_vec_kernel");
+    rc = launch_presum(pp, val_rows(n_val, val_start, T), s);
     if (rc) return rc;
     La = static_cast<const E*>(abar);
     Lg = static_cast<const E*>(gbar);

@@ -407,25 +407,23 @@ struct DmaStreamer {
   }
   // The L (or R) rows of the stage starting at k0 into the slot at LDS byte address `slot`.
   // `full` (wave-uniform): the stage lies wholly inside K, so no lane needs the k bound.
+  // Per stage only wave-uniform 32-bit values change: the k byte offset and the first k
+  // element past K within the stage (KB on full stages, so no lane is cut).
   __device__ __forceinline__ void issue_l(unsigned slot, int64_t k0, int64_t K) {
-    const bool full = k0 + D::KB <= K;
+    const int lim = k0 + D::KB <= K ? D::KB : static_cast<int>(K - k0);
     const unsigned kb = static_cast<unsigned>(k0 * 2);
 #pragma unroll
-    for (int q = 0; q < D::QL; ++q) {
-      unsigned off = offl[q] + kb;
-      if (!full && k0 + kl[q] >= K) off = DMA_OOB;
-      dma16_at(rl, off, slot + wl + q * D::NW * D::RPL * D::ROW_BYTES);
-    }
+    for (int q = 0; q < D::QL; ++q)
+      dma16_at(rl, kl[q] < lim ? offl[q] + kb : DMA_OOB,
+               slot + wl + q * D::NW * D::RPL * D::ROW_BYTES);
   }
   __device__ __forceinline__ void issue_r(unsigned slot, int64_t k0, int64_t K) {
-    const bool full = k0 + D::KB <= K;
+    const int lim = k0 + D::KB <= K ? D::KB : static_cast<int>(K - k0);
     const unsigned kb = static_cast<unsigned>(k0 * 2);
 #pragma unroll
-    for (int u = 0; u < D::QR; ++u) {
-      unsigned off = offr[u] + kb;
-      if (!full && k0 + kr[u] >= K) off = DMA_OOB;
-      dma16_at(rr, off, slot + wl + u * D::NW * D::RPL * D::ROW_BYTES);
-    }
+    for (int u = 0; u < D::QR; ++u)
+      dma16_at(rr, kr[u] < lim ? offr[u] + kb : DMA_OOB,
+               slot + wl + u * D::NW * D::RPL * D::ROW_BYTES);
   }
 };
 
@@ -1705,8 +1703,10 @@ struct TnStreamer {
   // or past gap_at come from gap rows further on.  Per stage only wave-uniform 32-bit values
   // change: the base offset of row k0, the first row taking the gap and the first row past
   // k_end (all byte offsets below 2^31: the operands are below 2 GiB).
-  __device__ __forceinline__ void issue(unsigned char* stage, int64_t k0, int64_t k_end) {
-    const int wid = threadIdx.x >> 6;
+  // `stage`: the LDS byte address of the stage (wave-uniform).
+  __device__ __forceinline__ void issue(unsigned stage, int64_t k0, int64_t k_end) {
+    const unsigned wb = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
+                        1024u;  // this wave's first 1 KiB of each part
     const int64_t kp0 = k0 >= gap_at ? k0 + gap : k0;
     const int e_rel = k_end - k0 < D::KB ? static_cast<int>(k_end - k0) : D::KB;
     const int g_rel = k0 < gap_at && gap_at - k0 < D::KB ? static_cast<int>(gap_at - k0) : D::KB;
@@ -1715,12 +1715,12 @@ struct TnStreamer {
 #pragma unroll
     for (int q = 0; q < D::QL; ++q) {
       const unsigned off = offl[q] + bl + (rowl[q] >= g_rel ? gl : 0u);
-      dma16(rl, rowl[q] < e_rel ? off : DMA_OOB, stage + (wid + D::NW * q) * 1024);
+      dma16_at(rl, rowl[q] < e_rel ? off : DMA_OOB, stage + wb + D::NW * q * 1024);
     }
 #pragma unroll
     for (int q = 0; q < D::QR; ++q) {
       const unsigned off = offr[q] + br + (rowr[q] >= g_rel ? gr : 0u);
-      dma16(rr, rowr[q] < e_rel ? off : DMA_OOB, stage + D::L_BYTES + (wid + D::NW * q) * 1024);
+      dma16_at(rr, rowr[q] < e_rel ? off : DMA_OOB, stage + D::L_BYTES + wb + D::NW * q * 1024);
     }
   }
 };
@@ -1863,14 +1863,18 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
   st.init(p, mt, nt);
   const int nk = static_cast<int>((k_end - k_begin + D::KB - 1) / D::KB);
   auto slot = [&](int k) { return lds + (k % D::STAGES) * D::STAGE_BYTES; };
+  const unsigned lds0 = lds_addr(lds);
+  auto slot_at = [&](int k) {  // the same slot as an LDS byte address
+    return lds0 + static_cast<unsigned>((k % D::STAGES) * D::STAGE_BYTES);
+  };
 #pragma unroll
   for (int s = 0; s < AHEAD; ++s)
-    if (s < nk) st.issue(slot(s), k_begin + static_cast<int64_t>(s) * D::KB, k_end);
+    if (s < nk) st.issue(slot_at(s), k_begin + static_cast<int64_t>(s) * D::KB, k_end);
   int kt = 0;
   for (; kt + AHEAD < nk; ++kt) {
     wait_vmcnt<(AHEAD - 1) * NQ>();
     raw_barrier();
-    st.issue(slot(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
+    st.issue(slot_at(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
     cmp(slot(kt), acc);
     hook(kt, slot(kt));
   }

@@ -1703,6 +1703,19 @@ struct TnStreamer {
   // or past gap_at come from gap rows further on.  Per stage only wave-uniform 32-bit values
   // change: the base offset of row k0, the first row taking the gap and the first row past
   // k_end (all byte offsets below 2^31: the operands are below 2 GiB).
+  // A whole stage that does not straddle the skipped block: one wave-uniform base per stage.
+  __device__ __forceinline__ void issue_clean(unsigned stage, int64_t k0) {
+    const unsigned wb = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
+                        1024u;
+    const int64_t kp0 = k0 >= gap_at ? k0 + gap : k0;
+    const unsigned bl = static_cast<unsigned>(kp0 * ldl2), br = static_cast<unsigned>(kp0 * ldr2);
+#pragma unroll
+    for (int q = 0; q < D::QL; ++q)
+      dma16_at(rl, offl[q] + bl, stage + wb + D::NW * q * 1024);
+#pragma unroll
+    for (int q = 0; q < D::QR; ++q)
+      dma16_at(rr, offr[q] + br, stage + D::L_BYTES + wb + D::NW * q * 1024);
+  }
   // `stage`: the LDS byte address of the stage (wave-uniform).
   __device__ __forceinline__ void issue(unsigned stage, int64_t k0, int64_t k_end) {
     const unsigned wb = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
@@ -1871,12 +1884,28 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
   for (int s = 0; s < AHEAD; ++s)
     if (s < nk) st.issue(slot_at(s), k_begin + static_cast<int64_t>(s) * D::KB, k_end);
   int kt = 0;
-  for (; kt + AHEAD < nk; ++kt) {
-    wait_vmcnt<(AHEAD - 1) * NQ>();
-    raw_barrier();
-    st.issue(slot_at(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
-    cmp(slot(kt), acc);
-    hook(kt, slot(kt));
+  // With whole stages and the skipped block (if any) at a stage boundary, every stage is
+  // clean: its loads need only the wave-uniform base (the common case, T a multiple of the
+  // stage height); one loop version each, so neither carries the other's instructions.
+  const bool clean = (k_end - k_begin) % D::KB == 0 &&
+                     (p.gap == 0 || p.gap_at <= k_begin || p.gap_at >= k_end ||
+                      (p.gap_at - k_begin) % D::KB == 0);
+  if (clean) {
+    for (; kt + AHEAD < nk; ++kt) {
+      wait_vmcnt<(AHEAD - 1) * NQ>();
+      raw_barrier();
+      st.issue_clean(slot_at(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB);
+      cmp(slot(kt), acc);
+      hook(kt, slot(kt));
+    }
+  } else {
+    for (; kt + AHEAD < nk; ++kt) {
+      wait_vmcnt<(AHEAD - 1) * NQ>();
+      raw_barrier();
+      st.issue(slot_at(kt + AHEAD), k_begin + static_cast<int64_t>(kt + AHEAD) * D::KB, k_end);
+      cmp(slot(kt), acc);
+      hook(kt, slot(kt));
+    }
   }
   for (; kt < nk; ++kt) {
     wait_stages<NQ, AHEAD - 1>(nk - 1 - kt);

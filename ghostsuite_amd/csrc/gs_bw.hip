@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
     for (int k = 0; k < PC; ++k)
 #pragma unroll
       for (int i = 0; i < VE; ++i) s += xv[k].v[i];
-    const float mean = wave_sum(s) * invF;
+    const float mean = wave_sum_dpp(s) * invF;
     float var = 0.f;
 #pragma unroll
     for (int k = 0; k < PC; ++k) {
@@ -130,7 +130,7 @@ __global__ void __launch_bounds__(64 * LN_WAVES) ln_sums_kernel(
         var += dlt * dlt;
       }
     }
-    const float rstd = rsqrtf(wave_sum(var) * invF + eps);
+    const float rstd = rsqrtf(wave_sum_dpp(var) * invF + eps);
 #pragma unroll
     for (int k = 0; k < PC; ++k)
 #pragma unroll
@@ -229,10 +229,12 @@ __global__ void __launch_bounds__(64 * LN2_WAVES) ln_rows_kernel(
 #pragma unroll
     for (int i = 0; i < VE; ++i) v[i] = to_f32<E>(w.e[i]);
   };
-  auto group_sum = [](float v) {
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+  auto group_sum = [](float v) {  // over the row's LPR lanes, by DPP (no LDS round trips)
+    static_assert(LPR == 64 || LPR == 32, "row lanes");
+    if constexpr (LPR == 64)
+      return wave_sum_dpp(v);
+    else
+      return half_sum_dpp(v);
   };
   constexpr int STEP = LN2_WAVES * RW;  // token rows per block-wide pass
   int64_t t = t0 + wid * RW + rh;
@@ -328,7 +330,7 @@ __global__ void __launch_bounds__(64 * LNS_WAVES) ln_row_stats_kernel(
 #pragma unroll
     for (int i = 0; i < VE; ++i) s += x.v[i];
   }
-  const float mean = wave_sum(s) * invF;
+  const float mean = wave_sum_dpp(s) * invF;
   float q = 0.f;
   for (int64_t f = static_cast<int64_t>(lane) * VE; f < F; f += 64 * VE) {
     Vec<E> x;
@@ -339,7 +341,7 @@ __global__ void __launch_bounds__(64 * LNS_WAVES) ln_row_stats_kernel(
       q += f + i < F ? d * d : 0.f;
     }
   }
-  const float rstd = rsqrtf(wave_sum(q) * invF + eps);
+  const float rstd = rsqrtf(wave_sum_dpp(q) * invF + eps);
   if (lane == 0) stats[r] = make_float2(mean, rstd);
 }
 

@@ -137,6 +137,20 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 63));
 }
 
+// The sum over each 32-lane half of the wave, in every lane of that half (DPP, as
+// wave_sum_dpp, with the two halves read back from lanes 31 and 63).
+__device__ __forceinline__ float half_sum_dpp(float v) {
+  float s = v + dpp_f32<0x111, 0xf, 0xf>(v);
+  s += dpp_f32<0x112, 0xf, 0xf>(v);
+  s += dpp_f32<0x113, 0xf, 0xf>(v);
+  s += dpp_f32<0x114, 0xf, 0xe>(s);
+  s += dpp_f32<0x118, 0xf, 0xc>(s);
+  s += dpp_f32<0x142, 0xa, 0xf>(s);  // lane 31: rows 0 + 1, lane 63: rows 2 + 3
+  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 31));
+  const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 63));
+  return (threadIdx.x & 32) ? hi : lo;
+}
+
 // Block-wide sum; `red` must hold blockDim.x/64 floats.  Result is valid in every thread.
 __device__ __forceinline__ float block_sum(float v, float* red) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;

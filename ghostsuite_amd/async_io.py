@@ -12,8 +12,9 @@ the next one.  Here:
   after that stream waits for the current stream, and returns the host tensor plus the event
   that completes it.
 - ``PendingLog`` is a ``list`` of per-step records whose tensors may still be in flight; every
-  read of the records (indexing, iteration, pickling, ``clear``) first waits for the pending
-  copies, so readers always see finished values, exactly what the reference's list holds.
+  read of the records (indexing, iteration, pickling) first waits for the pending copies, so
+  readers always see finished values, exactly what the reference's list holds; ``clear``
+  drops the records without waiting.
 - ``FileWriter`` runs ``torch.save`` on a background thread once a record's copies are done;
   ``flush()`` waits for every write (the engines call it on save, detach and exit).
 
@@ -111,7 +112,11 @@ class PendingLog(list):
         return (list, (self.plain(),))
 
     def clear(self):
-        self.resolve()
+        # The records are dropped unread, so their copies need not be waited for: the pinned
+        # buffers are not reused before the copy stream has passed the copies (torch's host
+        # allocator tracks non-blocking copies), and the device snapshots were marked in use
+        # by the copy stream.
+        self._pending = []
         super().clear()
 
 

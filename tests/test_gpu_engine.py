@@ -276,6 +276,20 @@ def test_async_host_copies_and_files_match_device_results(gpu, tmp_path):
     assert type(saved) is list and len(saved) == 3
     assert set(saved[0]) == {"dot_product", "X_train", "Y_train", "iter_num", "batch_idx"}
     assert saved[2]["iter_num"] == 2 and saved[2]["dot_product"].dtype == torch.float32
+    # clear() drops records whose copies may still be in flight, without waiting; the
+    # records logged afterwards read back finished values.
+    for step in range(3, 6):
+        eng.attach_train_batch(X[:8], Y[:8], step, step)
+        F.cross_entropy(model(X), Y).backward()
+        want = sum(p.grad_dot_prod.clone() for _, p in model.named_parameters()
+                   if hasattr(p, "grad_dot_prod")).cpu()
+        eng.prepare_gradients()
+        eng.aggregate_and_log()
+        eng.clear_gradients()
+        if step < 5:
+            eng.dot_product_log.clear()
+    assert len(eng.dot_product_log) == 1
+    assert_close(eng.dot_product_log[0]["dot_product"], want, 1e-6, "log after clear")
     eng.detach()
 
     proj_dir = tmp_path / "proj"

@@ -449,3 +449,44 @@ def test_linear_dot_train_grad_declines(gpu):
     assert ops.linear_dot_train_grad(A.to(gpu), G.to(gpu), 2, grad_scale=1.0) is None
     A, G = _inputs(6, 64, 64, 256, 7, torch.float32)          # fp32 operands
     assert ops.linear_dot_train_grad(A.to(gpu), G.to(gpu), 2, grad_scale=1.0) is None
+
+
+@pytest.mark.parametrize("case", [
+    # N, n_val, T, d_in, d_out
+    (6, 2, 128, 136, 264),
+    (20, 4, 1024, 768, 3072),    # GPT-2-small mlp.c_fc
+])
+def test_conv1d_sampler_fused_dot_and_train_grad(gpu, case):
+    """HF Conv1D (weight [d_in, d_out]) takes the fused pass with its operands swapped: the
+    presum dots and the [d_in, d_out] train gradient against float64 closed forms, the bias
+    dot and train gradient from the bias pass, and the same dots as the unfused path."""
+    transformers = pytest.importorskip("transformers")
+    from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+    N, n_val, T, d_in, d_out = case
+    n_t = N - n_val
+    print(f"conv1d fused case={case}", flush=True)
+    layer = transformers.pytorch_utils.Conv1D(d_out, d_in).to(gpu, torch.bfloat16)
+    for p in layer.parameters():
+        p.initially_requires_grad = True
+    A = randn((N, T, d_in), 120, 1.0, torch.bfloat16)
+    G = randn((N, T, d_out), 121, 1e-3, torch.bfloat16)
+    Ad, Gd = A.to(gpu), G.to(gpu)
+    layer._gs_bias_grad_scale = 1.5 / n_t
+    S._compute_Conv1D_dot_product(layer, Ad, Gd, n_val)
+    assert "_gs_weight_train_grad" in layer.__dict__          # the fused pass ran
+    dot = layer.weight.grad_dot_prod.cpu()
+    want_dot = R.linear_dot_valterm_exact(Ad, Gd, n_val, "presum").cpu()
+    assert_close(dot, want_dot, BF16_TOL, "weight dot")
+    grad = S._compute_Conv1D_train_grad(layer, Ad, Gd, n_val, scale=1.5)
+    assert grad.shape == (d_in, d_out)
+    assert_close(grad.float().cpu(), _train_grad_want(A, G, n_val, N - n_val, 1.5 / n_t, True, gpu),
+                 1e-2, "weight train grad")
+    assert_close(layer.bias.grad_dot_prod.cpu(), R.bias_dot_exact(G, n_val), BF16_TOL, "bias dot")
+    tr, _ = R.split_rows(G.double(), n_val, N - n_val)
+    assert_close(layer._gs_bias_train_grad.float().cpu(), tr.sum((0, 1)) * (1.5 / n_t), 1e-2,
+                 "bias train grad")
+    # without the announced scale the dots come from the unfused path
+    del layer._gs_bias_grad_scale
+    S._compute_Conv1D_dot_product(layer, Ad, Gd, n_val)
+    assert "_gs_weight_train_grad" not in layer.__dict__
+    assert_close(layer.weight.grad_dot_prod.cpu(), dot, BF16_TOL, "unfused weight dot")

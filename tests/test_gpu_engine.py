@@ -146,6 +146,66 @@ def test_hf_conv1d_layers_use_presum(gpu):
         assert_close(d, brute.pairwise_dots(g[name], n_v), FP32_TOL, f"conv1d {name}")
 
 
+@pytest.mark.parametrize("n_v", [1, 2])
+def test_hf_conv1d_bf16_fused_path(gpu, n_v, monkeypatch):
+    """A bf16 HF Conv1D model at tile-aligned sizes takes the fused dot + train-gradient pass
+    (operands swapped, [d_in, d_out] gradient popped into train_grad): dots and weights'
+    gradients against the unfused passes on the same run, and at n_v = 1 (presum equals
+    pairwise) the dots against brute force."""
+    transformers = pytest.importorskip("transformers")
+    Conv1D = transformers.pytorch_utils.Conv1D
+    torch.manual_seed(31)
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.c1 = Conv1D(128, 64)   # nf=128 out, nx=64 in
+            self.c2 = Conv1D(64, 128)
+
+        def forward(self, x):
+            return self.c2(torch.tanh(self.c1(x)))
+
+    net = Net().to(torch.bfloat16).float()   # the reference starts from the bf16 weights
+    ref = copy.deepcopy(net).double()
+    N, T = 3 + n_v, 64
+    X = torch.randn(N, T, 64, generator=gen(32)).to(torch.bfloat16).float()
+    head = torch.randn(64, generator=gen(33)).to(torch.bfloat16).float()
+    net = net.to(gpu, torch.bfloat16)
+    opt = torch.optim.SGD(net.parameters(), lr=0.0)
+    eng = GradDotProdEngine(net, val_batch_size=n_v, use_dummy_bias=False, record_algorithms=True)
+
+    def run():
+        S.ALGO_LOG.clear()
+        eng.attach(opt)
+        loss = (net(X.to(gpu, torch.bfloat16)) * head.to(gpu, torch.bfloat16))
+        loss.reshape(N, -1).float().sum(1).mean().backward()
+        torch.cuda.synchronize()
+        dots = {n: p.grad_dot_prod.float().cpu() for n, p in net.named_parameters()}
+        eng.prepare_gradients()
+        grads = {n: p.grad.float().cpu() for n, p in net.named_parameters()}
+        eng.clear_gradients()
+        eng.detach()
+        return dots, grads, dict(S.ALGO_LOG)
+
+    print(f"hf conv1d bf16 fused n_v={n_v}", flush=True)
+    dots, grads, log = run()
+    assert sorted(k for k, v in log.items() if v[1] == "valgrad+train_grad") == ["c1", "c2"], log
+    assert grads["c1.weight"].shape == (64, 128) and grads["c2.weight"].shape == (128, 64)
+    monkeypatch.setattr(S, "_fused_dot_train_grad", lambda *a, **k: False)
+    dots2, grads2, log2 = run()
+    assert not any(v[1] == "valgrad+train_grad" for v in log2.values()), log2
+    for name in dots:
+        assert_close(dots[name], dots2[name], 1e-2, f"fused vs unfused dot {name}")
+        assert_close(grads[name], grads2[name], 1e-2, f"fused vs unfused grad {name}")
+    if n_v == 1:
+        g = brute.per_sample_grads(ref, X.double(), X,
+                                   lambda m, x, y: (m(x) * head.double()).sum(), 1.0 / N)
+        for name, d in dots.items():
+            assert_close(d, brute.pairwise_dots(g[name], n_v), BF16_TOL, f"conv1d {name}")
+            want = brute.train_mean(g[name], n_v, N)
+            assert_close(grads[name], want, BF16_TOL, f"conv1d grad {name}")
+
+
 def test_gradproj_engine_on_gpu_naive_check(gpu, tmp_path):
     torch.manual_seed(20)
     model = nn.Sequential(nn.Linear(10, 20), nn.ReLU(), nn.Linear(20, 5)).to(gpu)

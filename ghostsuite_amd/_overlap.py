@@ -86,6 +86,15 @@ def on_side_stream(*tensors):
     side.wait_stream(cur)
     for t in ts:
         t.record_stream(side)
-    with torch.cuda.stream(side):
-        yield
+    if torch.cuda.current_device() == idx:
+        # Same device: switch the current stream only (the stream context manager also
+        # saves and restores the current device, several times the cost per hook).
+        torch.cuda.set_stream(side)
+        try:
+            yield
+        finally:
+            torch.cuda.set_stream(cur)
+    else:
+        with torch.cuda.stream(side):
+            yield
     _queue_join(idx, cur, side)

@@ -146,10 +146,12 @@ def _apply_train_grad(layer: nn.Module, val_batch_size: int, loss_reduction: str
     scale = getattr(layer, "backprops_scale", 1.0)
     # The train-gradient kernels join the layer's dot kernels on the side stream: both read
     # only this layer's activations and backprops, and the end-of-backward join orders
-    # param.train_grad before the optimizer reads it.
+    # param.train_grad before the optimizer reads it.  When the dot stage already formed
+    # every train gradient, nothing is enqueued here but an add_ into an existing train_grad
+    # (after a join), so the side stream is left alone.
     side = _overlap.on_side_stream(layer.__dict__.get("activations"),
                                    layer.__dict__.get("backprops")) \
-        if options["overlap"] else contextlib.nullcontext()
+        if options["overlap"] and not _train_grads_parked(layer) else contextlib.nullcontext()
     try:
         with side:
             _apply_train_grad_body(layer, compute_layer_train_grad, val_batch_size, scale,
@@ -159,6 +161,20 @@ def _apply_train_grad(layer: nn.Module, val_batch_size: int, loss_reduction: str
                      '_gs_weight_train_grad', '_gs_ln_train_grads', '_gs_bias_grad_scale',
                      '_gs_ln_grad_scale'):
             layer.__dict__.pop(attr, None)
+
+
+def _train_grads_parked(layer: nn.Module) -> bool:
+    """True when the dot stage parked every train gradient this layer applies."""
+    d = layer.__dict__
+    if isinstance(layer, nn.LayerNorm):
+        return "_gs_ln_train_grads" in d
+    w = getattr(layer, "weight", None)
+    if w is None or not getattr(w, "initially_requires_grad", False) or \
+            "_gs_weight_train_grad" not in d:
+        return False
+    b = getattr(layer, "bias", None)
+    return b is None or not getattr(b, "initially_requires_grad", False) or \
+        "_gs_bias_train_grad" in d
 
 
 def _apply_train_grad_body(layer: nn.Module, compute_layer_train_grad, val_batch_size: int,

@@ -326,6 +326,13 @@ def _compute_embedding_dot_product(layer: nn.Embedding, A: torch.Tensor, B: torc
         B = B.float()
     layer.weight.grad_dot_prod = ops().embedding_dot(A, B, val_batch_size,
                                                      vocab=layer.weight.shape[0])
+    # With the train-grad scale announced, the train gradient is formed here as well (same
+    # stream as the dot, no second hook-stage launch sequence) and parked for
+    # _compute_embedding_train_grad.
+    scale = getattr(layer, "_gs_bias_grad_scale", None)
+    if scale is not None and getattr(layer.weight, "initially_requires_grad", False):
+        layer._gs_weight_train_grad = _embedding_train_grad(layer, A, B, val_batch_size, scale,
+                                                            join=False)
 
 
 # Returned by a train-grad sampler that has already added its gradient into
@@ -344,17 +351,28 @@ def _compute_embedding_train_grad(layer: nn.Embedding, A: torch.Tensor, B: torch
     n_t = A.size(0) - val_batch_size
     if n_t <= 0:
         return None
+    parked = layer.__dict__.pop("_gs_weight_train_grad", None)
+    if parked is not None:   # formed with the dot, same scale
+        return parked
+    return _embedding_train_grad(layer, A, B, val_batch_size, scale / n_t, join=True)
+
+
+def _embedding_train_grad(layer: nn.Embedding, A: torch.Tensor, B: torch.Tensor,
+                          val_batch_size: int, alpha: float, join: bool):
+    """alpha * (sum of the train rows of B per token id) as a fresh gradient, or added into
+    the weight's existing train gradient (then APPLIED).  ``join``: order the current stream
+    after the side stream first (not needed on the side stream itself)."""
     B = B.detach()
     if B.dtype not in (torch.bfloat16, torch.float32):
         B = B.float()
     prev = getattr(layer.weight, "train_grad", None)
     if prev is not None and prev.shape == layer.weight.shape:
-        _overlap.join(prev.device)   # prev may come from the side stream
-        ops().embedding_train_grad(A.detach(), B, val_batch_size, scale / n_t, prev,
-                                   accumulate=True)
+        if join:
+            _overlap.join(prev.device)   # prev may come from the side stream
+        ops().embedding_train_grad(A.detach(), B, val_batch_size, alpha, prev, accumulate=True)
         return APPLIED
     grad = torch.empty_like(layer.weight)
-    ops().embedding_train_grad(A.detach(), B, val_batch_size, scale / n_t, grad)
+    ops().embedding_train_grad(A.detach(), B, val_batch_size, alpha, grad)
     return grad
 
 

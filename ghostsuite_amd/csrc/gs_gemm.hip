@@ -767,13 +767,20 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
 // Maps the launch index to (m tile, n tile): consecutive workgroups of one XCD get
 // consecutive logical ids, and logical ids sweep GROUP n-tiles per m-tile so that the
 // workgroups resident on an XCD share operand tiles in its L2.
+// Work index of workgroup w of a grid of `total`: the hardware deals workgroups to the 8 XCDs
+// round-robin (w mod 8), so XCD x is given the contiguous range of work indices that is its
+// share of the grid (the first total mod 8 XCDs one more), and the items it runs share
+// operand rows in its L2.
+__device__ __forceinline__ int64_t xcd_order(int64_t w, int64_t total) {
+  constexpr int64_t XCDS = 8;
+  const int64_t q = total / XCDS, rr = total % XCDS, x = w % XCDS;
+  return x * q + (x < rr ? x : rr) + w / XCDS;
+}
+
 __device__ __forceinline__ void tile_of_block(int64_t m_tiles, int64_t n_tiles, int64_t& mt,
                                               int64_t& nt) {
-  constexpr int64_t GROUP = GS_GROUP, XCDS = 8;
-  const int64_t nb = static_cast<int64_t>(gridDim.x);
-  const int64_t bid = blockIdx.x;
-  int64_t lid = bid;
-  if (nb % XCDS == 0) lid = (bid % XCDS) * (nb / XCDS) + bid / XCDS;
+  constexpr int64_t GROUP = GS_GROUP;
+  const int64_t lid = xcd_order(blockIdx.x, gridDim.x);
   const int64_t per_group = GROUP * m_tiles;
   const int64_t g = lid / per_group;
   const int64_t first_n = g * GROUP;
@@ -1924,9 +1931,7 @@ __device__ __forceinline__ void mainloop_tn(const TnParams& p, int64_t mt, int64
 // XCD streaming most of both operands.
 __device__ __forceinline__ void tn_item(const TnParams& p, int64_t& mt, int64_t& nt,
                                         int64_t& split) {
-  constexpr int64_t XCDS = 8;
-  const int64_t total = static_cast<int64_t>(gridDim.x), w = blockIdx.x;
-  const int64_t i = total % XCDS == 0 ? (w % XCDS) * (total / XCDS) + w / XCDS : w;
+  const int64_t i = xcd_order(blockIdx.x, gridDim.x);
   const int64_t tiles = p.m_tiles * p.n_tiles;
   split = i / tiles;
   const int64_t r = i - split * tiles;
@@ -2437,9 +2442,10 @@ bool tn_ok(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, in
 // Splits of the k-rows: enough workgroups to cover the CUs against the fp32 partials' extra
 // write + read.  Estimate: two workgroups fit on a CU (512 slots), so the launch takes
 // ceil(items / 512) rounds of one workgroup's k-rows at ~2 TF/s per workgroup when the CUs
-// hold two (~3.2 TF/s alone, at most 256 items), plus the partials at 4 TB/s and the reduction
-// launch (rates measured for the 128 x 128 tile at the GPT-2 shapes: train gradients with
-// 16k k-rows take 3-4 splits at fc / qkv, 7 at proj).
+// hold two (~2.2 TF/s alone, at most 256 items: a CU nearly doubles its rate with a second
+// workgroup), plus the partials at 4 TB/s and the reduction launch (rates measured for the
+// 128 x 128 tile at the GPT-2 shapes: train gradients with 16k k-rows take 3-4 splits at
+// fc / qkv, 14 at proj, where 7 splits measured 46 us and 14 splits 33 us).
 int64_t tn_kper(int64_t K, int sp) {
   return ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
          TnD::KB;
@@ -2453,7 +2459,7 @@ int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
   for (int sp = 1; sp <= 16 && sp <= std::max<int64_t>(1, ksteps / 4); ++sp) {
     const int64_t items = tiles * sp;
     const double rounds = std::ceil(static_cast<double>(items) / 512.0);
-    const double rate = items <= 256 ? 3.2e12 : 2.0e12;
+    const double rate = items <= 256 ? 2.2e12 : 2.0e12;
     const double t = rounds * 2.0 * TnC::BM * TnC::BN * tn_kper(K, sp) / rate +
                      (sp > 1 ? 8.0 * sp * M * N / 4e12 + 3e-6 : 0.0);
     if (t < best_t) {

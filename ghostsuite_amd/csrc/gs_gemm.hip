@@ -2170,6 +2170,30 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   store_epilogue<TrF32, C>(e, acc, mt, nt);
 }
 
+// part[0][i..i+3] + part[1][i..i+3] + ... over the splits, added in split order; the loads
+// of four splits at a time are unguarded, so they are in flight together.
+__device__ __forceinline__ float4 split_sum4(const float* __restrict__ part, int64_t count,
+                                             int splits, int64_t i) {
+  auto ld = [&](int k) { return *reinterpret_cast<const float4*>(part + k * count + i); };
+  auto add = [](float4& a, const float4& b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  };
+  float4 s = ld(0);
+  int k = 1;
+  for (; k + 4 <= splits; k += 4) {
+    const float4 v0 = ld(k), v1 = ld(k + 1), v2 = ld(k + 2), v3 = ld(k + 3);
+    add(s, v0);
+    add(s, v1);
+    add(s, v2);
+    add(s, v3);
+  }
+  for (; k < splits; ++k) add(s, ld(k));
+  return s;
+}
+
 // out[i] = alpha * (sum over the splits of part[s][i]) in fixed order, rounded once to bf16
 // (or stored as fp32 with out_f32), 4 elements per thread.  With vsum ([vs_rows][vs_n]) its
 // rows are also summed into row 0, in place.
@@ -2179,38 +2203,37 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
                                                         int64_t vs_n, int64_t vs_rows) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (vsum != nullptr && i < vs_n) {
-    // Rows k = j mod 4 into four running sums (loads in flight together), then combined.
+    // Rows k = j mod 4 into four running sums, then combined.  Whole groups of four rows are
+    // loaded unguarded, so the four loads are in flight together (a guarded load per row
+    // compiles to a wait after every load); four, not more, keep the kernel's registers (and
+    // the occupancy of its bandwidth-bound partial sums) low.
     float4 t[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) t[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int64_t k = 0; k < vs_rows; k += 4) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (k + j < vs_rows) {
-          const float4 v = *reinterpret_cast<const float4*>(vsum + (k + j) * vs_n + i);
-          t[j].x += v.x;
-          t[j].y += v.y;
-          t[j].z += v.z;
-          t[j].w += v.w;
-        }
-      }
+    auto add = [](float4& a, const float4& b) {
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    };
+    auto row = [&](int64_t k) { return *reinterpret_cast<const float4*>(vsum + k * vs_n + i); };
+    int64_t k = 0;
+    for (; k + 4 <= vs_rows; k += 4) {
+      const float4 v0 = row(k), v1 = row(k + 1), v2 = row(k + 2), v3 = row(k + 3);
+      add(t[0], v0);
+      add(t[1], v1);
+      add(t[2], v2);
+      add(t[3], v3);
     }
-    float4 r;
-    r.x = (t[0].x + t[1].x) + (t[2].x + t[3].x);
-    r.y = (t[0].y + t[1].y) + (t[2].y + t[3].y);
-    r.z = (t[0].z + t[1].z) + (t[2].z + t[3].z);
-    r.w = (t[0].w + t[1].w) + (t[2].w + t[3].w);
+    for (; k < vs_rows; ++k) add(t[k & 3], row(k));
+    add(t[0], t[1]);
+    add(t[2], t[3]);
+    add(t[0], t[2]);
+    const float4 r = t[0];
     *reinterpret_cast<float4*>(vsum + i) = r;
   }
   if (i >= count) return;
-  float4 s = *reinterpret_cast<const float4*>(part + i);
-  for (int k = 1; k < splits; ++k) {
-    const float4 v = *reinterpret_cast<const float4*>(part + k * count + i);
-    s.x += v.x;
-    s.y += v.y;
-    s.z += v.z;
-    s.w += v.w;
-  }
+  float4 s = split_sum4(part, count, splits, i);
   s.x *= alpha;
   s.y *= alpha;
   s.z *= alpha;

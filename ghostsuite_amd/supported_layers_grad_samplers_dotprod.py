@@ -280,8 +280,8 @@ def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tenso
 
 # Output tiles (128 x 128) below which the K-major train-gradient GEMM beats hipBLASLt:
 # with fewer tiles than CUs the product is a long-K, small-output GEMM that the K-major kernel
-# splits over the token rows (GPT-2-small: fc / fc_out 96-100 us against 152-160 us through
-# torch.addmm, proj 46-48 against 98), while outputs of 256 tiles and more (Pythia-1B layers,
+# splits over the token rows (GPT-2-small: fc / fc_out 85-88 us against 152-160 us through
+# torch.addmm, proj 31 against 98), while outputs of 256 tiles and more (Pythia-1B layers,
 # the 50k-row lm_head) run faster through hipBLASLt (e.g. 2048x8192: 506 against 572 us).
 _TRAIN_GRAD_MAX_TILES = 256
 

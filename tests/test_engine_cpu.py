@@ -401,3 +401,31 @@ def test_embedding_id_promotion(promote):
     # the reference's own op sequence on the promoted ids is the bucketed value
     assert_close(R.embedding_dot_ref(ids.to(torch.bfloat16), B, n_v, vocab), bucketed,
                  BF16_TOL, "reference sequence")
+
+
+def test_gradient_stage_skips_side_stream_only_when_everything_is_parked():
+    """The hook's gradient stage leaves the side stream alone only when the dot stage parked
+    every train gradient the layer applies (weight, and the bias when it trains)."""
+    from ghostsuite_amd.autograd_grad_sample_dotprod import _train_grads_parked
+    lin = nn.Linear(4, 3)
+    for p in lin.parameters():
+        p.initially_requires_grad = True
+    assert not _train_grads_parked(lin)
+    lin._gs_weight_train_grad = torch.zeros(3, 4)
+    assert not _train_grads_parked(lin)            # bias trains and is not parked
+    lin._gs_bias_train_grad = torch.zeros(3)
+    assert _train_grads_parked(lin)
+    lin.bias.initially_requires_grad = False
+    del lin._gs_bias_train_grad
+    assert _train_grads_parked(lin)                # a frozen bias needs nothing
+    lin.weight.initially_requires_grad = False
+    assert not _train_grads_parked(lin)            # nothing parked for a frozen weight
+    ln = nn.LayerNorm(4)
+    assert not _train_grads_parked(ln)
+    ln._gs_ln_train_grads = (torch.zeros(4), torch.zeros(4))
+    assert _train_grads_parked(ln)
+    emb = nn.Embedding(5, 4)
+    emb.weight.initially_requires_grad = True
+    assert not _train_grads_parked(emb)
+    emb._gs_weight_train_grad = S.APPLIED          # added into a tied weight's train_grad
+    assert _train_grads_parked(emb)

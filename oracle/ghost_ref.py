@@ -141,11 +141,17 @@ def linear_dot_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, semantics: st
 
 def linear_dot_valterm_exact(A: torch.Tensor, B: torch.Tensor, n_val: int,
                              semantics: str = "pairwise",
-                             val_start: Optional[int] = None) -> torch.Tensor:
+                             val_start: Optional[int] = None,
+                             round_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """The linear_dot_exact vector through the val term: dot_i = sum_t b_it^T V a_it with V
     from val_term_exact, since <sum_t b_it a_it^T, V>_F = sum_t b_it^T V a_it.  Float64,
     with 2-D products only and one train row at a time, so that it runs at full model sizes
-    on whichever device holds A and B (no [n_train, d_out, d_in] tensor is formed)."""
+    on whichever device holds A and B (no [n_train, d_out, d_in] tensor is formed).
+
+    ``round_dtype`` (e.g. bf16): the val-gradient kernels' rounding points, otherwise exact:
+    the presummed val rows (presum) and V are rounded to that dtype before the products.  A
+    dot whose train gradient is nearly orthogonal to V amplifies these roundings; this form
+    then checks the kernels to their own arithmetic."""
     N = A.shape[0]
     d, p = A.shape[-1], B.shape[-1]
     a = A.reshape(N, -1, d)
@@ -153,12 +159,14 @@ def linear_dot_valterm_exact(A: torch.Tensor, B: torch.Tensor, n_val: int,
     vs = N - n_val if val_start is None else val_start
     va_a = a[vs:vs + n_val].double()
     va_b = b[vs:vs + n_val].double()
+    rnd = (lambda x: x.to(round_dtype).double()) if round_dtype is not None else (lambda x: x)
     if semantics == "pairwise":
         V = torch.mm(va_b.reshape(-1, p).t(), va_a.reshape(-1, d))
     elif semantics == "presum":
-        V = torch.mm(va_b.sum(0).t(), va_a.sum(0))
+        V = torch.mm(rnd(va_b.sum(0)).t(), rnd(va_a.sum(0)))
     else:
         raise ValueError(semantics)
+    V = rnd(V)
     del va_a, va_b
     rows = [i for i in range(N) if not vs <= i < vs + n_val]
     out = torch.empty(len(rows), dtype=torch.float64, device=A.device)

@@ -490,3 +490,59 @@ def test_conv1d_sampler_fused_dot_and_train_grad(gpu, case):
     S._compute_Conv1D_dot_product(layer, Ad, Gd, n_val)
     assert "_gs_weight_train_grad" not in layer.__dict__
     assert_close(layer.weight.grad_dot_prod.cpu(), dot, BF16_TOL, "unfused weight dot")
+
+
+def _random_fused_cases(n, seed):
+    """Seeded shapes inside the fused op's domain: T a multiple of 64, feature counts
+    multiples of 8, 1-4 val rows anywhere in the batch, both semantics, with and without a
+    bias; sizes kept small enough for float64 checks in seconds."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    cases = []
+    for _ in range(n):
+        n_val = pick(1, 4)
+        N = n_val + pick(1, 6)
+        T = 64 * pick(1, 6)
+        d_in, d_out = 8 * pick(1, 64), 8 * pick(1, 64)
+        vs = pick(0, N - n_val)
+        sem = "presum" if pick(0, 1) else "pairwise"
+        cases.append((N, n_val, vs, T, d_in, d_out, sem, bool(pick(0, 1))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_fused_cases(24, 2026))
+def test_linear_dot_train_grad_random_shapes(gpu, case):
+    """gs_linear_dot_train_grad over seeded random shapes (split counts, tile edges, cut
+    samples and val positions vary together) against the float64 closed forms; the same call
+    with the operands swapped (the HF Conv1D path) gives the same dots and the transposed
+    train gradient.  The dots are checked against the val-term form with the kernels' bf16
+    rounding points (presummed val rows, V): with one or two train rows a dot can be nearly
+    orthogonal to V (cos ~ 1e-3 at these sizes), which turns their 0.2% rounding into
+    several percent of the dot."""
+    N, n_val, vs, T, d_in, d_out, sem, bias = case
+    print(f"random fused case={case}", flush=True)
+    A = randn((N, T, d_in), 130 + N + T, 1.0, torch.bfloat16)
+    G = randn((N, T, d_out), 131 + d_in, 1e-3, torch.bfloat16)
+    n_t = N - n_val
+    semantics = _native.SEM_PAIRWISE_SUM if sem == "pairwise" else _native.SEM_PRESUM
+    Ad, Gd = A.to(gpu), G.to(gpu)
+    ops = _native.ops()
+    res = ops.linear_dot_train_grad(Ad, Gd, n_val, val_start=vs, semantics=semantics,
+                                    grad_scale=1.0 / n_t, grad_dtype=torch.float32, bias=bias,
+                                    bias_grad_scale=1.0 / n_t, bias_grad_dtype=torch.float32)
+    assert res is not None
+    dot, grad, bdot, bgrad = res
+    want_dot = R.linear_dot_valterm_exact(Ad, Gd, n_val, sem, val_start=vs,
+                                          round_dtype=torch.bfloat16).cpu()
+    assert_close(dot.cpu(), want_dot, BF16_TOL, "weight dot")
+    want_grad = _train_grad_want(A, G, n_val, vs, 1.0 / n_t, False, gpu)
+    assert_close(grad.cpu(), want_grad, FP32_TOL, "weight train grad")
+    if bias:
+        assert_close(bdot.cpu(), R.bias_dot_exact(G, n_val, vs), BF16_TOL, "bias dot")
+        tr, _ = R.split_rows(G.double(), n_val, vs)
+        assert_close(bgrad.cpu(), tr.sum((0, 1)) / n_t, FP32_TOL, "bias train grad")
+    sw = ops.linear_dot_train_grad(Gd, Ad, n_val, val_start=vs, semantics=semantics,
+                                   grad_scale=1.0 / n_t, grad_dtype=torch.float32)
+    assert sw is not None
+    assert_close(sw[0].cpu(), want_dot, BF16_TOL, "swapped dot")
+    assert_close(sw[1].cpu(), want_grad.t(), FP32_TOL, "swapped train grad")

@@ -125,6 +125,34 @@ def test_linear_val_term_form_equals_closed_form(semantics, val_start):
     assert not ok
 
 
+@pytest.mark.parametrize("semantics", ["pairwise", "presum"])
+def test_linear_val_term_rounding_points(semantics):
+    """The val-term form with the kernels' bf16 rounding points (presummed val rows and V):
+    on small-integer inputs every presummed row and every V entry is exactly representable
+    in bf16, so the rounded form equals the exact one bit for bit (no term dropped, nothing
+    transposed); on random inputs the rounding moves V, and only V, by bf16 relative error,
+    and the rounded form equals the dot against that rounded V."""
+    N, n_val, T, d_in, d_out = 7, 3, 5, 6, 4
+    g = torch.Generator().manual_seed(54)
+    Ai = torch.randint(-2, 3, (N, T, d_in), generator=g).double()
+    Bi = torch.randint(-2, 3, (N, T, d_out), generator=g).double()
+    exact = R.linear_dot_valterm_exact(Ai, Bi, n_val, semantics)
+    assert torch.equal(R.linear_dot_valterm_exact(Ai, Bi, n_val, semantics,
+                                                  round_dtype=torch.bfloat16), exact)
+    A = randn((N, T, d_in), 55).bfloat16()
+    B = randn((N, T, d_out), 56, 1e-3).bfloat16()
+    V = R.val_term_exact(A, B, n_val, semantics)          # [d_out, d_in], float64
+    if semantics == "presum":
+        vs = N - n_val
+        V = B[vs:].double().sum(0).bfloat16().double().t() @ \
+            A[vs:].double().sum(0).bfloat16().double()
+    Vr = V.bfloat16().double()
+    assert 0 < (Vr - V).abs().max() <= 2.0 ** -8 * V.abs().max()
+    want = torch.stack([(B[i].double() @ Vr * A[i].double()).sum() for i in range(N - n_val)])
+    assert_close(R.linear_dot_valterm_exact(A, B, n_val, semantics, round_dtype=torch.bfloat16),
+                 want, 1e-12, "rounded val-term form")
+
+
 @pytest.mark.parametrize("T", [1, 6])
 def test_linear_reference_sequence_within_bf16_tolerance(T):
     N, n_val, d_in, d_out = 8, 2, 32, 24

@@ -546,3 +546,60 @@ def test_linear_dot_train_grad_random_shapes(gpu, case):
     assert sw is not None
     assert_close(sw[0].cpu(), want_dot, BF16_TOL, "swapped dot")
     assert_close(sw[1].cpu(), want_grad.t(), FP32_TOL, "swapped train grad")
+
+
+def _random_dot_cases(n, seed):
+    """Seeded shapes for the separate dot and train-gradient entry points: any T, feature
+    counts aligned or not (aligned ones take the DMA / K-major kernels, the others the
+    transposing path), 1-4 val rows anywhere, at least four train rows (a single near-zero
+    dot is then judged against the vector's scale)."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    cases = []
+    for _ in range(n):
+        n_val = pick(1, 4)
+        N = n_val + pick(4, 8)
+        T = pick(1, 160)
+        d_in = 8 * pick(1, 40) if pick(0, 1) else pick(1, 300)
+        d_out = 8 * pick(1, 40) if pick(0, 1) else pick(1, 300)
+        cases.append((N, n_val, pick(0, N - n_val), T, d_in, d_out,
+                      "presum" if pick(0, 1) else "pairwise",
+                      _native.ALGO_GHOST if pick(0, 1) else _native.ALGO_VALGRAD))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_dot_cases(24, 2027))
+def test_linear_dot_random_shapes(gpu, case):
+    """gs_linear_dot (ghost and val-gradient algorithms, both semantics) over seeded random
+    shapes against the float64 closed form, bf16 operands."""
+    N, n_val, vs, T, d_in, d_out, sem, algo = case
+    print(f"random linear_dot case={case}", flush=True)
+    A = randn((N, T, d_in), 140 + N + T, 1.0, torch.bfloat16)
+    G = randn((N, T, d_out), 141 + d_out, 1e-3, torch.bfloat16)
+    semantics = _native.SEM_PAIRWISE_SUM if sem == "pairwise" else _native.SEM_PRESUM
+    dot, _ = _native.ops().linear_dot(A.to(gpu), G.to(gpu), n_val, val_start=vs,
+                                      semantics=semantics, algo=algo)
+    want = R.linear_dot_exact(A, G, n_val, sem, val_start=vs)
+    assert_close(dot.cpu(), want, BF16_TOL, f"{sem}/{algo}")
+
+
+@pytest.mark.parametrize("case", _random_dot_cases(16, 2028))
+def test_linear_train_grad_random_shapes(gpu, case):
+    """gs_linear_train_grad over seeded random shapes (Linear and Conv1D layouts, bf16 and
+    fp32 outputs) against the float64 GEMM; shapes outside the kernel decline with None."""
+    N, n_val, vs, T, d_in, d_out, _, algo = case
+    conv1d = algo == _native.ALGO_GHOST
+    out_dtype = torch.float32 if T % 2 else torch.bfloat16
+    print(f"random train grad case={case} conv1d={conv1d} out={out_dtype}", flush=True)
+    A = randn((N, T, d_in), 150 + N + T, 1.0, torch.bfloat16)
+    G = randn((N, T, d_out), 151 + d_in, 1e-3, torch.bfloat16)
+    n_t = N - n_val
+    out = _native.ops().linear_train_grad(A.to(gpu), G.to(gpu), n_val, 1.0 / n_t, val_start=vs,
+                                          out_dtype=out_dtype, conv1d=conv1d)
+    if d_in % 8 or d_out % 8:
+        assert out is None
+        return
+    assert out is not None
+    tol = 1e-2 if out_dtype == torch.bfloat16 else FP32_TOL
+    assert_close(out.float().cpu(), _train_grad_want(A, G, n_val, vs, 1.0 / n_t, conv1d, gpu),
+                 tol, "train grad")

@@ -233,3 +233,82 @@ def test_kron_embedding_projection(gpu, dtype, conf):
     want = R.kron_embed_proj_exact(ids, G.float(), P_i.to(dtype).float(), P_o.to(dtype).float())
     tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
     assert_close(out.cpu(), want, tol, "kron embed")
+
+
+def _random_bw_cases(n, seed):
+    """Seeded (N, n_val, val_start, T, d, vocab) for the bandwidth ops: any T and feature
+    count (aligned or not), small to 50k vocabularies, 1-4 val rows anywhere, at least four
+    train rows."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    out = []
+    for _ in range(n):
+        n_val = pick(1, 4)
+        N = n_val + pick(4, 8)
+        d = 8 * pick(1, 200) if pick(0, 1) else pick(1, 1500)
+        vocab = [pick(1, 40), pick(100, 5000), 50257][pick(0, 2)]
+        out.append((N, n_val, pick(0, N - n_val), pick(1, 300), d, vocab))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_bw_cases(16, 2029))
+def test_layernorm_random_shapes(gpu, case):
+    """LayerNorm dots and train gradients over seeded random shapes against float64."""
+    N, n_val, vs, T, Fd, _ = case
+    print(f"random layernorm case={case}", flush=True)
+    X = randn((N, T, Fd), 160 + T, 2.0, torch.bfloat16) + 0.5
+    G = randn((N, T, Fd), 161 + Fd, 1e-3, torch.bfloat16)
+    n_t = N - n_val
+    dw, db, gw, gb = _native.ops().layernorm_dot(X.to(gpu), G.to(gpu), n_val, 1e-5, val_start=vs,
+                                                 grad_scale=N / n_t, grad_dtype=torch.float32)
+    X = torch.cat([X[:vs], X[vs + n_val:], X[vs:vs + n_val]])  # val rows last for the oracle
+    G = torch.cat([G[:vs], G[vs + n_val:], G[vs:vs + n_val]])
+    ww, wb = R.layernorm_dot_exact(X, G, n_val, 1e-5)
+    assert_close(dw.cpu(), ww, BF16_TOL, "ln weight dot")
+    assert_close(db.cpu(), wb, BF16_TOL, "ln bias dot")
+    gw_ref, gb_ref = R.layernorm_train_grad(X.double(), G.double() * N, n_val, 1e-5)
+    assert_close(gw.cpu(), gw_ref, BF16_TOL, "ln weight grad")
+    assert_close(gb.cpu(), gb_ref, BF16_TOL, "ln bias grad")
+
+
+@pytest.mark.parametrize("case", _random_bw_cases(16, 2030))
+def test_embedding_random_shapes(gpu, case):
+    """Embedding dot and train gradient over seeded random shapes and vocabularies (a few ids
+    out of range) against float64."""
+    N, n_val, vs, T, d, vocab = case
+    print(f"random embedding case={case}", flush=True)
+    ids = torch.randint(0, vocab, (N, T), generator=gen(170 + T))
+    ids[0, 0] = -1
+    G = randn((N, T, d), 171 + d, 1e-3, torch.bfloat16)
+    idd, Gd = ids.to(gpu), G.to(gpu)
+    dot = _native.ops().embedding_dot(idd, Gd, n_val, vocab, val_start=vs)
+    want = R.embedding_dot_exact(ids.clamp(0, vocab - 1), G * (ids >= 0).unsqueeze(-1), n_val,
+                                 val_start=vs)
+    assert_close(dot.cpu(), want, BF16_TOL, "embedding dot")
+    scale = N / (N - n_val)
+    out = torch.full((vocab, d), float("nan"), dtype=torch.float32, device=gpu)
+    _native.ops().embedding_train_grad(idd, Gd, n_val, scale, out, val_start=vs)
+    g_want, touched = _emb_grad_exact(ids, G, n_val, vs, vocab, scale)
+    got = out.cpu()
+    assert_close(got, g_want, FP32_TOL, "embedding train grad")
+    assert torch.all(got[~touched] == 0)
+
+
+@pytest.mark.parametrize("case", _random_bw_cases(12, 2031))
+def test_kron_projection_random_shapes(gpu, case):
+    """Kronecker projection (Linear layout) over seeded random shapes and ranks (1-80 rows of
+    P on each side) against float64."""
+    B, _, _, T, n_i, n_o = case
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    k_i, k_o = int(torch.randint(1, 81, (1,), generator=g)), int(torch.randint(1, 81, (1,), generator=g))
+    n_o = max(1, n_o % 2048)
+    print(f"random kron case={(B, T, n_i, n_o, k_i, k_o)}", flush=True)
+    A = randn((B, T, n_i), 180 + T, 1.0, torch.bfloat16)
+    G = randn((B, T, n_o), 181 + T, 1e-3, torch.bfloat16)
+    P_i = randn((k_i, n_i), 182, 1.0 / k_i ** 0.5)
+    P_o = randn((k_o, n_o), 183, 1.0 / k_o ** 0.5)
+    out = _native.ops().kron_proj(A.to(gpu), G.to(gpu), P_i.to(gpu), P_o.to(gpu), float(B),
+                                  layout=_native.PROJ_KO_KI)
+    want = R.kron_proj_exact(A.float(), G.float(), P_i.to(torch.bfloat16).float(),
+                             P_o.to(torch.bfloat16).float(), float(B))
+    assert_close(out.cpu(), want, BF16_TOL, "kron")

@@ -79,6 +79,68 @@ def test_gpt2_engine_on_gpu_matches_per_sample_gradients(gpu, precision, tol, al
         assert_close(gr, brute.train_mean(g_tied[name], n_v, N), tol, f"grad {name}")
 
 
+def _random_lm_configs(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda opts: opts[int(torch.randint(0, len(opts), (1,), generator=g))]
+    out = []
+    for _ in range(n):
+        n_head, hd = pick([1, 2, 4]), pick([8, 16])
+        T = pick([3, 7, 12, 24])
+        cfg = LMConfig(n_layer=pick([1, 2]), n_head=n_head, d_model=n_head * hd,
+                       d_mlp=n_head * hd * pick([2, 4]), vocab=pick([20, 57, 120]), n_ctx=T,
+                       rotary=pick([False, True]), tied=pick([False, True]))
+        out.append((cfg, pick([3, 4, 6]), pick([1, 2, 3]), int(torch.randint(0, 1000, (1,),
+                                                                            generator=g))))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_lm_configs(6, 2032))
+def test_random_lm_configs_engine_matches_per_sample_gradients(gpu, case):
+    """Seeded random causal-LM configurations (layers, heads, widths, vocabulary, T, rotary or
+    learned positions, tied or untied head, 1-3 val rows) through the engine in fp32 against
+    float64 per-sample gradients: every parameter's dot (presum layers at n_v = 1, where
+    presum equals the pairwise sum) and every train gradient."""
+    cfg, n_t, n_v, seed = case
+    torch.manual_seed(seed)
+    T, vocab = cfg.n_ctx, cfg.vocab
+    model = CausalLM(cfg)
+    untied = copy.deepcopy(model)
+    if cfg.tied:
+        untied.lm_head.weight = nn.Parameter(model.wte.weight.detach().clone())
+    ref = copy.deepcopy(model).double()
+    untied = untied.double()
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=seed + 1)
+    model = model.to(gpu)
+    print(f"random lm engine cfg={cfg} n_t={n_t} n_v={n_v}", flush=True)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True, precision="fp32")
+    eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+    eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+    model(X.to(gpu), Y.to(gpu)).backward()
+    torch.cuda.synchronize()
+    dots = {n: p.grad_dot_prod.cpu() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    semantics = {n: m.use_ghost_computation for n, m in model.named_modules()
+                 if hasattr(m, "use_ghost_computation")}
+    eng.prepare_gradients()
+    grads = {n: p.grad.cpu() for n, p in model.named_parameters()
+             if p.grad is not None and "dummy_bias" not in n}
+    eng.detach()
+    N = n_t + n_v
+    g_dot = brute.per_sample_grads(untied, X, Y, _lm_loss(T), 1.0 / (N * T))
+    g_grad = brute.per_sample_grads(ref, X, Y, _lm_loss(T), 1.0 / (N * T))
+    checked = 0
+    for name, d in dots.items():
+        layer = name.rsplit(".", 1)[0]
+        if not semantics.get(layer, True) and n_v > 1:
+            continue   # presum: not a function of the per-sample gradients
+        assert_close(d, brute.pairwise_dots(g_dot[name], n_v), FP32_TOL, f"dot {name}")
+        checked += 1
+    assert checked > 0
+    assert grads
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g_grad[name], n_v, N), FP32_TOL, f"grad {name}")
+
+
 def test_mlp_engine_on_gpu_ten_steps(gpu):
     """configs[0] in small: 10 SGD steps, per-step aggregated dots vs brute force."""
     torch.manual_seed(14)

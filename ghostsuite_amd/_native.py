@@ -78,6 +78,9 @@ _SIGNATURES = {
     "gs_linear_dot_train_grad_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I]),
     "gs_linear_dot_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
                                       _P, _I, _F, _P, _P, _I, _F, _P, _SZ, _P]),
+    "gs_conv1d_dot_train_grad_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I]),
+    "gs_conv1d_dot_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                                      _P, _I, _F, _P, _P, _I, _F, _P, _SZ, _P]),
     "gs_linear_train_grad_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64]),
     "gs_linear_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I,
                                   _I, _P, _SZ, _P]),
@@ -275,9 +278,11 @@ class HipOps:
                               grad_scale: Optional[float] = None,
                               grad_dtype: Optional[torch.dtype] = None, bias: bool = False,
                               bias_grad_scale: Optional[float] = None,
-                              bias_grad_dtype: Optional[torch.dtype] = None):
+                              bias_grad_dtype: Optional[torch.dtype] = None,
+                              conv1d: bool = False):
         """Weight dots and weight train gradient in one pass over the train rows
-        (gs_linear_dot_train_grad), with the bias dots and bias train gradient when `bias`.
+        (gs_linear_dot_train_grad), with the bias dots and bias train gradient when `bias`;
+        with conv1d the HF Conv1D form (gs_conv1d_dot_train_grad: train gradient [d_in, d_out]).
         Returns (dot, grad, bias_dot, bias_grad), entries not asked for None; None for the
         cases the kernels do not take (non-bf16, unaligned, T not a multiple of 64, feature
         counts not multiples of 8)."""
@@ -294,8 +299,9 @@ class HipOps:
         vs = N - n_val if val_start is None else int(val_start)
         dt = _gs_dtype(A)
         lib = load_library()
-        ws_bytes = lib.gs_linear_dot_train_grad_workspace(dt, N, n_val, T, d_in, d_out,
-                                                          semantics, 1 if bias else 0)
+        name = "gs_conv1d_dot_train_grad" if conv1d else "gs_linear_dot_train_grad"
+        ws_bytes = getattr(lib, name + "_workspace")(dt, N, n_val, T, d_in, d_out, semantics,
+                                                     1 if bias else 0)
         if ws_bytes == 0:
             return None
         ws = _workspace(ws_bytes, dev)
@@ -303,12 +309,13 @@ class HipOps:
         dot = torch.empty(n_t, dtype=torch.float32, device=dev)
         grad = None
         if grad_scale is not None:
-            grad = torch.empty((d_out, d_in), dtype=grad_dtype or A.dtype, device=dev)
+            grad = torch.empty((d_in, d_out) if conv1d else (d_out, d_in),
+                               dtype=grad_dtype or A.dtype, device=dev)
         bdot = torch.empty(n_t, dtype=torch.float32, device=dev) if bias else None
         bgrad = None
         if bias and bias_grad_scale is not None:
             bgrad = torch.empty(d_out, dtype=bias_grad_dtype or A.dtype, device=dev)
-        rc = lib.gs_linear_dot_train_grad(
+        rc = getattr(lib, name)(
             A.data_ptr(), G.data_ptr(), dt, N, n_val, vs, T, d_in, d_out, semantics,
             dot.data_ptr(), _ptr(grad), _gs_dtype(grad) if grad is not None else DTYPE_BF16,
             float(grad_scale or 0.0), _ptr(bdot), _ptr(bgrad),
@@ -316,7 +323,7 @@ class HipOps:
             ws.data_ptr(), ws_bytes, _stream(dev))
         if rc == ERR_UNSUPPORTED:
             return None
-        _check(rc, "gs_linear_dot_train_grad")
+        _check(rc, name)
         return dot, grad, bdot, bgrad
 
     def linear_train_grad(self, A: torch.Tensor, G: torch.Tensor, n_val: int, scale: float, *,

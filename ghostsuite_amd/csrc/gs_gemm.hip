@@ -1536,15 +1536,16 @@ __global__ void presum_rows_kernel(const E* __restrict__ in, int64_t ld, RowMap 
 
 // out_z[t][f] = sum over the nseg val rows of in_z[row(s, t)][f] for z = 0, 1 (blockIdx.z):
 // fp32 sums rounded once.  A block takes PS_F * 8 features (16 bytes per thread) of PS_T
-// positions, PS_P position lanes per feature chunk; with colsum the z = 1 blocks also write
-// the fp32 sums over their positions, one row per block row: colsum [ceil(T / PS_T)][d[1]]
-// (the val rows' column sums, combined in a fixed order).  Rows 16-byte aligned, d % 8 == 0.
+// positions, PS_P position lanes per feature chunk; with colsum the z = 1 blocks (z = 0 with
+// cs_in0) also write the fp32 sums over their positions, one row per block row: colsum
+// [ceil(T / PS_T)][d[z]] (the val rows' column sums, combined in a fixed order).  Rows 16-byte aligned, d % 8 == 0.
 constexpr int PS_F = 32, PS_P = 8, PS_T = 32;
 struct PresumPair {
   const uint16_t* in[2];
   uint16_t* out[2];
   int64_t d[2];
   float* colsum;
+  int cs_in0;  // the column sums are of in[0] instead of in[1]
 };
 __global__ void __launch_bounds__(256) presum_rows_vec_kernel(PresumPair pp, RowMap map) {
   static_assert(PS_F * PS_P == 256, "block shape");
@@ -1555,7 +1556,7 @@ __global__ void __launch_bounds__(256) presum_rows_vec_kernel(PresumPair pp, Row
   const int64_t f = (static_cast<int64_t>(blockIdx.x) * PS_F + fc) * 8;
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * PS_T;
   const int64_t t1 = t0 + PS_T < map.seglen ? t0 + PS_T : map.seglen;
-  const bool cs_on = z == 1 && pp.colsum != nullptr;  // block-uniform
+  const bool cs_on = z == (pp.cs_in0 ? 0 : 1) && pp.colsum != nullptr;  // block-uniform
   float cs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (f < d) {
     for (int64_t t = t0 + pl; t < t1; t += PS_P) {
@@ -2035,14 +2036,15 @@ struct TgParams {
   const uint16_t* Vt;   // V^T: [N][M] bf16
   int64_t T, n_t;       // k-rows per sample (a multiple of the stage height), train samples
   float* pdot;          // [m_tiles * n_tiles][NW][2 slots][n_t] wave shares of the weight dots
-  float* csum;          // with CS: [n_t][2 T / stage height][M] column sums of L, two rows
-                        // (halves of the stage's k-rows) per stage
-  const float* vb;      // with CS: [M] the val rows' column sums of L (G)
-  float* pbias;         // with CS: [n_t][T / stage height][m_tiles][WM] bias-dot shares:
-                        //   a stage's column sums of one wave's columns dotted with vb
+  float* csum;          // with CS: [n_t][2 T / stage height][M] column sums of L (CS 1; of R,
+                        // [..][N], with CS 2), two rows (halves of the stage's k-rows) per stage
+  const float* vb;      // with CS: [M] ([N]) the val rows' column sums of the same side
+  float* pbias;         // with CS: [n_t][T / stage height][m_tiles][WM] ([..][n_tiles][WN])
+                        //   bias-dot shares: a stage's column sums of one wave's columns
+                        //   dotted with vb
 };
 
-template <class C, class D, bool CS>
+template <class C, class D, int CS>
 __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) {
   const TnParams& p = q.tn;
   __shared__ __attribute__((aligned(16))) unsigned char lds[D::STAGES * D::STAGE_BYTES];
@@ -2083,13 +2085,19 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   // the MFMAs used, still in registers (the two waves wm = 0, 1 cover the m-tile's columns
   // once), then stores the sums in the rows of (stage within its sample) of that sample:
   // every (sample, stage, column) is written once.
-  const int cs_every = static_cast<int>(p.n_tiles) * C::WN;
-  int cs_left = static_cast<int>(nt) * C::WN + wn;  // stages until this wave's next sum
-  float vbr[C::MI];  // vb at this lane's columns (the bias-dot shares)
+  // CS 2 takes the R tile's columns instead (A's train rows, with the operands swapped for a
+  // Conv1D layer: its bias terms), the waves along M sharing them.
+  constexpr int F = CS == 2 ? C::NI : C::MI, W = CS == 2 ? C::WM : C::WN;
+  const int64_t ext = CS == 2 ? p.N : p.M;  // columns of the summed side
+  const int cs_every = static_cast<int>(CS == 2 ? p.m_tiles : p.n_tiles) * W;
+  int cs_left = static_cast<int>(CS == 2 ? mt : nt) * W + (CS == 2 ? wm : wn);
+  const int64_t col0 = (CS == 2 ? nt * C::BN + wn * 32 * C::NI : mt * C::BM + wm * 32 * C::MI) +
+                       (lane & 31);
+  float vbr[F];  // vb at this lane's columns (the bias-dot shares)
 #pragma unroll
-  for (int i = 0; i < C::MI; ++i) {
-    const int64_t col = mt * C::BM + wm * 32 * C::MI + i * 32 + (lane & 31);
-    vbr[i] = CS && col < p.M ? q.vb[col] : 0.f;
+  for (int i = 0; i < F; ++i) {
+    const int64_t col = col0 + i * 32;
+    vbr[i] = CS && col < ext ? q.vb[col] : 0.f;
   }
   const int64_t tile = mt * p.n_tiles + nt;
   // Stages left in the current sample (wave-uniform; no division in the stage loop).  A
@@ -2125,25 +2133,30 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
     }
     s_prev = d;
   };
-  bf16x8_t keep[D::KSTEPS][C::MI];  // with CS: the stage's L fragments, kept by tn_compute
+  bf16x8_t keep[D::KSTEPS][F];  // with CS: the stage's L (R) fragments, kept by tn_compute
   auto hook = [&](int, const unsigned char*) {
-    if constexpr (CS) {
+    if constexpr (CS != 0) {
       if (cs_left == 0) {
         cs_left = cs_every;
-        float rc[C::MI];
-        tn_fsum<D, C::MI>(keep, rc);
+        float rc[F];
+        tn_fsum<D, F>(keep, rc);
         const int64_t row = sample * sps + (sps - left);  // stage within its sample
         // lanes l and l + 32 hold halves of the same column: rows 2 s and 2 s + 1
-        float* dst = q.csum + (2 * row + (lane >> 5)) * p.M;
+        float* dst = q.csum + (2 * row + (lane >> 5)) * ext;
         float bd = 0.f;
 #pragma unroll
-        for (int i = 0; i < C::MI; ++i) {
-          const int64_t col = mt * C::BM + wm * 32 * C::MI + i * 32 + (lane & 31);
-          if (col < p.M) dst[col] = rc[i];
+        for (int i = 0; i < F; ++i) {
+          const int64_t col = col0 + i * 32;
+          if (col < ext) dst[col] = rc[i];
           bd += rc[i] * vbr[i];
         }
         bd = wave_sum_dpp(bd);
-        if (lane == 0) q.pbias[(row * p.m_tiles + mt) * C::WM + wm] = bd;
+        if (lane == 0) {
+          if constexpr (CS == 2)
+            q.pbias[(row * p.n_tiles + nt) * C::WN + wn] = bd;
+          else
+            q.pbias[(row * p.m_tiles + mt) * C::WM + wm] = bd;
+        }
       }
       --cs_left;
     }
@@ -2153,9 +2166,9 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
     started = true;
     ++sample;
   };
-  if constexpr (CS) {
+  if constexpr (CS != 0) {
     auto cmp = [&](const unsigned char* stage, f32x16_t (&a)[C::MI][C::NI]) {
-      tn_compute<C, D, 1>(stage, a, keep);
+      tn_compute<C, D, CS>(stage, a, keep);
     };
     mainloop_tn<C, D>(p, mt, nt, k_begin, k_end, lds, acc, hook, cmp);
   } else {
@@ -3286,6 +3299,8 @@ struct TgPlan {
   int64_t n_val, n_t, K;     // val and train samples, train k-rows
   int64_t kper, sp;          // k-rows per split (at least one sample), splits
   int64_t m_tiles, n_tiles, bias;  // bias: the bias terms are wanted
+  int bias_a;                // the bias terms are A's column sums (d_in wide), not G's
+  int64_t bias_d;            // features of the bias side
 };
 bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
            int semantics) {
@@ -3295,8 +3310,10 @@ bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t
   return tn_ok(nullptr, d_out, nullptr, d_in, N * T, d_out, d_in);
 }
 TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, int semantics,
-               bool bias) {
+               bool bias, bool bias_a = false) {
   TgPlan t{};
+  t.bias_a = bias_a ? 1 : 0;
+  t.bias_d = bias_a ? d_in : d_out;
   t.presum = semantics == GS_SEM_PRESUM ? 1 : 0;
   t.vk = (t.presum ? 1 : n_val) * T;
   t.n_val = n_val;
@@ -3327,14 +3344,29 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
   // Val column sums of G: the V GEMM's own partials for the pairwise semantics (its operands
   // are the val rows as they lie); for the presum, whose V operands are rounded to bf16, the
   // presum kernel's fp32 sums.
-  const int64_t vp_rows = t.presum ? presum_rows(T) : tn_vsum_rows(t.vk, d_in, d_out, true);
-  b.vp = t.bias ? c.template take<float>(vp_rows * d_out) : nullptr;
+  const int64_t vp_rows =
+      t.presum ? presum_rows(T) : tn_vsum_rows(t.vk, d_in, d_out, !t.bias_a);
+  b.vp = t.bias ? c.template take<float>(vp_rows * t.bias_d) : nullptr;
   b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2 * t.n_t);
-  b.csum = t.bias ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * d_out) : nullptr;
-  b.pbias = t.bias ? c.template take<float>(t.n_t * (T / TnD::KB) * t.m_tiles * TnC::WM)
-                     : nullptr;
+  b.csum = t.bias ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * t.bias_d) : nullptr;
+  const int64_t bw = t.bias_a ? t.n_tiles * TnC::WN : t.m_tiles * TnC::WM;
+  b.pbias = t.bias ? c.template take<float>(t.n_t * (T / TnD::KB) * bw) : nullptr;
   b.tgpart = c.template take<float>(t.sp * d_out * d_in);
   return b;
+}
+}  // namespace
+}  // namespace gs
+
+namespace gs {
+namespace {
+size_t tg_workspace(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
+                    int semantics, bool bias, bool bias_a) {
+  if (N <= 0 || T <= 0 || d_in <= 0 || d_out <= 0) return 0;
+  if (!tg_ok(dtype, N, n_val, T, d_in, d_out, semantics)) return 0;
+  const TgPlan t = plan_tg(N, n_val, T, d_in, d_out, semantics, bias, bias_a);
+  Sizer sz;
+  carve_tg(sz, t, T, d_in, d_out);
+  return sz.used + 256;
 }
 }  // namespace
 }  // namespace gs
@@ -3342,44 +3374,50 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
 extern "C" size_t gs_linear_dot_train_grad_workspace(int dtype, int64_t N, int64_t n_val,
                                                      int64_t T, int64_t d_in, int64_t d_out,
                                                      int semantics, int with_bias) {
-  if (N <= 0 || T <= 0 || d_in <= 0 || d_out <= 0) return 0;
-  if (!tg_ok(dtype, N, n_val, T, d_in, d_out, semantics)) return 0;
-  const TgPlan t = plan_tg(N, n_val, T, d_in, d_out, semantics, with_bias != 0);
-  Sizer sz;
-  carve_tg(sz, t, T, d_in, d_out);
-  return sz.used + 256;
+  return tg_workspace(dtype, N, n_val, T, d_in, d_out, semantics, with_bias != 0, false);
 }
 
-extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype, int64_t N,
-                                        int64_t n_val, int64_t val_start, int64_t T,
-                                        int64_t d_in, int64_t d_out, int semantics,
-                                        float* out_dot, void* out_grad, int grad_dtype,
-                                        float grad_scale, float* out_bias_dot,
-                                        void* out_bias_grad, int bias_grad_dtype,
-                                        float bias_grad_scale, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+// The HF Conv1D layer (weight [d_in, d_out]) through the same pass with A and G swapped: the
+// dots are unchanged (<G_i^T A_i, V> = <A_i^T G_i, V^T>), the train gradient comes out as
+// sum A_i^T G_i, and the bias terms are the column sums of the swapped-in first operand (G).
+extern "C" size_t gs_conv1d_dot_train_grad_workspace(int dtype, int64_t N, int64_t n_val,
+                                                     int64_t T, int64_t d_in, int64_t d_out,
+                                                     int semantics, int with_bias) {
+  return tg_workspace(dtype, N, n_val, T, d_out, d_in, semantics, with_bias != 0, true);
+}
+
+namespace gs {
+namespace {
+// The fused pass (gs_linear_dot_train_grad); bias_a: the bias terms are A's column sums.
+int dot_train_grad(bool bias_a, const void* A, const void* G, int dtype, int64_t N,
+                   int64_t n_val, int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                   int semantics, float* out_dot, void* out_grad, int grad_dtype,
+                   float grad_scale, float* out_bias_dot, void* out_bias_grad,
+                   int bias_grad_dtype, float bias_grad_scale, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  const std::string who = bias_a ? "gs_conv1d_dot_train_grad" : "gs_linear_dot_train_grad";
   if (N <= 0 || T <= 0 || d_in <= 0 || d_out <= 0 || n_val <= 0 || n_val >= N)
-    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: invalid shape");
+    return fail(GS_ERR_INVALID, who + ": invalid shape");
   if (val_start < 0 || val_start + n_val > N)
-    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: val block outside the batch");
+    return fail(GS_ERR_INVALID, who + ": val block outside the batch");
   if (A == nullptr || G == nullptr || out_dot == nullptr)
-    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: null pointer");
+    return fail(GS_ERR_INVALID, who + ": null pointer");
   if (semantics != GS_SEM_PAIRWISE_SUM && semantics != GS_SEM_PRESUM)
-    return fail(GS_ERR_INVALID, "gs_linear_dot_train_grad: invalid semantics");
+    return fail(GS_ERR_INVALID, who + ": invalid semantics");
   if ((out_grad != nullptr && grad_dtype != GS_DTYPE_BF16 && grad_dtype != GS_DTYPE_F32) ||
       (out_bias_grad != nullptr && bias_grad_dtype != GS_DTYPE_BF16 &&
        bias_grad_dtype != GS_DTYPE_F32))
-    return fail(GS_ERR_DTYPE, "gs_linear_dot_train_grad: gradient dtypes must be bf16 or fp32");
+    return fail(GS_ERR_DTYPE, who + ": gradient dtypes must be bf16 or fp32");
   if (!tg_ok(dtype, N, n_val, T, d_in, d_out, semantics) || !aligned16(A) || !aligned16(G))
     return fail(GS_ERR_UNSUPPORTED,
-                "gs_linear_dot_train_grad: needs bf16, 16-byte aligned operands below 2 GiB, "
+                who + ": needs bf16, 16-byte aligned operands below 2 GiB, "
                 "T a multiple of 64 and feature counts that are multiples of 8");
   const bool bias = out_bias_dot != nullptr || out_bias_grad != nullptr;
-  const TgPlan t = plan_tg(N, n_val, T, d_in, d_out, semantics, bias);
+  const TgPlan t = plan_tg(N, n_val, T, d_in, d_out, semantics, bias, bias_a);
   if (workspace == nullptr ||
-      workspace_bytes < gs_linear_dot_train_grad_workspace(dtype, N, n_val, T, d_in, d_out,
-                                                           semantics, bias ? 1 : 0) - 256)
-    return fail(GS_ERR_WORKSPACE, "gs_linear_dot_train_grad: workspace too small");
+      workspace_bytes < tg_workspace(dtype, N, n_val, T, d_in, d_out, semantics, bias, bias_a) -
+                            256)
+    return fail(GS_ERR_WORKSPACE, who + ": workspace too small");
   Carver cv(workspace, workspace_bytes);
   const TgBufs b = carve_tg(cv, t, T, d_in, d_out);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -3402,6 +3440,7 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
     pp.d[0] = d_in;
     pp.d[1] = d_out;
     pp.colsum = b.vp;
+    pp.cs_in0 = t.bias_a;
     int rc = launch_presum(pp, val_rows(n_val, val_start, T), s);
     if (rc) return rc;
     La = b.abar;
@@ -3412,7 +3451,7 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
     }
   }
   int rc = launch_tn(La, d_in, Lg, d_out, t.vk, d_in, d_out, b.V, b.vpart, s,
-                     t.presum ? nullptr : b.vp, true, vo);
+                     t.presum ? nullptr : b.vp, !t.bias_a, vo);
   if (rc) return rc;
   // The train rows: dots at every sample boundary, train-gradient partials per split.
   TgParams q{};
@@ -3443,34 +3482,66 @@ extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype,
   q.pbias = b.pbias;
   const int64_t items = t.m_tiles * t.n_tiles * t.sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-  if (q.csum != nullptr)
-    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, true>), dim3(static_cast<unsigned>(items)),
+  if (q.csum == nullptr)
+    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 0>), dim3(static_cast<unsigned>(items)),
+                       dim3(TnC::NT), 0, s, q);
+  else if (!t.bias_a)
+    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 1>), dim3(static_cast<unsigned>(items)),
                        dim3(TnC::NT), 0, s, q);
   else
-    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, false>), dim3(static_cast<unsigned>(items)),
+    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 2>), dim3(static_cast<unsigned>(items)),
                        dim3(TnC::NT), 0, s, q);
   rc = check_launch("tgdot_kernel");
   if (rc) return rc;
   // One launch: the dots, the bias train gradient and the train-gradient reduction.
   const int64_t shares = t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2;
   const int64_t sps = T / TnD::KB;
-  const int64_t bshares = sps * t.m_tiles * TnC::WM;
+  const int64_t bshares = sps * (t.bias_a ? t.n_tiles * TnC::WN : t.m_tiles * TnC::WM);
   const float* pbias = out_bias_dot != nullptr ? b.pbias : nullptr;
-  const int64_t gblocks = out_bias_grad != nullptr ? ceil_div(d_out, int64_t{FINISH_GF}) : 0;
+  const int64_t gblocks =
+      out_bias_grad != nullptr ? ceil_div(t.bias_d, int64_t{FINISH_GF}) : 0;
   const int64_t count = out_grad != nullptr ? d_out * d_in : 0;  // a multiple of 8
   const dim3 grid(static_cast<unsigned>(t.n_t + gblocks + ceil_div(count / 4, int64_t{256})));
   const int gf32 = grad_dtype == GS_DTYPE_F32 ? 1 : 0;
   if (bias_grad_dtype == GS_DTYPE_F32)
     hipLaunchKernelGGL(tgdot_finish_kernel<float>, grid, dim3(256), 0, s, b.pdot, shares, t.n_t,
-                       pbias, bshares, b.csum, 2 * sps, d_out, out_dot, out_bias_dot,
+                       pbias, bshares, b.csum, 2 * sps, t.bias_d, out_dot, out_bias_dot,
                        static_cast<float*>(out_bias_grad), bias_grad_scale, gblocks, b.tgpart,
                        count, static_cast<int>(t.sp), out_grad, grad_scale, gf32);
   else
     hipLaunchKernelGGL(tgdot_finish_kernel<uint16_t>, grid, dim3(256), 0, s, b.pdot, shares,
-                       t.n_t, pbias, bshares, b.csum, 2 * sps, d_out, out_dot, out_bias_dot,
+                       t.n_t, pbias, bshares, b.csum, 2 * sps, t.bias_d, out_dot, out_bias_dot,
                        static_cast<uint16_t*>(out_bias_grad), bias_grad_scale, gblocks,
                        b.tgpart, count, static_cast<int>(t.sp), out_grad, grad_scale, gf32);
   return check_launch("tgdot_finish_kernel");
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_linear_dot_train_grad(const void* A, const void* G, int dtype, int64_t N,
+                                        int64_t n_val, int64_t val_start, int64_t T,
+                                        int64_t d_in, int64_t d_out, int semantics,
+                                        float* out_dot, void* out_grad, int grad_dtype,
+                                        float grad_scale, float* out_bias_dot,
+                                        void* out_bias_grad, int bias_grad_dtype,
+                                        float bias_grad_scale, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return dot_train_grad(false, A, G, dtype, N, n_val, val_start, T, d_in, d_out, semantics,
+                        out_dot, out_grad, grad_dtype, grad_scale, out_bias_dot, out_bias_grad,
+                        bias_grad_dtype, bias_grad_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gs_conv1d_dot_train_grad(const void* A, const void* G, int dtype, int64_t N,
+                                        int64_t n_val, int64_t val_start, int64_t T,
+                                        int64_t d_in, int64_t d_out, int semantics,
+                                        float* out_dot, void* out_grad, int grad_dtype,
+                                        float grad_scale, float* out_bias_dot,
+                                        void* out_bias_grad, int bias_grad_dtype,
+                                        float bias_grad_scale, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return dot_train_grad(true, G, A, dtype, N, n_val, val_start, T, d_out, d_in, semantics,
+                        out_dot, out_grad, grad_dtype, grad_scale, out_bias_dot, out_bias_grad,
+                        bias_grad_dtype, bias_grad_scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t gs_linear_rowdot_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,

@@ -195,12 +195,12 @@ def _fused_dot_train_grad(layer: nn.Module, A: torch.Tensor, B: torch.Tensor,
     for bf16 layers on the val-gradient algorithm whose weight trains; the train gradients
     are parked for _apply_train_grad.  Returns False when the other paths must run.
 
-    With ``conv1d`` (HF Conv1D, weight [d_in, d_out]) the operands go in swapped: the dot
-    <G_i^T A_i, V> equals <A_i^T G_i, V^T>, and the train gradient comes out as the sum of
-    A_i^T G_i, the Conv1D layout.  The bias is then left to its own pass (the fused pass sums
-    the columns of its second operand, here the activations)."""
+    With ``conv1d`` (HF Conv1D, weight [d_in, d_out]) the Conv1D entry point runs the same
+    pass with the operands swapped: the dot <G_i^T A_i, V> equals <A_i^T G_i, V^T>, the train
+    gradient comes out as the sum of A_i^T G_i (the Conv1D layout), and the bias terms come
+    from the column sums of G as for a Linear layer."""
     scale = getattr(layer, "_gs_bias_grad_scale", None)
-    bias = layer.bias is not None and not conv1d
+    bias = layer.bias is not None
     if scale is None or dtype != torch.bfloat16 or A.dtype != torch.bfloat16 or \
             (pairwise and options["store_pairs"]) or \
             not getattr(layer.weight, "initially_requires_grad", False) or \
@@ -208,16 +208,16 @@ def _fused_dot_train_grad(layer: nn.Module, A: torch.Tensor, B: torch.Tensor,
                        not getattr(layer.bias, "initially_requires_grad", False))):
         return False
     Bc = B.to(dtype) if B.dtype != dtype else B
-    L, R = (Bc, A) if conv1d else (A, Bc)
-    N, d_in, d_out = L.shape[0], L.shape[-1], R.shape[-1]
-    T = L.numel() // (N * d_in)
+    N, d_in, d_out = A.shape[0], A.shape[-1], Bc.shape[-1]
+    T = A.numel() // (N * d_in)
     sem = _native.SEM_PAIRWISE_SUM if pairwise else _native.SEM_PRESUM
     if ops().linear_algo(dtype, N, val_batch_size, T, d_in, d_out, sem,
                          _ALGOS[options["linear_algo"]], False) != _native.ALGO_VALGRAD:
         return False
-    res = ops().linear_dot_train_grad(L, R, val_batch_size, semantics=sem, grad_scale=scale,
+    res = ops().linear_dot_train_grad(A, Bc, val_batch_size, semantics=sem, grad_scale=scale,
                                       grad_dtype=A.dtype, bias=bias, bias_grad_scale=scale,
-                                      bias_grad_dtype=layer.bias.dtype if bias else None)
+                                      bias_grad_dtype=layer.bias.dtype if bias else None,
+                                      conv1d=conv1d)
     if res is None:
         return False
     dot, grad, bias_dot, bias_grad = res
@@ -450,8 +450,6 @@ def _compute_Conv1D_dot_product(layer, A: torch.Tensor, B: torch.Tensor, val_bat
                          "Extending this to 4D or higher requires additional handling.")
     dt = torch.float32 if options["precision"] == "fp32" else torch.bfloat16
     if _fused_dot_train_grad(layer, A, B, val_batch_size, False, dt, conv1d=True):
-        if layer.bias is not None:
-            _bias_dot_and_grad(layer, B, val_batch_size, dt)
         return
     if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, False, dt, dt):
         return

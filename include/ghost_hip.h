@@ -153,6 +153,23 @@ int gs_linear_dot_train_grad(const void* A, const void* G, int dtype, int64_t N,
                              int bias_grad_dtype, float bias_grad_scale, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* The same pass for an HF Conv1D layer (weight [d_in, d_out]): A [N, T, d_in], G [N, T, d_out]
+ * as for gs_linear_dot_train_grad, the same out_dot, out_bias_dot and out_bias_grad, and
+ *   out_grad = grad_scale * sum over the train rows of a g^T, [d_in, d_out]
+ * (the operands go into the pass swapped, and the bias terms are taken from the other side).
+ * Reference: _compute_Conv1D_dot_product (supported_layers_grad_samplers_dotprod.py:369-471)
+ * and _compute_Conv1D_train_grad (:474-506) with _compute_train_grad_bias
+ * (autograd_grad_sample_dotprod.py:199-222). */
+size_t gs_conv1d_dot_train_grad_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
+                                          int64_t d_in, int64_t d_out, int semantics,
+                                          int with_bias);
+int gs_conv1d_dot_train_grad(const void* A, const void* G, int dtype, int64_t N, int64_t n_val,
+                             int64_t val_start, int64_t T, int64_t d_in, int64_t d_out,
+                             int semantics, float* out_dot, void* out_grad, int grad_dtype,
+                             float grad_scale, float* out_bias_dot, void* out_bias_grad,
+                             int bias_grad_dtype, float bias_grad_scale, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Train gradient of a Linear / HF Conv1D weight from the train rows (the val block
  * [val_start, val_start + n_val) skipped), fp32 accumulation, scale applied before the one
  * rounding to out_dtype (GS_DTYPE_BF16 or GS_DTYPE_F32):

@@ -457,9 +457,10 @@ def test_linear_dot_train_grad_declines(gpu):
     (20, 4, 1024, 768, 3072),    # GPT-2-small mlp.c_fc
 ])
 def test_conv1d_sampler_fused_dot_and_train_grad(gpu, case):
-    """HF Conv1D (weight [d_in, d_out]) takes the fused pass with its operands swapped: the
-    presum dots and the [d_in, d_out] train gradient against float64 closed forms, the bias
-    dot and train gradient from the bias pass, and the same dots as the unfused path."""
+    """HF Conv1D (weight [d_in, d_out]) takes the fused pass through its own entry point (the
+    operands swapped inside): the presum dots, the [d_in, d_out] train gradient and the bias
+    dot and train gradient against float64 closed forms, and the same dots as the unfused
+    path."""
     transformers = pytest.importorskip("transformers")
     from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
     N, n_val, T, d_in, d_out = case
@@ -546,6 +547,17 @@ def test_linear_dot_train_grad_random_shapes(gpu, case):
     assert sw is not None
     assert_close(sw[0].cpu(), want_dot, BF16_TOL, "swapped dot")
     assert_close(sw[1].cpu(), want_grad.t(), FP32_TOL, "swapped train grad")
+    # the Conv1D entry point: same dots, [d_in, d_out] train gradient, G's bias terms
+    cv = ops.linear_dot_train_grad(Ad, Gd, n_val, val_start=vs, semantics=semantics,
+                                   grad_scale=1.0 / n_t, grad_dtype=torch.float32, bias=bias,
+                                   bias_grad_scale=1.0 / n_t, bias_grad_dtype=torch.float32,
+                                   conv1d=True)
+    assert cv is not None
+    assert_close(cv[0].cpu(), want_dot, BF16_TOL, "conv1d dot")
+    assert_close(cv[1].cpu(), want_grad.t(), FP32_TOL, "conv1d train grad")
+    if bias:
+        assert_close(cv[2].cpu(), R.bias_dot_exact(G, n_val, vs), BF16_TOL, "conv1d bias dot")
+        assert_close(cv[3].cpu(), tr.sum((0, 1)) / n_t, FP32_TOL, "conv1d bias train grad")
 
 
 def _random_dot_cases(n, seed):

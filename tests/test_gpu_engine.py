@@ -268,6 +268,91 @@ def test_hf_conv1d_bf16_fused_path(gpu, n_v, monkeypatch):
             assert_close(grads[name], want, BF16_TOL, f"conv1d grad {name}")
 
 
+def test_hf_gpt2_model_through_the_engine(gpu):
+    """The reference LM example's model family: a tiny Hugging Face GPT2LMHeadModel (Conv1D
+    attention and MLP layers, LayerNorms, wte / wpe, tied lm_head), per-sample position ids
+    passed explicitly, fp32, one val row (presum equals the pairwise sum), against float64
+    per-sample gradients: every parameter's dot and train gradient."""
+    transformers = pytest.importorskip("transformers")
+    torch.manual_seed(41)
+    cfg = transformers.GPT2Config(n_layer=2, n_embd=32, n_head=2, vocab_size=50, n_positions=16,
+                                  resid_pdrop=0.0, embd_pdrop=0.0, attn_pdrop=0.0,
+                                  bos_token_id=0, eos_token_id=0)
+    model = transformers.GPT2LMHeadModel(cfg).eval()
+    untied = copy.deepcopy(model)
+    untied.lm_head.weight = nn.Parameter(model.transformer.wte.weight.detach().clone())
+    untied = untied.double()
+    ref = copy.deepcopy(model).double()
+    N, n_v, T = 5, 1, 12
+    X = torch.randint(0, 50, (N, T), generator=gen(42))
+    pos = torch.arange(T).expand(N, T).contiguous()
+
+    def sample_loss(m, x, y):   # the batch loss is the mean of the per-sample token means
+        return m(input_ids=x, position_ids=torch.arange(T)[None], labels=x).loss
+
+    model = model.to(gpu)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False, precision="fp32")
+    eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+    print("hf gpt2 engine", flush=True)
+    model(input_ids=X.to(gpu), position_ids=pos.to(gpu), labels=X.to(gpu)).loss.backward()
+    torch.cuda.synchronize()
+    dots = {n: p.grad_dot_prod.cpu() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    eng.prepare_gradients()
+    grads = {n: p.grad.cpu() for n, p in model.named_parameters() if p.grad is not None}
+    eng.detach()
+    g_dot = brute.per_sample_grads(untied, X, X, sample_loss, 1.0 / N)
+    g_grad = brute.per_sample_grads(ref, X, X, sample_loss, 1.0 / N)
+    assert any(".attn.c_attn." in n for n in dots) and "transformer.wpe.weight" in dots
+    for name, d in dots.items():
+        assert_close(d, brute.pairwise_dots(g_dot[name], n_v), FP32_TOL, f"dot {name}")
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g_grad[name], n_v, N), FP32_TOL, f"grad {name}")
+
+
+def test_hf_gpt2_bf16_conv1d_layers_take_the_fused_pass(gpu, monkeypatch):
+    """A bf16 Hugging Face GPT2LMHeadModel at tile-aligned sizes: its four Conv1D layers take
+    the fused dot + train-gradient pass (gs_conv1d_dot_train_grad, bias included), and the
+    dots and gradients equal those of the separate passes on the same run."""
+    transformers = pytest.importorskip("transformers")
+    torch.manual_seed(43)
+    cfg = transformers.GPT2Config(n_layer=1, n_embd=64, n_head=2, vocab_size=50, n_positions=64,
+                                  resid_pdrop=0.0, embd_pdrop=0.0, attn_pdrop=0.0,
+                                  bos_token_id=0, eos_token_id=0)
+    model = transformers.GPT2LMHeadModel(cfg).eval().to(gpu, torch.bfloat16)
+    N, n_v, T = 6, 2, 64
+    X = torch.randint(0, 50, (N, T), generator=gen(44)).to(gpu)
+    pos = torch.arange(T, device=gpu).expand(N, T).contiguous()
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False, record_algorithms=True)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+
+    def run():
+        S.ALGO_LOG.clear()
+        eng.attach(opt)
+        model(input_ids=X, position_ids=pos, labels=X).loss.backward()
+        torch.cuda.synchronize()
+        dots = {n: p.grad_dot_prod.float().cpu() for n, p in model.named_parameters()
+                if hasattr(p, "grad_dot_prod")}
+        eng.prepare_gradients()
+        grads = {n: p.grad.float().cpu() for n, p in model.named_parameters()
+                 if p.grad is not None}
+        eng.clear_gradients()
+        eng.detach()
+        return dots, grads, dict(S.ALGO_LOG)
+
+    print("hf gpt2 bf16 fused", flush=True)
+    dots, grads, log = run()
+    fused = sorted(k for k, v in log.items() if v[1] == "valgrad+train_grad")
+    assert fused == ["transformer.h.0.attn.c_attn", "transformer.h.0.attn.c_proj",
+                     "transformer.h.0.mlp.c_fc", "transformer.h.0.mlp.c_proj"], log
+    monkeypatch.setattr(S, "_fused_dot_train_grad", lambda *a, **k: False)
+    dots2, grads2, _ = run()
+    for name in dots:
+        assert_close(dots[name], dots2[name], 1e-2, f"fused vs separate dot {name}")
+    for name in grads:
+        assert_close(grads[name], grads2[name], 1e-2, f"fused vs separate grad {name}")
+
+
 def test_gradproj_engine_on_gpu_naive_check(gpu, tmp_path):
     torch.manual_seed(20)
     model = nn.Sequential(nn.Linear(10, 20), nn.ReLU(), nn.Linear(20, 5)).to(gpu)

@@ -115,7 +115,8 @@ class TimedOps:
         dot = 2.0 * (nv * T + (N - n_val) * T) * d_in * d_out
         grad = 2.0 * (N - n_val) * T * d_in * d_out if k.get("grad_scale") is not None else 0.0
         tag = "+bias" if k.get("bias") else ""
-        out = self._run(f"linear_valgrad{tag}+train_grad[{d_in}x{d_out}]",
+        kind = "conv1d" if k.get("conv1d") else "linear"
+        out = self._run(f"{kind}_valgrad{tag}+train_grad[{d_in}x{d_out}]",
                         ("mfma", dot + grad, dot),
                         self.inner.linear_dot_train_grad, A, G, n_val, **k)
         if out is None and self.enabled:
@@ -419,6 +420,89 @@ def pythia_bench(steps: int, warmup: int, dev):
                         ("TFLOP/s" if a["bound"] == "mfma" else "GB/s"): rate / 1e12
                         if a["bound"] == "mfma" else rate / 1e9}
     return {"workload": "Pythia-1B shape GradDotProd, 8 train + 2 val, T=2048",
+            "ms_per_step": out["ghost"] * 1e3, "plain_ms_per_step": out["plain"] * 1e3,
+            "ms_per_step_serialised_dots": out["serial"] * 1e3,
+            "samples_per_s": n_train / out["ghost"], "step_overhead": out["ghost"] / out["plain"],
+            "ops": per_op}
+
+
+def hf_gpt2_bench(steps: int, warmup: int, dev):
+    """The reference LM example's model: a Hugging Face GPT2LMHeadModel at the GPT-2-small
+    configuration (HF Conv1D attention and MLP layers, tied head, dropout off), bf16, 16 train
+    + 4 val rows at T=1024 with per-sample position ids, against plain backprop of the same
+    model.  Random-init weights, synthetic ids."""
+    import transformers
+    from ghostsuite_amd import GradDotProdEngine, _native
+    from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+    from ghostsuite_amd.workloads import synthetic_tokens
+    n_train, n_val, T, vocab = 16, 4, 1024, 50257
+    cfg = transformers.GPT2Config(n_layer=12, n_embd=768, n_head=12, vocab_size=vocab,
+                                  n_positions=T, resid_pdrop=0.0, embd_pdrop=0.0,
+                                  attn_pdrop=0.0)
+    torch.manual_seed(0)
+    model = transformers.GPT2LMHeadModel(cfg).eval().to(dev, torch.bfloat16)
+    plain = transformers.GPT2LMHeadModel(cfg).eval().to(dev, torch.bfloat16)
+    plain.load_state_dict(model.state_dict())
+    X, _ = synthetic_tokens(n_train + n_val, T, vocab, seed=98, device=dev)
+    pos = torch.arange(T, device=dev).expand(n_train + n_val, T).contiguous()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    # The embeddings get the engine's dummy bias (as the reference's forward swapper gives
+    # them), so that autograd skips every weight-gradient GEMM the hooks supply.
+    model.ghost_embeddings = ["transformer.wte", "transformer.wpe"]
+    eng = GradDotProdEngine(model, val_batch_size=n_val, use_dummy_bias=True)
+    eng.attach(opt)
+    popt = torch.optim.AdamW(plain.parameters(), lr=1e-4)
+
+    def ghost_step(i):
+        eng.attach_train_batch(X[:n_train], X[:n_train], i, 0)
+        model(input_ids=X, position_ids=pos, labels=X).loss.backward()
+        eng.prepare_gradients()
+        opt.step()
+        eng.aggregate_and_log()
+        eng.clear_gradients()
+        opt.zero_grad(set_to_none=True)
+        eng.dot_product_log.clear()
+
+    def plain_step(i):
+        plain(input_ids=X, position_ids=pos, labels=X).loss.backward()
+        popt.step()
+        popt.zero_grad(set_to_none=True)
+
+    timed = TimedOps(_native.ops())
+    _native._install_backend(timed)
+
+    def timed_run(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            fn(i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    out = {"ghost": timed_run(ghost_step)}
+    S.options["overlap"] = False
+    timed.enabled = True
+    out["serial"] = timed_run(ghost_step)
+    timed.enabled = False
+    S.options["overlap"] = True
+    ops = timed.summary()
+    _native._install_backend(None)
+    out["plain"] = timed_run(plain_step)
+    eng.detach()
+    del model, plain, opt, popt, eng
+    torch.cuda.empty_cache()
+    per_op = {}
+    for name, a in sorted(ops.items(), key=lambda kv: -kv[1]["ms"]):
+        avg_ms = a["ms"] / a["n"]
+        rate = a["work"] / (avg_ms * 1e-3)
+        per_op[name] = {"ms_per_step": a["ms"] / (steps + warmup),
+                        "calls_per_step": a["n"] / (steps + warmup), "avg_us": avg_ms * 1e3,
+                        ("TFLOP/s" if a["bound"] == "mfma" else "GB/s"): rate / 1e12
+                        if a["bound"] == "mfma" else rate / 1e9}
+    return {"workload": "Hugging Face GPT2LMHeadModel (GPT-2-small config, Conv1D layers) "
+                        "GradDotProd step, 16 train + 4 val, T=1024",
             "ms_per_step": out["ghost"] * 1e3, "plain_ms_per_step": out["plain"] * 1e3,
             "ms_per_step_serialised_dots": out["serial"] * 1e3,
             "samples_per_s": n_train / out["ghost"], "step_overhead": out["ghost"] / out["plain"],
@@ -758,8 +842,9 @@ def measured_traffic(op_name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--mode", choices=["full", "kernels"], default="full")
-    ap.add_argument("--legs", default="gradproj,pythia",
-                    help="extra legs after the GPT-2 step: gradproj, pythia (comma list or none)")
+    ap.add_argument("--legs", default="gradproj,pythia,hf_gpt2",
+                    help="extra legs after the GPT-2 step: gradproj, pythia, hf_gpt2 (comma "
+                         "list or none)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
@@ -797,6 +882,9 @@ def main():
         if "pythia" in legs:
             extra["pythia"] = pythia_bench(3, 1, dev)
             log(f"[bench] pythia: {extra['pythia']['ms_per_step']:.1f} ms/step")
+        if "hf_gpt2" in legs:
+            extra["hf_gpt2"] = hf_gpt2_bench(5, 2, dev)
+            log(f"[bench] hf_gpt2: {extra['hf_gpt2']['ms_per_step']:.1f} ms/step")
 
     ops = res["ops"]
     steps = args.steps

@@ -268,11 +268,14 @@ def test_hf_conv1d_bf16_fused_path(gpu, n_v, monkeypatch):
             assert_close(grads[name], want, BF16_TOL, f"conv1d grad {name}")
 
 
-def test_hf_gpt2_model_through_the_engine(gpu):
+@pytest.mark.parametrize("dummy", [False, True])
+def test_hf_gpt2_model_through_the_engine(gpu, dummy):
     """The reference LM example's model family: a tiny Hugging Face GPT2LMHeadModel (Conv1D
     attention and MLP layers, LayerNorms, wte / wpe, tied lm_head), per-sample position ids
     passed explicitly, fp32, one val row (presum equals the pairwise sum), against float64
-    per-sample gradients: every parameter's dot and train gradient."""
+    per-sample gradients: every parameter's dot and train gradient; with `dummy` through the
+    documented dummy-bias setup (embeddings listed in ghost_embeddings, weights frozen for
+    autograd)."""
     transformers = pytest.importorskip("transformers")
     torch.manual_seed(41)
     cfg = transformers.GPT2Config(n_layer=2, n_embd=32, n_head=2, vocab_size=50, n_positions=16,
@@ -291,16 +294,21 @@ def test_hf_gpt2_model_through_the_engine(gpu):
         return m(input_ids=x, position_ids=torch.arange(T)[None], labels=x).loss
 
     model = model.to(gpu)
-    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False, precision="fp32")
-    eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
-    print("hf gpt2 engine", flush=True)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    if dummy:
+        model.ghost_embeddings = ["transformer.wte", "transformer.wpe"]
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=dummy, precision="fp32")
+    eng.attach(opt)
+    print(f"hf gpt2 engine dummy={dummy}", flush=True)
     model(input_ids=X.to(gpu), position_ids=pos.to(gpu), labels=X.to(gpu)).loss.backward()
     torch.cuda.synchronize()
     dots = {n: p.grad_dot_prod.cpu() for n, p in model.named_parameters()
             if hasattr(p, "grad_dot_prod")}
     eng.prepare_gradients()
-    grads = {n: p.grad.cpu() for n, p in model.named_parameters() if p.grad is not None}
+    grads = {n: p.grad.cpu() for n, p in model.named_parameters()
+             if p.grad is not None and "dummy_bias" not in n}
     eng.detach()
+    assert len(grads) == len(list(ref.named_parameters()))
     g_dot = brute.per_sample_grads(untied, X, X, sample_loss, 1.0 / N)
     g_grad = brute.per_sample_grads(ref, X, X, sample_loss, 1.0 / N)
     assert any(".attn.c_attn." in n for n in dots) and "transformer.wpe.weight" in dots

@@ -6,12 +6,15 @@ attach_and_store_valset, attach_train_batch, the dot_product_log record format).
 keyword arguments set the sampler options of
 ``supported_layers_grad_samplers_dotprod.options`` (precision, linear_algo, rounding,
 store_pairs, skip_overwritten_tied_dots, record_algorithms, overlap,
-reference_id_promotion); each engine starts from the defaults.
+reference_id_promotion).  Options belong to the engine: each starts from the defaults, and
+the engine whose model runs its forward installs its own into the shared dict the samplers
+read, keeping direct changes made to that dict while it was the one installed.
 """
 from __future__ import annotations
 
 import os
 import warnings
+import weakref
 from typing import Optional
 
 import torch
@@ -36,9 +39,10 @@ class GradDotProdEngine:
         if unknown:
             raise TypeError(f"unknown GradDotProdEngine options: {sorted(unknown)}")
         # Options apply per engine: nothing an earlier engine set carries over.
-        _samplers.options.clear()
-        _samplers.options.update(_samplers.DEFAULT_OPTIONS)
-        _samplers.options.update(sampler_options)
+        self._options = dict(_samplers.DEFAULT_OPTIONS)
+        self._options.update(sampler_options)
+        self._options_hook = None
+        self._activate_options()
 
         self.module = module
         self.val_batch_size = val_batch_size
@@ -58,6 +62,25 @@ class GradDotProdEngine:
 
         transformers_support.forward_swapper(module=module)
 
+    @property
+    def options(self) -> dict:
+        """This engine's sampler options: the shared dict while they are installed."""
+        return _samplers.options if _options_owner() is self else self._options
+
+    def _activate_options(self, *_):
+        """Installs this engine's options into the shared dict the samplers read (a forward
+        pre-hook of the model once attached).  The engine installed before keeps the values
+        the shared dict holds now, direct changes included."""
+        global _options_owner
+        prev = _options_owner()
+        if prev is self:
+            return
+        if prev is not None:
+            prev._options = dict(_samplers.options)
+        _samplers.options.clear()
+        _samplers.options.update(self._options)
+        _options_owner = weakref.ref(self)
+
     def _lock_grad_creation(self):
         self._grad_creation_locked = True
 
@@ -70,6 +93,8 @@ class GradDotProdEngine:
         autograd_grad_sample_dotprod.add_hooks(model=self.module,
                                                val_batch_size=self.val_batch_size,
                                                loss_reduction=self.loss_reduction)
+        self._activate_options()
+        self._options_hook = self.module.register_forward_pre_hook(self._activate_options)
         optimizer.grad_dot_prod_engine = self
 
     def detach(self):
@@ -78,6 +103,9 @@ class GradDotProdEngine:
         if hasattr(optimizer, "grad_dot_prod_engine"):
             del optimizer.grad_dot_prod_engine
         autograd_grad_sample_dotprod.remove_hooks(self.module)
+        if self._options_hook is not None:
+            self._options_hook.remove()
+            self._options_hook = None
         self.module.zero_grad()
         for param in self.module.parameters():
             for attr in ('train_grad', 'grad_dot_prod', 'grad_dot_prod_pair', 'activations',
@@ -174,6 +202,14 @@ class GradDotProdEngine:
         self.Y_train = Y_train
         self.iter_num = iter_num
         self.batch_idx = batch_idx
+
+
+def _no_owner():
+    return None
+
+
+# The engine whose options the shared dict holds (a weak reference).
+_options_owner = _no_owner
 
 
 def to_device(data, device):

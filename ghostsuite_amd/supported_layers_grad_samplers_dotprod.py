@@ -331,8 +331,13 @@ def _compute_embedding_dot_product(layer: nn.Embedding, A: torch.Tensor, B: torc
     # _compute_embedding_train_grad.
     scale = getattr(layer, "_gs_bias_grad_scale", None)
     if scale is not None and getattr(layer.weight, "initially_requires_grad", False):
-        layer._gs_weight_train_grad = _embedding_train_grad(layer, A, B, val_batch_size, scale,
-                                                            join=False)
+        # The train gradient is built from the ids the layer saw: the reference's gradient
+        # stage reads layer.activations (autograd_grad_sample_dotprod.py:166-181), not the ids
+        # its dot stage promoted to the backprops' dtype (:116-123), which may have rounded.
+        ids = layer.__dict__.get("activations")
+        ids = A if ids is None or ids.is_floating_point() else ids.detach()
+        layer._gs_weight_train_grad = _embedding_train_grad(layer, ids, B, val_batch_size,
+                                                            scale, join=False)
 
 
 # Returned by a train-grad sampler that has already added its gradient into

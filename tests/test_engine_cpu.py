@@ -371,6 +371,44 @@ def test_options_do_not_carry_over_between_engines():
         assert S.options == S.DEFAULT_OPTIONS
 
 
+def test_each_engine_runs_with_its_own_options():
+    """Two engines on two models: each model's backward runs with its engine's options, and a
+    direct change to the shared dict stays with the engine that was installed when it was
+    made."""
+    torch.manual_seed(0)
+    m1, m2 = MLP((6, 5, 3)), MLP((6, 5, 3))
+    x = torch.randn(4, 6, generator=gen(3))
+    y = torch.randint(0, 3, (4,), generator=gen(4))
+    seen = []
+    orig = S._supported_layers_dotprod[nn.Linear]
+
+    def spy(layer, A, B, val_batch_size):
+        seen.append((S.options["precision"], S.options["overlap"]))
+        return orig[0](layer, A, B, val_batch_size)
+
+    with use_oracle_backend():
+        e1 = GradDotProdEngine(m1, val_batch_size=1, precision="fp32", overlap=False)
+        e1.attach(torch.optim.SGD(m1.parameters(), lr=0.0))
+        e2 = GradDotProdEngine(m2, val_batch_size=1)
+        e2.attach(torch.optim.SGD(m2.parameters(), lr=0.0))
+        S._supported_layers_dotprod[nn.Linear] = (spy, orig[1])
+        try:
+            for m, want in ((m1, ("fp32", False)), (m2, ("reference", True)),
+                            (m1, ("fp32", False))):
+                seen.clear()
+                F.cross_entropy(m(x), y).backward()
+                assert seen and all(s == want for s in seen), (want, seen)
+            S.options["linear_algo"] = "valgrad"      # a direct change while e1 is installed
+            F.cross_entropy(m2(x), y).backward()
+            assert S.options["linear_algo"] == "auto" and e1.options["linear_algo"] == "valgrad"
+            F.cross_entropy(m1(x), y).backward()
+            assert S.options["linear_algo"] == "valgrad" and e2.options["linear_algo"] == "auto"
+        finally:
+            S._supported_layers_dotprod[nn.Linear] = orig
+            e1.detach()
+            e2.detach()
+
+
 @pytest.mark.parametrize("promote", [False, True])
 def test_embedding_id_promotion(promote):
     """The reference's hook promotes an Embedding's int64 ids to the backprops' dtype
@@ -391,6 +429,7 @@ def test_embedding_id_promotion(promote):
         head = torch.randn(3, T, d, generator=gen(70)).to(torch.bfloat16)
         (emb(ids).float() * head.float()).sum().backward()
         got = emb.weight.grad_dot_prod.clone()
+        train_grad = emb.weight.train_grad.clone()
         eng.detach()
     B = head.float()
     exact = R.embedding_dot_exact(ids, B, n_v)
@@ -398,6 +437,15 @@ def test_embedding_id_promotion(promote):
     bucketed = R.embedding_dot_exact(rounded_ids, B, n_v)
     assert not torch.allclose(exact, bucketed)
     assert_close(got, bucketed if promote else exact, 1e-6, "promotion")
+    # The train gradient comes from the ids as given in both settings (the reference's
+    # gradient stage reads layer.activations): rows 1022 and 1023, whose ids round to 1024,
+    # keep their own contributions.
+    N, n_t = ids.shape[0], ids.shape[0] - n_v
+    want = torch.zeros(vocab, d, dtype=torch.float64)
+    want.index_add_(0, ids[:n_t].reshape(-1), head[:n_t].double().reshape(-1, d) * N / n_t)
+    assert want[1023].abs().sum() > 0 and want[1022].abs().sum() > 0
+    assert_close(train_grad.double(), want, BF16_TOL, "train grad from the unrounded ids")
+    assert torch.equal(train_grad[1020:1030].double() != 0, want[1020:1030] != 0)
     # the reference's own op sequence on the promoted ids is the bucketed value
     assert_close(R.embedding_dot_ref(ids.to(torch.bfloat16), B, n_v, vocab), bucketed,
                  BF16_TOL, "reference sequence")

@@ -16,6 +16,10 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 // Checks the launch status of the kernels enqueued so far by this thread.
 int check_launch(const char* what);
+// The allocation-free entry point's scratch array on the current device (gs_noalloc.hip):
+// GS_LINEAR_NOALLOC_SCRATCH_BYTES, its address looked up once per device; fails when the
+// stream belongs to another device.
+int noalloc_scratch(hipStream_t s, void** out);
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 

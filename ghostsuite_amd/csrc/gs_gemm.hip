@@ -3023,51 +3023,8 @@ extern "C" int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N,
 }
 
 // ------------------------------------------------------------------ allocation-free variant
-// gs_linear_dot_noalloc's scratch memory: a file-scope device array, one copy on every GPU
-// the library runs on, held until the process ends.  Host code never uses the array's name
-// as an address (on the host it is only a stand-in for the symbol): the device address comes
-// from hipGetSymbolAddress, looked up once per device with that device current.
-static __device__ __align__(256) unsigned char scratch[GS_LINEAR_NOALLOC_SCRATCH_BYTES];
-
-namespace gs {
-namespace {
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// The scratch array's address on the current device, which must be the stream's device.
-int scratch_address(hipStream_t s, void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(GS_ERR_LAUNCH, std::string("hipGetDevice: ") +
-                                                      hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxDevices)
-    return fail(GS_ERR_UNSUPPORTED, "gs_linear_dot_noalloc: device index above 63");
-  if (s != nullptr) {
-    int sdev = -1;
-    e = hipStreamGetDevice(s, &sdev);
-    if (e != hipSuccess) return fail(GS_ERR_LAUNCH, std::string("hipStreamGetDevice: ") +
-                                                        hipGetErrorString(e));
-    if (sdev != dev)
-      return fail(GS_ERR_INVALID,
-                  "gs_linear_dot_noalloc: the stream belongs to another device than the "
-                  "current one");
-  }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[dev] == nullptr) {
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr)
-      return fail(GS_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") +
-                                     hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
-  }
-  *out = g_scratch_ptr[dev];
-  return GS_OK;
-}
-}  // namespace
-}  // namespace gs
-
+// gs_linear_dot's plan and kernels on the file-scope scratch array of gs_noalloc.hip
+// (noalloc_scratch), sized GS_LINEAR_NOALLOC_SCRATCH_BYTES per device.
 extern "C" size_t gs_linear_dot_noalloc_bytes(const void* A, const void* G, int dtype,
                                               int64_t N, int64_t n_val, int64_t T, int64_t d_in,
                                               int64_t d_out, int semantics, int algo,
@@ -3095,7 +3052,7 @@ extern "C" int gs_linear_dot_noalloc(const void* A, const void* G, int dtype, in
                     " (use gs_linear_dot with a workspace)");
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* ptr = nullptr;
-  rc = scratch_address(s, &ptr);
+  rc = noalloc_scratch(s, &ptr);
   if (rc) return rc;
   Carver cv(ptr, GS_LINEAR_NOALLOC_SCRATCH_BYTES);
   return run_linear_any(A, G, dtype, N, n_val, val_start, T, d_in, d_out, semantics, rounding,

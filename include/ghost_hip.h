@@ -13,9 +13,12 @@
  *   - T is the number of tokens per row (product of the middle dims; 1 for 2-D inputs).
  *   - Outputs are fp32 unless stated.  Nothing is allocated: scratch memory comes from the
  *     caller as (workspace, workspace_bytes), sized by the matching *_workspace() query.
+ *     The one exception is gs_linear_dot_noalloc, which takes no workspace and runs on a
+ *     fixed scratch array of the library's own (one per GPU that calls it; see there).
  *   - Every call is asynchronous on `stream` (a hipStream_t; NULL = default stream) and
  *     makes no host synchronisation.  The caller keeps inputs alive until the stream
- *     passes.  Functions are stateless and re-entrant.
+ *     passes.  Functions keep no state between calls and are re-entrant, except that calls
+ *     of gs_linear_dot_noalloc that overlap on one GPU share its scratch array.
  *   - Return value: GS_OK or a negative gs_status; gs_last_error() returns a thread-local
  *     message for the last failure on the calling thread.  The library never aborts.
  */
@@ -98,8 +101,10 @@ int gs_linear_dot(const void* A, const void* G, int dtype, int64_t N, int64_t n_
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments, semantics, kernels and results
  * as gs_linear_dot, without (workspace, workspace_bytes): the scratch memory is a fixed
- * device array of GS_LINEAR_NOALLOC_SCRATCH_BYTES inside the library, one copy per GPU, held
- * until the process ends.  The call allocates nothing and frees nothing.
+ * device array of GS_LINEAR_NOALLOC_SCRATCH_BYTES inside the library, one copy per GPU,
+ * reserved on a GPU by the first call there (the array sits in a code object of its own,
+ * which the other entry points never load) and held until the process ends.  The call
+ * allocates nothing and frees nothing.
  *   - `stream` must belong to the current device (NULL = its default stream).
  *   - A call that needs more scratch than the array holds returns GS_ERR_UNSUPPORTED
  *     (gs_linear_dot_noalloc_bytes tells the need; use gs_linear_dot with a workspace then).

@@ -701,3 +701,67 @@ def test_manager_step_contract_on_gpu(gpu, tmp_path):
     rest = torch.load(d / "dot_prod_log_iter_-1.pt", weights_only=True)
     assert [r["iter_num"] for r in rest] == [2, 3]
     assert not hasattr(model, "autograd_grad_sample_hooks")
+
+
+@pytest.mark.parametrize("promote", [False, True])
+def test_embedding_id_promotion_on_gpu(gpu, promote):
+    """GPT-2-small wte [50257, 768] and wpe [1024, 768] tables, bf16, 16 train + 4 val rows of
+    T = 1024, through the engine and the HIP embedding kernels.  reference_id_promotion=True
+    runs the dots on the ids the reference's hook makes (int64 -> bf16 -> int64,
+    autograd_grad_sample_dotprod.py:116-123): wte against the reference's own op sequence on
+    those ids; wpe's position 1023 rounds to 1024, past the 1024-row table (where the
+    reference's index_add_ would raise), and such a token takes no part, as any out-of-range
+    id.  The train gradients use the ids as given in both settings."""
+    from oracle import ghost_ref as R
+    N, n_val, T, d, V = 20, 4, 1024, 768, 50257
+    n_t = N - n_val
+
+    class Embeddings(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.wte = nn.Embedding(V, d)
+            self.wpe = nn.Embedding(T, d)
+
+        def forward(self, ids):
+            pos = torch.arange(T, device=ids.device).repeat(ids.shape[0], 1)
+            return self.wte(ids) + self.wpe(pos)
+
+    torch.manual_seed(5)
+    model = Embeddings().to(gpu, torch.bfloat16)
+    ids = torch.randint(0, V, (N, T), generator=gen(501))
+    ids[0, :4] = torch.tensor([1023, 50000, 50256, 257])   # ids that round in bf16
+    head = (torch.randn(N, T, d, generator=gen(502)) * 1e-2).to(torch.bfloat16)
+    eng = GradDotProdEngine(model, val_batch_size=n_val, use_dummy_bias=False,
+                            reference_id_promotion=promote)
+    eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+    print(f"embedding id promotion promote={promote}", flush=True)
+    (model(ids.to(gpu)).float() * head.to(gpu).float()).sum().backward()
+    torch.cuda.synchronize()
+    got_te = model.wte.weight.grad_dot_prod.cpu()
+    got_pe = model.wpe.weight.grad_dot_prod.cpu()
+    grad_te = model.wte.weight.train_grad.float().cpu()
+    grad_pe = model.wpe.weight.train_grad.float().cpu()
+    eng.detach()
+    B = head.float()
+    pos = torch.arange(T).repeat(N, 1)
+    if promote:
+        p_ids = ids.to(torch.bfloat16).long()
+        assert not torch.equal(p_ids, ids)
+        assert_close(got_te, R.embedding_dot_ref(p_ids.to(torch.bfloat16), B, n_val, V),
+                     BF16_TOL, "wte dot, reference sequence on promoted ids")
+        p_pos = pos.to(torch.bfloat16).long()
+        past = p_pos >= T
+        assert past.any() and int(p_pos.max()) == T   # 1023 -> 1024
+        Bz = B.clone()
+        Bz[past] = 0
+        assert_close(got_pe, R.embedding_dot_exact(p_pos.clamp(max=T - 1), Bz, n_val), BF16_TOL,
+                     "wpe dot on promoted positions")
+        assert not torch.allclose(got_te.double(), R.embedding_dot_exact(ids, B, n_val),
+                                  rtol=1e-3)
+    else:
+        assert_close(got_te, R.embedding_dot_exact(ids, B, n_val), BF16_TOL, "wte dot")
+        assert_close(got_pe, R.embedding_dot_exact(pos, B, n_val), BF16_TOL, "wpe dot")
+    for tab, x, got in ((V, ids, grad_te), (T, pos, grad_pe)):
+        want = torch.zeros(tab, d, dtype=torch.float64)
+        want.index_add_(0, x[:n_t].reshape(-1), B[:n_t].double().reshape(-1, d) * N / n_t)
+        assert_close(got.double(), want, BF16_TOL, f"train grad [{tab}]")

@@ -542,6 +542,38 @@ def ghost_kernel_bench(dev, reps: int = 20, T: int = 1024):
             "valgrad_ms": ms_vg}
 
 
+def emb_grad_pad_bench(dev, reps: int = 10):
+    """The Embedding train gradient on a padded batch: 32 train + 2 val rows of T=2048 with
+    90% of the tokens one pad id (65536 train tokens, a 59k-token run), d=768, vocab 50257,
+    bf16, both modes; against the same call on uniform ids of the same shape."""
+    from ghostsuite_amd import _native
+    g = torch.Generator().manual_seed(5)
+    N, n_val, T, d, V = 34, 2, 2048, 768, 50257
+    ids = torch.randint(0, V, (N, T), generator=g)
+    ids_pad = ids.clone()
+    ids_pad[torch.rand(N, T, generator=g) < 0.9] = V - 1
+    G = (torch.randn(N, T, d, generator=g) * 1e-2).to(dev, torch.bfloat16)
+    tab = torch.zeros(V, d, dtype=torch.bfloat16, device=dev)
+    ops = _native.ops()
+    out = {}
+    for name, x in (("padded", ids_pad.to(dev)), ("uniform", ids.to(dev))):
+        for acc in (False, True):
+            fn = lambda: ops.embedding_train_grad(x, G, n_val, 1.0, tab, accumulate=acc)
+            fn()
+            torch.cuda.synchronize()
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                fn()
+            e.record()
+            torch.cuda.synchronize()
+            out[f"{name}_{'accumulate' if acc else 'overwrite'}_us"] = s.elapsed_time(e) / reps * 1e3
+    del G, tab
+    return {"shape": "ids[34,2048] (32 train + 2 val rows), G[34,2048,768] bf16, vocab 50257",
+            **out}
+
+
 def ghost_sweep(dev, reps: int = 10):
     """BASELINE configs[1] sweep over T: the reference's switch (2T^2 <= d_in*d_out) picks the
     ghost (pairwise-sum) branch up to T=1024 and the materialised (presum) branch at T=2048;
@@ -872,6 +904,8 @@ def main():
     log(f"[bench] ghost kernel T=1024: {gk['ms']:.3f} ms, {gk['tflops']:.1f} TF/s")
     sweep = ghost_sweep(dev)
     log("[bench] configs[1] T sweep done")
+    emb_pad = emb_grad_pad_bench(dev)
+    log(f"[bench] embedding train grad, padded batch: {emb_pad}")
     legs = [l for l in args.legs.split(",") if l and l != "none"]
     extra = {}
     import contextlib
@@ -963,6 +997,7 @@ def main():
                     ("TFLOP/s" if v["bound"] == "mfma" else "GB/s"):
                         v["work"] / (v["ms"] / v["n"] * 1e-3) / (1e12 if v["bound"] == "mfma" else 1e9)}
                 for k, v in sorted(ops.items(), key=lambda kv: -kv[1]["ms"])},
+        "embedding_train_grad_padded_batch": emb_pad,
         "algorithms": {k: list(v) for k, v in list(res["algos"].items())[:8]},
         "cpu_baseline": cpu,
         **extra,

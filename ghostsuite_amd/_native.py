@@ -60,7 +60,7 @@ _SIGNATURES = {
     "gs_embedding_dot_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "gs_embedding_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _SZ,
                               _P]),
-    "gs_embedding_train_grad_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+    "gs_embedding_train_grad_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "gs_embedding_train_grad": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P,
                                      _I, _I, _P, _SZ, _P]),
     "gs_layernorm_dot_workspace": (_SZ, [_I64, _I64, _I64]),
@@ -530,7 +530,7 @@ class HipOps:
         vocab = out.shape[0]
         vs = N - n_val if val_start is None else int(val_start)
         lib = load_library()
-        ws_bytes = lib.gs_embedding_train_grad_workspace(N, n_val, T, vocab)
+        ws_bytes = lib.gs_embedding_train_grad_workspace(N, n_val, T, d, vocab)
         if ws_bytes == 0:
             raise GhostHipError(f"gs_embedding_train_grad: invalid arguments N={N} n_val={n_val}")
         ws = _workspace(ws_bytes, dev)

@@ -2,17 +2,28 @@
 //
 //   grad[v] = scale * sum over the train tokens t with id_t = v of g_t        grad: [vocab, d]
 //
-// The train tokens are grouped by id without float atomics, so the result is the same bits
-// on every run: integer atomics count each id's tokens and find its first token, which
-// reserves the id's range of a token list from a bump cursor; the tokens are placed in their
-// ranges (in any order), then each finds its place in index order by counting the smaller
-// token indices in its range.  One wave per vocabulary row sums the rows of its tokens in
-// index order in fp32 and writes the row once, scaled and converted to the grad dtype.
-// Overwrite mode writes every row (zeros where no train token has the id), which replaces a
-// zero-fill, a scatter-add and a full-table scale; accumulate mode adds the touched rows into
-// what `grad` holds (a tied weight whose Linear train gradient is already there) and leaves
-// the other rows alone.  Where a range sits in the list depends on the order the atomics ran
-// in; only its contents and their order enter the sums.
+// The train tokens are sorted by the key (id << 32 | token index), so every id's tokens form
+// one run, in index order, of a sorted token list; sums run over that list in a fixed order,
+// so the result is the same bits on every run, and every step's work is linear in the number
+// of tokens however often an id repeats.  Four launches:
+//   1. eg_sort_kernel    -- chunks of EG_CHUNK tokens sorted in registers and LDS (bitonic);
+//                           per-chunk counts of in-range ids; the id-presence bitmap cleared.
+//   2. eg_merge_kernel   -- every key's place in the whole list = its place in its chunk plus
+//                           the number of smaller keys in each other chunk (binary search);
+//                           the presence bitmap set.
+//   3. eg_window_kernel  -- one wave per window of EG_WIN places: each run inside the window
+//                           is summed in index order and its row written (scaled, added to
+//                           the old row when accumulating); a run crossing a window boundary
+//                           leaves its part of the window as an fp32 partial.  In overwrite
+//                           mode further waves write zeros to the rows of absent ids.
+//   4. eg_combine_kernel -- per run that crosses windows, its partials summed in window order
+//                           and the row written: by one wave for a run of a few windows, by
+//                           the 16 waves of a workgroup (contiguous shares combined in wave
+//                           order) for a longer one.
+// Token ids outside [0, vocab) take no part.  Measured on MI355X (GPT-2 wte, 16 train rows of
+// 1024 tokens, d = 768, bf16): sort 15 us, merge 19, windows 19-21, combine 5-7; a padded
+// batch of 65536 train tokens with one id on 59k of them: 0.59 ms, most of it the long run's
+// combine on one workgroup.
 
 #include <algorithm>
 
@@ -21,244 +32,624 @@
 namespace gs {
 namespace {
 
-constexpr int EG_THREADS = 256;
+constexpr int EG_CHUNK = 2048;                  // keys per sort workgroup
+constexpr int EG_SORT_THREADS = 1024;
+constexpr int EG_KPT = EG_CHUNK / EG_SORT_THREADS;  // keys per thread (2)
+constexpr int EG_WIN = 8;                       // list places per window (one wave)
+constexpr int EG_BATCH = 8;                     // rows of a window loaded together
+constexpr int EG_THREADS = 256;                 // window / zero / combine workgroups
+constexpr unsigned long long EG_NONE = ~0ull;   // key of an out-of-range id (sorts last)
 
-// cnt[v] = fill[v] = 0, first[v] = INT32_MAX, cursor[0..1] = 0.
-__global__ void __launch_bounds__(EG_THREADS) eg_clear_kernel(int32_t* __restrict__ cnt,
-                                                              int32_t* __restrict__ fill,
-                                                              int32_t* __restrict__ first,
-                                                              int32_t* __restrict__ cursor,
-                                                              int64_t vocab) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (v0 == 0) {
-    cursor[0] = 0;   // token-list cursor
-    cursor[1] = 0;   // number of ids present
-  }
-  for (int64_t v = v0; v < vocab; v += stride) {
-    cnt[v] = 0;
-    fill[v] = 0;
-    first[v] = INT32_MAX;
-  }
+__device__ __forceinline__ int64_t key_id(unsigned long long k) {
+  return static_cast<int64_t>(k >> 32);
+}
+__device__ __forceinline__ int64_t key_tok(unsigned long long k) {
+  return static_cast<int64_t>(k & 0xffffffffull);
 }
 
-// The id of train token q (tokens numbered in train-row order), or -1 when out of range.
-__device__ __forceinline__ int64_t eg_id(const int64_t* __restrict__ ids, const RowMap& tr,
-                                         int64_t vocab, int64_t q) {
+// Physical row of train token q (tokens numbered in train-row order).
+__device__ __forceinline__ int64_t eg_row(const RowMap& tr, int64_t q) {
   const int64_t seg = q / tr.seglen;
-  const int64_t id = ids[tr.phys_row(seg, q - seg * tr.seglen)];
-  return (id >= 0 && id < vocab) ? id : -1;
+  return tr.phys_row(seg, q - seg * tr.seglen);
 }
 
-// cnt[id] = tokens with the id, first[id] = the smallest such token index.
-__global__ void __launch_bounds__(EG_THREADS) eg_count_kernel(const int64_t* __restrict__ ids,
-                                                              RowMap tr, int64_t vocab,
-                                                              int32_t* __restrict__ cnt,
-                                                              int32_t* __restrict__ first) {
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (q >= tr.total()) return;
-  const int64_t id = eg_id(ids, tr, vocab, q);
-  if (id < 0) return;
-  atomicAdd(cnt + id, 1);
-  atomicMin(first + id, static_cast<int32_t>(q));
+// Lane l's value of v, as a wave-uniform value (l a compile-time or uniform lane index).
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long v, int l) {
+  const unsigned lo = static_cast<unsigned>(
+      __builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffull), l));
+  const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), l));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
 }
 
-// base[id] = the start of the id's range in the token list, reserved by its first token;
-// segs[j] = the ids present (in reservation order), cursor[1] = their number.  A workgroup's
-// reservations go through one 64-bit atomic on the packed (ranges, ids) cursor; prefix sums
-// over the workgroup place its lanes.
-__global__ void __launch_bounds__(EG_THREADS) eg_alloc_kernel(const int64_t* __restrict__ ids,
-                                                              RowMap tr, int64_t vocab,
-                                                              const int32_t* __restrict__ cnt,
-                                                              const int32_t* __restrict__ first,
-                                                              int32_t* __restrict__ cursor,
-                                                              int32_t* __restrict__ base,
-                                                              int32_t* __restrict__ segs) {
-  constexpr int NW = EG_THREADS / 64;
-  __shared__ int32_t wn[NW], wo[NW];
-  __shared__ unsigned long long blk;
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  int64_t id = -1;
-  if (q < tr.total()) id = eg_id(ids, tr, vocab, q);
-  const bool mine = id >= 0 && first[id] == static_cast<int32_t>(q);
-  const int32_t n = mine ? cnt[id] : 0, one = mine ? 1 : 0;
-  int32_t pn = n, po = one;  // inclusive prefix sums over the wave
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
+  return static_cast<int64_t>(readlane_u64(static_cast<unsigned long long>(v), l));
+}
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+  const int lo = __shfl_xor(static_cast<int>(v & 0xffffffffull), m, 64);
+  const int hi = __shfl_xor(static_cast<int>(v >> 32), m, 64);
+  return (static_cast<unsigned long long>(static_cast<unsigned>(hi)) << 32) |
+         static_cast<unsigned>(lo);
+}
+
+// Sort keys of chunk c: (id << 11 | index within the chunk) as 32 bits while every id is
+// below 2^20, else (id << 32 | token index) as 64 bits; an out-of-range id (and the tail past
+// M) is the largest key.  Both orders are (id, token index) within a chunk.
+template <class K>
+struct EgKey;
+template <>
+struct EgKey<uint32_t> {
+  static constexpr uint32_t NONE = ~0u;
+  __device__ static uint32_t make(int64_t id, int64_t q, int64_t q0) {
+    return (static_cast<uint32_t>(id) << 11) | static_cast<uint32_t>(q - q0);
+  }
+  __device__ static int64_t id(uint32_t k) { return k >> 11; }
+  __device__ static int64_t tok(uint32_t k, int64_t q0) { return q0 + (k & 2047u); }
+  // keys of another chunk that precede (id, q): ids below `id` (chunk after q's), or ids up
+  // to `id` (chunk before q's) -- the count of keys below the returned bound
+  __device__ static uint32_t bound(int64_t id, bool earlier_chunk) {
+    return earlier_chunk ? ((static_cast<uint32_t>(id) + 1u) << 11)
+                         : (static_cast<uint32_t>(id) << 11);
+  }
+};
+template <>
+struct EgKey<unsigned long long> {
+  static constexpr unsigned long long NONE = ~0ull;
+  __device__ static unsigned long long make(int64_t id, int64_t q, int64_t) {
+    return (static_cast<unsigned long long>(id) << 32) | static_cast<unsigned long long>(q);
+  }
+  __device__ static int64_t id(unsigned long long k) { return static_cast<int64_t>(k >> 32); }
+  __device__ static int64_t tok(unsigned long long k, int64_t) {
+    return static_cast<int64_t>(k & 0xffffffffull);
+  }
+  __device__ static unsigned long long bound(int64_t id, bool earlier_chunk) {
+    return earlier_chunk ? (static_cast<unsigned long long>(id + 1) << 32)
+                         : (static_cast<unsigned long long>(id) << 32);
+  }
+};
+constexpr int64_t EG_KEY32_VOCAB = int64_t(1) << 20;
+
+__device__ __forceinline__ uint32_t shfl_xor_key(uint32_t v, int m) {
+  return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), m, 64));
+}
+__device__ __forceinline__ unsigned long long shfl_xor_key(unsigned long long v, int m) {
+  return shfl_xor_u64(v, m);
+}
+
+// Chunk c (tokens [c * EG_CHUNK, ...)): its keys sorted ascending into ck[c][0, EG_CHUNK),
+// the number of in-range keys into cnt[c]; the workgroups also clear the presence bitmap.
+// Key u of thread t is element t + 1024 u of the chunk: compare-exchange partners at distance
+// j = 1024 are in the same thread, at j < 64 in the same wave (lane shuffles), the others go
+// through LDS; sixteen waves per workgroup hide each other's shuffle and LDS latency.
+template <class K>
+__global__ void __launch_bounds__(EG_SORT_THREADS) eg_sort_kernel(
+    const int64_t* __restrict__ ids, RowMap tr, int64_t vocab, K* __restrict__ ck,
+    int32_t* __restrict__ cnt, uint32_t* __restrict__ present, int64_t present_words) {
+  __shared__ K xs[EG_CHUNK];
+  __shared__ int32_t wcount[EG_SORT_THREADS / 64];
+  const int t = threadIdx.x, lane = t & 63;
+  const int64_t M = tr.total();
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * EG_CHUNK;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * EG_SORT_THREADS + t; w < present_words;
+       w += static_cast<int64_t>(gridDim.x) * EG_SORT_THREADS)
+    present[w] = 0u;
+  K key[EG_KPT];
+  int valid = 0;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int32_t a = __shfl_up(pn, off, 64), b = __shfl_up(po, off, 64);
-    if (lane >= off) {
-      pn += a;
-      po += b;
+  for (int u = 0; u < EG_KPT; ++u) {
+    const int64_t q = q0 + t + EG_SORT_THREADS * u;
+    K k = EgKey<K>::NONE;
+    if (q < M) {
+      const int64_t id = ids[eg_row(tr, q)];
+      if (id >= 0 && id < vocab) {
+        k = EgKey<K>::make(id, q, q0);
+        ++valid;
+      }
+    }
+    key[u] = k;
+  }
+  for (int k = 2; k <= EG_CHUNK; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= EG_SORT_THREADS) {
+        const int uj = j / EG_SORT_THREADS;
+#pragma unroll
+        for (int u = 0; u < EG_KPT; ++u) {
+          if (u & uj) continue;
+          const int i = t + EG_SORT_THREADS * u;
+          const bool asc = (i & k) == 0;
+          const K a = key[u], b = key[u | uj];
+          const K lo = a < b ? a : b, hi = a < b ? b : a;
+          key[u] = asc ? lo : hi;
+          key[u | uj] = asc ? hi : lo;
+        }
+        continue;
+      }
+      K other[EG_KPT];
+      if (j >= 64) {
+        __syncthreads();   // earlier readers of xs are done
+#pragma unroll
+        for (int u = 0; u < EG_KPT; ++u) xs[t + EG_SORT_THREADS * u] = key[u];
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < EG_KPT; ++u) other[u] = xs[(t ^ j) + EG_SORT_THREADS * u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < EG_KPT; ++u) other[u] = shfl_xor_key(key[u], j);
+      }
+#pragma unroll
+      for (int u = 0; u < EG_KPT; ++u) {
+        const int i = t + EG_SORT_THREADS * u;
+        const bool asc = (i & k) == 0, lower = (i & j) == 0;
+        const K a = key[u], b = other[u];
+        // the lower element keeps the minimum when ascending, the upper one the maximum
+        key[u] = (lower == asc) ? (a < b ? a : b) : (a < b ? b : a);
+      }
     }
   }
-  if (lane == 63) {
-    wn[wid] = pn;
-    wo[wid] = po;
-  }
+  K* out = ck + static_cast<int64_t>(blockIdx.x) * EG_CHUNK;
+#pragma unroll
+  for (int u = 0; u < EG_KPT; ++u) out[t + EG_SORT_THREADS * u] = key[u];
+  // in-range keys of the chunk: a fixed-order integer sum
+  for (int off = 32; off > 0; off >>= 1) valid += __shfl_xor(valid, off, 64);
+  if (lane == 0) wcount[t >> 6] = valid;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long tn = 0, to = 0;
-    for (int w = 0; w < NW; ++w) {
-      tn += static_cast<unsigned>(wn[w]);
-      to += static_cast<unsigned>(wo[w]);
-    }
-    blk = to > 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(cursor), tn | (to << 32))
-                 : 0ull;
-  }
-  __syncthreads();
-  if (mine) {
-    int32_t bn = static_cast<int32_t>(blk & 0xffffffffull);
-    int32_t bo = static_cast<int32_t>(blk >> 32);
-    for (int w = 0; w < wid; ++w) {
-      bn += wn[w];
-      bo += wo[w];
-    }
-    base[id] = bn + pn - n;
-    segs[bo + po - 1] = static_cast<int32_t>(id);
+  if (t == 0) {
+    int s = 0;
+    for (int w = 0; w < EG_SORT_THREADS / 64; ++w) s += wcount[w];
+    cnt[blockIdx.x] = s;
   }
 }
 
-// list[base[id] + k] = q for some k in [0, cnt[id]) (the order inside a range is arbitrary).
-__global__ void __launch_bounds__(EG_THREADS) eg_place_kernel(const int64_t* __restrict__ ids,
-                                                              RowMap tr, int64_t vocab,
-                                                              const int32_t* __restrict__ base,
-                                                              int32_t* __restrict__ fill,
-                                                              int32_t* __restrict__ list) {
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (q >= tr.total()) return;
-  const int64_t id = eg_id(ids, tr, vocab, q);
-  if (id < 0) return;
-  const int32_t k = atomicAdd(fill + id, 1);
-  list[base[id] + k] = static_cast<int32_t>(q);
+// sk[place] = (id << 32 | token index), place = the key's index in its chunk + the keys of
+// every other chunk that precede it; present[id] set.  One thread per chunk slot, a
+// workgroup per 256 consecutive slots of one chunk (slots holding the largest key do
+// nothing).  The keys of other chunks that precede a key depend only on its id, so the first
+// slot of each id within the workgroup searches (the binary searches over the other chunks
+// advance together, eight chunks at a time, so their loads are in flight at once) and the
+// slots after it take its count from LDS: an id that fills the chunk searches once per
+// workgroup, not once per token.
+template <class K>
+__global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
+    const K* __restrict__ ck, int64_t chunks, unsigned long long* __restrict__ sk,
+    uint32_t* __restrict__ present) {
+  // STEPS halvings take an interval of 2^(STEPS - 1) = EG_CHUNK slots down to empty
+  constexpr int G = 8, STEPS = 12;
+  static_assert((1 << (STEPS - 1)) == EG_CHUNK, "search steps");
+  static_assert(EG_CHUNK % EG_THREADS == 0, "a merge workgroup stays inside one chunk");
+  __shared__ int64_t kid[EG_THREADS];    // ids of the workgroup's slots (-1: none)
+  __shared__ int64_t before[EG_THREADS];  // at run heads: keys of other chunks preceding
+  const int t = threadIdx.x;
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * EG_THREADS + t;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * EG_THREADS / EG_CHUNK, q0 = c * EG_CHUNK;
+  const K k = ck[s];
+  const bool valid = k != EgKey<K>::NONE;
+  const int64_t id = valid ? EgKey<K>::id(k) : -1;
+  kid[t] = id;
+  __syncthreads();
+  const bool head = valid && (t == 0 || kid[t - 1] != id);
+  // 64-bit keys hold the token index: the plain order of keys; 32-bit keys compare ids only
+  // across chunks (every token of an earlier chunk precedes, of a later one follows)
+  const K lo_bound = sizeof(K) == 8 ? k : EgKey<K>::bound(id, false);
+  const K hi_bound = sizeof(K) == 8 ? k : EgKey<K>::bound(id, true);
+  if (head) {
+    int64_t n_before = 0;
+    for (int64_t o0 = 0; o0 < chunks; o0 += G) {
+      int lo[G], hi[G];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const int64_t o = o0 + u;
+        lo[u] = 0;
+        hi[u] = (o < chunks && o != c) ? EG_CHUNK : 0;
+      }
+#pragma unroll
+      for (int step = 0; step < STEPS; ++step) {
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+          if (lo[u] >= hi[u]) continue;
+          const int mid = (lo[u] + hi[u]) >> 1;
+          const int64_t o = o0 + u;
+          const K b = o < c ? hi_bound : lo_bound;
+          if (ck[o * EG_CHUNK + mid] < b) lo[u] = mid + 1; else hi[u] = mid;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < G; ++u) n_before += lo[u];
+    }
+    before[t] = n_before;
+  }
+  __syncthreads();
+  if (!valid) return;
+  // the run head of this slot's id in the workgroup: the first slot with the id (ids sorted)
+  int lo = 0, hi = t;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (kid[mid] < id) lo = mid + 1; else hi = mid;
+  }
+  const int64_t place = (s - q0) + before[lo];
+  sk[place] = (static_cast<unsigned long long>(id) << 32) |
+              static_cast<unsigned long long>(EgKey<K>::tok(k, q0));
+  if (head) atomicOr(present + (id >> 5), 1u << (id & 31));
 }
 
-// sorted[base[id] + r] = q with r = the number of tokens of the same id before q: each range
-// of `sorted` lists its tokens in index order.
-__global__ void __launch_bounds__(EG_THREADS) eg_order_kernel(const int64_t* __restrict__ ids,
-                                                              RowMap tr, int64_t vocab,
-                                                              const int32_t* __restrict__ base,
-                                                              const int32_t* __restrict__ cnt,
-                                                              const int32_t* __restrict__ list,
-                                                              int32_t* __restrict__ sorted) {
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (q >= tr.total()) return;
-  const int64_t id = eg_id(ids, tr, vocab, q);
-  if (id < 0) return;
-  const int32_t s = base[id], n = cnt[id];
-  int32_t r = 0;
-  for (int32_t k = 0; k < n; ++k) r += list[s + k] < static_cast<int32_t>(q) ? 1 : 0;
-  sorted[s + r] = static_cast<int32_t>(q);
+// Sum of cnt[0, chunks): the number of in-range keys, the length of the sorted list.
+__device__ __forceinline__ int64_t list_length(const int32_t* __restrict__ cnt, int64_t chunks) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;   // below 2^31 (checked by the entry point)
+  for (int64_t c = lane; c < chunks; c += 64) n += cnt[c];
+  for (int off = 32; off > 0; off >>= 1) n += __shfl_xor(n, off, 64);
+  return n;
 }
 
 template <class E>
 struct EgVec {
-  static constexpr int VE = 16 / sizeof(E);
+  static constexpr int VE = 16 / sizeof(E);  // elements per 16-byte chunk
+  union U {
+    uint4 u;
+    E e[VE];
+  };
 };
 
-// One wave per output row: lanes own 16-byte chunks of the G row (VE elements, several
-// passes when d > 64 VE); each lane sums its chunk over the row's tokens in index order
-// (fp32) and writes scale * sum (plus the old value when accumulating), as whole 16-byte
-// stores when `vec`.  Overwrite mode: the waves walk every vocabulary row (zeros where no token
-// has the id); accumulate mode: only the ids present, from segs[0, *nseg).
+// Loads the VE elements at f0 of a row (zeros past d); whole 16 bytes when `full`.
+template <class E>
+__device__ __forceinline__ uint4 eg_load(const E* __restrict__ row, int64_t f0, int64_t d,
+                                         bool full) {
+  typename EgVec<E>::U x;
+  if (full) {
+    x.u = *reinterpret_cast<const uint4*>(row + f0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < EgVec<E>::VE; ++i) x.e[i] = f0 + i < d ? row[f0 + i] : E(0);
+  }
+  return x.u;
+}
+
+// Writes scale * acc (+ the old row when accumulating) at f0 of an output row.
+template <class GE, int VE>
+__device__ __forceinline__ void eg_store(GE* __restrict__ out, int64_t f0, int64_t d,
+                                         const float (&acc)[VE], float scale, int accumulate,
+                                         bool full) {
+  constexpr int NV = VE * static_cast<int>(sizeof(GE)) / 16;  // whole 16-byte vectors
+  if (NV > 0 && full) {
+    union { uint4 u[NV > 0 ? NV : 1]; GE e[VE]; } o;
+    if (accumulate) {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) o.u[c] = reinterpret_cast<const uint4*>(out + f0)[c];
+    }
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      float x = scale * acc[i];
+      if (accumulate) x += to_f32<GE>(o.e[i]);
+      o.e[i] = from_f32<GE>(x);
+    }
+#pragma unroll
+    for (int c = 0; c < NV; ++c) reinterpret_cast<uint4*>(out + f0)[c] = o.u[c];
+  } else {
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      if (f0 + i >= d) break;
+      float x = scale * acc[i];
+      if (accumulate) x += to_f32<GE>(out[f0 + i]);
+      out[f0 + i] = from_f32<GE>(x);
+    }
+  }
+}
+
+// Waves [0, windows): window w = list places [w EG_WIN, (w + 1) EG_WIN).  Lanes own 16-byte
+// chunks of the feature row (several passes when d > 64 VE); per pass a lane loads its chunk
+// of every row of the window (all in flight), then walks the window's runs in place order,
+// summing in fp32.  A run wholly inside the window writes its row; the run holding the
+// window's first place, when it began in an earlier window, goes to part[w][0], and the run
+// holding the last place, when it continues into the next window (and began in this one),
+// to part[w][1] (fp32, [windows][2][d]).
+// Waves [windows, windows + zero_waves), overwrite mode: 16 table rows each; rows whose id is
+// absent from the list are written as zeros.
 template <class E, class GE>
-__global__ void __launch_bounds__(EG_THREADS) eg_rows_kernel(
+__global__ void __launch_bounds__(EG_THREADS) eg_window_kernel(
     const E* __restrict__ G, RowMap tr, int64_t d, int64_t vocab,
-    const int32_t* __restrict__ base, const int32_t* __restrict__ cnt,
-    const int32_t* __restrict__ sorted, const int32_t* __restrict__ segs,
-    const int32_t* __restrict__ nseg, float scale, int accumulate, int vec,
-    GE* __restrict__ grad) {
+    const unsigned long long* __restrict__ sk, const int32_t* __restrict__ cnt, int64_t chunks,
+    const uint32_t* __restrict__ present, int64_t windows, float scale, int accumulate, int vec,
+    float* __restrict__ part, GE* __restrict__ grad) {
   constexpr int VE = EgVec<E>::VE;
   const int lane = threadIdx.x & 63;
   const int64_t w = static_cast<int64_t>(blockIdx.x) * (EG_THREADS / 64) + (threadIdx.x >> 6);
-  int64_t v;
-  if (accumulate) {
-    if (w >= *nseg) return;
-    v = segs[w];
-  } else {
-    if (w >= vocab) return;
-    v = w;
-  }
-  const int32_t n = cnt[v];
-  const int32_t s = n > 0 ? base[v] : 0;   // base[v] is set only for ids present
-  GE* out = grad + v * d;
-  for (int64_t f0 = static_cast<int64_t>(lane) * VE; f0 < d; f0 += 64 * VE) {
-    const bool full = vec && f0 + VE <= d;
-    float acc[VE];
+  if (w >= windows) {
+    // absent rows, overwrite mode only (the last workgroup's surplus waves land here in
+    // both modes): 16 rows, lanes over chunks
+    const int64_t v0 = (w - windows) * 16;
+    if (accumulate || v0 >= vocab) return;
+    const uint32_t bits = present[v0 >> 5] >> (v0 & 31);   // v0 is a multiple of 16
+    for (int r = 0; r < 16 && v0 + r < vocab; ++r) {
+      if ((bits >> r) & 1u) continue;
+      GE* out = grad + (v0 + r) * d;
+      for (int64_t f0 = static_cast<int64_t>(lane) * VE; f0 < d; f0 += 64 * VE) {
+        float z[VE];
 #pragma unroll
-    for (int i = 0; i < VE; ++i) acc[i] = 0.f;
-    for (int32_t k = 0; k < n; ++k) {
-      const int64_t q = sorted[s + k];
-      const int64_t seg = q / tr.seglen;
-      const E* row = G + tr.phys_row(seg, q - seg * tr.seglen) * d + f0;
-      if (full) {
-        union { uint4 u; E e[VE]; } x;
-        x.u = *reinterpret_cast<const uint4*>(row);
-#pragma unroll
-        for (int i = 0; i < VE; ++i) acc[i] += to_f32<E>(x.e[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VE; ++i)
-          if (f0 + i < d) acc[i] += to_f32<E>(row[i]);
+        for (int i = 0; i < VE; ++i) z[i] = 0.f;
+        eg_store<GE, VE>(out, f0, d, z, 0.f, 0, vec && f0 + VE <= d);
       }
     }
-    // The chunk's VE outputs as whole 16-byte vectors (8 bf16, 8 or 4 fp32; 4 bf16 are 8
-    // bytes and take the element path).
-    constexpr int NV = VE * static_cast<int>(sizeof(GE)) / 16;
-    if (NV > 0 && full) {
-      union { uint4 u[NV > 0 ? NV : 1]; GE e[VE]; } o;
-      if (accumulate) {
+    return;
+  }
+  const int64_t n_list = list_length(cnt, chunks);
+  const int64_t r0 = w * EG_WIN;
+  if (r0 >= n_list) return;
+  const int n = static_cast<int>(std::min<int64_t>(EG_WIN, n_list - r0));
+  // lane i < n: the key at place r0 + i, its id and G row; read as wave-uniform values below
+  const unsigned long long k = lane < n ? sk[r0 + lane] : EG_NONE;
+  const int64_t my_id = key_id(k);
+  const int64_t my_row = lane < n ? eg_row(tr, key_tok(k)) : 0;
+  const bool from_before = r0 > 0 && key_id(sk[r0 - 1]) == readlane_i64(my_id, 0);
+  const bool into_next = r0 + n < n_list && key_id(sk[r0 + n]) == readlane_i64(my_id, n - 1);
+  // two feature passes per round (lanes own chunks f0 and f0 + 64 VE); the window's rows in
+  // batches, each batch's loads of both passes issued together, the sums carried across
+  // batches
+  for (int64_t fb = static_cast<int64_t>(lane) * VE; fb < d; fb += 128 * VE) {
+    float acc[2][VE];
 #pragma unroll
-        for (int c = 0; c < NV; ++c) o.u[c] = reinterpret_cast<const uint4*>(out + f0)[c];
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
+    bool first_run = true;
+#pragma unroll
+    for (int b0 = 0; b0 < EG_WIN; b0 += EG_BATCH) {
+      if (b0 >= n) break;   // wave-uniform
+      uint4 x[2][EG_BATCH];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t f0 = fb + h * 64 * VE;
+        const bool full = vec && f0 + VE <= d;
+#pragma unroll
+        for (int i = 0; i < EG_BATCH; ++i)
+          x[h][i] = b0 + i < n && f0 < d
+                        ? eg_load<E>(G + readlane_i64(my_row, b0 + i) * d, f0, d, full)
+                        : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
-      for (int i = 0; i < VE; ++i) {
-        float x = n > 0 ? scale * acc[i] : 0.f;
-        if (accumulate) x += to_f32<GE>(o.e[i]);
-        o.e[i] = from_f32<GE>(x);
+      for (int i = 0; i < EG_BATCH; ++i) {
+        const int p = b0 + i;
+        if (p < n) {   // wave-uniform
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            typename EgVec<E>::U u;
+            u.u = x[h][i];
+#pragma unroll
+            for (int e = 0; e < VE; ++e) acc[h][e] += to_f32<E>(u.e[e]);
+          }
+          const int64_t id_p = readlane_i64(my_id, p);
+          const bool last_run = p == n - 1;
+          const bool ends = last_run || (p + 1 < EG_WIN && readlane_i64(my_id, p + 1) != id_p);
+          if (ends) {
+            float* pp = nullptr;
+            if (first_run && from_before)
+              pp = part + (w * 2) * d;        // began in an earlier window
+            else if (last_run && into_next)
+              pp = part + (w * 2 + 1) * d;    // continues into the next window
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int64_t f0 = fb + h * 64 * VE;
+              if (f0 < d) {
+                if (pp != nullptr) {
+#pragma unroll
+                  for (int e = 0; e < VE; ++e)
+                    if (f0 + e < d) pp[f0 + e] = acc[h][e];
+                } else {
+                  eg_store<GE, VE>(grad + id_p * d, f0, d, acc[h], scale, accumulate,
+                                   vec && f0 + VE <= d);
+                }
+              }
+#pragma unroll
+              for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
+            }
+            first_run = false;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Workgroup b looks at windows [16 b, 16 b + 16), one wave each: a window whose last run
+// began in it and continues into the next window hands that run over (in window order,
+// through LDS); the workgroup then takes the runs one by one: the run's partials part[w][1],
+// part[w + 1][0], ..., part[w_end][0] are split into 16 contiguous shares summed by the 16
+// waves, the shares combined in wave order, and the row written.
+constexpr int EG_COMBINE_WAVES = 16;
+
+template <class GE>
+__global__ void __launch_bounds__(EG_COMBINE_WAVES * 64) eg_combine_kernel(
+    const unsigned long long* __restrict__ sk, const int32_t* __restrict__ cnt, int64_t chunks,
+    const float* __restrict__ part, int64_t windows, int64_t d, float scale, int accumulate,
+    GE* __restrict__ grad) {
+  constexpr int NW = EG_COMBINE_WAVES, CB = 1024;   // waves; features per block
+  static_assert(NW * 64 == CB, "one feature of a block per thread");
+  __shared__ __attribute__((aligned(16))) float red[NW][CB];
+  __shared__ int64_t run_w[NW], run_end[NW], run_id[NW];
+  __shared__ int n_runs;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (threadIdx.x == 0) n_runs = 0;
+  __syncthreads();
+  const int64_t n_list = list_length(cnt, chunks);
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * NW + wid;
+  bool found = false;
+  int64_t id = 0, end = 0;
+  const int64_t r0 = w * EG_WIN;
+  if (w < windows && r0 + EG_WIN < n_list) {   // a next window exists
+    const int64_t r_last = r0 + EG_WIN - 1;
+    id = key_id(sk[r_last]);
+    // the last run continues, and began in this window (at r0 or after an id change)
+    if (key_id(sk[r_last + 1]) == id &&
+        !(key_id(sk[r0]) == id && r0 > 0 && key_id(sk[r0 - 1]) == id)) {
+      // the run's end: the first place past r_last with a larger id -- among the next 64
+      // places (one load per lane), else by binary search beyond them
+      const int64_t r = r_last + 1 + lane;
+      const unsigned long long past = __ballot(r >= n_list || key_id(sk[r]) != id);
+      if (past != 0) {
+        end = r_last + 1 + __builtin_ctzll(past);
+      } else {
+        int64_t lo = r_last + 65, hi = n_list;
+        const unsigned long long bnd =
+            (static_cast<unsigned long long>(id) << 32) | 0xffffffffull;
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (sk[mid] <= bnd) lo = mid + 1; else hi = mid;
+        }
+        end = lo;
+      }
+      found = true;
+    }
+  }
+  // A run of at most EG_LIGHT partials is summed by the wave that found it; longer runs are
+  // handed over in window order (wave v's run to slot = longer runs of waves below v) and
+  // summed by the whole workgroup.
+  constexpr int EG_LIGHT = 8;
+  const int64_t parts_found = found ? (end - 1) / EG_WIN - w + 1 : 0;
+  if (found && parts_found <= EG_LIGHT) {
+    GE* out = grad + id * d;
+    for (int64_t f = static_cast<int64_t>(lane) * 4; f < d; f += 256) {
+      float4 x[EG_LIGHT];
+#pragma unroll
+      for (int p = 0; p < EG_LIGHT; ++p) {
+        x[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p < parts_found) {
+          const float* src = part + ((w + p) * 2 + (p == 0 ? 1 : 0)) * d + f;
+          if ((d & 3) == 0) {
+            x[p] = *reinterpret_cast<const float4*>(src);
+          } else {
+            x[p].x = src[0];
+            if (f + 1 < d) x[p].y = src[1];
+            if (f + 2 < d) x[p].z = src[2];
+            if (f + 3 < d) x[p].w = src[3];
+          }
+        }
+      }
+      float t[4] = {x[0].x, x[0].y, x[0].z, x[0].w};
+#pragma unroll
+      for (int p = 1; p < EG_LIGHT; ++p) {
+        if (p < parts_found) {
+          t[0] += x[p].x;
+          t[1] += x[p].y;
+          t[2] += x[p].z;
+          t[3] += x[p].w;
+        }
       }
 #pragma unroll
-      for (int c = 0; c < NV; ++c) reinterpret_cast<uint4*>(out + f0)[c] = o.u[c];
-    } else {
-#pragma unroll
-      for (int i = 0; i < VE; ++i) {
-        if (f0 + i >= d) break;
-        float x = n > 0 ? scale * acc[i] : 0.f;
-        if (accumulate) x += to_f32<GE>(out[f0 + i]);
-        out[f0 + i] = from_f32<GE>(x);
+      for (int e = 0; e < 4; ++e) {
+        if (f + e >= d) break;
+        float v = scale * t[e];
+        if (accumulate) v += to_f32<GE>(out[f + e]);
+        out[f + e] = from_f32<GE>(v);
       }
+    }
+  }
+  const bool heavy = found && parts_found > EG_LIGHT;
+  __shared__ int flags[NW];
+  if (lane == 0) flags[wid] = heavy ? 1 : 0;
+  __syncthreads();
+  if (lane == 0 && heavy) {
+    int slot = 0;
+    for (int v = 0; v < wid; ++v) slot += flags[v];
+    run_w[slot] = w;
+    run_end[slot] = end;
+    run_id[slot] = id;
+    atomicAdd(&n_runs, 1);
+  }
+  __syncthreads();
+  const int runs = n_runs;
+  for (int r = 0; r < runs; ++r) {
+    const int64_t ws = run_w[r], rid = run_id[r];
+    const int64_t w_end = (run_end[r] - 1) / EG_WIN;   // window of the run's last place
+    const int64_t parts = w_end - ws + 1;   // part[ws][1], then part[ws + 1 .. w_end][0]
+    const int64_t share = (parts + NW - 1) / NW;
+    const int64_t p_begin = std::min<int64_t>(parts, wid * share);
+    const int64_t p_end = std::min<int64_t>(parts, p_begin + share);
+    GE* out = grad + rid * d;
+    const bool v4 = (d & 3) == 0;   // rows of whole float4s (part is 256-byte aligned)
+    // feature blocks of CB = 4 x 256: lane l owns features 4 l + 256 j, j < 4, so a partial
+    // row's block is one round of loads
+    for (int64_t c0 = 0; c0 < d; c0 += CB) {
+      float4 sum[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sum[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+      for (int64_t p = p_begin; p < p_end; ++p) {
+        const float* src = part + ((ws + p) * 2 + (p == 0 ? 1 : 0)) * d;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t f = c0 + 256 * j + lane * 4;
+          if (f >= d) continue;
+          if (v4) {
+            const float4 x = *reinterpret_cast<const float4*>(src + f);
+            sum[j].x += x.x;
+            sum[j].y += x.y;
+            sum[j].z += x.z;
+            sum[j].w += x.w;
+          } else {
+            sum[j].x += src[f];
+            if (f + 1 < d) sum[j].y += src[f + 1];
+            if (f + 2 < d) sum[j].z += src[f + 2];
+            if (f + 3 < d) sum[j].w += src[f + 3];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(&red[wid][256 * j + lane * 4]) = sum[j];
+      __syncthreads();
+      // the block's features, one per thread: shares added in wave order
+      const int e = threadIdx.x;
+      if (c0 + e < d) {
+        float t = red[0][e];
+        for (int v = 1; v < NW; ++v) t += red[v][e];
+        float x = scale * t;
+        if (accumulate) x += to_f32<GE>(out[c0 + e]);
+        out[c0 + e] = from_f32<GE>(x);
+      }
+      __syncthreads();
     }
   }
 }
 
 int64_t eg_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+struct EgPlan {
+  int64_t M, chunks, windows, present_words;
+};
+
+EgPlan eg_plan(int64_t M, int64_t vocab) {
+  EgPlan p;
+  p.M = M;
+  p.chunks = eg_cdiv(M, EG_CHUNK);
+  p.windows = eg_cdiv(M, EG_WIN);
+  p.present_words = eg_cdiv(vocab, 32);
+  return p;
+}
+
 template <class S>
-void carve_emb_grad(S& c, int64_t M, int64_t vocab, int32_t** cnt, int32_t** fill,
-                    int32_t** first, int32_t** base, int32_t** cursor, int32_t** list,
-                    int32_t** sorted, int32_t** segs) {
-  *cnt = c.template take<int32_t>(vocab);
-  *fill = c.template take<int32_t>(vocab);
-  *first = c.template take<int32_t>(vocab);
-  *base = c.template take<int32_t>(vocab);
-  *cursor = c.template take<int32_t>(2);
-  *list = c.template take<int32_t>(M);
-  *sorted = c.template take<int32_t>(M);
-  *segs = c.template take<int32_t>(M);
+void carve_emb_grad(S& c, const EgPlan& p, int64_t d, unsigned long long** ck,
+                    unsigned long long** sk, int32_t** cnt, uint32_t** present, float** part) {
+  *ck = c.template take<unsigned long long>(p.chunks * EG_CHUNK);
+  *sk = c.template take<unsigned long long>(p.M);
+  *cnt = c.template take<int32_t>(p.chunks);
+  *present = c.template take<uint32_t>(p.present_words);
+  *part = c.template take<float>(p.windows * 2 * d);
 }
 
 template <class E, class GE>
-int launch_rows(const void* G, const RowMap& tr, int64_t d, int64_t vocab, const int32_t* base,
-                const int32_t* cnt, const int32_t* sorted, const int32_t* segs,
-                const int32_t* nseg, float scale, int accumulate, int vec, void* grad,
-                hipStream_t s) {
-  // accumulate: at most one wave per train token (ids present); overwrite: one per row
-  const int64_t waves = accumulate ? std::min<int64_t>(tr.total(), vocab) : vocab;
-  hipLaunchKernelGGL((eg_rows_kernel<E, GE>),
+int launch_rows(const void* G, const RowMap& tr, int64_t d, int64_t vocab, const EgPlan& pl,
+                const unsigned long long* sk, const int32_t* cnt, const uint32_t* present,
+                float* part, float scale, int accumulate, int vec, void* grad, hipStream_t s) {
+  const int64_t zero_waves = accumulate ? 0 : eg_cdiv(vocab, 16);
+  const int64_t waves = pl.windows + zero_waves;
+  hipLaunchKernelGGL((eg_window_kernel<E, GE>),
                      dim3(static_cast<unsigned>(eg_cdiv(waves, EG_THREADS / 64))),
-                     dim3(EG_THREADS), 0, s, static_cast<const E*>(G), tr, d, vocab, base, cnt,
-                     sorted, segs, nseg, scale, accumulate, vec, static_cast<GE*>(grad));
-  return check_launch("eg_rows_kernel");
+                     dim3(EG_THREADS), 0, s, static_cast<const E*>(G), tr, d, vocab, sk, cnt,
+                     pl.chunks, present, pl.windows, scale, accumulate, vec, part,
+                     static_cast<GE*>(grad));
+  hipLaunchKernelGGL((eg_combine_kernel<GE>),
+                     dim3(static_cast<unsigned>(eg_cdiv(pl.windows, EG_COMBINE_WAVES))),
+                     dim3(EG_COMBINE_WAVES * 64), 0, s, sk, cnt, pl.chunks, part, pl.windows, d,
+                     scale, accumulate, static_cast<GE*>(grad));
+  return check_launch("eg_window_kernel / eg_combine_kernel");
 }
 
 }  // namespace
@@ -267,12 +658,15 @@ int launch_rows(const void* G, const RowMap& tr, int64_t d, int64_t vocab, const
 using namespace gs;
 
 extern "C" size_t gs_embedding_train_grad_workspace(int64_t N, int64_t n_val, int64_t T,
-                                                    int64_t vocab) {
-  if (N <= 0 || n_val < 0 || n_val >= N || T <= 0 || vocab <= 0) return 0;
+                                                    int64_t d, int64_t vocab) {
+  if (N <= 0 || n_val < 0 || n_val >= N || T <= 0 || d <= 0 || vocab <= 0) return 0;
+  const EgPlan pl = eg_plan((N - n_val) * T, vocab);
   Sizer sz;
-  int32_t *cnt, *fill, *first, *base, *cursor, *list, *sorted, *segs;
-  carve_emb_grad(sz, (N - n_val) * T, vocab, &cnt, &fill, &first, &base, &cursor, &list,
-                 &sorted, &segs);
+  unsigned long long *ck, *sk;
+  int32_t* cnt;
+  uint32_t* present;
+  float* part;
+  carve_emb_grad(sz, pl, d, &ck, &sk, &cnt, &present, &part);
   return sz.used + 256;
 }
 
@@ -291,45 +685,51 @@ extern "C" int gs_embedding_train_grad(const int64_t* ids, const void* G, int dt
   const int64_t M = (N - n_val) * T;
   if (M >= INT32_MAX || vocab >= INT32_MAX)
     return fail(GS_ERR_UNSUPPORTED, "gs_embedding_train_grad: 2^31 or more tokens or ids");
+  const EgPlan pl = eg_plan(M, vocab);
   Sizer sz;
-  int32_t *cnt, *fill, *first, *base, *cursor, *list, *sorted, *segs;
-  carve_emb_grad(sz, M, vocab, &cnt, &fill, &first, &base, &cursor, &list, &sorted, &segs);
+  unsigned long long *ck, *sk;
+  int32_t* cnt;
+  uint32_t* present;
+  float* part;
+  carve_emb_grad(sz, pl, d, &ck, &sk, &cnt, &present, &part);
   if (workspace == nullptr || workspace_bytes < sz.used)
     return fail(GS_ERR_WORKSPACE, "gs_embedding_train_grad: workspace too small");
   Carver cv(workspace, workspace_bytes);
-  carve_emb_grad(cv, M, vocab, &cnt, &fill, &first, &base, &cursor, &list, &sorted, &segs);
+  carve_emb_grad(cv, pl, d, &ck, &sk, &cnt, &present, &part);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const RowMap tr = train_rows(N, n_val, val_start, T);
-  const unsigned vb = static_cast<unsigned>(std::min<int64_t>(eg_cdiv(vocab, EG_THREADS), 4096));
-  const unsigned tb = static_cast<unsigned>(eg_cdiv(M, EG_THREADS));
-  hipLaunchKernelGGL(eg_clear_kernel, dim3(vb), dim3(EG_THREADS), 0, s, cnt, fill, first, cursor,
-                     vocab);
-  hipLaunchKernelGGL(eg_count_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, cnt,
-                     first);
-  hipLaunchKernelGGL(eg_alloc_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, cnt,
-                     first, cursor, base, segs);
-  hipLaunchKernelGGL(eg_place_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, base,
-                     fill, list);
-  hipLaunchKernelGGL(eg_order_kernel, dim3(tb), dim3(EG_THREADS), 0, s, ids, tr, vocab, base,
-                     cnt, list, sorted);
-  int rc = check_launch("embedding train-gradient grouping kernels");
+  const dim3 mgrid(static_cast<unsigned>(eg_cdiv(pl.chunks * EG_CHUNK, EG_THREADS)));
+  if (vocab <= EG_KEY32_VOCAB) {
+    uint32_t* ck32 = reinterpret_cast<uint32_t*>(ck);
+    hipLaunchKernelGGL(eg_sort_kernel<uint32_t>, dim3(static_cast<unsigned>(pl.chunks)),
+                       dim3(EG_SORT_THREADS), 0, s, ids, tr, vocab, ck32, cnt, present,
+                       pl.present_words);
+    hipLaunchKernelGGL(eg_merge_kernel<uint32_t>, mgrid, dim3(EG_THREADS), 0, s, ck32,
+                       pl.chunks, sk, present);
+  } else {
+    hipLaunchKernelGGL(eg_sort_kernel<unsigned long long>, dim3(static_cast<unsigned>(pl.chunks)),
+                       dim3(EG_SORT_THREADS), 0, s, ids, tr, vocab, ck, cnt, present,
+                       pl.present_words);
+    hipLaunchKernelGGL(eg_merge_kernel<unsigned long long>, mgrid, dim3(EG_THREADS), 0, s, ck,
+                       pl.chunks, sk, present);
+  }
+  int rc = check_launch("eg_sort_kernel / eg_merge_kernel");
   if (rc) return rc;
   const size_t esz = elem_size(dtype), gsz = elem_size(grad_dtype);
   const int vec = (reinterpret_cast<uintptr_t>(G) % 16 == 0) &&
                   (reinterpret_cast<uintptr_t>(grad) % 16 == 0) &&
                   (d * static_cast<int64_t>(esz)) % 16 == 0 &&
                   (d * static_cast<int64_t>(gsz)) % 16 == 0;
-  const int32_t* nseg = cursor + 1;
   const int acc = accumulate ? 1 : 0;
   if (dtype == GS_DTYPE_BF16)
     return grad_dtype == GS_DTYPE_BF16
-               ? launch_rows<uint16_t, uint16_t>(G, tr, d, vocab, base, cnt, sorted, segs, nseg,
+               ? launch_rows<uint16_t, uint16_t>(G, tr, d, vocab, pl, sk, cnt, present, part,
                                                  scale, acc, vec, grad, s)
-               : launch_rows<uint16_t, float>(G, tr, d, vocab, base, cnt, sorted, segs, nseg,
+               : launch_rows<uint16_t, float>(G, tr, d, vocab, pl, sk, cnt, present, part,
                                               scale, acc, vec, grad, s);
   return grad_dtype == GS_DTYPE_BF16
-             ? launch_rows<float, uint16_t>(G, tr, d, vocab, base, cnt, sorted, segs, nseg, scale,
+             ? launch_rows<float, uint16_t>(G, tr, d, vocab, pl, sk, cnt, present, part, scale,
                                             acc, vec, grad, s)
-             : launch_rows<float, float>(G, tr, d, vocab, base, cnt, sorted, segs, nseg, scale,
-                                         acc, vec, grad, s);
+             : launch_rows<float, float>(G, tr, d, vocab, pl, sk, cnt, present, part, scale, acc,
+                                         vec, grad, s);
 }

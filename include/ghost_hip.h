@@ -269,13 +269,17 @@ int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, int64_t N, in
  * Replaces _compute_embedding_train_grad (:214-235):
  *   grad[v] = scale * sum over the train tokens t with x_t = v of g_t     grad: [vocab, d]
  * (the reference: index_add_ of the N-scaled train rows into zeros_like(weight), then / n_t;
- * here scale = N / n_t carries both factors).  Rows are summed in fp32 in token order and
- * written once, so the result is deterministic and rounded once to grad_dtype.
+ * here scale = N / n_t carries both factors).  The train tokens are sorted by (id, token
+ * index); each id's rows are summed in fp32 in token order over windows of 16 places of the
+ * sorted list, a run that crosses windows by its window parts in window order, and written
+ * once, rounded once to grad_dtype: the same bits on every run, and work linear in the
+ * number of tokens however often an id repeats.
  * accumulate = 0: every row of grad is written (zeros where no train token has the id).
  * accumulate = 1: the rows of ids present are added to grad's contents, others untouched
  *   (a tied weight's Linear train gradient already there).
  * Ids outside [0, vocab) are skipped.  ids: [N, T] int64, G: [N, T, d] (dtype). */
-size_t gs_embedding_train_grad_workspace(int64_t N, int64_t n_val, int64_t T, int64_t vocab);
+size_t gs_embedding_train_grad_workspace(int64_t N, int64_t n_val, int64_t T, int64_t d,
+                                         int64_t vocab);
 int gs_embedding_train_grad(const int64_t* ids, const void* G, int dtype, int64_t N,
                             int64_t n_val, int64_t val_start, int64_t T, int64_t d,
                             int64_t vocab, float scale, void* grad, int grad_dtype,

@@ -139,6 +139,50 @@ def test_embedding_train_grad(gpu, gdt, odt, shape):
     assert_close(got, prev.double() + want, tol, "accumulate")
 
 
+@pytest.mark.parametrize("shape,pad_frac", [
+    # N, n_val, T, d, vocab
+    ((34, 2, 2048, 256, 50257), 0.9),   # 65536 train tokens, 90% one pad id
+    ((9, 1, 1000, 72, 40), 0.0),        # runs of ~200 tokens across many windows
+    ((3, 1, 4099, 8, 50257), 1.0),      # every train token the pad id, ragged T
+    ((5, 1, 900, 16, 2_000_000), 0.3),  # ids of 2^20 and above: 64-bit sort keys
+])
+def test_embedding_train_grad_heavy_ids(gpu, shape, pad_frac):
+    """Ids that repeat thousands of times (a padded batch): the sorted-list pipeline stays
+    linear in the token count (the call is timed against a generous bound) and sums each
+    run in a fixed order (bit-identical on a second run), against float64 index_add."""
+    import time
+    N, n_val, T, d, vocab = shape
+    ids = torch.randint(0, vocab, (N, T), generator=gen(90 + T))
+    pad = torch.rand(N, T, generator=gen(91 + T)) < pad_frac
+    ids[pad] = vocab - 1
+    G = randn((N, T, d), 92 + T, 1e-2, torch.bfloat16)
+    scale = N / (N - n_val)
+    print(f"embedding train grad heavy ids shape={shape} pad={pad_frac}", flush=True)
+    idd, Gd = ids.to(gpu), G.to(gpu)
+    out = torch.empty((vocab, d), dtype=torch.float32, device=gpu)
+    ops = _native.ops()
+    ops.embedding_train_grad(idd, Gd, n_val, scale, out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    again = torch.empty_like(out)
+    ops.embedding_train_grad(idd, Gd, n_val, scale, again)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    print(f"  one call {dt * 1e3:.2f} ms", flush=True)
+    assert dt < 0.05, f"{dt * 1e3:.1f} ms for {(N - n_val) * T} tokens"
+    assert torch.equal(again, out)
+    want, touched = _emb_grad_exact(ids, G, n_val, N - n_val, vocab, scale)
+    got = out.cpu()
+    assert_close(got, want, FP32_TOL, "heavy ids")
+    assert torch.all(got[~touched] == 0)
+    prev = randn((vocab, d), 93, 1e-2, torch.bfloat16)
+    acc = prev.to(gpu)
+    ops.embedding_train_grad(idd, Gd, n_val, scale, acc, accumulate=True)
+    got = acc.cpu()
+    assert torch.equal(got[~touched], prev[~touched])
+    assert_close(got, prev.double() + want, 1e-2, "heavy ids, accumulate")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(6, 2, 5, 24), (20, 4, 70, 768), (5, 1, 3, 2048), (4, 1, 2, 100),
                                    (3, 1, 130, 1024), (4, 2, 64, 1600), (20, 4, 1024, 768),

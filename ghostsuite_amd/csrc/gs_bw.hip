@@ -15,10 +15,7 @@ namespace gs {
 
 constexpr int BW_THREADS = 256;
 constexpr int TOK_CHUNK = 32;     // tokens per stage-1 block (bias, embedding)
-#ifndef GS_LN_TOK
-#define GS_LN_TOK 64
-#endif
-constexpr int LN_TOK_CHUNK = GS_LN_TOK;  // tokens per LayerNorm stage-1 block
+constexpr int LN_TOK_CHUNK = 64;  // tokens per LayerNorm stage-1 block
 
 template <class E>
 __device__ __forceinline__ float ld(const E* p) {
@@ -618,10 +615,7 @@ __global__ void __launch_bounds__(BW_THREADS) emb_key_kernel(
     ukeys[j] = j < n ? emb_key(ids, val, vocab, static_cast<int>(j)) : EMB_PAD;
 }
 
-#ifndef GS_EMB_RK
-#define GS_EMB_RK 4
-#endif
-constexpr int EMB_RK = GS_EMB_RK, EMB_RP = BW_THREADS / EMB_RK;
+constexpr int EMB_RK = 4, EMB_RP = BW_THREADS / EMB_RK;
 __global__ void __launch_bounds__(BW_THREADS) emb_rank_kernel(const uint32_t* __restrict__ ukeys,
                                                               int n,
                                                               uint32_t* __restrict__ keys) {

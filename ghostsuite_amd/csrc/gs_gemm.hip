@@ -290,22 +290,6 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned voff,
                : "memory");
 }
 constexpr unsigned DMA_OOB = 0xFFFFFFF0u;
-#ifndef GS_SCHED
-#define GS_SCHED 1
-#endif
-#ifndef GS_GROUP
-#define GS_GROUP 8
-#endif
-// Stage geometry of the DMA GEMMs whose tiles are too large for three 128-byte stages.
-#ifndef GS_WIDE_DMA
-#define GS_WIDE_DMA 128, 2
-#endif
-#ifndef GS_TN_SCHED
-#define GS_TN_SCHED 1
-#endif
-#ifndef GS_PF
-#define GS_PF 1
-#endif
 
 // Geometry of one LDS-DMA pipeline over the tile of config C: each stage holds ROWB bytes
 // (ROWB / 2 bf16 of K) of every L and R row.  The L rows cycle through NS slots and the R
@@ -435,7 +419,8 @@ __device__ __forceinline__ void dma_compute(const unsigned char* lslot, const un
   const int lo = D::swz(lane & 31), hi = lane >> 5;  // fragment rows start at multiples of 32
   const unsigned char* lt = lslot + (wm * 32 * C::MI + (lane & 31)) * D::ROW_BYTES;
   const unsigned char* rt = rslot + (wn * 32 * C::NI + (lane & 31)) * D::ROW_BYTES;
-  constexpr int NB = GS_PF + 1;  // fragment buffers: reads run GS_PF k-steps ahead
+  constexpr int AHEAD = 1;        // fragment reads run one k-step ahead of the MFMAs
+  constexpr int NB = AHEAD + 1;   // fragment buffers
   bf16x8_t a[NB][C::MI], b[NB][C::NI];
   auto load = [&](int buf, int ks) {
     const int off = ((2 * ks + hi) ^ lo) * 16;
@@ -447,10 +432,10 @@ __device__ __forceinline__ void dma_compute(const unsigned char* lslot, const un
       b[buf][j] = *reinterpret_cast<const bf16x8_t*>(rt + j * 32 * D::ROW_BYTES + off);
   };
 #pragma unroll
-  for (int ks = 0; ks < GS_PF && ks < D::KSTEPS; ++ks) load(ks, ks);
+  for (int ks = 0; ks < AHEAD && ks < D::KSTEPS; ++ks) load(ks, ks);
 #pragma unroll
   for (int ks = 0; ks < D::KSTEPS; ++ks) {
-    if (ks + GS_PF < D::KSTEPS) load((ks + GS_PF) % NB, ks + GS_PF);
+    if (ks + AHEAD < D::KSTEPS) load((ks + AHEAD) % NB, ks + AHEAD);
 #pragma unroll
     for (int i = 0; i < C::MI; ++i)
 #pragma unroll
@@ -458,12 +443,11 @@ __device__ __forceinline__ void dma_compute(const unsigned char* lslot, const un
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks % NB][i], b[ks % NB][j],
                                                             acc[i][j], 0, 0, 0);
   }
-#if GS_SCHED
-  // Instruction order for the scheduler: the first GS_PF k-steps' fragment reads, then
-  // each k-step's MFMAs with the reads GS_PF k-steps ahead interleaved one by one, so that
+  // Instruction order for the scheduler: the first AHEAD k-steps' fragment reads, then
+  // each k-step's MFMAs with the reads AHEAD k-steps ahead interleaved one by one, so that
   // LDS latency hides behind MFMAs instead of being waited out before each k-step.
   constexpr int R = C::MI + C::NI, M = C::MI * C::NI;
-  constexpr int PF = GS_PF < D::KSTEPS ? GS_PF : D::KSTEPS;
+  constexpr int PF = AHEAD < D::KSTEPS ? AHEAD : D::KSTEPS;
   __builtin_amdgcn_sched_group_barrier(0x100, R * PF, 0);
 #pragma unroll
   for (int ks = 0; ks + PF < D::KSTEPS; ++ks) {
@@ -476,7 +460,6 @@ __device__ __forceinline__ void dma_compute(const unsigned char* lslot, const un
     if constexpr (R > M) __builtin_amdgcn_sched_group_barrier(0x100, R - M, 0);
   }
   __builtin_amdgcn_sched_group_barrier(0x008, M * PF, 0);
-#endif
 }
 
 // The stage buffers: one __shared__ array of LDS_BYTES (the DMA is inline asm, so the
@@ -779,7 +762,7 @@ __device__ __forceinline__ int64_t xcd_order(int64_t w, int64_t total) {
 
 __device__ __forceinline__ void tile_of_block(int64_t m_tiles, int64_t n_tiles, int64_t& mt,
                                               int64_t& nt) {
-  constexpr int64_t GROUP = GS_GROUP;
+  constexpr int64_t GROUP = 8;
   const int64_t lid = xcd_order(blockIdx.x, gridDim.x);
   const int64_t per_group = GROUP * m_tiles;
   const int64_t g = lid / per_group;
@@ -1117,12 +1100,8 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
     store_epilogue<TrBF16, C>(p, acc, mt, nt);
   } else {
     float colsum[C::NI];
-    if constexpr (EPI == EPI_GHOST) {
-      f32x16_t acc2[C::MI][C::NI];
-      zero_acc<TrBF16, C>(acc2);
-      mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc2);
-      ghost_colsum<C>(p, acc, acc2, colsum);
-    } else if constexpr (EPI == EPI_ROWDOT_KS) {
+    static_assert(EPI != EPI_GHOST, "bf16 GHOST tiles take ghost_stash_kernel");
+    if constexpr (EPI == EPI_ROWDOT_KS) {
       // Every tile is whole along M and takes the LDS epilogue (checked by the host).
       constexpr int ZB = C::BN * C::BM * 2, RED = C::NT / 64;
       static_assert(ZB <= SB, "Z tile in LDS");
@@ -1823,7 +1802,6 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
                                                              fb[KR ? ks : ks % NB][jj],
                                                              acc[i][jj], 0, 0, 0);
   }
-#if GS_TN_SCHED
   // Instruction order: the first k-step's transpose reads, then each k-step's MFMAs with the
   // next k-step's reads (two per fragment) spread between them.
   constexpr int RD = 2 * (C::MI + C::NI), M = C::MI * C::NI;
@@ -1831,7 +1809,6 @@ __device__ __forceinline__ void tn_compute(const unsigned char* stage,
 #pragma unroll
   for (int ks = 0; ks + 1 < D::KSTEPS; ++ks) tn_sched_kstep<RD, M, 0>();
   __builtin_amdgcn_sched_group_barrier(0x008, M, 0);
-#endif
 }
 
 // rc[i] (+)= the column sums over a stage's k-rows of this wave's fragment i, from the F
@@ -2262,76 +2239,35 @@ __global__ void __launch_bounds__(256) tn_reduce_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------------------------ host side
-// Tile shapes per epilogue (overridable at build time for tuning sweeps).
-#ifndef GS_GHOST_TILE
-#define GS_GHOST_TILE 4, 2, 2, 2
-#endif
-#ifndef GS_ROWDOT_TILE
-#define GS_ROWDOT_TILE 2, 4, 4, 2
-#endif
-#ifndef GS_STORE_TILE
-#define GS_STORE_TILE 2, 2, 1, 1
-#endif
+// Tile shapes per epilogue.
 // bf16 GHOST through ghost_stash_kernel: 256x256 tiles, 8 waves of 128x64 (2x4 waves),
 // 128-byte stage rows, 2 L slots and 3 R slots (160 KiB of LDS).
-#ifndef GS_GHOST_STASH
-#define GS_GHOST_STASH 1
-#endif
-#ifndef GS_STASH_TILE
-#define GS_STASH_TILE 2, 4, 4, 2
-#endif
-#ifndef GS_STASH_DMA
-#define GS_STASH_DMA 128, 2, 3
-#endif
 // fp32 operands (precision checks, fp32 models) keep the small 128 x 128 tile.
 template <class Tr, int... Tile>
 using PickCfg = std::conditional_t<std::is_same<Tr, TrF32>::value, Cfg<Tr, 2, 2, 2, 2>,
                                    Cfg<Tr, Tile...>>;
-template <class Tr> using GhostCfg = PickCfg<Tr, GS_GHOST_TILE>;
-template <class Tr> using RowdotCfg = PickCfg<Tr, GS_ROWDOT_TILE>;
-template <class Tr> using StoreCfg = PickCfg<Tr, GS_STORE_TILE>;
-using StashCfg = Cfg<TrBF16, GS_STASH_TILE>;
-using StashDma = DmaCfg<StashCfg, GS_STASH_DMA>;
+template <class Tr> using GhostCfg = PickCfg<Tr, 4, 2, 2, 2>;
+template <class Tr> using RowdotCfg = PickCfg<Tr, 2, 4, 4, 2>;
+template <class Tr> using StoreCfg = PickCfg<Tr, 2, 2, 1, 1>;
+using StashCfg = Cfg<TrBF16, 2, 4, 4, 2>;
+using StashDma = DmaCfg<StashCfg, 128, 2, 3>;
 // Both bf16 GHOST kernels share the M tile, so the partial-sum layout (one row per M tile,
 // one column per train token) does not depend on which one runs.
 static_assert(StashCfg::BM == GhostCfg<TrBF16>::BM, "GHOST kernels must share BM");
 
 namespace {
 
-#ifndef GS_USE_DMA
-#define GS_USE_DMA 1
-#endif
 // Stage geometry of gemm_dma_kernel: three 128-byte-row stages when they fit in LDS; else
-// a third slot for one ring (GS_RDEEP 1: the R ring, 2: the L ring) when it fits beside the
-// epilogue's own LDS (`extra` bytes); else GS_WIDE_DMA.
-#ifndef GS_RDEEP
-#define GS_RDEEP 1
-#endif
-template <class C>
-using DmaDeep = std::conditional_t<GS_RDEEP == 2, DmaCfg<C, 128, 3, 2>, DmaCfg<C, 128, 2, 3>>;
+// two L slots and three R slots (the R operand streams from HBM) when they fit beside the
+// epilogue's own LDS (`extra` bytes; the K-side sums keep 3 NW x 64 floats); else two and
+// two.
 template <class C, int extra = 0>
 using DmaFor = std::conditional_t<
     3 * (C::BM + C::BN) * 128 <= 160 * 1024, DmaCfg<C, 128, 3>,
-    std::conditional_t<GS_RDEEP && DmaDeep<C>::LDS_BYTES + extra <= 160 * 1024, DmaDeep<C>,
-                       DmaCfg<C, GS_WIDE_DMA>>>;
-// The row-dot kernel's stage geometry (GS_ROWDOT_DMACFG = row bytes, stages) or DmaFor; the
-// K-side sums keep 3 NW x 64 floats of LDS beside the rings.
+    std::conditional_t<DmaCfg<C, 128, 2, 3>::LDS_BYTES + extra <= 160 * 1024,
+                       DmaCfg<C, 128, 2, 3>, DmaCfg<C, 128, 2>>>;
 template <class C, int EPI>
-using DmaForAuto = DmaFor<C, EPI == EPI_ROWDOT_KS ? 3 * C::WM * C::WN * 64 * 4 : 0>;
-#ifdef GS_ROWDOT_DMACFG
-template <class C, int EPI>
-using DmaForEpi = std::conditional_t<EPI == EPI_ROWDOT || EPI == EPI_ROWDOT_KS,
-                                     DmaCfg<C, GS_ROWDOT_DMACFG>, DmaForAuto<C, EPI>>;
-#else
-template <class C, int EPI>
-using DmaForEpi = DmaForAuto<C, EPI>;
-#endif
-#ifndef GS_ROWDOT_DMA
-#define GS_ROWDOT_DMA 1
-#endif
-#ifndef GS_STORE_DMA
-#define GS_STORE_DMA 1
-#endif
+using DmaForEpi = DmaFor<C, EPI == EPI_ROWDOT_KS ? 3 * C::WM * C::WN * 64 * 4 : 0>;
 
 bool dma_ok(const Operand& o) { return o.vec_ok && o.nbytes > 0 && o.nbytes < INT32_MAX; }
 
@@ -2344,14 +2280,11 @@ struct Launch {
     if (blocks > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
     const dim3 grid(static_cast<unsigned>(blocks)), block(C::NT);
     using D = DmaForEpi<C, EPI>;
-    if constexpr (std::is_same<Tr, TrBF16>::value &&
+    // bf16 GHOST tiles take ghost_stash_kernel when they qualify for the LDS-DMA path, so
+    // a GHOST call here goes to the register-staged kernel.
+    if constexpr (std::is_same<Tr, TrBF16>::value && EPI != EPI_GHOST &&
                   D::LDS_BYTES <= 160 * 1024) {
-      const bool on = EPI == EPI_GHOST ||
-                      ((EPI == EPI_ROWDOT || EPI == EPI_ROWDOT_KS) && GS_ROWDOT_DMA) ||
-                      (EPI == EPI_STORE && GS_STORE_DMA);
-      const bool dma = GS_USE_DMA && on && aligned &&
-                       dma_ok(p.L1) && dma_ok(p.R1) &&
-                       (EPI != EPI_GHOST || (dma_ok(p.L2) && dma_ok(p.R2)));
+      const bool dma = aligned && dma_ok(p.L1) && dma_ok(p.R1);
       if (dma) {
         hipLaunchKernelGGL((gemm_dma_kernel<C, D, EPI>), grid, block, 0, s, p);
         return check_launch("gemm_dma_kernel");
@@ -2422,24 +2355,17 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // divides d_out and fills whole waves of 256 workgroups better (fc_out / proj with d_out 768:
 // 256 tiles instead of 192; qkv with 2304: 768 instead of 576).  `full`: every tile must be
 // whole along d_out (the fused bias pass), so 256 only when it divides d_out.
-#ifndef GS_ROWDOT192
-#define GS_ROWDOT192 1
-#endif
-#ifndef GS_ROWDOT192_TILE
-#define GS_ROWDOT192_TILE 2, 4, 3, 2
-#endif
-using RowdotCfg192 = Cfg<TrBF16, GS_ROWDOT192_TILE>;
-// The K-side-sum row-dot (one feature per lane, 8 per wave) keeps 8 waves.
-using RowdotCfg192K = Cfg<TrBF16, 2, 4, 3, 2>;
-static_assert(RowdotCfg192K::BM == RowdotCfg192::BM && RowdotCfg192K::BN == RowdotCfg192::BN,
-              "both 192-row tiles share the tile shape");
+// 8 waves of 96 x 64 (the K-side-sum row-dot needs 8 waves: one feature per lane, 8 per
+// wave).
+using RowdotCfg192 = Cfg<TrBF16, 2, 4, 3, 2>;
+using RowdotCfg192K = RowdotCfg192;
 template <class Tr>
 int64_t rowdot_bm(int64_t d_out, int64_t n_tiles, bool full) {
   constexpr int64_t B = RowdotCfg<Tr>::BM, B2 = RowdotCfg192::BM;
   if constexpr (!std::is_same<Tr, TrBF16>::value) {
     return B;
   } else {
-    const bool ok2 = GS_ROWDOT192 && d_out % B2 == 0;
+    const bool ok2 = d_out % B2 == 0;
     if (!ok2) return B;
     if (full && d_out % B != 0) return B2;
     auto fill = [&](int64_t bm) {
@@ -2451,25 +2377,13 @@ int64_t rowdot_bm(int64_t d_out, int64_t n_tiles, bool full) {
 }
 
 // The K-major val-term GEMM (tn_gemm_kernel): tile shape, stage geometry and split count
-// (GS_TN_SPLIT 0 = chosen by the estimate in tn_splits).
-#ifndef GS_TN_TILE
-#define GS_TN_TILE 2, 2, 2, 2
-#endif
-#ifndef GS_TN_STAGE
-#define GS_TN_STAGE 64, 2
-#endif
-#ifndef GS_TN_SPLIT
-#define GS_TN_SPLIT 0
-#endif
-#ifndef GS_USE_TN
-#define GS_USE_TN 1
-#endif
-using TnC = Cfg<TrBF16, GS_TN_TILE>;
-using TnD = TnCfg<TnC, GS_TN_STAGE>;
+// (chosen by the estimate in tn_splits).
+using TnC = Cfg<TrBF16, 2, 2, 2, 2>;
+using TnD = TnCfg<TnC, 64, 2>;
 
 bool tn_ok(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K, int64_t M,
            int64_t N) {
-  if (!GS_USE_TN || K <= 0 || M <= 0 || N <= 0) return false;
+  if (K <= 0 || M <= 0 || N <= 0) return false;
   if (ldl % 8 || ldr % 8 || M % 8 || N % 8) return false;
   if (K * ldl * 2 >= INT32_MAX || K * ldr * 2 >= INT32_MAX) return false;
   return L == nullptr || (aligned16(L) && aligned16(R));
@@ -2488,7 +2402,6 @@ int64_t tn_kper(int64_t K, int sp) {
 }
 int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
   const int64_t ksteps = ceil_div(K, static_cast<int64_t>(TnD::KB));
-  if (GS_TN_SPLIT > 0) return static_cast<int>(std::min<int64_t>(GS_TN_SPLIT, ksteps));
   const int64_t tiles = ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN);
   int best = 1;
   double best_t = 1e30;
@@ -2595,12 +2508,9 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
 
 // The VALGRAD row-dot contracts over the longer feature dimension (bf16): with d_out > d_in
 // it computes sum_t <a_t, V^T g_t>, whose GEMM has the longer K and the narrower Z.
-#ifndef GS_ROWDOT_SWAP
-#define GS_ROWDOT_SWAP 1
-#endif
 template <class Tr>
 bool rowdot_swap(int64_t d_in, int64_t d_out) {
-  return GS_ROWDOT_SWAP && std::is_same<Tr, TrBF16>::value && d_out > d_in && d_in % 8 == 0 &&
+  return std::is_same<Tr, TrBF16>::value && d_out > d_in && d_in % 8 == 0 &&
          d_out % 8 == 0;
 }
 template <class Tr>
@@ -2850,7 +2760,7 @@ int run_linear(const void* A, const void* G, int64_t N, int64_t n_val, int64_t v
     const bool al = p.L1.vec_ok && p.R1.vec_ok && p.L2.vec_ok && p.R2.vec_ok;
     bool stash = false;
     if constexpr (std::is_same<Tr, TrBF16>::value)
-      stash = GS_GHOST_STASH && al && dma_ok(p.L1) && dma_ok(p.R1) && dma_ok(p.L2) &&
+      stash = al && dma_ok(p.L1) && dma_ok(p.R1) && dma_ok(p.L2) &&
               dma_ok(p.R2);
     // Partials: one per (M tile, N tile) when N tiles never straddle samples, else one per
     // (M tile, train token); the workspace holds the larger layout.
@@ -3550,8 +3460,8 @@ namespace {
 bool rowdot_bias_ok(int dtype, const void* A, const void* G, const void* V, int64_t N,
                     int64_t T, int64_t d_in, int64_t d_out) {
   using RC = RowdotCfg<TrBF16>;
-  if (dtype != GS_DTYPE_BF16 || !GS_USE_DMA || !GS_ROWDOT_DMA) return false;
-  const bool whole = d_out % RC::BM == 0 || (GS_ROWDOT192 && d_out % RowdotCfg192::BM == 0);
+  if (dtype != GS_DTYPE_BF16) return false;
+  const bool whole = d_out % RC::BM == 0 || d_out % RowdotCfg192::BM == 0;
   if (T % RC::BN != 0 || !whole || d_in % 8 != 0 || d_out % 8 != 0) return false;
   const int64_t ga = N * T * d_in * 2, gg = N * T * d_out * 2, gv = d_out * d_in * 2;
   if (ga >= INT32_MAX || gg >= INT32_MAX || gv >= INT32_MAX) return false;
@@ -3568,9 +3478,6 @@ namespace {
 // The fused pass contracts over the longer feature dimension.  With d_out > d_in (swap) it
 // runs over K = d_out: L = V^T [d_in][d_out], R = the train rows of G, Z = the train rows of
 // A, and the bias column sums come from the R stages (EPI_ROWDOT_KS), so the M tiles span d_in.
-#ifndef GS_BIAS_SWAP
-#define GS_BIAS_SWAP 1
-#endif
 struct RowdotBiasPlan {
   RowdotPlan pl;
   int64_t n_t, n_tiles;
@@ -3578,7 +3485,7 @@ struct RowdotBiasPlan {
   int64_t bp_rows;  // rows of BP: n_tiles, or with swap m tiles x n_tiles
 };
 bool bias_swap(int dtype, int64_t N, int64_t T, int64_t d_in, int64_t d_out) {
-  return GS_BIAS_SWAP && d_out > d_in &&
+  return d_out > d_in &&
          rowdot_bias_ok(dtype, nullptr, nullptr, nullptr, N, T, d_out, d_in);
 }
 RowdotBiasPlan plan_rowdot_bias(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in,

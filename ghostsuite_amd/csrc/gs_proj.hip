@@ -29,14 +29,8 @@ namespace gs {
 typedef __bf16 bf16x8p_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-#ifndef GS_PJ_TOK
-#define GS_PJ_TOK 64
-#endif
-#ifndef GS_PJ_THREADS
-#define GS_PJ_THREADS 512
-#endif
-constexpr int PJ_TOK = GS_PJ_TOK;  // tokens per workgroup
-constexpr int PJ_THREADS = GS_PJ_THREADS;
+constexpr int PJ_TOK = 64;  // tokens per workgroup
+constexpr int PJ_THREADS = 512;
 constexpr int PJ_KMAX = 64;     // projection rows per side of one launch
 
 struct PjBF16 {
@@ -79,9 +73,6 @@ __device__ __forceinline__ uint4 lane_load(const typename Tr::E* row, int64_t k,
   return u.v;
 }
 
-#ifndef GS_PJ_U
-#define GS_PJ_U 1
-#endif
 constexpr int PJ_WAVES = PJ_THREADS / 64;
 constexpr int PJ_TG = PJ_TOK / 16;  // 16-token MFMA row groups per workgroup
 
@@ -101,7 +92,7 @@ __device__ __forceinline__ void project_rows(const typename Tr::E* const (&rows)
   for (int nb = 0; nb < NB; ++nb)
     prow[nb] = 16 * nb + (lane & 15) < kP ? P + static_cast<int64_t>(16 * nb + (lane & 15)) * n
                                           : nullptr;
-  constexpr int U = GS_PJ_U;  // k-steps of loads in flight (x PJ_TG rows)
+  constexpr int U = 1;  // k-steps of loads in flight (x PJ_TG rows)
   // The waves interleave in pieces of U k-steps, so a workgroup reads one contiguous run
   // of PJ_WAVES pieces of every row at a time.
   const int64_t f_step = static_cast<int64_t>(PJ_WAVES) * U * Tr::KSTEP;

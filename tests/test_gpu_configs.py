@@ -220,6 +220,73 @@ def test_config1_reference_sequence_t1024(gpu):
     assert_close(dot, want, 2e-3, "ghost reference rounding")
 
 
+# ------------------------------------------------------------------ configs[2] samplers
+def test_config2_reference_sequences_gpt2_shapes(gpu):
+    """Every GPT-2-small sampler the step runs, at its full shape (16 train + 4 val rows,
+    T = 1024, bf16, reference layout), against the reference's own op sequence rather than
+    the float64 forms: the fused dot + train-gradient op on fc / fc_out (the reference's
+    ghost branch: bf16 Gram products, bf16 Hadamard product, fp32 sums; 2-D products on the
+    GPU) and on qkv / proj (its materialised branch: per-sample gradients and the presummed
+    val gradient in bf16, on the CPU), the HF Conv1D form on c_fc (ghost branch) and c_attn
+    (materialised; presum in both, all bf16), bias dots alike, the Embedding on wte and wpe
+    (bf16 index_add_ table, bf16 gather-product) and LayerNorm weight / bias dots (bf16
+    layer_norm), each within the bf16 tolerance, with the distances printed."""
+    from ghostsuite_amd import _native as NV
+    N, n_val, T = 20, 4, 1024
+    n_t = N - n_val
+    ops = NV.ops()
+    dist = {}
+
+    def check(name, got, want):
+        dist[name] = assert_close(got.float().cpu(), want.float().cpu(), BF16_TOL, name)
+
+    for name, d_in, d_out, seed in (("fc", 768, 3072, 300), ("fc_out", 3072, 768, 302),
+                                    ("qkv", 768, 2304, 304), ("proj", 768, 768, 306)):
+        ghost = R.should_use_ghost(T, d_in * d_out)
+        assert ghost == (name in ("fc", "fc_out"))
+        A = randn((N, T, d_in), seed, 1.0, BF16)
+        G = randn((N, T, d_out), seed + 1, 1e-3, BF16)
+        _say(f"config2 reference sequence {name}")
+        dot, _, bdot, _ = ops.linear_dot_train_grad(
+            A.to(gpu), G.to(gpu), n_val,
+            semantics=NV.SEM_PAIRWISE_SUM if ghost else NV.SEM_PRESUM,
+            grad_scale=N / n_t, bias=True, bias_grad_scale=N / n_t)
+        torch.cuda.synchronize()
+        if ghost:
+            w, b = R.linear_dot_ref(A.to(gpu), G.to(gpu), n_val, use_ghost=True)
+        else:
+            w, b = R.linear_dot_ref(A, G, n_val, use_ghost=False)
+        check(f"{name} weight", dot, w)
+        check(f"{name} bias", bdot, b)
+    for name, d_in, d_out, seed in (("c_fc", 768, 3072, 310), ("c_attn", 768, 2304, 312)):
+        A = randn((N, T, d_in), seed, 1.0, BF16)
+        G = randn((N, T, d_out), seed + 1, 1e-3, BF16)
+        _say(f"config2 reference sequence Conv1D {name}")
+        dot, _, bdot, _ = ops.linear_dot_train_grad(
+            A.to(gpu), G.to(gpu), n_val, semantics=NV.SEM_PRESUM, grad_scale=N / n_t,
+            bias=True, bias_grad_scale=N / n_t, conv1d=True)
+        torch.cuda.synchronize()
+        w, b = R.conv1d_dot_ref(A, G, n_val, R.should_use_ghost(T, d_in * d_out))
+        check(f"{name} weight", dot, w)
+        check(f"{name} bias", bdot, b)
+    G = randn((N, T, 768), 320, 1e-3, BF16)
+    for name, ids, vocab in (("wte", torch.randint(0, 50257, (N, T), generator=gen(321)), 50257),
+                             ("wpe", torch.arange(T).repeat(N, 1), T)):
+        _say(f"config2 reference sequence embedding {name}")
+        dot = ops.embedding_dot(ids.to(gpu), G.to(gpu), n_val, vocab)
+        torch.cuda.synchronize()
+        check(name, dot, R.embedding_dot_ref(ids, G, n_val, vocab))
+    X = randn((N, T, 768), 322, 1.0, BF16)
+    _say("config2 reference sequence layernorm")
+    dw, db, _, _ = ops.layernorm_dot(X.to(gpu), G.to(gpu), n_val, 1e-5)
+    torch.cuda.synchronize()
+    w, b = R.layernorm_dot_ref(X, G, n_val, 1e-5)
+    check("layernorm weight", dw, w)
+    check("layernorm bias", db, b)
+    print("normwise distances to the reference sequence: " +
+          ", ".join(f"{k} {v:.2e}" for k, v in dist.items()), flush=True)
+
+
 # ------------------------------------------------------------------ configs[0]
 @pytest.mark.parametrize("precision,tol", [("fp32", FP32_TOL), ("reference", BF16_TOL)])
 def test_config0_mlp_ten_steps(gpu, precision, tol):

@@ -3,14 +3,15 @@ functions whose results no closed form, brute-force check or invariant fixes bit
 
 Run in the build container only (the reference is not present on the GPU box):
 
-    python tests/golden/make_golden.py /root/reference
+    PYTHONDONTWRITEBYTECODE=1 python tests/golden/make_golden.py /root/reference
 
 What is recorded (all on the CPU, small seeded inputs, the reference imported unchanged):
   - the bf16 rounding sequences of the GradDotProd samplers
     (ghostEngines/supported_layers_grad_samplers_dotprod.py): _compute_linear_dot_product in
     both branches (:75-146), _compute_embedding_dot_product (:181-211),
     _compute_layernorm_dot_product (:242-300), _compute_Conv1D_dot_product in both branches
-    (:369-471), each with fp32 and bf16 inputs;
+    (:369-471), _compute_conv2d_dot_product's materialised branch (:513-563), each with fp32
+    and bf16 inputs;
   - GradDotProdEngine's aggregation and routing with real hook firing order
     (graddotprod_engine.py:131-230, autograd_grad_sample_dotprod.py:23-222) on a small model
     whose output Linear is tied to its input Embedding (the Embedding's later assignment
@@ -87,6 +88,19 @@ def _sampler_vectors(S):
                     "A": A, "B": B, "n_val": 3,
                     "dot": conv.weight.grad_dot_prod.detach().clone(),
                     "bias_dot": conv.bias.grad_dot_prod.detach().clone()}
+        # Conv2d, the materialised branch (the ghost branch multiplies [d, d] by [p, p]
+        # blocks and needs C_in kh kw == C_out): bf16 unfold, per-sample gradients and the
+        # presummed val gradient by einsum, their dot; bias dot alike.
+        conv2 = nn.Conv2d(3, 4, kernel_size=3, padding=1, stride=2)
+        conv2.use_ghost_computation = False
+        A = _randn((6, 3, 8, 8), 18).to(dt)
+        B = _randn((6, 4, 4, 4), 19, 1e-2).to(dt)
+        S._compute_conv2d_dot_product(conv2, A, B, 2)
+        out[f"conv2d_mat_{dt_name}"] = {
+            "A": A, "B": B, "n_val": 2, "kernel_size": 3, "padding": 1, "stride": 2,
+            "dilation": 1,
+            "dot": conv2.weight.grad_dot_prod.detach().clone(),
+            "bias_dot": conv2.bias.grad_dot_prod.detach().clone()}
     return out
 
 
@@ -170,6 +184,7 @@ def _hashes(ref_root):
 
 
 def main(ref_root):
+    sys.dont_write_bytecode = True   # nothing is written under the reference tree
     sys.path.insert(0, ref_root)
     import transformers
     from ghostEngines import supported_layers_grad_samplers_dotprod as S

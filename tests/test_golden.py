@@ -46,7 +46,7 @@ def test_vectors_present_and_from_the_reference(golden):
     meta = golden["meta"]
     assert set(meta["sha256"]) >= {"ghostEngines/supported_layers_grad_samplers_dotprod.py",
                                    "ghostEngines/graddotprod_engine.py"}
-    assert len(golden["samplers"]) == 22 and len(golden["projection"]) == 3
+    assert len(golden["samplers"]) == 24 and len(golden["projection"]) == 3
 
 
 def test_linear_reference_sequence_bits(golden):
@@ -62,6 +62,21 @@ def test_linear_reference_sequence_bits(golden):
                      f"{name} exact")
         assert_close(R.bias_dot_exact(c["B"], c["n_val"]), c["bias_dot"],
                      BF16_TOL if c["B"].dtype == torch.bfloat16 else 1e-5, f"{name} bias exact")
+
+
+def test_conv2d_reference_sequence_bits(golden):
+    """The reference's Conv2d materialised branch (all bf16) against conv2d_dot_ref bit for
+    bit, and the float64 presum form within the bf16 tolerance."""
+    torch.set_num_threads(1)
+    cases = _cases(golden, "conv2d_")
+    assert sorted(cases) == ["conv2d_mat_bf16", "conv2d_mat_fp32"]
+    for name, c in cases.items():
+        conv = {k: c[k] for k in ("kernel_size", "padding", "stride", "dilation")}
+        w, b = R.conv2d_dot_ref(c["A"], c["B"], c["n_val"], conv)
+        _bitwise_or_one_step(w, c["dot"], f"{name} weight")
+        _bitwise_or_one_step(b, c["bias_dot"], f"{name} bias")
+        assert_close(R.conv2d_dot_exact(c["A"], c["B"], c["n_val"], conv), c["dot"], BF16_TOL,
+                     f"{name} exact")
 
 
 def test_embedding_reference_sequence_bits(golden):

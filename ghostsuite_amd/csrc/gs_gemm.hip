@@ -3114,6 +3114,48 @@ bool plan_train_grad(const void* A, const void* G, int64_t N, int64_t n_val, int
 }  // namespace
 }  // namespace gs
 
+namespace gs {
+namespace {
+// Outputs of many tiles (the 50k-row lm_head or embed_out of a tied or untied language-model
+// head, the Pythia-1B MLP): 256 x 256 tiles of 8 waves of 128 x 64 and no split, since the
+// tiles alone fill the chip.  Per flop they read a quarter fewer MFMA fragment bytes from LDS
+// than 64 x 64 wave tiles and half the stage bytes (one 128 KiB workgroup per CU).
+using TnCW = Cfg<TrBF16, 2, 4, 4, 2>;
+using TnDW = TnCfg<TnCW, 64, 2>;
+constexpr int64_t TN_WIDE_MIN_TILES = 256;
+bool tn_wide(int64_t M, int64_t N) {
+  return ceil_div(M, TnCW::BM) * ceil_div(N, TnCW::BN) >= TN_WIDE_MIN_TILES;
+}
+int launch_tn_wide(const TrainGradPlan& t, void* out, hipStream_t s) {
+  TnParams p{};
+  p.L = t.L;
+  p.R = t.R;
+  p.ldl = t.ldl;
+  p.ldr = t.ldr;
+  const int64_t rows = t.o.gap_at < t.K ? t.K + t.o.gap : t.K;
+  p.l_nbytes = rows * t.ldl * 2;
+  p.r_nbytes = rows * t.ldr * 2;
+  p.gap_at = t.o.gap_at;
+  p.gap = t.o.gap;
+  p.K = t.K;
+  p.kper = t.K;
+  p.M = t.M;
+  p.N = t.N;
+  p.m_tiles = ceil_div(t.M, TnCW::BM);
+  p.n_tiles = ceil_div(t.N, TnCW::BN);
+  p.part_out = 0;
+  p.alpha = t.o.alpha;
+  p.out_f32 = t.o.out_f32;
+  p.out = out;
+  const int64_t items = p.m_tiles * p.n_tiles;
+  if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
+  hipLaunchKernelGGL((tn_gemm_kernel<TnCW, TnDW, 0>), dim3(static_cast<unsigned>(items)),
+                     dim3(TnCW::NT), 0, s, p);
+  return check_launch("tn_gemm_kernel (256 x 256 tiles)");
+}
+}  // namespace
+}  // namespace gs
+
 extern "C" size_t gs_linear_train_grad_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,
                                                  int64_t d_in, int64_t d_out) {
   if (dtype != GS_DTYPE_BF16 || N <= 0 || n_val < 0 || n_val >= N || T <= 0 || d_in <= 0 ||
@@ -3151,6 +3193,7 @@ extern "C" int gs_linear_train_grad(const void* A, const void* G, int dtype, int
   const size_t need = gs_linear_train_grad_workspace(dtype, N, n_val, T, d_in, d_out);
   if (workspace == nullptr || workspace_bytes < need - 256)
     return fail(GS_ERR_WORKSPACE, "gs_linear_train_grad: workspace too small");
+  if (tn_wide(t.M, t.N)) return launch_tn_wide(t, out, static_cast<hipStream_t>(stream));
   Carver cv(workspace, workspace_bytes);
   float* part = cv.take<float>(tn_part_elems(t.K, t.M, t.N));
   return launch_tn(t.L, t.ldl, t.R, t.ldr, t.K, t.M, t.N, out, part,

@@ -278,12 +278,15 @@ def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tenso
     return _scaled_mm(B_tr.t(), A_tr, scale / n_t)
 
 
-# Output tiles (128 x 128) below which the K-major train-gradient GEMM beats hipBLASLt:
-# with fewer tiles than CUs the product is a long-K, small-output GEMM that the K-major kernel
-# splits over the token rows (GPT-2-small: fc / fc_out 85-88 us against 152-160 us through
-# torch.addmm, proj 31 against 98), while outputs of 256 tiles and more (Pythia-1B layers,
-# the 50k-row lm_head) run faster through hipBLASLt (e.g. 2048x8192: 506 against 572 us).
+# Where the K-major train-gradient GEMM beats hipBLASLt (measured on MI355X, 16k-32k train
+# token rows): below 256 output tiles of 128 x 128 it splits the long token contraction
+# (GPT-2-small fc / fc_out 85-88 us against 152-160 us through torch.addmm, proj 31 against
+# 98); from 256 tiles of 256 x 256 up its wide-tile kernel fills the chip without a split
+# (Pythia-1B fc / fc_out 430-443 us against 505-511, embed_out 2851 against 3085); in between
+# (e.g. 2048 x 6144: 470 against 354 us) hipBLASLt is faster.  The GPT-2 lm_head (50257
+# columns) is not 16-byte aligned and takes hipBLASLt either way.
 _TRAIN_GRAD_MAX_TILES = 256
+_TRAIN_GRAD_WIDE_TILES = 256
 
 
 def _native_train_grad(A: torch.Tensor, B: torch.Tensor, val_batch_size: int, alpha: float,
@@ -291,11 +294,13 @@ def _native_train_grad(A: torch.Tensor, B: torch.Tensor, val_batch_size: int, al
     """The weight's train gradient from the K-major GEMM over the train rows as they lie
     (gs_linear_train_grad: fp32 accumulation, alpha before the one rounding, in A's dtype);
     None where that kernel does not apply (fp32 operands, unaligned or >2 GiB rows) or where
-    hipBLASLt is faster (outputs of _TRAIN_GRAD_MAX_TILES tiles and more)."""
+    hipBLASLt is faster (from _TRAIN_GRAD_MAX_TILES tiles of 128 x 128 to below
+    _TRAIN_GRAD_WIDE_TILES tiles of 256 x 256)."""
     if A.dtype != torch.bfloat16 or A.dim() < 2:
         return None
     tiles = math.ceil(A.shape[-1] / 128) * math.ceil(B.shape[-1] / 128)
-    if tiles >= _TRAIN_GRAD_MAX_TILES:
+    wide = math.ceil(A.shape[-1] / 256) * math.ceil(B.shape[-1] / 256)
+    if _TRAIN_GRAD_MAX_TILES <= tiles and wide < _TRAIN_GRAD_WIDE_TILES:
         return None
     B = B if B.dtype == A.dtype else B.to(A.dtype)
     return ops().linear_train_grad(A, B, val_batch_size, alpha,

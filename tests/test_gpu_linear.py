@@ -341,6 +341,8 @@ def _train_grad_want(A, G, n_val, vs, scale, conv1d, dev):
     (20, 4, 1024, 768, 3072, "last"), (20, 4, 1024, 3072, 768, "last"),
     (20, 4, 1024, 768, 2304, "mid"), (20, 4, 1024, 768, 768, "first"),
     (10, 2, 2048, 2048, 8192, "last"),
+    # 256 or more 256 x 256 output tiles: the wide-tile kernel (edge tiles, val block inside)
+    (3, 1, 256, 4104, 4096, "mid"), (4, 2, 192, 8192, 2056, "first"),
 ])
 @pytest.mark.parametrize("conv1d", [False, True])
 def test_linear_train_grad(gpu, out_dtype, case, conv1d):
@@ -382,13 +384,18 @@ def test_linear_train_grad_declines_and_sampler_falls_back(gpu):
     G3 = randn((4, 32, 24), 100, 1e-3, torch.bfloat16).to(gpu)
     got = _compute_linear_train_grad(torch.nn.Linear(40, 24), A3, G3, 1, scale=2.0)
     assert torch.equal(got, ops.linear_train_grad(A3, G3, 1, 2.0 / 3))
-    # 256 output tiles and more: hipBLASLt through addmm (faster there).
+    # 256 to 1023 output tiles of 128 x 128: hipBLASLt through addmm (faster there).
     from ghostsuite_amd.supported_layers_grad_samplers_dotprod import _scaled_mm
     A4 = randn((3, 8, 2048), 101, 1.0, torch.bfloat16).to(gpu)
     G4 = randn((3, 8, 2048), 102, 1e-3, torch.bfloat16).to(gpu)
     got = _compute_linear_train_grad(torch.nn.Linear(2048, 2048), A4, G4, 1, scale=2.0)
     want = _scaled_mm(G4[:2].reshape(-1, 2048).t(), A4[:2].reshape(-1, 2048), 1.0)
     assert torch.equal(got, want)
+    # 256 tiles of 256 x 256 and more: the wide-tile kernel again.
+    A5 = randn((3, 16, 2048), 103, 1.0, torch.bfloat16).to(gpu)
+    G5 = randn((3, 16, 8192), 104, 1e-3, torch.bfloat16).to(gpu)
+    got = _compute_linear_train_grad(torch.nn.Linear(2048, 8192), A5, G5, 1, scale=2.0)
+    assert torch.equal(got, ops.linear_train_grad(A5, G5, 1, 2.0 / 2))
 
 
 @pytest.mark.parametrize("case", [

@@ -268,7 +268,25 @@ __global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
   const int64_t place = (s - q0) + before[lo];
   sk[place] = (static_cast<unsigned long long>(id) << 32) |
               static_cast<unsigned long long>(EgKey<K>::tok(k, q0));
-  if (head) atomicOr(present + (id >> 5), 1u << (id & 31));
+  // Presence bits: the workgroup's first slot of each bitmap word ORs the bits of the ids
+  // that follow it in that word (the slots are in id order), so a word takes one atomic per
+  // workgroup, not one per id (position ids put a chunk's 1024 ids in 32 words).
+  const int64_t word = id >> 5;
+  if (t == 0 || (kid[t - 1] >> 5) != word) {
+    uint32_t bits = 0;
+    bool more = true;
+    for (int u0 = t; more && u0 < EG_THREADS; u0 += 8) {   // 8 independent LDS reads a round
+      int64_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = u0 + j < EG_THREADS ? kid[u0 + j] : -1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        more = more && v[j] >= 0 && (v[j] >> 5) == word;
+        if (more) bits |= 1u << (v[j] & 31);
+      }
+    }
+    atomicOr(present + word, bits);
+  }
 }
 
 // Sum of cnt[0, chunks): the number of in-range keys, the length of the sorted list.

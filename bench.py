@@ -746,6 +746,19 @@ KERNEL_SHAPES = {
                            "ids[20,1024] vocab 50257, G[20,1024,768] bf16, 4 val",
     "embedding_grad_untied": "embedding_train_grad overwrite (every row written), ids[20,1024] "
                              "vocab 50257, G[20,1024,768] bf16, 4 val",
+    "dot_train_grad_conv1d_c_fc": "conv1d_dot_train_grad presum (HF Conv1D c_fc: weight + bias "
+                                  "dots and train grads), A[20,1024,768] G[20,1024,3072] bf16, "
+                                  "4 val",
+    "dot_train_grad_conv1d_c_attn": "conv1d_dot_train_grad presum (HF Conv1D c_attn), "
+                                    "A[20,1024,768] G[20,1024,2304] bf16, 4 val",
+    "embedding_grad_padded": "embedding_train_grad overwrite, ids[34,2048] with 90% one pad id "
+                             "(65536 train tokens), vocab 50257, G[34,2048,768] bf16, 2 val",
+    "train_grad_lm_head_hipblaslt": "torch.addmm (hipBLASLt): the GPT-2 tied lm_head's train "
+                                    "gradient [50257,768] from 16 train rows of T=1024 (50257 "
+                                    "columns: rows not 16-byte aligned for the K-major kernel)",
+    "train_grad_pythia_fc": "linear_train_grad (256x256-tile K-major kernel), A[10,2048,2048] "
+                            "G[10,2048,8192] bf16, 8 train rows",
+    "train_grad_pythia_fc_hipblaslt": "torch.addmm (hipBLASLt) at the same shape",
     "kron_fc": "kron_proj, A[32,1024,1024] G[32,1024,4096] bf16, k=16x16",
     "kron_embed_wte": "kron_embed_proj, ids[32,1024] vocab 50257, G[32,1024,1024] bf16, k=16x16",
     "copy_1GiB": "device copy of 1 GiB (HBM calibration)",
@@ -826,7 +839,36 @@ def kernels_leg(dev, reps: int = 10):
     out["embedding_grad_untied"] = timeit(lambda: ops.embedding_train_grad(ids, GL, 4, 1.25,
                                                                            tab))
     del tab
-    del A, G, A2, G2, X, GL
+    del X, GL
+    A2, G2 = A[:20].contiguous(), G[:20].contiguous()
+    for key, g_src in (("dot_train_grad_conv1d_c_fc", G2),
+                       ("dot_train_grad_conv1d_c_attn", G2[..., :2304])):
+        g_op = g_src.contiguous()
+        out[key] = timeit(lambda: ops.linear_dot_train_grad(
+            A2, g_op, 4, semantics=_native.SEM_PRESUM, grad_scale=1.25 / 16, bias=True,
+            bias_grad_scale=1.25 / 16, conv1d=True))
+        del g_op
+    del A, G, A2, G2
+    idp = torch.randint(0, 50257, (34, 2048), generator=g)
+    idp[torch.rand(34, 2048, generator=g) < 0.9] = 50256
+    idp = idp.to(dev)
+    Gp = rnd(34, 2048, 768, s=1e-2)
+    tab = torch.empty(50257, 768, dtype=torch.bfloat16, device=dev)
+    out["embedding_grad_padded"] = timeit(lambda: ops.embedding_train_grad(idp, Gp, 2, 1.0, tab))
+    del idp, Gp, tab
+    A_lm = rnd(16 * 1024, 768)
+    G_lm = rnd(16 * 1024, 50257, s=1e-4)
+    zero = torch.zeros((), dtype=torch.bfloat16, device=dev)
+    out["train_grad_lm_head_hipblaslt"] = timeit(
+        lambda: torch.addmm(zero, G_lm.t(), A_lm, beta=0.0, alpha=1.25 / 16))
+    del A_lm, G_lm
+    Ap = rnd(10, 2048, 2048)
+    Gq = rnd(10, 2048, 8192, s=1e-3)
+    out["train_grad_pythia_fc"] = timeit(lambda: ops.linear_train_grad(Ap, Gq, 2, 1.25 / 8))
+    At, Gt = Ap[:8].reshape(-1, 2048), Gq[:8].reshape(-1, 8192)
+    out["train_grad_pythia_fc_hipblaslt"] = timeit(
+        lambda: torch.addmm(zero, Gt.t(), At, beta=0.0, alpha=1.25 / 8))
+    del Ap, Gq, At, Gt
     Ak = rnd(32, 1024, 1024)
     Gk = rnd(32, 1024, 4096, s=1e-3)
     Pi = rnd(16, 1024, s=0.25)
@@ -857,6 +899,8 @@ TRAFFIC_KEYS = {"linear_valgrad[768x3072]": "valgrad_fc",
                 "linear_valgrad+bias+train_grad[768x2304]": "dot_train_grad_qkv",
                 "linear_valgrad+bias+train_grad[768x768]": "dot_train_grad_proj",
                 "layernorm_dot": "layernorm", "embedding_dot": "embedding_wte",
+                "conv1d_valgrad+bias+train_grad[768x3072]": "dot_train_grad_conv1d_c_fc",
+                "conv1d_valgrad+bias+train_grad[768x2304]": "dot_train_grad_conv1d_c_attn",
                 "kron_proj": "kron_fc", "kron_embed_proj": "kron_embed_wte",
                 "ghost": "ghost_microbench"}
 

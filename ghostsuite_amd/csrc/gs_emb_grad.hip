@@ -16,14 +16,15 @@
 //                           the old row when accumulating); a run crossing a window boundary
 //                           leaves its part of the window as an fp32 partial.  In overwrite
 //                           mode further waves write zeros to the rows of absent ids.
-//   4. eg_combine_kernel -- per run that crosses windows, its partials summed in window order
-//                           and the row written: by one wave for a run of a few windows, by
-//                           the 16 waves of a workgroup (contiguous shares combined in wave
-//                           order) for a longer one.
+//   4. eg_combine_kernel -- per run that crosses windows, its partials summed in a fixed
+//                           order and the row written: by one wave for a run of a few
+//                           windows, by the 16 waves of a workgroup for a longer one, and by
+//                           the workgroups whose windows it covers, a share of the features
+//                           each, for a run of hundreds of tokens or more.
 // Token ids outside [0, vocab) take no part.  Measured on MI355X (GPT-2 wte, 16 train rows of
-// 1024 tokens, d = 768, bf16): sort 15 us, merge 19, windows 19-21, combine 5-7; a padded
-// batch of 65536 train tokens with one id on 59k of them: 0.59 ms, most of it the long run's
-// combine on one workgroup.
+// 1024 tokens, d = 768, bf16): sort 15 us, merge 19, windows 19-21, combine 6-8; a padded
+// batch of 65536 train tokens with one id on 59k of them: sort 15, merge 60, windows 41-47,
+// combine 34 (the same case took 0.59 ms with each long run summed by one workgroup).
 
 #include <algorithm>
 
@@ -203,11 +204,13 @@ __global__ void __launch_bounds__(EG_SORT_THREADS) eg_sort_kernel(
 // sk[place] = (id << 32 | token index), place = the key's index in its chunk + the keys of
 // every other chunk that precede it; present[id] set.  One thread per chunk slot, a
 // workgroup per 256 consecutive slots of one chunk (slots holding the largest key do
-// nothing).  The keys of other chunks that precede a key depend only on its id, so the first
-// slot of each id within the workgroup searches (the binary searches over the other chunks
-// advance together, eight chunks at a time, so their loads are in flight at once) and the
-// slots after it take its count from LDS: an id that fills the chunk searches once per
-// workgroup, not once per token.
+// nothing).  The keys of other chunks that precede a key depend only on its id, so only the
+// first slot of each id within the workgroup (its run head) needs them, and the slots after
+// it take the head's count from LDS: an id that fills the chunk is searched for once per
+// workgroup, not once per token.  The (run head, other chunk) binary searches are spread over
+// all the workgroup's threads, eight per thread advancing together so their loads are in
+// flight at once; each adds its count to the head's total (integer adds: any order gives the
+// same total).
 template <class K>
 __global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
     const K* __restrict__ ck, int64_t chunks, unsigned long long* __restrict__ sk,
@@ -216,46 +219,71 @@ __global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
   constexpr int G = 8, STEPS = 12;
   static_assert((1 << (STEPS - 1)) == EG_CHUNK, "search steps");
   static_assert(EG_CHUNK % EG_THREADS == 0, "a merge workgroup stays inside one chunk");
-  __shared__ int64_t kid[EG_THREADS];    // ids of the workgroup's slots (-1: none)
-  __shared__ int64_t before[EG_THREADS];  // at run heads: keys of other chunks preceding
-  const int t = threadIdx.x;
+  __shared__ int64_t kid[EG_THREADS];  // ids of the workgroup's slots (-1: none)
+  __shared__ int before[EG_THREADS];   // at run heads: keys of other chunks preceding (< 2^31)
+  __shared__ int hslot[EG_THREADS];    // the run heads' slots, in slot order
+  __shared__ K hkey[EG_THREADS];       // and their keys
+  __shared__ int wheads[EG_THREADS / 64];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int64_t s = static_cast<int64_t>(blockIdx.x) * EG_THREADS + t;
   const int64_t c = static_cast<int64_t>(blockIdx.x) * EG_THREADS / EG_CHUNK, q0 = c * EG_CHUNK;
   const K k = ck[s];
   const bool valid = k != EgKey<K>::NONE;
   const int64_t id = valid ? EgKey<K>::id(k) : -1;
   kid[t] = id;
+  before[t] = 0;
   __syncthreads();
   const bool head = valid && (t == 0 || kid[t - 1] != id);
-  // 64-bit keys hold the token index: the plain order of keys; 32-bit keys compare ids only
-  // across chunks (every token of an earlier chunk precedes, of a later one follows)
-  const K lo_bound = sizeof(K) == 8 ? k : EgKey<K>::bound(id, false);
-  const K hi_bound = sizeof(K) == 8 ? k : EgKey<K>::bound(id, true);
+  const unsigned long long hb = __ballot(head);
+  if (lane == 0) wheads[wv] = __popcll(hb);
+  __syncthreads();
+  int hbase = 0, nh = 0;
+#pragma unroll
+  for (int v = 0; v < EG_THREADS / 64; ++v) {
+    const int x = wheads[v];
+    hbase += v < wv ? x : 0;
+    nh += x;
+  }
   if (head) {
-    int64_t n_before = 0;
-    for (int64_t o0 = 0; o0 < chunks; o0 += G) {
-      int lo[G], hi[G];
+    const int h = hbase + __popcll(hb & ((1ull << lane) - 1ull));
+    hslot[h] = t;
+    hkey[h] = k;
+  }
+  __syncthreads();
+  // pair p = (head p / chunks, chunk p % chunks); thread t takes pairs t + EG_THREADS j
+  // (fewer than 2^28 pairs: chunks < 2^20, as the entry point takes fewer than 2^31 tokens)
+  const unsigned nc = static_cast<unsigned>(chunks), cc = static_cast<unsigned>(c);
+  const unsigned pairs = static_cast<unsigned>(nh) * nc;
+  for (unsigned p0 = t; p0 < pairs; p0 += G * EG_THREADS) {
+    int lo[G], hi[G], hh[G];
+    K bnd[G];
+    int64_t oo[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const unsigned p = p0 + u * EG_THREADS;
+      const unsigned h = p < pairs ? p / nc : 0u;
+      const unsigned o = p < pairs ? p - h * nc : cc;
+      hh[u] = static_cast<int>(h);
+      oo[u] = o;
+      const K hk = hkey[h];
+      // 64-bit keys hold the token index: the plain order of keys; 32-bit keys compare ids
+      // only across chunks (every token of an earlier chunk precedes, of a later one follows)
+      bnd[u] = sizeof(K) == 8 ? hk : EgKey<K>::bound(EgKey<K>::id(hk), o < cc);
+      lo[u] = 0;
+      hi[u] = o != cc ? EG_CHUNK : 0;
+    }
+#pragma unroll
+    for (int step = 0; step < STEPS; ++step) {
 #pragma unroll
       for (int u = 0; u < G; ++u) {
-        const int64_t o = o0 + u;
-        lo[u] = 0;
-        hi[u] = (o < chunks && o != c) ? EG_CHUNK : 0;
+        if (lo[u] >= hi[u]) continue;
+        const int mid = (lo[u] + hi[u]) >> 1;
+        if (ck[oo[u] * EG_CHUNK + mid] < bnd[u]) lo[u] = mid + 1; else hi[u] = mid;
       }
-#pragma unroll
-      for (int step = 0; step < STEPS; ++step) {
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-          if (lo[u] >= hi[u]) continue;
-          const int mid = (lo[u] + hi[u]) >> 1;
-          const int64_t o = o0 + u;
-          const K b = o < c ? hi_bound : lo_bound;
-          if (ck[o * EG_CHUNK + mid] < b) lo[u] = mid + 1; else hi[u] = mid;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < G; ++u) n_before += lo[u];
     }
-    before[t] = n_before;
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      if (lo[u] != 0) atomicAdd(&before[hslot[hh[u]]], lo[u]);
   }
   __syncthreads();
   if (!valid) return;
@@ -466,12 +494,95 @@ __global__ void __launch_bounds__(EG_THREADS) eg_window_kernel(
   }
 }
 
-// Workgroup b looks at windows [16 b, 16 b + 16), one wave each: a window whose last run
-// began in it and continues into the next window hands that run over (in window order,
-// through LDS); the workgroup then takes the runs one by one: the run's partials part[w][1],
-// part[w + 1][0], ..., part[w_end][0] are split into 16 contiguous shares summed by the 16
-// waves, the shares combined in wave order, and the row written.
+// Workgroup b looks at windows [16 b, 16 b + 16), one wave each.  A window whose last run
+// began in it and continues into the next window owns that run; its partials are part[w][1],
+// part[w + 1][0], ..., part[w_end][0] (w_end: the window of the run's last place).
+//  - At most EG_LIGHT partials: the owning wave sums them and writes the row.
+//  - A run whose windows cover the whole range of fewer than EG_SPREAD other workgroups (at
+//    most 48 partials): handed over in window order through LDS; the owner's workgroup splits
+//    the partials into 16 contiguous shares summed by its 16 waves, combines the shares in
+//    wave order and writes the row.
+//  - A longer run: the workgroups whose whole range it covers (b_lo = w / 16 + 1 ..
+//    b_hi = w_end / 16 - 1; such a workgroup owns no run) sum it, each a share of the
+//    features over all the partials in a fixed order.  Every workgroup works alone: a run of
+//    59k tokens is summed by hundreds of workgroups, and none waits for another.
 constexpr int EG_COMBINE_WAVES = 16;
+constexpr int EG_LIGHT = 8, EG_SPREAD = 2;
+
+// Features [j sw, (j + 1) sw) of row `id` for a long run, sw = the row split evenly over the
+// nb covering workgroups (whole float4s), but at least 16 features: 64-byte pieces of the
+// partial rows (measured at GPT-2 width, d = 768, and a 59k-token run: 34 us with 48
+// workgroups reading 64-byte pieces, 46 us with 192 reading 16-byte ones; a run covering few
+// workgroups gives each a wide share in one pass).  In passes of at most 4096 features, a pass of
+// `cols` float4 columns has ng = 1024 / cols groups of threads, group g summing partials g,
+// g + ng, ... of its column in order; the ng group sums are combined in a fixed tree (sixteen
+// at a time, then those results), and the row's features written.
+template <class GE>
+__device__ void eg_spread_sum(const float* __restrict__ part, int64_t ws, int64_t parts,
+                              int64_t d, int64_t id, int64_t j, int64_t nb, float scale,
+                              int accumulate, float* __restrict__ red, GE* __restrict__ grad) {
+  constexpr int NT = EG_COMBINE_WAVES * 64, B = 8, PASS = 4 * NT;
+  const int t = threadIdx.x;
+  const bool v4 = (d & 3) == 0;   // rows of whole float4s (part is 256-byte aligned)
+  const int64_t sw = std::max<int64_t>(16, ((d + nb - 1) / nb + 3) & ~int64_t(3));
+  const int64_t f_begin = j * sw, f_end = std::min(d, f_begin + sw);
+  GE* out = grad + id * d;
+  float* red2 = red + PASS;   // the tree's first level: at most 4096 + 256 floats
+  for (int64_t fp = f_begin; fp < f_end; fp += PASS) {
+    const int width = static_cast<int>(std::min<int64_t>(PASS, f_end - fp));
+    const int cols = (width + 3) / 4, w4 = 4 * cols;
+    const int ng = NT / cols;   // at least 1
+    const int col = t % cols, g = t / cols;
+    if (g < ng) {
+      const int64_t f = fp + 4 * col;
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int64_t p0 = g; p0 < parts; p0 += static_cast<int64_t>(B) * ng) {
+        float4 x[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int64_t p = p0 + static_cast<int64_t>(u) * ng;
+          x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (p < parts) {
+            const float* src = part + ((ws + p) * 2 + (p == 0 ? 1 : 0)) * d + f;
+            if (v4) {
+              x[u] = *reinterpret_cast<const float4*>(src);
+            } else {
+              x[u].x = src[0];
+              if (f + 1 < f_end) x[u].y = src[1];
+              if (f + 2 < f_end) x[u].z = src[2];
+              if (f + 3 < f_end) x[u].w = src[3];
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          a[0] += x[u].x;
+          a[1] += x[u].y;
+          a[2] += x[u].z;
+          a[3] += x[u].w;
+        }
+      }
+      *reinterpret_cast<float4*>(red + g * w4 + 4 * col) = make_float4(a[0], a[1], a[2], a[3]);
+    }
+    __syncthreads();
+    const int n1 = (ng + 15) / 16;
+    for (int i = t; i < n1 * w4; i += NT) {
+      const int h = i / w4, e = i - h * w4, g_end = std::min(ng, 16 * h + 16);
+      float s = red[(16 * h) * w4 + e];
+      for (int gg = 16 * h + 1; gg < g_end; ++gg) s += red[gg * w4 + e];
+      red2[h * w4 + e] = s;
+    }
+    __syncthreads();
+    for (int e = t; e < width; e += NT) {
+      float s = red2[e];
+      for (int h = 1; h < n1; ++h) s += red2[h * w4 + e];
+      float x = scale * s;
+      if (accumulate) x += to_f32<GE>(out[fp + e]);
+      out[fp + e] = from_f32<GE>(x);
+    }
+    __syncthreads();   // red is reused by the next pass
+  }
+}
 
 template <class GE>
 __global__ void __launch_bounds__(EG_COMBINE_WAVES * 64) eg_combine_kernel(
@@ -484,9 +595,41 @@ __global__ void __launch_bounds__(EG_COMBINE_WAVES * 64) eg_combine_kernel(
   __shared__ int64_t run_w[NW], run_end[NW], run_id[NW];
   __shared__ int n_runs;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t n_list = list_length(cnt, chunks);
+  {
+    // A workgroup whose whole range of places lies inside one run that began before it and
+    // continues after it (every thread decides alike): its share of that run if the run is
+    // spread, else nothing (its windows own no run).
+    constexpr int64_t SPAN = static_cast<int64_t>(NW) * EG_WIN;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * SPAN;
+    if (r0 > 0 && r0 + SPAN < n_list) {
+      const int64_t id0 = key_id(sk[r0]);
+      if (key_id(sk[r0 - 1]) == id0 && key_id(sk[r0 + SPAN]) == id0) {
+        const unsigned long long k_lo = static_cast<unsigned long long>(id0) << 32;
+        const unsigned long long k_hi = k_lo | 0xffffffffull;
+        int64_t lo = 0, hi = r0 - 1;   // the run's first place
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (sk[mid] < k_lo) lo = mid + 1; else hi = mid;
+        }
+        const int64_t first = lo;
+        lo = r0 + SPAN + 1;             // one past its last place
+        hi = n_list;
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (sk[mid] <= k_hi) lo = mid + 1; else hi = mid;
+        }
+        const int64_t ws = first / EG_WIN, w_end = (lo - 1) / EG_WIN;
+        const int64_t b_lo = ws / NW + 1, nb = w_end / NW - 1 - b_lo + 1;
+        if (nb >= EG_SPREAD)
+          eg_spread_sum<GE>(part, ws, w_end - ws + 1, d, id0, blockIdx.x - b_lo, nb, scale,
+                            accumulate, &red[0][0], grad);
+        return;
+      }
+    }
+  }
   if (threadIdx.x == 0) n_runs = 0;
   __syncthreads();
-  const int64_t n_list = list_length(cnt, chunks);
   const int64_t w = static_cast<int64_t>(blockIdx.x) * NW + wid;
   bool found = false;
   int64_t id = 0, end = 0;
@@ -513,13 +656,14 @@ __global__ void __launch_bounds__(EG_COMBINE_WAVES * 64) eg_combine_kernel(
         }
         end = lo;
       }
-      found = true;
+      // a spread run is left to the workgroups it covers
+      const int64_t w_end = (end - 1) / EG_WIN;
+      found = (w_end / NW - 1) - (w / NW + 1) + 1 < EG_SPREAD;
     }
   }
   // A run of at most EG_LIGHT partials is summed by the wave that found it; longer runs are
   // handed over in window order (wave v's run to slot = longer runs of waves below v) and
   // summed by the whole workgroup.
-  constexpr int EG_LIGHT = 8;
   const int64_t parts_found = found ? (end - 1) / EG_WIN - w + 1 : 0;
   if (found && parts_found <= EG_LIGHT) {
     GE* out = grad + id * d;

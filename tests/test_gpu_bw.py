@@ -145,11 +145,15 @@ def test_embedding_train_grad(gpu, gdt, odt, shape):
     ((9, 1, 1000, 72, 40), 0.0),        # runs of ~200 tokens across many windows
     ((3, 1, 4099, 8, 50257), 1.0),      # every train token the pad id, ragged T
     ((5, 1, 900, 16, 2_000_000), 0.3),  # ids of 2^20 and above: 64-bit sort keys
+    ((4, 1, 3000, 10, 7), 0.97),        # long runs, rows of 10 features (no whole float4s)
+    ((40, 2, 2048, 768, 50257), 0.9),   # GPT-2 width: a 70k-token run over many workgroups
 ])
 def test_embedding_train_grad_heavy_ids(gpu, shape, pad_frac):
     """Ids that repeat thousands of times (a padded batch): the sorted-list pipeline stays
     linear in the token count (the call is timed against a generous bound) and sums each
-    run in a fixed order (bit-identical on a second run), against float64 index_add."""
+    run in a fixed order (bit-identical on a second run), against float64 index_add.  A run
+    longer than a few hundred tokens is summed by the workgroups whose windows it covers,
+    each taking feature slices; shorter ones by the workgroup where they begin."""
     import time
     N, n_val, T, d, vocab = shape
     ids = torch.randint(0, vocab, (N, T), generator=gen(90 + T))

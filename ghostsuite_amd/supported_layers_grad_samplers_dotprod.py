@@ -49,6 +49,10 @@ except Exception:  # pragma: no cover - transformers absent
 #   reference_id_promotion: pass an Embedding's token ids through the backprops' dtype
 #                  before its dot, as the reference's hook does (ids >= 256 round in a bf16
 #                  model); off by default: the ids are used as given
+#   dot_dtypes:    'reference' -- each grad_dot_prod in the dtype the reference's sampler
+#                  returns: the materialised-branch weight dots and the bias dots of Linear,
+#                  Conv1D and Conv2d layers in the operands' dtype (bf16 in a bf16 model),
+#                  every other dot fp32; 'fp32' -- every dot fp32 (the kernels' own output)
 options = {
     "precision": "reference",
     "linear_algo": "auto",
@@ -59,6 +63,7 @@ options = {
     # Run the dot kernels on a side stream, overlapped with the rest of backward.
     "overlap": True,
     "reference_id_promotion": False,
+    "dot_dtypes": "reference",
 }
 DEFAULT_OPTIONS = dict(options)
 ALGO_LOG: dict = {}
@@ -103,6 +108,22 @@ def _dot_dtype(x: torch.Tensor, pairwise: bool) -> torch.dtype:
     if pairwise:
         return torch.bfloat16
     return x.dtype if x.dtype in (torch.bfloat16, torch.float32) else torch.float32
+
+
+def _reference_dtypes(layer: nn.Module, weight_dtype: Optional[torch.dtype],
+                      bias_dtype: Optional[torch.dtype]) -> None:
+    """Casts the dots the sampler set to the dtypes the reference's sampler returns (a None
+    dtype: left fp32).  Its materialised branches and bias dots are einsums over operands in
+    the layer's dtype (Linear :131-146 in the original dtype, Conv1D :445-471 and Conv2d
+    :552-559 in bf16); its ghost branches sum in fp32 (:129-130, :437, :550)."""
+    if options["dot_dtypes"] != "reference" or options["precision"] == "fp32":
+        return
+    for param, dt in ((layer.weight, weight_dtype), (getattr(layer, "bias", None), bias_dtype)):
+        if param is None or dt is None:
+            continue
+        dot = param.__dict__.get("grad_dot_prod")
+        if dot is not None and dot.dtype != dt:
+            param.grad_dot_prod = dot.to(dt)
 
 
 def _overwritten_later(layer: nn.Module) -> bool:
@@ -160,8 +181,10 @@ def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tens
                                 val_batch_size: int):
     """Gradient dot-product of an nn.Linear layer (reference :75-146).
 
-    Sets ``layer.weight.grad_dot_prod`` ([n_train] fp32) and, with a bias,
-    ``layer.bias.grad_dot_prod``.
+    Sets ``layer.weight.grad_dot_prod`` ([n_train]) and, with a bias,
+    ``layer.bias.grad_dot_prod``: fp32 from the ghost branch (pairwise sum), in the
+    operands' dtype from the materialised branch and for the bias, as the reference returns
+    them (``dot_dtypes='fp32'``: always fp32).
     """
     if A is None:
         raise ValueError("Input activations A cannot be None.")
@@ -173,6 +196,11 @@ def _compute_linear_dot_product(layer: nn.Linear, A: torch.Tensor, B: torch.Tens
     if train_bs <= 0:
         raise ValueError("No training samples to compute dot product, check batch sizes.")
     _should_use_ghost_computation(layer, A, B)
+    _linear_dots(layer, A, B, val_batch_size)
+    _reference_dtypes(layer, None if layer.use_ghost_computation else A.dtype, B.dtype)
+
+
+def _linear_dots(layer: nn.Linear, A: torch.Tensor, B: torch.Tensor, val_batch_size: int):
     pairwise = layer.use_ghost_computation
     if not _overwritten_later(layer):
         dt = _dot_dtype(A, pairwise)
@@ -444,7 +472,9 @@ def _compute_layernorm_train_grad(layer: nn.LayerNorm, A: torch.Tensor, B: torch
 # HF Conv1D (weight [d_in, d_out]) ##########################################################
 
 def _compute_Conv1D_dot_product(layer, A: torch.Tensor, B: torch.Tensor, val_batch_size: int):
-    """Conv1D dot-products (reference :369-471): presum in both branches, bf16."""
+    """Conv1D dot-products (reference :369-471): presum in both branches, bf16 operands; the
+    ghost branch's dot fp32, the materialised branch's and the bias dot bf16, as the
+    reference returns them (``dot_dtypes='fp32'``: always fp32)."""
     if A is None:
         raise ValueError("Input activations A cannot be None.")
     if B is None:
@@ -459,13 +489,14 @@ def _compute_Conv1D_dot_product(layer, A: torch.Tensor, B: torch.Tensor, val_bat
         raise ValueError("Currently we only expect 3D input tensors (batch, seq_len, features). "
                          "Extending this to 4D or higher requires additional handling.")
     dt = torch.float32 if options["precision"] == "fp32" else torch.bfloat16
-    if _fused_dot_train_grad(layer, A, B, val_batch_size, False, dt, conv1d=True):
-        return
-    if layer.bias is not None and _fused_bias_dot(layer, A, B, val_batch_size, False, dt, dt):
-        return
-    _linear_like_dot(layer, A, B, val_batch_size, False, dt)
-    if layer.bias is not None:
-        _bias_dot_and_grad(layer, B, val_batch_size, dt)
+    if not _fused_dot_train_grad(layer, A, B, val_batch_size, False, dt, conv1d=True) and \
+            not (layer.bias is not None and
+                 _fused_bias_dot(layer, A, B, val_batch_size, False, dt, dt)):
+        _linear_like_dot(layer, A, B, val_batch_size, False, dt)
+        if layer.bias is not None:
+            _bias_dot_and_grad(layer, B, val_batch_size, dt)
+    _reference_dtypes(layer, None if layer.use_ghost_computation else torch.bfloat16,
+                      torch.bfloat16)
 
 
 def _compute_Conv1D_train_grad(layer, A: torch.Tensor, B: torch.Tensor, val_batch_size: int,
@@ -521,6 +552,8 @@ def _compute_conv2d_dot_product(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tens
     _linear_like_dot(layer, A_rows, B_rows, val_batch_size, False, dt)
     if layer.bias is not None:
         _bias_dot_and_grad(layer, B_rows, val_batch_size, dt)
+    _reference_dtypes(layer, None if layer.use_ghost_computation else torch.bfloat16,
+                      torch.bfloat16)
 
 
 def _compute_conv2d_train_grad(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor,

@@ -477,3 +477,63 @@ def test_gradient_stage_skips_side_stream_only_when_everything_is_parked():
     assert not _train_grads_parked(emb)
     emb._gs_weight_train_grad = S.APPLIED          # added into a tied weight's train_grad
     assert _train_grads_parked(emb)
+
+
+def test_dot_dtypes_follow_the_reference():
+    """Each grad_dot_prod comes in the dtype the reference's sampler returns for a bf16
+    layer: fp32 from a ghost branch (its fp32 sums, supported_layers_grad_samplers_dotprod.py
+    :129-130, :437, :550) and from Embedding / LayerNorm, the operands' dtype from a
+    materialised branch and from every bias dot (einsums, :131-146, :445-471, :552-559) --
+    the dtypes of the oracle's restatement of those sequences.  dot_dtypes='fp32' keeps every
+    dot fp32, and the reference-dtype dots are those fp32 values rounded once."""
+    from transformers.pytorch_utils import Conv1D
+    bf = torch.bfloat16
+    N, n_v = 5, 2
+
+    def run():
+        got = {}
+        for T, ghost in ((3, True), (12, False)):   # 2 T^2 <= 12 x 10 or not
+            A = torch.randn(N, T, 12, generator=gen(T)).to(bf)
+            B = (torch.randn(N, T, 10, generator=gen(T + 1)) * 1e-2).to(bf)
+            lin = nn.Linear(12, 10).to(bf)
+            S._compute_linear_dot_product(lin, A, B, n_v)
+            assert lin.use_ghost_computation == ghost
+            w_ref, b_ref = R.linear_dot_ref(A, B, n_v, ghost)
+            got[f"linear {ghost}"] = (lin, w_ref.dtype, b_ref.dtype)
+            conv = Conv1D(10, 12).to(bf)
+            S._compute_Conv1D_dot_product(conv, A, B, n_v)
+            assert conv.use_ghost_computation == ghost
+            w_ref, b_ref = R.conv1d_dot_ref(A, B, n_v, ghost)
+            got[f"conv1d {ghost}"] = (conv, w_ref.dtype, b_ref.dtype)
+        c2 = nn.Conv2d(3, 4, 3, padding=1, stride=2).to(bf)
+        X = torch.randn(N, 3, 6, 6, generator=gen(5)).to(bf)
+        Gc = (torch.randn(N, 4, 3, 3, generator=gen(6)) * 1e-2).to(bf)
+        S._compute_conv2d_dot_product(c2, X, Gc, n_v)
+        # the reference's Conv2d casts to bf16 and returns its einsums (:522-559)
+        got["conv2d"] = (c2, torch.float32 if c2.use_ghost_computation else bf, bf)
+        emb = nn.Embedding(30, 8).to(bf)
+        ids = torch.randint(0, 30, (N, 7), generator=gen(7))
+        S._compute_embedding_dot_product(emb, ids, (torch.randn(N, 7, 8, generator=gen(8)) *
+                                                     1e-2).to(bf), n_v)
+        got["embedding"] = (emb, torch.float32, None)
+        ln = nn.LayerNorm(8).to(bf)
+        S._compute_layernorm_dot_product(ln, torch.randn(N, 7, 8, generator=gen(9)).to(bf),
+                                         (torch.randn(N, 7, 8, generator=gen(10)) * 1e-2).to(bf),
+                                         n_v)
+        got["layernorm"] = (ln, torch.float32, torch.float32)
+        return {k: (lay.weight.grad_dot_prod, w, None if b is None else lay.bias.grad_dot_prod, b)
+                for k, (lay, w, b) in got.items()}
+
+    with use_oracle_backend():
+        S.options["dot_dtypes"] = "fp32"
+        full = run()
+        S.options["dot_dtypes"] = "reference"
+        ref = run()
+    assert ref["linear False"][1] == bf and ref["linear True"][1] == torch.float32
+    for name, (w, w_dt, b, b_dt) in ref.items():
+        fw, _, fb, _ = full[name]
+        assert fw.dtype == torch.float32 and w.dtype == w_dt, name
+        assert torch.equal(w, fw.to(w_dt)), name
+        if b_dt is not None:
+            assert fb.dtype == torch.float32 and b.dtype == b_dt, name
+            assert torch.equal(b, fb.to(b_dt)), name

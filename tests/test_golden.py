@@ -174,3 +174,45 @@ def test_engine_routing_matches_reference_engine(golden):
         eng.detach()
     for k, v in net.state_dict().items():
         assert_close(v, g["final"][k], 1e-5, f"final {k}")
+
+
+def test_sampler_dot_dtypes_match_reference_outputs(golden):
+    """The dtype of every grad_dot_prod the samplers set equals the dtype of the reference's
+    own output for the same layer and inputs (the golden vectors): fp32 from the ghost
+    branches, Embedding and LayerNorm, the operands' dtype from Linear's materialised branch
+    and bias, bf16 from Conv1D's materialised branch and bias and from Conv2d even on fp32
+    inputs (those samplers cast to bf16 first).  The values come from the oracle backend
+    here; the GPU golden test checks the HIP path's dtypes and values."""
+    from torch import nn
+    from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
+    from tests.oracle_backend import use_oracle_backend
+    checked = 0
+    with use_oracle_backend():
+        for name, c in golden["samplers"].items():
+            if name.startswith("linear_"):
+                layer = nn.Linear(c["A"].shape[-1], c["B"].shape[-1]).to(c["A"].dtype)
+                layer.use_ghost_computation = "_ghost_" in name
+                S._compute_linear_dot_product(layer, c["A"], c["B"], c["n_val"])
+            elif name.startswith("conv1d_"):
+                from transformers.pytorch_utils import Conv1D
+                layer = Conv1D(c["B"].shape[-1], c["A"].shape[-1]).to(c["A"].dtype)
+                layer.use_ghost_computation = "_ghost_" in name
+                S._compute_Conv1D_dot_product(layer, c["A"], c["B"], c["n_val"])
+            elif name.startswith("conv2d_"):
+                layer = nn.Conv2d(c["A"].shape[1], c["B"].shape[1], c["kernel_size"],
+                                  stride=c["stride"], padding=c["padding"],
+                                  dilation=c["dilation"]).to(c["A"].dtype)
+                S._compute_conv2d_dot_product(layer, c["A"], c["B"], c["n_val"])
+            elif name.startswith("embedding_"):
+                layer = nn.Embedding(c["vocab"], c["B"].shape[-1]).to(c["B"].dtype)
+                S._compute_embedding_dot_product(layer, c["ids"], c["B"], c["n_val"])
+            elif name.startswith("layernorm_"):
+                layer = nn.LayerNorm(c["A"].shape[-1], eps=c["eps"]).to(c["A"].dtype)
+                S._compute_layernorm_dot_product(layer, c["A"], c["B"], c["n_val"])
+            else:
+                continue
+            assert layer.weight.grad_dot_prod.dtype == c["dot"].dtype, name
+            if c.get("bias_dot") is not None:
+                assert layer.bias.grad_dot_prod.dtype == c["bias_dot"].dtype, name
+            checked += 1
+    assert checked == 24

@@ -582,8 +582,10 @@ def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
     model = model.to(gpu, torch.bfloat16)
 
     opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    # the kernels' own fp32 dots for the arithmetic checks; the reference-dtype hand-over is
+    # checked against them below
     eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True,
-                            record_algorithms=True, linear_algo="valgrad")
+                            record_algorithms=True, linear_algo="valgrad", dot_dtypes="fp32")
 
     def run():
         S.ALGO_LOG.clear()
@@ -591,7 +593,7 @@ def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
         eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
         model(X.to(gpu), Y.to(gpu)).backward()
         torch.cuda.synchronize()
-        dots = {n: p.grad_dot_prod.float().cpu() for n, p in model.named_parameters()
+        dots = {n: p.grad_dot_prod.cpu() for n, p in model.named_parameters()
                 if hasattr(p, "grad_dot_prod")}
         eng.prepare_gradients()
         grads = {n: p.grad.float().cpu() for n, p in model.named_parameters()
@@ -606,6 +608,20 @@ def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
     # default: weight + bias dots and both train grads from one pass over the train rows
     dots, grads, log = run()
     assert sorted(k for k, v in log.items() if v[1] == "valgrad+train_grad") == linears, log
+    # the default hand-over: each dot in the dtype the reference returns (a Linear's
+    # materialised-branch weight dot and its bias dot in bf16, the rest fp32), the fp32 value
+    # rounded once
+    eng.options["dot_dtypes"] = "reference"
+    dots_ref, _, _ = run()
+    eng.options["dot_dtypes"] = "fp32"
+    modules = dict(model.named_modules())
+    for name, d in dots.items():
+        mod = modules[name.rsplit(".", 1)[0]]
+        bf = isinstance(mod, nn.Linear) and (name.endswith("bias") or
+                                             not mod.use_ghost_computation)
+        assert d.dtype == torch.float32, name
+        assert dots_ref[name].dtype == (torch.bfloat16 if bf else torch.float32), name
+        assert torch.equal(dots_ref[name], d.to(dots_ref[name].dtype)), name
     # without it: the fused weight + bias dot pass, train grad separately
     monkeypatch.setattr(S, "_fused_dot_train_grad", lambda *a, **k: False)
     dots1, grads1, log1 = run()

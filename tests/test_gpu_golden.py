@@ -53,6 +53,8 @@ def test_linear_samplers_match_reference_outputs(gpu, golden):
         assert_close(lin.weight.grad_dot_prod.cpu(), c["dot"], _tol(c, ghost), f"{name} dot")
         assert_close(lin.bias.grad_dot_prod.cpu(), c["bias_dot"], _tol(c, False),
                      f"{name} bias")
+        assert lin.weight.grad_dot_prod.dtype == c["dot"].dtype, name
+        assert lin.bias.grad_dot_prod.dtype == c["bias_dot"].dtype, name
 
 
 def test_embedding_layernorm_conv1d_samplers_match_reference_outputs(gpu, golden):
@@ -63,12 +65,15 @@ def test_embedding_layernorm_conv1d_samplers_match_reference_outputs(gpu, golden
             S._compute_embedding_dot_product(emb, c["ids"].to(gpu), c["B"].to(gpu), c["n_val"])
             torch.cuda.synchronize()
             assert_close(emb.weight.grad_dot_prod.cpu(), c["dot"], BF16_TOL, name)
+            assert emb.weight.grad_dot_prod.dtype == c["dot"].dtype, name
         elif name.startswith("layernorm_"):
             ln = nn.LayerNorm(c["A"].shape[-1], eps=c["eps"]).to(gpu, c["A"].dtype)
             S._compute_layernorm_dot_product(ln, c["A"].to(gpu), c["B"].to(gpu), c["n_val"])
             torch.cuda.synchronize()
             assert_close(ln.weight.grad_dot_prod.cpu(), c["dot"], BF16_TOL, f"{name} w")
             assert_close(ln.bias.grad_dot_prod.cpu(), c["bias_dot"], BF16_TOL, f"{name} b")
+            assert ln.weight.grad_dot_prod.dtype == c["dot"].dtype, name
+            assert ln.bias.grad_dot_prod.dtype == c["bias_dot"].dtype, name
         elif name.startswith("conv1d_"):
             transformers = pytest.importorskip("transformers")
             conv = transformers.pytorch_utils.Conv1D(c["B"].shape[-1], c["A"].shape[-1])
@@ -79,6 +84,8 @@ def test_embedding_layernorm_conv1d_samplers_match_reference_outputs(gpu, golden
             assert_close(conv.weight.grad_dot_prod.cpu(), c["dot"], BF16_TOL, f"{name} dot")
             assert_close(conv.bias.grad_dot_prod.cpu(), c["bias_dot"], BF16_TOL,
                          f"{name} bias")
+            assert conv.weight.grad_dot_prod.dtype == c["dot"].dtype, name
+            assert conv.bias.grad_dot_prod.dtype == c["bias_dot"].dtype, name
 
 
 def test_engine_on_gpu_matches_reference_engine(gpu, golden):

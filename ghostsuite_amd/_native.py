@@ -25,7 +25,7 @@ ALGO_AUTO, ALGO_GHOST, ALGO_VALGRAD = 0, 1, 2
 ROUND_FP32, ROUND_REF_BF16 = 0, 1
 PROJ_KO_KI, PROJ_KI_KO = 0, 1
 ERR_UNSUPPORTED = -5  # gs_status GS_ERR_UNSUPPORTED: a valid request outside the kernels' limits
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _TORCH_TO_GS = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32, torch.float16: DTYPE_F16}
 ALGO_NAMES = {ALGO_AUTO: "auto", ALGO_GHOST: "ghost", ALGO_VALGRAD: "valgrad"}
@@ -92,6 +92,7 @@ _SIGNATURES = {
     "gs_linear_bias_dot_workspace": (_SZ, [_I, _I64, _I64, _I64, _I64, _I64, _I]),
     "gs_linear_bias_dot": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _P, _P,
                                 _I, _F, _P, _SZ, _P]),
+    "gs_ordered_sum": (_I, [_P, _P, _I, _I64, _P, _I, _P]),
 }
 
 
@@ -634,6 +635,27 @@ class HipOps:
                                     ws.data_ptr(), ws_bytes, _stream(dev))
         _check(rc, "gs_kron_embed_proj")
         return out
+
+
+    def ordered_sum_(self, tensors) -> torch.Tensor:
+        """tensors[0] += tensors[1], then += tensors[2], ... in order, in place, in one launch
+        per 48 tensors: fp32 arithmetic, each partial sum rounded to tensors[0]'s dtype (the
+        in-place adds' own rounding).  Every tensor: contiguous, bf16 or fp32, the same
+        number of elements, on one device.  Returns tensors[0]."""
+        total = tensors[0]
+        dev = _require_device(*tensors)
+        n = total.numel()
+        for t in tensors:
+            if t.numel() != n or not t.is_contiguous() or \
+                    t.dtype not in (torch.bfloat16, torch.float32):
+                raise GhostHipError("ordered_sum_: contiguous bf16 / fp32 tensors of one size")
+        k = len(tensors)
+        ptrs = (ctypes.c_void_p * k)(*[t.data_ptr() for t in tensors])
+        dts = (ctypes.c_int * k)(*[_TORCH_TO_GS[t.dtype] for t in tensors])
+        rc = load_library().gs_ordered_sum(ptrs, dts, k, n, total.data_ptr(),
+                                           _TORCH_TO_GS[total.dtype], _stream(dev))
+        _check(rc, "gs_ordered_sum")
+        return total
 
 
 _backend = None

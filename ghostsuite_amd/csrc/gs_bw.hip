@@ -907,10 +907,80 @@ int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F,
   return check_launch("ln_sums_kernel");
 }
 
+// ---------------------------------------------------------------- ordered sum
+// out[i] = ((s_0[i] + s_1[i]) + s_2[i]) + ... in the order given, each partial sum rounded
+// to out's dtype: the in-place `total += s_k` sequence of the engine's aggregation (fp32
+// arithmetic, then the total's dtype).  Up to OS_MAX sources per launch; longer lists
+// continue from out.
+constexpr int OS_MAX = 48;
+struct OrderedSrcs {
+  const void* p[OS_MAX];
+  uint64_t bf16;   // bit k: source k holds bf16
+  int count;
+};
+
+template <class OE>
+__global__ void __launch_bounds__(256) ordered_sum_kernel(OrderedSrcs src, int64_t n,
+                                                          OE* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  auto load = [&](int k) {
+    return (src.bf16 >> k) & 1ull ? bf16_to_f32(static_cast<const uint16_t*>(src.p[k])[i])
+                                  : static_cast<const float*>(src.p[k])[i];
+  };
+  float acc = load(0);
+  for (int k = 1; k < src.count; ++k) acc = to_f32<OE>(from_f32<OE>(acc + load(k)));
+  out[i] = from_f32<OE>(acc);
+}
+
 }  // namespace
 }  // namespace gs
 
 using namespace gs;
+
+extern "C" int gs_ordered_sum(const void* const* srcs, const int* dtypes, int count, int64_t n,
+                              void* out, int out_dtype, void* stream) {
+  if (srcs == nullptr || dtypes == nullptr || count <= 0 || n < 0 || out == nullptr)
+    return fail(GS_ERR_INVALID, "gs_ordered_sum: invalid arguments");
+  if (out_dtype != GS_DTYPE_F32 && out_dtype != GS_DTYPE_BF16)
+    return fail(GS_ERR_DTYPE, "gs_ordered_sum: out dtype must be bf16 or fp32");
+  for (int k = 0; k < count; ++k) {
+    if (srcs[k] == nullptr) return fail(GS_ERR_INVALID, "gs_ordered_sum: null source");
+    if (dtypes[k] != GS_DTYPE_F32 && dtypes[k] != GS_DTYPE_BF16)
+      return fail(GS_ERR_DTYPE, "gs_ordered_sum: source dtypes must be bf16 or fp32");
+  }
+  if (n == 0) return GS_OK;
+  if (n > static_cast<int64_t>(INT32_MAX) * 256)
+    return fail(GS_ERR_UNSUPPORTED, "gs_ordered_sum: too many elements");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  // the first launch starts from srcs[0]; each later one from out (the running total, already
+  // rounded to out's dtype) and the next OS_MAX - 1 sources
+  int k0 = 0;
+  while (k0 < count) {
+    OrderedSrcs o{};
+    int m = 0;
+    if (k0 > 0) {
+      o.p[m] = out;
+      o.bf16 |= out_dtype == GS_DTYPE_BF16 ? 1ull : 0ull;
+      ++m;
+    }
+    for (; m < OS_MAX && k0 < count; ++m, ++k0) {
+      o.p[m] = srcs[k0];
+      if (dtypes[k0] == GS_DTYPE_BF16) o.bf16 |= 1ull << m;
+    }
+    o.count = m;
+    if (out_dtype == GS_DTYPE_BF16)
+      hipLaunchKernelGGL(ordered_sum_kernel<uint16_t>, grid, dim3(256), 0, s, o, n,
+                         static_cast<uint16_t*>(out));
+    else
+      hipLaunchKernelGGL(ordered_sum_kernel<float>, grid, dim3(256), 0, s, o, n,
+                         static_cast<float*>(out));
+    const int rc = check_launch("ordered_sum_kernel");
+    if (rc) return rc;
+  }
+  return GS_OK;
+}
 
 // ------------------------------------------------------------------------------ bias
 extern "C" size_t gs_bias_dot_workspace(int64_t N, int64_t T, int64_t d_out) {

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 1
+#define GS_ABI_VERSION 2
 
 typedef enum {
   GS_OK = 0,
@@ -325,6 +325,19 @@ int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, int64_t B, 
                        int64_t n_g, const void* P_iT, const void* P_o, int p_dtype,
                        int64_t vocab, int64_t k_i, int64_t k_o, float scale, void* out,
                        int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Ordered sum of the per-parameter dot products --------------------------------------
+ * Replaces the summation loop of GradDotProdEngine._aggregate_and_log_dot_products
+ * (ghostEngines/graddotprod_engine.py:198-211: total = the first grad_dot_prod, then
+ * total += each later one, in named_parameters order) with one launch per 48 sources:
+ *   out[i] = ((s_0[i] + s_1[i]) + s_2[i]) + ...
+ * element by element in the order given, in fp32 arithmetic, each partial sum rounded to
+ * out_dtype -- the rounding of an in-place add into a total of that dtype; out may be s_0
+ * (the reference accumulates into its first tensor, whose dtype out_dtype then is).
+ * srcs: host array of `count` device pointers to n elements each; dtypes: host array of their
+ * dtypes (bf16 or fp32).  No workspace. */
+int gs_ordered_sum(const void* const* srcs, const int* dtypes, int count, int64_t n, void* out,
+                   int out_dtype, void* stream);
 
 #ifdef __cplusplus
 }

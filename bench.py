@@ -615,14 +615,24 @@ def ghost_sweep(dev, reps: int = 10):
 
 # ------------------------------------------------------------------ CPU baseline
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with its family / model numbers (a
+    virtualised host may report only the brand) and the logical CPUs the OS shows."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "cpu family", "model") and key not in fields:
+                    fields[key] = val.strip()
+                if len(fields) == 3:
+                    break
     except OSError:
         pass
-    return "unknown"
+    name = fields.get("model name", "unknown")
+    if "cpu family" in fields and "model" in fields:
+        name += f" (family {fields['cpu family']}, model {fields['model']})"
+    return f"{name}, {os.cpu_count()} logical CPUs on the host"
 
 
 def cpu_baseline(budget_s: float = 60.0):

@@ -1145,10 +1145,11 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) gemm_dma_kernel(GemmParam
   }
 }
 
-// GHOST with large wave tiles (one wave per SIMD): the first Gram tile (A_val A_tr^T over
-// K1) is rounded to bf16 and held packed in registers while the second (G_val G_tr^T over
-// K2) accumulates in fp32, which halves the registers the first tile needs.  The reference
-// rounds both Gram matrices to bf16 (its a_dot / b_dot are bf16 matmul outputs).
+// GHOST on 256 x 256 tiles of 128 x 64 wave tiles (8 waves, two per SIMD, 256 registers
+// each): the first Gram tile (A_val A_tr^T over K1) is rounded to bf16 and held packed in
+// registers while the second (G_val G_tr^T over K2) accumulates in fp32, which halves the
+// registers the first tile needs.  The reference rounds both Gram matrices to bf16 (its
+// a_dot / b_dot are bf16 matmul outputs).
 template <class C, class D>
 __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
   constexpr int SB = D::LDS_BYTES;

@@ -181,7 +181,9 @@ int gs_conv1d_dot_train_grad(const void* A, const void* G, int dtype, int64_t N,
  *   layout 0: out [d_out, d_in] = scale * sum over train rows and tokens of g a^T (Linear)
  *   layout 1: out [d_in, d_out] = scale * sum of a g^T (HF Conv1D)
  * bf16 operands, 16-byte aligned, d_in and d_out multiples of 8, every row of A and G below
- * 2 GiB of offset; other cases return GS_ERR_UNSUPPORTED (workspace query: 0).
+ * 2 GiB of offset; other cases return GS_ERR_UNSUPPORTED (workspace query: 0).  Outputs of
+ * 256 or more 256 x 256 tiles run one work item per tile over all the train rows; smaller
+ * ones on 128 x 128 tiles with the rows split, the fp32 split partials in the workspace.
  * Reference: _compute_linear_train_grad (supported_layers_grad_samplers_dotprod.py:155-173)
  * and _compute_Conv1D_train_grad (:474-506), with scale = 1 / n_train there. */
 size_t gs_linear_train_grad_workspace(int dtype, int64_t N, int64_t n_val, int64_t T,

@@ -910,12 +910,14 @@ int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F,
 // ---------------------------------------------------------------- ordered sum
 // out[i] = ((s_0[i] + s_1[i]) + s_2[i]) + ... in the order given, each partial sum rounded
 // to out's dtype: the in-place `total += s_k` sequence of the engine's aggregation (fp32
-// arithmetic, then the total's dtype).  Up to OS_MAX sources per launch; longer lists
-// continue from out.
-constexpr int OS_MAX = 48;
+// arithmetic, then the total's dtype).  Up to OS_MAX sources per launch (the pointers travel
+// in the kernel arguments, 2 KiB); longer lists continue from out.  The source loop is
+// unrolled with compile-time indices (the arguments stay in scalar registers), its loads
+// issued eight at a time before their adds.
+constexpr int OS_MAX = 256, OS_BATCH = 8;
 struct OrderedSrcs {
   const void* p[OS_MAX];
-  uint64_t bf16;   // bit k: source k holds bf16
+  uint32_t bf16[OS_MAX / 32];   // bit k % 32 of word k / 32: source k holds bf16
   int count;
 };
 
@@ -924,12 +926,29 @@ __global__ void __launch_bounds__(256) ordered_sum_kernel(OrderedSrcs src, int64
                                                           OE* __restrict__ out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n) return;
-  auto load = [&](int k) {
-    return (src.bf16 >> k) & 1ull ? bf16_to_f32(static_cast<const uint16_t*>(src.p[k])[i])
-                                  : static_cast<const float*>(src.p[k])[i];
-  };
-  float acc = load(0);
-  for (int k = 1; k < src.count; ++k) acc = to_f32<OE>(from_f32<OE>(acc + load(k)));
+  float acc = 0.f;
+#pragma unroll
+  for (int k0 = 0; k0 < OS_MAX; k0 += OS_BATCH) {
+    if (k0 >= src.count) break;
+    float v[OS_BATCH];
+#pragma unroll
+    for (int u = 0; u < OS_BATCH; ++u) {
+      const int k = k0 + u;
+      v[u] = 0.f;
+      if (k < src.count)
+        v[u] = (src.bf16[k / 32] >> (k % 32)) & 1u
+                   ? bf16_to_f32(static_cast<const uint16_t*>(src.p[k])[i])
+                   : static_cast<const float*>(src.p[k])[i];
+    }
+#pragma unroll
+    for (int u = 0; u < OS_BATCH; ++u) {
+      const int k = k0 + u;
+      if (k == 0)
+        acc = v[0];   // the first tensor is the total: no rounding
+      else if (k < src.count)
+        acc = to_f32<OE>(from_f32<OE>(acc + v[u]));
+    }
+  }
   out[i] = from_f32<OE>(acc);
 }
 
@@ -962,12 +981,12 @@ extern "C" int gs_ordered_sum(const void* const* srcs, const int* dtypes, int co
     int m = 0;
     if (k0 > 0) {
       o.p[m] = out;
-      o.bf16 |= out_dtype == GS_DTYPE_BF16 ? 1ull : 0ull;
+      if (out_dtype == GS_DTYPE_BF16) o.bf16[0] |= 1u;
       ++m;
     }
     for (; m < OS_MAX && k0 < count; ++m, ++k0) {
       o.p[m] = srcs[k0];
-      if (dtypes[k0] == GS_DTYPE_BF16) o.bf16 |= 1ull << m;
+      if (dtypes[k0] == GS_DTYPE_BF16) o.bf16[m / 32] |= 1u << (m % 32);
     }
     o.count = m;
     if (out_dtype == GS_DTYPE_BF16)

@@ -331,7 +331,7 @@ int gs_kron_embed_proj(const int64_t* ids, const void* G, int dtype, int64_t B, 
 /* ---- Ordered sum of the per-parameter dot products --------------------------------------
  * Replaces the summation loop of GradDotProdEngine._aggregate_and_log_dot_products
  * (ghostEngines/graddotprod_engine.py:198-211: total = the first grad_dot_prod, then
- * total += each later one, in named_parameters order) with one launch per 48 sources:
+ * total += each later one, in named_parameters order) with one launch per 256 sources:
  *   out[i] = ((s_0[i] + s_1[i]) + s_2[i]) + ...
  * element by element in the order given, in fp32 arithmetic, each partial sum rounded to
  * out_dtype -- the rounding of an in-place add into a total of that dtype; out may be s_0

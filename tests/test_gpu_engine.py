@@ -788,12 +788,12 @@ def test_embedding_id_promotion_on_gpu(gpu, promote):
 def test_ordered_sum_matches_sequential_in_place_adds(gpu, first, n):
     """gs_ordered_sum, the engine's aggregation of the per-parameter dots, against torch's
     in-place adds in the same order on the same GPU tensors (graddotprod_engine.py:204-211),
-    bit for bit: 150 sources of scales 1e-3..1e3 (four chained launches of at most 48), bf16
-    and fp32 mixed, the total in the first source's dtype and in its memory."""
+    bit for bit: 600 sources of scales 1e-3..1e3 (three chained launches of at most 256),
+    bf16 and fp32 mixed, the total in the first source's dtype and in its memory."""
     from ghostsuite_amd import _native
     g = gen(600 + n)
-    dts = [first] + [torch.bfloat16 if i % 3 else torch.float32 for i in range(149)]
-    scales = 10.0 ** torch.randint(-3, 4, (150,), generator=g).double()
+    dts = [first] + [torch.bfloat16 if i % 3 else torch.float32 for i in range(599)]
+    scales = 10.0 ** torch.randint(-3, 4, (600,), generator=g).double()
     srcs = [(torch.randn(n, generator=g) * float(sc)).to(dt) for dt, sc in zip(dts, scales)]
     print(f"ordered sum first={first} n={n}", flush=True)
     a = [s.to(gpu) for s in srcs]

@@ -22,9 +22,9 @@
 //                           the workgroups whose windows it covers, a share of the features
 //                           each, for a run of hundreds of tokens or more.
 // Token ids outside [0, vocab) take no part.  Measured on MI355X (GPT-2 wte, 16 train rows of
-// 1024 tokens, d = 768, bf16): sort 15 us, merge 19, windows 19-21, combine 6-8; a padded
-// batch of 65536 train tokens with one id on 59k of them: sort 15, merge 60, windows 41-47,
-// combine 34 (the same case took 0.59 ms with each long run summed by one workgroup).
+// 1024 tokens, d = 768, bf16): sort 15 us, merge 14, windows 19-21, combine 6-8; a padded
+// batch of 65536 train tokens with one id on 59k of them: sort 15, merge 52, windows 41-47,
+// combine 36 (the same case took 0.59 ms with each long run summed by one workgroup).
 
 #include <algorithm>
 
@@ -210,14 +210,25 @@ __global__ void __launch_bounds__(EG_SORT_THREADS) eg_sort_kernel(
 // workgroup, not once per token.  The (run head, other chunk) binary searches are spread over
 // all the workgroup's threads, eight per thread advancing together so their loads are in
 // flight at once; each adds its count to the head's total (integer adds: any order gives the
-// same total).
-template <class K>
+// same total).  With SAMP (32-bit keys, at most EG_SAMP_CHUNKS chunks) the workgroup first
+// copies every EG_SAMP-th key of every chunk into LDS; a search then narrows the range to
+// EG_SAMP - 1 keys among the samples in LDS and finishes over global memory in 5 steps
+// instead of 12 (the global loads, each a trip to L2, are what the searches wait on).
+constexpr int EG_SAMP = 32, EG_NSAMP = EG_CHUNK / EG_SAMP;  // 64 samples per chunk
+constexpr int64_t EG_SAMP_CHUNKS = 128;                      // 32 KiB of samples at most
+
+template <class K, bool SAMP>
 __global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
     const K* __restrict__ ck, int64_t chunks, unsigned long long* __restrict__ sk,
     uint32_t* __restrict__ present) {
-  // STEPS halvings take an interval of 2^(STEPS - 1) = EG_CHUNK slots down to empty
-  constexpr int G = 8, STEPS = 12;
+  // STEPS halvings take an interval of 2^(STEPS - 1) = EG_CHUNK slots down to empty;
+  // sampled: SSTEPS over the EG_NSAMP samples (EG_NSAMP + 1 outcomes), then GSTEPS over an
+  // interval of EG_SAMP - 1 keys
+  constexpr int G = 8, STEPS = 12, SSTEPS = 7, GSTEPS = 5;
   static_assert((1 << (STEPS - 1)) == EG_CHUNK, "search steps");
+  static_assert((1 << (SSTEPS - 1)) == EG_NSAMP && (1 << GSTEPS) == EG_SAMP, "sampled steps");
+  static_assert(!SAMP || sizeof(K) == 4, "samples of 32-bit keys");
+  extern __shared__ __attribute__((aligned(16))) unsigned char eg_samples[];
   static_assert(EG_CHUNK % EG_THREADS == 0, "a merge workgroup stays inside one chunk");
   __shared__ int64_t kid[EG_THREADS];  // ids of the workgroup's slots (-1: none)
   __shared__ int before[EG_THREADS];   // at run heads: keys of other chunks preceding (< 2^31)
@@ -232,6 +243,12 @@ __global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
   const int64_t id = valid ? EgKey<K>::id(k) : -1;
   kid[t] = id;
   before[t] = 0;
+  const K* samp = reinterpret_cast<const K*>(eg_samples);
+  if constexpr (SAMP) {
+    K* w = reinterpret_cast<K*>(eg_samples);
+    for (int64_t x = t; x < chunks * EG_NSAMP; x += EG_THREADS)
+      w[x] = ck[(x / EG_NSAMP) * EG_CHUNK + (x % EG_NSAMP) * EG_SAMP];
+  }
   __syncthreads();
   const bool head = valid && (t == 0 || kid[t - 1] != id);
   const unsigned long long hb = __ballot(head);
@@ -270,10 +287,29 @@ __global__ void __launch_bounds__(EG_THREADS) eg_merge_kernel(
       // only across chunks (every token of an earlier chunk precedes, of a later one follows)
       bnd[u] = sizeof(K) == 8 ? hk : EgKey<K>::bound(EgKey<K>::id(hk), o < cc);
       lo[u] = 0;
-      hi[u] = o != cc ? EG_CHUNK : 0;
+      hi[u] = o != cc ? (SAMP ? EG_NSAMP : EG_CHUNK) : 0;
+    }
+    if constexpr (SAMP) {
+      // samples below the bound: s of them means keys [0, EG_SAMP (s - 1)] are below it and
+      // the keys from EG_SAMP s on are not, so the count lies in (EG_SAMP (s - 1), EG_SAMP s]
+#pragma unroll
+      for (int step = 0; step < SSTEPS; ++step) {
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+          if (lo[u] >= hi[u]) continue;
+          const int mid = (lo[u] + hi[u]) >> 1;
+          if (samp[oo[u] * EG_NSAMP + mid] < bnd[u]) lo[u] = mid + 1; else hi[u] = mid;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const int sb = lo[u];
+        lo[u] = sb == 0 ? 0 : (sb - 1) * EG_SAMP + 1;
+        hi[u] = sb * EG_SAMP;
+      }
     }
 #pragma unroll
-    for (int step = 0; step < STEPS; ++step) {
+    for (int step = 0; step < (SAMP ? GSTEPS : STEPS); ++step) {
 #pragma unroll
       for (int u = 0; u < G; ++u) {
         if (lo[u] >= hi[u]) continue;
@@ -866,14 +902,19 @@ extern "C" int gs_embedding_train_grad(const int64_t* ids, const void* G, int dt
     hipLaunchKernelGGL(eg_sort_kernel<uint32_t>, dim3(static_cast<unsigned>(pl.chunks)),
                        dim3(EG_SORT_THREADS), 0, s, ids, tr, vocab, ck32, cnt, present,
                        pl.present_words);
-    hipLaunchKernelGGL(eg_merge_kernel<uint32_t>, mgrid, dim3(EG_THREADS), 0, s, ck32,
-                       pl.chunks, sk, present);
+    if (pl.chunks <= EG_SAMP_CHUNKS)
+      hipLaunchKernelGGL((eg_merge_kernel<uint32_t, true>), mgrid, dim3(EG_THREADS),
+                         static_cast<unsigned>(pl.chunks * EG_NSAMP * sizeof(uint32_t)), s,
+                         ck32, pl.chunks, sk, present);
+    else
+      hipLaunchKernelGGL((eg_merge_kernel<uint32_t, false>), mgrid, dim3(EG_THREADS), 0, s,
+                         ck32, pl.chunks, sk, present);
   } else {
     hipLaunchKernelGGL(eg_sort_kernel<unsigned long long>, dim3(static_cast<unsigned>(pl.chunks)),
                        dim3(EG_SORT_THREADS), 0, s, ids, tr, vocab, ck, cnt, present,
                        pl.present_words);
-    hipLaunchKernelGGL(eg_merge_kernel<unsigned long long>, mgrid, dim3(EG_THREADS), 0, s, ck,
-                       pl.chunks, sk, present);
+    hipLaunchKernelGGL((eg_merge_kernel<unsigned long long, false>), mgrid, dim3(EG_THREADS),
+                       0, s, ck, pl.chunks, sk, present);
   }
   int rc = check_launch("eg_sort_kernel / eg_merge_kernel");
   if (rc) return rc;

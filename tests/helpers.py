@@ -23,6 +23,20 @@ def assert_close(x, y, tol, what=""):
     return worst
 
 
+def assert_close_to_sum(got, want, mag, tol, what=""):
+    """|got - want| <= tol * max(mag, rms(want)) elementwise, mag = the summed magnitudes of
+    the addends of a sum formed from separately rounded contributions (a tied weight's two
+    train gradients): the rounding bound of such a sum, which where the addends cancel is
+    relative to them, not to the small sum."""
+    got = got.double().cpu()
+    want = want.double().cpu()
+    mag = mag.double().cpu()
+    rms = want.pow(2).mean().sqrt().item()
+    worst = ((got - want).abs() / torch.clamp(mag, min=max(rms, 1e-300))).max().item()
+    assert worst <= tol, f"{what}: worst error {worst:.3e} of the addends' size > {tol:.1e}"
+    return worst
+
+
 def conv_net():
     """Two Conv2d layers (stride, padding, dilation, rectangular kernels) and a Linear head."""
     from torch import nn

@@ -537,3 +537,32 @@ def test_dot_dtypes_follow_the_reference():
         if b_dt is not None:
             assert fb.dtype == torch.float32 and b.dtype == b_dt, name
             assert torch.equal(b, fb.to(b_dt)), name
+
+
+def test_sum_reduction_engine_dots_and_grads():
+    """loss_reduction='sum': the backprops are not rescaled (the reference scales them by N
+    only for 'mean', autograd_grad_sample_dotprod.py:132-134), so the dots are those of the
+    summed loss's per-sample gradients and every train gradient -- bias included, whose
+    stage divides by n_train either way (:67, :199-222) -- is their mean over the train rows."""
+    torch.manual_seed(3)
+    dims = (40, 24, 10)
+    model = MLP(dims)
+    ref = copy.deepcopy(model).double()
+    n_t, n_v = 12, 4
+    X = torch.randn(n_t + n_v, dims[0], generator=gen(11))
+    Y = torch.randint(0, 10, (n_t + n_v,), generator=gen(12))
+    with use_oracle_backend():
+        eng = GradDotProdEngine(model, val_batch_size=n_v, loss_reduction="sum",
+                                use_dummy_bias=False, precision="fp32")
+        eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+        eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+        F.cross_entropy(model(X), Y, reduction="sum").backward()
+        dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()}
+        eng.prepare_gradients()
+        grads = {n: p.grad.clone() for n, p in model.named_parameters()}
+        eng.clear_gradients()
+        eng.detach()
+    g = brute.per_sample_grads(ref, X.double(), Y, _ce_sum, 1.0)
+    for name, gr in g.items():
+        assert_close(dots[name], brute.pairwise_dots(gr, n_v), FP32_TOL, f"dot {name}")
+        assert_close(grads[name], brute.train_mean(gr, n_v, 1.0), FP32_TOL, f"grad {name}")

@@ -26,10 +26,10 @@ from torch import nn
 from ghostsuite_amd import GradDotProdEngine, GradProjLoraEngine, _native
 from ghostsuite_amd import supported_layers_grad_samplers_dotprod as S
 from ghostsuite_amd.workloads import (CausalLM, GPT2_MEDIUM, GPT2_SMALL, MLP, PYTHIA_1B,
-                                      synthetic_tokens)
+                                      LMConfig, synthetic_tokens)
 from oracle import brute
 from oracle import ghost_ref as R
-from tests.helpers import BF16_TOL, FP32_TOL, assert_close, gen, randn
+from tests.helpers import BF16_TOL, FP32_TOL, assert_close, assert_close_to_sum, gen, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -82,10 +82,11 @@ def _train_rows(x, n_t):
     return x[:n_t].reshape(-1, x.shape[-1])
 
 
-def _expected_lm(model, cap, n_t, n_v):
+def _expected_lm(model, cap, n_t, n_v, reduction="mean"):
     """{param name: expected dot} and {param name: expected .grad}, float64 on the device."""
     N = n_t + n_v
-    s = N / n_t   # the train grads average the N-scaled backprops over the train rows
+    # the train grads average the backprops, N-scaled for a mean loss, over the train rows
+    s = (N if reduction == "mean" else 1) / n_t
     names = _param_names(model)
     dots, grads, mags = {}, {}, {}
 
@@ -123,25 +124,20 @@ def _expected_lm(model, cap, n_t, n_v):
     return dots, grads, mags
 
 
-def _close_to_sum(got, want, mag, tol, what):
-    """|got - want| <= tol * max(mag, rms(want)) elementwise, mag = the summed magnitudes of
-    the addends: the rounding bound of a sum of separately rounded contributions."""
-    got = got.double()
-    rms = want.pow(2).mean().sqrt().item()
-    worst = ((got - want).abs() / torch.clamp(mag, min=max(rms, 1e-300))).max().item()
-    assert worst <= tol, f"{what}: worst error {worst:.3e} of the addends' size > {tol:.1e}"
-    return worst
-
-
-def _lm_step(model, X, Y, n_t, n_v, **options):
+def _lm_step(model, X, Y, n_t, n_v, loss_reduction="mean", **options):
     """One GradDotProd step through the engine (the reference's step order); returns the
-    per-parameter dots, the .grad values, the logged aggregate and the capture."""
+    per-parameter dots, the .grad values, the logged aggregate and the capture.  With
+    loss_reduction='sum' the loss is the token sum (the model's token mean times N T)."""
     opt = torch.optim.SGD(model.parameters(), lr=0.0)
-    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True, **options)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True,
+                            loss_reduction=loss_reduction, **options)
     eng.attach(opt)
     cap = HookCapture(model, tuple(S._supported_layers_dotprod))
     eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
-    model(X, Y).backward()
+    loss = model(X, Y)
+    if loss_reduction == "sum":
+        loss = loss * X.numel()
+    loss.backward()
     torch.cuda.synchronize()
     dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()
             if hasattr(p, "grad_dot_prod")}
@@ -154,8 +150,8 @@ def _lm_step(model, X, Y, n_t, n_v, **options):
     return eng, dots, grads, total, cap
 
 
-def _check_lm(model, dots, grads, total, cap, n_t, n_v):
-    want_dots, want_grads, mags = _expected_lm(model, cap, n_t, n_v)
+def _check_lm(model, dots, grads, total, cap, n_t, n_v, reduction="mean"):
+    want_dots, want_grads, mags = _expected_lm(model, cap, n_t, n_v, reduction)
     contributions = {}
     for mname, m in model.named_modules():
         if mname in cap.A:
@@ -171,7 +167,7 @@ def _check_lm(model, dots, grads, total, cap, n_t, n_v):
     assert sorted(grads) == trainable and sorted(want_grads) == trainable
     for name in trainable:
         if contributions.get(name, 1) > 1:   # a tied weight: Linear + Embedding train grads
-            worst = _close_to_sum(grads[name], want_grads[name], mags[name], BF16_TOL,
+            worst = assert_close_to_sum(grads[name], want_grads[name], mags[name], BF16_TOL,
                                   f"grad {name}")
         else:
             worst = assert_close(grads[name], want_grads[name], BF16_TOL, f"grad {name}")
@@ -483,3 +479,25 @@ def test_linear_operand_above_2gib(gpu):
     bdot, _ = _native.ops().bias_dot(G, n_val)
     torch.cuda.synchronize()
     assert_close(bdot, R.bias_dot_exact(G, n_val), BF16_TOL, "bias_dot > 2 GiB")
+
+
+def test_sum_reduction_lm_step(gpu):
+    """loss_reduction='sum' through the fused dot + train-gradient pass (bf16, T = 64, every
+    Linear on the val-gradient algorithm): the backprops are not rescaled (the reference
+    scales them by N only for 'mean', autograd_grad_sample_dotprod.py:132-134), so the dots
+    are those of the token-summed loss and every train gradient -- bias included, whose stage
+    divides by n_train either way (:67, :199-222) -- is the train rows' mean; checked against
+    the float64 forms on the captured activations and backprops."""
+    torch.manual_seed(31)
+    T, vocab, n_t, n_v = 64, 64, 3, 2
+    cfg = LMConfig(n_layer=1, n_head=2, d_model=64, d_mlp=128, vocab=vocab, n_ctx=T)
+    model = CausalLM(cfg).to(gpu, torch.bfloat16)
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=32, device=gpu)
+    _say("sum-reduction LM step")
+    S.ALGO_LOG.clear()
+    eng, dots, grads, total, cap = _lm_step(model, X, Y, n_t, n_v, loss_reduction="sum",
+                                            record_algorithms=True, linear_algo="valgrad")
+    fused = sorted(k for k, v in S.ALGO_LOG.items() if v[1] == "valgrad+train_grad")
+    assert fused == ["h.0.fc", "h.0.fc_out", "h.0.proj", "h.0.qkv"], S.ALGO_LOG
+    _check_lm(model, dots, grads, total, cap, n_t, n_v, reduction="sum")
+    eng.detach()

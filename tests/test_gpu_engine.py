@@ -807,3 +807,4 @@ def test_ordered_sum_matches_sequential_in_place_adds(gpu, first, n):
     # a different order gives different bits: the order is the reference's, not any order
     rev = [s.to(gpu) for s in srcs[:1] + srcs[:0:-1]]
     assert not torch.equal(_native.ops().ordered_sum_(rev), want)
+

@@ -566,3 +566,34 @@ def test_sum_reduction_engine_dots_and_grads():
     for name, gr in g.items():
         assert_close(dots[name], brute.pairwise_dots(gr, n_v), FP32_TOL, f"dot {name}")
         assert_close(grads[name], brute.train_mean(gr, n_v, 1.0), FP32_TOL, f"grad {name}")
+
+
+def test_gradient_accumulation_over_backward_passes():
+    """Several backward passes before prepare_gradients (the reference loop's gradient
+    accumulation, Examples/GradDotProd_LM/training_loop.py:122-144, each on loss / k):
+    grad_dot_prod is the last pass's (assigned), train_grad the sum of every pass's (added in
+    place, supported_layers_grad_samplers_dotprod.py:44-70)."""
+    torch.manual_seed(4)
+    dims = (32, 24, 10)
+    model = MLP(dims)
+    ref = copy.deepcopy(model).double()
+    n_t, n_v, k = 10, 3, 3
+    X = torch.randn(n_t + n_v, dims[0], generator=gen(21))
+    Y = torch.randint(0, 10, (n_t + n_v,), generator=gen(22))
+    with use_oracle_backend():
+        eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=False,
+                                precision="fp32")
+        eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
+        eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+        for _ in range(k):
+            (F.cross_entropy(model(X), Y) / k).backward()
+        dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()}
+        eng.prepare_gradients()
+        grads = {n: p.grad.clone() for n, p in model.named_parameters()}
+        eng.clear_gradients()
+        eng.detach()
+    N = n_t + n_v
+    g = brute.per_sample_grads(ref, X.double(), Y, _ce_sum, 1.0 / (N * k))
+    for name, gr in g.items():
+        assert_close(dots[name], brute.pairwise_dots(gr, n_v), FP32_TOL, f"dot {name}")
+        assert_close(grads[name], k * brute.train_mean(gr, n_v, N), FP32_TOL, f"grad {name}")

@@ -150,8 +150,12 @@ def _lm_step(model, X, Y, n_t, n_v, loss_reduction="mean", **options):
     return eng, dots, grads, total, cap
 
 
-def _check_lm(model, dots, grads, total, cap, n_t, n_v, reduction="mean"):
+def _check_lm(model, dots, grads, total, cap, n_t, n_v, reduction="mean", backwards=1):
+    """``backwards``: backward passes of the same batch and weights before the gradients were
+    read (gradient accumulation): the train gradients add up, the dots are the last pass's."""
     want_dots, want_grads, mags = _expected_lm(model, cap, n_t, n_v, reduction)
+    want_grads = {k: backwards * v for k, v in want_grads.items()}
+    mags = {k: backwards * v for k, v in mags.items()}
     contributions = {}
     for mname, m in model.named_modules():
         if mname in cap.A:
@@ -500,4 +504,40 @@ def test_sum_reduction_lm_step(gpu):
     fused = sorted(k for k, v in S.ALGO_LOG.items() if v[1] == "valgrad+train_grad")
     assert fused == ["h.0.fc", "h.0.fc_out", "h.0.proj", "h.0.qkv"], S.ALGO_LOG
     _check_lm(model, dots, grads, total, cap, n_t, n_v, reduction="sum")
+    eng.detach()
+
+
+def test_gradient_accumulation_lm_steps(gpu):
+    """Two backward passes per optimizer step, each on loss / 2 (the reference loop's
+    gradient accumulation, Examples/GradDotProd_LM/training_loop.py:122-144), through the
+    fused pass (bf16, T = 64): every parameter's dot is the last pass's (the samplers assign
+    it), every train gradient the sum of both passes' (added into param.train_grad,
+    supported_layers_grad_samplers_dotprod.py:44-70), tied weight included."""
+    torch.manual_seed(33)
+    T, vocab, n_t, n_v = 64, 64, 3, 2
+    cfg = LMConfig(n_layer=1, n_head=2, d_model=64, d_mlp=128, vocab=vocab, n_ctx=T)
+    model = CausalLM(cfg).to(gpu, torch.bfloat16)
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=34, device=gpu)
+    _say("gradient accumulation, 2 backward passes")
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True,
+                            record_algorithms=True, linear_algo="valgrad")
+    eng.attach(opt)
+    cap = HookCapture(model, tuple(S._supported_layers_dotprod))
+    eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+    S.ALGO_LOG.clear()
+    for _ in range(2):
+        (model(X, Y) / 2).backward()
+    torch.cuda.synchronize()
+    fused = sorted(k for k, v in S.ALGO_LOG.items() if v[1] == "valgrad+train_grad")
+    assert fused == ["h.0.fc", "h.0.fc_out", "h.0.proj", "h.0.qkv"], S.ALGO_LOG
+    dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    eng.prepare_gradients()
+    grads = {n: p.grad for n, p in model.named_parameters()
+             if p.grad is not None and "dummy_bias" not in n}
+    eng.aggregate_and_log()
+    total = eng.dot_product_log[-1]["dot_product"]
+    cap.remove()
+    _check_lm(model, dots, grads, total, cap, n_t, n_v, backwards=2)
     eng.detach()

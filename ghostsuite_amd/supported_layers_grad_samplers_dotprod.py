@@ -229,10 +229,12 @@ def _fused_dot_train_grad(layer: nn.Module, A: torch.Tensor, B: torch.Tensor,
     from the column sums of G as for a Linear layer."""
     scale = getattr(layer, "_gs_bias_grad_scale", None)
     bias = layer.bias is not None
+    grad_dtypes = (torch.bfloat16, torch.float32)   # train gradients in the parameters' dtype
     if scale is None or dtype != torch.bfloat16 or A.dtype != torch.bfloat16 or \
             (pairwise and options["store_pairs"]) or \
+            layer.weight.dtype not in grad_dtypes or \
             not getattr(layer.weight, "initially_requires_grad", False) or \
-            (bias and (layer.bias.dtype != torch.bfloat16 or
+            (bias and (layer.bias.dtype not in grad_dtypes or
                        not getattr(layer.bias, "initially_requires_grad", False))):
         return False
     Bc = B.to(dtype) if B.dtype != dtype else B
@@ -243,7 +245,8 @@ def _fused_dot_train_grad(layer: nn.Module, A: torch.Tensor, B: torch.Tensor,
                          _ALGOS[options["linear_algo"]], False) != _native.ALGO_VALGRAD:
         return False
     res = ops().linear_dot_train_grad(A, Bc, val_batch_size, semantics=sem, grad_scale=scale,
-                                      grad_dtype=A.dtype, bias=bias, bias_grad_scale=scale,
+                                      grad_dtype=layer.weight.dtype, bias=bias,
+                                      bias_grad_scale=scale,
                                       bias_grad_dtype=layer.bias.dtype if bias else None,
                                       conv1d=conv1d)
     if res is None:
@@ -296,14 +299,23 @@ def _compute_linear_train_grad(layer: nn.Linear, A: torch.Tensor, B: torch.Tenso
     parked = layer.__dict__.pop("_gs_weight_train_grad", None)
     if parked is not None:   # formed with the dots (_fused_dot_train_grad), same scale
         return parked
-    grad = _native_train_grad(A, B, val_batch_size, scale / n_t, False)
+    wdt = _grad_dtype(layer, A)
+    grad = _native_train_grad(A, B, val_batch_size, scale / n_t, False, wdt)
     if grad is not None:
         return grad
     A_tr = A[:n_t].reshape(-1, A.shape[-1])
     B_tr = B[:n_t].reshape(-1, B.shape[-1])
     if B_tr.dtype != A_tr.dtype:
         B_tr = B_tr.to(A_tr.dtype)
-    return _scaled_mm(B_tr.t(), A_tr, scale / n_t)
+    return _scaled_mm(B_tr.t(), A_tr, scale / n_t).to(wdt)
+
+
+def _grad_dtype(layer: nn.Module, A: torch.Tensor) -> torch.dtype:
+    """The dtype a weight's train gradient is formed in: the parameter's own, so that it can
+    become the parameter's .grad (under autocast the operands may be bf16 while the parameter
+    is fp32), else the activations'."""
+    wdt = layer.weight.dtype
+    return wdt if wdt in (torch.bfloat16, torch.float32, torch.float16) else A.dtype
 
 
 # Where the K-major train-gradient GEMM beats hipBLASLt (measured on MI355X, 16k-32k train
@@ -318,13 +330,14 @@ _TRAIN_GRAD_WIDE_TILES = 256
 
 
 def _native_train_grad(A: torch.Tensor, B: torch.Tensor, val_batch_size: int, alpha: float,
-                       conv1d: bool) -> Optional[torch.Tensor]:
+                       conv1d: bool, out_dtype: torch.dtype) -> Optional[torch.Tensor]:
     """The weight's train gradient from the K-major GEMM over the train rows as they lie
-    (gs_linear_train_grad: fp32 accumulation, alpha before the one rounding, in A's dtype);
-    None where that kernel does not apply (fp32 operands, unaligned or >2 GiB rows) or where
-    hipBLASLt is faster (from _TRAIN_GRAD_MAX_TILES tiles of 128 x 128 to below
-    _TRAIN_GRAD_WIDE_TILES tiles of 256 x 256)."""
-    if A.dtype != torch.bfloat16 or A.dim() < 2:
+    (gs_linear_train_grad: fp32 accumulation, alpha before the one rounding to out_dtype);
+    None where that kernel does not apply (fp32 operands or output dtype other than bf16 /
+    fp32, unaligned or >2 GiB rows) or where hipBLASLt is faster (from _TRAIN_GRAD_MAX_TILES
+    tiles of 128 x 128 to below _TRAIN_GRAD_WIDE_TILES tiles of 256 x 256)."""
+    if A.dtype != torch.bfloat16 or A.dim() < 2 or \
+            out_dtype not in (torch.bfloat16, torch.float32):
         return None
     tiles = math.ceil(A.shape[-1] / 128) * math.ceil(B.shape[-1] / 128)
     wide = math.ceil(A.shape[-1] / 256) * math.ceil(B.shape[-1] / 256)
@@ -332,7 +345,7 @@ def _native_train_grad(A: torch.Tensor, B: torch.Tensor, val_batch_size: int, al
         return None
     B = B if B.dtype == A.dtype else B.to(A.dtype)
     return ops().linear_train_grad(A, B, val_batch_size, alpha,
-                                   val_start=A.size(0) - val_batch_size, out_dtype=A.dtype,
+                                   val_start=A.size(0) - val_batch_size, out_dtype=out_dtype,
                                    conv1d=conv1d)
 
 
@@ -506,12 +519,13 @@ def _compute_Conv1D_train_grad(layer, A: torch.Tensor, B: torch.Tensor, val_batc
     parked = layer.__dict__.pop("_gs_weight_train_grad", None)
     if parked is not None:   # formed with the dots (_fused_dot_train_grad), same scale
         return parked
-    grad = _native_train_grad(A, B, val_batch_size, scale / n_t, True)
+    wdt = _grad_dtype(layer, A)
+    grad = _native_train_grad(A, B, val_batch_size, scale / n_t, True, wdt)
     if grad is not None:
         return grad
     A_tr = A[:n_t].reshape(-1, A.shape[-1])
     B_tr = B[:n_t].reshape(-1, B.shape[-1]).to(A_tr.dtype)
-    return _scaled_mm(A_tr.t(), B_tr, scale / n_t)
+    return _scaled_mm(A_tr.t(), B_tr, scale / n_t).to(wdt)
 
 
 # Conv2d ###################################################################################

@@ -541,3 +541,44 @@ def test_gradient_accumulation_lm_steps(gpu):
     cap.remove()
     _check_lm(model, dots, grads, total, cap, n_t, n_v, backwards=2)
     eng.detach()
+
+
+def test_autocast_lm_step(gpu):
+    """fp32 parameters with a bf16 autocast forward (the reference LM example's setting when
+    model_dtype and train_dtype differ, Examples/shared/training_utils.py:193-201): the hooks
+    see fp32 and bf16 activations and bf16 output gradients in varying pairs, promoted to a
+    common dtype before each dot (autograd_grad_sample_dotprod.py:116-123); the layers whose
+    operands are both bf16 take the fused pass.  Every dot and train gradient against the
+    float64 forms on the captured operands."""
+    torch.manual_seed(35)
+    T, vocab, n_t, n_v = 64, 64, 3, 2
+    cfg = LMConfig(n_layer=1, n_head=2, d_model=64, d_mlp=128, vocab=vocab, n_ctx=T)
+    model = CausalLM(cfg).to(gpu)
+    X, Y = synthetic_tokens(n_t + n_v, T, vocab, seed=36, device=gpu)
+    _say("autocast LM step")
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    eng = GradDotProdEngine(model, val_batch_size=n_v, use_dummy_bias=True,
+                            record_algorithms=True, linear_algo="valgrad")
+    eng.attach(opt)
+    cap = HookCapture(model, tuple(S._supported_layers_dotprod))
+    eng.attach_train_batch(X[:n_t], Y[:n_t], 0, 0)
+    S.ALGO_LOG.clear()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss = model(X, Y)
+    loss.backward()
+    torch.cuda.synchronize()
+    kinds = {n: (cap.A[n].dtype, cap.B[n].dtype) for n in cap.A if n.startswith("h.0.")}
+    assert len(set(kinds.values())) > 1, kinds   # mixed operand dtypes across the layers
+    fused = [n for n, v in S.ALGO_LOG.items() if v[1] == "valgrad+train_grad"]
+    assert fused, S.ALGO_LOG   # bf16 operands with fp32 parameters take the fused pass
+    dots = {n: p.grad_dot_prod.clone() for n, p in model.named_parameters()
+            if hasattr(p, "grad_dot_prod")}
+    eng.prepare_gradients()
+    grads = {n: p.grad for n, p in model.named_parameters()
+             if p.grad is not None and "dummy_bias" not in n}
+    assert all(g.dtype == torch.float32 for g in grads.values())   # the parameters' dtype
+    eng.aggregate_and_log()
+    total = eng.dot_product_log[-1]["dot_product"]
+    cap.remove()
+    _check_lm(model, dots, grads, total, cap, n_t, n_v)
+    eng.detach()

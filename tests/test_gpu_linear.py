@@ -382,19 +382,24 @@ def test_linear_train_grad_declines_and_sampler_falls_back(gpu):
         assert_close(got.float().cpu(), want, 1e-2, "sampler fallback")
     A3 = randn((4, 32, 40), 99, 1.0, torch.bfloat16).to(gpu)
     G3 = randn((4, 32, 24), 100, 1e-3, torch.bfloat16).to(gpu)
-    got = _compute_linear_train_grad(torch.nn.Linear(40, 24), A3, G3, 1, scale=2.0)
+    bf16 = dict(dtype=torch.bfloat16)
+    got = _compute_linear_train_grad(torch.nn.Linear(40, 24, **bf16), A3, G3, 1, scale=2.0)
     assert torch.equal(got, ops.linear_train_grad(A3, G3, 1, 2.0 / 3))
+    # An fp32 parameter with bf16 operands (autocast): the gradient in the parameter's dtype.
+    got = _compute_linear_train_grad(torch.nn.Linear(40, 24), A3, G3, 1, scale=2.0)
+    assert got.dtype == torch.float32
+    assert torch.equal(got, ops.linear_train_grad(A3, G3, 1, 2.0 / 3, out_dtype=torch.float32))
     # 256 to 1023 output tiles of 128 x 128: hipBLASLt through addmm (faster there).
     from ghostsuite_amd.supported_layers_grad_samplers_dotprod import _scaled_mm
     A4 = randn((3, 8, 2048), 101, 1.0, torch.bfloat16).to(gpu)
     G4 = randn((3, 8, 2048), 102, 1e-3, torch.bfloat16).to(gpu)
-    got = _compute_linear_train_grad(torch.nn.Linear(2048, 2048), A4, G4, 1, scale=2.0)
+    got = _compute_linear_train_grad(torch.nn.Linear(2048, 2048, **bf16), A4, G4, 1, scale=2.0)
     want = _scaled_mm(G4[:2].reshape(-1, 2048).t(), A4[:2].reshape(-1, 2048), 1.0)
     assert torch.equal(got, want)
     # 256 tiles of 256 x 256 and more: the wide-tile kernel again.
     A5 = randn((3, 16, 2048), 103, 1.0, torch.bfloat16).to(gpu)
     G5 = randn((3, 16, 8192), 104, 1e-3, torch.bfloat16).to(gpu)
-    got = _compute_linear_train_grad(torch.nn.Linear(2048, 8192), A5, G5, 1, scale=2.0)
+    got = _compute_linear_train_grad(torch.nn.Linear(2048, 8192, **bf16), A5, G5, 1, scale=2.0)
     assert torch.equal(got, ops.linear_train_grad(A5, G5, 1, 2.0 / 2))
 
 

@@ -1342,6 +1342,30 @@ __global__ void __launch_bounds__(256) rowdot_bias_finish_kernel(
   }
 }
 
+// part[0][i..i+3] + part[1][i..i+3] + ... over the splits, added in split order; the loads
+// of four splits at a time are unguarded, so they are in flight together.
+__device__ __forceinline__ float4 split_sum4(const float* __restrict__ part, int64_t count,
+                                             int splits, int64_t i) {
+  auto ld = [&](int k) { return *reinterpret_cast<const float4*>(part + k * count + i); };
+  auto add = [](float4& a, const float4& b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  };
+  float4 s = ld(0);
+  int k = 1;
+  for (; k + 4 <= splits; k += 4) {
+    const float4 v0 = ld(k), v1 = ld(k + 1), v2 = ld(k + 2), v3 = ld(k + 3);
+    add(s, v0);
+    add(s, v1);
+    add(s, v2);
+    add(s, v3);
+  }
+  for (; k < splits; ++k) add(s, ld(k));
+  return s;
+}
+
 // After tgdot_kernel, three independent block ranges of one launch, fixed order throughout:
 // blocks b < n_t take weight dot b from its `shares` wave shares and, with pbias, bias dot b
 // from its `bshares` shares; then (with bgrad) the bias train gradient, FINISH_GF features
@@ -1409,14 +1433,7 @@ __global__ void __launch_bounds__(256) tgdot_finish_kernel(
   b -= gblocks;
   const int64_t i = (b * 256 + threadIdx.x) * 4;
   if (i >= count) return;
-  float4 v = *reinterpret_cast<const float4*>(part + i);
-  for (int k = 1; k < sp; ++k) {
-    const float4 w = *reinterpret_cast<const float4*>(part + k * count + i);
-    v.x += w.x;
-    v.y += w.y;
-    v.z += w.z;
-    v.w += w.w;
-  }
+  float4 v = split_sum4(part, count, sp, i);
   v.x *= gscale;
   v.y *= gscale;
   v.z *= gscale;
@@ -2036,26 +2053,30 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   f32x16_t acc[C::MI][C::NI];
   zero_acc<TrBF16, C>(acc);
   float s_prev = 0.f;  // <acc, V tile> of this wave at the previous boundary
-  // This lane's V elements, loaded once and held for the work item: for block (i, j) and
-  // row group g, the 4 consecutive rows m(i, g) .. m(i, g) + 3 of column n(j), one 8-byte
-  // load of V^T row n (M and N are multiples of 8, so a group is wholly inside or outside
-  // the matrix).
-  uint2 vr[C::MI][C::NI][4];
-  {
-    const int64_t m_lane = mt * C::BM + wm * 32 * C::MI + 4 * (lane >> 5);
+  // This lane's V elements: for block (i, j) and row group g, the 4 consecutive rows
+  // m(i, g) .. m(i, g) + 3 of column n(j), one 8-byte load of V^T row n (M and N are
+  // multiples of 8, so a group is wholly inside or outside the matrix).  With 64 x 64 wave
+  // tiles they are loaded once and held for the work item (32 registers); wider wave tiles
+  // have no registers to spare beside their accumulators, and load them again from V^T (in
+  // L2) at each boundary, a few per sample.
+  constexpr bool VHELD = C::MI * C::NI <= 4;
+  const int64_t m_lane = mt * C::BM + wm * 32 * C::MI + 4 * (lane >> 5);
+  const int64_t n_lane = nt * C::BN + wn * 32 * C::NI + (lane & 31);
+  // (captures by value: a reference to the kernel-argument struct from inside the stage
+  // loop makes the compiler copy the struct to private memory)
+  auto vload = [Vt = q.Vt, M = p.M, N = p.N, m_lane, n_lane](int i, int j, int g) {
+    const int64_t n = n_lane + j * 32, m = m_lane + i * 32 + 8 * g;
+    return (n < N && m < M) ? *reinterpret_cast<const uint2*>(Vt + n * M + m)
+                            : make_uint2(0u, 0u);
+  };
+  uint2 vr[VHELD ? C::MI : 1][VHELD ? C::NI : 1][4];
+  if constexpr (VHELD) {
 #pragma unroll
-    for (int j = 0; j < C::NI; ++j) {
-      const int64_t n = nt * C::BN + wn * 32 * C::NI + j * 32 + (lane & 31);
+    for (int j = 0; j < C::NI; ++j)
 #pragma unroll
       for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t m = m_lane + i * 32 + 8 * g;
-          vr[i][j][g] = (n < p.N && m < p.M)
-                            ? *reinterpret_cast<const uint2*>(q.Vt + n * p.M + m)
-                            : make_uint2(0u, 0u);
-        }
-    }
+        for (int g = 0; g < 4; ++g) vr[i][j][g] = vload(i, j, g);
   }
   // Column sums of L (G's train rows: the bias terms), with CS: every workgroup along N
   // takes a share, so no work item runs longer than the others.  After the MFMAs of the
@@ -2087,7 +2108,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   int64_t sample = k_begin / q.T;
   int left = static_cast<int>(((sample + 1) * q.T - k_begin) / D::KB);
   bool started = sample * q.T == k_begin;  // the current sample starts inside this split
-  auto flush = [&](bool ended) {
+  auto flush = [&](bool ended) __attribute__((always_inline)) {
     float d = 0.f;
 #pragma unroll
     for (int i = 0; i < C::MI; ++i)
@@ -2095,7 +2116,7 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
       for (int j = 0; j < C::NI; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const uint2 w = vr[i][j][g];
+          const uint2 w = VHELD ? vr[VHELD ? i : 0][VHELD ? j : 0][g] : vload(i, j, g);
           d += acc[i][j][4 * g] * __uint_as_float(w.x << 16) +
                acc[i][j][4 * g + 1] * __uint_as_float(w.x & 0xFFFF0000u) +
                acc[i][j][4 * g + 2] * __uint_as_float(w.y << 16) +
@@ -2159,30 +2180,6 @@ __global__ void __launch_bounds__(C::NT, C::MIN_WAVES) tgdot_kernel(TgParams q) 
   e.c_ld = p.N;
   e.C = static_cast<float*>(p.out) + split * p.M * p.N;
   store_epilogue<TrF32, C>(e, acc, mt, nt);
-}
-
-// part[0][i..i+3] + part[1][i..i+3] + ... over the splits, added in split order; the loads
-// of four splits at a time are unguarded, so they are in flight together.
-__device__ __forceinline__ float4 split_sum4(const float* __restrict__ part, int64_t count,
-                                             int splits, int64_t i) {
-  auto ld = [&](int k) { return *reinterpret_cast<const float4*>(part + k * count + i); };
-  auto add = [](float4& a, const float4& b) {
-    a.x += b.x;
-    a.y += b.y;
-    a.z += b.z;
-    a.w += b.w;
-  };
-  float4 s = ld(0);
-  int k = 1;
-  for (; k + 4 <= splits; k += 4) {
-    const float4 v0 = ld(k), v1 = ld(k + 1), v2 = ld(k + 2), v3 = ld(k + 3);
-    add(s, v0);
-    add(s, v1);
-    add(s, v2);
-    add(s, v3);
-  }
-  for (; k < splits; ++k) add(s, ld(k));
-  return s;
 }
 
 // out[i] = alpha * (sum over the splits of part[s][i]) in fixed order, rounded once to bf16
@@ -3212,6 +3209,8 @@ struct TgPlan {
   int64_t m_tiles, n_tiles, bias;  // bias: the bias terms are wanted
   int bias_a;                // the bias terms are A's column sums (d_in wide), not G's
   int64_t bias_d;            // features of the bias side
+  int wide;                  // train rows in 256 x 256 tiles (TnCW), else 128 x 128 (TnC)
+  int wm, wn;                // waves of a tile along M and N
 };
 bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
            int semantics) {
@@ -3220,6 +3219,7 @@ bool tg_ok(int dtype, int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t
   if (!val_tn(dtype, n_val, T, d_in, d_out, semantics == GS_SEM_PRESUM)) return false;
   return tn_ok(nullptr, d_out, nullptr, d_in, N * T, d_out, d_in);
 }
+static_assert(TnDW::KB == TnD::KB, "both train-row tile shapes share the stage height");
 TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out, int semantics,
                bool bias, bool bias_a = false) {
   TgPlan t{};
@@ -3230,12 +3230,28 @@ TgPlan plan_tg(int64_t N, int64_t n_val, int64_t T, int64_t d_in, int64_t d_out,
   t.n_val = n_val;
   t.n_t = N - n_val;
   t.K = t.n_t * T;
-  t.m_tiles = ceil_div(d_out, TnC::BM);
-  t.n_tiles = ceil_div(d_in, TnC::BN);
-  // The train-gradient GEMM's splits, at least one sample long (a sample then meets at most
-  // two splits).
-  t.sp = tn_splits(t.K, d_out, d_in);
-  t.kper = tn_kper(t.K, static_cast<int>(t.sp));
+  // The train rows' GEMM in 256 x 256 tiles of 8 waves of 128 x 64 (a quarter fewer LDS
+  // fragment bytes per flop than 64 x 64 wave tiles, half the stage bytes; one workgroup per
+  // CU), unsplit, when those tiles alone cover 7/8 of the CUs or more (the Pythia-1B MLP and
+  // vocabulary head: 8-10% faster); in 128 x 128 tiles (two workgroups per CU) with split
+  // k-rows otherwise: filling the CUs by splitting wide tiles costs their fp32 partials (7
+  // splits of a 768 x 3072 gradient write 66 MB, and measured slower).
+  const int64_t wt = ceil_div(d_out, TnCW::BM) * ceil_div(d_in, TnCW::BN);
+  t.wide = wt >= 224 ? 1 : 0;
+  if (t.wide) {
+    t.m_tiles = ceil_div(d_out, TnCW::BM);
+    t.n_tiles = ceil_div(d_in, TnCW::BN);
+    t.wm = TnCW::WM;
+    t.wn = TnCW::WN;
+    t.kper = t.K;
+  } else {
+    t.m_tiles = ceil_div(d_out, TnC::BM);
+    t.n_tiles = ceil_div(d_in, TnC::BN);
+    t.wm = TnC::WM;
+    t.wn = TnC::WN;
+    t.kper = tn_kper(t.K, tn_splits(t.K, d_out, d_in));
+  }
+  // Splits at least one sample long (a sample then meets at most two splits).
   if (t.kper < T) t.kper = T;
   t.sp = ceil_div(t.K, t.kper);
   t.bias = bias ? 1 : 0;
@@ -3258,9 +3274,9 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
   const int64_t vp_rows =
       t.presum ? presum_rows(T) : tn_vsum_rows(t.vk, d_in, d_out, !t.bias_a);
   b.vp = t.bias ? c.template take<float>(vp_rows * t.bias_d) : nullptr;
-  b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2 * t.n_t);
+  b.pdot = c.template take<float>(t.m_tiles * t.n_tiles * (t.wm * t.wn) * 2 * t.n_t);
   b.csum = t.bias ? c.template take<float>(t.n_t * 2 * (T / TnD::KB) * t.bias_d) : nullptr;
-  const int64_t bw = t.bias_a ? t.n_tiles * TnC::WN : t.m_tiles * TnC::WM;
+  const int64_t bw = t.bias_a ? t.n_tiles * t.wn : t.m_tiles * t.wm;
   b.pbias = t.bias ? c.template take<float>(t.n_t * (T / TnD::KB) * bw) : nullptr;
   b.tgpart = c.template take<float>(t.sp * d_out * d_in);
   return b;
@@ -3393,21 +3409,29 @@ int dot_train_grad(bool bias_a, const void* A, const void* G, int dtype, int64_t
   q.pbias = b.pbias;
   const int64_t items = t.m_tiles * t.n_tiles * t.sp;
   if (items > INT32_MAX) return fail(GS_ERR_UNSUPPORTED, "GEMM grid too large");
-  if (q.csum == nullptr)
-    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 0>), dim3(static_cast<unsigned>(items)),
-                       dim3(TnC::NT), 0, s, q);
-  else if (!t.bias_a)
-    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 1>), dim3(static_cast<unsigned>(items)),
-                       dim3(TnC::NT), 0, s, q);
-  else
-    hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 2>), dim3(static_cast<unsigned>(items)),
-                       dim3(TnC::NT), 0, s, q);
+  const dim3 tg_grid(static_cast<unsigned>(items));
+  const int cs = q.csum == nullptr ? 0 : (t.bias_a ? 2 : 1);
+  if (t.wide) {
+    if (cs == 0)
+      hipLaunchKernelGGL((tgdot_kernel<TnCW, TnDW, 0>), tg_grid, dim3(TnCW::NT), 0, s, q);
+    else if (cs == 1)
+      hipLaunchKernelGGL((tgdot_kernel<TnCW, TnDW, 1>), tg_grid, dim3(TnCW::NT), 0, s, q);
+    else
+      hipLaunchKernelGGL((tgdot_kernel<TnCW, TnDW, 2>), tg_grid, dim3(TnCW::NT), 0, s, q);
+  } else {
+    if (cs == 0)
+      hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 0>), tg_grid, dim3(TnC::NT), 0, s, q);
+    else if (cs == 1)
+      hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 1>), tg_grid, dim3(TnC::NT), 0, s, q);
+    else
+      hipLaunchKernelGGL((tgdot_kernel<TnC, TnD, 2>), tg_grid, dim3(TnC::NT), 0, s, q);
+  }
   rc = check_launch("tgdot_kernel");
   if (rc) return rc;
   // One launch: the dots, the bias train gradient and the train-gradient reduction.
-  const int64_t shares = t.m_tiles * t.n_tiles * (TnC::WM * TnC::WN) * 2;
+  const int64_t shares = t.m_tiles * t.n_tiles * (t.wm * t.wn) * 2;
   const int64_t sps = T / TnD::KB;
-  const int64_t bshares = sps * (t.bias_a ? t.n_tiles * TnC::WN : t.m_tiles * TnC::WM);
+  const int64_t bshares = sps * (t.bias_a ? t.n_tiles * t.wn : t.m_tiles * t.wm);
   const float* pbias = out_bias_dot != nullptr ? b.pbias : nullptr;
   const int64_t gblocks =
       out_bias_grad != nullptr ? ceil_div(t.bias_d, int64_t{FINISH_GF}) : 0;

@@ -420,6 +420,11 @@ def test_linear_train_grad_declines_and_sampler_falls_back(gpu):
     (9, 1, 192, 512, 512, "presum", "last", True),
     (12, 2, 320, 1024, 1024, "pairwise", "first", True),
     (5, 1, 1024, 136, 264, "pairwise", "mid", True),
+    # 256 x 256 train-row tiles (224 tiles and more): whole, and cut by the matrix edges on
+    # both sides, with and without the bias terms
+    (4, 1, 64, 2048, 7168, "pairwise", "mid", True),
+    (4, 1, 64, 2000, 7176, "presum", "first", True),
+    (4, 2, 64, 7176, 2000, "pairwise", "last", False),
 ])
 @pytest.mark.parametrize("grad_dtype", [torch.bfloat16, torch.float32])
 def test_linear_dot_train_grad(gpu, case, grad_dtype):
@@ -523,7 +528,31 @@ def _random_fused_cases(n, seed):
     return cases
 
 
-@pytest.mark.parametrize("case", _random_fused_cases(24, 2026))
+def _wide_tiles(d_in, d_out):
+    """Whether the fused pass takes the train rows in 256 x 256 tiles: 224 of them or more."""
+    return -(-d_out // 256) * -(-d_in // 256) >= 224
+
+
+def _random_wide_cases(n, seed):
+    """Seeded shapes of the 256 x 256 train-row tiles: wide feature counts, ragged at both
+    edges, and few rows, so the float64 checks stay within seconds."""
+    g = torch.Generator().manual_seed(seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    cases = []
+    while len(cases) < n:
+        n_val = pick(1, 2)
+        N = n_val + pick(1, 3)
+        T = 64
+        d_in, d_out = 8 * pick(200, 1000), 8 * pick(200, 1000)
+        if not _wide_tiles(d_in, d_out):
+            continue
+        vs = pick(0, N - n_val)
+        sem = "presum" if pick(0, 1) else "pairwise"
+        cases.append((N, n_val, vs, T, d_in, d_out, sem, bool(pick(0, 1))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_fused_cases(24, 2026) + _random_wide_cases(3, 2027))
 def test_linear_dot_train_grad_random_shapes(gpu, case):
     """gs_linear_dot_train_grad over seeded random shapes (split counts, tile edges, cut
     samples and val positions vary together) against the float64 closed forms; the same call

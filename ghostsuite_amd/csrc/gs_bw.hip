@@ -590,48 +590,49 @@ constexpr int EMB_SORT_MAX = 8192, EMB_QBITS = 13;
 constexpr uint32_t EMB_NOKEY = 0xFFFFE000u, EMB_PAD = 0xFFFFFFFFu;
 __device__ __forceinline__ bool emb_nokey(uint32_t k) { return k >= EMB_NOKEY; }
 
-__device__ __forceinline__ uint32_t emb_key(const int64_t* __restrict__ ids, const RowMap& val,
-                                            int64_t vocab, int i) {
-  const uint32_t len = static_cast<uint32_t>(val.seglen);  // n_vt < 2^13: 32-bit division
-  const uint32_t seg = static_cast<uint32_t>(i) / len;
-  const int64_t id = ids[val.phys_row(seg, static_cast<uint32_t>(i) - seg * len)];
-  return (id >= 0 && id < vocab) ? (static_cast<uint32_t>(id) << EMB_QBITS) |
-                                       static_cast<uint32_t>(i)
-                                 : EMB_NOKEY | static_cast<uint32_t>(i);
-}
-
-// keys[rank(i)] = key(i); val tokens whose id is out of range go last, in index order.  A
-// workgroup ranks EMB_RK keys, each counted against all keys by EMB_RP threads (one slice of
-// the keys each) and the slice counts combined through LDS.
-// ukeys[i] = key(i) for i < n4 (padded with no-keys to a multiple of 4), table[0, vocab) = -1.
-__global__ void __launch_bounds__(BW_THREADS) emb_key_kernel(
+// keys[rank(i)] = key(i) for the n val tokens (the keys are distinct, so a key's rank is the
+// number of smaller keys); val tokens whose id is out of range go last, in index order.  Each
+// workgroup forms all n keys in LDS from the ids and ranks EMB_RK of them, each counted
+// against all keys by EMB_RP threads (one interleaved slice of the keys each) with the slice
+// counts combined through LDS; it also resets its grid-stride share of table[0, vocab) to -1.
+constexpr int EMB_RK = 8, EMB_RP = BW_THREADS / EMB_RK;
+__global__ void __launch_bounds__(BW_THREADS) emb_rank_kernel(
     const int64_t* __restrict__ ids, RowMap val, int64_t vocab, int32_t* __restrict__ table,
-    uint32_t* __restrict__ ukeys) {
-  const int n = static_cast<int>(val.total()), n4 = (n + 3) / 4 * 4;
-  const int64_t gstride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  const int64_t x0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  for (int64_t x = x0; x < vocab; x += gstride) table[x] = -1;
-  for (int64_t j = x0; j < n4; j += gstride)
-    ukeys[j] = j < n ? emb_key(ids, val, vocab, static_cast<int>(j)) : EMB_PAD;
-}
-
-constexpr int EMB_RK = 4, EMB_RP = BW_THREADS / EMB_RK;
-__global__ void __launch_bounds__(BW_THREADS) emb_rank_kernel(const uint32_t* __restrict__ ukeys,
-                                                              int n,
-                                                              uint32_t* __restrict__ keys) {
+    uint32_t* __restrict__ keys) {
   __shared__ __attribute__((aligned(16))) uint32_t sk[EMB_SORT_MAX];
   __shared__ int cnt[EMB_RP][EMB_RK];
-  const int n4 = (n + 3) / 4 * 4;
-  for (int j = threadIdx.x * 4; j < n4; j += blockDim.x * 4)
-    *reinterpret_cast<uint4*>(sk + j) = *reinterpret_cast<const uint4*>(ukeys + j);
+  const int n = static_cast<int>(val.total()), n4 = (n + 3) / 4 * 4;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t x = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; x < vocab;
+       x += gstride)
+    table[x] = -1;
+  // The val rows are one contiguous block, so val token j is ids[first + j]; a thread's
+  // loads are all issued before the first key is formed.
+  const int64_t* vids = ids + val.phys_row(0, 0);
+  constexpr int PER = EMB_SORT_MAX / BW_THREADS;
+  int64_t idr[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int j = threadIdx.x + q * BW_THREADS;
+    idr[q] = j < n ? vids[j] : -1;
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int j = threadIdx.x + q * BW_THREADS;
+    if (j < n4)
+      sk[j] = j >= n ? EMB_PAD
+                     : (idr[q] >= 0 && idr[q] < vocab)
+                           ? (static_cast<uint32_t>(idr[q]) << EMB_QBITS) | static_cast<uint32_t>(j)
+                           : EMB_NOKEY | static_cast<uint32_t>(j);
+  }
   __syncthreads();
   const int kk = threadIdx.x % EMB_RK, part = threadIdx.x / EMB_RK;
   const int i = blockIdx.x * EMB_RK + kk;
   const uint32_t k = i < n ? sk[i] : EMB_PAD;
-  const int span = (n4 / 4 + EMB_RP - 1) / EMB_RP * 4;  // keys per slice, a multiple of 4
-  const int j0 = part * span, j1 = j0 + span < n4 ? j0 + span : n4;
-  int lt = 0;  // keys are distinct, so the rank is the number of smaller keys
-  for (int j = j0; j < j1; j += 4) {
+  // Slice `part` is every EMB_RP-th group of four keys, so the parts of a wave read
+  // consecutive 16-byte words (no LDS bank conflicts).
+  int lt = 0;
+  for (int j = part * 4; j < n4; j += EMB_RP * 4) {
     const uint4 w = *reinterpret_cast<const uint4*>(sk + j);
     lt += (w.x < k) + (w.y < k) + (w.z < k) + (w.w < k);
   }
@@ -1116,7 +1117,6 @@ void carve_embedding(S& c, int64_t N, int64_t n_val, int64_t T, int64_t d, int64
   c.template take<int32_t>(vocab);
   if (emb_sorted(n_val, T, vocab)) {
     c.template take<uint32_t>(n_vt);
-    c.template take<uint32_t>(cdiv(n_vt, 4) * 4);
     c.template take<float>(n_vt * d);
   } else {
     c.template take<unsigned>(EMB_SLOTS);
@@ -1157,14 +1157,10 @@ extern "C" int gs_embedding_dot(const int64_t* ids, const void* G, int dtype, in
   const RowMap tr = train_rows(N, n_val, val_start, T);
   if (emb_sorted(n_val, T, vocab)) {
     uint32_t* keys = cv.take<uint32_t>(n_vt);
-    uint32_t* ukeys = cv.take<uint32_t>(cdiv(n_vt, 4) * 4);
     float* S = cv.take<float>(n_vt * d);
     float* part = cv.take<float>(n_t * chunks);
-    hipLaunchKernelGGL(emb_key_kernel,
-                       dim3(static_cast<unsigned>(cdiv(std::max(vocab, n_vt), BW_THREADS))),
-                       dim3(BW_THREADS), 0, s, ids, va, vocab, table, ukeys);
     hipLaunchKernelGGL(emb_rank_kernel, dim3(static_cast<unsigned>(cdiv(n_vt, EMB_RK))),
-                       dim3(BW_THREADS), 0, s, ukeys, static_cast<int>(n_vt), keys);
+                       dim3(BW_THREADS), 0, s, ids, va, vocab, table, keys);
     const dim3 gv(static_cast<unsigned>(n_vt));
     const dim3 gt(static_cast<unsigned>(chunks), static_cast<unsigned>(n_t));
     if (dtype == GS_DTYPE_BF16) {

@@ -912,44 +912,53 @@ int launch_ln_any(const void* X, const void* G, int64_t N, int64_t T, int64_t F,
 // out[i] = ((s_0[i] + s_1[i]) + s_2[i]) + ... in the order given, each partial sum rounded
 // to out's dtype: the in-place `total += s_k` sequence of the engine's aggregation (fp32
 // arithmetic, then the total's dtype).  Up to OS_MAX sources per launch (the pointers travel
-// in the kernel arguments, 2 KiB); longer lists continue from out.  The source loop is
-// unrolled with compile-time indices (the arguments stay in scalar registers), its loads
-// issued eight at a time before their adds.
-constexpr int OS_MAX = 256, OS_BATCH = 8;
+// in the kernel arguments, 2 KiB); longer lists continue from out.
+constexpr int OS_MAX = 256;
 struct OrderedSrcs {
   const void* p[OS_MAX];
   uint32_t bf16[OS_MAX / 32];   // bit k % 32 of word k / 32: source k holds bf16
   int count;
 };
 
+// A workgroup takes OS_E consecutive elements.  First every source's values are staged in
+// LDS as fp32 (exact for bf16): wave w loads sources w, w + 4, ... with its lanes over the
+// elements, so a source's pointer is wave-uniform and all the loads are in flight together.
+// Then the lanes of wave 0 run the sums over the staged values in source order.
+constexpr int OS_E = 64;
 template <class OE>
 __global__ void __launch_bounds__(256) ordered_sum_kernel(OrderedSrcs src, int64_t n,
                                                           OE* __restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  float acc = 0.f;
+  __shared__ float vals[OS_MAX][OS_E];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * OS_E + lane;
+  const bool live = i < n;
+  const int64_t ic = live ? i : n - 1;
+  // Branch-free loads (a branch around a load makes the compiler wait for it before the
+  // next): each value as two 16-bit halves at a wave-uniform stride, the high half of an fp32
+  // value being the whole of a bf16 one; sources past the end reload the last one.
+  constexpr int B = 16;
+  for (int k0 = wid; k0 < src.count; k0 += 4 * B) {
+    uint32_t bits[B];
 #pragma unroll
-  for (int k0 = 0; k0 < OS_MAX; k0 += OS_BATCH) {
-    if (k0 >= src.count) break;
-    float v[OS_BATCH];
-#pragma unroll
-    for (int u = 0; u < OS_BATCH; ++u) {
-      const int k = k0 + u;
-      v[u] = 0.f;
-      if (k < src.count)
-        v[u] = (src.bf16[k / 32] >> (k % 32)) & 1u
-                   ? bf16_to_f32(static_cast<const uint16_t*>(src.p[k])[i])
-                   : static_cast<const float*>(src.p[k])[i];
+    for (int u = 0; u < B; ++u) {
+      const int k = k0 + 4 * u < src.count ? k0 + 4 * u : src.count - 1;
+      const bool b16 = (src.bf16[k / 32] >> (k % 32)) & 1u;
+      const int64_t st = b16 ? 2 : 4;
+      const unsigned char* p = static_cast<const unsigned char*>(src.p[k]) + ic * st;
+      const uint32_t lo = *reinterpret_cast<const uint16_t*>(p);
+      const uint32_t hi = *reinterpret_cast<const uint16_t*>(p + st - 2);
+      bits[u] = (hi << 16) | (b16 ? 0u : lo);
     }
 #pragma unroll
-    for (int u = 0; u < OS_BATCH; ++u) {
-      const int k = k0 + u;
-      if (k == 0)
-        acc = v[0];   // the first tensor is the total: no rounding
-      else if (k < src.count)
-        acc = to_f32<OE>(from_f32<OE>(acc + v[u]));
-    }
+    for (int u = 0; u < B; ++u)
+      if (k0 + 4 * u < src.count) vals[k0 + 4 * u][lane] = __uint_as_float(bits[u]);
   }
+  __syncthreads();
+  if (wid != 0 || !live) return;
+  float acc = vals[0][lane];   // the first tensor is the total: no rounding
+#pragma unroll 8
+  for (int k = 1; k < src.count; ++k) acc = to_f32<OE>(from_f32<OE>(acc + vals[k][lane]));
   out[i] = from_f32<OE>(acc);
 }
 
@@ -970,10 +979,10 @@ extern "C" int gs_ordered_sum(const void* const* srcs, const int* dtypes, int co
       return fail(GS_ERR_DTYPE, "gs_ordered_sum: source dtypes must be bf16 or fp32");
   }
   if (n == 0) return GS_OK;
-  if (n > static_cast<int64_t>(INT32_MAX) * 256)
+  if (n > static_cast<int64_t>(INT32_MAX) * OS_E)
     return fail(GS_ERR_UNSUPPORTED, "gs_ordered_sum: too many elements");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  const dim3 grid(static_cast<unsigned>((n + OS_E - 1) / OS_E));
   // the first launch starts from srcs[0]; each later one from out (the running total, already
   // rounded to out's dtype) and the next OS_MAX - 1 sources
   int k0 = 0;

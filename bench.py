@@ -565,6 +565,45 @@ def achievable_peak(dev, reps: int = 10, n: int = 8192):
             "TFLOP/s": 2.0 * n ** 3 / (ms * 1e-3) / 1e12}
 
 
+def vendor_route(dev, reps: int = 10):
+    """The dominant op's outputs at the fc_out shape (A[20,1024,3072], G[20,1024,768] bf16,
+    4 val rows last) through the vendor library instead: V = G_val^T A_val, the row-dot
+    GEMM A_train V^T with its per-sample reduction against G_train, and the train gradient
+    G_train^T A_train (three torch.mm calls on hipBLASLt plus torch's elementwise reduction;
+    the transposed operands made contiguous outside the timed region, except V^T)."""
+    g = torch.Generator().manual_seed(21)
+    N, n_val, T, d_in, d_out = 20, 4, 1024, 3072, 768
+    n_t = N - n_val
+    A = torch.randn(N * T, d_in, generator=g).to(dev, torch.bfloat16)
+    G = (torch.randn(N * T, d_out, generator=g) * 1e-3).to(dev, torch.bfloat16)
+    A_tr, A_v = A[: n_t * T], A[n_t * T:]
+    G_tr = G[: n_t * T]
+    G_vT = G[n_t * T:].t().contiguous()
+    G_trT = G_tr.t().contiguous()
+
+    def route():
+        V = torch.mm(G_vT, A_v)                                   # [d_out, d_in]
+        U = torch.mm(A_tr, V.t().contiguous())                    # [n_t T, d_out]
+        dots = (U.float() * G_tr.float()).sum(1).view(n_t, T).sum(1)
+        grad = torch.mm(G_trT, A_tr)                              # [d_out, d_in]
+        return dots, grad
+
+    for _ in range(3):
+        route()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        route()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    del A, G, G_vT, G_trT
+    return {"shape": "A[20,1024,3072] G[20,1024,768] bf16, 4 val rows last (fc_out)",
+            "ms": ms, "kernels": "torch.mm (hipBLASLt) x3 + torch elementwise row-dot"}
+
+
 def emb_grad_pad_bench(dev, reps: int = 10):
     """The Embedding train gradient on a padded batch: 32 train + 2 val rows of T=2048 with
     90% of the tokens one pad id (65536 train tokens, a 59k-token run), d=768, vocab 50257,
@@ -985,6 +1024,8 @@ def main():
     log(f"[bench] embedding train grad, padded batch: {emb_pad}")
     peak = achievable_peak(dev)
     log(f"[bench] achievable bf16 GEMM rate: {peak['TFLOP/s']:.0f} TFLOP/s")
+    vendor = vendor_route(dev)
+    log(f"[bench] fc_out outputs through hipBLASLt: {vendor['ms'] * 1e3:.1f} us")
     legs = [l for l in args.legs.split(",") if l and l != "none"]
     extra = {}
     import contextlib
@@ -1032,6 +1073,11 @@ def main():
                                    "note": "frac of the vendor library's own large-GEMM rate on "
                                            "this box; `frac` above is against the nominal "
                                            "2.5 PF/s"}
+        if dom_name == "linear_valgrad+bias+train_grad[3072x768]":
+            roof["vendor_route_same_outputs"] = {
+                **vendor, "speedup": vendor["ms"] / avg_ms,
+                "note": "the op's weight dots and weight train gradient through hipBLASLt "
+                        "(isolated, no bias terms) against this op's in-step time"}
     hot_ms = sum(v["ms"] for v in ops.values()) / steps
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
     value = res["n_train"] / res["t_ghost"]

@@ -775,7 +775,18 @@ def cpu_baseline(budget_s: float = 60.0):
             fn()
         parts[name] = time.perf_counter() - t0
     t_step = time.perf_counter() - t_all
+    # The Linear microbench (configs[1], T=1024: A[32,1024,768], G[32,1024,3072] bf16, 8 val
+    # rows), the reference's ghost branch on the same cores, once, if the budget allows.
+    micro = None
+    if time.perf_counter() - t_all < budget_s:
+        del acts, A_lm, B_lm, model
+        A_mb, G_mb = rnd(32, 1024, 768), rnd(32, 1024, 3072, s=1e-3)
+        t0 = time.perf_counter()
+        R.linear_dot_ref(A_mb, G_mb, 8, True, has_bias=False)
+        micro = {"shape": "A[32,1024,768] G[32,1024,3072] bf16, 8 val rows, ghost branch",
+                 "s": time.perf_counter() - t0}
     return {"value": n_t / t_step, "unit": "samples/s", "cores": threads, "kind": "port",
+            "ghost_microbench": micro,
             "cpu_model": _cpu_model(), "s_per_step": t_step,
             "s_per_step_parts": {k: round(v, 3) for k, v in parts.items()},
             "complete": not skipped, "skipped": skipped,

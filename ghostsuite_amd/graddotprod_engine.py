@@ -6,9 +6,10 @@ attach_and_store_valset, attach_train_batch, the dot_product_log record format).
 keyword arguments set the sampler options of
 ``supported_layers_grad_samplers_dotprod.options`` (precision, linear_algo, rounding,
 store_pairs, skip_overwritten_tied_dots, record_algorithms, overlap,
-reference_id_promotion, dot_dtypes).  Options belong to the engine: each starts from the defaults, and
-the engine whose model runs its forward installs its own into the shared dict the samplers
-read, keeping direct changes made to that dict while it was the one installed.
+reference_id_promotion, reference_conv2d_ghost, dot_dtypes).  Options belong to the engine:
+each starts from the defaults, and the engine whose model runs its forward installs its own
+into the shared dict the samplers read, keeping direct changes made to that dict while it
+was the one installed.
 """
 from __future__ import annotations
 

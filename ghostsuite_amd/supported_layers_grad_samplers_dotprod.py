@@ -49,6 +49,11 @@ except Exception:  # pragma: no cover - transformers absent
 #   reference_id_promotion: pass an Embedding's token ids through the backprops' dtype
 #                  before its dot, as the reference's hook does (ids >= 256 round in a bf16
 #                  model); off by default: the ids are used as given
+#   reference_conv2d_ghost: a Conv2d layer on the reference's ghost branch gets that branch's
+#                  quantity, sum over [i, i] of (the val-summed unfolded input Gram) times
+#                  (the val-summed backprop Gram), i = C_in*kh*kw = C_out (:546-550), instead
+#                  of the presum dot of the per-sample gradients that both branches aim at;
+#                  off by default
 #   dot_dtypes:    'reference' -- each grad_dot_prod in the dtype the reference's sampler
 #                  returns: the materialised-branch weight dots and the bias dots of Linear,
 #                  Conv1D and Conv2d layers in the operands' dtype (bf16 in a bf16 model),
@@ -63,6 +68,7 @@ options = {
     # Run the dot kernels on a side stream, overlapped with the rest of backward.
     "overlap": True,
     "reference_id_promotion": False,
+    "reference_conv2d_ghost": False,
     "dot_dtypes": "reference",
 }
 DEFAULT_OPTIONS = dict(options)
@@ -544,6 +550,33 @@ def _conv2d_rows(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor, dtype: torc
     return A_rows, B_rows
 
 
+def _conv2d_reference_ghost(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor, n_val: int,
+                            dtype: torch.dtype) -> torch.Tensor:
+    """The reference's Conv2d ghost-branch quantity (:546-550): with the unfolded inputs
+    A_u [N, i, L] and backprops B_r [N, p, L], their val sums Abar, Bbar, per train sample b
+    sum_{x,y} (Abar A_b^T)[x, y] (Bbar B_b^T)[x, y], both Grams contracting over the L
+    positions.  That is the fused ghost kernel with the i (= p) channel rows as its tokens, the
+    positions as its features and the val block summed into one row; with bf16 operands the
+    Gram entries and their products are rounded to bf16 as the reference's bf16 matmuls and
+    multiply round them."""
+    A_u = F.unfold(A.to(dtype), kernel_size=layer.kernel_size, dilation=layer.dilation,
+                   padding=layer.padding, stride=layer.stride)
+    B_r = B.to(dtype).reshape(B.size(0), B.size(1), -1)
+    i, p = A_u.size(1), B_r.size(1)
+    if i != p:
+        raise RuntimeError(
+            f"Conv2d ghost branch of the reference (reference_conv2d_ghost): its [{i}, {i}] "
+            f"input Gram and [{p}, {p}] backprop Gram multiply elementwise only when "
+            f"C_in*kh*kw ({i}) equals C_out ({p})")
+    n_t = A_u.size(0) - n_val
+    rows_a = torch.cat([A_u[:n_t], A_u[n_t:].sum(0, keepdim=True)])
+    rows_b = torch.cat([B_r[:n_t], B_r[n_t:].sum(0, keepdim=True)])
+    rounding = _native.ROUND_REF_BF16 if dtype == torch.bfloat16 else _native.ROUND_FP32
+    dot, _ = _native.ops().linear_dot(rows_a, rows_b, 1, semantics=_native.SEM_PAIRWISE_SUM,
+                                      algo=_native.ALGO_GHOST, rounding=rounding)
+    return dot
+
+
 def _compute_conv2d_dot_product(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tensor,
                                 val_batch_size: int) -> None:
     """Gradient dot-products of an nn.Conv2d (reference :513-560): unfold, then the presum
@@ -552,7 +585,8 @@ def _compute_conv2d_dot_product(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tens
 
     Both of the reference's branches aim at this presum quantity; its materialised branch
     (:552-555) computes it, its ghost branch (:546-550) multiplies [d, d] by [p, p] blocks (it
-    raises unless C_in*kh*kw == C_out).  The switch is still cached on the layer."""
+    raises unless C_in*kh*kw == C_out).  The switch is still cached on the layer; with the
+    option reference_conv2d_ghost a layer on the ghost branch gets that branch's quantity."""
     A = A.detach()
     B = B.detach()
     train_bs = A.size(0) - val_batch_size
@@ -563,7 +597,10 @@ def _compute_conv2d_dot_product(layer: nn.Conv2d, A: torch.Tensor, B: torch.Tens
     # The reference's switch on the unfolded shapes: T = L, 2 L^2 <= weight.numel().
     _should_use_ghost_computation(layer, A_rows.transpose(1, 2), B_rows.transpose(1, 2),
                                   conv=True)
-    _linear_like_dot(layer, A_rows, B_rows, val_batch_size, False, dt)
+    if options["reference_conv2d_ghost"] and layer.use_ghost_computation:
+        layer.weight.grad_dot_prod = _conv2d_reference_ghost(layer, A, B, val_batch_size, dt)
+    else:
+        _linear_like_dot(layer, A_rows, B_rows, val_batch_size, False, dt)
     if layer.bias is not None:
         _bias_dot_and_grad(layer, B_rows, val_batch_size, dt)
     _reference_dtypes(layer, None if layer.use_ghost_computation else torch.bfloat16,

@@ -354,6 +354,36 @@ def conv2d_dot_ref(A: torch.Tensor, B: torch.Tensor, n_val: int, conv: dict,
     return w.float(), None if b is None else b.float()
 
 
+def conv2d_ghost_ref(A: torch.Tensor, B: torch.Tensor, n_val: int, conv: dict) -> torch.Tensor:
+    """_compute_conv2d_dot_product, ghost branch (supported_layers_grad_samplers_dotprod.py
+    :546-550): bf16 unfold A_u [b, i, L] and B_r [b, p, L], the val sums over samples,
+    AA = A_val_sum @ A_u^T ([b, i, i]) and BB = B_val_sum @ B_r^T ([b, p, p]), both bf16
+    matmul outputs, then sum((AA * BB).float()) per train sample.  Defined when i == p."""
+    Ab, Bb = A.to(BF16), B.to(BF16)
+    n_t = Ab.size(0) - n_val
+    A_tr, A_va = torch.split(Ab, [n_t, n_val], dim=0)
+    B_tr, B_va = torch.split(Bb, [n_t, n_val], dim=0)
+    A_tr_u, A_va_u = F.unfold(A_tr, **conv), F.unfold(A_va, **conv)
+    B_tr_r = B_tr.reshape(n_t, B_tr.size(1), -1)
+    B_va_r = B_va.reshape(n_val, B_va.size(1), -1)
+    AA = torch.matmul(torch.sum(A_va_u, dim=0).unsqueeze(0), A_tr_u.transpose(1, 2))
+    BB = torch.matmul(torch.sum(B_va_r, dim=0).unsqueeze(0), B_tr_r.transpose(1, 2))
+    return torch.sum((AA * BB).float(), dim=[1, 2])
+
+
+def conv2d_ghost_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, conv: dict) -> torch.Tensor:
+    """float64 value of the reference's Conv2d ghost-branch quantity, contracted in the other
+    order: sum_{x,y} (Abar A_b^T)[x,y] (Bbar B_b^T)[x,y] = <Abar^T Bbar, A_b^T B_b> over
+    [L, L] position pairs (Abar, Bbar the val sums of the unfolded A and of B)."""
+    A64, B64 = A.double(), B.double()
+    n_t = A64.size(0) - n_val
+    A_u = F.unfold(A64, **conv)                            # [N, i, L]
+    B_r = B64.reshape(B64.size(0), B64.size(1), -1)        # [N, p, L]
+    cross_val = A_u[n_t:].sum(0).t() @ B_r[n_t:].sum(0)    # [L, L]
+    cross_tr = torch.einsum('bxk,bxl->bkl', A_u[:n_t], B_r[:n_t])
+    return torch.einsum('kl,bkl->b', cross_val, cross_tr)
+
+
 def conv2d_dot_exact(A: torch.Tensor, B: torch.Tensor, n_val: int, conv: dict):
     """float64 presum dot of the Conv2d weight gradients: G_i = sum_l b_il a_il^T over the
     unfolded positions, Gbar the same with the val sums of a and b."""

@@ -46,12 +46,23 @@ def conv_net():
         nn.Flatten(), nn.Linear(4 * 4 * 2, 5))
 
 
-def run_conv_engine(model, X, Y, n_val, device, precision="fp32"):
+def conv_net_square():
+    """A Conv2d with C_in*kh*kw == C_out whose switch picks the ghost branch (2 L^2 <=
+    weight.numel(): L = 16, 36 x 36 weight), then a 1x1 Conv2d on the materialised branch and a
+    Linear head, for 8 x 8 inputs with 4 channels."""
+    from torch import nn
+    return nn.Sequential(
+        nn.Conv2d(4, 36, kernel_size=3, padding=1, stride=2), nn.ReLU(),
+        nn.Conv2d(36, 4, kernel_size=1), nn.ReLU(),
+        nn.Flatten(), nn.Linear(4 * 4 * 4, 5))
+
+
+def run_conv_engine(model, X, Y, n_val, device, precision="fp32", **options):
     """One GradDotProd step on `model`; returns ({name: dot}, {name: grad}) on the CPU."""
     import torch.nn.functional as F
     from ghostsuite_amd import GradDotProdEngine
     eng = GradDotProdEngine(model, val_batch_size=n_val, use_dummy_bias=False,
-                            precision=precision)
+                            precision=precision, **options)
     eng.attach(torch.optim.SGD(model.parameters(), lr=0.0))
     eng.attach_train_batch(X[:-n_val], Y[:-n_val], 0, 0)
     F.cross_entropy(model(X.to(device)), Y.to(device)).backward()

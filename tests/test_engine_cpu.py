@@ -361,6 +361,49 @@ def test_conv2d_engine_dots_and_grads(n_val):
     assert model[0].use_ghost_computation == (2 * 16 ** 2 <= 6 * 3 * 9)
 
 
+@pytest.mark.parametrize("n_val", [1, 2])
+def test_conv2d_reference_ghost_option(n_val):
+    """reference_conv2d_ghost: the Conv2d layer on the ghost branch gets the reference's
+    ghost-branch quantity; the one on the materialised branch keeps the presum dot; the train
+    gradients are unchanged."""
+    from tests.helpers import conv_net_square
+    torch.manual_seed(63)
+    model = conv_net_square()
+    ref = copy.deepcopy(model).double()
+    N = 6
+    X = torch.randn(N, 4, 8, 8, generator=gen(64))
+    Y = torch.randint(0, 5, (N,), generator=gen(65))
+    caps = {}
+    for idx in (0, 2):
+        model[idx].register_forward_hook(
+            lambda m, i, o, k=idx: caps.__setitem__(("A", k), i[0].detach().clone()))
+        model[idx].register_full_backward_hook(
+            lambda m, gi, go, k=idx: caps.__setitem__(("B", k), go[0].detach().clone()))
+    with use_oracle_backend():
+        dots, grads = run_conv_engine(model, X, Y, n_val, "cpu", reference_conv2d_ghost=True)
+    assert model[0].use_ghost_computation and not model[2].use_ghost_computation
+    convs = {idx: dict(kernel_size=model[idx].kernel_size, dilation=model[idx].dilation,
+                       padding=model[idx].padding, stride=model[idx].stride) for idx in (0, 2)}
+    assert_close(dots["0.weight"], R.conv2d_ghost_exact(caps[("A", 0)], caps[("B", 0)], n_val,
+                                                        convs[0]), FP32_TOL, "ghost branch")
+    assert_close(dots["2.weight"], R.conv2d_dot_exact(caps[("A", 2)], caps[("B", 2)], n_val,
+                                                      convs[2]), FP32_TOL, "materialised")
+    g = brute.per_sample_grads(ref, X.double(), Y, _ce_sum, 1.0 / N)
+    for name, gr in grads.items():
+        assert_close(gr, brute.train_mean(g[name], n_val, N), FP32_TOL, f"grad {name}")
+
+
+def test_conv2d_reference_ghost_option_rejects_non_square_blocks():
+    """On the ghost branch with C_in*kh*kw != C_out the reference's elementwise product of the
+    two Grams fails; the option raises there too."""
+    model = torch.nn.Sequential(torch.nn.Conv2d(2, 5, kernel_size=2, stride=2),
+                                torch.nn.Flatten(), torch.nn.Linear(5 * 2 * 2, 3))
+    X = torch.randn(4, 2, 4, 4, generator=gen(66))   # L = 4: 2 L^2 <= 5 * 8, ghost branch
+    Y = torch.randint(0, 3, (4,), generator=gen(67))
+    with use_oracle_backend(), pytest.raises(RuntimeError, match="C_in\\*kh\\*kw"):
+        run_conv_engine(model, X, Y, 1, "cpu", reference_conv2d_ghost=True)
+
+
 def test_options_do_not_carry_over_between_engines():
     S = __import__("ghostsuite_amd.supported_layers_grad_samplers_dotprod",
                    fromlist=["options"])

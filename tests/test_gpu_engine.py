@@ -565,6 +565,46 @@ def test_conv2d_engine_on_gpu(gpu, precision, tol, n_val):
         assert_close(gr, brute.train_mean(g[name], n_val, N), tol, f"grad {name}")
 
 
+@pytest.mark.parametrize("precision", ["fp32", "reference"])
+@pytest.mark.parametrize("n_val", [1, 2])
+def test_conv2d_reference_ghost_on_gpu(gpu, precision, n_val):
+    """reference_conv2d_ghost through the HIP ghost kernel: the Conv2d layer on the ghost
+    branch (C_in*kh*kw == C_out) against the reference's bf16 op sequence
+    (oracle.conv2d_ghost_ref, precision 'reference') or the quantity in float64 (fp32); the
+    layer on the materialised branch keeps the presum dot."""
+    from oracle import ghost_ref as R
+    from tests.helpers import conv_net_square, run_conv_engine
+    torch.manual_seed(63)
+    model = conv_net_square().to(gpu)
+    N = 6
+    X = torch.randn(N, 4, 8, 8, generator=gen(64))
+    Y = torch.randint(0, 5, (N,), generator=gen(65))
+    caps = {}
+    for idx in (0, 2):
+        model[idx].register_forward_hook(
+            lambda m, i, o, k=idx: caps.__setitem__(("A", k), i[0].detach().cpu()))
+        model[idx].register_full_backward_hook(
+            lambda m, gi, go, k=idx: caps.__setitem__(("B", k), go[0].detach().cpu()))
+    print(f"conv2d reference ghost precision={precision} n_val={n_val}", flush=True)
+    dots, _ = run_conv_engine(model, X, Y, n_val, gpu, precision, reference_conv2d_ghost=True)
+    assert model[0].use_ghost_computation and not model[2].use_ghost_computation
+    convs = {idx: dict(kernel_size=model[idx].kernel_size, dilation=model[idx].dilation,
+                       padding=model[idx].padding, stride=model[idx].stride) for idx in (0, 2)}
+    A0, B0 = caps[("A", 0)], caps[("B", 0)]
+    exact = R.conv2d_ghost_exact(A0, B0, n_val, convs[0])
+    if precision == "fp32":
+        assert_close(dots["0.weight"], exact, FP32_TOL, "ghost branch")
+        tol = FP32_TOL
+    else:
+        assert dots["0.weight"].dtype == torch.float32
+        assert_close(dots["0.weight"], R.conv2d_ghost_ref(A0, B0, n_val, convs[0]).double(),
+                     BF16_TOL, "ghost branch vs the reference's op sequence")
+        assert_close(dots["0.weight"], exact, BF16_TOL, "ghost branch vs float64")
+        tol = BF16_TOL
+    assert_close(dots["2.weight"], R.conv2d_dot_exact(caps[("A", 2)], caps[("B", 2)], n_val,
+                                                      convs[2]), tol, "materialised branch")
+
+
 @pytest.mark.parametrize("n_v", [1, 2])
 def test_gpt2_engine_fused_bias_path_on_gpu(gpu, n_v, monkeypatch):
     """Tile-aligned shapes (T and every d_out multiples of 256) route each Linear with a bias

@@ -300,6 +300,36 @@ def test_conv2d_forms_match_per_sample_gradients():
                  brute.pairwise_dots(g["bias"], n_val), 1e-10, "conv2d bias exact")
 
 
+@pytest.mark.parametrize("n_val", [1, 2])
+def test_conv2d_ghost_branch_forms(n_val):
+    """The reference's Conv2d ghost-branch quantity (defined when C_in*kh*kw == C_out):
+    conv2d_ghost_exact's [L, L] cross-Gram contraction against the Gram-Hadamard sum written
+    as explicit loops, and the bf16 op sequence against both."""
+    import torch.nn.functional as F
+    N, C, H, W = 4 + n_val, 2, 7, 6
+    i = C * 3 * 2
+    X = randn((N, C, H, W), 53).double()
+    A_u = F.unfold(X, **CONV)                                  # [N, i, L]
+    L = A_u.size(2)
+    B = randn((N, i, L), 54).double().reshape(N, i, 4, L // 4)  # a C_out = i backprop
+    n_t = N - n_val
+    Abar, Bbar = A_u[n_t:].sum(0), B.reshape(N, i, L)[n_t:].sum(0)
+    want = torch.zeros(n_t, dtype=torch.float64)
+    for b in range(n_t):
+        Ab, Bb = A_u[b], B[b].reshape(i, L)
+        for x in range(i):
+            for y in range(i):
+                aa = sum(Abar[x, k] * Ab[y, k] for k in range(L))
+                bb = sum(Bbar[x, k] * Bb[y, k] for k in range(L))
+                want[b] += aa * bb
+    assert_close(R.conv2d_ghost_exact(X, B, n_val, CONV), want, 1e-10, "cross-Gram form")
+    assert_close(R.conv2d_ghost_ref(X.float(), B.float(), n_val, CONV).double(), want,
+                 BF16_TOL, "bf16 op sequence")
+    # Not the presum dot of the per-sample gradients (the quantity both branches aim at).
+    presum = R.conv2d_dot_exact(X, B, n_val, CONV)
+    assert (presum - want).abs().max() > 1e-3 * want.abs().max()
+
+
 def test_conv2d_presum_by_explicit_position_loops():
     """n_val = 2: dot_i = sum_{l,m} <a_il, abar_m> <b_il, bbar_m> over unfolded positions."""
     N, n_val, C, H, W, P = 4, 2, 2, 5, 4, 3

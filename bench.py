@@ -511,6 +511,25 @@ def hf_gpt2_bench(steps: int, warmup: int, dev):
 
 
 # ------------------------------------------------------------------ ghost kernel microbench
+def timed_blocks(fn, warmup: int, reps: int, blocks: int):
+    """`warmup` untimed calls of fn, then `blocks` timed blocks of `reps` calls on the current
+    stream; returns (the median block's average ms per call, every block's average)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    block_ms = []
+    for _ in range(blocks):
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        block_ms.append(s.elapsed_time(e) / reps)
+    return sorted(block_ms)[len(block_ms) // 2], block_ms
+
+
 def ghost_kernel_bench(dev, reps: int = 20, T: int = 1024, warmup: int = 12, blocks: int = 5):
     """A[32,T,768], G[32,T,3072] bf16, first 8 rows val, fused ghost.
 
@@ -523,28 +542,14 @@ def ghost_kernel_bench(dev, reps: int = 20, T: int = 1024, warmup: int = 12, blo
     A = torch.randn(N, T, d_in, generator=g).to(dev, torch.bfloat16)
     G = (torch.randn(N, T, d_out, generator=g) * 1e-3).to(dev, torch.bfloat16)
     ops = _native.ops()
-    for _ in range(warmup):
-        ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_GHOST)
-    torch.cuda.synchronize()
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    block_ms = []
-    for _ in range(blocks):
-        s.record()
-        for _ in range(reps):
-            ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_GHOST)
-        e.record()
-        torch.cuda.synchronize()
-        block_ms.append(s.elapsed_time(e) / reps)
-    ms = sorted(block_ms)[len(block_ms) // 2]
+    ms, block_ms = timed_blocks(
+        lambda: ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_GHOST),
+        warmup, reps, blocks)
     flops = 2.0 * (N - n_val) * n_val * T * T * (d_in + d_out)
     # same semantics through the val-gradient algorithm, for reference
-    s.record()
-    for _ in range(reps):
-        ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_VALGRAD)
-    e.record()
-    torch.cuda.synchronize()
-    ms_vg = s.elapsed_time(e) / reps
+    ms_vg, _ = timed_blocks(
+        lambda: ops.linear_dot(A, G, n_val, val_start=0, algo=_native.ALGO_VALGRAD),
+        warmup, reps, 3)
     return {"T": T, "ms": ms, "tflops": flops / ms / 1e9, "frac": flops / (ms * 1e-3) / PEAK_BF16,
             "valgrad_ms": ms_vg, "block_ms": block_ms, "warmup_calls": warmup,
             "calls_per_block": reps}
@@ -558,20 +563,7 @@ def achievable_peak(dev, reps: int = 10, n: int = 8192, warmup: int = 12, blocks
     g = torch.Generator().manual_seed(11)
     a = torch.randn(n, n, generator=g).to(dev, torch.bfloat16)
     b = torch.randn(n, n, generator=g).to(dev, torch.bfloat16)
-    for _ in range(warmup):
-        torch.mm(a, b)
-    torch.cuda.synchronize()
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    block_ms = []
-    for _ in range(blocks):
-        s.record()
-        for _ in range(reps):
-            torch.mm(a, b)
-        e.record()
-        torch.cuda.synchronize()
-        block_ms.append(s.elapsed_time(e) / reps)
-    ms = sorted(block_ms)[len(block_ms) // 2]
+    ms, block_ms = timed_blocks(lambda: torch.mm(a, b), warmup, reps, blocks)
     del a, b
     return {"kernel": f"torch.mm (hipBLASLt) bf16 {n}x{n}x{n}", "ms": ms,
             "TFLOP/s": 2.0 * n ** 3 / (ms * 1e-3) / 1e12, "ms_per_block": block_ms}
@@ -648,10 +640,10 @@ def emb_grad_pad_bench(dev, reps: int = 10):
             **out}
 
 
-def ghost_sweep(dev, reps: int = 10):
+def ghost_sweep(dev, reps: int = 6, warmup: int = 6, blocks: int = 3):
     """BASELINE configs[1] sweep over T: the reference's switch (2T^2 <= d_in*d_out) picks the
     ghost (pairwise-sum) branch up to T=1024 and the materialised (presum) branch at T=2048;
-    each semantics is timed with both algorithms."""
+    each semantics is timed with both algorithms (timed_blocks: the median block)."""
     from ghostsuite_amd import _native
     g = torch.Generator().manual_seed(1234)
     N, n_val, d_in, d_out = 32, 8, 768, 3072
@@ -666,17 +658,7 @@ def ghost_sweep(dev, reps: int = 10):
                "semantics": "pairwise" if ghost_branch else "presum"}
         for algo, name in ((_native.ALGO_GHOST, "ghost"), (_native.ALGO_VALGRAD, "valgrad")):
             fn = lambda: ops.linear_dot(A, G, n_val, val_start=0, semantics=sem, algo=algo)
-            for _ in range(2):
-                fn()
-            torch.cuda.synchronize()
-            s = torch.cuda.Event(enable_timing=True)
-            e = torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                fn()
-            e.record()
-            torch.cuda.synchronize()
-            row[f"{name}_ms"] = s.elapsed_time(e) / reps
+            row[f"{name}_ms"], _ = timed_blocks(fn, warmup, reps, blocks)
         n_t, nv = N - n_val, (n_val if ghost_branch else 1)
         ghost_flops = 2.0 * n_t * nv * T * T * (d_in + d_out)
         row["ghost_TFLOPs"] = ghost_flops / row["ghost_ms"] / 1e9

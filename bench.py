@@ -842,10 +842,11 @@ KERNEL_SHAPES = {
 }
 
 
-def kernels_leg(dev, reps: int = 10):
-    """Kernel-level leg for counter runs: every hot-path entry point once per rep at its bench
-    shape (KERNEL_SHAPES), plus a 1 GiB device copy (the calibration for FETCH_SIZE and
-    WRITE_SIZE).  Prints one JSON line of average milliseconds per call."""
+def kernels_leg(dev, reps: int = 10, warmup: int = 4):
+    """Kernel-level leg for counter runs: every hot-path entry point at its bench shape,
+    `warmup` untimed calls (12 for the ghost kernel, which runs first, while the clock
+    settles) and `reps` timed ones, plus a 1 GiB device copy (the calibration for FETCH_SIZE
+    and WRITE_SIZE).  Prints one JSON line of average milliseconds per call."""
     from ghostsuite_amd import _native
     ops = _native.ops()
     g = torch.Generator().manual_seed(7)
@@ -853,13 +854,14 @@ def kernels_leg(dev, reps: int = 10):
     def rnd(*shape, s=1.0):
         return (torch.randn(*shape, generator=g) * s).to(dev, torch.bfloat16)
 
-    # A one-element bitwise_not separates the entry points in kernel traces and counter
-    # dumps (kernel order follows KERNEL_SHAPES).
+    # One-element ops bracket each entry point in kernel traces and counter dumps: a
+    # bitwise_not before its first call and a neg after its last (entries in the order of
+    # the printed JSON line).
     marker = torch.zeros(1, dtype=torch.int32, device=dev)
 
-    def timeit(fn):
+    def timeit(fn, warm=warmup):
         marker.bitwise_not_()
-        for _ in range(2):
+        for _ in range(warm):
             fn()
         torch.cuda.synchronize()
         s = torch.cuda.Event(enable_timing=True)
@@ -868,6 +870,7 @@ def kernels_leg(dev, reps: int = 10):
         for _ in range(reps):
             fn()
         e.record()
+        marker.neg_()
         torch.cuda.synchronize()
         return s.elapsed_time(e) / reps
 
@@ -875,7 +878,7 @@ def kernels_leg(dev, reps: int = 10):
     A = rnd(32, 1024, 768)
     G = rnd(32, 1024, 3072, s=1e-3)
     out["ghost_microbench"] = timeit(lambda: ops.linear_dot(A, G, 8, val_start=0,
-                                                           algo=_native.ALGO_GHOST))
+                                                           algo=_native.ALGO_GHOST), warm=12)
     A2, G2 = A[:20].contiguous(), G[:20].contiguous()
     out["valgrad_fc"] = timeit(lambda: ops.linear_dot(A2, G2, 4, algo=_native.ALGO_VALGRAD))
     out["valgrad_bias_fc"] = timeit(lambda: ops.linear_bias_dot(A2, G2, 4,

@@ -665,11 +665,16 @@ __device__ __forceinline__ int dma_pending(int kt, int nk) {
 }
 
 // Returns this lane's sum from ks_final with KS (0 without).
-template <class C, class D, bool KS = false>
+// `pre()` runs after the first stages' loads are issued and before the first wait: work that
+// needs no LDS (the ghost kernel's packing of its first Gram tile) overlaps their latency.
+struct NoPre {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <class C, class D, bool KS = false, class Pre = NoPre>
 __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R, int64_t mt,
                                              int64_t nt, int64_t K, const DmaLds& l,
                                              f32x16_t (&acc)[C::MI][C::NI],
-                                             const KsState* ks = nullptr) {
+                                             const KsState* ks = nullptr, Pre pre = Pre{}) {
   using O = DmaOrder<D>;
   constexpr int AL = O::AL, AR = O::AR;  // stages each ring runs ahead
   constexpr int PEND = O::PEND;
@@ -701,6 +706,7 @@ __device__ __forceinline__ float mainloop_dma(const Operand& L, const Operand& R
   uint32_t kv[8];           // KS: the stage's first row reads
 #pragma unroll
   for (int i = -O::A2; i < 0; ++i) issue(i);
+  pre();
   // One iteration after its wait: the column-sum store (before the loads), the loads (both
   // rings in the steady state), then the stage's MFMAs.
   auto body = [&](int kt, auto steady) {
@@ -1180,8 +1186,9 @@ __global__ void __launch_bounds__(C::NT, 1) ghost_stash_kernel(GemmParams p) {
     zero_acc<TrBF16, C>(a);
   };
   mainloop_dma<C, D>(p.L1, p.R1, mt, nt, p.K1, l, acc);
-  pack(acc);
-  mainloop_dma<C, D>(p.L2, p.R2, mt, nt, p.K2, l, acc);
+  // The first GEMM's mainloop ends with every wave past its last LDS read, so the second
+  // GEMM's first stages are loaded into the rings while the first Gram tile is packed.
+  mainloop_dma<C, D, false>(p.L2, p.R2, mt, nt, p.K2, l, acc, nullptr, [&]() { pack(acc); });
   float colsum[C::NI];
   auto hadamard = [&](auto ref) {
 #pragma unroll

@@ -2405,7 +2405,9 @@ int64_t tn_kper(int64_t K, int sp) {
   return ceil_div(ceil_div(K, static_cast<int64_t>(sp)), static_cast<int64_t>(TnD::KB)) *
          TnD::KB;
 }
-int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
+// reduce_free: the reduction launch runs whatever the split count (it also folds column-sum
+// rows written before the GEMM), so extra splits are not charged for it.
+int tn_splits_raw(int64_t K, int64_t M, int64_t N, bool reduce_free = false) {
   const int64_t ksteps = ceil_div(K, static_cast<int64_t>(TnD::KB));
   const int64_t tiles = ceil_div(M, TnC::BM) * ceil_div(N, TnC::BN);
   int best = 1;
@@ -2415,7 +2417,7 @@ int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
     const double rounds = std::ceil(static_cast<double>(items) / 512.0);
     const double rate = items <= 256 ? 2.2e12 : 2.0e12;
     const double t = rounds * 2.0 * TnC::BM * TnC::BN * tn_kper(K, sp) / rate +
-                     (sp > 1 ? 8.0 * sp * M * N / 4e12 + 3e-6 : 0.0);
+                     (sp > 1 ? 8.0 * sp * M * N / 4e12 + (reduce_free ? 0.0 : 3e-6) : 0.0);
     if (t < best_t) {
       best_t = t;
       best = sp;
@@ -2424,11 +2426,11 @@ int tn_splits_raw(int64_t K, int64_t M, int64_t N) {
   return best;
 }
 // The split count a launch uses: the k-rows per split are rounded up to whole stages.
-int tn_splits(int64_t K, int64_t M, int64_t N) {
-  return static_cast<int>(ceil_div(K, tn_kper(K, tn_splits_raw(K, M, N))));
+int tn_splits(int64_t K, int64_t M, int64_t N, bool reduce_free = false) {
+  return static_cast<int>(ceil_div(K, tn_kper(K, tn_splits_raw(K, M, N, reduce_free))));
 }
-int64_t tn_part_elems(int64_t K, int64_t M, int64_t N) {
-  const int sp = tn_splits(K, M, N);
+int64_t tn_part_elems(int64_t K, int64_t M, int64_t N, bool reduce_free = false) {
+  const int sp = tn_splits(K, M, N, reduce_free);
   return sp > 1 ? sp * M * N : 0;
 }
 
@@ -2476,8 +2478,9 @@ int launch_tn(const void* L, int64_t ldl, const void* R, int64_t ldr, int64_t K,
   p.N = N;
   p.m_tiles = ceil_div(M, TnC::BM);
   p.n_tiles = ceil_div(N, TnC::BN);
-  p.kper = tn_kper(K, tn_splits_raw(K, M, N));
-  const int sp = tn_splits(K, M, N);
+  const bool rf = o.vrows != nullptr && o.vrows_n > 1;  // the reduction runs anyway
+  p.kper = tn_kper(K, tn_splits_raw(K, M, N, rf));
+  const int sp = tn_splits(K, M, N, rf);
   p.vsum = vsum;
   p.vsum_r = vsum_r ? 1 : 0;
   p.vparts = static_cast<int>(tn_vparts(M, N, vsum_r));
@@ -3274,7 +3277,10 @@ TgBufs carve_tg(S& c, const TgPlan& t, int64_t T, int64_t d_in, int64_t d_out) {
   b.abar = t.presum ? c.template take<uint16_t>(T * d_in) : nullptr;
   b.gbar = t.presum ? c.template take<uint16_t>(T * d_out) : nullptr;
   b.V = c.template take<uint16_t>(d_out * d_in);  // V^T, [d_in][d_out]
-  b.vpart = c.template take<float>(tn_part_elems(t.vk, d_out, d_in));
+  // Presum with a bias: the V GEMM's reduction also folds the presum kernel's column-sum rows
+  // (more than one when T > PS_T), as launch_tn sizes it.
+  b.vpart = c.template take<float>(
+      tn_part_elems(t.vk, d_out, d_in, t.presum && t.bias && presum_rows(T) > 1));
   // Val column sums of G: the V GEMM's own partials for the pairwise semantics (its operands
   // are the val rows as they lie); for the presum, whose V operands are rounded to bf16, the
   // presum kernel's fp32 sums.
